@@ -1,0 +1,158 @@
+/*
+ * locks_hip.h -- C ABI of liblocks_hip.so, the MI355X (gfx950) LOCKS decode
+ * hot path: rki4 page scoring, GQA combine + exact top-b page selection,
+ * split-K sparse paged decode with LSE merge.
+ *
+ * Conventions (same contract as the reference's kernels):
+ *   - every pointer is a device pointer; every buffer (outputs, partials,
+ *     workspace) is caller-owned and persistent; no entry point allocates;
+ *   - bf16 tensors are passed as uint16_t bit patterns;
+ *   - `stream` is a hipStream_t (NULL = the default stream); launches are
+ *     asynchronous and never synchronize the host, so every entry is safe
+ *     inside HIP graph capture;
+ *   - strides are in ELEMENTS of the pointed-to type;
+ *   - return 0 on success, <0 on a rejected argument (-1) or a failed launch
+ *     (-2); locks_last_error() then describes the failure (thread-local).
+ *
+ * Geometry contract of this build: head_dim 128, page 16, summary rank 8,
+ * int4 basis, 1 <= G <= 16 query heads per kv head.  (The reference's rki4
+ * state asserts d in {64,128,256}, page in {16,32,64}, G <= 8:
+ * src/locks/selection/rki4_state.py:288-334; G up to 16 is needed by the
+ * GLM-4-9B 32q/2kv geometry.)
+ *
+ * Reference interfaces each entry replaces (paths under src/locks/):
+ */
+#ifndef LOCKS_HIP_H_
+#define LOCKS_HIP_H_
+
+#include <stdint.h>
+
+#define LOCKS_ABI_VERSION 1
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ABI version of the loaded library (LOCKS_ABI_VERSION). */
+int32_t locks_abi_version(void);
+
+/* Message of the last failed call on this host thread. */
+const char* locks_last_error(void);
+
+/*
+ * Per-request page parameters for this step.
+ * Replaces the Triton _derive_params_kernel / derive_page_params
+ * (selection/select.py:28-58):
+ *   n_pages = ceil(seq_len / page), n_sel_hi = n_pages - window_pages,
+ *   S = n_sel_hi - sink_pages,
+ *   b = budget_abs > 0 ? max(min(budget_abs, max(S, 1)), 1)
+ *                      : min(max(ceil(S * budget), 1), max(S, 1))   (fp64 ceil)
+ */
+int32_t locks_derive_params(const int32_t* seq_lens, int32_t n_req, int32_t page,
+                            int32_t window_pages, int32_t sink_pages, int32_t budget_abs,
+                            double budget, int32_t* n_pages, int32_t* n_sel_hi,
+                            int32_t* b_fix, void* stream);
+
+/*
+ * Scorer launch shape: pages per workgroup (a multiple of 32) for a state
+ * with `max_pages` logical pages, and the resulting number of chunks, which
+ * sizes the page-max buffer (n_req, n_kv, chunks, 16) fp32.  Host-only
+ * integer math (the reference's auto_zsplit, selection/rki4_score_cuda.py:3161).
+ */
+int32_t locks_score_auto_chunk(int32_t n_req, int32_t n_kv, int32_t max_pages);
+int32_t locks_score_num_chunks(int32_t max_pages, int32_t chunk);
+
+/*
+ * rki4 per-head page LSE scores.
+ * Replaces rki4_score_bt(q, v4, vs, c8, cs, mu8, mus, bt, nsh, S, sm_scale,
+ * zsplit, n_req) (selection/rki4_score_cuda.py:2518-2619; math :653-722).
+ *   q          (n_req, n_kv*G, 128) bf16, strides (q_stride_req, q_stride_head, 1)
+ *   v4         (num_blocks, n_kv, 8, 64) u8   int4 column-major basis
+ *   vs         (num_blocks, n_kv, 8)     bf16 per-column scales
+ *   c8         (num_blocks, n_kv, 16, 8) i8   per-token coefficients
+ *   cs         (num_blocks, n_kv, 16)    bf16 per-token scales
+ *   mu8        (num_blocks, n_kv, 128)   i8   page centroid
+ *   mus        (num_blocks, n_kv)        bf16 centroid scale
+ *   block_table (n_req, bt_cols) i32, row stride bt_stride; page p -> block
+ *   n_sel_hi   (n_req,) i32: pages [0, n_sel_hi) are scored
+ *   score_h    (n_req, n_kv, G, max_pages) f32 -- written for p < n_sel_hi only
+ *   page_max   (n_req, n_kv, chunks, 16) f32 -- per-chunk per-head maxima
+ *   chunk      pages per workgroup (locks_score_auto_chunk)
+ * Block ids are clamped to [0, num_blocks) and page ids to [0, bt_cols).
+ */
+int32_t locks_score_rki4(const uint16_t* q, int64_t q_stride_req, int64_t q_stride_head,
+                         const uint8_t* v4, const uint16_t* vs, const int8_t* c8,
+                         const uint16_t* cs, const int8_t* mu8, const uint16_t* mus,
+                         int32_t num_blocks, const int32_t* block_table, int64_t bt_stride,
+                         int32_t bt_cols, const int32_t* n_sel_hi, float* score_h,
+                         int32_t max_pages, float* page_max, int32_t chunk, int32_t n_req,
+                         int32_t n_kv, int32_t G, int32_t head_dim, int32_t page,
+                         float sm_scale, void* stream);
+
+/* Workspace bytes locks_select_nrm_topb needs for this geometry. */
+int64_t locks_select_workspace_bytes(int32_t n_req, int32_t n_kv, int32_t max_pages);
+
+/*
+ * GQA combine + exact top-b page selection (sink + recent window always kept).
+ * Replaces nrmtopb_select_cuda(score_h, hmax, npg, nsh, bfix, score,
+ * page_table, page_cnt, n_req, n_kv, G, n_sink, mp, P_PAD, blk, has_hm, pdl)
+ * (selection/select_cuda.py:834-938) including its page-parallel split chain
+ * (:3528-3611), and for combine=1 the amax combine + topb_select_cuda
+ * (selection/rki4_score_cuda.py:3494-3497, selection/select_cuda.py:3734).
+ *   combine    0 = "nrm": score[p] = sum_g exp(score_h[g][p] - max_p score_h[g]),
+ *              1 = "max": score[p] = max_g score_h[g][p]
+ *   page_max / score_chunks: the scorer's per-chunk maxima (nrm only)
+ *   score      (n_req, n_kv, max_pages) f32, written for p < n_sel_hi
+ *   page_table (n_req, n_kv, max_pages) i32: kept pages ascending, -1 after
+ *   page_cnt   (n_req, n_kv) i32
+ *   workspace  >= locks_select_workspace_bytes(...) bytes (unused when
+ *              max_pages <= 2048)
+ */
+int32_t locks_select_nrm_topb(const float* score_h, const float* page_max, int32_t score_chunks,
+                              const int32_t* n_pages, const int32_t* n_sel_hi,
+                              const int32_t* b_fix, float* score, int32_t* page_table,
+                              int32_t* page_cnt, void* workspace, int64_t workspace_bytes,
+                              int32_t n_req, int32_t n_kv, int32_t G, int32_t n_sink,
+                              int32_t max_pages, int32_t combine, void* stream);
+
+/*
+ * Split-K sparse paged decode over the selected pages.
+ * Replaces sparse_decode_split_kernel (attention/decode.py:209-322) and the
+ * CUDA decode_split(q, k, v, bt, tab, cnt, sl, m_part, l_part, acc_part,
+ * scale, n_req, n_kv, G, split, pps_min, ...) (attention/decode_cuda.py:960-965).
+ *   k_cache / v_cache: element strides of (block, token, kv head); d contiguous
+ *   (vLLM kv_cache (NB, 2, page, n_kv, d) halves, attention/decode.py:64-73)
+ *   page_table (n_req, n_kv, pt_cols) i32; page_cnt (n_req, n_kv) i32
+ *   m_part, l_part (n_req, n_kv, split, G) f32; acc_part (..., G, 128) f32
+ *   pps = max(ceil(cnt / split), pps_min); inactive splits store nothing.
+ */
+int32_t locks_decode_splitk(const uint16_t* q, int64_t q_stride_req, int64_t q_stride_head,
+                            const uint16_t* k_cache, int64_t k_stride_block,
+                            int64_t k_stride_tok, int64_t k_stride_head,
+                            const uint16_t* v_cache, int64_t v_stride_block,
+                            int64_t v_stride_tok, int64_t v_stride_head, int32_t num_blocks,
+                            const int32_t* block_table, int64_t bt_stride, int32_t bt_cols,
+                            const int32_t* page_table, int64_t pt_stride_req,
+                            int64_t pt_stride_head, int32_t pt_cols, const int32_t* page_cnt,
+                            int64_t cnt_stride, const int32_t* seq_lens, float* m_part,
+                            float* l_part, float* acc_part, int32_t n_req, int32_t n_kv,
+                            int32_t G, int32_t head_dim, int32_t page, int32_t split,
+                            int32_t pps_min, float sm_scale, void* stream);
+
+/*
+ * LSE merge of the split-K partials into the attention output.
+ * Replaces merge_splits_kernel (attention/merge.py:105-152).
+ *   out (n_req, n_kv*G, 128) bf16 (out_is_f32 = 0) or f32 (out_is_f32 = 1),
+ *   strides (out_stride_req, out_stride_head, 1); rows with page_cnt 0 get 0.
+ */
+int32_t locks_decode_merge(const float* m_part, const float* l_part, const float* acc_part,
+                           const int32_t* page_cnt, int64_t cnt_stride, void* out,
+                           int64_t out_stride_req, int64_t out_stride_head, int32_t out_is_f32,
+                           int32_t n_req, int32_t n_kv, int32_t G, int32_t head_dim,
+                           int32_t split, int32_t pps_min, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LOCKS_HIP_H_ */

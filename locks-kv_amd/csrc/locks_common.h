@@ -1,0 +1,81 @@
+// Shared device/host helpers for the LOCKS gfx950 kernels.
+//
+// Everything here is CDNA4-specific: wave64, MFMA operand vector types, and
+// the order-preserving fp32 <-> uint32 radix key used by the page selector
+// (same key the reference's selector uses, selection/select_cuda.py:77-86).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace locks {
+
+constexpr int kWave = 64;
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+    return __uint_as_float(((uint32_t)b) << 16);
+}
+// low / high bf16 of a packed 32-bit word -> fp32
+__device__ __forceinline__ float bf16lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+
+// fp32 -> bf16 bits, round to nearest even (NaN stays NaN)
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu))
+        return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+// order-preserving fp32 -> uint32 key (monotone for finite values and +-inf)
+__device__ __forceinline__ uint32_t f2u(float f) {
+    uint32_t u = __float_as_uint(f);
+    uint32_t mask = (uint32_t)(-(int32_t)(u >> 31)) | 0x80000000u;
+    return u ^ mask;
+}
+__device__ __forceinline__ float u2f(uint32_t x) {
+    uint32_t mask = ((x >> 31) - 1u) | 0x80000000u;
+    return __uint_as_float(x ^ mask);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+    return v;
+}
+__device__ __forceinline__ int wave_sum_i(int v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+
+// Order LDS traffic between lanes of ONE wave (no cross-wave barrier).
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__host__ __device__ __forceinline__ int cdiv(int a, int b) { return (a + b - 1) / b; }
+
+}  // namespace locks
+
+// ---- host-side error plumbing for the C ABI -------------------------------
+namespace locks {
+void set_error(const char* fmt, ...);
+int check_launch(const char* what);
+}  // namespace locks
+
+#define LOCKS_REQUIRE(cond, ...)                                              \
+    do {                                                                      \
+        if (!(cond)) {                                                        \
+            ::locks::set_error(__VA_ARGS__);                                  \
+            return -1;                                                        \
+        }                                                                     \
+    } while (0)

@@ -1,0 +1,259 @@
+// Split-K sparse paged decode + LSE merge for gfx950.
+//
+// Semantics (reference: attention/decode.py:209-322, attention/merge.py:105-152):
+//   per (request r, kv head kh, split sp):
+//     pps = max(cdiv(cnt, SPLIT), PPS_MIN); pages [sp*pps, min(sp*pps+pps, cnt))
+//     of page_table[r][kh] (logical ids, ascending); block = block_table[r][pt];
+//     K/V tile = kv[block, :, kh, :] (16 tokens x d); token pt*16+t is masked
+//     when >= seq_len; online softmax over the split's tokens for all G heads
+//     of the group; partials m, l (G) and acc (G, d) in fp32.  Inactive splits
+//     store nothing.
+//   merge: n_act = cdiv(cnt, pps); w = (l > 0) ? exp(m - max m) : 0;
+//     out = sum w*acc / sum w*l  (0 when the denominator is 0).
+//
+// MI355X mapping: one wave per split.  Per 16-token page the wave issues
+// 8 x 16-byte loads per lane (K rows for the QK operand, V rows for the PV
+// operand), prefetching the next page while it computes the current one.
+//   * S^T = K Q^T on v_mfma_f32_16x16x32_bf16 (A = K tile: token rows; B = the
+//     GQA group's q rows, zero padded to 16) -- bf16 products, fp32 sum, like
+//     the reference's bf16 tl.dot.  Each lane ends with 4 tokens of one head.
+//   * online softmax per head: 4-token in-lane max + 2 cross-row shuffles.
+//   * O^T += V^T P^T on v_mfma_f32_16x16x16f16 with fp16 P and fp16 V (the
+//     reference's fp16 P.V with fp32 accumulation).  The V operand needs no
+//     transpose: the output d-index of MFMA block `blk`, row i is 8*i + blk,
+//     so each lane's four 16-byte V row loads ARE its A operand.  The softmax
+//     rescale is a per-lane scalar because O^T keeps one head per lane.
+#include "locks_common.h"
+#include "locks_hip.h"
+
+namespace locks {
+
+constexpr int DC_D = 128;
+constexpr int DC_PG = 16;
+constexpr int MG_BLK = 256;
+constexpr int MAX_SPLIT = 512;
+
+__device__ __forceinline__ uint32_t bf16_word(const uint4& w, int e) {
+    const uint32_t x = (e >> 1) == 0 ? w.x : (e >> 1) == 1 ? w.y : (e >> 1) == 2 ? w.z : w.w;
+    return (e & 1) ? (x >> 16) : (x & 0xFFFFu);
+}
+
+__global__ __launch_bounds__(kWave) void decode_split_kernel(
+    const uint16_t* __restrict__ q, long q_sr, long q_sh,
+    const uint16_t* __restrict__ kc, long k_sb, long k_st, long k_sh,
+    const uint16_t* __restrict__ vc, long v_sb, long v_st, long v_sh,
+    int NB, const int* __restrict__ bt, long bt_sr, int bt_cols,
+    const int* __restrict__ ptab, long pt_sr, long pt_sh, int pt_cols,
+    const int* __restrict__ pcnt, long cnt_sr, const int* __restrict__ seq_lens,
+    float* __restrict__ m_part, float* __restrict__ l_part, float* __restrict__ acc_part,
+    int G, int split, int pps_min, float sm_scale)
+{
+    const int sp = blockIdx.x, kh = blockIdx.y, r = blockIdx.z;
+    const int n_kv = gridDim.y;
+    const int cnt = min(pcnt[(long)r * cnt_sr + kh], pt_cols);
+    const int pps = max(cdiv(cnt, split), pps_min);
+    const int j0 = sp * pps;
+    if (j0 >= cnt) return;                        // inactive split: no store
+    const int j1 = min(j0 + pps, cnt);
+
+    const int lane = threadIdx.x;
+    const int c16 = lane & 15, kg = lane >> 4;
+    const int seq_len = seq_lens[r];
+
+    // B operand of QK: q[g = c16][32*kg + 8*s + 0..7]
+    v8bf qb[4];
+    {
+        const uint16_t* qp = q + (long)r * q_sr + (long)(kh * G + c16) * q_sh + 32 * kg;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            uint4 w = make_uint4(0u, 0u, 0u, 0u);
+            if (c16 < G) w = *reinterpret_cast<const uint4*>(qp + 8 * s);
+            qb[s] = __builtin_bit_cast(v8bf, w);
+        }
+    }
+
+    const int* prow = ptab + (long)r * pt_sr + (long)kh * pt_sh;
+    auto load_page = [&](int j, uint4 (&kr)[4], uint4 (&vr)[4]) -> int {
+        const int pt = prow[j];
+        const int ptc = min(max(pt, 0), bt_cols - 1);
+        int blk = bt[(long)r * bt_sr + ptc];
+        blk = min(max(blk, 0), NB - 1);
+        const uint16_t* kp = kc + (long)blk * k_sb + (long)kh * k_sh + (long)c16 * k_st + 32 * kg;
+        const uint16_t* vp = vc + (long)blk * v_sb + (long)kh * v_sh + 8 * c16;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) kr[i] = *reinterpret_cast<const uint4*>(kp + 8 * i);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) vr[i] = *reinterpret_cast<const uint4*>(vp + (long)(4 * kg + i) * v_st);
+        return pt;
+    };
+
+    float m = -INFINITY, lsum = 0.f;
+    v4f o[8];
+#pragma unroll
+    for (int b = 0; b < 8; ++b) o[b] = v4f{0.f, 0.f, 0.f, 0.f};
+
+    uint4 kcur[4], vcur[4];
+    int ptcur = load_page(j0, kcur, vcur);
+    for (int j = j0; j < j1; ++j) {
+        uint4 knx[4], vnx[4];
+        int ptnx = 0;
+        if (j + 1 < j1) ptnx = load_page(j + 1, knx, vnx);
+
+        // ---- S^T[t][g] = K[t] . q[g] ------------------------------------
+        v4f s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, kcur[i]), qb[i], s, 0, 0, 0);
+        const int pos0 = ptcur * DC_PG + 4 * kg;
+        float sv[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) sv[v] = (pos0 + v < seq_len) ? s[v] * sm_scale : -INFINITY;
+
+        // ---- online softmax (head = lane column) ------------------------
+        float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+        mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+        const float m_new = fmaxf(m, mx);
+        const float m_ref = (m_new == -INFINITY) ? 0.f : m_new;   // fully masked so far
+        const float alpha = __expf(m - m_ref);
+        float p[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) p[v] = __expf(sv[v] - m_ref);
+        lsum = lsum * alpha + (p[0] + p[1] + p[2] + p[3]);
+        m = m_new;
+        const v4h pb = {(_Float16)p[0], (_Float16)p[1], (_Float16)p[2], (_Float16)p[3]};
+
+        // ---- O^T[d][g] += V^T P^T ---------------------------------------
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            v4h a;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) a[v] = (_Float16)bf16_to_f32((uint16_t)bf16_word(vcur[v], b));
+            o[b] = o[b] * alpha;
+            o[b] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, pb, o[b], 0, 0, 0);
+        }
+
+#pragma unroll
+        for (int i = 0; i < 4; ++i) { kcur[i] = knx[i]; vcur[i] = vnx[i]; }
+        ptcur = ptnx;
+    }
+
+    lsum += __shfl_xor(lsum, 16, kWave);
+    lsum += __shfl_xor(lsum, 32, kWave);
+    if (c16 < G) {
+        const long base = (((long)r * n_kv + kh) * split + sp) * G + c16;
+        if (kg == 0) {
+            m_part[base] = m;
+            l_part[base] = lsum;
+        }
+        float* ap = acc_part + base * DC_D + 32 * kg;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            float4 lo = make_float4(o[0][v], o[1][v], o[2][v], o[3][v]);
+            float4 hi = make_float4(o[4][v], o[5][v], o[6][v], o[7][v]);
+            *reinterpret_cast<float4*>(ap + 8 * v) = lo;
+            *reinterpret_cast<float4*>(ap + 8 * v + 4) = hi;
+        }
+    }
+}
+
+__global__ __launch_bounds__(MG_BLK) void decode_merge_kernel(
+    const float* __restrict__ m_part, const float* __restrict__ l_part,
+    const float* __restrict__ acc_part, const int* __restrict__ pcnt, long cnt_sr,
+    void* __restrict__ out, long o_sr, long o_sh, int out_f32, int G, int split, int pps_min)
+{
+    const int kh = blockIdx.x, r = blockIdx.y;
+    const int n_kv = gridDim.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const long rk = (long)r * n_kv + kh;
+    const int cnt = pcnt[(long)r * cnt_sr + kh];
+    const int pps = max(cdiv(cnt, split), pps_min);
+    const int n_act = cnt > 0 ? min(cdiv(cnt, pps), split) : 0;
+
+    __shared__ float w_s[MAX_SPLIT][16];
+    __shared__ float lt_s[16];
+
+    for (int g = wave; g < G; g += MG_BLK / kWave) {
+        float mm = -INFINITY;
+        for (int s = lane; s < n_act; s += kWave) mm = fmaxf(mm, m_part[(rk * split + s) * G + g]);
+        mm = wave_max(mm);
+        float lt = 0.f;
+        for (int s = lane; s < n_act; s += kWave) {
+            const float l = l_part[(rk * split + s) * G + g];
+            const float w = (l > 0.f) ? __expf(m_part[(rk * split + s) * G + g] - mm) : 0.f;
+            w_s[s][g] = w;
+            lt += l * w;
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) lt += __shfl_xor(lt, o, kWave);
+        if (lane == 0) lt_s[g] = lt;
+    }
+    __syncthreads();
+
+    for (int i = tid; i < G * DC_D; i += MG_BLK) {
+        const int g = i / DC_D, d = i % DC_D;
+        float acc = 0.f;
+        for (int s = 0; s < n_act; ++s) acc += w_s[s][g] * acc_part[((rk * split + s) * G + g) * DC_D + d];
+        const float lt = lt_s[g];
+        const float o = (lt > 0.f) ? acc / lt : 0.f;
+        const long oi = (long)r * o_sr + (long)(kh * G + g) * o_sh + d;
+        if (out_f32) reinterpret_cast<float*>(out)[oi] = o;
+        else reinterpret_cast<uint16_t*>(out)[oi] = f32_to_bf16(o);
+    }
+}
+
+}  // namespace locks
+
+using namespace locks;
+
+extern "C" int32_t locks_decode_splitk(
+    const uint16_t* q, int64_t q_stride_req, int64_t q_stride_head,
+    const uint16_t* k_cache, int64_t k_stride_block, int64_t k_stride_tok, int64_t k_stride_head,
+    const uint16_t* v_cache, int64_t v_stride_block, int64_t v_stride_tok, int64_t v_stride_head,
+    int32_t num_blocks, const int32_t* block_table, int64_t bt_stride, int32_t bt_cols,
+    const int32_t* page_table, int64_t pt_stride_req, int64_t pt_stride_head, int32_t pt_cols,
+    const int32_t* page_cnt, int64_t cnt_stride, const int32_t* seq_lens,
+    float* m_part, float* l_part, float* acc_part,
+    int32_t n_req, int32_t n_kv, int32_t G, int32_t head_dim, int32_t page,
+    int32_t split, int32_t pps_min, float sm_scale, void* stream)
+{
+    LOCKS_REQUIRE(head_dim == DC_D, "locks_decode_splitk: head_dim %d unsupported (this build: 128)", head_dim);
+    LOCKS_REQUIRE(page == DC_PG, "locks_decode_splitk: page %d unsupported (this build: 16)", page);
+    LOCKS_REQUIRE(G >= 1 && G <= 16, "locks_decode_splitk: G=%d outside [1, 16]", G);
+    LOCKS_REQUIRE(split >= 1 && split <= MAX_SPLIT, "locks_decode_splitk: split %d outside [1, %d]", split, MAX_SPLIT);
+    LOCKS_REQUIRE(pps_min >= 1, "locks_decode_splitk: pps_min %d < 1", pps_min);
+    LOCKS_REQUIRE(num_blocks >= 1 && bt_cols >= 1 && pt_cols >= 1, "locks_decode_splitk: empty geometry");
+    LOCKS_REQUIRE(k_stride_tok % 8 == 0 && v_stride_tok % 8 == 0 && k_stride_block % 8 == 0 &&
+                  v_stride_block % 8 == 0 && k_stride_head % 8 == 0 && v_stride_head % 8 == 0 &&
+                  q_stride_req % 8 == 0 && q_stride_head % 8 == 0,
+                  "locks_decode_splitk: q/K/V strides must be multiples of 8 elements (16-byte loads)");
+    LOCKS_REQUIRE(q && k_cache && v_cache && block_table && page_table && page_cnt && seq_lens &&
+                  m_part && l_part && acc_part, "locks_decode_splitk: null pointer argument");
+    if (n_req == 0) return 0;
+    hipLaunchKernelGGL(decode_split_kernel, dim3(split, n_kv, n_req), dim3(kWave), 0,
+                       (hipStream_t)stream, q, (long)q_stride_req, (long)q_stride_head, k_cache,
+                       (long)k_stride_block, (long)k_stride_tok, (long)k_stride_head, v_cache,
+                       (long)v_stride_block, (long)v_stride_tok, (long)v_stride_head, num_blocks,
+                       block_table, (long)bt_stride, bt_cols, page_table, (long)pt_stride_req,
+                       (long)pt_stride_head, pt_cols, page_cnt, (long)cnt_stride, seq_lens,
+                       m_part, l_part, acc_part, G, split, pps_min, sm_scale);
+    return check_launch("decode_split_kernel");
+}
+
+extern "C" int32_t locks_decode_merge(
+    const float* m_part, const float* l_part, const float* acc_part,
+    const int32_t* page_cnt, int64_t cnt_stride, void* out, int64_t out_stride_req,
+    int64_t out_stride_head, int32_t out_is_f32, int32_t n_req, int32_t n_kv, int32_t G,
+    int32_t head_dim, int32_t split, int32_t pps_min, void* stream)
+{
+    LOCKS_REQUIRE(head_dim == DC_D, "locks_decode_merge: head_dim %d unsupported (this build: 128)", head_dim);
+    LOCKS_REQUIRE(G >= 1 && G <= 16, "locks_decode_merge: G=%d outside [1, 16]", G);
+    LOCKS_REQUIRE(split >= 1 && split <= MAX_SPLIT, "locks_decode_merge: split %d outside [1, %d]", split, MAX_SPLIT);
+    LOCKS_REQUIRE(pps_min >= 1, "locks_decode_merge: pps_min %d < 1", pps_min);
+    LOCKS_REQUIRE(m_part && l_part && acc_part && page_cnt && out, "locks_decode_merge: null pointer argument");
+    if (n_req == 0) return 0;
+    hipLaunchKernelGGL(decode_merge_kernel, dim3(n_kv, n_req), dim3(MG_BLK), 0, (hipStream_t)stream,
+                       m_part, l_part, acc_part, page_cnt, (long)cnt_stride, out, (long)out_stride_req,
+                       (long)out_stride_head, out_is_f32, G, split, pps_min);
+    return check_launch("decode_merge_kernel");
+}

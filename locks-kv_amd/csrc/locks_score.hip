@@ -1,0 +1,318 @@
+// rki4 page scorer for gfx950 (CDNA4).
+//
+// Computes, for every selectable logical page p < n_sel_hi[r] of request r
+// and kv head kh, the per-query-head page log-sum-exp estimate from the
+// packed rank-8 int4 summary (reference: selection/rki4_score_cuda.py:653-722,
+// fp32 twin selection/rki4_score_torch.py:111-160):
+//
+//   q8 = rint(q / qs), qs = max(|q|_inf, 1e-8) / 127           (per head)
+//   qt[g][c]  = (sum_d V4[c][d] * q8[g][d]) * qs[g] * vs[c]      c < 8
+//   mud[g]    = (sum_d mu8[d]   * q8[g][d]) * qs[g] * mus
+//   tok[g][t] = s * (cs[t] * sum_c c8[t][c] * qt[g][c] + mud[g])   t < 16
+//   score_h[g][p] = LSE_t tok[g][t]
+//
+// MI355X mapping.  One workgroup = 4 waves owns a contiguous chunk of pages
+// of one (request, kv head); a wave handles 8 pages per tile:
+//   * the int4 x int8 projection of the whole GQA group runs on the matrix
+//     core: v_mfma_i32_16x16x64_i8 with A = q8 (16 head rows, zero padded)
+//     and B = 2 pages x 8 basis columns.  The int4 nibbles are fed BIASED
+//     (n ^ 8 = V + 8, one AND per 4 values, no sign extension) and the
+//     +8 * sum_d q8 plane is removed exactly in int32 afterwards;
+//   * mu . q8 uses the same MFMA with B = one mu row per column (page);
+//   * the per-token reconstruction sum_c c8[t][c] qt[g][c] is a 16x8 by
+//     8xG product per page: v_mfma_f32_16x16x4_f32 with pages packed side by
+//     side when G < 16 (block-diagonal B), so the VALU only does the cs/mu
+//     epilogue and the 16-token LSE (4 tokens per lane + 2 cross-row steps).
+// Summary bytes are read exactly once, straight from the six slabs through
+// the block table.  Per-WG page maxima are published to `pmax` so the
+// selector can form the per-head max without re-reading score_h.
+#include "locks_common.h"
+#include "locks_hip.h"
+
+namespace locks {
+
+constexpr int SC_D = 128;     // head dim (geometry contract of this build)
+constexpr int SC_PG = 16;     // page size
+constexpr int SC_RNK = 8;     // summary rank
+constexpr int SC_TILE = 8;    // pages per wave tile
+constexpr int SC_WAVES = 4;
+constexpr int SC_BLOCK = SC_WAVES * kWave;
+constexpr int SC_VROW = SC_RNK * SC_D / 2;   // 512 B of packed V per row
+
+__device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d) {
+    return (uint32_t)(uint8_t)a | ((uint32_t)(uint8_t)b << 8) |
+           ((uint32_t)(uint8_t)c << 16) | ((uint32_t)(uint8_t)d << 24);
+}
+
+template <int GW>
+__global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
+    const uint16_t* __restrict__ q, long q_sr, long q_sh,
+    const uint8_t* __restrict__ v4, const uint16_t* __restrict__ vs,
+    const int8_t* __restrict__ c8, const uint16_t* __restrict__ cs,
+    const int8_t* __restrict__ mu8, const uint16_t* __restrict__ mus,
+    int NB, const int* __restrict__ bt, long bt_sr, int bt_cols,
+    const int* __restrict__ nsh, float* __restrict__ score_h, int MP,
+    float* __restrict__ pmax, int G, float sm_scale, int chunk)
+{
+    constexpr int PPM = 16 / GW;            // pages per token-stage MFMA
+    constexpr int NGRP = SC_TILE / PPM;     // token-stage groups per tile
+    const int z = blockIdx.x, kh = blockIdx.y, r = blockIdx.z;
+    const int n_kv = gridDim.y, Z = gridDim.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const long rk = (long)r * n_kv + kh;
+    const int P = min(nsh[r], MP);        // never score past the score_h row
+    const int c0 = z * chunk;
+    const int c1 = min(c0 + chunk, P);
+
+    if (c0 >= P) {                          // no page of this chunk is scored
+        if (tid < 16) pmax[(rk * Z + z) * 16 + tid] = -INFINITY;
+        return;
+    }
+
+    __shared__ float qf[16][SC_D];
+    __shared__ __attribute__((aligned(16))) int8_t q8s[16][SC_D];
+    __shared__ float qs_s[16];
+    __shared__ int qsum_s[16];
+    __shared__ __attribute__((aligned(16))) float qt_l[SC_WAVES][SC_TILE][SC_RNK][16];
+    __shared__ __attribute__((aligned(16))) float mud_l[SC_WAVES][SC_TILE][16];
+    __shared__ float wmax[SC_WAVES][16];
+
+    // ---- stage q (bf16 -> fp32), per-head int8 quantization -------------
+    for (int i = tid; i < 16 * SC_D; i += SC_BLOCK) {
+        const int g = i / SC_D, d = i % SC_D;
+        float v = 0.f;
+        if (g < G) v = bf16_to_f32(q[(long)r * q_sr + (long)(kh * G + g) * q_sh + d]);
+        qf[g][d] = v;
+    }
+    if (tid < SC_WAVES * 16) wmax[tid >> 4][tid & 15] = -INFINITY;
+    __syncthreads();
+    for (int g = wave; g < 16; g += SC_WAVES) {
+        const float a0 = qf[g][lane], a1 = qf[g][lane + 64];
+        const float am = wave_max(fmaxf(fabsf(a0), fabsf(a1)));
+        const float qs = fmaxf(am, 1e-8f) / 127.f;
+        int i0 = (int)rintf(__fdiv_rn(a0, qs));
+        int i1 = (int)rintf(__fdiv_rn(a1, qs));
+        if (g >= G) { i0 = 0; i1 = 0; }
+        q8s[g][lane] = (int8_t)i0;
+        q8s[g][lane + 64] = (int8_t)i1;
+        const int s = wave_sum_i(i0 + i1);
+        if (lane == 0) { qs_s[g] = (g < G) ? qs : 0.f; qsum_s[g] = s; }
+    }
+    __syncthreads();
+
+    // ---- per-lane MFMA A operands (constant across pages) ----------------
+    const int r16 = lane & 15, kg = lane >> 4;
+    v4i Av[2], Amu[2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+        const int8_t* qr = &q8s[r16][32 * kg + 16 * s];
+        // V operand order inside a 16-d window: even d (low nibbles) then odd d
+        Av[s][0] = (int)pack4_i8(qr[0], qr[2], qr[4], qr[6]);
+        Av[s][1] = (int)pack4_i8(qr[8], qr[10], qr[12], qr[14]);
+        Av[s][2] = (int)pack4_i8(qr[1], qr[3], qr[5], qr[7]);
+        Av[s][3] = (int)pack4_i8(qr[9], qr[11], qr[13], qr[15]);
+        Amu[s] = *reinterpret_cast<const v4i*>(qr);      // natural d order
+    }
+    float qs_row[4];
+    int qbias[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        qs_row[v] = qs_s[4 * kg + v];
+        qbias[v] = 8 * qsum_s[4 * kg + v];
+    }
+
+    const int jcol = lane & 15;
+    const int psub_l = jcol / GW;            // page slot of this lane's column
+    const int g_l = jcol % GW;               // head of this lane's column
+    float hmax = -INFINITY;
+    const uint32_t M4 = 0x0F0F0F0Fu;
+
+    const int n_tiles = cdiv(c1 - c0, SC_TILE);
+    for (int tt = wave; tt < n_tiles; tt += SC_WAVES) {
+        const int p0 = c0 + tt * SC_TILE;
+        const int nvalid = min(SC_TILE, c1 - p0);
+        // lane i (< 8) resolves the block of page p0 + i (clamped to the tile)
+        int pg = p0 + min(lane & 7, nvalid - 1);
+        pg = min(pg, bt_cols - 1);
+        int blk = bt[(long)r * bt_sr + pg];
+        blk = min(max(blk, 0), NB - 1);
+        int blkv[SC_TILE];
+#pragma unroll
+        for (int i = 0; i < SC_TILE; ++i) blkv[i] = __shfl(blk, i, kWave);
+        const long myrow = (long)blk * n_kv + kh;
+
+        // ---- issue every load of the tile up front -----------------------
+        uint4 vv[4];
+        float vsf[4];
+#pragma unroll
+        for (int pp = 0; pp < 4; ++pp) {
+            const int b = (lane & 8) ? blkv[2 * pp + 1] : blkv[2 * pp];
+            const long row = (long)b * n_kv + kh;
+            vv[pp] = *reinterpret_cast<const uint4*>(
+                v4 + row * SC_VROW + (lane & 7) * (SC_D / 2) + kg * 16);
+            vsf[pp] = bf16_to_f32(vs[row * SC_RNK + (lane & 7)]);
+        }
+        v4i mu0 = {0, 0, 0, 0}, mu1 = {0, 0, 0, 0};
+        float musf = 0.f;
+        if ((lane & 15) < 8) {
+            const int8_t* mp = mu8 + myrow * SC_D + kg * 32;
+            mu0 = *reinterpret_cast<const v4i*>(mp);
+            mu1 = *reinterpret_cast<const v4i*>(mp + 16);
+            musf = bf16_to_f32(mus[myrow]);
+        }
+        uint2 c8r[SC_TILE];
+#pragma unroll
+        for (int i = 0; i < SC_TILE; ++i) {
+            const long row = (long)blkv[i] * n_kv + kh;
+            c8r[i] = *reinterpret_cast<const uint2*>(c8 + row * (SC_PG * SC_RNK) + r16 * SC_RNK);
+        }
+        uint2 csv[NGRP];
+#pragma unroll
+        for (int gi = 0; gi < NGRP; ++gi) {
+            int b = blkv[gi * PPM];
+#pragma unroll
+            for (int u = 1; u < PPM; ++u) b = (psub_l == u) ? blkv[gi * PPM + u] : b;
+            const long row = (long)b * n_kv + kh;
+            csv[gi] = *reinterpret_cast<const uint2*>(cs + row * SC_PG + 4 * kg);
+        }
+
+        // ---- projection: qt (GQA group x 8 basis columns) per page -------
+#pragma unroll
+        for (int pp = 0; pp < 4; ++pp) {
+            const uint32_t w0 = vv[pp].x ^ 0x88888888u, w1 = vv[pp].y ^ 0x88888888u;
+            const uint32_t w2 = vv[pp].z ^ 0x88888888u, w3 = vv[pp].w ^ 0x88888888u;
+            const v4i b0 = {(int)(w0 & M4), (int)(w1 & M4), (int)((w0 >> 4) & M4), (int)((w1 >> 4) & M4)};
+            const v4i b1 = {(int)(w2 & M4), (int)(w3 & M4), (int)((w2 >> 4) & M4), (int)((w3 >> 4) & M4)};
+            v4i acc = {0, 0, 0, 0};
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(Av[0], b0, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(Av[1], b1, acc, 0, 0, 0);
+            float4 qt;
+            qt.x = (float)(acc[0] - qbias[0]) * qs_row[0] * vsf[pp];
+            qt.y = (float)(acc[1] - qbias[1]) * qs_row[1] * vsf[pp];
+            qt.z = (float)(acc[2] - qbias[2]) * qs_row[2] * vsf[pp];
+            qt.w = (float)(acc[3] - qbias[3]) * qs_row[3] * vsf[pp];
+            *reinterpret_cast<float4*>(&qt_l[wave][2 * pp + ((lane & 15) >> 3)][lane & 7][4 * kg]) = qt;
+        }
+        {
+            v4i accm = {0, 0, 0, 0};
+            accm = __builtin_amdgcn_mfma_i32_16x16x64_i8(Amu[0], mu0, accm, 0, 0, 0);
+            accm = __builtin_amdgcn_mfma_i32_16x16x64_i8(Amu[1], mu1, accm, 0, 0, 0);
+            if ((lane & 15) < 8) {
+                float4 md;
+                md.x = (float)accm[0] * qs_row[0] * musf;
+                md.y = (float)accm[1] * qs_row[1] * musf;
+                md.z = (float)accm[2] * qs_row[2] * musf;
+                md.w = (float)accm[3] * qs_row[3] * musf;
+                *reinterpret_cast<float4*>(&mud_l[wave][lane & 15][4 * kg]) = md;
+            }
+        }
+        wave_lds_sync();
+
+        // ---- token reconstruction + 16-token LSE per (page, head) --------
+#pragma unroll
+        for (int gi = 0; gi < NGRP; ++gi) {
+            v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < 2 * PPM; ++s) {
+                const int psub = s >> 1;
+                const int page = gi * PPM + psub;
+                const int cc = kg + 4 * (s & 1);
+                const uint32_t word = (s & 1) ? c8r[page].y : c8r[page].x;
+                const float a = (float)(int8_t)(word >> (8 * kg));
+                const float b = (psub_l == psub) ? qt_l[wave][page][cc][g_l] : 0.f;
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc, 0, 0, 0);
+            }
+            const int page = gi * PPM + psub_l;
+            const float mud = mud_l[wave][page][g_l];
+            const float cs0 = bf16lo(csv[gi].x), cs1 = bf16hi(csv[gi].x);
+            const float cs2 = bf16lo(csv[gi].y), cs3 = bf16hi(csv[gi].y);
+            const float t0 = sm_scale * fmaf(acc[0], cs0, mud);
+            const float t1 = sm_scale * fmaf(acc[1], cs1, mud);
+            const float t2 = sm_scale * fmaf(acc[2], cs2, mud);
+            const float t3 = sm_scale * fmaf(acc[3], cs3, mud);
+            float m = fmaxf(fmaxf(t0, t1), fmaxf(t2, t3));
+            m = fmaxf(m, __shfl_xor(m, 16, kWave));
+            m = fmaxf(m, __shfl_xor(m, 32, kWave));
+            float e = __expf(t0 - m) + __expf(t1 - m) + __expf(t2 - m) + __expf(t3 - m);
+            e += __shfl_xor(e, 16, kWave);
+            e += __shfl_xor(e, 32, kWave);
+            const float S = m + __logf(e);
+            const bool valid = (page < nvalid) && (g_l < G);
+            if (valid) {
+                hmax = fmaxf(hmax, S);
+                if (lane < 16) score_h[(rk * G + g_l) * (long)MP + p0 + page] = S;
+            }
+        }
+        wave_lds_sync();
+    }
+
+    // ---- publish this chunk's per-head page maxima -----------------------
+#pragma unroll
+    for (int o = GW; o < 16; o <<= 1) hmax = fmaxf(hmax, __shfl_xor(hmax, o, kWave));
+    if (lane < GW) wmax[wave][lane] = hmax;
+    __syncthreads();
+    if (tid < 16) {
+        float m = wmax[0][tid];
+#pragma unroll
+        for (int w = 1; w < SC_WAVES; ++w) m = fmaxf(m, wmax[w][tid]);
+        pmax[(rk * Z + z) * 16 + tid] = m;
+    }
+}
+
+}  // namespace locks
+
+using namespace locks;
+
+extern "C" int32_t locks_score_auto_chunk(int32_t n_req, int32_t n_kv, int32_t max_pages) {
+    // Aim for ~4 workgroups per CU on a 256-CU MI355X at the configured
+    // (n_req x n_kv) base grid, in whole 32-page units.
+    const long units = (long)cdiv(max_pages > 0 ? max_pages : 1, 32);
+    const long base = (long)(n_req > 0 ? n_req : 1) * (n_kv > 0 ? n_kv : 1);
+    long z_target = (1024 + base - 1) / base;
+    if (z_target < 1) z_target = 1;
+    long per = (units + z_target - 1) / z_target;
+    if (per < 1) per = 1;
+    if (per > 32) per = 32;      // <= 1024 pages per workgroup
+    return (int32_t)(per * 32);
+}
+
+extern "C" int32_t locks_score_num_chunks(int32_t max_pages, int32_t chunk) {
+    if (chunk <= 0) return -1;
+    return cdiv(max_pages > 0 ? max_pages : 1, chunk);
+}
+
+extern "C" int32_t locks_score_rki4(
+    const uint16_t* q, int64_t q_stride_req, int64_t q_stride_head,
+    const uint8_t* v4, const uint16_t* vs, const int8_t* c8, const uint16_t* cs,
+    const int8_t* mu8, const uint16_t* mus, int32_t num_blocks,
+    const int32_t* block_table, int64_t bt_stride, int32_t bt_cols,
+    const int32_t* n_sel_hi, float* score_h, int32_t max_pages,
+    float* page_max, int32_t chunk,
+    int32_t n_req, int32_t n_kv, int32_t G, int32_t head_dim, int32_t page,
+    float sm_scale, void* stream)
+{
+    LOCKS_REQUIRE(head_dim == SC_D, "locks_score_rki4: head_dim %d unsupported (this build: 128)", head_dim);
+    LOCKS_REQUIRE(page == SC_PG, "locks_score_rki4: page %d unsupported (this build: 16)", page);
+    LOCKS_REQUIRE(G >= 1 && G <= 16, "locks_score_rki4: G=%d outside [1, 16]", G);
+    LOCKS_REQUIRE(n_req >= 0 && n_kv >= 1, "locks_score_rki4: bad n_req=%d n_kv=%d", n_req, n_kv);
+    LOCKS_REQUIRE(num_blocks >= 1 && bt_cols >= 1 && max_pages >= 1,
+                  "locks_score_rki4: empty geometry (num_blocks=%d bt_cols=%d max_pages=%d)",
+                  num_blocks, bt_cols, max_pages);
+    LOCKS_REQUIRE(chunk >= 32 && chunk % 32 == 0, "locks_score_rki4: chunk %d must be a positive multiple of 32", chunk);
+    LOCKS_REQUIRE(q && v4 && vs && c8 && cs && mu8 && mus && block_table && n_sel_hi && score_h && page_max,
+                  "locks_score_rki4: null pointer argument");
+    if (n_req == 0) return 0;
+    const int Z = cdiv(max_pages, chunk);
+    dim3 grid(Z, n_kv, n_req);
+    hipStream_t st = (hipStream_t)stream;
+#define LAUNCH(GWV)                                                                   \
+    hipLaunchKernelGGL(rki4_score_kernel<GWV>, grid, dim3(SC_BLOCK), 0, st, q,         \
+                       (long)q_stride_req, (long)q_stride_head, v4, vs, c8, cs, mu8, mus, \
+                       num_blocks, block_table, (long)bt_stride, bt_cols, n_sel_hi,       \
+                       score_h, max_pages, page_max, G, sm_scale, chunk)
+    if (G <= 4) LAUNCH(4);
+    else if (G <= 8) LAUNCH(8);
+    else LAUNCH(16);
+#undef LAUNCH
+    return check_launch("rki4_score_kernel");
+}

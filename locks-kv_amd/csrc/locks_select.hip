@@ -1,0 +1,443 @@
+// GQA combine + exact top-b page selection for gfx950, and the per-step
+// page-parameter derivation.
+//
+// Semantics (reference: selection/select_cuda.py:547-828 fused nrm+top-b,
+// selection/select.py:28-58 derive, selection/select.py:123-180 top-b twin):
+//   hm[g]    = max_{0<=p<nsh} score_h[g][p]                    ("nrm" only)
+//   score[p] = sum_{g ascending} exp(score_h[g][p] - hm[g])    ("nrm")
+//            = max_g score_h[g][p]                             ("max")
+//   keep     = top-b of the selectable slice [sink, nsh) under the total
+//              order (score descending, page ascending) -- i.e. every page
+//              above the b-th largest score tau plus the lowest-index pages
+//              equal to tau up to exactly b -- U [0, sink) U [nsh, npg);
+//              (nsh - sink) <= 1 keeps every page of [0, npg).
+//   page_table[r][kh][:cnt] = kept pages ascending, -1 after; page_cnt = cnt.
+//
+// MI355X design.  At 1M context one (request, kv head) has 65536 pages and
+// bs=1 GLM has only two such groups, so a one-workgroup-per-group selector
+// would read 4 MB of score_h through a single CU.  Instead:
+//   sel_chunk_kernel  (grid: page chunks x kv heads x requests)
+//       forms hm from the scorer's per-chunk maxima, combines its 2048-page
+//       chunk, writes `score`, prefills its slice of page_table with -1, and
+//       emits the chunk's local top-b candidates (the total order restricted
+//       to a chunk keeps every globally kept page of that chunk) in ascending
+//       page order.  When one chunk covers the whole row it finishes the
+//       selection itself (one launch).
+//   sel_finish_kernel (grid: kv heads x requests)
+//       gathers the <= b candidates of every chunk into LDS, radix-selects
+//       the exact b-th largest key and compacts the kept pages.
+// Radix keys are the order-preserving fp32 -> u32 map; the keep test is a
+// key compare, so it is exact for every finite score.
+#include "locks_common.h"
+#include "locks_hip.h"
+
+namespace locks {
+
+constexpr int SEL_CH = 2048;       // pages per chunk workgroup
+constexpr int SEL_BLK = 512;       // threads per chunk workgroup
+constexpr int FIN_BLK = 1024;      // threads of the finishing workgroup
+constexpr int FIN_CAP = 6144;      // candidates held in LDS by the finisher
+constexpr int FIN_MAXZ = 1024;     // chunks per row the finisher can index
+
+// ---------------------------------------------------------------------------
+// block primitives
+// ---------------------------------------------------------------------------
+template <int BLK>
+__device__ __forceinline__ int block_excl_scan(int v, int* wsum, int& total) {
+    constexpr int NW = BLK / kWave;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    int incl = v;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+        const int t = __shfl_up(incl, o, kWave);
+        if (lane >= o) incl += t;
+    }
+    if (lane == kWave - 1) wsum[w] = incl;
+    __syncthreads();
+    if (w == 0) {
+        const int x = (lane < NW) ? wsum[lane] : 0;
+        int xi = x;
+#pragma unroll
+        for (int o = 1; o < kWave; o <<= 1) {
+            const int t = __shfl_up(xi, o, kWave);
+            if (lane >= o) xi += t;
+        }
+        if (lane < NW) wsum[lane] = xi - x;
+        if (lane == NW - 1) wsum[NW] = xi;
+    }
+    __syncthreads();
+    const int res = wsum[w] + incl - v;
+    total = wsum[NW];
+    __syncthreads();
+    return res;
+}
+
+// k-th largest (1 <= k <= n) u32 key by 4 passes of 8-bit MSD radix.  If a
+// pass finds that the whole boundary bin is needed it stops early and the
+// returned value has zero low digits (then #(key >= result) == k exactly).
+template <int BLK>
+__device__ uint32_t block_kth_largest(const uint32_t* keys, int n, int k, int* hist, int* s3) {
+    const int tid = threadIdx.x;
+    uint32_t prefix = 0u, kmask = 0u;
+    for (int digit = 0; digit < 4; ++digit) {
+        const int shift = 24 - 8 * digit;
+        for (int i = tid; i < 256; i += BLK) hist[i] = 0;
+        __syncthreads();
+        for (int i = tid; i < n; i += BLK) {
+            const uint32_t u = keys[i];
+            if ((u & kmask) == prefix) atomicAdd(&hist[(u >> shift) & 0xFF], 1);
+        }
+        __syncthreads();
+        if (tid < kWave) {
+            const int lane = tid;
+            const int seg = hist[4 * lane] + hist[4 * lane + 1] + hist[4 * lane + 2] + hist[4 * lane + 3];
+            int suf = seg;
+#pragma unroll
+            for (int o = 1; o < kWave; o <<= 1) {
+                const int t = __shfl_down(suf, o, kWave);
+                if (lane + o < kWave) suf += t;
+            }
+            const int above = suf - seg;
+            if (above < k && k <= suf) {
+                int acc = above, sel = 4 * lane, cb = 0;
+                for (int d = 4 * lane + 3; d >= 4 * lane; --d) {
+                    const int c = hist[d];
+                    if (acc + c >= k) { sel = d; cb = c; break; }
+                    acc += c;
+                }
+                s3[0] = sel;
+                s3[1] = k - acc;
+                s3[2] = cb;
+            }
+        }
+        __syncthreads();
+        prefix |= ((uint32_t)s3[0]) << shift;
+        k = s3[1];
+        const int cb = s3[2];
+        kmask |= 0xFFu << shift;
+        __syncthreads();
+        if (k == cb) break;
+    }
+    return prefix;
+}
+
+// Ordered emission of the top-k of keys[0, n) (page order) under
+// (key descending, index ascending): every key > tau plus the first
+// (k - #(>tau)) keys == tau.  Writes out_page[pos] = page_of(i) and, if
+// out_key != nullptr, out_key[pos] = key.  Returns the count (== k).
+template <int BLK, class PageOf>
+__device__ int emit_topk(const uint32_t* keys, int n, int k, uint32_t tau, PageOf page_of,
+                         int* out_page, uint32_t* out_key, int* wsum) {
+    const int tid = threadIdx.x;
+    const int E = cdiv(n, BLK);
+    const int i0 = min(tid * E, n), i1 = min(i0 + E, n);
+    int gt = 0, eq = 0;
+    for (int i = i0; i < i1; ++i) {
+        const uint32_t u = keys[i];
+        gt += (u > tau);
+        eq += (u == tau);
+    }
+    int gt_tot, eq_tot;
+    block_excl_scan<BLK>(gt, wsum, gt_tot);
+    const int eq_excl = block_excl_scan<BLK>(eq, wsum, eq_tot);
+    const int quota = k - gt_tot;
+    const int mine = gt + min(max(quota - eq_excl, 0), eq);
+    int total;
+    int pos = block_excl_scan<BLK>(mine, wsum, total);
+    int er = eq_excl;
+    for (int i = i0; i < i1; ++i) {
+        const uint32_t u = keys[i];
+        bool kp = u > tau;
+        if (u == tau) { kp = er < quota; ++er; }
+        if (kp) {
+            out_page[pos] = page_of(i);
+            if (out_key) out_key[pos] = u;
+            ++pos;
+        }
+    }
+    return total;
+}
+
+__device__ __forceinline__ void fill_all_pages(int* row, int n_pages, int MP, bool pad) {
+    for (int i = threadIdx.x; i < MP; i += blockDim.x) {
+        if (i < n_pages) row[i] = i;
+        else if (pad) row[i] = -1;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// chunk kernel
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(SEL_BLK) void sel_chunk_kernel(
+    const float* __restrict__ score_h, const float* __restrict__ pmax, int Zs,
+    const int* __restrict__ npg, const int* __restrict__ nsh, const int* __restrict__ bfix,
+    float* __restrict__ score, int* __restrict__ page_table, int* __restrict__ page_cnt,
+    uint32_t* __restrict__ cand_key, int* __restrict__ cand_page, int* __restrict__ cand_cnt,
+    int n_sink, int MP, int G, int combine)
+{
+    const int z = blockIdx.x, kh = blockIdx.y, r = blockIdx.z;
+    const int n_kv = gridDim.y, Z1 = gridDim.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const long rk = (long)r * n_kv + kh;
+    const int n_pages = min(npg[r], MP);
+    const int n_sel_hi = min(nsh[r], MP);
+    const int n_sel = n_sel_hi - n_sink;
+    const bool keep_all = n_sel <= 1;
+    int b = bfix[r];
+    b = max(1, min(b, max(n_sel, 1)));
+    const bool final_mode = (Z1 == 1);
+    const int c0 = z * SEL_CH;
+    const int c1 = min(c0 + SEL_CH, MP);
+
+    __shared__ float hm[16];
+    __shared__ uint32_t keys[SEL_CH];
+    __shared__ int hist[256];
+    __shared__ int s3[4];
+    __shared__ int wsum[SEL_BLK / kWave + 1];
+
+    int* trow = page_table + rk * (long)MP;
+    if (!final_mode) {
+        for (int i = c0 + tid; i < c1; i += SEL_BLK) trow[i] = -1;
+    }
+
+    // ---- per-head page max from the scorer's chunk maxima ("nrm") --------
+    if (combine == 0) {
+        for (int g = wave; g < G; g += SEL_BLK / kWave) {
+            float m = -INFINITY;
+            for (int zz = lane; zz < Zs; zz += kWave) m = fmaxf(m, pmax[(rk * Zs + zz) * 16 + g]);
+            m = wave_max(m);
+            if (lane == 0) hm[g] = m;
+        }
+        __syncthreads();
+    }
+
+    // ---- combine: score[p] for p < nsh, keys for the selectable slice ----
+    const float* shb = score_h + rk * (long)G * MP;
+    for (int p = c0 + tid; p < min(c1, max(n_sel_hi, c0)); p += SEL_BLK) {
+        float acc;
+        if (combine == 0) {
+            acc = 0.f;
+            for (int g = 0; g < G; ++g) acc += __expf(shb[(long)g * MP + p] - hm[g]);
+        } else {
+            acc = shb[p];
+            for (int g = 1; g < G; ++g) acc = fmaxf(acc, shb[(long)g * MP + p]);
+        }
+        score[rk * (long)MP + p] = acc;
+        keys[p - c0] = f2u(acc);
+    }
+    __syncthreads();
+
+    const int lo_c = min(max(n_sink, c0), c1) - c0;       // selectable slice of
+    const int hi_c = max(min(n_sel_hi, c1), c0) - c0;     // this chunk, local idx
+    const int n_loc = max(hi_c - lo_c, 0);
+
+    if (final_mode) {
+        // the whole row lives in this chunk: finish here
+        if (keep_all || b >= n_sel) {
+            fill_all_pages(trow, max(n_pages, 0), MP, true);
+            if (tid == 0) page_cnt[rk] = max(n_pages, 0);
+            return;
+        }
+        const uint32_t tau = block_kth_largest<SEL_BLK>(keys + lo_c, n_loc, b, hist, s3);
+        const int nsel_w = emit_topk<SEL_BLK>(keys + lo_c, n_loc, b, tau,
+                                              [&](int i) { return n_sink + i; },
+                                              trow + n_sink, nullptr, wsum);
+        const int cnt = n_sink + nsel_w + (n_pages - n_sel_hi);
+        for (int i = tid; i < MP; i += SEL_BLK) {
+            if (i < n_sink) trow[i] = i;
+            else if (i >= n_sink + nsel_w && i < cnt) trow[i] = n_sel_hi + (i - n_sink - nsel_w);
+            else if (i >= cnt) trow[i] = -1;
+        }
+        if (tid == 0) page_cnt[rk] = cnt;
+        return;
+    }
+
+    // ---- multi-chunk: emit this chunk's local top-min(b, n_loc) ----------
+    uint32_t* ck = cand_key + (rk * Z1 + z) * (long)SEL_CH;
+    int* cp = cand_page + (rk * Z1 + z) * (long)SEL_CH;
+    int ncand = 0;
+    if (!keep_all && n_loc > 0) {
+        const int k_loc = min(b, n_loc);
+        uint32_t tau = 0u;   // k_loc == n_loc: every key >= 0 is kept
+        if (k_loc < n_loc) tau = block_kth_largest<SEL_BLK>(keys + lo_c, n_loc, k_loc, hist, s3);
+        const int base = c0 + lo_c;
+        ncand = emit_topk<SEL_BLK>(keys + lo_c, n_loc, k_loc, tau,
+                                   [&](int i) { return base + i; }, cp, ck, wsum);
+    }
+    if (tid == 0) cand_cnt[rk * Z1 + z] = ncand;
+}
+
+// ---------------------------------------------------------------------------
+// finishing kernel (multi-chunk rows)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(FIN_BLK) void sel_finish_kernel(
+    const int* __restrict__ npg, const int* __restrict__ nsh, const int* __restrict__ bfix,
+    int* __restrict__ page_table, int* __restrict__ page_cnt,
+    const uint32_t* __restrict__ cand_key, const int* __restrict__ cand_page,
+    const int* __restrict__ cand_cnt, uint32_t* __restrict__ spill_key, int* __restrict__ spill_page,
+    int n_sink, int MP, int Z1)
+{
+    const int kh = blockIdx.y, r = blockIdx.z;
+    const int n_kv = gridDim.y;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    constexpr int NWV = FIN_BLK / kWave;
+    const long rk = (long)r * n_kv + kh;
+    const int n_pages = min(npg[r], MP);
+    const int n_sel_hi = min(nsh[r], MP);
+    const int n_sel = n_sel_hi - n_sink;
+    const bool keep_all = n_sel <= 1;
+    int b = bfix[r];
+    b = max(1, min(b, max(n_sel, 1)));
+    int* trow = page_table + rk * (long)MP;
+
+    if (keep_all || b >= n_sel) {
+        for (int i = tid; i < max(n_pages, 0); i += FIN_BLK) trow[i] = i;
+        if (tid == 0) page_cnt[rk] = max(n_pages, 0);
+        return;
+    }
+
+    __shared__ int offs[FIN_MAXZ + 1];
+    __shared__ uint32_t lkey[FIN_CAP];
+    __shared__ int lpage[FIN_CAP];
+    __shared__ int hist[256];
+    __shared__ int s3[4];
+    __shared__ int wsum[NWV + 1];
+
+    // exclusive scan of the chunk candidate counts
+    {
+        int run = 0;
+        for (int base = 0; base < Z1; base += FIN_BLK) {
+            const int zz = base + tid;
+            const int c = (zz < Z1) ? cand_cnt[rk * Z1 + zz] : 0;
+            int tot;
+            const int ex = block_excl_scan<FIN_BLK>(c, wsum, tot);
+            if (zz < Z1) offs[zz] = run + ex;
+            run += tot;
+        }
+        if (tid == 0) offs[Z1] = run;
+        __syncthreads();
+    }
+    const int N = offs[Z1];
+    uint32_t* kk = (N <= FIN_CAP) ? lkey : spill_key + rk * (long)MP;
+    int* pp = (N <= FIN_CAP) ? lpage : spill_page + rk * (long)MP;
+
+    // gather: wave w copies chunks w, w + NWV, ... (chunk order == page order)
+    for (int zz = wave; zz < Z1; zz += NWV) {
+        const int o = offs[zz], c = offs[zz + 1] - o;
+        const uint32_t* sk = cand_key + (rk * Z1 + zz) * (long)SEL_CH;
+        const int* sp = cand_page + (rk * Z1 + zz) * (long)SEL_CH;
+        for (int i = lane; i < c; i += kWave) {
+            kk[o + i] = sk[i];
+            pp[o + i] = sp[i];
+        }
+    }
+    __syncthreads();
+
+    const uint32_t tau = block_kth_largest<FIN_BLK>(kk, N, b, hist, s3);
+    const int nsel_w = emit_topk<FIN_BLK>(kk, N, b, tau, [&](int i) { return pp[i]; },
+                                          trow + n_sink, nullptr, wsum);
+    const int cnt = n_sink + nsel_w + (n_pages - n_sel_hi);
+    for (int i = tid; i < n_sink; i += FIN_BLK) trow[i] = i;
+    for (int i = n_sink + nsel_w + tid; i < cnt; i += FIN_BLK) trow[i] = n_sel_hi + (i - n_sink - nsel_w);
+    if (tid == 0) page_cnt[rk] = cnt;
+}
+
+// ---------------------------------------------------------------------------
+// derive (select.py:28-58)
+// ---------------------------------------------------------------------------
+__global__ void derive_kernel(const int* __restrict__ seq_lens, int n_req, int page, int window,
+                              int sink, int budget_abs, double budget, int* __restrict__ npg_o,
+                              int* __restrict__ nsh_o, int* __restrict__ b_o) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n_req; i += gridDim.x * blockDim.x) {
+        const int sl = seq_lens[i];
+        const int npg = (sl + page - 1) / page;
+        const int nsh = npg - window;
+        const int s = nsh - sink;
+        int b;
+        if (budget_abs > 0) {
+            b = min(budget_abs, max(s, 1));
+            b = max(b, 1);
+        } else {
+            const double bf = ceil((double)s * budget);
+            b = min(max((int)bf, 1), max(s, 1));
+        }
+        npg_o[i] = npg;
+        nsh_o[i] = nsh;
+        b_o[i] = b;
+    }
+}
+
+}  // namespace locks
+
+using namespace locks;
+
+extern "C" int64_t locks_select_workspace_bytes(int32_t n_req, int32_t n_kv, int32_t max_pages) {
+    if (n_req < 0 || n_kv < 1 || max_pages < 1) return -1;
+    const long Z1 = cdiv(max_pages, SEL_CH);
+    const long rows = (long)n_req * n_kv;
+    const long cand = rows * Z1 * SEL_CH;               // key + page per slot
+    const long spill = rows * (long)max_pages;           // key + page per page
+    const long counts = rows * Z1;
+    long bytes = cand * 8 + spill * 8 + counts * 4;
+    return (bytes + 255) / 256 * 256;
+}
+
+extern "C" int32_t locks_select_nrm_topb(
+    const float* score_h, const float* page_max, int32_t score_chunks,
+    const int32_t* n_pages, const int32_t* n_sel_hi, const int32_t* b_fix,
+    float* score, int32_t* page_table, int32_t* page_cnt,
+    void* workspace, int64_t workspace_bytes,
+    int32_t n_req, int32_t n_kv, int32_t G, int32_t n_sink, int32_t max_pages,
+    int32_t combine, void* stream)
+{
+    LOCKS_REQUIRE(G >= 1 && G <= 16, "locks_select_nrm_topb: G=%d outside [1, 16]", G);
+    LOCKS_REQUIRE(n_req >= 0 && n_kv >= 1 && max_pages >= 1, "locks_select_nrm_topb: bad geometry");
+    LOCKS_REQUIRE(n_sink >= 0, "locks_select_nrm_topb: n_sink=%d < 0", n_sink);
+    LOCKS_REQUIRE(combine == 0 || combine == 1, "locks_select_nrm_topb: combine must be 0 (nrm) or 1 (max)");
+    LOCKS_REQUIRE(combine == 1 || (page_max && score_chunks >= 1),
+                  "locks_select_nrm_topb: nrm combine needs the scorer's page maxima");
+    LOCKS_REQUIRE(score_h && n_pages && n_sel_hi && b_fix && score && page_table && page_cnt,
+                  "locks_select_nrm_topb: null pointer argument");
+    const int Z1 = cdiv(max_pages, SEL_CH);
+    LOCKS_REQUIRE(Z1 <= FIN_MAXZ, "locks_select_nrm_topb: max_pages=%d exceeds %d", max_pages, FIN_MAXZ * SEL_CH);
+    const int64_t need = locks_select_workspace_bytes(n_req, n_kv, max_pages);
+    LOCKS_REQUIRE(Z1 == 1 || (workspace && workspace_bytes >= need),
+                  "locks_select_nrm_topb: workspace %lld B < required %lld B",
+                  (long long)workspace_bytes, (long long)need);
+    if (n_req == 0) return 0;
+    hipStream_t st = (hipStream_t)stream;
+    const long rows = (long)n_req * n_kv;
+    uint8_t* ws = (uint8_t*)workspace;
+    uint32_t* cand_key = (uint32_t*)ws;
+    int* cand_page = (int*)(ws + rows * Z1 * SEL_CH * 4);
+    uint32_t* spill_key = (uint32_t*)(ws + rows * Z1 * SEL_CH * 8);
+    int* spill_page = (int*)(ws + rows * Z1 * SEL_CH * 8 + rows * (long)max_pages * 4);
+    int* cand_cnt = (int*)(ws + rows * Z1 * SEL_CH * 8 + rows * (long)max_pages * 8);
+    hipLaunchKernelGGL(sel_chunk_kernel, dim3(Z1, n_kv, n_req), dim3(SEL_BLK), 0, st,
+                       score_h, page_max, score_chunks, n_pages, n_sel_hi, b_fix, score,
+                       page_table, page_cnt, cand_key, cand_page, cand_cnt, n_sink,
+                       max_pages, G, combine);
+    int rc = check_launch("sel_chunk_kernel");
+    if (rc || Z1 == 1) return rc;
+    hipLaunchKernelGGL(sel_finish_kernel, dim3(1, n_kv, n_req), dim3(FIN_BLK), 0, st,
+                       n_pages, n_sel_hi, b_fix, page_table, page_cnt, cand_key, cand_page,
+                       cand_cnt, spill_key, spill_page, n_sink, max_pages, Z1);
+    return check_launch("sel_finish_kernel");
+}
+
+extern "C" int32_t locks_derive_params(const int32_t* seq_lens, int32_t n_req, int32_t page,
+                                       int32_t window_pages, int32_t sink_pages,
+                                       int32_t budget_abs, double budget, int32_t* n_pages,
+                                       int32_t* n_sel_hi, int32_t* b_fix, void* stream) {
+    LOCKS_REQUIRE(page >= 1 && window_pages >= 1 && sink_pages >= 0,
+                  "locks_derive_params: bad page=%d window=%d sink=%d", page, window_pages, sink_pages);
+    LOCKS_REQUIRE(budget_abs > 0 || (budget > 0.0 && budget <= 1.0),
+                  "locks_derive_params: budget %f outside (0, 1] with no absolute budget", budget);
+    LOCKS_REQUIRE(seq_lens && n_pages && n_sel_hi && b_fix, "locks_derive_params: null pointer argument");
+    if (n_req <= 0) return 0;
+    const int blk = 256, grid = cdiv(n_req, blk);
+    hipLaunchKernelGGL(derive_kernel, dim3(grid), dim3(blk), 0, (hipStream_t)stream, seq_lens,
+                       n_req, page, window_pages, sink_pages, budget_abs, budget, n_pages,
+                       n_sel_hi, b_fix);
+    return check_launch("derive_kernel");
+}

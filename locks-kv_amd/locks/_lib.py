@@ -1,0 +1,84 @@
+"""ctypes binding of liblocks_hip.so (the C ABI in include/locks_hip.h).
+
+The product path has exactly one implementation: the HIP kernels in this
+library.  If the library is missing the import of any hot-path entry raises
+``LocksLibraryError`` -- there is no CPU or PyTorch fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "liblocks_hip.so")
+ABI_VERSION = 1
+
+_c = ctypes
+_i32, _i64, _f32, _f64, _p = _c.c_int32, _c.c_int64, _c.c_float, _c.c_double, _c.c_void_p
+
+# name -> (restype, argtypes); mirrors include/locks_hip.h one to one
+SIGNATURES = {
+    "locks_abi_version": (_i32, []),
+    "locks_last_error": (_c.c_char_p, []),
+    "locks_derive_params": (_i32, [_p, _i32, _i32, _i32, _i32, _i32, _f64, _p, _p, _p, _p]),
+    "locks_score_auto_chunk": (_i32, [_i32, _i32, _i32]),
+    "locks_score_num_chunks": (_i32, [_i32, _i32]),
+    "locks_score_rki4": (_i32, [_p, _i64, _i64, _p, _p, _p, _p, _p, _p, _i32, _p, _i64, _i32,
+                                _p, _p, _i32, _p, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _p]),
+    "locks_select_workspace_bytes": (_i64, [_i32, _i32, _i32]),
+    "locks_select_nrm_topb": (_i32, [_p, _p, _i32, _p, _p, _p, _p, _p, _p, _p, _i64,
+                                     _i32, _i32, _i32, _i32, _i32, _i32, _p]),
+    "locks_decode_splitk": (_i32, [_p, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64,
+                                   _i32, _p, _i64, _i32, _p, _i64, _i64, _i32, _p, _i64, _p,
+                                   _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32,
+                                   _p]),
+    "locks_decode_merge": (_i32, [_p, _p, _p, _p, _i64, _p, _i64, _i64, _i32, _i32, _i32, _i32,
+                                  _i32, _i32, _i32, _p]),
+}
+
+
+class LocksLibraryError(RuntimeError):
+    """liblocks_hip.so is missing, stale or rejected a call."""
+
+
+_LIB = None
+
+
+def lib_path() -> str:
+    return _LIB_PATH
+
+
+def load() -> ctypes.CDLL:
+    """Load (once) and type the HIP library; raise if it is absent."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not os.path.isfile(_LIB_PATH):
+        raise LocksLibraryError(
+            f"{_LIB_PATH} not found: build it with `python locks-kv_amd/build_lib.py` "
+            "(or __graft_entry__.build()). The LOCKS hot path has no fallback.")
+    lib = ctypes.CDLL(_LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    v = lib.locks_abi_version()
+    if v != ABI_VERSION:
+        raise LocksLibraryError(f"liblocks_hip ABI {v} != expected {ABI_VERSION}; rebuild it")
+    _LIB = lib
+    return lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = load().locks_last_error().decode(errors="replace")
+        raise RuntimeError(f"locks: {what} failed ({rc}): {msg}")
+
+
+def ptr(t) -> int:
+    """Device pointer of a torch tensor (None -> NULL)."""
+    return 0 if t is None else int(t.data_ptr())
+
+
+def stream_ptr(device=None) -> int:
+    import torch
+    return int(torch.cuda.current_stream(device).cuda_stream)

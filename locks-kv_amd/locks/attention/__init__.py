@@ -1,0 +1,3 @@
+"""Stage B: sparse paged attention over the selected pages."""
+from .decode import (ResidentVSource, decode_merge, decode_splitk,  # noqa: F401
+                     ensure_stage_b_buffers, sparse_paged_decode_batched)

@@ -1,0 +1,127 @@
+"""Stage B: split-K sparse paged decode + LSE merge on the MI355X kernels.
+
+Call contract of the reference (src/locks/attention/decode.py:130-156,
+:328-387): partials m/l (R, n_kv, split, G) and acc (R, n_kv, split, G, D)
+fp32 live on the state; pps = max(cdiv(page_cnt, split), pps_min) is derived
+on device; ``out`` (T, H, d) rows [0, n_req) are written in place; no host
+sync, no allocation.  K comes from the resident paged cache; V through the
+V-source seam (only the resident source exists in this build).
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from .. import _lib
+
+MAX_SPLIT = 512
+
+
+def _split_kv(kv_cache: torch.Tensor):
+    """(K, V) views (num_blocks, page, n_kv, d) for either vLLM cache layout
+    ((NB, 2, page, n_kv, d) or (2, NB, page, n_kv, d)); decode.py:64-73."""
+    if kv_cache.shape[0] == 2 and kv_cache.shape[1] != 2:
+        return kv_cache[0], kv_cache[1]
+    if kv_cache.shape[1] == 1:
+        return kv_cache.select(1, 0), None
+    return kv_cache.select(1, 0), kv_cache.select(1, 1)
+
+
+class ResidentVSource:
+    """V = the resident engine V half of kv_cache (V_SRC=0, decode.py:76-101)."""
+
+    SRC_ID = 0
+
+    def __init__(self, kv_cache: torch.Tensor):
+        _, v = _split_kv(kv_cache)
+        if v is None:
+            raise ValueError("ResidentVSource requires a resident V half; this cache is "
+                             "K-only (mem variant, not built for MI355X)")
+        self._v = v
+
+    def args(self):
+        v = self._v
+        return v, v.stride(0), v.stride(1), v.stride(2)
+
+
+def _pps_min(n_req: int, n_kv: int = 8) -> int:
+    """Minimum pages per split (amortises the q load / partial store)."""
+    if n_req == 1:
+        return 2
+    return 8 if n_req < 16 else 16
+
+
+def _adaptive_split(max_reqs: int, max_pages: int, budget: float, hard_cap: int) -> int:
+    """Allocation-time split count: about the number of active splits the
+    expected selection needs at low batch (decode.py:103-127), capped."""
+    if int(max_reqs) > 4:
+        return min(hard_cap, MAX_SPLIT)
+    pps = _pps_min(int(max_reqs))
+    est = math.ceil(1.5 * float(budget) * int(max_pages) / max(1, pps))
+    p2 = 1 << max(0, (max(1, est) - 1).bit_length())
+    return int(min(hard_cap, MAX_SPLIT, max(16, p2)))
+
+
+def ensure_stage_b_buffers(st, device, split: int) -> None:
+    """Allocate the split-K partials on the state once (outside any graph)."""
+    if getattr(st, "m_part", None) is not None:
+        return
+    split = int(min(split, MAX_SPLIT))
+    R, n_kv, G, D = st.max_reqs, st.n_kv, st.G, st.D
+    st.split = split
+    st.m_part = torch.empty(R, n_kv, split, G, device=device, dtype=torch.float32)
+    st.l_part = torch.empty(R, n_kv, split, G, device=device, dtype=torch.float32)
+    st.acc_part = torch.empty(R, n_kv, split, G, D, device=device, dtype=torch.float32)
+
+
+def decode_splitk(q, k, v, block_table, seq_lens, page_table, page_cnt, m_part, l_part,
+                  acc_part, *, n_req: int, G: int, split: int, pps_min: int,
+                  scale: float) -> None:
+    """Launch the split kernel on explicit tensors.  k, v: (NB, page, n_kv, d)
+    views; page_table (R, n_kv, MP) i32; page_cnt (R, n_kv) i32."""
+    NB, page, n_kv, d = k.shape
+    lib = _lib.load()
+    _lib.check(lib.locks_decode_splitk(
+        _lib.ptr(q), q.stride(0), q.stride(1),
+        _lib.ptr(k), k.stride(0), k.stride(1), k.stride(2),
+        _lib.ptr(v), v.stride(0), v.stride(1), v.stride(2), int(NB),
+        _lib.ptr(block_table), block_table.stride(0), int(block_table.shape[1]),
+        _lib.ptr(page_table), page_table.stride(0), page_table.stride(1),
+        int(page_table.shape[2]), _lib.ptr(page_cnt), page_cnt.stride(0), _lib.ptr(seq_lens),
+        _lib.ptr(m_part), _lib.ptr(l_part), _lib.ptr(acc_part), int(n_req), int(n_kv), int(G),
+        int(d), int(page), int(split), int(pps_min), float(scale),
+        _lib.stream_ptr(q.device)), "decode_splitk")
+
+
+def decode_merge(m_part, l_part, acc_part, page_cnt, out, *, n_req: int, n_kv: int, G: int,
+                 split: int, pps_min: int) -> None:
+    if out.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"out must be bf16 or fp32, got {out.dtype}")
+    lib = _lib.load()
+    _lib.check(lib.locks_decode_merge(
+        _lib.ptr(m_part), _lib.ptr(l_part), _lib.ptr(acc_part), _lib.ptr(page_cnt),
+        page_cnt.stride(0), _lib.ptr(out), out.stride(0), out.stride(1),
+        1 if out.dtype == torch.float32 else 0, int(n_req), int(n_kv), int(G),
+        int(acc_part.shape[-1]), int(split), int(pps_min), _lib.stream_ptr(out.device)),
+        "decode_merge")
+
+
+def sparse_paged_decode_batched(q, kv_cache, block_table, seq_lens, st, out,
+                                vsource=None, *, scale: float = None) -> None:
+    """Batched Stage B (decode.py:328-387): 2 fixed-shape launches."""
+    if scale is None:
+        scale = st.scale
+    n_req = seq_lens.shape[0]
+    k, _ = _split_kv(kv_cache)
+    if vsource is None:
+        vsource = ResidentVSource(kv_cache)
+    if vsource.SRC_ID != 0:
+        raise NotImplementedError("only the resident V source exists in this build")
+    v = vsource.args()[0]
+    pps = _pps_min(n_req, st.n_kv)
+    decode_splitk(q, k, v, block_table, seq_lens, st.page_table, st.page_cnt, st.m_part,
+                  st.l_part, st.acc_part, n_req=n_req, G=st.G, split=st.split,
+                  pps_min=pps, scale=scale)
+    decode_merge(st.m_part, st.l_part, st.acc_part, st.page_cnt, out, n_req=n_req,
+                 n_kv=st.n_kv, G=st.G, split=st.split, pps_min=pps)

@@ -1,0 +1,4 @@
+"""Stage A: rki4 summaries, per-page scores and exact top-b page selection."""
+from .rki4_state import Rki4State, record_bytes  # noqa: F401
+from .ops import (derive_page_params, rki4_score_only, rki4_score_state,  # noqa: F401
+                  rki4_select_only, topb_select)

@@ -1,0 +1,123 @@
+"""Rki4State: persistent per-model summary state + per-step selection buffers.
+
+Tensor names, shapes and dtypes follow the reference's six-slab layout
+(src/locks/selection/rki4_state.py:7-16, allocation :229-273):
+
+    pp_v4  (L, NB, n_kv, 8, d/2) uint8  int4 basis V, column-major, low nibble = even d
+    pp_vs  (L, NB, n_kv, 8)      bf16   per-column scales (absmax/7)
+    pp_c8  (L, NB, n_kv, page, 8) int8  coefficients C = U8*S8
+    pp_cs  (L, NB, n_kv, page)   bf16   per-token scales (absmax/127)
+    pp_mu8 (L, NB, n_kv, d)      int8   page centroid
+    pp_mus (L, NB, n_kv)         bf16   centroid scale (absmax/127)
+    pp_tag (L, NB, n_kv, 8)      bf16   content tag, NaN-initialised
+
+Per-step outputs: score (R, n_kv, MP) f32, page_table (R, n_kv, MP) i32,
+page_cnt (R, n_kv) i32, score_h (R, n_kv, G, MP) f32, n_pages / n_sel_hi /
+b_fix (R,) i32.  Added for the MI355X kernels (all persistent, allocated here
+so no call allocates): page_max (R, n_kv, chunks, 16) f32 -- the scorer's
+per-chunk maxima -- and sel_ws, the selector's candidate workspace.
+
+Footprint per (page, kv head): 5d + 10*page + 18 bytes of summary (818 B at
+d=128, page 16) + 16 B tag (rki4_state.py:18-22, record_bytes :124-141).
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+
+TAGW = 8
+RNK = 8
+IBITS = 4
+QMAX = (1 << (IBITS - 1)) - 1
+QMIN = -(1 << (IBITS - 1))
+
+
+def record_bytes(d: int, page: int, tagw: int = TAGW) -> int:
+    """Per-(page, kv head) slab bytes including the tag (rki4_state.py:124-141)."""
+    return RNK * (d * IBITS // 8) + RNK * 2 + page * RNK + page * 2 + d + 2 + tagw * 2
+
+
+class Rki4State:
+    """Allocated once from engine maxima; every address is stable across
+    decode steps, so the per-layer chain can be captured in a HIP graph."""
+
+    def __init__(self, device, *, num_layers: int, num_blocks: int, n_kv: int, G: int,
+                 head_dim: int, page: int, max_reqs: int, max_pages: int, rank: int = RNK,
+                 budget: float = 0.1, budget_pages=None, sink_pages: int = 1,
+                 window_pages: int = 1, tagw: int = TAGW, combine: str = "nrm",
+                 zsplit=None):
+        assert window_pages >= 1, "window_pages>=1: the partial tail must live inside " \
+            "the always-attended window"
+        self.validate_geometry(head_dim=head_dim, G=G, page=page, rank=rank)
+        assert combine in ("max", "nrm")
+        L, NB, D, MP, R = num_layers, num_blocks, head_dim, max_pages, max_reqs
+        self.L, self.NB, self.n_kv, self.G, self.d = L, NB, n_kv, G, D
+        self.D = D
+        self.page, self.r, self.tagw = page, RNK, tagw
+        self.v_bits = IBITS
+        self.max_reqs, self.max_pages = R, MP
+        self.budget = float(budget)
+        self.budget_abs = int(budget_pages or 0)
+        self.sink_pages, self.window_pages = int(sink_pages), int(window_pages)
+        self.combine = combine
+        self.device = torch.device(device)
+        u8, i8, bf16 = torch.uint8, torch.int8, torch.bfloat16
+        i32, f32 = torch.int32, torch.float32
+        dev = self.device
+
+        self.pp_v4 = torch.zeros(L, NB, n_kv, RNK, D * IBITS // 8, device=dev, dtype=u8)
+        self.pp_vs = torch.zeros(L, NB, n_kv, RNK, device=dev, dtype=bf16)
+        self.pp_c8 = torch.zeros(L, NB, n_kv, page, RNK, device=dev, dtype=i8)
+        self.pp_cs = torch.zeros(L, NB, n_kv, page, device=dev, dtype=bf16)
+        self.pp_mu8 = torch.zeros(L, NB, n_kv, D, device=dev, dtype=i8)
+        self.pp_mus = torch.zeros(L, NB, n_kv, device=dev, dtype=bf16)
+        self.pp_tag = torch.full((L, NB, n_kv, tagw), float("nan"), device=dev, dtype=bf16)
+
+        self.score = torch.zeros(R, n_kv, MP, device=dev, dtype=f32)
+        self.page_table = torch.full((R, n_kv, MP), -1, device=dev, dtype=i32)
+        self.page_cnt = torch.zeros(R, n_kv, device=dev, dtype=i32)
+        self.score_h = torch.zeros(R, n_kv, G, MP, device=dev, dtype=f32)
+
+        self.n_pages = torch.zeros(R, device=dev, dtype=i32)
+        self.n_sel_hi = torch.zeros(R, device=dev, dtype=i32)
+        self.b_fix = torch.ones(R, device=dev, dtype=i32)
+
+        lib = _lib.load()
+        # scorer launch shape: pages per workgroup (explicit zsplit = chunks)
+        if zsplit:
+            chunk = max(32, -(-MP // int(zsplit)))
+            chunk = -(-chunk // 32) * 32
+        else:
+            chunk = int(lib.locks_score_auto_chunk(R, n_kv, MP))
+        self.score_chunk = chunk
+        self.score_chunks = int(lib.locks_score_num_chunks(MP, chunk))
+        self.zsplit = self.score_chunks
+        self.page_max = torch.full((R, n_kv, self.score_chunks, 16), float("-inf"),
+                                   device=dev, dtype=f32)
+        ws = int(lib.locks_select_workspace_bytes(R, n_kv, MP))
+        self.sel_ws = torch.zeros(max(ws, 256), device=dev, dtype=torch.uint8)
+
+        assert self.bytes_per_layer() == record_bytes(D, page, tagw) * n_kv * NB
+
+    @staticmethod
+    def validate_geometry(*, head_dim: int, G: int, page: int, rank: int = RNK) -> None:
+        """Supported set of the gfx950 kernels, checked at wiring time."""
+        assert head_dim == 128, f"this MI355X build supports d=128, model has d={head_dim}"
+        assert 1 <= G <= 16, f"this build supports 1 <= G <= 16 query heads per kv head, got {G}"
+        assert page == 16, f"this MI355X build supports page 16, engine block_size={page}"
+        assert rank == RNK, f"rki4 rank is fixed at {RNK} in this build, got {rank}"
+
+    @classmethod
+    def record_bytes(cls, d: int, page: int, tagw: int = TAGW) -> int:
+        return record_bytes(d, page, tagw)
+
+    def bytes_per_layer(self) -> int:
+        return (self.pp_v4[0].numel() + self.pp_vs[0].numel() * 2 + self.pp_c8[0].numel()
+                + self.pp_cs[0].numel() * 2 + self.pp_mu8[0].numel()
+                + self.pp_mus[0].numel() * 2 + self.pp_tag[0].numel() * 2)
+
+    def layer_state(self, layer: int):
+        """(v4, vs, c8, cs, mu8, mus, tag) views of one layer."""
+        return (self.pp_v4[layer], self.pp_vs[layer], self.pp_c8[layer], self.pp_cs[layer],
+                self.pp_mu8[layer], self.pp_mus[layer], self.pp_tag[layer])

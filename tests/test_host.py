@@ -1,0 +1,125 @@
+"""Host-only checks (no GPU): the C-ABI library loads and exports every
+symbol include/locks_hip.h declares, rejects bad arguments before touching
+the device, and the Python plugin surface mirrors the reference's."""
+from __future__ import annotations
+
+import ctypes
+import json
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _header_functions():
+    text = open(os.path.join(ROOT, "include", "locks_hip.h")).read()
+    return sorted(set(re.findall(r"^\s*(?:const char\*|int32_t|int64_t)\s+(locks_\w+)\(",
+                                 text, re.M)))
+
+
+def test_library_exports_header_symbols():
+    from locks import _lib
+    lib = _lib.load()
+    names = _header_functions()
+    assert len(names) >= 10
+    for n in names:
+        assert hasattr(lib, n), n
+        assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
+    assert set(_lib.SIGNATURES) == set(names)
+    assert lib.locks_abi_version() == _lib.ABI_VERSION
+
+
+def test_rejects_bad_geometry_without_device():
+    from locks import _lib
+    lib = _lib.load()
+    args = [0, 0, 0] + [1] * 6 + [1, 1, 0, 1, 1, 1, 16, 1, 32, 1, 2, 4, 64, 16, 0.1, None]
+    rc = lib.locks_score_rki4(*args)           # head_dim 64 is outside the contract
+    assert rc == -1 and b"head_dim 64" in lib.locks_last_error()
+    rc = lib.locks_decode_splitk(*([1, 8, 8] + [1, 8, 8, 8] * 2 + [1, 1, 8, 1, 1, 8, 8, 1, 1,
+                                   8, 1, 1, 1, 1, 1, 2, 17, 128, 16, 4, 1, 0.1, None]))
+    assert rc == -1 and b"G=17" in lib.locks_last_error()
+    # two chunks (max_pages 4096) need the candidate workspace: rejected pre-launch
+    rc = lib.locks_select_nrm_topb(*([1, 1, 1] + [1] * 7 + [0, 1, 2, 4, 1, 4096, 0, None]))
+    assert rc == -1 and b"workspace" in lib.locks_last_error()
+    rc = lib.locks_derive_params(1, 1, 16, 0, 1, 0, 0.1, 1, 1, 1, None)
+    assert rc == -1 and b"window" in lib.locks_last_error()
+
+
+def test_workspace_and_chunk_math():
+    from locks import _lib
+    lib = _lib.load()
+    c = lib.locks_score_auto_chunk(1, 2, 65536)
+    assert c % 32 == 0 and 32 <= c <= 1024
+    assert lib.locks_score_num_chunks(65536, c) == -(-65536 // c)
+    assert lib.locks_select_workspace_bytes(1, 2, 65536) >= 2 * 65536 * 16
+    assert lib.locks_select_workspace_bytes(0, 0, 1) == -1
+
+
+def test_record_bytes_matches_reference_footprint():
+    from locks.selection.rki4_state import record_bytes
+    assert record_bytes(128, 16) == 834          # 818 B summary + 16 B tag
+    assert record_bytes(128, 16, tagw=0) == 818
+
+
+def test_config_surface(monkeypatch, tmp_path):
+    from locks import LocksConfig
+    c = LocksConfig()
+    assert (c.variant, c.sink_pages, c.window_pages, c.quad_combine) == ("fast", 1, 1, "nrm")
+    with pytest.raises(ValueError):
+        LocksConfig(budget=1.5)
+    with pytest.raises(ValueError):
+        LocksConfig(quad_combine="sum")
+    assert LocksConfig(variant="mem-kv").r8_screen is True
+    monkeypatch.setenv("LOCKS_CONFIG", json.dumps({"budget_pages": 126}))
+    monkeypatch.setenv("LOCKS_RKI4_Z", "64")
+    c = LocksConfig.load({"sink_pages": 2})
+    assert (c.budget_pages, c.sink_pages, c.rki4_zsplit) == (126, 2, 64)
+    p = tmp_path / "c.yaml"
+    p.write_text("budget: 0.05\n")
+    monkeypatch.setenv("LOCKS_CONFIG", str(p))
+    assert LocksConfig.load().budget == 0.05
+    monkeypatch.setenv("LOCKS_CONFIG", json.dumps({"bogus": 1}))
+    with pytest.raises(ValueError):
+        LocksConfig.load()
+
+
+def test_register_inert_and_mem_refused(monkeypatch, capsys):
+    import locks
+    from locks.backend import _runtime, register as regmod
+    monkeypatch.delenv("LOCKS_CONFIG", raising=False)
+    monkeypatch.setattr(regmod, "_APPLIED", False)
+    locks.register()
+    assert "INERT" in capsys.readouterr().out
+    with pytest.raises(NotImplementedError):
+        locks.register({"variant": "mem-v"})
+    locks.register({"budget_pages": 126})
+    assert _runtime.get_config().budget_pages == 126
+
+
+def test_geometry_contract():
+    from locks.selection import Rki4State
+    Rki4State.validate_geometry(head_dim=128, G=16, page=16)
+    for kw in (dict(head_dim=64, G=4, page=16), dict(head_dim=128, G=17, page=16),
+               dict(head_dim=128, G=4, page=32)):
+        with pytest.raises(AssertionError):
+            Rki4State.validate_geometry(**kw)
+
+
+def test_product_path_has_no_oracle_import():
+    """Nothing under the shipped package imports the oracle or numpy CPU math."""
+    pkg = os.path.join(ROOT, "locks-kv_amd", "locks")
+    for dp, _, fs in os.walk(pkg):
+        for f in fs:
+            if f.endswith(".py"):
+                src = open(os.path.join(dp, f)).read()
+                assert "oracle" not in src.replace("no CPU or PyTorch fallback", ""), f
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    from locks import _lib
+    monkeypatch.setattr(_lib, "_LIB", None)
+    monkeypatch.setattr(_lib, "_LIB_PATH", str(tmp_path / "nope.so"))
+    with pytest.raises(_lib.LocksLibraryError):
+        _lib.load()
