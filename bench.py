@@ -1,0 +1,350 @@
+"""LOCKS sparse decode step on one MI355X: ms/step + achieved HBM GB/s.
+
+A "step" is one bs=1 decode step of the LOCKS attention hot path over every
+layer of the model: derive (once) and, per layer, rki4 score -> GQA combine +
+exact top-b -> split-K sparse paged decode -> LSE merge, captured in one HIP
+graph and replayed.  Inputs (K/V cache, summaries, q, block table) are
+resident in HBM before the timed region.  Synthetic data: K/V ~ N(0,1) bf16
+with 4 outlier channels x8 per kv head, q ~ N(0,1), block tables shuffled in
+a page pool, rki4 summaries built on the GPU from that K.
+
+Also measured in the same run: dense full-KV decode (same kernels, every
+page selected) on the same GPU, the scorer's live roofline, and the CPU
+oracle on a bounded sample (rank 0, N=1 only).
+
+    python bench.py [--workload llama8b-128k|glm9b-1m|glm9b-batch] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "locks-kv_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBPS = 8000.0
+SUMMARY_BYTES = 818          # rki4 bytes per (page, kv head) read by the scorer
+PAGE = 16
+D = 128
+
+WORKLOADS = {
+    # Llama-3.1-8B shape, 128K, bs=1, b=2048
+    "llama8b-128k": dict(layers=32, n_kv=8, G=4, seq_lens=[131072]),
+    # GLM-4-9B-1M shape, 1M context
+    "glm9b-1m": dict(layers=40, n_kv=2, G=16, seq_lens=[1 << 20]),
+    # batched ragged GLM
+    "glm9b-batch": dict(layers=40, n_kv=2, G=16, seq_lens=[262144, 196608, 131072, 65536]),
+    # small smoke-size workload
+    "tiny": dict(layers=2, n_kv=2, G=4, seq_lens=[16384]),
+}
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def make_model(wl, budget_pages, seed=0, summaries="build"):
+    import torch
+    from locks.attention import ensure_stage_b_buffers
+    from locks.selection import Rki4State
+    from locks.selection.rki4_build import rki4_build_blocks
+
+    dev = torch.device("cuda")
+    L, n_kv, G, sls = wl["layers"], wl["n_kv"], wl["G"], wl["seq_lens"]
+    R = len(sls)
+    npg = [(s + PAGE - 1) // PAGE for s in sls]
+    MP = max(npg)
+    NB = sum(npg) + 64                                   # shared page pool
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    perm = torch.randperm(NB, generator=g, device=dev).to(torch.int32)
+    bt = torch.zeros(R, MP, dtype=torch.int32, device=dev)
+    off = 0
+    for r, n in enumerate(npg):
+        bt[r, :n] = perm[off:off + n]
+        off += n
+    st = Rki4State(dev, num_layers=L, num_blocks=NB, n_kv=n_kv, G=G, head_dim=D, page=PAGE,
+                   max_reqs=R, max_pages=MP, budget=0.1, budget_pages=budget_pages)
+    ensure_stage_b_buffers(st, dev, 128)
+    kv_layers = []
+    t_build = 0.0
+    fin = torch.cat([bt[r, : sls[r] // PAGE] for r in range(R)]).to(torch.int64)
+    for layer in range(L):
+        scale = torch.ones(n_kv, D, device=dev)
+        for h in range(n_kv):
+            ch = torch.randperm(D, generator=g, device=dev)[:4]
+            scale[h, ch] = 8.0
+        kv = torch.empty(NB, 2, PAGE, n_kv, D, dtype=torch.bfloat16, device=dev)
+        for half in range(2):
+            x = torch.randn(NB, PAGE, n_kv, D, generator=g, device=dev) * scale
+            kv[:, half].copy_(x)
+            del x
+        kv_layers.append(kv)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        if summaries == "build" or layer == 0:
+            rki4_build_blocks(st, layer, kv[:, 0], fin)
+        else:                                            # reuse layer 0's slab bytes
+            for a in ("pp_v4", "pp_vs", "pp_c8", "pp_cs", "pp_mu8", "pp_mus", "pp_tag"):
+                getattr(st, a)[layer].copy_(getattr(st, a)[0])
+        torch.cuda.synchronize()
+        t_build += time.perf_counter() - t0
+        if layer == 0:
+            log(f"layer 0 summary build: {t_build:.2f}s for {fin.numel() * n_kv} grams")
+    st._layer_of = {kv.data_ptr(): i for i, kv in enumerate(kv_layers)}
+    q = [torch.randn(R, n_kv * G, D, generator=g, device=dev).to(torch.bfloat16)
+         for _ in range(L)]
+    sl = torch.tensor(sls, dtype=torch.int32, device=dev)
+    return dict(st=st, kv=kv_layers, q=q, bt=bt, sl=sl, R=R, L=L, n_kv=n_kv, G=G, MP=MP,
+                NB=NB, build_s=t_build, scale=1.0 / math.sqrt(D))
+
+
+def sparse_step(m, out):
+    from locks.backend import _runtime
+    from locks.selection import derive_page_params
+    st = m["st"]
+    derive_page_params(st, m["sl"], m["R"])
+    for layer in range(m["L"]):
+        kv = m["kv"][layer]
+        _runtime._rki4_select_adapter(m["q"][layer], kv, m["bt"], m["sl"], st, m["R"],
+                                      m["scale"], None)
+        _runtime.decode_dispatch(m["q"][layer], kv, m["bt"], m["sl"], st, out[layer], None,
+                                 m["scale"], None)
+
+
+def make_dense(m, split=512):
+    import torch
+    R, n_kv, MP, G = m["R"], m["n_kv"], m["MP"], m["G"]
+    tab = torch.full((R, n_kv, MP), -1, dtype=torch.int32, device="cuda")
+    cnt = torch.zeros(R, n_kv, dtype=torch.int32, device="cuda")
+    for r, s in enumerate(m["sl"].tolist()):
+        n = (s + PAGE - 1) // PAGE
+        tab[r, :, :n] = torch.arange(n, dtype=torch.int32, device="cuda")
+        cnt[r, :] = n
+    mp = torch.empty(R, n_kv, split, G, device="cuda")
+    lp = torch.empty_like(mp)
+    ap = torch.empty(R, n_kv, split, G, D, device="cuda")
+    return dict(tab=tab, cnt=cnt, m=mp, l=lp, acc=ap, split=split)
+
+
+def dense_step(m, dn, out):
+    from locks.attention import decode_merge, decode_splitk
+    from locks.attention.decode import _split_kv
+    for layer in range(m["L"]):
+        k, v = _split_kv(m["kv"][layer])
+        decode_splitk(m["q"][layer], k, v, m["bt"], m["sl"], dn["tab"], dn["cnt"], dn["m"],
+                      dn["l"], dn["acc"], n_req=m["R"], G=m["G"], split=dn["split"],
+                      pps_min=1, scale=m["scale"])
+        decode_merge(dn["m"], dn["l"], dn["acc"], dn["cnt"], out[layer], n_req=m["R"],
+                     n_kv=m["n_kv"], G=m["G"], split=dn["split"], pps_min=1)
+
+
+def capture(fn):
+    import torch
+    fn()                                  # eager warm-up outside capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fn()
+    torch.cuda.synchronize()
+    return graph
+
+
+def time_graph(graph, steps, warmup):
+    import torch
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    for _ in range(steps):
+        graph.replay()
+    e1.record(s)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def step_bytes(m):
+    """Algorithmic HBM bytes of one sparse step (per-stage formulas)."""
+    st = m["st"]
+    npg = [(s + PAGE - 1) // PAGE for s in m["sl"].tolist()]
+    nsc = [n - st.window_pages for n in npg]
+    L, n_kv, G = m["L"], m["n_kv"], m["G"]
+    cnt = st.page_cnt.cpu().numpy()
+    score = sum(n_kv * P * (SUMMARY_BYTES + G * 4) for P in nsc)
+    select = sum(n_kv * P * (G * 4 + 4) + n_kv * m["MP"] * 4 for P in nsc)
+    decode = int(cnt.sum()) * PAGE * D * 2 * 2
+    dense = sum(n_kv * n * PAGE * D * 2 * 2 for n in npg)
+    return dict(score=L * score, select=L * select, decode=L * decode, dense=L * dense,
+                score_per_launch=score)
+
+
+def scorer_roofline(m, reps=3):
+    """Average scorer launch duration (HIP events on the launch stream) over
+    every layer's slabs, cold across layers."""
+    import torch
+    from locks.selection import rki4_score_only
+    st = m["st"]
+    s = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    n = 0
+    e0.record(s)
+    for _ in range(reps):
+        for layer in range(m["L"]):
+            rki4_score_only(st, layer, m["q"][layer], m["bt"], m["sl"], m["R"], m["scale"])
+            n += 1
+    e1.record(s)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / n       # us per launch
+
+
+def cpu_baseline(m, sample_pages=4096):
+    """Oracle (numpy) timed on the host on a bounded sample: one layer,
+    `sample_pages` selectable pages of every kv head; scaled to ms/step."""
+    import numpy as np
+    import torch
+
+    from oracle import locks_oracle as O
+    st, n_kv, G = m["st"], m["n_kv"], m["G"]
+    P = min(sample_pages, int(m["sl"][0].item()) // PAGE - 1)
+    bt = m["bt"][:1, :P + 1].cpu().numpy()
+    blocks = np.unique(bt[0])
+    to_np = lambda t: t.cpu().numpy()
+    slabs = {}
+    for name, attr, bf in (("v4", "pp_v4", 0), ("vs", "pp_vs", 1), ("c8", "pp_c8", 0),
+                           ("cs", "pp_cs", 1), ("mu8", "pp_mu8", 0), ("mus", "pp_mus", 1)):
+        t = getattr(st, attr)[0]
+        a = to_np(t.view(torch.int16) if bf else t)
+        slabs[name] = a.view(np.uint16) if bf else a
+    kv = m["kv"][0]
+    k = to_np(kv[:, 0].view(torch.int16)).view(np.uint16)
+    v = to_np(kv[:, 1].view(torch.int16)).view(np.uint16)
+    q = to_np(m["q"][0][:1].view(torch.int16)).view(np.uint16)
+    sl = [(P + 1) * PAGE]
+    t0 = time.perf_counter()
+    npg, nsh, b = O.derive_page_params(sl, PAGE, 1, 1, st.budget_abs, st.budget)
+    sh = O.score_rki4_twin(q, slabs, bt, nsh, n_kv, G, m["scale"], P + 1)
+    t1 = time.perf_counter()
+    comb = O.combine_nrm(sh, nsh)
+    tab, cnt = O.topb_select(comb, npg, nsh, b, 1, P + 1)
+    t2 = time.perf_counter()
+    O.decode_attention(q, k, v, bt, sl, tab, cnt, G, m["scale"])
+    t3 = time.perf_counter()
+    full_P = (m["sl"][0].item() + PAGE - 1) // PAGE - 1
+    f = full_P / P
+    per_layer = (t1 - t0) * f + (t2 - t1) * f + (t3 - t2)
+    try:
+        from threadpoolctl import threadpool_info
+        cores = max([i.get("num_threads", 1) for i in threadpool_info()] + [1])
+    except Exception:
+        cores = 1
+    return dict(value=round(per_layer * m["L"] * 1e3, 3), unit="ms/step", cores=cores,
+                kind="port",
+                sample=(f"numpy oracle, layer 0, {P} of {full_P} selectable pages x {n_kv} kv "
+                        f"heads (score+select scaled x{f:.1f}), decode over the selected "
+                        f"pages, x{m['L']} layers"),
+                stages_s=dict(score=round(t1 - t0, 3), select=round(t2 - t1, 3),
+                              decode=round(t3 - t2, 3)))
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="llama8b-128k", choices=sorted(WORKLOADS))
+    ap.add_argument("--budget-pages", type=int, default=126)
+    ap.add_argument("--summaries", default="build", choices=["build", "copy"])
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-dense", action="store_true")
+    ap.add_argument("--calib-copy", type=int, default=0,
+                    help="only run N device copies of 1 GiB (PMC byte-counter calibration)")
+    ap.add_argument("--profile-scorer", type=int, default=0,
+                    help="only launch the scorer N times per layer (for rocprof)")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU; --gpus must be 1"}))
+        sys.exit(2)
+    import torch
+    if a.calib_copy:
+        src = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(a.calib_copy):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copied {a.calib_copy} x {src.numel() * 4} B (read + write each)")
+        return
+    wl = WORKLOADS[a.workload]
+    t0 = time.perf_counter()
+    m = make_model(wl, a.budget_pages, summaries=a.summaries)
+    log(f"model ready in {time.perf_counter() - t0:.1f}s (summary build {m['build_s']:.1f}s)")
+    if a.profile_scorer:
+        us = scorer_roofline(m, reps=a.profile_scorer)
+        log(f"scorer avg {us:.2f} us/launch")
+        return
+    out = [torch.empty(m["R"], m["n_kv"] * m["G"], D, dtype=torch.bfloat16, device="cuda")
+           for _ in range(m["L"])]
+    # eager vs graph consistency (graph replays must reproduce the eager step)
+    sparse_step(m, out)
+    torch.cuda.synchronize()
+    ref_tab = m["st"].page_table.clone()
+    ref_out = out[-1].clone()
+    g_sparse = capture(lambda: sparse_step(m, out))
+    for _ in range(3):
+        g_sparse.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(m["st"].page_table, ref_tab), "graph replay changed the selection"
+        assert torch.equal(out[-1], ref_out), "graph replay changed the output"
+    ms = time_graph(g_sparse, a.steps, a.warmup)
+    by = step_bytes(m)
+    sparse_bytes = by["score"] + by["select"] + by["decode"]
+    log(f"sparse step {ms:.3f} ms")
+    score_us = scorer_roofline(m)
+    score_gbps = by["score_per_launch"] / (score_us * 1e-6) / 1e9
+    res = {}
+    if not a.no_dense:
+        dn = make_dense(m)
+        outd = [torch.empty_like(o) for o in out]
+        g_dense = capture(lambda: dense_step(m, dn, outd))
+        ms_dense = time_graph(g_dense, max(3, a.steps // 5), 2)
+        res = dict(dense_ms_per_step=round(ms_dense, 4),
+                   dense_achieved_GBps=round(by["dense"] / (ms_dense * 1e-3) / 1e9, 1),
+                   speedup_vs_dense=round(ms_dense / ms, 3))
+        log(f"dense step {ms_dense:.3f} ms")
+    cpu = None
+    if not a.no_cpu:
+        cpu = cpu_baseline(m)
+        log(f"cpu baseline {cpu}")
+    line = {
+        "metric": "decode ms/step + achieved HBM GB/s, bs=1 @128K/1M ctx, b=2048",
+        "value": round(ms, 4), "unit": "ms/step", "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "ms_per_step": round(ms, 4), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": a.workload, "layers": m["L"], "n_kv": m["n_kv"], "G": m["G"],
+                   "seq_lens": wl["seq_lens"], "page": PAGE, "head_dim": D,
+                   "budget_pages": a.budget_pages, "attended_pages_per_kv_head":
+                       int(m["st"].page_cnt[0, 0].item()), "summaries": a.summaries,
+                   "parallelism": "single-gpu"},
+        "tokens_per_s": round(m["R"] * 1e3 / ms, 2),
+        "achieved_GBps": round(sparse_bytes / (ms * 1e-3) / 1e9, 1),
+        "step_algorithmic_bytes": sparse_bytes,
+        **res,
+        "roofline": {"bound": "hbm", "kernel": "rki4_score_kernel",
+                     "achieved": round(score_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(score_gbps / HBM_PEAK_GBPS, 4),
+                     "avg_launch_us": round(score_us, 3),
+                     "bytes_per_launch": by["score_per_launch"], "traffic": None},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

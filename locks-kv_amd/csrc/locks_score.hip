@@ -146,7 +146,7 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
         float vsf[4];
 #pragma unroll
         for (int pp = 0; pp < 4; ++pp) {
-            const int b = (lane & 8) ? blkv[2 * pp + 1] : blkv[2 * pp];
+            const int b = __shfl(blk, 2 * pp + ((lane >> 3) & 1), kWave);
             const long row = (long)b * n_kv + kh;
             vv[pp] = *reinterpret_cast<const uint4*>(
                 v4 + row * SC_VROW + (lane & 7) * (SC_D / 2) + kg * 16);
@@ -169,9 +169,7 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
         uint2 csv[NGRP];
 #pragma unroll
         for (int gi = 0; gi < NGRP; ++gi) {
-            int b = blkv[gi * PPM];
-#pragma unroll
-            for (int u = 1; u < PPM; ++u) b = (psub_l == u) ? blkv[gi * PPM + u] : b;
+            const int b = (PPM == 1) ? blkv[gi] : __shfl(blk, gi * PPM + psub_l, kWave);
             const long row = (long)b * n_kv + kh;
             csv[gi] = *reinterpret_cast<const uint2*>(cs + row * SC_PG + 4 * kg);
         }
