@@ -49,7 +49,7 @@ def log(*a):
     print("[bench]", *a, file=sys.stderr, flush=True)
 
 
-def make_model(wl, budget_pages, seed=0, summaries="build"):
+def make_model(wl, budget_pages, seed=0, summaries="build", zsplit=None):
     import torch
     from locks.attention import ensure_stage_b_buffers
     from locks.selection import Rki4State
@@ -70,7 +70,8 @@ def make_model(wl, budget_pages, seed=0, summaries="build"):
         bt[r, :n] = perm[off:off + n]
         off += n
     st = Rki4State(dev, num_layers=L, num_blocks=NB, n_kv=n_kv, G=G, head_dim=D, page=PAGE,
-                   max_reqs=R, max_pages=MP, budget=0.1, budget_pages=budget_pages)
+                   max_reqs=R, max_pages=MP, budget=0.1, budget_pages=budget_pages,
+                   zsplit=zsplit)
     ensure_stage_b_buffers(st, dev, 128)
     kv_layers = []
     t_build = 0.0
@@ -264,6 +265,8 @@ def main():
     ap.add_argument("--summaries", default="build", choices=["build", "copy"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-dense", action="store_true")
+    ap.add_argument("--zsplit", type=int, default=0, help="scorer chunks per (req, kv head)")
+    ap.add_argument("--pps-min", type=int, default=0, help="override the decode pps_min table")
     ap.add_argument("--calib-copy", type=int, default=0,
                     help="only run N device copies of 1 GiB (PMC byte-counter calibration)")
     ap.add_argument("--profile-scorer", type=int, default=0,
@@ -282,8 +285,11 @@ def main():
         log(f"copied {a.calib_copy} x {src.numel() * 4} B (read + write each)")
         return
     wl = WORKLOADS[a.workload]
+    if a.pps_min:
+        from locks.attention import decode as _dec
+        _dec.PPS_MIN_OVERRIDE = a.pps_min
     t0 = time.perf_counter()
-    m = make_model(wl, a.budget_pages, summaries=a.summaries)
+    m = make_model(wl, a.budget_pages, summaries=a.summaries, zsplit=a.zsplit or None)
     log(f"model ready in {time.perf_counter() - t0:.1f}s (summary build {m['build_s']:.1f}s)")
     if a.profile_scorer:
         us = scorer_roofline(m, reps=a.profile_scorer)

@@ -106,7 +106,9 @@ int64_t locks_select_workspace_bytes(int32_t n_req, int32_t n_kv, int32_t max_pa
  *   page_table (n_req, n_kv, max_pages) i32: kept pages ascending, -1 after
  *   page_cnt   (n_req, n_kv) i32
  *   workspace  >= locks_select_workspace_bytes(...) bytes (unused when
- *              max_pages <= 2048)
+ *              max_pages <= 2048); calls that overlap on one workspace race.
+ * Launches: one chunk kernel (combine + local top-b candidates, or the whole
+ * selection when max_pages <= 2048) and one finishing kernel otherwise.
  */
 int32_t locks_select_nrm_topb(const float* score_h, const float* page_max, int32_t score_chunks,
                               const int32_t* n_pages, const int32_t* n_sel_hi,
@@ -143,7 +145,8 @@ int32_t locks_decode_splitk(const uint16_t* q, int64_t q_stride_req, int64_t q_s
  * LSE merge of the split-K partials into the attention output.
  * Replaces merge_splits_kernel (attention/merge.py:105-152).
  *   out (n_req, n_kv*G, 128) bf16 (out_is_f32 = 0) or f32 (out_is_f32 = 1),
- *   strides (out_stride_req, out_stride_head, 1); rows with page_cnt 0 get 0.
+ *   strides (out_stride_req, out_stride_head, 1), multiples of 4 elements;
+ *   rows with page_cnt 0 get 0.
  */
 int32_t locks_decode_merge(const float* m_part, const float* l_part, const float* acc_part,
                            const int32_t* page_cnt, int64_t cnt_stride, void* out,

@@ -30,7 +30,8 @@ namespace locks {
 
 constexpr int DC_D = 128;
 constexpr int DC_PG = 16;
-constexpr int MG_BLK = 256;
+constexpr int DC_WAVES = 4;
+constexpr int DC_BLK = DC_WAVES * kWave;
 constexpr int MAX_SPLIT = 512;
 
 __device__ __forceinline__ uint32_t bf16_word(const uint4& w, int e) {
@@ -38,7 +39,58 @@ __device__ __forceinline__ uint32_t bf16_word(const uint4& w, int e) {
     return (e & 1) ? (x >> 16) : (x & 0xFFFFu);
 }
 
-__global__ __launch_bounds__(kWave) void decode_split_kernel(
+// Merge the first n_act split partials of row rk into out (one workgroup,
+// DC_BLK threads).  scratch: >= MAX_SPLIT * 16 floats of LDS.
+__device__ void merge_row(const float* __restrict__ m_part, const float* __restrict__ l_part,
+                          const float* __restrict__ acc_part, long rk, int r, int kh, int n_act,
+                          int G, int split, void* __restrict__ out, long o_sr, long o_sh,
+                          int out_f32, float* w_s, float* lt_s) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    constexpr int NWV = DC_BLK / kWave;
+    for (int g = wave; g < G; g += NWV) {
+        float mm = -INFINITY;
+        for (int s = lane; s < n_act; s += kWave) mm = fmaxf(mm, m_part[(rk * split + s) * G + g]);
+        mm = wave_max(mm);
+        float lt = 0.f;
+        for (int s = lane; s < n_act; s += kWave) {
+            const float l = l_part[(rk * split + s) * G + g];
+            const float w = (l > 0.f) ? __expf(m_part[(rk * split + s) * G + g] - mm) : 0.f;
+            w_s[s * 16 + g] = w;
+            lt += l * w;
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) lt += __shfl_xor(lt, o, kWave);
+        if (lane == 0) lt_s[g] = lt;
+    }
+    __syncthreads();
+    for (int i = tid; i < G * (DC_D / 4); i += DC_BLK) {
+        const int g = i / (DC_D / 4), d4 = (i % (DC_D / 4)) * 4;
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+        const float* ap = acc_part + (rk * split * G + g) * DC_D + d4;
+#pragma unroll 4
+        for (int s = 0; s < n_act; ++s) {
+            const float w = w_s[s * 16 + g];
+            const float4 a = *reinterpret_cast<const float4*>(ap + (long)s * G * DC_D);
+            acc.x += w * a.x; acc.y += w * a.y; acc.z += w * a.z; acc.w += w * a.w;
+        }
+        const float lt = lt_s[g];
+        const float inv = (lt > 0.f) ? 1.f / lt : 0.f;
+        const float o[4] = {acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv};
+        const long oi = (long)r * o_sr + (long)(kh * G + g) * o_sh + d4;
+        if (out_f32) {
+            *reinterpret_cast<float4*>(reinterpret_cast<float*>(out) + oi) =
+                make_float4(o[0], o[1], o[2], o[3]);
+        } else {
+            uint16_t* ob = reinterpret_cast<uint16_t*>(out) + oi;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) ob[e] = f32_to_bf16(o[e]);
+        }
+    }
+}
+
+// One workgroup = 4 waves per split; wave w takes pages j0+w, j0+w+4, ...
+// and the 4 wave states are merged in LDS into the split's partial.
+__global__ __launch_bounds__(DC_BLK) void decode_split_kernel(
     const uint16_t* __restrict__ q, long q_sr, long q_sh,
     const uint16_t* __restrict__ kc, long k_sb, long k_st, long k_sh,
     const uint16_t* __restrict__ vc, long v_sb, long v_st, long v_sh,
@@ -50,15 +102,19 @@ __global__ __launch_bounds__(kWave) void decode_split_kernel(
 {
     const int sp = blockIdx.x, kh = blockIdx.y, r = blockIdx.z;
     const int n_kv = gridDim.y;
+    const long rk = (long)r * n_kv + kh;
     const int cnt = min(pcnt[(long)r * cnt_sr + kh], pt_cols);
     const int pps = max(cdiv(cnt, split), pps_min);
     const int j0 = sp * pps;
     if (j0 >= cnt) return;                        // inactive split: no store
     const int j1 = min(j0 + pps, cnt);
 
-    const int lane = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int c16 = lane & 15, kg = lane >> 4;
     const int seq_len = seq_lens[r];
+
+    __shared__ float red[DC_WAVES * 16 * DC_D];   // wave partials [wave][g][d]
+    __shared__ float wm[DC_WAVES][16], wl[DC_WAVES][16];
 
     // B operand of QK: q[g = c16][32*kg + 8*s + 0..7]
     v8bf qb[4];
@@ -93,11 +149,13 @@ __global__ __launch_bounds__(kWave) void decode_split_kernel(
     for (int b = 0; b < 8; ++b) o[b] = v4f{0.f, 0.f, 0.f, 0.f};
 
     uint4 kcur[4], vcur[4];
-    int ptcur = load_page(j0, kcur, vcur);
-    for (int j = j0; j < j1; ++j) {
+    int j = j0 + wave;
+    int ptcur = 0;
+    if (j < j1) ptcur = load_page(j, kcur, vcur);
+    for (; j < j1; j += DC_WAVES) {
         uint4 knx[4], vnx[4];
         int ptnx = 0;
-        if (j + 1 < j1) ptnx = load_page(j + 1, knx, vnx);
+        if (j + DC_WAVES < j1) ptnx = load_page(j + DC_WAVES, knx, vnx);
 
         // ---- S^T[t][g] = K[t] . q[g] ------------------------------------
         v4f s = {0.f, 0.f, 0.f, 0.f};
@@ -132,74 +190,58 @@ __global__ __launch_bounds__(kWave) void decode_split_kernel(
             o[b] = o[b] * alpha;
             o[b] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, pb, o[b], 0, 0, 0);
         }
-
 #pragma unroll
         for (int i = 0; i < 4; ++i) { kcur[i] = knx[i]; vcur[i] = vnx[i]; }
         ptcur = ptnx;
     }
-
     lsum += __shfl_xor(lsum, 16, kWave);
     lsum += __shfl_xor(lsum, 32, kWave);
-    if (c16 < G) {
-        const long base = (((long)r * n_kv + kh) * split + sp) * G + c16;
-        if (kg == 0) {
-            m_part[base] = m;
-            l_part[base] = lsum;
-        }
-        float* ap = acc_part + base * DC_D + 32 * kg;
+
+    // ---- merge the 4 wave states of this split in LDS --------------------
+    if (kg == 0) { wm[wave][c16] = m; wl[wave][c16] = lsum; }
+    {
+        float* ow = red + (wave * 16 + c16) * DC_D + 32 * kg;       // [wave][g][d]
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-            float4 lo = make_float4(o[0][v], o[1][v], o[2][v], o[3][v]);
-            float4 hi = make_float4(o[4][v], o[5][v], o[6][v], o[7][v]);
-            *reinterpret_cast<float4*>(ap + 8 * v) = lo;
-            *reinterpret_cast<float4*>(ap + 8 * v + 4) = hi;
+            *reinterpret_cast<float4*>(ow + 8 * v) = make_float4(o[0][v], o[1][v], o[2][v], o[3][v]);
+            *reinterpret_cast<float4*>(ow + 8 * v + 4) = make_float4(o[4][v], o[5][v], o[6][v], o[7][v]);
         }
+    }
+    __syncthreads();
+    const long base = (rk * split + sp) * G;
+    for (int i = tid; i < G * DC_D; i += DC_BLK) {
+        const int g = i / DC_D, d = i % DC_D;
+        float M = wm[0][g];
+#pragma unroll
+        for (int w = 1; w < DC_WAVES; ++w) M = fmaxf(M, wm[w][g]);
+        const float Mr = (M == -INFINITY) ? 0.f : M;
+        float acc = 0.f, l = 0.f;
+#pragma unroll
+        for (int w = 0; w < DC_WAVES; ++w) {
+            const float e = __expf(wm[w][g] - Mr);
+            acc += e * red[(w * 16 + g) * DC_D + d];
+            l += e * wl[w][g];
+        }
+        acc_part[(base + g) * DC_D + d] = acc;
+        if (d == 0) { m_part[base + g] = M; l_part[base + g] = l; }
     }
 }
 
-__global__ __launch_bounds__(MG_BLK) void decode_merge_kernel(
+__global__ __launch_bounds__(DC_BLK) void decode_merge_kernel(
     const float* __restrict__ m_part, const float* __restrict__ l_part,
     const float* __restrict__ acc_part, const int* __restrict__ pcnt, long cnt_sr,
     void* __restrict__ out, long o_sr, long o_sh, int out_f32, int G, int split, int pps_min)
 {
     const int kh = blockIdx.x, r = blockIdx.y;
     const int n_kv = gridDim.x;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const long rk = (long)r * n_kv + kh;
     const int cnt = pcnt[(long)r * cnt_sr + kh];
     const int pps = max(cdiv(cnt, split), pps_min);
     const int n_act = cnt > 0 ? min(cdiv(cnt, pps), split) : 0;
-
-    __shared__ float w_s[MAX_SPLIT][16];
+    __shared__ float w_s[MAX_SPLIT * 16];
     __shared__ float lt_s[16];
-
-    for (int g = wave; g < G; g += MG_BLK / kWave) {
-        float mm = -INFINITY;
-        for (int s = lane; s < n_act; s += kWave) mm = fmaxf(mm, m_part[(rk * split + s) * G + g]);
-        mm = wave_max(mm);
-        float lt = 0.f;
-        for (int s = lane; s < n_act; s += kWave) {
-            const float l = l_part[(rk * split + s) * G + g];
-            const float w = (l > 0.f) ? __expf(m_part[(rk * split + s) * G + g] - mm) : 0.f;
-            w_s[s][g] = w;
-            lt += l * w;
-        }
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) lt += __shfl_xor(lt, o, kWave);
-        if (lane == 0) lt_s[g] = lt;
-    }
-    __syncthreads();
-
-    for (int i = tid; i < G * DC_D; i += MG_BLK) {
-        const int g = i / DC_D, d = i % DC_D;
-        float acc = 0.f;
-        for (int s = 0; s < n_act; ++s) acc += w_s[s][g] * acc_part[((rk * split + s) * G + g) * DC_D + d];
-        const float lt = lt_s[g];
-        const float o = (lt > 0.f) ? acc / lt : 0.f;
-        const long oi = (long)r * o_sr + (long)(kh * G + g) * o_sh + d;
-        if (out_f32) reinterpret_cast<float*>(out)[oi] = o;
-        else reinterpret_cast<uint16_t*>(out)[oi] = f32_to_bf16(o);
-    }
+    merge_row(m_part, l_part, acc_part, rk, r, kh, n_act, G, split, out, o_sr, o_sh, out_f32,
+              w_s, lt_s);
 }
 
 }  // namespace locks
@@ -230,7 +272,7 @@ extern "C" int32_t locks_decode_splitk(
     LOCKS_REQUIRE(q && k_cache && v_cache && block_table && page_table && page_cnt && seq_lens &&
                   m_part && l_part && acc_part, "locks_decode_splitk: null pointer argument");
     if (n_req == 0) return 0;
-    hipLaunchKernelGGL(decode_split_kernel, dim3(split, n_kv, n_req), dim3(kWave), 0,
+    hipLaunchKernelGGL(decode_split_kernel, dim3(split, n_kv, n_req), dim3(DC_BLK), 0,
                        (hipStream_t)stream, q, (long)q_stride_req, (long)q_stride_head, k_cache,
                        (long)k_stride_block, (long)k_stride_tok, (long)k_stride_head, v_cache,
                        (long)v_stride_block, (long)v_stride_tok, (long)v_stride_head, num_blocks,
@@ -251,9 +293,12 @@ extern "C" int32_t locks_decode_merge(
     LOCKS_REQUIRE(split >= 1 && split <= MAX_SPLIT, "locks_decode_merge: split %d outside [1, %d]", split, MAX_SPLIT);
     LOCKS_REQUIRE(pps_min >= 1, "locks_decode_merge: pps_min %d < 1", pps_min);
     LOCKS_REQUIRE(m_part && l_part && acc_part && page_cnt && out, "locks_decode_merge: null pointer argument");
+    LOCKS_REQUIRE(out_stride_req % 4 == 0 && out_stride_head % 4 == 0,
+                  "locks_decode_merge: out strides must be multiples of 4 elements");
     if (n_req == 0) return 0;
-    hipLaunchKernelGGL(decode_merge_kernel, dim3(n_kv, n_req), dim3(MG_BLK), 0, (hipStream_t)stream,
+    hipLaunchKernelGGL(decode_merge_kernel, dim3(n_kv, n_req), dim3(DC_BLK), 0, (hipStream_t)stream,
                        m_part, l_part, acc_part, page_cnt, (long)cnt_stride, out, (long)out_stride_req,
                        (long)out_stride_head, out_is_f32, G, split, pps_min);
     return check_launch("decode_merge_kernel");
 }
+

@@ -38,6 +38,7 @@ constexpr int SC_TILE = 8;    // pages per wave tile
 constexpr int SC_WAVES = 4;
 constexpr int SC_BLOCK = SC_WAVES * kWave;
 constexpr int SC_VROW = SC_RNK * SC_D / 2;   // 512 B of packed V per row
+constexpr int SC_MAX_CHUNK = 1024;          // pages per workgroup, upper bound
 
 __device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d) {
     return (uint32_t)(uint8_t)a | ((uint32_t)(uint8_t)b << 8) |
@@ -76,6 +77,7 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
     __shared__ __attribute__((aligned(16))) float qt_l[SC_WAVES][SC_TILE][SC_RNK][16];
     __shared__ __attribute__((aligned(16))) float mud_l[SC_WAVES][SC_TILE][16];
     __shared__ float wmax[SC_WAVES][16];
+    __shared__ int bt_l[SC_MAX_CHUNK];
 
     // ---- stage q (bf16 -> fp32), per-head int8 quantization -------------
     for (int i = tid; i < 16 * SC_D; i += SC_BLOCK) {
@@ -85,6 +87,10 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
         qf[g][d] = v;
     }
     if (tid < SC_WAVES * 16) wmax[tid >> 4][tid & 15] = -INFINITY;
+    for (int i = tid; i < c1 - c0; i += SC_BLOCK) {       // block ids of the chunk
+        const int b = bt[(long)r * bt_sr + min(c0 + i, bt_cols - 1)];
+        bt_l[i] = min(max(b, 0), NB - 1);
+    }
     __syncthreads();
     for (int g = wave; g < 16; g += SC_WAVES) {
         const float a0 = qf[g][lane], a1 = qf[g][lane + 64];
@@ -126,81 +132,88 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
     const int g_l = jcol % GW;               // head of this lane's column
     float hmax = -INFINITY;
     const uint32_t M4 = 0x0F0F0F0Fu;
-
     const int n_tiles = cdiv(c1 - c0, SC_TILE);
-    for (int tt = wave; tt < n_tiles; tt += SC_WAVES) {
+
+    // Everything one tile needs from HBM, held in registers so the next
+    // tile's loads are in flight while the current tile computes.
+    struct Tile {
+        uint4 vv[4];          // packed V: 2 pages x 8 columns x 16 B per lane
+        float vsf[4];         // basis-column scale of this lane's (page, column)
+        v4i mu0, mu1;         // mu row of page (lane & 15) (< 8), 32 B per lane
+        float musf;
+        uint2 c8r[SC_TILE];   // coefficient row of token (lane & 15), all 8 pages
+        uint2 csv[NGRP];      // 4 token scales of this lane's (page, token quad)
+    };
+    auto load_tile = [&](int tt, Tile& T) {
         const int p0 = c0 + tt * SC_TILE;
         const int nvalid = min(SC_TILE, c1 - p0);
-        // lane i (< 8) resolves the block of page p0 + i (clamped to the tile)
-        int pg = p0 + min(lane & 7, nvalid - 1);
-        pg = min(pg, bt_cols - 1);
-        int blk = bt[(long)r * bt_sr + pg];
-        blk = min(max(blk, 0), NB - 1);
-        int blkv[SC_TILE];
-#pragma unroll
-        for (int i = 0; i < SC_TILE; ++i) blkv[i] = __shfl(blk, i, kWave);
+        // block of page p0 + (lane & 7), clamped to the tile (LDS, preloaded)
+        const int blk = bt_l[p0 - c0 + min(lane & 7, nvalid - 1)];
         const long myrow = (long)blk * n_kv + kh;
-
-        // ---- issue every load of the tile up front -----------------------
-        uint4 vv[4];
-        float vsf[4];
 #pragma unroll
         for (int pp = 0; pp < 4; ++pp) {
             const int b = __shfl(blk, 2 * pp + ((lane >> 3) & 1), kWave);
             const long row = (long)b * n_kv + kh;
-            vv[pp] = *reinterpret_cast<const uint4*>(
+            T.vv[pp] = *reinterpret_cast<const uint4*>(
                 v4 + row * SC_VROW + (lane & 7) * (SC_D / 2) + kg * 16);
-            vsf[pp] = bf16_to_f32(vs[row * SC_RNK + (lane & 7)]);
+            T.vsf[pp] = bf16_to_f32(vs[row * SC_RNK + (lane & 7)]);
         }
-        v4i mu0 = {0, 0, 0, 0}, mu1 = {0, 0, 0, 0};
-        float musf = 0.f;
+        T.mu0 = v4i{0, 0, 0, 0};
+        T.mu1 = v4i{0, 0, 0, 0};
+        T.musf = 0.f;
         if ((lane & 15) < 8) {
             const int8_t* mp = mu8 + myrow * SC_D + kg * 32;
-            mu0 = *reinterpret_cast<const v4i*>(mp);
-            mu1 = *reinterpret_cast<const v4i*>(mp + 16);
-            musf = bf16_to_f32(mus[myrow]);
+            T.mu0 = *reinterpret_cast<const v4i*>(mp);
+            T.mu1 = *reinterpret_cast<const v4i*>(mp + 16);
+            T.musf = bf16_to_f32(mus[myrow]);
         }
-        uint2 c8r[SC_TILE];
 #pragma unroll
         for (int i = 0; i < SC_TILE; ++i) {
-            const long row = (long)blkv[i] * n_kv + kh;
-            c8r[i] = *reinterpret_cast<const uint2*>(c8 + row * (SC_PG * SC_RNK) + r16 * SC_RNK);
+            const long row = (long)__shfl(blk, i, kWave) * n_kv + kh;
+            T.c8r[i] = *reinterpret_cast<const uint2*>(c8 + row * (SC_PG * SC_RNK) + r16 * SC_RNK);
         }
-        uint2 csv[NGRP];
 #pragma unroll
         for (int gi = 0; gi < NGRP; ++gi) {
-            const int b = (PPM == 1) ? blkv[gi] : __shfl(blk, gi * PPM + psub_l, kWave);
-            const long row = (long)b * n_kv + kh;
-            csv[gi] = *reinterpret_cast<const uint2*>(cs + row * SC_PG + 4 * kg);
+            const long row = (long)__shfl(blk, gi * PPM + psub_l, kWave) * n_kv + kh;
+            T.csv[gi] = *reinterpret_cast<const uint2*>(cs + row * SC_PG + 4 * kg);
         }
+    };
+
+    Tile cur, nxt;
+    int tt = wave;
+    if (tt < n_tiles) load_tile(tt, cur);
+    for (; tt < n_tiles; tt += SC_WAVES) {
+        if (tt + SC_WAVES < n_tiles) load_tile(tt + SC_WAVES, nxt);
+        const int p0 = c0 + tt * SC_TILE;
+        const int nvalid = min(SC_TILE, c1 - p0);
 
         // ---- projection: qt (GQA group x 8 basis columns) per page -------
 #pragma unroll
         for (int pp = 0; pp < 4; ++pp) {
-            const uint32_t w0 = vv[pp].x ^ 0x88888888u, w1 = vv[pp].y ^ 0x88888888u;
-            const uint32_t w2 = vv[pp].z ^ 0x88888888u, w3 = vv[pp].w ^ 0x88888888u;
+            const uint32_t w0 = cur.vv[pp].x ^ 0x88888888u, w1 = cur.vv[pp].y ^ 0x88888888u;
+            const uint32_t w2 = cur.vv[pp].z ^ 0x88888888u, w3 = cur.vv[pp].w ^ 0x88888888u;
             const v4i b0 = {(int)(w0 & M4), (int)(w1 & M4), (int)((w0 >> 4) & M4), (int)((w1 >> 4) & M4)};
             const v4i b1 = {(int)(w2 & M4), (int)(w3 & M4), (int)((w2 >> 4) & M4), (int)((w3 >> 4) & M4)};
             v4i acc = {0, 0, 0, 0};
             acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(Av[0], b0, acc, 0, 0, 0);
             acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(Av[1], b1, acc, 0, 0, 0);
             float4 qt;
-            qt.x = (float)(acc[0] - qbias[0]) * qs_row[0] * vsf[pp];
-            qt.y = (float)(acc[1] - qbias[1]) * qs_row[1] * vsf[pp];
-            qt.z = (float)(acc[2] - qbias[2]) * qs_row[2] * vsf[pp];
-            qt.w = (float)(acc[3] - qbias[3]) * qs_row[3] * vsf[pp];
+            qt.x = (float)(acc[0] - qbias[0]) * qs_row[0] * cur.vsf[pp];
+            qt.y = (float)(acc[1] - qbias[1]) * qs_row[1] * cur.vsf[pp];
+            qt.z = (float)(acc[2] - qbias[2]) * qs_row[2] * cur.vsf[pp];
+            qt.w = (float)(acc[3] - qbias[3]) * qs_row[3] * cur.vsf[pp];
             *reinterpret_cast<float4*>(&qt_l[wave][2 * pp + ((lane & 15) >> 3)][lane & 7][4 * kg]) = qt;
         }
         {
             v4i accm = {0, 0, 0, 0};
-            accm = __builtin_amdgcn_mfma_i32_16x16x64_i8(Amu[0], mu0, accm, 0, 0, 0);
-            accm = __builtin_amdgcn_mfma_i32_16x16x64_i8(Amu[1], mu1, accm, 0, 0, 0);
+            accm = __builtin_amdgcn_mfma_i32_16x16x64_i8(Amu[0], cur.mu0, accm, 0, 0, 0);
+            accm = __builtin_amdgcn_mfma_i32_16x16x64_i8(Amu[1], cur.mu1, accm, 0, 0, 0);
             if ((lane & 15) < 8) {
                 float4 md;
-                md.x = (float)accm[0] * qs_row[0] * musf;
-                md.y = (float)accm[1] * qs_row[1] * musf;
-                md.z = (float)accm[2] * qs_row[2] * musf;
-                md.w = (float)accm[3] * qs_row[3] * musf;
+                md.x = (float)accm[0] * qs_row[0] * cur.musf;
+                md.y = (float)accm[1] * qs_row[1] * cur.musf;
+                md.z = (float)accm[2] * qs_row[2] * cur.musf;
+                md.w = (float)accm[3] * qs_row[3] * cur.musf;
                 *reinterpret_cast<float4*>(&mud_l[wave][lane & 15][4 * kg]) = md;
             }
         }
@@ -215,15 +228,15 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
                 const int psub = s >> 1;
                 const int page = gi * PPM + psub;
                 const int cc = kg + 4 * (s & 1);
-                const uint32_t word = (s & 1) ? c8r[page].y : c8r[page].x;
+                const uint32_t word = (s & 1) ? cur.c8r[page].y : cur.c8r[page].x;
                 const float a = (float)(int8_t)(word >> (8 * kg));
                 const float b = (psub_l == psub) ? qt_l[wave][page][cc][g_l] : 0.f;
                 acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc, 0, 0, 0);
             }
             const int page = gi * PPM + psub_l;
             const float mud = mud_l[wave][page][g_l];
-            const float cs0 = bf16lo(csv[gi].x), cs1 = bf16hi(csv[gi].x);
-            const float cs2 = bf16lo(csv[gi].y), cs3 = bf16hi(csv[gi].y);
+            const float cs0 = bf16lo(cur.csv[gi].x), cs1 = bf16hi(cur.csv[gi].x);
+            const float cs2 = bf16lo(cur.csv[gi].y), cs3 = bf16hi(cur.csv[gi].y);
             const float t0 = sm_scale * fmaf(acc[0], cs0, mud);
             const float t1 = sm_scale * fmaf(acc[1], cs1, mud);
             const float t2 = sm_scale * fmaf(acc[2], cs2, mud);
@@ -242,6 +255,7 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
             }
         }
         wave_lds_sync();
+        cur = nxt;
     }
 
     // ---- publish this chunk's per-head page maxima -----------------------
@@ -262,11 +276,11 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
 using namespace locks;
 
 extern "C" int32_t locks_score_auto_chunk(int32_t n_req, int32_t n_kv, int32_t max_pages) {
-    // Aim for ~4 workgroups per CU on a 256-CU MI355X at the configured
+    // Aim for ~2 workgroups per CU on a 256-CU MI355X at the configured
     // (n_req x n_kv) base grid, in whole 32-page units.
     const long units = (long)cdiv(max_pages > 0 ? max_pages : 1, 32);
     const long base = (long)(n_req > 0 ? n_req : 1) * (n_kv > 0 ? n_kv : 1);
-    long z_target = (1024 + base - 1) / base;
+    long z_target = (512 + base - 1) / base;
     if (z_target < 1) z_target = 1;
     long per = (units + z_target - 1) / z_target;
     if (per < 1) per = 1;
@@ -296,7 +310,8 @@ extern "C" int32_t locks_score_rki4(
     LOCKS_REQUIRE(num_blocks >= 1 && bt_cols >= 1 && max_pages >= 1,
                   "locks_score_rki4: empty geometry (num_blocks=%d bt_cols=%d max_pages=%d)",
                   num_blocks, bt_cols, max_pages);
-    LOCKS_REQUIRE(chunk >= 32 && chunk % 32 == 0, "locks_score_rki4: chunk %d must be a positive multiple of 32", chunk);
+    LOCKS_REQUIRE(chunk >= 32 && chunk % 32 == 0 && chunk <= SC_MAX_CHUNK,
+                  "locks_score_rki4: chunk %d must be a multiple of 32 in [32, %d]", chunk, SC_MAX_CHUNK);
     LOCKS_REQUIRE(q && v4 && vs && c8 && cs && mu8 && mus && block_table && n_sel_hi && score_h && page_max,
                   "locks_score_rki4: null pointer argument");
     if (n_req == 0) return 0;

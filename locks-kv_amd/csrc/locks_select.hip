@@ -26,6 +26,9 @@
 //   sel_finish_kernel (grid: kv heads x requests)
 //       gathers the <= b candidates of every chunk into LDS, radix-selects
 //       the exact b-th largest key and compacts the kept pages.
+// (Folding the finish into the last-arriving chunk needs an agent-scope
+// release fence, which on MI355X writes back the XCD's dirty L2 and measured
+// slower than the second launch.)
 // Radix keys are the order-preserving fp32 -> u32 map; the keep test is a
 // key compare, so it is exact for every finite score.
 #include "locks_common.h"
@@ -72,6 +75,21 @@ __device__ __forceinline__ int block_excl_scan(int v, int* wsum, int& total) {
     return res;
 }
 
+// LDS histogram increment with wave aggregation: lanes whose bin equals the
+// first active lane's bin are counted by one atomic (scores cluster, so most
+// keys of a digit pass share a bin and plain LDS atomics serialize).
+__device__ __forceinline__ void hist_add(int* hist, int bin, bool valid) {
+    const int lane = threadIdx.x & 63;
+    const unsigned long long act = __ballot(valid);
+    if (act == 0ull) return;
+    const int leader = __ffsll((long long)act) - 1;
+    const int b0 = __shfl(bin, leader, kWave);
+    const bool same = valid && bin == b0;
+    const unsigned long long m = __ballot(same);
+    if (lane == leader) atomicAdd(&hist[b0], __popcll(m));
+    if (valid && !same) atomicAdd(&hist[bin], 1);
+}
+
 // k-th largest (1 <= k <= n) u32 key by 4 passes of 8-bit MSD radix.  If a
 // pass finds that the whole boundary bin is needed it stops early and the
 // returned value has zero low digits (then #(key >= result) == k exactly).
@@ -85,7 +103,8 @@ __device__ uint32_t block_kth_largest(const uint32_t* keys, int n, int k, int* h
         __syncthreads();
         for (int i = tid; i < n; i += BLK) {
             const uint32_t u = keys[i];
-            if ((u & kmask) == prefix) atomicAdd(&hist[(u >> shift) & 0xFF], 1);
+            const bool in = (u & kmask) == prefix;
+            hist_add(hist, (u >> shift) & 0xFF, in);
         }
         __syncthreads();
         if (tid < kWave) {
@@ -163,6 +182,53 @@ __device__ __forceinline__ void fill_all_pages(int* row, int n_pages, int MP, bo
         if (i < n_pages) row[i] = i;
         else if (pad) row[i] = -1;
     }
+}
+
+// Finish one row from the chunk candidates (ascending page order per chunk):
+// exact b-th largest key over all candidates, ordered emission, sink/window.
+// LDS arguments: offs[FIN_MAXZ+1], lkey/lpage[FIN_CAP], hist[256], s3[4], wsum.
+template <int BLK>
+__device__ void finish_row(long rk, int n_pages, int n_sel_hi, int n_sink, int b, int MP, int Z1,
+                           int* __restrict__ trow, int* __restrict__ cnt_out,
+                           const uint32_t* __restrict__ cand_key, const int* __restrict__ cand_page,
+                           const int* __restrict__ cand_cnt, uint32_t* __restrict__ spill_key,
+                           int* __restrict__ spill_page, int* offs, uint32_t* lkey, int* lpage,
+                           int* hist, int* s3, int* wsum) {
+    constexpr int NWV = BLK / kWave;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    {
+        int run = 0;
+        for (int base = 0; base < Z1; base += BLK) {
+            const int zz = base + tid;
+            const int c = (zz < Z1) ? cand_cnt[rk * Z1 + zz] : 0;
+            int tot;
+            const int ex = block_excl_scan<BLK>(c, wsum, tot);
+            if (zz < Z1) offs[zz] = run + ex;
+            run += tot;
+        }
+        if (tid == 0) offs[Z1] = run;
+        __syncthreads();
+    }
+    const int N = offs[Z1];
+    uint32_t* kk = (N <= FIN_CAP) ? lkey : spill_key + rk * (long)MP;
+    int* pp = (N <= FIN_CAP) ? lpage : spill_page + rk * (long)MP;
+    for (int zz = wave; zz < Z1; zz += NWV) {                 // chunk order == page order
+        const int o = offs[zz], c = offs[zz + 1] - o;
+        const uint32_t* sk = cand_key + (rk * Z1 + zz) * (long)SEL_CH;
+        const int* sp = cand_page + (rk * Z1 + zz) * (long)SEL_CH;
+        for (int i = lane; i < c; i += kWave) {
+            kk[o + i] = sk[i];
+            pp[o + i] = sp[i];
+        }
+    }
+    __syncthreads();
+    const uint32_t tau = block_kth_largest<BLK>(kk, N, b, hist, s3);
+    const int nsel_w = emit_topk<BLK>(kk, N, b, tau, [&](int i) { return pp[i]; },
+                                      trow + n_sink, nullptr, wsum);
+    const int cnt = n_sink + nsel_w + (n_pages - n_sel_hi);
+    for (int i = tid; i < n_sink; i += BLK) trow[i] = i;
+    for (int i = n_sink + nsel_w + tid; i < cnt; i += BLK) trow[i] = n_sel_hi + (i - n_sink - nsel_w);
+    if (tid == 0) *cnt_out = cnt;
 }
 
 // ---------------------------------------------------------------------------
@@ -270,6 +336,9 @@ __global__ __launch_bounds__(SEL_BLK) void sel_chunk_kernel(
 // ---------------------------------------------------------------------------
 // finishing kernel (multi-chunk rows)
 // ---------------------------------------------------------------------------
+// ---------------------------------------------------------------------------
+// finishing kernel (rows spanning several chunks)
+// ---------------------------------------------------------------------------
 __global__ __launch_bounds__(FIN_BLK) void sel_finish_kernel(
     const int* __restrict__ npg, const int* __restrict__ nsh, const int* __restrict__ bfix,
     int* __restrict__ page_table, int* __restrict__ page_cnt,
@@ -278,68 +347,27 @@ __global__ __launch_bounds__(FIN_BLK) void sel_finish_kernel(
     int n_sink, int MP, int Z1)
 {
     const int kh = blockIdx.y, r = blockIdx.z;
-    const int n_kv = gridDim.y;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    constexpr int NWV = FIN_BLK / kWave;
-    const long rk = (long)r * n_kv + kh;
+    const long rk = (long)r * gridDim.y + kh;
     const int n_pages = min(npg[r], MP);
     const int n_sel_hi = min(nsh[r], MP);
     const int n_sel = n_sel_hi - n_sink;
-    const bool keep_all = n_sel <= 1;
     int b = bfix[r];
     b = max(1, min(b, max(n_sel, 1)));
     int* trow = page_table + rk * (long)MP;
-
-    if (keep_all || b >= n_sel) {
-        for (int i = tid; i < max(n_pages, 0); i += FIN_BLK) trow[i] = i;
-        if (tid == 0) page_cnt[rk] = max(n_pages, 0);
+    if (n_sel <= 1 || b >= n_sel) {
+        for (int i = threadIdx.x; i < max(n_pages, 0); i += FIN_BLK) trow[i] = i;
+        if (threadIdx.x == 0) page_cnt[rk] = max(n_pages, 0);
         return;
     }
-
     __shared__ int offs[FIN_MAXZ + 1];
     __shared__ uint32_t lkey[FIN_CAP];
     __shared__ int lpage[FIN_CAP];
     __shared__ int hist[256];
     __shared__ int s3[4];
-    __shared__ int wsum[NWV + 1];
-
-    // exclusive scan of the chunk candidate counts
-    {
-        int run = 0;
-        for (int base = 0; base < Z1; base += FIN_BLK) {
-            const int zz = base + tid;
-            const int c = (zz < Z1) ? cand_cnt[rk * Z1 + zz] : 0;
-            int tot;
-            const int ex = block_excl_scan<FIN_BLK>(c, wsum, tot);
-            if (zz < Z1) offs[zz] = run + ex;
-            run += tot;
-        }
-        if (tid == 0) offs[Z1] = run;
-        __syncthreads();
-    }
-    const int N = offs[Z1];
-    uint32_t* kk = (N <= FIN_CAP) ? lkey : spill_key + rk * (long)MP;
-    int* pp = (N <= FIN_CAP) ? lpage : spill_page + rk * (long)MP;
-
-    // gather: wave w copies chunks w, w + NWV, ... (chunk order == page order)
-    for (int zz = wave; zz < Z1; zz += NWV) {
-        const int o = offs[zz], c = offs[zz + 1] - o;
-        const uint32_t* sk = cand_key + (rk * Z1 + zz) * (long)SEL_CH;
-        const int* sp = cand_page + (rk * Z1 + zz) * (long)SEL_CH;
-        for (int i = lane; i < c; i += kWave) {
-            kk[o + i] = sk[i];
-            pp[o + i] = sp[i];
-        }
-    }
-    __syncthreads();
-
-    const uint32_t tau = block_kth_largest<FIN_BLK>(kk, N, b, hist, s3);
-    const int nsel_w = emit_topk<FIN_BLK>(kk, N, b, tau, [&](int i) { return pp[i]; },
-                                          trow + n_sink, nullptr, wsum);
-    const int cnt = n_sink + nsel_w + (n_pages - n_sel_hi);
-    for (int i = tid; i < n_sink; i += FIN_BLK) trow[i] = i;
-    for (int i = n_sink + nsel_w + tid; i < cnt; i += FIN_BLK) trow[i] = n_sel_hi + (i - n_sink - nsel_w);
-    if (tid == 0) page_cnt[rk] = cnt;
+    __shared__ int wsum[FIN_BLK / kWave + 1];
+    finish_row<FIN_BLK>(rk, n_pages, n_sel_hi, n_sink, b, MP, Z1, trow, page_cnt + rk, cand_key,
+                        cand_page, cand_cnt, spill_key, spill_page, offs, lkey, lpage, hist, s3,
+                        wsum);
 }
 
 // ---------------------------------------------------------------------------

@@ -45,11 +45,17 @@ class ResidentVSource:
         return v, v.stride(0), v.stride(1), v.stride(2)
 
 
+PPS_MIN_OVERRIDE = None        # set by bench sweeps; None = the table below
+
+
 def _pps_min(n_req: int, n_kv: int = 8) -> int:
-    """Minimum pages per split (amortises the q load / partial store)."""
+    """Minimum pages per split workgroup (4 waves x 2 pages at bs=1): amortises
+    the q load, the 4-wave LDS merge and the partial store."""
+    if PPS_MIN_OVERRIDE:
+        return int(PPS_MIN_OVERRIDE)
     if n_req == 1:
-        return 2
-    return 8 if n_req < 16 else 16
+        return 8
+    return 16 if n_req < 16 else 32
 
 
 def _adaptive_split(max_reqs: int, max_pages: int, budget: float, hard_cap: int) -> int:

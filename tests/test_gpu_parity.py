@@ -142,6 +142,12 @@ def test_select_matches_oracle(combine, seq_lens, n_kv, G, bp):
     sh, npg, nsh, b = _random_select_inputs(2, n_kv, G, seq_lens, MP, st)
     rki4_select_only(st, case.R)
     torch.cuda.synchronize()
+    first = (st.page_table.clone(), st.page_cnt.clone())
+    for _ in range(2):                  # repeated calls: arrival counters reset
+        st.page_table.fill_(7)
+        rki4_select_only(st, case.R)
+        torch.cuda.synchronize()
+        assert torch.equal(st.page_table, first[0]) and torch.equal(st.page_cnt, first[1])
     assert (st.n_pages.cpu().numpy() == npg).all() and (st.n_sel_hi.cpu().numpy() == nsh).all()
     assert (st.b_fix.cpu().numpy() == b).all()
     comb = O.combine_nrm(sh, nsh) if combine == "nrm" else O.combine_max(sh, nsh)
