@@ -292,6 +292,8 @@ def main():
     m = make_model(wl, a.budget_pages, summaries=a.summaries, zsplit=a.zsplit or None)
     log(f"model ready in {time.perf_counter() - t0:.1f}s (summary build {m['build_s']:.1f}s)")
     if a.profile_scorer:
+        from locks.selection import derive_page_params
+        derive_page_params(m["st"], m["sl"], m["R"])
         us = scorer_roofline(m, reps=a.profile_scorer)
         log(f"scorer avg {us:.2f} us/launch")
         return

@@ -154,6 +154,38 @@ int32_t locks_decode_merge(const float* m_part, const float* l_part, const float
                            int32_t n_req, int32_t n_kv, int32_t G, int32_t head_dim,
                            int32_t split, int32_t pps_min, void* stream);
 
+/*
+ * rki4 summary build on the GPU for the listed physical blocks of ONE layer.
+ * Replaces the reference build chain _write_pre -> _eigh_chunked ->
+ * _write_post (selection/rki4_build.py:147-158, :93-129, :178-225, the
+ * `rki4_build_{tail,bulk,delta,refresh}` producers :264-364 call it):
+ * gram on the matrix core, 16x16 parallel Jacobi eigensolver, quantize/pack.
+ *   k_cache   K half of one layer, element strides of (block, token, kv head)
+ *   blocks    (n_blocks,) i32 physical block ids; ids outside [0, num_blocks)
+ *             are skipped (rki4_build.py:133-144)
+ *   outputs   the layer's six slabs (as in locks_score_rki4) and the tag
+ *             (num_blocks, n_kv, 8) bf16 = K[page-1, kh, 0:8]
+ * Eigenvectors agree with any other eigensolver up to sign / rotation inside
+ * degenerate eigenspaces, so bytes are comparable only through the score.
+ */
+int32_t locks_build_rki4(const uint16_t* k_cache, int64_t k_stride_block, int64_t k_stride_tok,
+                         int64_t k_stride_head, int32_t num_blocks, const int32_t* blocks,
+                         int32_t n_blocks, int32_t n_kv, int32_t head_dim, int32_t page,
+                         uint8_t* v4, uint16_t* vs, int8_t* c8, uint16_t* cs, int8_t* mu8,
+                         uint16_t* mus, uint16_t* tag, void* stream);
+
+/*
+ * Quantize + pack from a given eigen decomposition (the _write_post half,
+ * selection/rki4_build.py:178-225 with the int4 pack :161-175), bit-exact to
+ * the reference op order.  Inputs per page i < n: mu (n, 128) f32, dc
+ * (n, 16, 128) f32, S2 (n, 16) f32 ascending, U (n, 16, 16) f32 (columns =
+ * eigenvectors); rows (n,) i32 = slab row (block * n_kv + kv head).
+ */
+int32_t locks_pack_rki4(const float* mu, const float* dc, const float* S2, const float* U,
+                        const int32_t* rows, int32_t n, int32_t head_dim, int32_t page,
+                        uint8_t* v4, uint16_t* vs, int8_t* c8, uint16_t* cs, int8_t* mu8,
+                        uint16_t* mus, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

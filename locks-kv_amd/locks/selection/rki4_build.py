@@ -1,98 +1,67 @@
 """rki4 summary build (off the hot path): finalized K pages -> six slabs.
 
-Op sequence of the reference builder (src/locks/selection/rki4_build.py:
-147-158 _write_pre, :93-129 chunked eigh, :178-225 _write_post, :161-175
-int4 pack), per (block, kv head):
-    mu = mean_t K; dc = K - mu; Gm = dc dc^T (page x page)
-    S2, U = eigh(Gm) (ascending); S8 = sqrt(max(S2[-8:], 1e-10)); U8 = U[:, -8:]
-    C = U8 * S8; V = dc^T U8 / S8
-    vs = max(|V|_d / 7, 1e-8); Vq = clamp(round(V / vs), -8, 7)   (int4, packed)
-    cs = max(|C|_r / 127, 1e-8); Cq = clamp(round(C / cs), +-127)  (int8)
-    ms = max(|mu| / 127, 1e-8);  muq = clamp(round(mu / ms), +-127) (int8)
-Scales are stored as bf16; the tag is K[page-1, :, :8].
-Runs with torch on the state's device (eigh: rocSOLVER on ROCm), chunked.
+Runs on the GPU through ``locks_build_rki4`` (gram on the matrix core,
+16x16 parallel Jacobi eigensolver, quantize/pack), following the reference
+builder's op sequence (src/locks/selection/rki4_build.py:147-158 _write_pre,
+:93-129 eigh, :178-225 _write_post, :161-175 int4 pack).  The lifecycle
+entry ``rki4_build_refresh`` mirrors rki4_build.py:318-364 (content-tag
+staleness); ``rki4_pack`` exposes the quantize/pack half for callers that
+bring their own eigen decomposition.
 """
 from __future__ import annotations
 
 import torch
 
-from .rki4_state import QMAX, QMIN, RNK
-
-EIGH_CHUNK = 8192
+from .. import _lib
 
 
-def pack_i4(vc: torch.Tensor) -> torch.Tensor:
-    """int8 (..., d) in [-8, 7] -> uint8 (..., d/2), low nibble = even d."""
-    lo = (vc[..., 0::2] & 0xF).to(torch.uint8)
-    hi = (vc[..., 1::2] & 0xF).to(torch.uint8)
-    return (lo | (hi << 4)).contiguous()
-
-
-def _eigh_chunked(Gf: torch.Tensor):
-    n = Gf.shape[-1]
-    S2 = torch.empty(Gf.shape[0], n, device=Gf.device, dtype=torch.float32)
-    U = torch.empty_like(Gf)
-    for i in range(0, Gf.shape[0], EIGH_CHUNK):
-        S2[i:i + EIGH_CHUNK], U[i:i + EIGH_CHUNK] = torch.linalg.eigh(Gf[i:i + EIGH_CHUNK])
-    return S2, U
-
-
-def summarize_pages(kp: torch.Tensor):
-    """kp (N, page, n_kv, d) bf16 -> dict of slab tensors for those N blocks."""
-    N, page, n_kv, d = kp.shape
-    tag = kp[:, page - 1, :, :8]
-    K = kp.permute(0, 2, 1, 3).float().contiguous()          # (N, n_kv, page, d)
-    mu = K.mean(2)
-    dc = K - mu[:, :, None]
-    Gm = dc @ dc.transpose(-1, -2)
-    S2, U = _eigh_chunked(Gm.reshape(-1, page, page))
-    S2 = S2.reshape(N, n_kv, page)
-    U = U.reshape(N, n_kv, page, page)
-    S8 = S2[..., -RNK:].clamp_min(1e-10).sqrt()
-    U8 = U[..., -RNK:]
-    C = U8 * S8[..., None, :]
-    V = dc.transpose(-1, -2) @ U8 / S8[..., None, :]
-    vsc = (V.abs().amax(2) / float(QMAX)).clamp_min(1e-8)
-    Vq = torch.round(V / vsc[:, :, None]).clamp(QMIN, QMAX)
-    v4 = pack_i4(Vq.permute(0, 1, 3, 2).contiguous().to(torch.int8))
-    csc = (C.abs().amax(-1) / 127.0).clamp_min(1e-8)
-    Cq = torch.round(C / csc[..., None]).clamp(-127, 127)
-    msc = (mu.abs().amax(-1) / 127.0).clamp_min(1e-8)
-    muq = torch.round(mu / msc[..., None]).clamp(-127, 127)
-    return dict(v4=v4, vs=vsc.to(torch.bfloat16), c8=Cq.to(torch.int8),
-                cs=csc.to(torch.bfloat16), mu8=muq.to(torch.int8),
-                mus=msc.to(torch.bfloat16), tag=tag.to(torch.bfloat16))
+def _slabs(st, layer):
+    return (st.pp_v4[layer], st.pp_vs[layer], st.pp_c8[layer], st.pp_cs[layer],
+            st.pp_mu8[layer], st.pp_mus[layer], st.pp_tag[layer])
 
 
 @torch.no_grad()
-def rki4_build_blocks(st, layer: int, K: torch.Tensor, blocks: torch.Tensor,
-                      chunk: int = 8192) -> int:
+def rki4_build_blocks(st, layer: int, K: torch.Tensor, blocks: torch.Tensor) -> int:
     """(Re)build the summaries of physical ``blocks`` of one layer from the K
-    half ``K`` (NB, page, n_kv, d).  Out-of-range block ids are dropped
-    (rki4_build.py:133-144)."""
+    half ``K`` (NB, page, n_kv, d) view.  Ids outside [0, NB) are skipped."""
+    if K.dtype != torch.bfloat16 or K.stride(-1) != 1:
+        raise TypeError("K must be bf16 with a contiguous head dim")
+    b = blocks.to(device=K.device, dtype=torch.int32).contiguous()
+    n = int(b.numel())
+    if n == 0:
+        return 0
+    v4, vs, c8, cs, mu8, mus, tag = _slabs(st, layer)
     nb = min(int(st.NB), int(K.shape[0]))
-    blocks = blocks.to(device=K.device, dtype=torch.int64)
-    blocks = blocks[(blocks >= 0) & (blocks < nb)]
-    n = int(blocks.numel())
-    for i in range(0, n, chunk):
-        b = blocks[i:i + chunk]
-        s = summarize_pages(K[b])
-        st.pp_v4[layer, b] = s["v4"]
-        st.pp_vs[layer, b] = s["vs"]
-        st.pp_c8[layer, b] = s["c8"]
-        st.pp_cs[layer, b] = s["cs"]
-        st.pp_mu8[layer, b] = s["mu8"]
-        st.pp_mus[layer, b] = s["mus"]
-        st.pp_tag[layer, b] = s["tag"]
+    lib = _lib.load()
+    _lib.check(lib.locks_build_rki4(
+        _lib.ptr(K), K.stride(0), K.stride(1), K.stride(2), nb, _lib.ptr(b), n, int(st.n_kv),
+        int(st.d), int(st.page), _lib.ptr(v4), _lib.ptr(vs), _lib.ptr(c8), _lib.ptr(cs),
+        _lib.ptr(mu8), _lib.ptr(mus), _lib.ptr(tag), _lib.stream_ptr(K.device)), "build_rki4")
     return n
+
+
+@torch.no_grad()
+def rki4_pack(st, layer: int, mu, dc, S2, U, rows) -> None:
+    """Quantize + pack from a given eigen decomposition (fp32 device tensors
+    mu (n, d), dc (n, page, d), S2 (n, page) ascending, U (n, page, page);
+    rows (n,) int32 = block * n_kv + kv head)."""
+    v4, vs, c8, cs, mu8, mus, _ = _slabs(st, layer)
+    ts = [t.contiguous() for t in (mu, dc, S2, U)]
+    rows = rows.to(torch.int32).contiguous()
+    lib = _lib.load()
+    _lib.check(lib.locks_pack_rki4(
+        *[_lib.ptr(t) for t in ts], _lib.ptr(rows), int(rows.numel()), int(st.d), int(st.page),
+        _lib.ptr(v4), _lib.ptr(vs), _lib.ptr(c8), _lib.ptr(cs), _lib.ptr(mu8), _lib.ptr(mus),
+        _lib.stream_ptr(rows.device)), "pack_rki4")
 
 
 @torch.no_grad()
 def rki4_build_refresh(st, layer: int, K: torch.Tensor, block_table: torch.Tensor,
                        seq_lens: torch.Tensor, n_req: int, *, force: bool = False) -> int:
-    """Rebuild every stale FINALIZED page of the batch (rki4_build.py:318-364):
-    a page is stale when its content tag (first 8 channels of the page's last
-    key) differs from the stored tag (NaN-initialised -> always stale)."""
+    """Rebuild every stale FINALIZED page of the batch: a page is stale when
+    its content tag (first 8 channels of the page's last key) differs from
+    the stored tag (NaN-initialised -> always stale).  Host-side gather of
+    the finalized block list (not graph-safe, like the reference)."""
     if n_req == 0:
         return 0
     page, tagw = st.page, st.tagw

@@ -1,0 +1,104 @@
+"""GPU summary build vs the CPU oracle.
+
+* locks_pack_rki4 (quantize + pack from given eigenpairs): bytes bit-exact
+  to the oracle's summary_post on the same (mu, dc, S2, U).
+* locks_build_rki4 (gram + Jacobi + pack): eigenvectors may differ from
+  LAPACK's by sign / rotation, so it is checked through what the summary is
+  for: dequantized reconstruction C V^T matches the oracle build within the
+  int4/int8 quantization floor, the centroid bytes are exact, the tag is
+  exact, and the page scores of the two builds agree closely.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import locks_oracle as O
+from tests.cases import make_case, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _state(case):
+    from locks.selection import Rki4State
+    return Rki4State("cuda", num_layers=1, num_blocks=case.NB, n_kv=case.n_kv, G=case.G,
+                     head_dim=128, page=16, max_reqs=case.R, max_pages=case.MP, budget_pages=126)
+
+
+def _slabs_np(st):
+    import torch
+    out = {}
+    for n, a, bf in (("v4", "pp_v4", 0), ("vs", "pp_vs", 1), ("c8", "pp_c8", 0), ("cs", "pp_cs", 1),
+                     ("mu8", "pp_mu8", 0), ("mus", "pp_mus", 1), ("tag", "pp_tag", 1)):
+        t = getattr(st, a)[0]
+        x = (t.view(torch.int16) if bf else t).cpu().numpy()
+        out[n] = x.view(np.uint16) if bf else x
+    return out
+
+
+def test_pack_bit_exact():
+    import torch
+    from locks.selection.rki4_build import rki4_pack
+    print("[case] pack bit-exact", flush=True)
+    case = make_case(11, 2, 4, [16 * 300], build=False)
+    blocks = case.bt[0, :300].astype(np.int64)
+    kp = case.k[blocks]
+    tag, mu, dc, gram = O.summary_pre(kp)
+    S2, U = O.summary_eigh(gram)
+    ref = O.summary_post(mu, dc, S2, U)
+    st = _state(case)
+    N, n_kv = mu.shape[:2]
+    rows = (blocks[:, None] * n_kv + np.arange(n_kv)[None, :]).reshape(-1).astype(np.int32)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32).reshape(N * n_kv, *a.shape[2:])).cuda()
+    rki4_pack(st, 0, dev(mu), dev(dc), dev(S2), dev(U), torch.from_numpy(rows).cuda())
+    torch.cuda.synchronize()
+    got = _slabs_np(st)
+    for k in ("v4", "vs", "c8", "cs", "mu8", "mus"):
+        assert np.array_equal(got[k][blocks], ref[k]), k
+
+
+def test_build_matches_oracle_build():
+    import torch
+    from locks.selection.rki4_build import rki4_build_blocks
+    print("[case] build vs oracle", flush=True)
+    case = make_case(12, 2, 4, [16 * 1000])
+    d = to_dev(case)
+    st = _state(case)
+    blocks = np.unique(case.bt[0, :1000]).astype(np.int64)
+    rki4_build_blocks(st, 0, d["kv"][:, 0], torch.from_numpy(blocks))
+    torch.cuda.synchronize()
+    got, ref = _slabs_np(st), case.slabs
+    b = blocks
+    assert np.array_equal(got["mu8"][b], ref["mu8"][b]) and np.array_equal(got["mus"][b], ref["mus"][b])
+    assert np.array_equal(got["tag"][b], case.k[b, 15, :, :8])
+
+    def recon(s):
+        V = O.unpack_i4(s["v4"][b]).astype(np.float64) * O.bf16_to_f32(s["vs"][b])[..., None]
+        C = s["c8"][b].astype(np.float64) * O.bf16_to_f32(s["cs"][b])[..., None]
+        return np.einsum("nktr,nkrd->nktd", C, V)
+    _, _, dc, _ = O.summary_pre(case.k[b])
+    rg, rr = recon(got), recon(ref)
+    eg = np.linalg.norm(rg - dc) / np.linalg.norm(dc)
+    er = np.linalg.norm(rr - dc) / np.linalg.norm(dc)
+    print(f"[case] reconstruction error gpu {eg:.4f} oracle {er:.4f}", flush=True)
+    assert abs(eg - er) < 0.01 and eg < 0.5
+    npg, nsh, _ = O.derive_page_params(case.seq_lens, 16, 1, 1, 126, 0.1)
+    sg = O.score_rki4_twin(case.q, got, case.bt, nsh, 2, 4, case.scale, case.MP)
+    so = O.score_rki4_twin(case.q, ref, case.bt, nsh, 2, 4, case.scale, case.MP)
+    P = int(nsh[0])
+    diff = np.abs(sg[..., :P] - so[..., :P])
+    print(f"[case] score |gpu-build - oracle-build| max {diff.max():.3e} mean {diff.mean():.3e}", flush=True)
+    assert diff.mean() < 0.02 and diff.max() < 0.5
+
+
+def test_refresh_is_tag_gated():
+    import torch
+    from locks.selection.rki4_build import rki4_build_refresh
+    case = make_case(13, 2, 4, [16 * 64 + 5], build=False)
+    d = to_dev(case)
+    st = _state(case)
+    K = d["kv"][:, 0]
+    n1 = rki4_build_refresh(st, 0, K, d["bt"], d["sl"], 1)
+    n2 = rki4_build_refresh(st, 0, K, d["bt"], d["sl"], 1)
+    torch.cuda.synchronize()
+    assert n1 == 64 and n2 == 0          # only finalized pages; second pass: all fresh
