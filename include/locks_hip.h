@@ -54,7 +54,7 @@ int32_t locks_derive_params(const int32_t* seq_lens, int32_t n_req, int32_t page
                             int32_t* b_fix, void* stream);
 
 /*
- * Scorer launch shape: pages per workgroup (a multiple of 32) for a state
+ * Scorer launch shape: pages per workgroup (a multiple of 8) for a state
  * with `max_pages` logical pages, and the resulting number of chunks, which
  * sizes the page-max buffer (n_req, n_kv, chunks, 16) fp32.  Host-only
  * integer math (the reference's auto_zsplit, selection/rki4_score_cuda.py:3161).
@@ -77,7 +77,8 @@ int32_t locks_score_num_chunks(int32_t max_pages, int32_t chunk);
  *   n_sel_hi   (n_req,) i32: pages [0, n_sel_hi) are scored
  *   score_h    (n_req, n_kv, G, max_pages) f32 -- written for p < n_sel_hi only
  *   page_max   (n_req, n_kv, chunks, 16) f32 -- per-chunk per-head maxima
- *   chunk      pages per workgroup (locks_score_auto_chunk)
+ *   chunk      pages per workgroup (locks_score_auto_chunk); one workgroup
+ *              scores its chunk for every kv head (n_kv <= 16, n_kv*G <= 128)
  * Block ids are clamped to [0, num_blocks) and page ids to [0, bt_cols).
  */
 int32_t locks_score_rki4(const uint16_t* q, int64_t q_stride_req, int64_t q_stride_head,

@@ -39,6 +39,8 @@ constexpr int SC_WAVES = 4;
 constexpr int SC_BLOCK = SC_WAVES * kWave;
 constexpr int SC_VROW = SC_RNK * SC_D / 2;   // 512 B of packed V per row
 constexpr int SC_MAX_CHUNK = 1024;          // pages per workgroup, upper bound
+constexpr int SC_MAXKV = 16;                // kv heads per request
+constexpr int SC_MAXHQ = 128;               // query heads per request (n_kv * G)
 
 __device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d) {
     return (uint32_t)(uint8_t)a | ((uint32_t)(uint8_t)b << 8) |
@@ -53,89 +55,75 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
     const int8_t* __restrict__ mu8, const uint16_t* __restrict__ mus,
     int NB, const int* __restrict__ bt, long bt_sr, int bt_cols,
     const int* __restrict__ nsh, float* __restrict__ score_h, int MP,
-    float* __restrict__ pmax, int G, float sm_scale, int chunk)
+    float* __restrict__ pmax, int n_kv, int G, float sm_scale, int chunk)
 {
     constexpr int PPM = 16 / GW;            // pages per token-stage MFMA
     constexpr int NGRP = SC_TILE / PPM;     // token-stage groups per tile
-    const int z = blockIdx.x, kh = blockIdx.y, r = blockIdx.z;
-    const int n_kv = gridDim.y, Z = gridDim.x;
+    const int z = blockIdx.x, r = blockIdx.y;
+    const int Z = gridDim.x;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const long rk = (long)r * n_kv + kh;
-    const int P = min(nsh[r], MP);        // never score past the score_h row
+    const int P = min(nsh[r], MP);          // never score past the score_h row
     const int c0 = z * chunk;
     const int c1 = min(c0 + chunk, P);
+    const int HQ = n_kv * G;
 
     if (c0 >= P) {                          // no page of this chunk is scored
-        if (tid < 16) pmax[(rk * Z + z) * 16 + tid] = -INFINITY;
+        for (int i = tid; i < n_kv * 16; i += SC_BLOCK)
+            pmax[(((long)r * n_kv + i / 16) * Z + z) * 16 + (i % 16)] = -INFINITY;
         return;
     }
 
-    __shared__ float qf[16][SC_D];
-    __shared__ __attribute__((aligned(16))) int8_t q8s[16][SC_D];
-    __shared__ float qs_s[16];
-    __shared__ int qsum_s[16];
+    __shared__ __attribute__((aligned(16))) int8_t q8s[SC_MAXHQ + 16][SC_D];   // + zero rows
+    __shared__ __attribute__((aligned(16))) float qsp[SC_MAXKV][16];
+    __shared__ __attribute__((aligned(16))) int qbp[SC_MAXKV][16];
     __shared__ __attribute__((aligned(16))) float qt_l[SC_WAVES][SC_TILE][SC_RNK][16];
     __shared__ __attribute__((aligned(16))) float mud_l[SC_WAVES][SC_TILE][16];
-    __shared__ float wmax[SC_WAVES][16];
+    __shared__ uint32_t wmax[SC_MAXKV][16];
     __shared__ int bt_l[SC_MAX_CHUNK];
 
-    // ---- stage q (bf16 -> fp32), per-head int8 quantization -------------
-    for (int i = tid; i < 16 * SC_D; i += SC_BLOCK) {
-        const int g = i / SC_D, d = i % SC_D;
-        float v = 0.f;
-        if (g < G) v = bf16_to_f32(q[(long)r * q_sr + (long)(kh * G + g) * q_sh + d]);
-        qf[g][d] = v;
-    }
-    if (tid < SC_WAVES * 16) wmax[tid >> 4][tid & 15] = -INFINITY;
-    for (int i = tid; i < c1 - c0; i += SC_BLOCK) {       // block ids of the chunk
+    // ---- stage: block ids of the chunk, int8 q of every head ------------
+    for (int i = tid; i < c1 - c0; i += SC_BLOCK) {
         const int b = bt[(long)r * bt_sr + min(c0 + i, bt_cols - 1)];
         bt_l[i] = min(max(b, 0), NB - 1);
     }
+    for (int i = tid; i < SC_MAXKV * 16; i += SC_BLOCK) {
+        wmax[i / 16][i % 16] = 0x007FFFFFu;                    // f2u(-inf)
+        qsp[i / 16][i % 16] = 0.f;
+        qbp[i / 16][i % 16] = 0;
+    }
+    for (int i = tid; i < 16 * SC_D / 4; i += SC_BLOCK)
+        reinterpret_cast<int*>(&q8s[HQ][0])[i] = 0;            // zero rows after the last head
     __syncthreads();
-    for (int g = wave; g < 16; g += SC_WAVES) {
-        const float a0 = qf[g][lane], a1 = qf[g][lane + 64];
+    const float s2 = sm_scale * 1.4426950408889634f;           // tokens in log2 units
+    for (int hq = wave; hq < HQ; hq += SC_WAVES) {
+        const uint32_t w = *reinterpret_cast<const uint32_t*>(
+            q + (long)r * q_sr + (long)hq * q_sh + 2 * lane);
+        const float a0 = bf16lo(w), a1 = bf16hi(w);
         const float am = wave_max(fmaxf(fabsf(a0), fabsf(a1)));
         const float qs = fmaxf(am, 1e-8f) / 127.f;
-        int i0 = (int)rintf(__fdiv_rn(a0, qs));
-        int i1 = (int)rintf(__fdiv_rn(a1, qs));
-        if (g >= G) { i0 = 0; i1 = 0; }
-        q8s[g][lane] = (int8_t)i0;
-        q8s[g][lane + 64] = (int8_t)i1;
-        const int s = wave_sum_i(i0 + i1);
-        if (lane == 0) { qs_s[g] = (g < G) ? qs : 0.f; qsum_s[g] = s; }
+        const int i0 = (int)rintf(__fdiv_rn(a0, qs));
+        const int i1 = (int)rintf(__fdiv_rn(a1, qs));
+        q8s[hq][2 * lane] = (int8_t)i0;
+        q8s[hq][2 * lane + 1] = (int8_t)i1;
+        const int sum = wave_sum_i(i0 + i1);
+        if (lane == 0) {
+            qsp[hq / G][hq % G] = qs * s2;
+            qbp[hq / G][hq % G] = 8 * sum;
+        }
     }
     __syncthreads();
 
-    // ---- per-lane MFMA A operands (constant across pages) ----------------
     const int r16 = lane & 15, kg = lane >> 4;
-    v4i Av[2], Amu[2];
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-        const int8_t* qr = &q8s[r16][32 * kg + 16 * s];
-        // V operand order inside a 16-d window: even d (low nibbles) then odd d
-        Av[s][0] = (int)pack4_i8(qr[0], qr[2], qr[4], qr[6]);
-        Av[s][1] = (int)pack4_i8(qr[8], qr[10], qr[12], qr[14]);
-        Av[s][2] = (int)pack4_i8(qr[1], qr[3], qr[5], qr[7]);
-        Av[s][3] = (int)pack4_i8(qr[9], qr[11], qr[13], qr[15]);
-        Amu[s] = *reinterpret_cast<const v4i*>(qr);      // natural d order
-    }
-    float qs_row[4];
-    int qbias[4];
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-        qs_row[v] = qs_s[4 * kg + v];
-        qbias[v] = 8 * qsum_s[4 * kg + v];
-    }
-
     const int jcol = lane & 15;
     const int psub_l = jcol / GW;            // page slot of this lane's column
     const int g_l = jcol % GW;               // head of this lane's column
-    float hmax = -INFINITY;
     const uint32_t M4 = 0x0F0F0F0Fu;
     const int n_tiles = cdiv(c1 - c0, SC_TILE);
+    const int n_units = n_tiles * n_kv;      // (tile, kv head) units of the chunk
 
-    // Everything one tile needs from HBM, held in registers so the next
-    // tile's loads are in flight while the current tile computes.
+    // Everything one unit needs from HBM, in registers, so the next unit's
+    // loads are in flight while the current one computes.  Consecutive
+    // units are the kv heads of one tile, whose slab rows are adjacent.
     struct Tile {
         uint4 vv[4];          // packed V: 2 pages x 8 columns x 16 B per lane
         float vsf[4];         // basis-column scale of this lane's (page, column)
@@ -144,48 +132,61 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
         uint2 c8r[SC_TILE];   // coefficient row of token (lane & 15), all 8 pages
         uint2 csv[NGRP];      // 4 token scales of this lane's (page, token quad)
     };
-    auto load_tile = [&](int tt, Tile& T) {
-        const int p0 = c0 + tt * SC_TILE;
-        const int nvalid = min(SC_TILE, c1 - p0);
-        // block of page p0 + (lane & 7), clamped to the tile (LDS, preloaded)
-        const int blk = bt_l[p0 - c0 + min(lane & 7, nvalid - 1)];
-        const long myrow = (long)blk * n_kv + kh;
+    auto load_unit = [&](int u, Tile& T) {
+        const int t = u / n_kv, h = u - t * n_kv;
+        const int p0 = t * SC_TILE;
+        const int last = min(SC_TILE, c1 - c0 - p0) - 1;
+        const int* bl = bt_l + p0;
+        auto row_of = [&](int i) -> uint32_t { return (uint32_t)bl[min(i, last)] * (uint32_t)n_kv + (uint32_t)h; };
 #pragma unroll
         for (int pp = 0; pp < 4; ++pp) {
-            const int b = __shfl(blk, 2 * pp + ((lane >> 3) & 1), kWave);
-            const long row = (long)b * n_kv + kh;
-            T.vv[pp] = *reinterpret_cast<const uint4*>(
-                v4 + row * SC_VROW + (lane & 7) * (SC_D / 2) + kg * 16);
+            const uint32_t row = row_of(2 * pp + ((lane >> 3) & 1));
+            T.vv[pp] = *reinterpret_cast<const uint4*>(v4 + (row * SC_VROW + (lane & 7) * (SC_D / 2) + kg * 16));
             T.vsf[pp] = bf16_to_f32(vs[row * SC_RNK + (lane & 7)]);
         }
         T.mu0 = v4i{0, 0, 0, 0};
         T.mu1 = v4i{0, 0, 0, 0};
         T.musf = 0.f;
         if ((lane & 15) < 8) {
-            const int8_t* mp = mu8 + myrow * SC_D + kg * 32;
+            const uint32_t row = row_of(lane & 7);
+            const int8_t* mp = mu8 + (row * SC_D + kg * 32);
             T.mu0 = *reinterpret_cast<const v4i*>(mp);
             T.mu1 = *reinterpret_cast<const v4i*>(mp + 16);
-            T.musf = bf16_to_f32(mus[myrow]);
+            T.musf = bf16_to_f32(mus[row]);
         }
 #pragma unroll
-        for (int i = 0; i < SC_TILE; ++i) {
-            const long row = (long)__shfl(blk, i, kWave) * n_kv + kh;
-            T.c8r[i] = *reinterpret_cast<const uint2*>(c8 + row * (SC_PG * SC_RNK) + r16 * SC_RNK);
-        }
+        for (int i = 0; i < SC_TILE; ++i)
+            T.c8r[i] = *reinterpret_cast<const uint2*>(c8 + (row_of(i) * (SC_PG * SC_RNK) + r16 * SC_RNK));
 #pragma unroll
-        for (int gi = 0; gi < NGRP; ++gi) {
-            const long row = (long)__shfl(blk, gi * PPM + psub_l, kWave) * n_kv + kh;
-            T.csv[gi] = *reinterpret_cast<const uint2*>(cs + row * SC_PG + 4 * kg);
-        }
+        for (int gi = 0; gi < NGRP; ++gi)
+            T.csv[gi] = *reinterpret_cast<const uint2*>(cs + (row_of(gi * PPM + psub_l) * SC_PG + 4 * kg));
     };
 
     Tile cur, nxt;
-    int tt = wave;
-    if (tt < n_tiles) load_tile(tt, cur);
-    for (; tt < n_tiles; tt += SC_WAVES) {
-        if (tt + SC_WAVES < n_tiles) load_tile(tt + SC_WAVES, nxt);
-        const int p0 = c0 + tt * SC_TILE;
+    int u = wave;
+    if (u < n_units) load_unit(u, cur);
+    for (; u < n_units; u += SC_WAVES) {
+        if (u + SC_WAVES < n_units) load_unit(u + SC_WAVES, nxt);
+        const int t = u / n_kv, h = u - t * n_kv;
+        const int p0 = c0 + t * SC_TILE;
         const int nvalid = min(SC_TILE, c1 - p0);
+
+        // A operands of this kv head's GQA group (int8 q rows, zero padded)
+        v4i Av[2], Amu[2];
+        {
+            const int row = (r16 < G) ? h * G + r16 : HQ;        // HQ.. = zero rows
+            const uint4 n0 = *reinterpret_cast<const uint4*>(&q8s[row][32 * kg]);
+            const uint4 n1 = *reinterpret_cast<const uint4*>(&q8s[row][32 * kg + 16]);
+            Amu[0] = v4i{(int)n0.x, (int)n0.y, (int)n0.z, (int)n0.w};
+            Amu[1] = v4i{(int)n1.x, (int)n1.y, (int)n1.z, (int)n1.w};
+            // V operand order inside a 16-d window: even d (low nibbles), then odd d
+            Av[0] = v4i{(int)__builtin_amdgcn_perm(n0.y, n0.x, 0x06040200u), (int)__builtin_amdgcn_perm(n0.w, n0.z, 0x06040200u),
+                        (int)__builtin_amdgcn_perm(n0.y, n0.x, 0x07050301u), (int)__builtin_amdgcn_perm(n0.w, n0.z, 0x07050301u)};
+            Av[1] = v4i{(int)__builtin_amdgcn_perm(n1.y, n1.x, 0x06040200u), (int)__builtin_amdgcn_perm(n1.w, n1.z, 0x06040200u),
+                        (int)__builtin_amdgcn_perm(n1.y, n1.x, 0x07050301u), (int)__builtin_amdgcn_perm(n1.w, n1.z, 0x07050301u)};
+        }
+        const float4 qsl = *reinterpret_cast<const float4*>(&qsp[h][4 * kg]);
+        const int4 qb = *reinterpret_cast<const int4*>(&qbp[h][4 * kg]);
 
         // ---- projection: qt (GQA group x 8 basis columns) per page -------
 #pragma unroll
@@ -198,10 +199,10 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
             acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(Av[0], b0, acc, 0, 0, 0);
             acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(Av[1], b1, acc, 0, 0, 0);
             float4 qt;
-            qt.x = (float)(acc[0] - qbias[0]) * qs_row[0] * cur.vsf[pp];
-            qt.y = (float)(acc[1] - qbias[1]) * qs_row[1] * cur.vsf[pp];
-            qt.z = (float)(acc[2] - qbias[2]) * qs_row[2] * cur.vsf[pp];
-            qt.w = (float)(acc[3] - qbias[3]) * qs_row[3] * cur.vsf[pp];
+            qt.x = (float)(acc[0] - qb.x) * qsl.x * cur.vsf[pp];
+            qt.y = (float)(acc[1] - qb.y) * qsl.y * cur.vsf[pp];
+            qt.z = (float)(acc[2] - qb.z) * qsl.z * cur.vsf[pp];
+            qt.w = (float)(acc[3] - qb.w) * qsl.w * cur.vsf[pp];
             *reinterpret_cast<float4*>(&qt_l[wave][2 * pp + ((lane & 15) >> 3)][lane & 7][4 * kg]) = qt;
         }
         {
@@ -210,16 +211,17 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
             accm = __builtin_amdgcn_mfma_i32_16x16x64_i8(Amu[1], cur.mu1, accm, 0, 0, 0);
             if ((lane & 15) < 8) {
                 float4 md;
-                md.x = (float)accm[0] * qs_row[0] * cur.musf;
-                md.y = (float)accm[1] * qs_row[1] * cur.musf;
-                md.z = (float)accm[2] * qs_row[2] * cur.musf;
-                md.w = (float)accm[3] * qs_row[3] * cur.musf;
+                md.x = (float)accm[0] * qsl.x * cur.musf;
+                md.y = (float)accm[1] * qsl.y * cur.musf;
+                md.z = (float)accm[2] * qsl.z * cur.musf;
+                md.w = (float)accm[3] * qsl.w * cur.musf;
                 *reinterpret_cast<float4*>(&mud_l[wave][lane & 15][4 * kg]) = md;
             }
         }
         wave_lds_sync();
 
         // ---- token reconstruction + 16-token LSE per (page, head) --------
+        float tmax = -INFINITY;
 #pragma unroll
         for (int gi = 0; gi < NGRP; ++gi) {
             v4f acc = {0.f, 0.f, 0.f, 0.f};
@@ -235,40 +237,33 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
             }
             const int page = gi * PPM + psub_l;
             const float mud = mud_l[wave][page][g_l];
-            const float cs0 = bf16lo(cur.csv[gi].x), cs1 = bf16hi(cur.csv[gi].x);
-            const float cs2 = bf16lo(cur.csv[gi].y), cs3 = bf16hi(cur.csv[gi].y);
-            const float t0 = sm_scale * fmaf(acc[0], cs0, mud);
-            const float t1 = sm_scale * fmaf(acc[1], cs1, mud);
-            const float t2 = sm_scale * fmaf(acc[2], cs2, mud);
-            const float t3 = sm_scale * fmaf(acc[3], cs3, mud);
+            const float t0 = fmaf(acc[0], bf16lo(cur.csv[gi].x), mud);
+            const float t1 = fmaf(acc[1], bf16hi(cur.csv[gi].x), mud);
+            const float t2 = fmaf(acc[2], bf16lo(cur.csv[gi].y), mud);
+            const float t3 = fmaf(acc[3], bf16hi(cur.csv[gi].y), mud);
             float m = fmaxf(fmaxf(t0, t1), fmaxf(t2, t3));
             m = fmaxf(m, __shfl_xor(m, 16, kWave));
             m = fmaxf(m, __shfl_xor(m, 32, kWave));
-            float e = __expf(t0 - m) + __expf(t1 - m) + __expf(t2 - m) + __expf(t3 - m);
+            float e = __builtin_amdgcn_exp2f(t0 - m) + __builtin_amdgcn_exp2f(t1 - m) +
+                      __builtin_amdgcn_exp2f(t2 - m) + __builtin_amdgcn_exp2f(t3 - m);
             e += __shfl_xor(e, 16, kWave);
             e += __shfl_xor(e, 32, kWave);
-            const float S = m + __logf(e);
-            const bool valid = (page < nvalid) && (g_l < G);
-            if (valid) {
-                hmax = fmaxf(hmax, S);
-                if (lane < 16) score_h[(rk * G + g_l) * (long)MP + p0 + page] = S;
+            const float S = (m + __builtin_amdgcn_logf(e)) * 0.6931471805599453f;
+            if ((page < nvalid) && (g_l < G)) {
+                tmax = fmaxf(tmax, S);
+                if (lane < 16) score_h[(((long)r * n_kv + h) * G + g_l) * (long)MP + p0 + page] = S;
             }
         }
+        // this unit's per-head maxima -> LDS (ordered-uint atomic max)
+#pragma unroll
+        for (int o = GW; o < 16; o <<= 1) tmax = fmaxf(tmax, __shfl_xor(tmax, o, kWave));
+        if (lane < GW && lane < G) atomicMax(&wmax[h][lane], f2u(tmax));
         wave_lds_sync();
         cur = nxt;
     }
-
-    // ---- publish this chunk's per-head page maxima -----------------------
-#pragma unroll
-    for (int o = GW; o < 16; o <<= 1) hmax = fmaxf(hmax, __shfl_xor(hmax, o, kWave));
-    if (lane < GW) wmax[wave][lane] = hmax;
     __syncthreads();
-    if (tid < 16) {
-        float m = wmax[0][tid];
-#pragma unroll
-        for (int w = 1; w < SC_WAVES; ++w) m = fmaxf(m, wmax[w][tid]);
-        pmax[(rk * Z + z) * 16 + tid] = m;
-    }
+    for (int i = tid; i < n_kv * 16; i += SC_BLOCK)
+        pmax[(((long)r * n_kv + i / 16) * Z + z) * 16 + (i % 16)] = u2f(wmax[i / 16][i % 16]);
 }
 
 }  // namespace locks
@@ -276,16 +271,15 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
 using namespace locks;
 
 extern "C" int32_t locks_score_auto_chunk(int32_t n_req, int32_t n_kv, int32_t max_pages) {
-    // Aim for ~2 workgroups per CU on a 256-CU MI355X at the configured
-    // (n_req x n_kv) base grid, in whole 32-page units.
-    const long units = (long)cdiv(max_pages > 0 ? max_pages : 1, 32);
-    const long base = (long)(n_req > 0 ? n_req : 1) * (n_kv > 0 ? n_kv : 1);
-    long z_target = (512 + base - 1) / base;
-    if (z_target < 1) z_target = 1;
-    long per = (units + z_target - 1) / z_target;
-    if (per < 1) per = 1;
-    if (per > 32) per = 32;      // <= 1024 pages per workgroup
-    return (int32_t)(per * 32);
+    // ~512 workgroups (2 per CU on a 256-CU MI355X, the VGPR-limited
+    // occupancy) over all (request, 8-page tile, kv head) units, in whole tiles.
+    const long tiles = (long)cdiv(max_pages > 0 ? max_pages : 1, SC_TILE);
+    const long units = tiles * (n_kv > 0 ? n_kv : 1) * (n_req > 0 ? n_req : 1);
+    const long per_wg = (units + 511) / 512;
+    long ct = (per_wg + (n_kv > 0 ? n_kv : 1) - 1) / (n_kv > 0 ? n_kv : 1);
+    if (ct < 1) ct = 1;
+    if (ct > SC_MAX_CHUNK / SC_TILE) ct = SC_MAX_CHUNK / SC_TILE;
+    return (int32_t)(ct * SC_TILE);
 }
 
 extern "C" int32_t locks_score_num_chunks(int32_t max_pages, int32_t chunk) {
@@ -306,23 +300,29 @@ extern "C" int32_t locks_score_rki4(
     LOCKS_REQUIRE(head_dim == SC_D, "locks_score_rki4: head_dim %d unsupported (this build: 128)", head_dim);
     LOCKS_REQUIRE(page == SC_PG, "locks_score_rki4: page %d unsupported (this build: 16)", page);
     LOCKS_REQUIRE(G >= 1 && G <= 16, "locks_score_rki4: G=%d outside [1, 16]", G);
-    LOCKS_REQUIRE(n_req >= 0 && n_kv >= 1, "locks_score_rki4: bad n_req=%d n_kv=%d", n_req, n_kv);
+    LOCKS_REQUIRE(n_req >= 0 && n_kv >= 1 && n_kv <= SC_MAXKV && n_kv * G <= SC_MAXHQ,
+                  "locks_score_rki4: n_kv=%d G=%d outside this build (n_kv <= %d, n_kv*G <= %d)",
+                  n_kv, G, SC_MAXKV, SC_MAXHQ);
+    LOCKS_REQUIRE(q_stride_head % 2 == 0, "locks_score_rki4: q head stride must be even");
+    LOCKS_REQUIRE((long)num_blocks * n_kv * SC_VROW < (1L << 32),
+                  "locks_score_rki4: slab too large for 32-bit offsets");
     LOCKS_REQUIRE(num_blocks >= 1 && bt_cols >= 1 && max_pages >= 1,
                   "locks_score_rki4: empty geometry (num_blocks=%d bt_cols=%d max_pages=%d)",
                   num_blocks, bt_cols, max_pages);
-    LOCKS_REQUIRE(chunk >= 32 && chunk % 32 == 0 && chunk <= SC_MAX_CHUNK,
-                  "locks_score_rki4: chunk %d must be a multiple of 32 in [32, %d]", chunk, SC_MAX_CHUNK);
+    LOCKS_REQUIRE(chunk >= SC_TILE && chunk % SC_TILE == 0 && chunk <= SC_MAX_CHUNK,
+                  "locks_score_rki4: chunk %d must be a multiple of %d in [%d, %d]", chunk, SC_TILE,
+                  SC_TILE, SC_MAX_CHUNK);
     LOCKS_REQUIRE(q && v4 && vs && c8 && cs && mu8 && mus && block_table && n_sel_hi && score_h && page_max,
                   "locks_score_rki4: null pointer argument");
     if (n_req == 0) return 0;
     const int Z = cdiv(max_pages, chunk);
-    dim3 grid(Z, n_kv, n_req);
+    dim3 grid(Z, n_req);
     hipStream_t st = (hipStream_t)stream;
-#define LAUNCH(GWV)                                                                   \
-    hipLaunchKernelGGL(rki4_score_kernel<GWV>, grid, dim3(SC_BLOCK), 0, st, q,         \
+#define LAUNCH(GWV)                                                                    \
+    hipLaunchKernelGGL((rki4_score_kernel<GWV>), grid, dim3(SC_BLOCK), 0, st, q,        \
                        (long)q_stride_req, (long)q_stride_head, v4, vs, c8, cs, mu8, mus, \
                        num_blocks, block_table, (long)bt_stride, bt_cols, n_sel_hi,       \
-                       score_h, max_pages, page_max, G, sm_scale, chunk)
+                       score_h, max_pages, page_max, n_kv, G, sm_scale, chunk)
     if (G <= 4) LAUNCH(4);
     else if (G <= 8) LAUNCH(8);
     else LAUNCH(16);

@@ -266,6 +266,19 @@ __global__ __launch_bounds__(SEL_BLK) void sel_chunk_kernel(
         for (int i = c0 + tid; i < c1; i += SEL_BLK) trow[i] = -1;
     }
 
+    // ---- issue every score_h load of this thread first (4 pages x G rows)
+    const float* shb = score_h + rk * (long)G * MP;
+    const int pend = min(c1, max(n_sel_hi, c0));
+    constexpr int SEL_E = SEL_CH / SEL_BLK;
+    float x[SEL_E][16];
+#pragma unroll
+    for (int e = 0; e < SEL_E; ++e) {
+        const int p = c0 + tid + e * SEL_BLK;
+#pragma unroll
+        for (int g = 0; g < 16; ++g)
+            x[e][g] = (g < G && p < pend) ? shb[(long)g * MP + p] : 0.f;
+    }
+
     // ---- per-head page max from the scorer's chunk maxima ("nrm") --------
     if (combine == 0) {
         for (int g = wave; g < G; g += SEL_BLK / kWave) {
@@ -278,15 +291,21 @@ __global__ __launch_bounds__(SEL_BLK) void sel_chunk_kernel(
     }
 
     // ---- combine: score[p] for p < nsh, keys for the selectable slice ----
-    const float* shb = score_h + rk * (long)G * MP;
-    for (int p = c0 + tid; p < min(c1, max(n_sel_hi, c0)); p += SEL_BLK) {
+#pragma unroll
+    for (int e = 0; e < SEL_E; ++e) {
+        const int p = c0 + tid + e * SEL_BLK;
+        if (p >= pend) continue;
         float acc;
         if (combine == 0) {
             acc = 0.f;
-            for (int g = 0; g < G; ++g) acc += __expf(shb[(long)g * MP + p] - hm[g]);
+#pragma unroll
+            for (int g = 0; g < 16; ++g)
+                if (g < G) acc += __expf(x[e][g] - hm[g]);
         } else {
-            acc = shb[p];
-            for (int g = 1; g < G; ++g) acc = fmaxf(acc, shb[(long)g * MP + p]);
+            acc = x[e][0];
+#pragma unroll
+            for (int g = 1; g < 16; ++g)
+                if (g < G) acc = fmaxf(acc, x[e][g]);
         }
         score[rk * (long)MP + p] = acc;
         keys[p - c0] = f2u(acc);

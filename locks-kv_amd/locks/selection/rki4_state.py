@@ -86,8 +86,8 @@ class Rki4State:
         lib = _lib.load()
         # scorer launch shape: pages per workgroup (explicit zsplit = chunks)
         if zsplit:
-            chunk = max(32, -(-MP // int(zsplit)))
-            chunk = -(-chunk // 32) * 32
+            chunk = max(8, -(-MP // int(zsplit)))
+            chunk = min(1024, -(-chunk // 8) * 8)
         else:
             chunk = int(lib.locks_score_auto_chunk(R, n_kv, MP))
         self.score_chunk = chunk

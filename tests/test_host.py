@@ -51,7 +51,7 @@ def test_workspace_and_chunk_math():
     from locks import _lib
     lib = _lib.load()
     c = lib.locks_score_auto_chunk(1, 2, 65536)
-    assert c % 32 == 0 and 32 <= c <= 1024
+    assert c % 8 == 0 and 8 <= c <= 1024
     assert lib.locks_score_num_chunks(65536, c) == -(-65536 // c)
     assert lib.locks_select_workspace_bytes(1, 2, 65536) >= 2 * 65536 * 16
     assert lib.locks_select_workspace_bytes(0, 0, 1) == -1
