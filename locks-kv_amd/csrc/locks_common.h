@@ -55,6 +55,28 @@ __device__ __forceinline__ int wave_sum_i(int v) {
     return v;
 }
 
+// Pair reductions across lanes l and l^16 / l^32 with the gfx950 permlane
+// swaps (plain VALU, no LDS round trip).  Swapping a value with itself
+// leaves {x[l], x[l^16]} (resp. {x[l], x[l^32]}) in the two results, in
+// row order, so the pair sum / max equals x + shfl_xor(x, 16 / 32) bit for
+// bit (fp32 add and max are commutative).
+__device__ __forceinline__ float xor16_sum(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_sum(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor16_max(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_max(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 // Order LDS traffic between lanes of ONE wave (no cross-wave barrier).
 __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");

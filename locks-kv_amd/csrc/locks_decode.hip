@@ -17,6 +17,8 @@
 //   * S^T = K Q^T on v_mfma_f32_16x16x32_bf16 (A = K tile: token rows; B = the
 //     GQA group's q rows, zero padded to 16) -- bf16 products, fp32 sum, like
 //     the reference's bf16 tl.dot.  Each lane ends with 4 tokens of one head.
+//     The k-slot -> d map is chosen so each K load reads 64 contiguous bytes
+//     per token row.
 //   * online softmax per head: 4-token in-lane max + 2 cross-row shuffles.
 //   * O^T += V^T P^T on v_mfma_f32_16x16x16f16 with fp16 P and fp16 V (the
 //     reference's fp16 P.V with fp32 accumulation).  The V operand needs no
@@ -32,6 +34,9 @@ constexpr int DC_D = 128;
 constexpr int DC_PG = 16;
 constexpr int DC_WAVES = 4;
 constexpr int DC_BLK = DC_WAVES * kWave;
+constexpr int DC_PAGE_BYTES = 8192;       // K + V of one (page, kv head)
+typedef __attribute__((address_space(3))) void* lds_ptr;
+typedef __attribute__((address_space(3))) const uint8_t* lds_u8_ptr;
 constexpr int MAX_SPLIT = 512;
 
 __device__ __forceinline__ uint32_t bf16_word(const uint4& w, int e) {
@@ -89,7 +94,13 @@ __device__ void merge_row(const float* __restrict__ m_part, const float* __restr
 }
 
 // One workgroup = 4 waves per split; wave w takes pages j0+w, j0+w+4, ...
-// and the 4 wave states are merged in LDS into the split's partial.
+// Pages are DMA'd into per-wave LDS stages with global_load_lds_dwordx4 in
+// the exact lane order the MFMA operands need, so each lane later reads
+// back only the 16-byte slots it loaded itself (conflict-free, coalesced
+// 64/256-byte row segments in HBM) and in-flight pages cost no VGPRs; two
+// stages ping-pong so one page is always in flight while the other is
+// consumed.  The 4 wave states are then merged in LDS into the split's
+// partial.
 __global__ __launch_bounds__(DC_BLK) void decode_split_kernel(
     const uint16_t* __restrict__ q, long q_sr, long q_sh,
     const uint16_t* __restrict__ kc, long k_sb, long k_st, long k_sh,
@@ -113,33 +124,53 @@ __global__ __launch_bounds__(DC_BLK) void decode_split_kernel(
     const int c16 = lane & 15, kg = lane >> 4;
     const int seq_len = seq_lens[r];
 
-    __shared__ float red[DC_WAVES * 16 * DC_D];   // wave partials [wave][g][d]
+    // two page stages per wave (distinct arrays), later reused for the merge
+    __shared__ __attribute__((aligned(16))) uint8_t stA[DC_WAVES][DC_PAGE_BYTES];
+    __shared__ __attribute__((aligned(16))) uint8_t stB[DC_WAVES][DC_PAGE_BYTES];
     __shared__ float wm[DC_WAVES][16], wl[DC_WAVES][16];
 
-    // B operand of QK: q[g = c16][32*kg + 8*s + 0..7]
+    // B operand of QK, k-slot (kg, s) <-> d = 32*s + 8*kg + 0..7
     v8bf qb[4];
     {
-        const uint16_t* qp = q + (long)r * q_sr + (long)(kh * G + c16) * q_sh + 32 * kg;
+        const uint16_t* qp = q + (long)r * q_sr + (long)(kh * G + c16) * q_sh + 8 * kg;
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             uint4 w = make_uint4(0u, 0u, 0u, 0u);
-            if (c16 < G) w = *reinterpret_cast<const uint4*>(qp + 8 * s);
+            if (c16 < G) w = *reinterpret_cast<const uint4*>(qp + 32 * s);
             qb[s] = __builtin_bit_cast(v8bf, w);
         }
     }
 
     const int* prow = ptab + (long)r * pt_sr + (long)kh * pt_sh;
-    auto load_page = [&](int j, uint4 (&kr)[4], uint4 (&vr)[4]) -> int {
-        const int pt = prow[j];
-        const int ptc = min(max(pt, 0), bt_cols - 1);
-        int blk = bt[(long)r * bt_sr + ptc];
-        blk = min(max(blk, 0), NB - 1);
-        const uint16_t* kp = kc + (long)blk * k_sb + (long)kh * k_sh + (long)c16 * k_st + 32 * kg;
+    // DMA page j into stage `st`: K slot s (0..3) = K[t = lane&15][32 s + 8 kg ..],
+    // V slot v (0..3) = V[4 kg + v][8 (lane&15) ..]
+    // Page and block ids of up to 64 steps of this wave are fetched up front
+    // (lane i holds step i), so no dependent id load sits behind a stage's
+    // DMA in the in-order vmcnt queue.
+    int ptv = 0, blkv = 0;
+    auto fetch_ids = [&](int jb) {
+        const int jj = jb + DC_WAVES * lane;
+        ptv = 0;
+        blkv = 0;
+        if (jj < j1) {
+            ptv = prow[jj];
+            const int ptc = min(max(ptv, 0), bt_cols - 1);
+            blkv = min(max(bt[(long)r * bt_sr + ptc], 0), NB - 1);
+        }
+    };
+    // DMA step s of the current id batch into stage `st`:
+    // K slot i (0..3) = K[t = lane&15][32 i + 8 kg ..], V slot i = V[4 kg + i][8 (lane&15) ..]
+    auto issue = [&](int s, uint8_t* st) -> int {
+        const int pt = __builtin_amdgcn_readlane(ptv, s);
+        const int blk = __builtin_amdgcn_readlane(blkv, s);
+        const uint16_t* kp = kc + (long)blk * k_sb + (long)kh * k_sh + (long)c16 * k_st + 8 * kg;
         const uint16_t* vp = vc + (long)blk * v_sb + (long)kh * v_sh + 8 * c16;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) kr[i] = *reinterpret_cast<const uint4*>(kp + 8 * i);
+        for (int i = 0; i < 4; ++i)
+            __builtin_amdgcn_global_load_lds(kp + 32 * i, (lds_ptr)(st + i * 1024), 16, 0, 0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) vr[i] = *reinterpret_cast<const uint4*>(vp + (long)(4 * kg + i) * v_st);
+        for (int i = 0; i < 4; ++i)
+            __builtin_amdgcn_global_load_lds(vp + (long)(4 * kg + i) * v_st, (lds_ptr)(st + 4096 + i * 1024), 16, 0, 0);
         return pt;
     };
 
@@ -148,29 +179,38 @@ __global__ __launch_bounds__(DC_BLK) void decode_split_kernel(
 #pragma unroll
     for (int b = 0; b < 8; ++b) o[b] = v4f{0.f, 0.f, 0.f, 0.f};
 
-    uint4 kcur[4], vcur[4];
-    int j = j0 + wave;
-    int ptcur = 0;
-    if (j < j1) ptcur = load_page(j, kcur, vcur);
-    for (; j < j1; j += DC_WAVES) {
-        uint4 knx[4], vnx[4];
-        int ptnx = 0;
-        if (j + DC_WAVES < j1) ptnx = load_page(j + DC_WAVES, knx, vnx);
-
+    auto consume = [&](const uint8_t* st, int pt) {
+        // The stage is read with ds_read in inline asm: the compiler cannot
+        // tell these reads from the other stage's DMA still in flight and
+        // would otherwise wait for every outstanding load (vmcnt(0)) here.
+        // The caller has already waited for this stage's own DMA.
+        v4i kr[4], vr[4];
+        const uint32_t la = (uint32_t)(uintptr_t)(lds_u8_ptr)(st) + lane * 16;
+        asm volatile(
+            "ds_read_b128 %0, %8\n\t"
+            "ds_read_b128 %1, %8 offset:1024\n\t"
+            "ds_read_b128 %2, %8 offset:2048\n\t"
+            "ds_read_b128 %3, %8 offset:3072\n\t"
+            "ds_read_b128 %4, %8 offset:4096\n\t"
+            "ds_read_b128 %5, %8 offset:5120\n\t"
+            "ds_read_b128 %6, %8 offset:6144\n\t"
+            "ds_read_b128 %7, %8 offset:7168\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=v"(kr[0]), "=v"(kr[1]), "=v"(kr[2]), "=v"(kr[3]),
+              "=v"(vr[0]), "=v"(vr[1]), "=v"(vr[2]), "=v"(vr[3])
+            : "v"(la));
         // ---- S^T[t][g] = K[t] . q[g] ------------------------------------
         v4f s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, kcur[i]), qb[i], s, 0, 0, 0);
-        const int pos0 = ptcur * DC_PG + 4 * kg;
+            s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, kr[i]), qb[i], s, 0, 0, 0);
+        const int pos0 = pt * DC_PG + 4 * kg;
         float sv[4];
 #pragma unroll
         for (int v = 0; v < 4; ++v) sv[v] = (pos0 + v < seq_len) ? s[v] * sm_scale : -INFINITY;
-
         // ---- online softmax (head = lane column) ------------------------
         float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-        mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+        mx = xor32_max(xor16_max(mx));
         const float m_new = fmaxf(m, mx);
         const float m_ref = (m_new == -INFINITY) ? 0.f : m_new;   // fully masked so far
         const float alpha = __expf(m - m_ref);
@@ -180,27 +220,46 @@ __global__ __launch_bounds__(DC_BLK) void decode_split_kernel(
         lsum = lsum * alpha + (p[0] + p[1] + p[2] + p[3]);
         m = m_new;
         const v4h pb = {(_Float16)p[0], (_Float16)p[1], (_Float16)p[2], (_Float16)p[3]};
-
         // ---- O^T[d][g] += V^T P^T ---------------------------------------
 #pragma unroll
         for (int b = 0; b < 8; ++b) {
             v4h a;
 #pragma unroll
-            for (int v = 0; v < 4; ++v) a[v] = (_Float16)bf16_to_f32((uint16_t)bf16_word(vcur[v], b));
+            for (int v = 0; v < 4; ++v) a[v] = (_Float16)bf16_to_f32((uint16_t)bf16_word(__builtin_bit_cast(uint4, vr[v]), b));
             o[b] = o[b] * alpha;
             o[b] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, pb, o[b], 0, 0, 0);
         }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) { kcur[i] = knx[i]; vcur[i] = vnx[i]; }
-        ptcur = ptnx;
+    };
+
+    // ping-pong over the two stages: iteration s issues step s+1 into one
+    // stage and consumes step s from the other (one page always in flight)
+    for (int jb = j0 + wave; jb < j1; jb += DC_WAVES * kWave) {
+        fetch_ids(jb);
+        __builtin_amdgcn_s_waitcnt(0x0070);   // ids (and q) resident before any DMA
+        const int ns = min(kWave, cdiv(j1 - jb, DC_WAVES));   // steps of this batch
+        int pt_cur = 0;
+        for (int s = -1; s < ns; ++s) {
+            const bool nxt = s + 1 < ns;
+            int pt_nxt = 0;
+            if (nxt) pt_nxt = issue(s + 1, ((s + 1) & 1) ? stB[wave] : stA[wave]);
+            if (s >= 0) {
+                if (nxt) __builtin_amdgcn_s_waitcnt(0x0078);   // vmcnt(8): step s landed
+                else __builtin_amdgcn_s_waitcnt(0x0070);      // vmcnt(0)
+                __builtin_amdgcn_wave_barrier();
+                consume((s & 1) ? stB[wave] : stA[wave], pt_cur);
+                __builtin_amdgcn_wave_barrier();
+            }
+            pt_cur = pt_nxt;
+        }
     }
-    lsum += __shfl_xor(lsum, 16, kWave);
-    lsum += __shfl_xor(lsum, 32, kWave);
+    lsum = xor32_sum(xor16_sum(lsum));
 
     // ---- merge the 4 wave states of this split in LDS --------------------
+    __syncthreads();                              // every stage consumed
+    float* red = reinterpret_cast<float*>(&stA[0][0]);   // [wave][g][d], 32 KB
     if (kg == 0) { wm[wave][c16] = m; wl[wave][c16] = lsum; }
     {
-        float* ow = red + (wave * 16 + c16) * DC_D + 32 * kg;       // [wave][g][d]
+        float* ow = red + (wave * 16 + c16) * DC_D + 32 * kg;
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
             *reinterpret_cast<float4*>(ow + 8 * v) = make_float4(o[0][v], o[1][v], o[2][v], o[3][v]);

@@ -41,6 +41,14 @@ constexpr int SC_VROW = SC_RNK * SC_D / 2;   // 512 B of packed V per row
 constexpr int SC_MAX_CHUNK = 1024;          // pages per workgroup, upper bound
 constexpr int SC_MAXKV = 16;                // kv heads per request
 constexpr int SC_MAXHQ = 128;               // query heads per request (n_kv * G)
+// per-wave LDS staging of one (tile, kv head) unit, filled by LDS DMA
+constexpr int ST_V = 0;                     // 8 pages x 512 B packed V  (-> qt after use)
+constexpr int ST_C8 = 4096;                 // 8 pages x 128 B coefficients
+constexpr int ST_MU = 5120;                 // 8 pages x 128 B centroid  (-> mud after use)
+constexpr int ST_CS = 6144;                 // 8 pages x 32 B token scales
+constexpr int ST_VS = 6400;                 // 8 pages x 16 B column scales
+constexpr int ST_MUS = 6528;                // 8 dwords holding the centroid scales
+constexpr int ST_BYTES = 6560;
 
 __device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d) {
     return (uint32_t)(uint8_t)a | ((uint32_t)(uint8_t)b << 8) |
@@ -73,15 +81,26 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
         return;
     }
 
-    __shared__ __attribute__((aligned(16))) int8_t q8s[SC_MAXHQ + 16][SC_D];   // + zero rows
     __shared__ __attribute__((aligned(16))) float qsp[SC_MAXKV][16];
     __shared__ __attribute__((aligned(16))) int qbp[SC_MAXKV][16];
-    __shared__ __attribute__((aligned(16))) float qt_l[SC_WAVES][SC_TILE][SC_RNK][16];
-    __shared__ __attribute__((aligned(16))) float mud_l[SC_WAVES][SC_TILE][16];
+    __shared__ __attribute__((aligned(16))) uint8_t stage_l[SC_WAVES][ST_BYTES];
     __shared__ uint32_t wmax[SC_MAXKV][16];
-    __shared__ int bt_l[SC_MAX_CHUNK];
+    // dynamic LDS: int8 q rows of every head (+16 zero rows), chunk block ids
+    extern __shared__ __attribute__((aligned(16))) uint8_t dyn_l[];
+    int8_t (*q8s)[SC_D] = reinterpret_cast<int8_t (*)[SC_D]>(dyn_l);
+    int* bt_l = reinterpret_cast<int*>(dyn_l + (size_t)(HQ + 16) * SC_D);
 
-    // ---- stage: block ids of the chunk, int8 q of every head ------------
+    // ---- prologue: q rows and block ids are fetched together; the first
+    // unit's summary loads are issued before q is quantized, so the
+    // quantization overlaps them.
+    constexpr int QPW = SC_MAXHQ / SC_WAVES;                  // q rows per wave, max
+    uint32_t qw[QPW];
+#pragma unroll
+    for (int i = 0; i < QPW; ++i) {
+        const int hq = wave + SC_WAVES * i;
+        qw[i] = 0u;
+        if (hq < HQ) qw[i] = *reinterpret_cast<const uint32_t*>(q + (long)r * q_sr + (long)hq * q_sh + 2 * lane);
+    }
     for (int i = tid; i < c1 - c0; i += SC_BLOCK) {
         const int b = bt[(long)r * bt_sr + min(c0 + i, bt_cols - 1)];
         bt_l[i] = min(max(b, 0), NB - 1);
@@ -94,11 +113,73 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
     for (int i = tid; i < 16 * SC_D / 4; i += SC_BLOCK)
         reinterpret_cast<int*>(&q8s[HQ][0])[i] = 0;            // zero rows after the last head
     __syncthreads();
+
+    const int r16 = lane & 15, kg = lane >> 4;
+    const int jcol = lane & 15;
+    const int psub_l = jcol / GW;            // page slot of this lane's column
+    const int g_l = jcol % GW;               // head of this lane's column
+    const uint32_t MH = 0xF0F0F0F0u;
+    const int n_tiles = cdiv(c1 - c0, SC_TILE);
+    const int n_units = n_tiles * n_kv;      // (tile, kv head) units of the chunk
+
+    // Each (8-page tile, kv head) unit is fetched into VGPRs in natural
+    // (contiguous) lane order -- fully coalesced 16-byte loads -- one unit
+    // ahead of the one being scored, then written to this wave's LDS stage
+    // and read back in MFMA operand order.  Consecutive units are the kv
+    // heads of one tile, whose slab rows are adjacent.
+    uint4 fv0, fv1, fv2, fv3, fc8, fmu, fcs, fvs;
+    uint32_t fmus;
+    auto load_unit = [&](int u) {
+        const int t = u / n_kv, h = u - t * n_kv;
+        const int p0 = t * SC_TILE;
+        const int last = min(SC_TILE, c1 - c0 - p0) - 1;
+        const int* bl = bt_l + p0;
+        auto row_of = [&](int i) -> uint32_t { return (uint32_t)bl[min(i, last)] * (uint32_t)n_kv + (uint32_t)h; };
+        // 2 pages x 512 B of packed V per load
+        const uint32_t vo = (lane & 31) * 16;
+        fv0 = *reinterpret_cast<const uint4*>(v4 + (row_of(0 + (lane >> 5)) * SC_VROW + vo));
+        fv1 = *reinterpret_cast<const uint4*>(v4 + (row_of(2 + (lane >> 5)) * SC_VROW + vo));
+        fv2 = *reinterpret_cast<const uint4*>(v4 + (row_of(4 + (lane >> 5)) * SC_VROW + vo));
+        fv3 = *reinterpret_cast<const uint4*>(v4 + (row_of(6 + (lane >> 5)) * SC_VROW + vo));
+        {
+            const uint32_t row = row_of(lane >> 3);   // 8 pages x 128 B
+            fc8 = *reinterpret_cast<const uint4*>(c8 + (row * (SC_PG * SC_RNK) + (lane & 7) * 16));
+            fmu = *reinterpret_cast<const uint4*>(mu8 + (row * SC_D + (lane & 7) * 16));
+        }
+        if (lane < 16) {                              // 8 pages x 32 B token scales
+            const uint32_t row = row_of(lane >> 1);
+            fcs = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(cs) + (row * (SC_PG * 2) + (lane & 1) * 16));
+        }
+        if (lane < 8) {                               // 8 pages x 16 B column scales
+            const uint32_t row = row_of(lane);
+            fvs = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(vs) + row * (SC_RNK * 2));
+            // aligned dword holding this page's centroid scale
+            fmus = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint8_t*>(mus) + ((row * 2u) & ~3u));
+        }
+    };
+    auto store_unit = [&](uint8_t* stg) {
+        *reinterpret_cast<uint4*>(stg + ST_V + 0 * 1024 + lane * 16) = fv0;
+        *reinterpret_cast<uint4*>(stg + ST_V + 1 * 1024 + lane * 16) = fv1;
+        *reinterpret_cast<uint4*>(stg + ST_V + 2 * 1024 + lane * 16) = fv2;
+        *reinterpret_cast<uint4*>(stg + ST_V + 3 * 1024 + lane * 16) = fv3;
+        *reinterpret_cast<uint4*>(stg + ST_C8 + lane * 16) = fc8;
+        *reinterpret_cast<uint4*>(stg + ST_MU + lane * 16) = fmu;
+        if (lane < 16) *reinterpret_cast<uint4*>(stg + ST_CS + lane * 16) = fcs;
+        if (lane < 8) {
+            *reinterpret_cast<uint4*>(stg + ST_VS + lane * 16) = fvs;
+            *reinterpret_cast<uint32_t*>(stg + ST_MUS + lane * 4) = fmus;
+        }
+    };
+    __builtin_amdgcn_s_waitcnt(0x0070);      // q rows resident before the unit loads queue
+    if (wave < n_units) load_unit(wave);
+
+    // ---- quantize q (the first unit's loads are in flight) --------------
     const float s2 = sm_scale * 1.4426950408889634f;           // tokens in log2 units
-    for (int hq = wave; hq < HQ; hq += SC_WAVES) {
-        const uint32_t w = *reinterpret_cast<const uint32_t*>(
-            q + (long)r * q_sr + (long)hq * q_sh + 2 * lane);
-        const float a0 = bf16lo(w), a1 = bf16hi(w);
+#pragma unroll
+    for (int i = 0; i < QPW; ++i) {
+        const int hq = wave + SC_WAVES * i;
+        if (hq >= HQ) break;
+        const float a0 = bf16lo(qw[i]), a1 = bf16hi(qw[i]);
         const float am = wave_max(fmaxf(fabsf(a0), fabsf(a1)));
         const float qs = fmaxf(am, 1e-8f) / 127.f;
         const int i0 = (int)rintf(__fdiv_rn(a0, qs));
@@ -113,60 +194,10 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
     }
     __syncthreads();
 
-    const int r16 = lane & 15, kg = lane >> 4;
-    const int jcol = lane & 15;
-    const int psub_l = jcol / GW;            // page slot of this lane's column
-    const int g_l = jcol % GW;               // head of this lane's column
-    const uint32_t M4 = 0x0F0F0F0Fu;
-    const int n_tiles = cdiv(c1 - c0, SC_TILE);
-    const int n_units = n_tiles * n_kv;      // (tile, kv head) units of the chunk
-
-    // Everything one unit needs from HBM, in registers, so the next unit's
-    // loads are in flight while the current one computes.  Consecutive
-    // units are the kv heads of one tile, whose slab rows are adjacent.
-    struct Tile {
-        uint4 vv[4];          // packed V: 2 pages x 8 columns x 16 B per lane
-        float vsf[4];         // basis-column scale of this lane's (page, column)
-        v4i mu0, mu1;         // mu row of page (lane & 15) (< 8), 32 B per lane
-        float musf;
-        uint2 c8r[SC_TILE];   // coefficient row of token (lane & 15), all 8 pages
-        uint2 csv[NGRP];      // 4 token scales of this lane's (page, token quad)
-    };
-    auto load_unit = [&](int u, Tile& T) {
-        const int t = u / n_kv, h = u - t * n_kv;
-        const int p0 = t * SC_TILE;
-        const int last = min(SC_TILE, c1 - c0 - p0) - 1;
-        const int* bl = bt_l + p0;
-        auto row_of = [&](int i) -> uint32_t { return (uint32_t)bl[min(i, last)] * (uint32_t)n_kv + (uint32_t)h; };
-#pragma unroll
-        for (int pp = 0; pp < 4; ++pp) {
-            const uint32_t row = row_of(2 * pp + ((lane >> 3) & 1));
-            T.vv[pp] = *reinterpret_cast<const uint4*>(v4 + (row * SC_VROW + (lane & 7) * (SC_D / 2) + kg * 16));
-            T.vsf[pp] = bf16_to_f32(vs[row * SC_RNK + (lane & 7)]);
-        }
-        T.mu0 = v4i{0, 0, 0, 0};
-        T.mu1 = v4i{0, 0, 0, 0};
-        T.musf = 0.f;
-        if ((lane & 15) < 8) {
-            const uint32_t row = row_of(lane & 7);
-            const int8_t* mp = mu8 + (row * SC_D + kg * 32);
-            T.mu0 = *reinterpret_cast<const v4i*>(mp);
-            T.mu1 = *reinterpret_cast<const v4i*>(mp + 16);
-            T.musf = bf16_to_f32(mus[row]);
-        }
-#pragma unroll
-        for (int i = 0; i < SC_TILE; ++i)
-            T.c8r[i] = *reinterpret_cast<const uint2*>(c8 + (row_of(i) * (SC_PG * SC_RNK) + r16 * SC_RNK));
-#pragma unroll
-        for (int gi = 0; gi < NGRP; ++gi)
-            T.csv[gi] = *reinterpret_cast<const uint2*>(cs + (row_of(gi * PPM + psub_l) * SC_PG + 4 * kg));
-    };
-
-    Tile cur, nxt;
-    int u = wave;
-    if (u < n_units) load_unit(u, cur);
-    for (; u < n_units; u += SC_WAVES) {
-        if (u + SC_WAVES < n_units) load_unit(u + SC_WAVES, nxt);
+    uint8_t* stg = stage_l[wave];
+    for (int u = wave; u < n_units; u += SC_WAVES) {
+        store_unit(stg);
+        if (u + SC_WAVES < n_units) load_unit(u + SC_WAVES);   // next unit in flight
         const int t = u / n_kv, h = u - t * n_kv;
         const int p0 = c0 + t * SC_TILE;
         const int nvalid = min(SC_TILE, c1 - p0);
@@ -187,35 +218,60 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
         }
         const float4 qsl = *reinterpret_cast<const float4*>(&qsp[h][4 * kg]);
         const int4 qb = *reinterpret_cast<const int4*>(&qbp[h][4 * kg]);
+        wave_lds_sync();
 
         // ---- projection: qt (GQA group x 8 basis columns) per page -------
+        uint4 vv[4];
+        float vsf[4];
 #pragma unroll
         for (int pp = 0; pp < 4; ++pp) {
-            const uint32_t w0 = cur.vv[pp].x ^ 0x88888888u, w1 = cur.vv[pp].y ^ 0x88888888u;
-            const uint32_t w2 = cur.vv[pp].z ^ 0x88888888u, w3 = cur.vv[pp].w ^ 0x88888888u;
-            const v4i b0 = {(int)(w0 & M4), (int)(w1 & M4), (int)((w0 >> 4) & M4), (int)((w1 >> 4) & M4)};
-            const v4i b1 = {(int)(w2 & M4), (int)(w3 & M4), (int)((w2 >> 4) & M4), (int)((w3 >> 4) & M4)};
+            const int pg = (lane & 15) >> 3, c = lane & 7;
+            vv[pp] = *reinterpret_cast<const uint4*>(stg + ST_V + pp * 1024 + pg * 512 + c * 64 + kg * 16);
+            vsf[pp] = bf16_to_f32(*reinterpret_cast<const uint16_t*>(stg + ST_VS + (2 * pp + pg) * 16 + c * 2));
+        }
+        v4i mu0 = {0, 0, 0, 0}, mu1 = {0, 0, 0, 0};
+        float musf = 0.f;
+        if ((lane & 15) < 8) {
+            const int pg = lane & 15;
+            mu0 = *reinterpret_cast<const v4i*>(stg + ST_MU + pg * 128 + kg * 32);
+            mu1 = *reinterpret_cast<const v4i*>(stg + ST_MU + pg * 128 + kg * 32 + 16);
+            const uint32_t row = (uint32_t)bt_l[t * SC_TILE + min(pg, nvalid - 1)] * (uint32_t)n_kv + (uint32_t)h;
+            const uint32_t w = *reinterpret_cast<const uint32_t*>(stg + ST_MUS + pg * 4);
+            musf = (row & 1u) ? bf16hi(w) : bf16lo(w);
+        }
+        wave_lds_sync();                               // V / mu consumed: reuse as qt / mud
+        float* qt_w = reinterpret_cast<float*>(stg + ST_V);      // [page][c][16]
+        float* mud_w = reinterpret_cast<float*>(stg + ST_MU);    // [page][16]
+#pragma unroll
+        for (int pp = 0; pp < 4; ++pp) {
+            // signed nibbles moved to the high half of each byte: 16 * V as int8
+            const uint32_t w0 = vv[pp].x, w1 = vv[pp].y, w2 = vv[pp].z, w3 = vv[pp].w;
+            const v4i b0 = {(int)((w0 << 4) & MH), (int)((w1 << 4) & MH), (int)(w0 & MH), (int)(w1 & MH)};
+            const v4i b1 = {(int)((w2 << 4) & MH), (int)((w3 << 4) & MH), (int)(w2 & MH), (int)(w3 & MH)};
             v4i acc = {0, 0, 0, 0};
             acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(Av[0], b0, acc, 0, 0, 0);
             acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(Av[1], b1, acc, 0, 0, 0);
+            // acc = 16 * sum_d V q8 exactly (|acc| < 2^22): the 1/16 rides on
+            // the column scale, a power of two, so qt is unchanged bit for bit
+            const float vsc = vsf[pp] * 0.0625f;
             float4 qt;
-            qt.x = (float)(acc[0] - qb.x) * qsl.x * cur.vsf[pp];
-            qt.y = (float)(acc[1] - qb.y) * qsl.y * cur.vsf[pp];
-            qt.z = (float)(acc[2] - qb.z) * qsl.z * cur.vsf[pp];
-            qt.w = (float)(acc[3] - qb.w) * qsl.w * cur.vsf[pp];
-            *reinterpret_cast<float4*>(&qt_l[wave][2 * pp + ((lane & 15) >> 3)][lane & 7][4 * kg]) = qt;
+            qt.x = (float)acc[0] * qsl.x * vsc;
+            qt.y = (float)acc[1] * qsl.y * vsc;
+            qt.z = (float)acc[2] * qsl.z * vsc;
+            qt.w = (float)acc[3] * qsl.w * vsc;
+            *reinterpret_cast<float4*>(qt_w + ((2 * pp + ((lane & 15) >> 3)) * SC_RNK + (lane & 7)) * 16 + 4 * kg) = qt;
         }
         {
             v4i accm = {0, 0, 0, 0};
-            accm = __builtin_amdgcn_mfma_i32_16x16x64_i8(Amu[0], cur.mu0, accm, 0, 0, 0);
-            accm = __builtin_amdgcn_mfma_i32_16x16x64_i8(Amu[1], cur.mu1, accm, 0, 0, 0);
+            accm = __builtin_amdgcn_mfma_i32_16x16x64_i8(Amu[0], mu0, accm, 0, 0, 0);
+            accm = __builtin_amdgcn_mfma_i32_16x16x64_i8(Amu[1], mu1, accm, 0, 0, 0);
             if ((lane & 15) < 8) {
                 float4 md;
-                md.x = (float)accm[0] * qsl.x * cur.musf;
-                md.y = (float)accm[1] * qsl.y * cur.musf;
-                md.z = (float)accm[2] * qsl.z * cur.musf;
-                md.w = (float)accm[3] * qsl.w * cur.musf;
-                *reinterpret_cast<float4*>(&mud_l[wave][lane & 15][4 * kg]) = md;
+                md.x = (float)accm[0] * qsl.x * musf;
+                md.y = (float)accm[1] * qsl.y * musf;
+                md.z = (float)accm[2] * qsl.z * musf;
+                md.w = (float)accm[3] * qsl.w * musf;
+                *reinterpret_cast<float4*>(mud_w + (lane & 15) * 16 + 4 * kg) = md;
             }
         }
         wave_lds_sync();
@@ -226,29 +282,40 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
         for (int gi = 0; gi < NGRP; ++gi) {
             v4f acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int s = 0; s < 2 * PPM; ++s) {
-                const int psub = s >> 1;
-                const int page = gi * PPM + psub;
-                const int cc = kg + 4 * (s & 1);
-                const uint32_t word = (s & 1) ? cur.c8r[page].y : cur.c8r[page].x;
-                const float a = (float)(int8_t)(word >> (8 * kg));
-                const float b = (psub_l == psub) ? qt_l[wave][page][cc][g_l] : 0.f;
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc, 0, 0, 0);
+            for (int ps = 0; ps < PPM; ++ps) {
+                const int page = gi * PPM + ps;
+                const uint2 crow = *reinterpret_cast<const uint2*>(stg + ST_C8 + page * 128 + r16 * 8);
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const uint32_t word = hh ? crow.y : crow.x;
+                    const float a = (float)(int8_t)(word >> (8 * kg));
+                    const float b = (psub_l == ps) ? qt_w[(page * SC_RNK + kg + 4 * hh) * 16 + g_l] : 0.f;
+                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc, 0, 0, 0);
+                }
             }
             const int page = gi * PPM + psub_l;
-            const float mud = mud_l[wave][page][g_l];
-            const float t0 = fmaf(acc[0], bf16lo(cur.csv[gi].x), mud);
-            const float t1 = fmaf(acc[1], bf16hi(cur.csv[gi].x), mud);
-            const float t2 = fmaf(acc[2], bf16lo(cur.csv[gi].y), mud);
-            const float t3 = fmaf(acc[3], bf16hi(cur.csv[gi].y), mud);
-            float m = fmaxf(fmaxf(t0, t1), fmaxf(t2, t3));
-            m = fmaxf(m, __shfl_xor(m, 16, kWave));
-            m = fmaxf(m, __shfl_xor(m, 32, kWave));
-            float e = __builtin_amdgcn_exp2f(t0 - m) + __builtin_amdgcn_exp2f(t1 - m) +
-                      __builtin_amdgcn_exp2f(t2 - m) + __builtin_amdgcn_exp2f(t3 - m);
-            e += __shfl_xor(e, 16, kWave);
-            e += __shfl_xor(e, 32, kWave);
-            const float S = (m + __builtin_amdgcn_logf(e)) * 0.6931471805599453f;
+            const float mud = mud_w[page * 16 + g_l];
+            const uint2 csw = *reinterpret_cast<const uint2*>(stg + ST_CS + page * 32 + kg * 8);
+            // 16-token LSE taken relative to the centroid term: tok - mud =
+            // cs * acc.  The sum of exp2 is exact whenever it lies in
+            // [2^-60, 2^60] (no overflow; flushed terms < 2^-62 of the sum);
+            // otherwise the wave redoes the column with the exact max.
+            const float x0 = acc[0] * bf16lo(csw.x), x1 = acc[1] * bf16hi(csw.x);
+            const float x2 = acc[2] * bf16lo(csw.y), x3 = acc[3] * bf16hi(csw.y);
+            float e = __builtin_amdgcn_exp2f(x0) + __builtin_amdgcn_exp2f(x1) +
+                      __builtin_amdgcn_exp2f(x2) + __builtin_amdgcn_exp2f(x3);
+            e = xor32_sum(xor16_sum(e));
+            float S;
+            const bool ok = (e >= 0x1p-60f) && (e <= 0x1p60f);
+            if (__builtin_expect(__ballot(!ok) == 0ull, 1)) {
+                S = (mud + __builtin_amdgcn_logf(e)) * 0.6931471805599453f;
+            } else {
+                const float m = xor32_max(xor16_max(fmaxf(fmaxf(x0, x1), fmaxf(x2, x3))));
+                float f = __builtin_amdgcn_exp2f(x0 - m) + __builtin_amdgcn_exp2f(x1 - m) +
+                          __builtin_amdgcn_exp2f(x2 - m) + __builtin_amdgcn_exp2f(x3 - m);
+                f = xor32_sum(xor16_sum(f));
+                S = ((mud + m) + __builtin_amdgcn_logf(f)) * 0.6931471805599453f;
+            }
             if ((page < nvalid) && (g_l < G)) {
                 tmax = fmaxf(tmax, S);
                 if (lane < 16) score_h[(((long)r * n_kv + h) * G + g_l) * (long)MP + p0 + page] = S;
@@ -258,8 +325,7 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
 #pragma unroll
         for (int o = GW; o < 16; o <<= 1) tmax = fmaxf(tmax, __shfl_xor(tmax, o, kWave));
         if (lane < GW && lane < G) atomicMax(&wmax[h][lane], f2u(tmax));
-        wave_lds_sync();
-        cur = nxt;
+        wave_lds_sync();                               // staging reused by the next unit
     }
     __syncthreads();
     for (int i = tid; i < n_kv * 16; i += SC_BLOCK)
@@ -317,9 +383,10 @@ extern "C" int32_t locks_score_rki4(
     if (n_req == 0) return 0;
     const int Z = cdiv(max_pages, chunk);
     dim3 grid(Z, n_req);
+    const size_t dyn = (size_t)(n_kv * G + 16) * SC_D + (size_t)chunk * sizeof(int);
     hipStream_t st = (hipStream_t)stream;
 #define LAUNCH(GWV)                                                                    \
-    hipLaunchKernelGGL((rki4_score_kernel<GWV>), grid, dim3(SC_BLOCK), 0, st, q,        \
+    hipLaunchKernelGGL((rki4_score_kernel<GWV>), grid, dim3(SC_BLOCK), dyn, st, q, \
                        (long)q_stride_req, (long)q_stride_head, v4, vs, c8, cs, mu8, mus, \
                        num_blocks, block_table, (long)bt_stride, bt_cols, n_sel_hi,       \
                        score_h, max_pages, page_max, n_kv, G, sm_scale, chunk)
