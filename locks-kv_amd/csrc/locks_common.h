@@ -44,15 +44,14 @@ __device__ __forceinline__ float u2f(uint32_t x) {
     return __uint_as_float(x ^ mask);
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-    return v;
+// DPP row rotate (by N lanes inside each 16-lane row): a plain VALU move.
+template <int N>
+__device__ __forceinline__ int row_ror(int x) {
+    return __builtin_amdgcn_update_dpp(0, x, 0x120 + N, 0xF, 0xF, false);
 }
-__device__ __forceinline__ int wave_sum_i(int v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, kWave);
-    return v;
+template <int N>
+__device__ __forceinline__ float row_ror(float x) {
+    return __int_as_float(row_ror<N>(__float_as_int(x)));
 }
 
 // Pair reductions across lanes l and l^16 / l^32 with the gfx950 permlane
@@ -75,6 +74,26 @@ __device__ __forceinline__ float xor16_max(float x) {
 __device__ __forceinline__ float xor32_max(float x) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// Whole-wave max / integer sum, result in every lane: row rotations, then
+// the two pair swaps -- no LDS round trip.
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, row_ror<8>(v));
+    v = fmaxf(v, row_ror<4>(v));
+    v = fmaxf(v, row_ror<2>(v));
+    v = fmaxf(v, row_ror<1>(v));
+    return xor32_max(xor16_max(v));
+}
+__device__ __forceinline__ int wave_sum_i(int v) {
+    v += row_ror<8>(v);
+    v += row_ror<4>(v);
+    v += row_ror<2>(v);
+    v += row_ror<1>(v);
+    const auto a = __builtin_amdgcn_permlane16_swap((uint32_t)v, (uint32_t)v, false, false);
+    v = (int)a[0] + (int)a[1];
+    const auto b = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
+    return (int)b[0] + (int)b[1];
 }
 
 // Order LDS traffic between lanes of ONE wave (no cross-wave barrier).

@@ -82,7 +82,6 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
     }
 
     __shared__ __attribute__((aligned(16))) float qsp[SC_MAXKV][16];
-    __shared__ __attribute__((aligned(16))) int qbp[SC_MAXKV][16];
     __shared__ __attribute__((aligned(16))) uint8_t stage_l[SC_WAVES][ST_BYTES];
     __shared__ uint32_t wmax[SC_MAXKV][16];
     // dynamic LDS: int8 q rows of every head (+16 zero rows), chunk block ids
@@ -108,7 +107,6 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
     for (int i = tid; i < SC_MAXKV * 16; i += SC_BLOCK) {
         wmax[i / 16][i % 16] = 0x007FFFFFu;                    // f2u(-inf)
         qsp[i / 16][i % 16] = 0.f;
-        qbp[i / 16][i % 16] = 0;
     }
     for (int i = tid; i < 16 * SC_D / 4; i += SC_BLOCK)
         reinterpret_cast<int*>(&q8s[HQ][0])[i] = 0;            // zero rows after the last head
@@ -186,11 +184,7 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
         const int i1 = (int)rintf(__fdiv_rn(a1, qs));
         q8s[hq][2 * lane] = (int8_t)i0;
         q8s[hq][2 * lane + 1] = (int8_t)i1;
-        const int sum = wave_sum_i(i0 + i1);
-        if (lane == 0) {
-            qsp[hq / G][hq % G] = qs * s2;
-            qbp[hq / G][hq % G] = 8 * sum;
-        }
+        if (lane == 0) qsp[hq / G][hq % G] = qs * s2;
     }
     __syncthreads();
 
@@ -202,32 +196,46 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
         const int p0 = c0 + t * SC_TILE;
         const int nvalid = min(SC_TILE, c1 - p0);
 
-        // A operands of this kv head's GQA group (int8 q rows, zero padded)
-        v4i Av[2], Amu[2];
+        // int8 q rows of this kv head's GQA group as matrix-core operands:
+        // Bq = projection B (column j <-> head j % GW, replicated over the
+        // GW-wide page slots), Amu = centroid A (row <-> head, zero padded)
+        v4i Bq[2], Amu[2];
         {
-            const int row = (r16 < G) ? h * G + r16 : HQ;        // HQ.. = zero rows
-            const uint4 n0 = *reinterpret_cast<const uint4*>(&q8s[row][32 * kg]);
-            const uint4 n1 = *reinterpret_cast<const uint4*>(&q8s[row][32 * kg + 16]);
-            Amu[0] = v4i{(int)n0.x, (int)n0.y, (int)n0.z, (int)n0.w};
-            Amu[1] = v4i{(int)n1.x, (int)n1.y, (int)n1.z, (int)n1.w};
+            const int gq = r16 % GW;
+            const int rowq = (gq < G) ? h * G + gq : HQ;          // HQ.. = zero rows
+            const int rowm = (r16 < G) ? h * G + r16 : HQ;
+            const uint4 n0 = *reinterpret_cast<const uint4*>(&q8s[rowq][32 * kg]);
+            const uint4 n1 = *reinterpret_cast<const uint4*>(&q8s[rowq][32 * kg + 16]);
+            const uint4 m0 = *reinterpret_cast<const uint4*>(&q8s[rowm][32 * kg]);
+            const uint4 m1 = *reinterpret_cast<const uint4*>(&q8s[rowm][32 * kg + 16]);
+            Amu[0] = v4i{(int)m0.x, (int)m0.y, (int)m0.z, (int)m0.w};
+            Amu[1] = v4i{(int)m1.x, (int)m1.y, (int)m1.z, (int)m1.w};
             // V operand order inside a 16-d window: even d (low nibbles), then odd d
-            Av[0] = v4i{(int)__builtin_amdgcn_perm(n0.y, n0.x, 0x06040200u), (int)__builtin_amdgcn_perm(n0.w, n0.z, 0x06040200u),
+            Bq[0] = v4i{(int)__builtin_amdgcn_perm(n0.y, n0.x, 0x06040200u), (int)__builtin_amdgcn_perm(n0.w, n0.z, 0x06040200u),
                         (int)__builtin_amdgcn_perm(n0.y, n0.x, 0x07050301u), (int)__builtin_amdgcn_perm(n0.w, n0.z, 0x07050301u)};
-            Av[1] = v4i{(int)__builtin_amdgcn_perm(n1.y, n1.x, 0x06040200u), (int)__builtin_amdgcn_perm(n1.w, n1.z, 0x06040200u),
+            Bq[1] = v4i{(int)__builtin_amdgcn_perm(n1.y, n1.x, 0x06040200u), (int)__builtin_amdgcn_perm(n1.w, n1.z, 0x06040200u),
                         (int)__builtin_amdgcn_perm(n1.y, n1.x, 0x07050301u), (int)__builtin_amdgcn_perm(n1.w, n1.z, 0x07050301u)};
         }
-        const float4 qsl = *reinterpret_cast<const float4*>(&qsp[h][4 * kg]);
-        const int4 qb = *reinterpret_cast<const int4*>(&qbp[h][4 * kg]);
+        const float4 qsl = *reinterpret_cast<const float4*>(&qsp[h][4 * kg]);   // rows 4kg.. (mud)
+        const float qsj = qsp[h][r16 % GW];                                    // column head (qt)
         wave_lds_sync();
 
-        // ---- projection: qt (GQA group x 8 basis columns) per page -------
+        // ---- projection: qt (8 basis columns x GQA group) per page -------
+        // One MFMA pair per 2 pages: A = the 16 packed-V rows of the pair,
+        // ordered so that row 4a + b holds (page 2pp + (b & 1), column
+        // 2a + (b >> 1)); B = int8 q.  The result lands in lane (kg, j) as
+        // qt[pp][v] = qt[head j % GW][page 2pp + (v & 1)][column 2kg + (v >> 1)],
+        // which is exactly the B operand the token stage needs (its k-slot
+        // kg, step hh reads column 2kg + hh), so qt never goes through LDS.
+        const int i_pg = r16 & 1, i_c = 2 * (r16 >> 2) + ((r16 >> 1) & 1);
         uint4 vv[4];
-        float vsf[4];
+        uint32_t vsw[4][2];
 #pragma unroll
         for (int pp = 0; pp < 4; ++pp) {
-            const int pg = (lane & 15) >> 3, c = lane & 7;
-            vv[pp] = *reinterpret_cast<const uint4*>(stg + ST_V + pp * 1024 + pg * 512 + c * 64 + kg * 16);
-            vsf[pp] = bf16_to_f32(*reinterpret_cast<const uint16_t*>(stg + ST_VS + (2 * pp + pg) * 16 + c * 2));
+            vv[pp] = *reinterpret_cast<const uint4*>(stg + ST_V + pp * 1024 + i_pg * 512 + i_c * 64 + kg * 16);
+#pragma unroll
+            for (int pg = 0; pg < 2; ++pg)          // column scales (2kg, 2kg+1) of page 2pp+pg
+                vsw[pp][pg] = *reinterpret_cast<const uint32_t*>(stg + ST_VS + (2 * pp + pg) * 16 + kg * 4);
         }
         v4i mu0 = {0, 0, 0, 0}, mu1 = {0, 0, 0, 0};
         float musf = 0.f;
@@ -239,27 +247,26 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
             const uint32_t w = *reinterpret_cast<const uint32_t*>(stg + ST_MUS + pg * 4);
             musf = (row & 1u) ? bf16hi(w) : bf16lo(w);
         }
-        wave_lds_sync();                               // V / mu consumed: reuse as qt / mud
-        float* qt_w = reinterpret_cast<float*>(stg + ST_V);      // [page][c][16]
+        wave_lds_sync();                               // mu consumed: reuse as mud
         float* mud_w = reinterpret_cast<float*>(stg + ST_MU);    // [page][16]
+        float qt[4][4];
 #pragma unroll
         for (int pp = 0; pp < 4; ++pp) {
             // signed nibbles moved to the high half of each byte: 16 * V as int8
             const uint32_t w0 = vv[pp].x, w1 = vv[pp].y, w2 = vv[pp].z, w3 = vv[pp].w;
-            const v4i b0 = {(int)((w0 << 4) & MH), (int)((w1 << 4) & MH), (int)(w0 & MH), (int)(w1 & MH)};
-            const v4i b1 = {(int)((w2 << 4) & MH), (int)((w3 << 4) & MH), (int)(w2 & MH), (int)(w3 & MH)};
+            const v4i a0 = {(int)((w0 << 4) & MH), (int)((w1 << 4) & MH), (int)(w0 & MH), (int)(w1 & MH)};
+            const v4i a1 = {(int)((w2 << 4) & MH), (int)((w3 << 4) & MH), (int)(w2 & MH), (int)(w3 & MH)};
             v4i acc = {0, 0, 0, 0};
-            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(Av[0], b0, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(Av[1], b1, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, Bq[0], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, Bq[1], acc, 0, 0, 0);
             // acc = 16 * sum_d V q8 exactly (|acc| < 2^22): the 1/16 rides on
-            // the column scale, a power of two, so qt is unchanged bit for bit
-            const float vsc = vsf[pp] * 0.0625f;
-            float4 qt;
-            qt.x = (float)acc[0] * qsl.x * vsc;
-            qt.y = (float)acc[1] * qsl.y * vsc;
-            qt.z = (float)acc[2] * qsl.z * vsc;
-            qt.w = (float)acc[3] * qsl.w * vsc;
-            *reinterpret_cast<float4*>(qt_w + ((2 * pp + ((lane & 15) >> 3)) * SC_RNK + (lane & 7)) * 16 + 4 * kg) = qt;
+            // the column scale, a power of two, so qt is exact to the same bits
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const uint32_t w = vsw[pp][v & 1];
+                const float vsc = ((v >> 1) ? bf16hi(w) : bf16lo(w)) * 0.0625f;
+                qt[pp][v] = (float)acc[v] * qsj * vsc;
+            }
         }
         {
             v4i accm = {0, 0, 0, 0};
@@ -277,6 +284,7 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
         wave_lds_sync();
 
         // ---- token reconstruction + 16-token LSE per (page, head) --------
+        // k-slot kg, step hh <-> basis column 2kg + hh (both operands)
         float tmax = -INFINITY;
 #pragma unroll
         for (int gi = 0; gi < NGRP; ++gi) {
@@ -284,12 +292,11 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
 #pragma unroll
             for (int ps = 0; ps < PPM; ++ps) {
                 const int page = gi * PPM + ps;
-                const uint2 crow = *reinterpret_cast<const uint2*>(stg + ST_C8 + page * 128 + r16 * 8);
+                const uint32_t cw = *reinterpret_cast<const uint16_t*>(stg + ST_C8 + page * 128 + r16 * 8 + 2 * kg);
 #pragma unroll
                 for (int hh = 0; hh < 2; ++hh) {
-                    const uint32_t word = hh ? crow.y : crow.x;
-                    const float a = (float)(int8_t)(word >> (8 * kg));
-                    const float b = (psub_l == ps) ? qt_w[(page * SC_RNK + kg + 4 * hh) * 16 + g_l] : 0.f;
+                    const float a = (float)(int8_t)(cw >> (8 * hh));
+                    const float b = (psub_l == ps) ? qt[page >> 1][2 * hh + (page & 1)] : 0.f;
                     acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc, 0, 0, 0);
                 }
             }
@@ -323,7 +330,8 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
         }
         // this unit's per-head maxima -> LDS (ordered-uint atomic max)
 #pragma unroll
-        for (int o = GW; o < 16; o <<= 1) tmax = fmaxf(tmax, __shfl_xor(tmax, o, kWave));
+        for (int o = GW; o < 16; o <<= 1)    // max over the lanes of one head column
+            tmax = fmaxf(tmax, o == 4 ? row_ror<4>(tmax) : o == 8 ? row_ror<8>(tmax) : row_ror<2>(tmax));
         if (lane < GW && lane < G) atomicMax(&wmax[h][lane], f2u(tmax));
         wave_lds_sync();                               // staging reused by the next unit
     }
