@@ -285,9 +285,7 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
 
         // ---- token reconstruction + 16-token LSE per (page, head) --------
         // k-slot kg, step hh <-> basis column 2kg + hh (both operands)
-        float tmax = -INFINITY;
-#pragma unroll
-        for (int gi = 0; gi < NGRP; ++gi) {
+        auto tok_group = [&](int gi) -> v4f {        // cs * (C8 qt) of group gi, 4 tokens
             v4f acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ps = 0; ps < PPM; ++ps) {
@@ -300,32 +298,48 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
                     acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc, 0, 0, 0);
                 }
             }
-            const int page = gi * PPM + psub_l;
-            const float mud = mud_w[page * 16 + g_l];
-            const uint2 csw = *reinterpret_cast<const uint2*>(stg + ST_CS + page * 32 + kg * 8);
-            // 16-token LSE taken relative to the centroid term: tok - mud =
-            // cs * acc.  The sum of exp2 is exact whenever it lies in
-            // [2^-60, 2^60] (no overflow; flushed terms < 2^-62 of the sum);
-            // otherwise the wave redoes the column with the exact max.
-            const float x0 = acc[0] * bf16lo(csw.x), x1 = acc[1] * bf16hi(csw.x);
-            const float x2 = acc[2] * bf16lo(csw.y), x3 = acc[3] * bf16hi(csw.y);
-            float e = __builtin_amdgcn_exp2f(x0) + __builtin_amdgcn_exp2f(x1) +
-                      __builtin_amdgcn_exp2f(x2) + __builtin_amdgcn_exp2f(x3);
+            const uint2 csw = *reinterpret_cast<const uint2*>(stg + ST_CS + (gi * PPM + psub_l) * 32 + kg * 8);
+            return v4f{acc[0] * bf16lo(csw.x), acc[1] * bf16hi(csw.x), acc[2] * bf16lo(csw.y),
+                       acc[3] * bf16hi(csw.y)};
+        };
+        // 16-token LSE taken relative to the centroid term: tok - mud =
+        // cs * acc.  The exp2 sum is exact whenever it lies in [2^-60, 2^60]
+        // (no overflow; flushed terms < 2^-62 of the sum).  All groups are
+        // formed first (independent matrix-core chains interleave), then one
+        // wave-wide test picks this fast form or the exact-max recomputation.
+        float ev[NGRP], Sv[NGRP];
+        bool ok = true;
+#pragma unroll
+        for (int gi = 0; gi < NGRP; ++gi) {
+            const v4f x = tok_group(gi);
+            float e = __builtin_amdgcn_exp2f(x[0]) + __builtin_amdgcn_exp2f(x[1]) +
+                      __builtin_amdgcn_exp2f(x[2]) + __builtin_amdgcn_exp2f(x[3]);
             e = xor32_sum(xor16_sum(e));
-            float S;
-            const bool ok = (e >= 0x1p-60f) && (e <= 0x1p60f);
-            if (__builtin_expect(__ballot(!ok) == 0ull, 1)) {
-                S = (mud + __builtin_amdgcn_logf(e)) * 0.6931471805599453f;
-            } else {
-                const float m = xor32_max(xor16_max(fmaxf(fmaxf(x0, x1), fmaxf(x2, x3))));
-                float f = __builtin_amdgcn_exp2f(x0 - m) + __builtin_amdgcn_exp2f(x1 - m) +
-                          __builtin_amdgcn_exp2f(x2 - m) + __builtin_amdgcn_exp2f(x3 - m);
+            ev[gi] = e;
+            ok = ok && (e >= 0x1p-60f) && (e <= 0x1p60f);
+        }
+        if (__builtin_expect(__ballot(!ok) == 0ull, 1)) {
+#pragma unroll
+            for (int gi = 0; gi < NGRP; ++gi)
+                Sv[gi] = (mud_w[(gi * PPM + psub_l) * 16 + g_l] + __builtin_amdgcn_logf(ev[gi])) * 0.6931471805599453f;
+        } else {
+#pragma unroll
+            for (int gi = 0; gi < NGRP; ++gi) {
+                const v4f x = tok_group(gi);
+                const float m = xor32_max(xor16_max(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]))));
+                float f = __builtin_amdgcn_exp2f(x[0] - m) + __builtin_amdgcn_exp2f(x[1] - m) +
+                          __builtin_amdgcn_exp2f(x[2] - m) + __builtin_amdgcn_exp2f(x[3] - m);
                 f = xor32_sum(xor16_sum(f));
-                S = ((mud + m) + __builtin_amdgcn_logf(f)) * 0.6931471805599453f;
+                Sv[gi] = ((mud_w[(gi * PPM + psub_l) * 16 + g_l] + m) + __builtin_amdgcn_logf(f)) * 0.6931471805599453f;
             }
+        }
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int gi = 0; gi < NGRP; ++gi) {
+            const int page = gi * PPM + psub_l;
             if ((page < nvalid) && (g_l < G)) {
-                tmax = fmaxf(tmax, S);
-                if (lane < 16) score_h[(((long)r * n_kv + h) * G + g_l) * (long)MP + p0 + page] = S;
+                tmax = fmaxf(tmax, Sv[gi]);
+                if (lane < 16) score_h[(((long)r * n_kv + h) * G + g_l) * (long)MP + p0 + page] = Sv[gi];
             }
         }
         // this unit's per-head maxima -> LDS (ordered-uint atomic max)

@@ -232,6 +232,195 @@ __device__ void finish_row(long rk, int n_pages, int n_sel_hi, int n_sink, int b
 }
 
 // ---------------------------------------------------------------------------
+// whole-row kernel (max_pages <= ROW_MAXP): one 1024-thread workgroup per
+// (request, kv head) does combine, exact top-b and the page table in one
+// launch.  Thread t owns pages [E t, E t + E) (contiguous, so one packed
+// block scan orders the emission); the keys stay in registers; the radix
+// select runs 12 + 12 + 8-bit MSD passes over an LDS histogram.
+// ---------------------------------------------------------------------------
+constexpr int ROW_BLK = 1024;
+constexpr int ROW_NW = ROW_BLK / kWave;
+constexpr int ROW_MAXP = 16 * ROW_BLK;
+
+template <int E>
+__global__ __launch_bounds__(ROW_BLK) void sel_row_kernel(
+    const float* __restrict__ score_h, const float* __restrict__ pmax, int Zs,
+    const int* __restrict__ npg, const int* __restrict__ nsh, const int* __restrict__ bfix,
+    float* __restrict__ score, int* __restrict__ page_table, int* __restrict__ page_cnt,
+    int n_sink, int MP, int G, int combine)
+{
+    static_assert(E % 4 == 0, "pages per thread must be a multiple of 4");
+    const int kh = blockIdx.x, r = blockIdx.y, n_kv = gridDim.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const long rk = (long)r * n_kv + kh;
+    const int n_pages = max(min(npg[r], MP), 0);
+    const int n_sel_hi = min(nsh[r], MP);
+    const int n_sel = n_sel_hi - n_sink;
+    const bool keep_all = n_sel <= 1;
+    int b = bfix[r];
+    b = max(1, min(b, max(n_sel, 1)));
+    const int pend = max(n_sel_hi, 0);                    // score written for p < pend
+    const int p0 = tid * E;
+
+    __shared__ float hm[16];
+    __shared__ int hist[4096];
+    __shared__ int wtot[ROW_NW];
+    __shared__ int s3[4];
+    __shared__ int wsum[ROW_NW + 1];
+
+    // ---- score_h of the first 4 heads in flight before the head maxima --
+    const float* shb = score_h + rk * (long)G * MP;
+    float4 xv[4][E / 4];
+    auto load4 = [&](int g0) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int v = 0; v < E / 4; ++v) {
+                const int g = g0 + j, p = p0 + 4 * v;
+                xv[j][v] = (g < G && p < pend) ? *reinterpret_cast<const float4*>(shb + (long)g * MP + p)
+                                               : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+    };
+    load4(0);
+    if (combine == 0) {
+        if (wave < G) {
+            float m = -INFINITY;
+            for (int zz = lane; zz < Zs; zz += kWave) m = fmaxf(m, pmax[(rk * Zs + zz) * 16 + wave]);
+            m = wave_max(m);
+            if (lane == 0) hm[wave] = m;
+        }
+        __syncthreads();
+    }
+    float acc[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) acc[e] = (combine == 0) ? 0.f : -INFINITY;
+    for (int g0 = 0; g0 < G; g0 += 4) {
+        if (g0 > 0) load4(g0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int g = g0 + j;
+            if (g >= G) break;
+            const float h = (combine == 0) ? hm[g] : 0.f;
+#pragma unroll
+            for (int v = 0; v < E / 4; ++v) {
+                const float x4[4] = {xv[j][v].x, xv[j][v].y, xv[j][v].z, xv[j][v].w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    if (combine == 0) acc[4 * v + i] += __expf(x4[i] - h);
+                    else acc[4 * v + i] = (g == 0) ? x4[i] : fmaxf(acc[4 * v + i], x4[i]);
+                }
+            }
+        }
+    }
+    float* srow = score + rk * (long)MP;
+#pragma unroll
+    for (int e = 0; e < E; ++e)
+        if (p0 + e < pend) srow[p0 + e] = acc[e];
+
+    int* trow = page_table + rk * (long)MP;
+    if (keep_all || b >= n_sel) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const int i = p0 + e;
+            if (i < MP) trow[i] = (i < n_pages) ? i : -1;
+        }
+        if (tid == 0) page_cnt[rk] = n_pages;
+        return;
+    }
+
+    // ---- exact b-th largest key among the selectable pages [n_sink, nsh) --
+    uint32_t key[E];
+    bool val[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const int p = p0 + e;
+        val[e] = (p >= n_sink) && (p < n_sel_hi);
+        key[e] = f2u(acc[e]);
+    }
+    uint32_t prefix = 0u, kmask = 0u;
+    int k = b;
+    bool whole_bin = false;
+#pragma unroll 1
+    for (int pass = 0; pass < 3; ++pass) {
+        const int shift = pass == 0 ? 20 : pass == 1 ? 8 : 0;
+        const int nb = pass < 2 ? 4096 : 256;
+        for (int i = tid; i < nb; i += ROW_BLK) hist[i] = 0;
+        __syncthreads();
+#pragma unroll
+        for (int e = 0; e < E; ++e)
+            hist_add(hist, (int)((key[e] >> shift) & (uint32_t)(nb - 1)), val[e] && (key[e] & kmask) == prefix);
+        __syncthreads();
+        // wave w, lane l: bins top, top-1, top-2, top-3 with top = nb-1-256w-4l
+        // (ascending lane order = descending bin order)
+        const int top = nb - 1 - 256 * wave - 4 * lane;
+        int c = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) c += (top - j >= 0) ? hist[top - j] : 0;
+        int incl = c;
+#pragma unroll
+        for (int o = 1; o < kWave; o <<= 1) {
+            const int t = __shfl_up(incl, o, kWave);
+            if (lane >= o) incl += t;
+        }
+        if (lane == kWave - 1) wtot[wave] = incl;
+        __syncthreads();
+        int base = 0;
+        for (int w = 0; w < wave; ++w) base += wtot[w];
+        const int above0 = base + incl - c;
+        if (c > 0 && above0 < k && k <= base + incl) {
+            int above = above0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int cb = hist[top - j];
+                if (above + cb >= k) { s3[0] = top - j; s3[1] = k - above; s3[2] = cb; break; }
+                above += cb;
+            }
+        }
+        __syncthreads();
+        prefix |= ((uint32_t)s3[0]) << shift;
+        kmask |= ((uint32_t)(nb - 1)) << shift;
+        const int cb = s3[2];
+        k = s3[1];
+        if (k == cb) { whole_bin = true; break; }     // every key of the bin is kept
+    }
+
+    // ---- ordered emission: one packed (greater, equal) block scan --------
+    int gt = 0, eq = 0;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        if (!val[e]) continue;
+        if (whole_bin) gt += (key[e] & kmask) >= prefix;    // == prefix bin or above
+        else { gt += key[e] > prefix; eq += key[e] == prefix; }
+    }
+    int tot;
+    const int ex = block_excl_scan<ROW_BLK>(gt | (eq << 16), wsum, tot);
+    const int quota = whole_bin ? 0 : k;
+    int pos = (ex & 0xFFFF) + min(ex >> 16, quota);
+    int er = ex >> 16;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        if (!val[e]) continue;
+        bool kp;
+        if (whole_bin) kp = (key[e] & kmask) >= prefix;
+        else {
+            kp = key[e] > prefix;
+            if (key[e] == prefix) { kp = er < quota; ++er; }
+        }
+        if (kp) trow[n_sink + pos++] = p0 + e;
+    }
+    const int cnt = n_sink + b + (n_pages - n_sel_hi);
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const int i = p0 + e;
+        if (i >= MP) break;
+        if (i < n_sink) trow[i] = i;
+        else if (i >= n_sink + b && i < cnt) trow[i] = n_sel_hi + (i - n_sink - b);
+        else if (i >= cnt) trow[i] = -1;
+    }
+    if (tid == 0) page_cnt[rk] = cnt;
+}
+
+// ---------------------------------------------------------------------------
 // chunk kernel
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(SEL_BLK) void sel_chunk_kernel(
@@ -460,6 +649,17 @@ extern "C" int32_t locks_select_nrm_topb(
     uint32_t* spill_key = (uint32_t*)(ws + rows * Z1 * SEL_CH * 8);
     int* spill_page = (int*)(ws + rows * Z1 * SEL_CH * 8 + rows * (long)max_pages * 4);
     int* cand_cnt = (int*)(ws + rows * Z1 * SEL_CH * 8 + rows * (long)max_pages * 8);
+    if (max_pages <= ROW_MAXP && max_pages % 4 == 0 && max_pages > SEL_CH) {
+#define ROW_LAUNCH(EV)                                                                     \
+        hipLaunchKernelGGL((sel_row_kernel<EV>), dim3(n_kv, n_req), dim3(ROW_BLK), 0, st, score_h, \
+                           page_max, score_chunks, n_pages, n_sel_hi, b_fix, score, page_table, \
+                           page_cnt, n_sink, max_pages, G, combine)
+        if (max_pages <= 4 * ROW_BLK) ROW_LAUNCH(4);
+        else if (max_pages <= 8 * ROW_BLK) ROW_LAUNCH(8);
+        else ROW_LAUNCH(16);
+#undef ROW_LAUNCH
+        return check_launch("sel_row_kernel");
+    }
     hipLaunchKernelGGL(sel_chunk_kernel, dim3(Z1, n_kv, n_req), dim3(SEL_BLK), 0, st,
                        score_h, page_max, score_chunks, n_pages, n_sel_hi, b_fix, score,
                        page_table, page_cnt, cand_key, cand_page, cand_cnt, n_sink,

@@ -125,6 +125,9 @@ def _random_select_inputs(seed, n_kv, G, seq_lens, MP, st, ties=None):
 @pytest.mark.parametrize("combine", ["max", "nrm"])
 @pytest.mark.parametrize("seq_lens,n_kv,G,bp", [
     ([16384], 8, 4, 126),            # one chunk (fused finish)
+    ([131072], 8, 4, 126),           # Llama 128K: whole-row kernel, 8 pages/thread
+    ([200000], 2, 16, 126),          # whole-row kernel, 16 pages/thread, G=16
+    ([40000], 2, 4, 1000),           # whole-row kernel, 4 pages/thread, large b
     ([1 << 20], 2, 16, 126),         # 1M context, 32 chunks
     ([262144, 196608, 131072, 65536], 2, 16, 126),   # ragged batch
     ([100000], 2, 4, 5000),          # large b (spills past the LDS cap)
@@ -179,7 +182,7 @@ def test_select_matches_oracle(combine, seq_lens, n_kv, G, bp):
 
 
 @pytest.mark.parametrize("ties", ["all_equal", "bands", "underflow"])
-@pytest.mark.parametrize("ctx", [16384, 1 << 19])
+@pytest.mark.parametrize("ctx", [16384, 131072, 1 << 19])
 def test_select_tie_batteries(ties, ctx):
     import torch
     from locks.selection import derive_page_params, rki4_select_only
