@@ -187,6 +187,21 @@ def step_bytes(m):
                 score_per_launch=score)
 
 
+def scorer_traffic(workload):
+    """HBM bytes per scorer launch measured with rocprofv3 PMC (FETCH_SIZE,
+    WRITE_SIZE, KiB per dispatch) and scaled by the counters' reading of a
+    plain 1 GiB copy; the commands and raw counts are in profiles/."""
+    path = os.path.join(ROOT, "profiles", "rki4_score_traffic.json")
+    if not os.path.isfile(path):
+        return None
+    with open(path) as f:
+        t = json.load(f)
+    w = t.get(workload)
+    if not w:
+        return None
+    return int((w["fetch_kib"] * t["fetch_factor"] + w["write_kib"] * t["write_factor"]) * 1024)
+
+
 def scorer_roofline(m, reps=3):
     """Average scorer launch duration (HIP events on the launch stream) over
     every layer's slabs, cold across layers."""
@@ -348,7 +363,8 @@ def main():
                      "achieved": round(score_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(score_gbps / HBM_PEAK_GBPS, 4),
                      "avg_launch_us": round(score_us, 3),
-                     "bytes_per_launch": by["score_per_launch"], "traffic": None},
+                     "bytes_per_launch": by["score_per_launch"],
+                     "traffic": scorer_traffic(a.workload)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -177,6 +177,25 @@ __device__ int emit_topk(const uint32_t* keys, int n, int k, uint32_t tau, PageO
     return total;
 }
 
+// Max over the n per-chunk entries p[16 * z] held by this wave's lanes, 8
+// independent loads in flight per lane (a serial load chain costs one
+// memory latency per step).
+__device__ __forceinline__ float chunk_max(const float* __restrict__ p, int n) {
+    const int lane = threadIdx.x & 63;
+    float m = -INFINITY;
+    for (int z0 = lane; z0 < n; z0 += 8 * kWave) {
+        float t[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int z = z0 + j * kWave;
+            t[j] = (z < n) ? p[(long)z * 16] : -INFINITY;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) m = fmaxf(m, t[j]);
+    }
+    return m;
+}
+
 __device__ __forceinline__ void fill_all_pages(int* row, int n_pages, int MP, bool pad) {
     for (int i = threadIdx.x; i < MP; i += blockDim.x) {
         if (i < n_pages) row[i] = i;
@@ -268,24 +287,27 @@ __global__ __launch_bounds__(ROW_BLK) void sel_row_kernel(
     __shared__ int s3[4];
     __shared__ int wsum[ROW_NW + 1];
 
-    // ---- score_h of the first 4 heads in flight before the head maxima --
+    // ---- score_h of the first HB heads in flight before the head maxima.
+    // Loads are bounded by the row (MP), not by n_sel_hi, so they do not wait
+    // for the per-request parameters; pages >= n_sel_hi are ignored below.
+    constexpr int HB = (E <= 8) ? 8 : 4;                  // heads per load batch
     const float* shb = score_h + rk * (long)G * MP;
-    float4 xv[4][E / 4];
-    auto load4 = [&](int g0) {
+    float4 xv[HB][E / 4];
+    auto load_batch = [&](int g0) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < HB; ++j)
 #pragma unroll
             for (int v = 0; v < E / 4; ++v) {
                 const int g = g0 + j, p = p0 + 4 * v;
-                xv[j][v] = (g < G && p < pend) ? *reinterpret_cast<const float4*>(shb + (long)g * MP + p)
-                                               : make_float4(0.f, 0.f, 0.f, 0.f);
+                xv[j][v] = (g < G && p < MP) ? *reinterpret_cast<const float4*>(shb + (long)g * MP + p)
+                                             : make_float4(0.f, 0.f, 0.f, 0.f);
             }
     };
-    load4(0);
+    load_batch(0);
     if (combine == 0) {
         if (wave < G) {
             float m = -INFINITY;
-            for (int zz = lane; zz < Zs; zz += kWave) m = fmaxf(m, pmax[(rk * Zs + zz) * 16 + wave]);
+            m = chunk_max(pmax + rk * Zs * 16 + wave, Zs);
             m = wave_max(m);
             if (lane == 0) hm[wave] = m;
         }
@@ -294,10 +316,10 @@ __global__ __launch_bounds__(ROW_BLK) void sel_row_kernel(
     float acc[E];
 #pragma unroll
     for (int e = 0; e < E; ++e) acc[e] = (combine == 0) ? 0.f : -INFINITY;
-    for (int g0 = 0; g0 < G; g0 += 4) {
-        if (g0 > 0) load4(g0);
+    for (int g0 = 0; g0 < G; g0 += HB) {
+        if (g0 > 0) load_batch(g0);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < HB; ++j) {
             const int g = g0 + j;
             if (g >= G) break;
             const float h = (combine == 0) ? hm[g] : 0.f;
@@ -313,9 +335,15 @@ __global__ __launch_bounds__(ROW_BLK) void sel_row_kernel(
         }
     }
     float* srow = score + rk * (long)MP;
+    if (p0 + E <= pend) {
 #pragma unroll
-    for (int e = 0; e < E; ++e)
-        if (p0 + e < pend) srow[p0 + e] = acc[e];
+        for (int v = 0; v < E / 4; ++v)
+            *reinterpret_cast<float4*>(srow + p0 + 4 * v) = make_float4(acc[4 * v], acc[4 * v + 1], acc[4 * v + 2], acc[4 * v + 3]);
+    } else {
+#pragma unroll
+        for (int e = 0; e < E; ++e)
+            if (p0 + e < pend) srow[p0 + e] = acc[e];
+    }
 
     int* trow = page_table + rk * (long)MP;
     if (keep_all || b >= n_sel) {
@@ -409,13 +437,18 @@ __global__ __launch_bounds__(ROW_BLK) void sel_row_kernel(
         if (kp) trow[n_sink + pos++] = p0 + e;
     }
     const int cnt = n_sink + b + (n_pages - n_sel_hi);
+    if (p0 >= cnt && p0 + E <= MP) {                      // padding only
 #pragma unroll
-    for (int e = 0; e < E; ++e) {
-        const int i = p0 + e;
-        if (i >= MP) break;
-        if (i < n_sink) trow[i] = i;
-        else if (i >= n_sink + b && i < cnt) trow[i] = n_sel_hi + (i - n_sink - b);
-        else if (i >= cnt) trow[i] = -1;
+        for (int v = 0; v < E / 4; ++v) *reinterpret_cast<int4*>(trow + p0 + 4 * v) = make_int4(-1, -1, -1, -1);
+    } else {
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const int i = p0 + e;
+            if (i >= MP) break;
+            if (i < n_sink) trow[i] = i;
+            else if (i >= n_sink + b && i < cnt) trow[i] = n_sel_hi + (i - n_sink - b);
+            else if (i >= cnt) trow[i] = -1;
+        }
     }
     if (tid == 0) page_cnt[rk] = cnt;
 }
@@ -472,7 +505,7 @@ __global__ __launch_bounds__(SEL_BLK) void sel_chunk_kernel(
     if (combine == 0) {
         for (int g = wave; g < G; g += SEL_BLK / kWave) {
             float m = -INFINITY;
-            for (int zz = lane; zz < Zs; zz += kWave) m = fmaxf(m, pmax[(rk * Zs + zz) * 16 + g]);
+            m = chunk_max(pmax + rk * Zs * 16 + g, Zs);
             m = wave_max(m);
             if (lane == 0) hm[g] = m;
         }
