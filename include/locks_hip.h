@@ -15,7 +15,8 @@
  *     (-2); locks_last_error() then describes the failure (thread-local).
  *
  * Geometry contract of this build: head_dim 128, page 16, summary rank 8,
- * int4 basis, 1 <= G <= 16 query heads per kv head.  (The reference's rki4
+ * int4 basis, 1 <= G <= 16 query heads per kv head; MLA: kv_lora_rank 512 +
+ * 64 RoPE dims, <= 16 query heads.  (The reference's rki4
  * state asserts d in {64,128,256}, page in {16,32,64}, G <= 8:
  * src/locks/selection/rki4_state.py:288-334; G up to 16 is needed by the
  * GLM-4-9B 32q/2kv geometry.)
@@ -156,7 +157,8 @@ int32_t locks_decode_merge(const float* m_part, const float* l_part, const float
                            int32_t split, int32_t pps_min, void* stream);
 
 /*
- * rki4 summary build on the GPU for the listed physical blocks of ONE layer.
+ * rki4 summary build on the GPU for the listed physical blocks of ONE layer
+ * (head_dim 128: GQA K heads; head_dim 512: the MLA latent, n_kv 1).
  * Replaces the reference build chain _write_pre -> _eigh_chunked ->
  * _write_post (selection/rki4_build.py:147-158, :93-129, :178-225, the
  * `rki4_build_{tail,bulk,delta,refresh}` producers :264-364 call it):
@@ -186,6 +188,75 @@ int32_t locks_pack_rki4(const float* mu, const float* dc, const float* S2, const
                         const int32_t* rows, int32_t n, int32_t head_dim, int32_t page,
                         uint8_t* v4, uint16_t* vs, int8_t* c8, uint16_t* cs, int8_t* mu8,
                         uint16_t* mus, void* stream);
+
+
+/* ---------------------------------------------------------------------------
+ * MLA (one latent KV head shared by all query heads; DeepSeek-V2-Lite:
+ * kv_lora_rank 512 + 64 RoPE dims, 16 heads).  The cache is the engine's
+ * latent cache (num_blocks, page, 576) bf16.  Summaries are the rki4 record
+ * of the latent block built by locks_build_rki4 with head_dim 512, n_kv 1
+ * (v4 (NB,1,8,256), vs (NB,1,8), c8 (NB,1,16,8), cs (NB,1,16), mu8 (NB,1,512),
+ * mus (NB,1)); the RoPE keys are read from the cache.  Selection reuses
+ * locks_derive_params (budget_abs = budget_pages - sink - window) and
+ * locks_select_nrm_topb (n_kv 1, G 1, combine 1 = max), which together
+ * equal the reference's topb_middle (selection/mla_score_torch.py:51-73).
+ * ------------------------------------------------------------------------- */
+
+/*
+ * Latent page score.  Replaces mla_page_score_factored_batched /
+ * mla_page_score_ref (selection/mla_score_triton.py:97-151,
+ * selection/mla_score_torch.py:27-48):
+ *   score[r][p] = scale * max_{h < n_heads, t} (q_c8[h] . khat_t + q_rope[h] . k_rope_t)
+ * for pages p < n_sel_hi[r] (full pages; written there only), where q_c is
+ * int8-quantized per head and khat_t = mu + C_t V^T is the summary's
+ * reconstruction of token t.
+ *   q      (n_req, n_heads, 576) bf16, strides (q_stride_req, q_stride_head, 1)
+ *   score  (n_req, score_stride) f32
+ *   chunk  pages per workgroup (even, <= 1024; locks_mla_score_auto_chunk)
+ */
+int32_t locks_mla_score(const uint16_t* q, int64_t q_stride_req, int64_t q_stride_head,
+                        const uint8_t* v4, const uint16_t* vs, const int8_t* c8,
+                        const uint16_t* cs, const int8_t* mu8, const uint16_t* mus,
+                        const uint16_t* cache, int64_t c_stride_block, int64_t c_stride_tok,
+                        int32_t num_blocks, const int32_t* block_table, int64_t bt_stride,
+                        int32_t bt_cols, const int32_t* n_sel_hi, float* score,
+                        int64_t score_stride, int32_t max_pages, int32_t chunk, int32_t n_req,
+                        int32_t n_heads, int32_t kv_lora_rank, int32_t rope_dim, int32_t page,
+                        float scale, void* stream);
+int32_t locks_mla_score_auto_chunk(int32_t n_req, int32_t max_pages);
+
+/*
+ * Split-K sparse decode over the selected latent pages.  Replaces the
+ * gathered fp32 attention of LocksMLAImpl.forward_mqa
+ * (backend/mla_attn.py:178-201): per request, softmax over the tokens of the
+ * selected pages (position < seq_len) of q . [latent | rope] * scale;
+ * values = the latent.  bf16 products, fp32 softmax, fp16 P . V with fp32
+ * accumulation.
+ *   page_table (n_req, pt_stride) i32 ascending; page_cnt (n_req,) i32
+ *   m_part, l_part (n_req, split, 16) f32; acc_part (n_req, split, 16, 512) f32
+ */
+int32_t locks_mla_decode_splitk(const uint16_t* q, int64_t q_stride_req, int64_t q_stride_head,
+                                const uint16_t* cache, int64_t c_stride_block,
+                                int64_t c_stride_tok, int32_t num_blocks,
+                                const int32_t* block_table, int64_t bt_stride, int32_t bt_cols,
+                                const int32_t* page_table, int64_t pt_stride, int32_t pt_cols,
+                                const int32_t* page_cnt, const int32_t* seq_lens, float* m_part,
+                                float* l_part, float* acc_part, int32_t n_req, int32_t n_heads,
+                                int32_t kv_lora_rank, int32_t rope_dim, int32_t page,
+                                int32_t split, int32_t pps_min, float scale, void* stream);
+
+/*
+ * LSE merge of the MLA split partials (the attention/merge.py:105-152 rule)
+ * into o (n_req, n_heads, 512) bf16 (out_is_f32 = 0) or f32, and lse
+ * (n_req, lse_stride_req) f32 (may be NULL).  Rows with page_cnt 0 get 0
+ * and lse -inf.
+ */
+int32_t locks_mla_decode_merge(const float* m_part, const float* l_part, const float* acc_part,
+                               const int32_t* page_cnt, int32_t pt_cols, void* out,
+                               int64_t out_stride_req, int64_t out_stride_head,
+                               int32_t out_is_f32, float* lse, int64_t lse_stride_req,
+                               int32_t n_req, int32_t n_heads, int32_t kv_lora_rank,
+                               int32_t split, int32_t pps_min, void* stream);
 
 #ifdef __cplusplus
 }

@@ -27,15 +27,16 @@
 
 namespace locks {
 
-constexpr int BD_D = 128;
 constexpr int BD_PG = 16;
 constexpr int BD_RNK = 8;
-constexpr int BD_WAVES = 4;
 constexpr int BD_SWEEPS = 12;
+// waves per workgroup: the per-wave LDS image of a d = 512 page is ~37 KB
+template <int D> constexpr int bd_waves() { return D <= 128 ? 4 : 1; }
 
+template <int D>
 struct WaveLds {
-    float dc[BD_PG][BD_D + 1];   // centred page (padded rows)
-    float mu[BD_D];
+    float dc[BD_PG][D + 1];      // centred page (padded rows)
+    float mu[D];
     float A[BD_PG][BD_PG + 1];   // gram, rotated in place
     float U[BD_PG][BD_PG + 1];   // accumulated eigenvectors (columns)
     float cc[BD_PG], ss[BD_PG];
@@ -46,38 +47,48 @@ struct WaveLds {
 };
 
 // quantize + pack one page from mu (LDS), dc (LDS), U8 = U[:, col[r]],
-// S8 (LDS), writing the six slab rows.
-__device__ void pack_page(WaveLds& L, long row, uint8_t* __restrict__ v4, uint16_t* __restrict__ vs,
+// S8 (LDS), writing the six slab rows.  Lane l owns the packed bytes
+// j = l + 64 k (d = 2j, 2j + 1).
+template <int D>
+__device__ void pack_page(WaveLds<D>& L, long row, uint8_t* __restrict__ v4, uint16_t* __restrict__ vs,
                           int8_t* __restrict__ c8, uint16_t* __restrict__ cs,
                           int8_t* __restrict__ mu8, uint16_t* __restrict__ mus) {
+    constexpr int NK = D / 128;
     const int lane = threadIdx.x & 63;
-    // V[d][r] for d = 2*lane, 2*lane+1: sequential over t, separately rounded
-    float V[2][BD_RNK];
+    // V[d][r]: sequential over t, separately rounded
+    float V[NK][2][BD_RNK];
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
-        const int d = 2 * lane + e;
+    for (int k = 0; k < NK; ++k)
 #pragma unroll
-        for (int r = 0; r < BD_RNK; ++r) {
-            float acc = 0.f;
-            const int c = L.col[r];
-            for (int t = 0; t < BD_PG; ++t) acc = __fadd_rn(acc, __fmul_rn(L.dc[t][d], L.U[t][c]));
-            V[e][r] = __fdiv_rn(acc, L.S8[r]);
+        for (int e = 0; e < 2; ++e) {
+            const int d = 2 * (lane + 64 * k) + e;
+#pragma unroll
+            for (int r = 0; r < BD_RNK; ++r) {
+                float acc = 0.f;
+                const int c = L.col[r];
+                for (int t = 0; t < BD_PG; ++t) acc = __fadd_rn(acc, __fmul_rn(L.dc[t][d], L.U[t][c]));
+                V[k][e][r] = __fdiv_rn(acc, L.S8[r]);
+            }
         }
-    }
     // per-column absmax over d
     float vsc[BD_RNK];
 #pragma unroll
     for (int r = 0; r < BD_RNK; ++r) {
-        const float am = wave_max(fmaxf(fabsf(V[0][r]), fabsf(V[1][r])));
+        float am = 0.f;
+#pragma unroll
+        for (int k = 0; k < NK; ++k) am = fmaxf(am, fmaxf(fabsf(V[k][0][r]), fabsf(V[k][1][r])));
+        am = wave_max(am);
         vsc[r] = fmaxf(__fdiv_rn(am, 7.f), 1e-8f);
     }
-    uint8_t* vrow = v4 + row * (BD_RNK * BD_D / 2);
+    uint8_t* vrow = v4 + row * (BD_RNK * D / 2);
 #pragma unroll
-    for (int r = 0; r < BD_RNK; ++r) {
-        const int lo = (int)fminf(fmaxf(rintf(__fdiv_rn(V[0][r], vsc[r])), -8.f), 7.f);
-        const int hi = (int)fminf(fmaxf(rintf(__fdiv_rn(V[1][r], vsc[r])), -8.f), 7.f);
-        vrow[r * (BD_D / 2) + lane] = (uint8_t)((lo & 15) | ((hi & 15) << 4));
-    }
+    for (int r = 0; r < BD_RNK; ++r)
+#pragma unroll
+        for (int k = 0; k < NK; ++k) {
+            const int lo = (int)fminf(fmaxf(rintf(__fdiv_rn(V[k][0][r], vsc[r])), -8.f), 7.f);
+            const int hi = (int)fminf(fmaxf(rintf(__fdiv_rn(V[k][1][r], vsc[r])), -8.f), 7.f);
+            vrow[r * (D / 2) + lane + 64 * k] = (uint8_t)((lo & 15) | ((hi & 15) << 4));
+        }
     if (lane < BD_RNK) vs[row * BD_RNK + lane] = f32_to_bf16(vsc[lane]);
     // coefficients: lane t < 16 owns token t
     if (lane < BD_PG) {
@@ -97,16 +108,25 @@ __device__ void pack_page(WaveLds& L, long row, uint8_t* __restrict__ v4, uint16
         cs[row * BD_PG + t] = f32_to_bf16(csc);
     }
     // centroid
-    const float m0 = L.mu[2 * lane], m1 = L.mu[2 * lane + 1];
-    const float am = wave_max(fmaxf(fabsf(m0), fabsf(m1)));
+    float am = 0.f;
+#pragma unroll
+    for (int k = 0; k < NK; ++k)
+        am = fmaxf(am, fmaxf(fabsf(L.mu[2 * (lane + 64 * k)]), fabsf(L.mu[2 * (lane + 64 * k) + 1])));
+    am = wave_max(am);
     const float msc = fmaxf(__fdiv_rn(am, 127.f), 1e-8f);
-    mu8[row * BD_D + 2 * lane] = (int8_t)fminf(fmaxf(rintf(__fdiv_rn(m0, msc)), -127.f), 127.f);
-    mu8[row * BD_D + 2 * lane + 1] = (int8_t)fminf(fmaxf(rintf(__fdiv_rn(m1, msc)), -127.f), 127.f);
+#pragma unroll
+    for (int k = 0; k < NK; ++k)
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int d = 2 * (lane + 64 * k) + e;
+            mu8[row * D + d] = (int8_t)fminf(fmaxf(rintf(__fdiv_rn(L.mu[d], msc)), -127.f), 127.f);
+        }
     if (lane == 0) mus[row] = f32_to_bf16(msc);
 }
 
 // Parallel cyclic Jacobi on L.A (16x16 symmetric); eigenvectors -> L.U columns.
-__device__ void jacobi16(WaveLds& L) {
+template <class W>
+__device__ void jacobi16(W& L) {
     const int lane = threadIdx.x & 63;
     for (int i = lane; i < BD_PG * BD_PG; i += kWave) L.U[i / BD_PG][i % BD_PG] = (i / BD_PG == i % BD_PG) ? 1.f : 0.f;
     wave_lds_sync();
@@ -176,7 +196,8 @@ __device__ void jacobi16(WaveLds& L) {
 }
 
 // eigenvalues on the diagonal of L.A -> ascending ranks -> top-8 columns
-__device__ void select_top8(WaveLds& L) {
+template <class W>
+__device__ void select_top8(W& L) {
     const int lane = threadIdx.x & 63;
     if (lane < BD_PG) {
         const float li = L.A[lane][lane];
@@ -194,17 +215,19 @@ __device__ void select_top8(WaveLds& L) {
     wave_lds_sync();
 }
 
-__global__ __launch_bounds__(BD_WAVES * kWave) void rki4_build_kernel(
+template <int D>
+__global__ __launch_bounds__(bd_waves<D>() * kWave) void rki4_build_kernel(
     const uint16_t* __restrict__ kc, long k_sb, long k_st, long k_sh, int NB,
     const int* __restrict__ blocks, int n_blocks, int n_kv,
     uint8_t* __restrict__ v4, uint16_t* __restrict__ vs, int8_t* __restrict__ c8,
     uint16_t* __restrict__ cs, int8_t* __restrict__ mu8, uint16_t* __restrict__ mus,
     uint16_t* __restrict__ tag)
 {
-    __shared__ WaveLds lds[BD_WAVES];
+    constexpr int NW = bd_waves<D>();
+    __shared__ WaveLds<D> lds[NW];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    WaveLds& L = lds[wave];
-    const long item = (long)blockIdx.x * BD_WAVES + wave;      // (block index, kv head)
+    WaveLds<D>& L = lds[wave];
+    const long item = (long)blockIdx.x * NW + wave;      // (block index, kv head)
     if (item >= (long)n_blocks * n_kv) return;
     const int bi = (int)(item / n_kv), kh = (int)(item % n_kv);
     const int blk = blocks[bi];
@@ -213,8 +236,8 @@ __global__ __launch_bounds__(BD_WAVES * kWave) void rki4_build_kernel(
     const uint16_t* kp = kc + (long)blk * k_sb + (long)kh * k_sh;
 
     // stage K (fp32) and the centroid (sequential sum over t, then / 16)
-    for (int i = lane; i < BD_PG * BD_D / 8; i += kWave) {
-        const int t = i / (BD_D / 8), d0 = (i % (BD_D / 8)) * 8;
+    for (int i = lane; i < BD_PG * D / 8; i += kWave) {
+        const int t = i / (D / 8), d0 = (i % (D / 8)) * 8;
         const uint4 w = *reinterpret_cast<const uint4*>(kp + (long)t * k_st + d0);
         const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
@@ -225,9 +248,7 @@ __global__ __launch_bounds__(BD_WAVES * kWave) void rki4_build_kernel(
     }
     if (lane < 8) tag[row * 8 + lane] = kp[(long)(BD_PG - 1) * k_st + lane];
     wave_lds_sync();
-#pragma unroll
-    for (int e = 0; e < 2; ++e) {
-        const int d = 2 * lane + e;
+    for (int d = lane; d < D; d += kWave) {
         float acc = 0.f;
         for (int t = 0; t < BD_PG; ++t) acc = __fadd_rn(acc, L.dc[t][d]);
         const float m = __fdiv_rn(acc, (float)BD_PG);
@@ -240,7 +261,7 @@ __global__ __launch_bounds__(BD_WAVES * kWave) void rki4_build_kernel(
     {
         const int i = lane & 15, kq = lane >> 4;
         v4f g = {0.f, 0.f, 0.f, 0.f};
-        for (int s = 0; s < BD_D / 4; ++s) {
+        for (int s = 0; s < D / 4; ++s) {
             const float a = L.dc[i][4 * s + kq];
             g = __builtin_amdgcn_mfma_f32_16x16x4f32(a, a, g, 0, 0, 0);
         }
@@ -250,20 +271,21 @@ __global__ __launch_bounds__(BD_WAVES * kWave) void rki4_build_kernel(
     wave_lds_sync();
     jacobi16(L);
     select_top8(L);
-    pack_page(L, row, v4, vs, c8, cs, mu8, mus);
+    pack_page<D>(L, row, v4, vs, c8, cs, mu8, mus);
 }
 
 // locks_pack_rki4: quantize + pack given the caller's eigen decomposition.
-__global__ __launch_bounds__(BD_WAVES * kWave) void rki4_pack_kernel(
+__global__ __launch_bounds__(4 * kWave) void rki4_pack_kernel(
     const float* __restrict__ mu, const float* __restrict__ dc, const float* __restrict__ S2,
     const float* __restrict__ U, const int* __restrict__ rows, int n,
     uint8_t* __restrict__ v4, uint16_t* __restrict__ vs, int8_t* __restrict__ c8,
     uint16_t* __restrict__ cs, int8_t* __restrict__ mu8, uint16_t* __restrict__ mus)
 {
-    __shared__ WaveLds lds[BD_WAVES];
+    constexpr int BD_D = 128;
+    __shared__ WaveLds<BD_D> lds[4];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    WaveLds& L = lds[wave];
-    const long item = (long)blockIdx.x * BD_WAVES + wave;
+    WaveLds<BD_D>& L = lds[wave];
+    const long item = (long)blockIdx.x * 4 + wave;
     if (item >= n) return;
     for (int i = lane; i < BD_PG * BD_D; i += kWave) L.dc[i / BD_D][i % BD_D] = dc[item * BD_PG * BD_D + i];
     for (int i = lane; i < BD_D; i += kWave) L.mu[i] = mu[item * BD_D + i];
@@ -274,7 +296,7 @@ __global__ __launch_bounds__(BD_WAVES * kWave) void rki4_pack_kernel(
         L.S8[lane] = __fsqrt_rn(fmaxf(S2[item * BD_PG + c], 1e-10f));
     }
     wave_lds_sync();
-    pack_page(L, rows[item], v4, vs, c8, cs, mu8, mus);
+    pack_page<BD_D>(L, rows[item], v4, vs, c8, cs, mu8, mus);
 }
 
 }  // namespace locks
@@ -287,8 +309,9 @@ extern "C" int32_t locks_build_rki4(
     int32_t page, uint8_t* v4, uint16_t* vs, int8_t* c8, uint16_t* cs, int8_t* mu8,
     uint16_t* mus, uint16_t* tag, void* stream)
 {
-    LOCKS_REQUIRE(head_dim == BD_D && page == BD_PG,
-                  "locks_build_rki4: geometry d=%d page=%d unsupported (this build: 128/16)", head_dim, page);
+    LOCKS_REQUIRE((head_dim == 128 || head_dim == 512) && page == BD_PG,
+                  "locks_build_rki4: geometry d=%d page=%d unsupported (this build: d 128 or 512, page 16)",
+                  head_dim, page);
     LOCKS_REQUIRE(n_kv >= 1 && num_blocks >= 1 && n_blocks >= 0, "locks_build_rki4: bad geometry");
     LOCKS_REQUIRE(k_stride_tok % 8 == 0 && k_stride_block % 8 == 0 && k_stride_head % 8 == 0,
                   "locks_build_rki4: K strides must be multiples of 8 elements");
@@ -296,12 +319,17 @@ extern "C" int32_t locks_build_rki4(
                   "locks_build_rki4: null pointer argument");
     if (n_blocks == 0) return 0;
     const long items = (long)n_blocks * n_kv;
-    const long grid = (items + BD_WAVES - 1) / BD_WAVES;
+    const int nw = head_dim == 128 ? bd_waves<128>() : bd_waves<512>();
+    const long grid = (items + nw - 1) / nw;
     LOCKS_REQUIRE(grid < (1L << 31), "locks_build_rki4: too many pages in one call");
-    hipLaunchKernelGGL(rki4_build_kernel, dim3((unsigned)grid), dim3(BD_WAVES * kWave), 0,
-                       (hipStream_t)stream, k_cache, (long)k_stride_block, (long)k_stride_tok,
-                       (long)k_stride_head, num_blocks, blocks, n_blocks, n_kv, v4, vs, c8, cs,
-                       mu8, mus, tag);
+#define BUILD_LAUNCH(DV)                                                                     \
+    hipLaunchKernelGGL((rki4_build_kernel<DV>), dim3((unsigned)grid), dim3(nw * kWave), 0,  \
+                       (hipStream_t)stream, k_cache, (long)k_stride_block, (long)k_stride_tok, \
+                       (long)k_stride_head, num_blocks, blocks, n_blocks, n_kv, v4, vs, c8, cs, \
+                       mu8, mus, tag)
+    if (head_dim == 128) BUILD_LAUNCH(128);
+    else BUILD_LAUNCH(512);
+#undef BUILD_LAUNCH
     return check_launch("rki4_build_kernel");
 }
 
@@ -311,13 +339,13 @@ extern "C" int32_t locks_pack_rki4(const float* mu, const float* dc, const float
                                    int8_t* c8, uint16_t* cs, int8_t* mu8, uint16_t* mus,
                                    void* stream)
 {
-    LOCKS_REQUIRE(head_dim == BD_D && page == BD_PG,
+    LOCKS_REQUIRE(head_dim == 128 && page == BD_PG,
                   "locks_pack_rki4: geometry d=%d page=%d unsupported (this build: 128/16)", head_dim, page);
     LOCKS_REQUIRE(n >= 0, "locks_pack_rki4: n=%d < 0", n);
     LOCKS_REQUIRE(mu && dc && S2 && U && rows && v4 && vs && c8 && cs && mu8 && mus,
                   "locks_pack_rki4: null pointer argument");
     if (n == 0) return 0;
-    hipLaunchKernelGGL(rki4_pack_kernel, dim3((n + BD_WAVES - 1) / BD_WAVES), dim3(BD_WAVES * kWave),
+    hipLaunchKernelGGL(rki4_pack_kernel, dim3((n + 3) / 4), dim3(4 * kWave),
                        0, (hipStream_t)stream, mu, dc, S2, U, rows, n, v4, vs, c8, cs, mu8, mus);
     return check_launch("rki4_pack_kernel");
 }

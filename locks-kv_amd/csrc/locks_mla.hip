@@ -1,0 +1,601 @@
+// LOCKS on MLA (one latent KV head shared by all query heads) for gfx950:
+// latent page scorer, split-K sparse decode over the selected pages, merge.
+//
+// Semantics (reference, paths under src/locks/):
+//   page score  selection/mla_score_torch.py:27-48 -- max over heads and
+//               valid tokens of (q_c . khat_t + q_rope . k_rope_t) * scale;
+//               khat is the page summary's reconstruction of the latent.
+//   selection   selection/mla_score_torch.py:51-73 (sink + recent window
+//               forced inside the budget, top-scored middle) -- served by
+//               locks_select_nrm_topb with G = 1, "max" combine.
+//   attention   backend/mla_attn.py:178-201 -- softmax over the selected
+//               tokens of q . [latent | rope] * scale, o = P . latent, lse.
+//
+// The page summary is the rki4 record of the latent block (d = kv_lora_rank
+// = 512: mean + rank-8 int4 basis + int8 coefficients, built by
+// locks_build_rki4) -- the reference keeps fp32 factors Lf, Rf instead
+// (mla_select.py:69-108), larger than the page itself; the RoPE keys are
+// read exact (bf16) straight from the cache.  Per (page): 2738 B of summary
+// + 2048 B of RoPE keys.
+//
+//   tok[h][t] = cs_t sum_c c8[t][c] qt[h][c] + mud[h] + q_rope[h] . k_rope[t]
+//   qt[h][c]  = (sum_d V4[c][d] q8[h][d]) qs[h] vs[c]
+//   mud[h]    = (sum_d mu8[d] q8[h][d]) qs[h] mus
+//   score[p]  = scale * max_{h < H, t} tok[h][t]
+#include "locks_common.h"
+#include "locks_hip.h"
+
+namespace locks {
+
+constexpr int ML_D = 512;                    // kv_lora_rank
+constexpr int ML_DR = 64;                    // RoPE dims
+constexpr int ML_HS = ML_D + ML_DR;          // cache row (576)
+constexpr int ML_PG = 16;
+constexpr int ML_RNK = 8;
+constexpr int ML_H = 16;                     // query heads (upper bound)
+constexpr int ML_WAVES = 4;
+constexpr int ML_BLK = ML_WAVES * kWave;
+constexpr int ML_VROW = ML_RNK * ML_D / 2;   // 2048 B packed V per page
+constexpr int ML_MAX_CHUNK = 1024;
+// per-wave LDS stage of one unit (2 pages)
+constexpr int MS_V = 0;                      // 2 x 2048 packed V
+constexpr int MS_MU = 4096;                  // 2 x 512 centroid
+constexpr int MS_C8 = 5120;                  // 2 x 128 coefficients
+constexpr int MS_CS = 5376;                  // 2 x 32 token scales
+constexpr int MS_VS = 5440;                  // 2 x 16 column scales
+constexpr int MS_MUS = 5472;                 // 2 dwords: centroid scales (bf16 in the low half)
+constexpr int MS_RP = 5504;                  // 2 x 16 x 128 B RoPE keys
+constexpr int MS_MD = 9600;                  // 2 x 16 fp32 centroid terms
+constexpr int MS_BYTES = 9728;
+
+__device__ __forceinline__ v4i perm_even_odd(const uint4 n) {
+    // 16 int8 in d order -> even d of the window first, then odd d (the
+    // order the int4 nibble operand of the projection uses)
+    return v4i{(int)__builtin_amdgcn_perm(n.y, n.x, 0x06040200u), (int)__builtin_amdgcn_perm(n.w, n.z, 0x06040200u),
+               (int)__builtin_amdgcn_perm(n.y, n.x, 0x07050301u), (int)__builtin_amdgcn_perm(n.w, n.z, 0x07050301u)};
+}
+
+// ---------------------------------------------------------------------------
+// latent page scorer: grid (chunks, requests), 4 waves; unit = 2 pages
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(ML_BLK) void mla_score_kernel(
+    const uint16_t* __restrict__ q, long q_sr, long q_sh,
+    const uint8_t* __restrict__ v4, const uint16_t* __restrict__ vs,
+    const int8_t* __restrict__ c8, const uint16_t* __restrict__ cs,
+    const int8_t* __restrict__ mu8, const uint16_t* __restrict__ mus,
+    const uint16_t* __restrict__ cache, long c_sb, long c_st,
+    int NB, const int* __restrict__ bt, long bt_sr, int bt_cols,
+    const int* __restrict__ nsh, float* __restrict__ score, long sc_sr, int MP,
+    int H, float scale, int chunk)
+{
+    const int z = blockIdx.x, r = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int P = min(nsh[r], MP);
+    const int c0 = z * chunk;
+    const int c1 = min(c0 + chunk, P);
+    if (c0 >= c1) return;
+
+    __shared__ __attribute__((aligned(16))) int8_t q8s[ML_H + 1][ML_D];   // row 16 = zeros
+    __shared__ __attribute__((aligned(16))) uint16_t qrs[ML_H][ML_DR];
+    __shared__ float qss[ML_H];
+    __shared__ int bt_l[ML_MAX_CHUNK];
+    __shared__ __attribute__((aligned(16))) uint8_t stage_l[ML_WAVES][MS_BYTES];
+
+    // ---- prologue: block ids, q quantized per head (absmax / 127) --------
+    for (int i = tid; i < c1 - c0; i += ML_BLK) {
+        const int b = bt[(long)r * bt_sr + min(c0 + i, bt_cols - 1)];
+        bt_l[i] = min(max(b, 0), NB - 1);
+    }
+    for (int i = tid; i < ML_D / 4; i += ML_BLK) reinterpret_cast<int*>(&q8s[ML_H][0])[i] = 0;
+    for (int h = wave; h < ML_H; h += ML_WAVES) {
+        const uint16_t* qh = q + (long)r * q_sr + (long)h * q_sh;
+        float a[8];
+        if (h < H) {
+            const uint4 w = *reinterpret_cast<const uint4*>(qh + 8 * lane);
+            const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) { a[2 * e] = bf16lo(ws[e]); a[2 * e + 1] = bf16hi(ws[e]); }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) a[e] = 0.f;
+        }
+        float am = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) am = fmaxf(am, fabsf(a[e]));
+        am = wave_max(am);
+        const float qs = fmaxf(am, 1e-8f) / 127.f;
+        uint32_t pk[2] = {0u, 0u};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int v = (h < H) ? (int)rintf(__fdiv_rn(a[e], qs)) : 0;
+            pk[e >> 2] |= ((uint32_t)(uint8_t)v) << (8 * (e & 3));
+        }
+        *reinterpret_cast<uint2*>(&q8s[h][8 * lane]) = make_uint2(pk[0], pk[1]);
+        if (lane < ML_DR / 8) {
+            uint4 w = make_uint4(0u, 0u, 0u, 0u);
+            if (h < H) w = *reinterpret_cast<const uint4*>(qh + ML_D + 8 * lane);
+            *reinterpret_cast<uint4*>(&qrs[h][8 * lane]) = w;
+        }
+        if (lane == 0) qss[h] = (h < H) ? qs : 0.f;
+    }
+    __syncthreads();
+
+    const int r16 = lane & 15, kg = lane >> 4;
+    const uint32_t MH = 0xF0F0F0F0u;
+    // q operands shared by every unit: projection B (column j = head j),
+    // RoPE B (column = head), per-head scale of this lane's column
+    v4i Bq[4][2];
+    {
+        const int hrow = r16 < H ? r16 : ML_H;
+#pragma unroll
+        for (int k4 = 0; k4 < 4; ++k4) {
+            Bq[k4][0] = perm_even_odd(*reinterpret_cast<const uint4*>(&q8s[hrow][128 * k4 + 32 * kg]));
+            Bq[k4][1] = perm_even_odd(*reinterpret_cast<const uint4*>(&q8s[hrow][128 * k4 + 32 * kg + 16]));
+        }
+    }
+    v8bf Br[2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+        Br[s] = __builtin_bit_cast(v8bf, *reinterpret_cast<const uint4*>(&qrs[r16][32 * s + 8 * kg]));
+    const float qsj = qss[r16];
+    const bool col_ok = r16 < H;
+
+    const int n_units = cdiv(c1 - c0, 2);
+    uint4 fv0, fv1, fv2, fv3, fmu, fc8, fcs, fvs, fr0, fr1, fr2, fr3;
+    uint32_t fmus = 0u;
+    // natural-order (coalesced) loads of unit u into registers
+    auto load_unit = [&](int u) {
+        const int p0 = 2 * u;
+        const int last = c1 - c0 - 1;
+        auto blk_of = [&](int pg) -> long { return (long)bt_l[min(p0 + pg, last)]; };
+        // 16-byte chunk i = lane + 64 m of the 2 V rows
+        auto vload = [&](int i) { return *reinterpret_cast<const uint4*>(v4 + blk_of(i >> 7) * ML_VROW + (i & 127) * 16); };
+        fv0 = vload(lane); fv1 = vload(lane + 64); fv2 = vload(lane + 128); fv3 = vload(lane + 192);
+        fmu = *reinterpret_cast<const uint4*>(mu8 + blk_of(lane >> 5) * ML_D + (lane & 31) * 16);
+        if (lane < 16) fc8 = *reinterpret_cast<const uint4*>(c8 + blk_of(lane >> 3) * (ML_PG * ML_RNK) + (lane & 7) * 16);
+        if (lane < 4) fcs = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(cs) + blk_of(lane >> 1) * (ML_PG * 2) + (lane & 1) * 16);
+        if (lane < 2) {
+            fvs = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(vs) + blk_of(lane) * (ML_RNK * 2));
+            fmus = (uint32_t)mus[blk_of(lane)];
+        }
+        // RoPE chunk i = (page i >> 7, token (i >> 3) & 15, 16-byte part i & 7)
+        auto rload = [&](int i) {
+            return *reinterpret_cast<const uint4*>(cache + blk_of(i >> 7) * c_sb + (long)((i >> 3) & 15) * c_st + ML_D + 8 * (i & 7));
+        };
+        fr0 = rload(lane); fr1 = rload(lane + 64); fr2 = rload(lane + 128); fr3 = rload(lane + 192);
+    };
+    auto store_unit = [&](uint8_t* st) {
+        *reinterpret_cast<uint4*>(st + MS_V + lane * 16) = fv0;
+        *reinterpret_cast<uint4*>(st + MS_V + (lane + 64) * 16) = fv1;
+        *reinterpret_cast<uint4*>(st + MS_V + (lane + 128) * 16) = fv2;
+        *reinterpret_cast<uint4*>(st + MS_V + (lane + 192) * 16) = fv3;
+        *reinterpret_cast<uint4*>(st + MS_MU + lane * 16) = fmu;
+        if (lane < 16) *reinterpret_cast<uint4*>(st + MS_C8 + lane * 16) = fc8;
+        if (lane < 4) *reinterpret_cast<uint4*>(st + MS_CS + lane * 16) = fcs;
+        if (lane < 2) {
+            *reinterpret_cast<uint4*>(st + MS_VS + lane * 16) = fvs;
+            *reinterpret_cast<uint32_t*>(st + MS_MUS + lane * 4) = fmus;
+        }
+        *reinterpret_cast<uint4*>(st + MS_RP + lane * 16) = fr0;
+        *reinterpret_cast<uint4*>(st + MS_RP + (lane + 64) * 16) = fr1;
+        *reinterpret_cast<uint4*>(st + MS_RP + (lane + 128) * 16) = fr2;
+        *reinterpret_cast<uint4*>(st + MS_RP + (lane + 192) * 16) = fr3;
+    };
+
+    uint8_t* st = stage_l[wave];
+    if (wave < n_units) load_unit(wave);
+    for (int u = wave; u < n_units; u += ML_WAVES) {
+        store_unit(st);
+        if (u + ML_WAVES < n_units) load_unit(u + ML_WAVES);   // next unit in flight
+        wave_lds_sync();
+        const int p0 = c0 + 2 * u;
+        const int nvalid = min(2, c1 - p0);
+
+        // ---- projection (A = the 16 V rows of the pair, row 4a + b <->
+        // page b & 1, column 2a + (b >> 1); B = int8 q) and the centroid
+        // term (A rows 0/1 = the two mu rows, same B) ----------------------
+        const int i_pg = r16 & 1, i_c = 2 * (r16 >> 2) + ((r16 >> 1) & 1);
+        v4i acc = {0, 0, 0, 0}, accm = {0, 0, 0, 0};
+#pragma unroll
+        for (int k4 = 0; k4 < 4; ++k4) {
+            const uint4 w = *reinterpret_cast<const uint4*>(st + MS_V + i_pg * ML_VROW + i_c * (ML_D / 2) + k4 * 64 + kg * 16);
+            const v4i a0 = {(int)((w.x << 4) & MH), (int)((w.y << 4) & MH), (int)(w.x & MH), (int)(w.y & MH)};
+            const v4i a1 = {(int)((w.z << 4) & MH), (int)((w.w << 4) & MH), (int)(w.z & MH), (int)(w.w & MH)};
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, Bq[k4][0], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, Bq[k4][1], acc, 0, 0, 0);
+            v4i m0 = {0, 0, 0, 0}, m1 = {0, 0, 0, 0};
+            if (r16 < 2) {
+                m0 = perm_even_odd(*reinterpret_cast<const uint4*>(st + MS_MU + r16 * ML_D + 128 * k4 + 32 * kg));
+                m1 = perm_even_odd(*reinterpret_cast<const uint4*>(st + MS_MU + r16 * ML_D + 128 * k4 + 32 * kg + 16));
+            }
+            accm = __builtin_amdgcn_mfma_i32_16x16x64_i8(m0, Bq[k4][0], accm, 0, 0, 0);
+            accm = __builtin_amdgcn_mfma_i32_16x16x64_i8(m1, Bq[k4][1], accm, 0, 0, 0);
+        }
+        // qt[v] = qt[head r16][page v & 1][column 2kg + (v >> 1)]; the 1/16 of
+        // the high-nibble operand rides on the power-of-two column scale
+        float qt[4];
+        {
+            const uint32_t w0 = *reinterpret_cast<const uint32_t*>(st + MS_VS + 0 * 16 + kg * 4);
+            const uint32_t w1 = *reinterpret_cast<const uint32_t*>(st + MS_VS + 1 * 16 + kg * 4);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const uint32_t w = (v & 1) ? w1 : w0;
+                const float vsc = ((v >> 1) ? bf16hi(w) : bf16lo(w)) * 0.0625f;
+                qt[v] = (float)acc[v] * qsj * vsc;
+            }
+        }
+        // centroid term of (page v, head r16) lives in lanes kg = 0, v = 0/1
+        float* md = reinterpret_cast<float*>(st + MS_MD);
+        if (kg == 0) {
+#pragma unroll
+            for (int v = 0; v < 2; ++v) {
+                const float musf = bf16lo(*reinterpret_cast<const uint32_t*>(st + MS_MUS + v * 4));
+                md[v * 16 + r16] = (float)accm[v] * qsj * musf;
+            }
+        }
+        wave_lds_sync();
+
+        // ---- per page: token reconstruction + RoPE, max over (t, h) -------
+#pragma unroll
+        for (int pg = 0; pg < 2; ++pg) {
+            v4f tk = {0.f, 0.f, 0.f, 0.f};
+            const uint32_t cw = *reinterpret_cast<const uint16_t*>(st + MS_C8 + pg * 128 + r16 * 8 + 2 * kg);
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const float a = (float)(int8_t)(cw >> (8 * hh));
+                tk = __builtin_amdgcn_mfma_f32_16x16x4f32(a, qt[2 * hh + pg], tk, 0, 0, 0);
+            }
+            v4f rp = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+                const v8bf a = __builtin_bit_cast(v8bf, *reinterpret_cast<const uint4*>(
+                    st + MS_RP + (pg * 16 + r16) * 128 + (32 * s + 8 * kg) * 2));
+                rp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, Br[s], rp, 0, 0, 0);
+            }
+            const uint2 csw = *reinterpret_cast<const uint2*>(st + MS_CS + pg * 32 + kg * 8);
+            const float mud = md[pg * 16 + r16];
+            const float t0 = fmaf(tk[0], bf16lo(csw.x), rp[0]);
+            const float t1 = fmaf(tk[1], bf16hi(csw.x), rp[1]);
+            const float t2 = fmaf(tk[2], bf16lo(csw.y), rp[2]);
+            const float t3 = fmaf(tk[3], bf16hi(csw.y), rp[3]);
+            float m = col_ok ? fmaxf(fmaxf(t0, t1), fmaxf(t2, t3)) + mud : -INFINITY;
+            m = wave_max(m);
+            if (lane == 0 && pg < nvalid) score[(long)r * sc_sr + p0 + pg] = m * scale;
+        }
+        wave_lds_sync();                                 // stage reused by the next unit
+    }
+}
+
+// ---------------------------------------------------------------------------
+// split-K sparse decode over the selected latent pages
+// ---------------------------------------------------------------------------
+// Workgroup = 4 waves = one split of one request.  A page (16 tokens x 576
+// bf16 = 18 KB) is DMA'd with global_load_lds_dwordx4 into one of two
+// workgroup stages while the other is consumed.  S = K Q^T is split over the
+// waves by head-dim k-steps (partials summed through LDS in a fixed order,
+// so every wave holds the identical S); each wave then owns a 128-d slice of
+// the 512-d output for O^T += V^T P^T.  All stage and partial accesses are
+// inline-asm LDS ops: the compiler cannot tell them from the DMA in flight
+// and would otherwise wait for it before every access.
+constexpr int MD_PAGE_B = ML_PG * ML_HS * 2;          // 18432 B
+constexpr int MD_CHUNKS = MD_PAGE_B / 16;             // 1152 16-byte DMA chunks
+constexpr int MD_IDS = 256;                           // page ids staged per batch
+constexpr int MD_MAX_SPLIT = 512;
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)(p);
+}
+__device__ __forceinline__ v4i ds_read16(uint32_t a) {
+    v4i v;
+    asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(a));
+    return v;
+}
+__device__ __forceinline__ void ds_write16(uint32_t a, v4i x) {
+    asm volatile("ds_write_b128 %0, %1" : : "v"(a), "v"(x));
+}
+// Wait for the outstanding LDS ops; the loaded registers pass through the
+// wait as operands so no use of them can be scheduled before it.
+__device__ __forceinline__ void lgkm_wait() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+__device__ __forceinline__ void lgkm_wait(v4i& a, v4i& b, v4i& c, v4i& d) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) :: "memory");
+}
+__device__ __forceinline__ void lgkm_wait(v4i& a, v4i& b, v4i& c, v4i& d, v4i& e) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d), "+v"(e) :: "memory");
+}
+
+__global__ __launch_bounds__(ML_BLK) void mla_decode_split_kernel(
+    const uint16_t* __restrict__ q, long q_sr, long q_sh,
+    const uint16_t* __restrict__ cache, long c_sb, long c_st, int NB,
+    const int* __restrict__ bt, long bt_sr, int bt_cols,
+    const int* __restrict__ ptab, long pt_sr, int pt_cols, const int* __restrict__ pcnt,
+    const int* __restrict__ seq_lens, float* __restrict__ m_part, float* __restrict__ l_part,
+    float* __restrict__ acc_part, int H, int split, int pps_min, float scale)
+{
+    const int sp = blockIdx.x, r = blockIdx.y;
+    const int cnt = min(pcnt[r], pt_cols);
+    const int pps = max(cdiv(cnt, split), pps_min);
+    const int j0 = sp * pps;
+    if (j0 >= cnt) return;                               // inactive split: no store
+    const int j1 = min(j0 + pps, cnt);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r16 = lane & 15, kg = lane >> 4;
+    const int seq_len = seq_lens[r];
+
+    __shared__ __attribute__((aligned(16))) uint8_t stg[2][MD_PAGE_B];
+    __shared__ __attribute__((aligned(16))) float spart[ML_WAVES][kWave * 4];
+    __shared__ int ids_pt[MD_IDS], ids_blk[MD_IDS];
+
+    // QK k-steps of this wave: 18 steps of 32 dims split 5/5/4/4
+    const int s_lo = wave < 2 ? 5 * wave : 10 + 4 * (wave - 2);
+    const int s_n = wave < 2 ? 5 : 4;
+    v8bf qb[5];
+    {
+        const uint16_t* qp = q + (long)r * q_sr + (long)r16 * q_sh + 8 * kg;
+#pragma unroll
+        for (int i = 0; i < 5; ++i) {
+            uint4 w = make_uint4(0u, 0u, 0u, 0u);
+            if (i < s_n && r16 < H) w = *reinterpret_cast<const uint4*>(qp + 32 * (s_lo + i));
+            qb[i] = __builtin_bit_cast(v8bf, w);
+        }
+    }
+    float m = -INFINITY, lsum = 0.f;
+    v4f o[8];
+#pragma unroll
+    for (int b = 0; b < 8; ++b) o[b] = v4f{0.f, 0.f, 0.f, 0.f};
+
+    const uint32_t st0 = lds_addr(&stg[0][0]);
+    const uint32_t sp_base = lds_addr(&spart[0][0]);
+    auto issue = [&](int slot, int blk) {
+        const uint16_t* base = cache + (long)blk * c_sb;
+#pragma unroll
+        for (int mm = 0; mm < 5; ++mm) {
+            const int i0 = 256 * mm + 64 * wave;             // first chunk of this wave's instruction
+            if (i0 < MD_CHUNKS) {
+                const int i = i0 + lane;
+                const int t = i / 72, part = i % 72;
+                __builtin_amdgcn_global_load_lds(base + (long)t * c_st + 8 * part,
+                                                 (lds_ptr_t)(&stg[slot][16 * i0]), 16, 0, 0);
+            }
+        }
+    };
+
+    for (int jb = j0; jb < j1; jb += MD_IDS) {
+        const int nb = min(MD_IDS, j1 - jb);
+        __syncthreads();                                      // previous batch fully consumed
+        for (int i = tid; i < nb; i += ML_BLK) {
+            const int pt = ptab[(long)r * pt_sr + jb + i];
+            const int ptc = min(max(pt, 0), bt_cols - 1);
+            ids_pt[i] = pt;
+            ids_blk[i] = min(max(bt[(long)r * bt_sr + ptc], 0), NB - 1);
+        }
+        __syncthreads();
+        issue(0, ids_blk[0]);
+        for (int i = 0; i < nb; ++i) {
+            const int slot = i & 1;
+            __builtin_amdgcn_s_waitcnt(0x0070);               // this wave's part of page i landed
+            __builtin_amdgcn_s_barrier();                     // every part landed; page i-1 consumed
+            if (i + 1 < nb) issue(slot ^ 1, ids_blk[i + 1]);
+            const int pt = ids_pt[i];
+            const uint32_t sb = st0 + slot * MD_PAGE_B;
+            // ---- partial S^T[t][h] over this wave's k-steps ----------------
+            v4f sacc = {0.f, 0.f, 0.f, 0.f};
+            v4i ka[5];
+#pragma unroll
+            for (int k = 0; k < 5; ++k)
+                if (k < s_n) ka[k] = ds_read16(sb + r16 * (ML_HS * 2) + (32 * (s_lo + k) + 8 * kg) * 2);
+            lgkm_wait(ka[0], ka[1], ka[2], ka[3], ka[4]);
+#pragma unroll
+            for (int k = 0; k < 5; ++k)
+                if (k < s_n)
+                    sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, ka[k]), qb[k], sacc, 0, 0, 0);
+            ds_write16(sp_base + (wave * kWave + lane) * 16, __builtin_bit_cast(v4i, sacc));
+            lgkm_wait();
+            __builtin_amdgcn_s_barrier();
+            v4i px[4];
+#pragma unroll
+            for (int w = 0; w < ML_WAVES; ++w) px[w] = ds_read16(sp_base + (w * kWave + lane) * 16);
+            lgkm_wait(px[0], px[1], px[2], px[3]);
+            v4f sv = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int w = 0; w < ML_WAVES; ++w) sv = sv + __builtin_bit_cast(v4f, px[w]);   // fixed order
+            // ---- online softmax (head = lane column) ----------------------
+            float s4[4];
+            const int pos0 = pt * ML_PG + 4 * kg;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) s4[v] = (pos0 + v < seq_len && r16 < H) ? sv[v] * scale : -INFINITY;
+            float mx = fmaxf(fmaxf(s4[0], s4[1]), fmaxf(s4[2], s4[3]));
+            mx = xor32_max(xor16_max(mx));
+            const float m_new = fmaxf(m, mx);
+            const float m_ref = (m_new == -INFINITY) ? 0.f : m_new;
+            const float alpha = __expf(m - m_ref);
+            float p[4];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) p[v] = __expf(s4[v] - m_ref);
+            lsum = lsum * alpha + (p[0] + p[1] + p[2] + p[3]);
+            m = m_new;
+            const v4h pb = {(_Float16)p[0], (_Float16)p[1], (_Float16)p[2], (_Float16)p[3]};
+            // ---- O^T[d][h] += V^T P^T over this wave's 128 dims ------------
+            v4i vi[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                vi[j] = ds_read16(sb + (4 * kg + j) * (ML_HS * 2) + (128 * wave + 8 * r16) * 2);
+            lgkm_wait(vi[0], vi[1], vi[2], vi[3]);
+            uint4 vr[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) vr[j] = __builtin_bit_cast(uint4, vi[j]);
+#pragma unroll
+            for (int b = 0; b < 8; ++b) {
+                v4h a;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t x = (b >> 1) == 0 ? vr[j].x : (b >> 1) == 1 ? vr[j].y : (b >> 1) == 2 ? vr[j].z : vr[j].w;
+                    a[j] = (_Float16)bf16_to_f32((uint16_t)((b & 1) ? (x >> 16) : (x & 0xFFFFu)));
+                }
+                o[b] = o[b] * alpha;
+                o[b] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, pb, o[b], 0, 0, 0);
+            }
+        }
+    }
+    lsum = xor32_sum(xor16_sum(lsum));
+    // ---- partial of this split: m, l (G) and acc (G, 512) ------------------
+    const long base = (long)r * split + sp;
+    if (wave == 0 && kg == 0 && r16 < H) {
+        m_part[base * ML_H + r16] = m;
+        l_part[base * ML_H + r16] = lsum;
+    }
+    if (r16 < H) {
+        float* ap = acc_part + (base * ML_H + r16) * ML_D + 128 * wave + 32 * kg;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            *reinterpret_cast<float4*>(ap + 8 * v) = make_float4(o[0][v], o[1][v], o[2][v], o[3][v]);
+            *reinterpret_cast<float4*>(ap + 8 * v + 4) = make_float4(o[4][v], o[5][v], o[6][v], o[7][v]);
+        }
+    }
+}
+
+// LSE merge of the active splits (merge.py:105-152 rule) into o (R, H, 512)
+// and lse (R, H); grid (H, R), 128 threads x 4 dims.
+__global__ __launch_bounds__(128) void mla_merge_kernel(
+    const float* __restrict__ m_part, const float* __restrict__ l_part,
+    const float* __restrict__ acc_part, const int* __restrict__ pcnt, int pt_cols,
+    void* __restrict__ out, long o_sr, long o_sh, int out_f32,
+    float* __restrict__ lse, long lse_sr, int split, int pps_min)
+{
+    const int h = blockIdx.x, r = blockIdx.y, tid = threadIdx.x;
+    const int cnt = min(pcnt[r], pt_cols);
+    const int pps = max(cdiv(cnt, split), pps_min);
+    const int n_act = cnt > 0 ? cdiv(cnt, pps) : 0;
+    __shared__ float w_s[MD_MAX_SPLIT];
+    __shared__ float red[2];
+    float M = -INFINITY;
+    for (int s = 0; s < n_act; ++s) {
+        const float l = l_part[((long)r * split + s) * ML_H + h];
+        if (l > 0.f) M = fmaxf(M, m_part[((long)r * split + s) * ML_H + h]);
+    }
+    float L = 0.f;
+    for (int s = tid; s < n_act; s += 128) {
+        const long i = ((long)r * split + s) * ML_H + h;
+        const float l = l_part[i];
+        const float w = (l > 0.f) ? __expf(m_part[i] - M) : 0.f;
+        w_s[s] = w;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int s = 0; s < n_act; ++s) L += w_s[s] * l_part[((long)r * split + s) * ML_H + h];
+        red[0] = L;
+    }
+    __syncthreads();
+    L = red[0];
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s = 0; s < n_act; ++s) {
+        const float w = w_s[s];
+        if (w == 0.f) continue;
+        const float4 a = *reinterpret_cast<const float4*>(acc_part + (((long)r * split + s) * ML_H + h) * ML_D + 4 * tid);
+        acc.x += w * a.x; acc.y += w * a.y; acc.z += w * a.z; acc.w += w * a.w;
+    }
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    const float4 o4 = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
+    if (out_f32) {
+        *reinterpret_cast<float4*>(static_cast<float*>(out) + r * o_sr + h * o_sh + 4 * tid) = o4;
+    } else {
+        uint16_t* op = static_cast<uint16_t*>(out) + r * o_sr + h * o_sh + 4 * tid;
+        *reinterpret_cast<uint2*>(op) = make_uint2((uint32_t)f32_to_bf16(o4.x) | ((uint32_t)f32_to_bf16(o4.y) << 16),
+                                                   (uint32_t)f32_to_bf16(o4.z) | ((uint32_t)f32_to_bf16(o4.w) << 16));
+    }
+    if (tid == 0 && lse) lse[r * lse_sr + h] = L > 0.f ? M + __logf(L) : -INFINITY;
+}
+
+}  // namespace locks
+
+using namespace locks;
+
+extern "C" int32_t locks_mla_score(
+    const uint16_t* q, int64_t q_stride_req, int64_t q_stride_head,
+    const uint8_t* v4, const uint16_t* vs, const int8_t* c8, const uint16_t* cs,
+    const int8_t* mu8, const uint16_t* mus, const uint16_t* cache, int64_t c_stride_block,
+    int64_t c_stride_tok, int32_t num_blocks, const int32_t* block_table, int64_t bt_stride,
+    int32_t bt_cols, const int32_t* n_sel_hi, float* score, int64_t score_stride,
+    int32_t max_pages, int32_t chunk, int32_t n_req, int32_t n_heads, int32_t kv_lora_rank,
+    int32_t rope_dim, int32_t page, float scale, void* stream)
+{
+    LOCKS_REQUIRE(kv_lora_rank == ML_D && rope_dim == ML_DR && page == ML_PG,
+                  "locks_mla_score: geometry (%d, %d, page %d) unsupported (this build: 512 + 64, page 16)",
+                  kv_lora_rank, rope_dim, page);
+    LOCKS_REQUIRE(n_heads >= 1 && n_heads <= ML_H, "locks_mla_score: n_heads=%d outside [1, %d]", n_heads, ML_H);
+    LOCKS_REQUIRE(n_req >= 0 && num_blocks >= 1 && bt_cols >= 1 && max_pages >= 1,
+                  "locks_mla_score: empty geometry");
+    LOCKS_REQUIRE(chunk >= 2 && chunk % 2 == 0 && chunk <= ML_MAX_CHUNK,
+                  "locks_mla_score: chunk %d must be even in [2, %d]", chunk, ML_MAX_CHUNK);
+    LOCKS_REQUIRE(q_stride_head % 8 == 0 && q_stride_req % 8 == 0 && c_stride_tok % 8 == 0 &&
+                  c_stride_block % 8 == 0, "locks_mla_score: strides must be multiples of 8 elements");
+    LOCKS_REQUIRE(q && v4 && vs && c8 && cs && mu8 && mus && cache && block_table && n_sel_hi && score,
+                  "locks_mla_score: null pointer argument");
+    if (n_req == 0) return 0;
+    const int Z = cdiv(max_pages, chunk);
+    hipLaunchKernelGGL(mla_score_kernel, dim3(Z, n_req), dim3(ML_BLK), 0, (hipStream_t)stream, q,
+                       (long)q_stride_req, (long)q_stride_head, v4, vs, c8, cs, mu8, mus, cache,
+                       (long)c_stride_block, (long)c_stride_tok, num_blocks, block_table,
+                       (long)bt_stride, bt_cols, n_sel_hi, score, (long)score_stride, max_pages,
+                       n_heads, scale, chunk);
+    return check_launch("mla_score_kernel");
+}
+
+extern "C" int32_t locks_mla_score_auto_chunk(int32_t n_req, int32_t max_pages) {
+    // ~512 workgroups over all (request, page pair) units, whole pairs
+    const long pairs = (long)cdiv(max_pages > 0 ? max_pages : 1, 2) * (n_req > 0 ? n_req : 1);
+    long per_wg = (pairs + 511) / 512;
+    if (per_wg < 1) per_wg = 1;
+    if (per_wg > ML_MAX_CHUNK / 2) per_wg = ML_MAX_CHUNK / 2;
+    return (int32_t)(2 * per_wg);
+}
+
+extern "C" int32_t locks_mla_decode_splitk(
+    const uint16_t* q, int64_t q_stride_req, int64_t q_stride_head, const uint16_t* cache,
+    int64_t c_stride_block, int64_t c_stride_tok, int32_t num_blocks, const int32_t* block_table,
+    int64_t bt_stride, int32_t bt_cols, const int32_t* page_table, int64_t pt_stride,
+    int32_t pt_cols, const int32_t* page_cnt, const int32_t* seq_lens, float* m_part,
+    float* l_part, float* acc_part, int32_t n_req, int32_t n_heads, int32_t kv_lora_rank,
+    int32_t rope_dim, int32_t page, int32_t split, int32_t pps_min, float scale, void* stream)
+{
+    LOCKS_REQUIRE(kv_lora_rank == ML_D && rope_dim == ML_DR && page == ML_PG,
+                  "locks_mla_decode_splitk: geometry (%d, %d, page %d) unsupported (this build: 512 + 64, page 16)",
+                  kv_lora_rank, rope_dim, page);
+    LOCKS_REQUIRE(n_heads >= 1 && n_heads <= ML_H, "locks_mla_decode_splitk: n_heads=%d outside [1, %d]",
+                  n_heads, ML_H);
+    LOCKS_REQUIRE(split >= 1 && split <= MD_MAX_SPLIT && pps_min >= 1,
+                  "locks_mla_decode_splitk: split=%d pps_min=%d (split in [1, %d])", split, pps_min, MD_MAX_SPLIT);
+    LOCKS_REQUIRE(q_stride_head % 8 == 0 && q_stride_req % 8 == 0 && c_stride_tok % 8 == 0 &&
+                  c_stride_block % 8 == 0, "locks_mla_decode_splitk: strides must be multiples of 8 elements");
+    LOCKS_REQUIRE(n_req >= 0 && num_blocks >= 1 && bt_cols >= 1 && pt_cols >= 1,
+                  "locks_mla_decode_splitk: empty geometry");
+    LOCKS_REQUIRE(q && cache && block_table && page_table && page_cnt && seq_lens && m_part && l_part && acc_part,
+                  "locks_mla_decode_splitk: null pointer argument");
+    if (n_req == 0) return 0;
+    hipLaunchKernelGGL(mla_decode_split_kernel, dim3(split, n_req), dim3(ML_BLK), 0, (hipStream_t)stream,
+                       q, (long)q_stride_req, (long)q_stride_head, cache, (long)c_stride_block,
+                       (long)c_stride_tok, num_blocks, block_table, (long)bt_stride, bt_cols,
+                       page_table, (long)pt_stride, pt_cols, page_cnt, seq_lens, m_part, l_part,
+                       acc_part, n_heads, split, pps_min, scale);
+    return check_launch("mla_decode_split_kernel");
+}
+
+extern "C" int32_t locks_mla_decode_merge(
+    const float* m_part, const float* l_part, const float* acc_part, const int32_t* page_cnt,
+    int32_t pt_cols, void* out, int64_t out_stride_req, int64_t out_stride_head, int32_t out_is_f32,
+    float* lse, int64_t lse_stride_req, int32_t n_req, int32_t n_heads, int32_t kv_lora_rank,
+    int32_t split, int32_t pps_min, void* stream)
+{
+    LOCKS_REQUIRE(kv_lora_rank == ML_D, "locks_mla_decode_merge: kv_lora_rank %d unsupported (512)", kv_lora_rank);
+    LOCKS_REQUIRE(n_heads >= 1 && n_heads <= ML_H, "locks_mla_decode_merge: n_heads=%d outside [1, %d]",
+                  n_heads, ML_H);
+    LOCKS_REQUIRE(split >= 1 && split <= MD_MAX_SPLIT && pps_min >= 1, "locks_mla_decode_merge: bad split");
+    LOCKS_REQUIRE(out_stride_req % 4 == 0 && out_stride_head % 4 == 0,
+                  "locks_mla_decode_merge: out strides must be multiples of 4 elements");
+    LOCKS_REQUIRE(m_part && l_part && acc_part && page_cnt && out, "locks_mla_decode_merge: null pointer argument");
+    if (n_req == 0) return 0;
+    hipLaunchKernelGGL(mla_merge_kernel, dim3(n_heads, n_req), dim3(128), 0, (hipStream_t)stream,
+                       m_part, l_part, acc_part, page_cnt, pt_cols, out, (long)out_stride_req,
+                       (long)out_stride_head, out_is_f32, lse, (long)lse_stride_req, split, pps_min);
+    return check_launch("mla_merge_kernel");
+}

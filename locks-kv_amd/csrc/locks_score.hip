@@ -47,7 +47,7 @@ constexpr int ST_C8 = 4096;                 // 8 pages x 128 B coefficients
 constexpr int ST_MU = 5120;                 // 8 pages x 128 B centroid  (-> mud after use)
 constexpr int ST_CS = 6144;                 // 8 pages x 32 B token scales
 constexpr int ST_VS = 6400;                 // 8 pages x 16 B column scales
-constexpr int ST_MUS = 6528;                // 8 dwords holding the centroid scales
+constexpr int ST_MUS = 6528;                // 8 dwords: the pages' centroid scales (bf16 in the low half)
 constexpr int ST_BYTES = 6560;
 
 __device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d) {
@@ -151,8 +151,7 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
         if (lane < 8) {                               // 8 pages x 16 B column scales
             const uint32_t row = row_of(lane);
             fvs = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(vs) + row * (SC_RNK * 2));
-            // aligned dword holding this page's centroid scale
-            fmus = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint8_t*>(mus) + ((row * 2u) & ~3u));
+            fmus = (uint32_t)mus[row];              // this page's centroid scale
         }
     };
     auto store_unit = [&](uint8_t* stg) {
@@ -243,9 +242,7 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
             const int pg = lane & 15;
             mu0 = *reinterpret_cast<const v4i*>(stg + ST_MU + pg * 128 + kg * 32);
             mu1 = *reinterpret_cast<const v4i*>(stg + ST_MU + pg * 128 + kg * 32 + 16);
-            const uint32_t row = (uint32_t)bt_l[t * SC_TILE + min(pg, nvalid - 1)] * (uint32_t)n_kv + (uint32_t)h;
-            const uint32_t w = *reinterpret_cast<const uint32_t*>(stg + ST_MUS + pg * 4);
-            musf = (row & 1u) ? bf16hi(w) : bf16lo(w);
+            musf = bf16lo(*reinterpret_cast<const uint32_t*>(stg + ST_MUS + pg * 4));
         }
         wave_lds_sync();                               // mu consumed: reuse as mud
         float* mud_w = reinterpret_cast<float*>(stg + ST_MU);    // [page][16]

@@ -34,6 +34,15 @@ SIGNATURES = {
     "locks_build_rki4": (_i32, [_p, _i64, _i64, _i64, _i32, _p, _i32, _i32, _i32, _i32,
                                 _p, _p, _p, _p, _p, _p, _p, _p]),
     "locks_pack_rki4": (_i32, [_p, _p, _p, _p, _p, _i32, _i32, _i32, _p, _p, _p, _p, _p, _p, _p]),
+    "locks_mla_score": (_i32, [_p, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _p,
+                               _i64, _i32, _p, _p, _i64, _i32, _i32, _i32, _i32, _i32, _i32,
+                               _i32, _f32, _p]),
+    "locks_mla_score_auto_chunk": (_i32, [_i32, _i32]),
+    "locks_mla_decode_splitk": (_i32, [_p, _i64, _i64, _p, _i64, _i64, _i32, _p, _i64, _i32, _p,
+                                       _i64, _i32, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32,
+                                       _i32, _i32, _i32, _f32, _p]),
+    "locks_mla_decode_merge": (_i32, [_p, _p, _p, _p, _i32, _p, _i64, _i64, _i32, _p, _i64, _i32,
+                                      _i32, _i32, _i32, _i32, _p]),
     "locks_decode_merge": (_i32, [_p, _p, _p, _p, _i64, _p, _i64, _i64, _i32, _i32, _i32, _i32,
                                   _i32, _i32, _i32, _p]),
 }

@@ -1,0 +1,183 @@
+"""GPU parity of the MLA path (config 5 shape: one latent head of 512 + 64
+RoPE dims, 16 query heads, page 16) through the C ABI, against the numpy
+MLA oracle (oracle/mla_oracle.py) on seeded inputs."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import locks_oracle as O
+from oracle import mla_oracle as M
+
+pytestmark = pytest.mark.gpu
+
+LKV, DR, HS, PAGE = 512, 64, 576, 16
+
+
+def say(*a):
+    print("[mla]", *a, flush=True)
+
+
+def _case(seed, seq_lens, H=16, extra=8):
+    rng = np.random.default_rng(seed)
+    npg = [(s + PAGE - 1) // PAGE for s in seq_lens]
+    NB = sum(npg) + extra
+    MP = max(npg)
+    cache = M.synth_latent(rng, NB, PAGE, LKV, DR)
+    bt = O.synth_block_table(rng, seq_lens, PAGE, NB, MP)
+    q = O.f32_to_bf16(rng.standard_normal((len(seq_lens), H, HS)).astype(np.float32))
+    return dict(cache=cache, bt=bt, q=q, sl=np.array(seq_lens, np.int32), NB=NB, MP=MP, H=H, R=len(seq_lens))
+
+
+def _dev(c):
+    import torch
+    u16 = lambda a: torch.from_numpy(a.view(np.int16).copy()).view(torch.bfloat16).cuda()
+    return dict(cache=u16(c["cache"]), q=u16(c["q"]), bt=torch.from_numpy(c["bt"]).cuda(),
+                sl=torch.from_numpy(c["sl"]).cuda())
+
+
+def _state(c, budget, L=1, window=10, sink=1):
+    from locks.selection import MlaState
+    return MlaState("cuda", num_layers=L, num_blocks=c["NB"], n_heads=c["H"], max_reqs=c["R"],
+                    max_pages=c["MP"], budget_pages=budget, sink_pages=sink, window_pages=window)
+
+
+def _upload_slabs(st, slabs, layer=0):
+    import torch
+    for k, name in (("v4", "pp_v4"), ("vs", "pp_vs"), ("c8", "pp_c8"), ("cs", "pp_cs"),
+                    ("mu8", "pp_mu8"), ("mus", "pp_mus")):
+        a = slabs[k]
+        t = getattr(st, name)[layer]
+        if a.dtype == np.uint16:
+            t.copy_(torch.from_numpy(a.view(np.int16).copy()).view(torch.bfloat16).reshape(t.shape))
+        else:
+            t.copy_(torch.from_numpy(a.copy()).reshape(t.shape))
+
+
+def _blocks_of(c):
+    out = []
+    for r, s in enumerate(c["sl"]):
+        out.extend(c["bt"][r, :int(s) // PAGE].tolist())
+    return np.array(sorted(set(out)), np.int32)
+
+
+@pytest.mark.parametrize("seq_lens,H", [([16 * 40 + 5], 16), ([16 * 300, 16 * 77 + 9], 16), ([16 * 50 + 1], 5)])
+def test_mla_score_matches_oracle(seq_lens, H):
+    import torch
+    from locks.selection import mla_derive, mla_score_only
+    say("score", seq_lens, H)
+    c = _case(11, seq_lens, H)
+    d = _dev(c)
+    st = _state(c, budget=32)
+    slabs = M.mla_build_summaries(c["cache"], _blocks_of(c), c["NB"])
+    _upload_slabs(st, slabs)
+    mla_derive(st, d["sl"], c["R"])
+    st.score_h.fill_(123.0)
+    mla_score_only(st, 0, d["q"], d["cache"], d["bt"], c["R"], 0.07)
+    torch.cuda.synchronize()
+    npg, nsh, b = M.mla_derive(c["sl"], PAGE, 10, 1, 32)
+    ref = M.mla_score_rki4(c["q"], slabs, c["cache"], c["bt"], nsh, 0.07, c["MP"])
+    got = st.score_h[:, 0, 0, :].cpu().numpy()
+    for r in range(c["R"]):
+        P = int(nsh[r])
+        err = np.abs(got[r, :P] - ref[r, :P]).max()
+        say(f"row {r}: {P} pages, max |d| {err:.2e}")
+        assert err <= 2e-4 * max(1.0, np.abs(ref[r, :P]).max())
+        assert np.all(got[r, P:] == 123.0)                       # never written past n_sel_hi
+
+
+def test_mla_build_matches_oracle_through_the_score():
+    """Eigenvectors agree only up to sign/rotation, so the GPU-built latent
+    summary is compared through the oracle score it produces."""
+    import torch
+    from locks.selection import mla_build_blocks
+    say("build")
+    c = _case(12, [16 * 64 + 3])
+    d = _dev(c)
+    st = _state(c, budget=32)
+    blocks = _blocks_of(c)
+    mla_build_blocks(st, 0, d["cache"], torch.from_numpy(blocks).cuda())
+    torch.cuda.synchronize()
+    gpu = dict(v4=st.pp_v4[0].cpu().numpy(), vs=st.pp_vs[0].view(torch.int16).cpu().numpy().view(np.uint16),
+               c8=st.pp_c8[0].cpu().numpy(), cs=st.pp_cs[0].view(torch.int16).cpu().numpy().view(np.uint16),
+               mu8=st.pp_mu8[0].cpu().numpy(), mus=st.pp_mus[0].view(torch.int16).cpu().numpy().view(np.uint16))
+    ref = M.mla_build_summaries(c["cache"], blocks, c["NB"])
+    assert np.array_equal(gpu["mu8"][blocks], ref["mu8"][blocks])          # mean path is exact
+    assert np.array_equal(gpu["mus"][blocks], ref["mus"][blocks])
+    npg, nsh, b = M.mla_derive(c["sl"], PAGE, 10, 1, 32)
+    s_gpu = M.mla_score_rki4(c["q"], gpu, c["cache"], c["bt"], nsh, 0.07, c["MP"])[0, :int(nsh[0])]
+    s_ref = M.mla_score_rki4(c["q"], ref, c["cache"], c["bt"], nsh, 0.07, c["MP"])[0, :int(nsh[0])]
+    rel = np.abs(s_gpu - s_ref).max() / np.abs(s_ref).max()
+    say(f"score from GPU vs oracle build: max rel {rel:.2e}")
+    assert rel <= 5e-3
+
+
+@pytest.mark.parametrize("seq_lens,budget", [([16 * 200 + 7], 32), ([16 * 100, 16 * 20 + 3, 16 * 9], 24),
+                                             ([16 * 8192], 128)])
+def test_mla_select_matches_topb_middle(seq_lens, budget):
+    import torch
+    from locks.selection import mla_select_pages
+    say("select", seq_lens, budget)
+    c = _case(13, seq_lens)
+    d = _dev(c)
+    st = _state(c, budget=budget)
+    slabs = M.mla_build_summaries(c["cache"], _blocks_of(c), c["NB"])
+    _upload_slabs(st, slabs)
+    mla_select_pages(st, 0, d["q"], d["cache"], d["bt"], d["sl"], c["R"], 0.07)
+    torch.cuda.synchronize()
+    tab, cnt = st.page_table[:, 0].cpu().numpy(), st.page_cnt[:, 0].cpu().numpy()
+    gsc = st.score_h[:, 0, 0, :].cpu().numpy()
+    for r in range(c["R"]):
+        P = (int(c["sl"][r]) + PAGE - 1) // PAGE
+        ps = np.full(P, -np.inf, np.float32)
+        nfull = int(c["sl"][r]) // PAGE
+        n_sc = max(min(nfull, P - 10), 0)
+        ps[:n_sc] = gsc[r, :n_sc]
+        keep = M.topb_middle(ps, budget, 1, 10)                  # reference rule on GPU scores
+        assert np.array_equal(np.nonzero(keep)[0], tab[r, :cnt[r]]), f"row {r}"
+        assert (tab[r, cnt[r]:] == -1).all()
+        assert cnt[r] == min(P, budget)
+
+
+@pytest.mark.parametrize("seq_lens,budget", [([16 * 60 + 5], 24), ([16 * 30, 16 * 7 + 2], 16),
+                                             ([16 * 2048], 128)])
+def test_mla_decode_matches_oracle(seq_lens, budget):
+    import torch
+    from locks.backend.mla_attn import mla_forward_mqa
+    say("decode", seq_lens, budget)
+    c = _case(14, seq_lens)
+    d = _dev(c)
+    st = _state(c, budget=budget)
+    slabs = M.mla_build_summaries(c["cache"], _blocks_of(c), c["NB"])
+    _upload_slabs(st, slabs)
+    out = torch.empty(c["R"], c["H"], LKV, dtype=torch.bfloat16, device="cuda")
+    o, lse = mla_forward_mqa(d["q"], d["cache"], d["bt"], d["sl"], st, 0.07, out=out, layer=0)
+    torch.cuda.synchronize()
+    tab, cnt = st.page_table[:, 0].cpu().numpy(), st.page_cnt[:, 0].cpu().numpy()
+    ref_o, ref_lse = M.mla_attention(c["q"], c["cache"], c["bt"], c["sl"], tab, cnt, 0.07)
+    got = o.float().cpu().numpy()
+    ref_b = O.bf16_round(ref_o.astype(np.float32))
+    err = np.abs(got - ref_b)
+    mr = err.sum() / np.abs(ref_b).sum()
+    lerr = np.abs(lse.cpu().numpy() - ref_lse).max()
+    say(f"o max-abs {err.max():.2e} mean-rel {mr:.2e}; lse max-abs {lerr:.2e}")
+    assert err.max() <= 2e-2 and mr <= 1e-3 and lerr <= 2e-3
+
+
+def test_mla_dense_equality():
+    """Budget >= page count keeps every page: the sparse decode equals dense
+    attention over the whole sequence."""
+    import torch
+    from locks.backend.mla_attn import mla_forward_mqa
+    c = _case(15, [16 * 37 + 11])
+    d = _dev(c)
+    st = _state(c, budget=10_000)
+    out = torch.empty(1, c["H"], LKV, dtype=torch.float32, device="cuda")
+    o, lse = mla_forward_mqa(d["q"], d["cache"], d["bt"], d["sl"], st, 0.07, out=out, layer=0)
+    torch.cuda.synchronize()
+    P = (int(c["sl"][0]) + 15) // 16
+    assert int(st.page_cnt[0, 0]) == P
+    ref_o, ref_lse = M.mla_attention(c["q"], c["cache"], c["bt"], c["sl"],
+                                     np.arange(P, dtype=np.int32)[None], np.array([P]), 0.07)
+    assert np.abs(o.cpu().numpy() - ref_o).max() <= 2e-3
+    assert np.abs(lse.cpu().numpy() - ref_lse).max() <= 1e-3
