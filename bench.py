@@ -12,7 +12,8 @@ Also measured in the same run: dense full-KV decode (same kernels, every
 page selected) on the same GPU, the scorer's live roofline, and the CPU
 oracle on a bounded sample (rank 0, N=1 only).
 
-    python bench.py [--workload llama8b-128k|glm9b-1m|glm9b-batch] [--steps K] [--warmup W]
+    python bench.py [--workload llama8b-128k|glm9b-1m|glm9b-batch|dsv2lite-mla-128k]
+                    [--steps K] [--warmup W]
 """
 from __future__ import annotations
 
@@ -42,7 +43,14 @@ WORKLOADS = {
     "glm9b-batch": dict(layers=40, n_kv=2, G=16, seq_lens=[262144, 196608, 131072, 65536]),
     # small smoke-size workload
     "tiny": dict(layers=2, n_kv=2, G=4, seq_lens=[16384]),
+    # DeepSeek-V2-Lite MLA, 27 layers, 16 heads over one
+    # latent of 512 + 64 RoPE dims, 128K, b=2048 tokens (128 pages incl. the
+    # sink and the 10-page window)
+    "dsv2lite-mla-128k": dict(layers=27, heads=16, seq_lens=[131072], mla=True,
+                              budget_pages=128, window_pages=10),
 }
+MLA_LKV, MLA_DR = 512, 64
+MLA_SCALE = 1.0 / math.sqrt(128 + 64)        # softmax scale over the q/k head dim (nope + rope)
 
 
 def log(*a):
@@ -270,6 +278,208 @@ def cpu_baseline(m, sample_pages=4096):
                               decode=round(t3 - t2, 3)))
 
 
+# --------------------------------------------------------------------------- #
+# MLA (config 5)
+# --------------------------------------------------------------------------- #
+def make_mla_model(wl, seed=0):
+    import torch
+    from locks.selection import MlaState, mla_build_blocks
+    dev = torch.device("cuda")
+    L, H, sls = wl["layers"], wl["heads"], wl["seq_lens"]
+    R = len(sls)
+    npg = [(s + PAGE - 1) // PAGE for s in sls]
+    MP, NB = max(npg), sum(npg) + 64
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    perm = torch.randperm(NB, generator=g, device=dev).to(torch.int32)
+    bt = torch.zeros(R, MP, dtype=torch.int32, device=dev)
+    off = 0
+    for r, n in enumerate(npg):
+        bt[r, :n] = perm[off:off + n]
+        off += n
+    st = MlaState(dev, num_layers=L, num_blocks=NB, n_heads=H, max_reqs=R, max_pages=MP,
+                  budget_pages=wl["budget_pages"], sink_pages=1, window_pages=wl["window_pages"])
+    fin = torch.cat([bt[r, : sls[r] // PAGE] for r in range(R)])
+    caches, t_build = [], 0.0
+    for layer in range(L):
+        sc = torch.exp(torch.randn(MLA_LKV + MLA_DR, generator=g, device=dev) * 0.5)
+        x = torch.randn(NB, PAGE, MLA_LKV + MLA_DR, generator=g, device=dev) * sc
+        cache = x.to(torch.bfloat16)
+        del x
+        caches.append(cache)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        mla_build_blocks(st, layer, cache, fin)
+        torch.cuda.synchronize()
+        t_build += time.perf_counter() - t0
+    st._layer_of = {c.data_ptr(): i for i, c in enumerate(caches)}
+    q = [torch.randn(R, H, MLA_LKV + MLA_DR, generator=g, device=dev).to(torch.bfloat16)
+         for _ in range(L)]
+    sl = torch.tensor(sls, dtype=torch.int32, device=dev)
+    return dict(st=st, cache=caches, q=q, bt=bt, sl=sl, R=R, L=L, H=H, MP=MP, NB=NB,
+                build_s=t_build, scale=MLA_SCALE)
+
+
+def mla_sparse_step(m, out, lse):
+    from locks.backend.mla_attn import mla_forward_mqa
+    for layer in range(m["L"]):                    # derive once per step (layer 0)
+        mla_forward_mqa(m["q"][layer], m["cache"][layer], m["bt"], m["sl"], m["st"], m["scale"],
+                        out=out[layer], lse=lse[layer], layer=layer, derive=(layer == 0))
+
+
+def make_mla_dense(m):
+    import torch
+    from locks.selection import MlaState
+    dn = MlaState("cuda", num_layers=1, num_blocks=8, n_heads=m["H"], max_reqs=m["R"],
+                  max_pages=m["MP"], budget_pages=m["MP"] + 1, split=512)
+    for r, s in enumerate(m["sl"].tolist()):
+        n = (s + PAGE - 1) // PAGE
+        dn.page_table[r, 0, :n] = torch.arange(n, dtype=torch.int32, device="cuda")
+        dn.page_cnt[r, 0] = n
+    dn.NB = m["NB"]
+    return dn
+
+
+def mla_dense_step(m, dn, out, lse):
+    from locks.attention import mla_decode
+    for layer in range(m["L"]):
+        mla_decode(dn, m["q"][layer], m["cache"][layer], m["bt"], m["sl"], m["R"], m["scale"],
+                   out[layer], lse[layer])
+
+
+def mla_step_bytes(m):
+    st = m["st"]
+    npg = [(s + PAGE - 1) // PAGE for s in m["sl"].tolist()]
+    nsc = [n - st.window_pages for n in npg]
+    cnt = int(st.page_cnt.sum().item())
+    page_b = PAGE * (MLA_LKV + MLA_DR) * 2
+    score = sum(P * (st.summary_bytes_per_page() + 4) for P in nsc)
+    select = sum(P * 8 + m["MP"] * 4 for P in nsc)
+    decode = cnt * page_b
+    dense = sum(n * page_b for n in npg)
+    L = m["L"]
+    return dict(score=L * score, select=L * select, decode=L * decode, dense=L * dense,
+                score_per_launch=score)
+
+
+def mla_scorer_us(m, reps=3):
+    import torch
+    from locks.selection import mla_derive, mla_score_only
+    st = m["st"]
+    mla_derive(st, m["sl"], m["R"])
+    s = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    for _ in range(reps):
+        for layer in range(m["L"]):
+            mla_score_only(st, layer, m["q"][layer], m["cache"][layer], m["bt"], m["R"], m["scale"])
+    e1.record(s)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (reps * m["L"])
+
+
+def mla_cpu_baseline(m, sample_pages=1024):
+    """MLA oracle on the host: layer 0's latent score + topb_middle over a
+    sample of `sample_pages` pages (scaled to the row) + attention over the
+    selected pages, x layers."""
+    import numpy as np
+    import torch
+
+    from oracle import locks_oracle as O
+    from oracle import mla_oracle as M
+    st = m["st"]
+    P = min(sample_pages, int(m["sl"][0].item()) // PAGE - st.window_pages)
+    to_np = lambda t: t.cpu().numpy()
+    slabs = {}
+    for name, attr, bf in (("v4", "pp_v4", 0), ("vs", "pp_vs", 1), ("c8", "pp_c8", 0),
+                           ("cs", "pp_cs", 1), ("mu8", "pp_mu8", 0), ("mus", "pp_mus", 1)):
+        t = getattr(st, attr)[0]
+        a = to_np(t.view(torch.int16) if bf else t)
+        slabs[name] = a.view(np.uint16) if bf else a
+    cache = to_np(m["cache"][0].view(torch.int16)).view(np.uint16)
+    q = to_np(m["q"][0][:1].view(torch.int16)).view(np.uint16)
+    sl = [(P + st.window_pages) * PAGE]
+    bt = m["bt"][:1, :P + st.window_pages].cpu().numpy()
+    t0 = time.perf_counter()
+    npg, nsh, b = M.mla_derive(sl, PAGE, st.window_pages, st.sink_pages, st.budget_pages)
+    sc = M.mla_score_rki4(q, slabs, cache, bt, nsh, m["scale"], int(npg[0]))
+    tab, cnt = O.topb_select(sc[:, None, :], npg, nsh, b, st.sink_pages, int(npg[0]))
+    t1 = time.perf_counter()
+    M.mla_attention(q, cache, bt, sl, tab[:, 0], cnt[:, 0], m["scale"])
+    t2 = time.perf_counter()
+    full_P = int(m["sl"][0].item()) // PAGE - st.window_pages
+    f = full_P / P
+    per_layer = (t1 - t0) * f + (t2 - t1)
+    try:
+        from threadpoolctl import threadpool_info
+        cores = max([i.get("num_threads", 1) for i in threadpool_info()] + [1])
+    except Exception:
+        cores = 1
+    return dict(value=round(per_layer * m["L"] * 1e3, 3), unit="ms/step", cores=cores,
+                kind="port",
+                sample=(f"numpy MLA oracle, layer 0, latent score + topb_middle over {P} of "
+                        f"{full_P} selectable pages (scaled x{f:.1f}), attention over the "
+                        f"selected pages, x{m['L']} layers"))
+
+
+def run_mla(a, wl):
+    import torch
+    t0 = time.perf_counter()
+    m = make_mla_model(wl)
+    log(f"MLA model ready in {time.perf_counter() - t0:.1f}s (latent summary build {m['build_s']:.1f}s)")
+    R, H, L = m["R"], m["H"], m["L"]
+    out = [torch.empty(R, H, MLA_LKV, dtype=torch.bfloat16, device="cuda") for _ in range(L)]
+    lse = [torch.empty(R, H, dtype=torch.float32, device="cuda") for _ in range(L)]
+    mla_sparse_step(m, out, lse)
+    torch.cuda.synchronize()
+    ref_tab, ref_out = m["st"].page_table.clone(), out[-1].clone()
+    g = capture(lambda: mla_sparse_step(m, out, lse))
+    for _ in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(m["st"].page_table, ref_tab), "graph replay changed the selection"
+        assert torch.equal(out[-1], ref_out), "graph replay changed the output"
+    ms = time_graph(g, a.steps, a.warmup)
+    by = mla_step_bytes(m)
+    score_us = mla_scorer_us(m)
+    score_gbps = by["score_per_launch"] / (score_us * 1e-6) / 1e9
+    res = {}
+    if not a.no_dense:
+        dn = make_mla_dense(m)
+        outd = [torch.empty_like(o) for o in out]
+        lsed = [torch.empty_like(x) for x in lse]
+        gd = capture(lambda: mla_dense_step(m, dn, outd, lsed))
+        ms_dense = time_graph(gd, max(3, a.steps // 5), 2)
+        res = dict(dense_ms_per_step=round(ms_dense, 4),
+                   dense_achieved_GBps=round(by["dense"] / (ms_dense * 1e-3) / 1e9, 1),
+                   speedup_vs_dense=round(ms_dense / ms, 3))
+    cpu = None if a.no_cpu else mla_cpu_baseline(m)
+    sparse_bytes = by["score"] + by["select"] + by["decode"]
+    line = {
+        "metric": "decode ms/step + achieved HBM GB/s, bs=1 @128K/1M ctx, b=2048",
+        "value": round(ms, 4), "unit": "ms/step", "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "ms_per_step": round(ms, 4), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": a.workload, "layers": L, "heads": H, "kv_lora_rank": MLA_LKV,
+                   "rope_dim": MLA_DR, "seq_lens": wl["seq_lens"], "page": PAGE,
+                   "budget_pages": wl["budget_pages"], "window_pages": wl["window_pages"],
+                   "attended_pages": int(m["st"].page_cnt[0, 0].item()),
+                   "parallelism": "single-gpu"},
+        "tokens_per_s": round(R * 1e3 / ms, 2),
+        "achieved_GBps": round(sparse_bytes / (ms * 1e-3) / 1e9, 1),
+        "step_algorithmic_bytes": sparse_bytes,
+        **res,
+        "roofline": {"bound": "hbm", "kernel": "mla_score_kernel", "achieved": round(score_gbps, 1),
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(score_gbps / HBM_PEAK_GBPS, 4),
+                     "avg_launch_us": round(score_us, 3),
+                     "bytes_per_launch": by["score_per_launch"],
+                     "traffic": scorer_traffic(a.workload)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -300,6 +510,9 @@ def main():
         log(f"copied {a.calib_copy} x {src.numel() * 4} B (read + write each)")
         return
     wl = WORKLOADS[a.workload]
+    if wl.get("mla"):
+        run_mla(a, wl)
+        return
     if a.pps_min:
         from locks.attention import decode as _dec
         _dec.PPS_MIN_OVERRIDE = a.pps_min

@@ -455,55 +455,98 @@ __global__ __launch_bounds__(ML_BLK) void mla_decode_split_kernel(
 }
 
 // LSE merge of the active splits (merge.py:105-152 rule) into o (R, H, 512)
-// and lse (R, H); grid (H, R), 128 threads x 4 dims.
-__global__ __launch_bounds__(128) void mla_merge_kernel(
+// and lse (R, H).  Grid (H, R, 4 slices of 128 dims); 256 threads = 32
+// float4 columns x 8 split groups, so hundreds of split partials (dense
+// decode) are read with 8 independent streams per column and reduced in LDS.
+constexpr int MG_BLK = 256;
+constexpr int MG_GRP = MG_BLK / 32;
+
+__global__ __launch_bounds__(MG_BLK) void mla_merge_kernel(
     const float* __restrict__ m_part, const float* __restrict__ l_part,
     const float* __restrict__ acc_part, const int* __restrict__ pcnt, int pt_cols,
     void* __restrict__ out, long o_sr, long o_sh, int out_f32,
     float* __restrict__ lse, long lse_sr, int split, int pps_min)
 {
-    const int h = blockIdx.x, r = blockIdx.y, tid = threadIdx.x;
+    const int h = blockIdx.x, r = blockIdx.y, zc = blockIdx.z, tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
     const int cnt = min(pcnt[r], pt_cols);
     const int pps = max(cdiv(cnt, split), pps_min);
     const int n_act = cnt > 0 ? cdiv(cnt, pps) : 0;
     __shared__ float w_s[MD_MAX_SPLIT];
-    __shared__ float red[2];
-    float M = -INFINITY;
-    for (int s = 0; s < n_act; ++s) {
-        const float l = l_part[((long)r * split + s) * ML_H + h];
-        if (l > 0.f) M = fmaxf(M, m_part[((long)r * split + s) * ML_H + h]);
+    __shared__ float red[MG_BLK / kWave];
+    __shared__ __attribute__((aligned(16))) float4 part[MG_GRP][32];
+    const long rb = (long)r * split;
+    // M = max over live splits; weights; L = sum w l (fixed reduction tree)
+    float mx = -INFINITY;
+    for (int s = tid; s < n_act; s += MG_BLK) {
+        const long i = (rb + s) * ML_H + h;
+        if (l_part[i] > 0.f) mx = fmaxf(mx, m_part[i]);
     }
-    float L = 0.f;
-    for (int s = tid; s < n_act; s += 128) {
-        const long i = ((long)r * split + s) * ML_H + h;
+    mx = wave_max(mx);
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    float M = red[0];
+#pragma unroll
+    for (int w = 1; w < MG_BLK / kWave; ++w) M = fmaxf(M, red[w]);
+    __syncthreads();
+    float lp = 0.f;
+    for (int s = tid; s < n_act; s += MG_BLK) {
+        const long i = (rb + s) * ML_H + h;
         const float l = l_part[i];
         const float w = (l > 0.f) ? __expf(m_part[i] - M) : 0.f;
         w_s[s] = w;
+        lp += w * l;
     }
+    lp += row_ror<8>(lp); lp += row_ror<4>(lp); lp += row_ror<2>(lp); lp += row_ror<1>(lp);
+    lp = xor32_sum(xor16_sum(lp));
+    if (lane == 0) red[wave] = lp;
     __syncthreads();
-    if (tid == 0) {
-        for (int s = 0; s < n_act; ++s) L += w_s[s] * l_part[((long)r * split + s) * ML_H + h];
-        red[0] = L;
-    }
-    __syncthreads();
-    L = red[0];
+    float L = 0.f;
+#pragma unroll
+    for (int w = 0; w < MG_BLK / kWave; ++w) L += red[w];
+    // acc over this slice: column c (4 dims), split group g
+    const int c = tid & 31, g = tid >> 5;
+    const int d0 = 128 * zc + 4 * c;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int s = 0; s < n_act; ++s) {
+    int s = g;
+    for (; s + 3 * MG_GRP < n_act; s += 4 * MG_GRP) {
+        float4 a[4];
+        float w[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            a[k] = *reinterpret_cast<const float4*>(acc_part + ((rb + s + k * MG_GRP) * ML_H + h) * ML_D + d0);
+            w[k] = w_s[s + k * MG_GRP];
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            acc.x += w[k] * a[k].x; acc.y += w[k] * a[k].y; acc.z += w[k] * a[k].z; acc.w += w[k] * a[k].w;
+        }
+    }
+    for (; s < n_act; s += MG_GRP) {
+        const float4 a = *reinterpret_cast<const float4*>(acc_part + ((rb + s) * ML_H + h) * ML_D + d0);
         const float w = w_s[s];
-        if (w == 0.f) continue;
-        const float4 a = *reinterpret_cast<const float4*>(acc_part + (((long)r * split + s) * ML_H + h) * ML_D + 4 * tid);
         acc.x += w * a.x; acc.y += w * a.y; acc.z += w * a.z; acc.w += w * a.w;
     }
-    const float inv = L > 0.f ? 1.f / L : 0.f;
-    const float4 o4 = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
-    if (out_f32) {
-        *reinterpret_cast<float4*>(static_cast<float*>(out) + r * o_sr + h * o_sh + 4 * tid) = o4;
-    } else {
-        uint16_t* op = static_cast<uint16_t*>(out) + r * o_sr + h * o_sh + 4 * tid;
-        *reinterpret_cast<uint2*>(op) = make_uint2((uint32_t)f32_to_bf16(o4.x) | ((uint32_t)f32_to_bf16(o4.y) << 16),
-                                                   (uint32_t)f32_to_bf16(o4.z) | ((uint32_t)f32_to_bf16(o4.w) << 16));
+    part[g][c] = acc;
+    __syncthreads();
+    if (g == 0) {
+        float4 o = part[0][c];
+#pragma unroll
+        for (int k = 1; k < MG_GRP; ++k) {
+            const float4 x = part[k][c];
+            o.x += x.x; o.y += x.y; o.z += x.z; o.w += x.w;
+        }
+        const float inv = L > 0.f ? 1.f / L : 0.f;
+        const float4 o4 = make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
+        if (out_f32) {
+            *reinterpret_cast<float4*>(static_cast<float*>(out) + r * o_sr + h * o_sh + d0) = o4;
+        } else {
+            uint16_t* op = static_cast<uint16_t*>(out) + r * o_sr + h * o_sh + d0;
+            *reinterpret_cast<uint2*>(op) = make_uint2((uint32_t)f32_to_bf16(o4.x) | ((uint32_t)f32_to_bf16(o4.y) << 16),
+                                                       (uint32_t)f32_to_bf16(o4.z) | ((uint32_t)f32_to_bf16(o4.w) << 16));
+        }
     }
-    if (tid == 0 && lse) lse[r * lse_sr + h] = L > 0.f ? M + __logf(L) : -INFINITY;
+    if (zc == 0 && tid == 0 && lse) lse[r * lse_sr + h] = L > 0.f ? M + __logf(L) : -INFINITY;
 }
 
 }  // namespace locks
@@ -594,7 +637,7 @@ extern "C" int32_t locks_mla_decode_merge(
                   "locks_mla_decode_merge: out strides must be multiples of 4 elements");
     LOCKS_REQUIRE(m_part && l_part && acc_part && page_cnt && out, "locks_mla_decode_merge: null pointer argument");
     if (n_req == 0) return 0;
-    hipLaunchKernelGGL(mla_merge_kernel, dim3(n_heads, n_req), dim3(128), 0, (hipStream_t)stream,
+    hipLaunchKernelGGL(mla_merge_kernel, dim3(n_heads, n_req, ML_D / 128), dim3(MG_BLK), 0, (hipStream_t)stream,
                        m_part, l_part, acc_part, page_cnt, pt_cols, out, (long)out_stride_req,
                        (long)out_stride_head, out_is_f32, lse, (long)lse_stride_req, split, pps_min);
     return check_launch("mla_merge_kernel");

@@ -16,7 +16,7 @@ from __future__ import annotations
 import torch
 
 from ..attention.mla_decode import mla_decode
-from ..selection.mla_select import mla_select_pages
+from ..selection.mla_select import mla_score_only, mla_select_only, mla_select_pages
 
 
 def mla_layer_index(st, kv_cache) -> int:
@@ -27,12 +27,14 @@ def mla_layer_index(st, kv_cache) -> int:
 
 
 def mla_forward_mqa(q, kv_c_and_k_pe_cache, block_table, seq_lens, st, scale: float, out=None,
-                    lse=None, layer: int | None = None):
+                    lse=None, layer: int | None = None, derive: bool = True):
     """q: (B, H, kv_lora_rank + rope_dim) bf16 (or the tuple (q_c, q_rope),
     concatenated as the reference does, mla_attn.py:100-101); the cache
     (num_blocks, page, kv_lora_rank + rope_dim) bf16; seq_lens (B,) int32
     including the current token.  Returns (o (B, H, kv_lora_rank) q.dtype,
-    lse (B, H) fp32); ``out`` / ``lse`` are written in place when given."""
+    lse (B, H) fp32); ``out`` / ``lse`` are written in place when given.
+    ``derive=False`` reuses the page parameters derived earlier in the same
+    step (they depend only on seq_lens, so one derive per step suffices)."""
     if isinstance(q, tuple):
         q = torch.cat(q, dim=-1)
     B, H, _ = q.shape
@@ -42,6 +44,10 @@ def mla_forward_mqa(q, kv_c_and_k_pe_cache, block_table, seq_lens, st, scale: fl
         out = torch.empty(B, H, st.D, dtype=q.dtype, device=q.device)
     if lse is None:
         lse = st.lse[:B, :H]
-    mla_select_pages(st, layer, q, kv_c_and_k_pe_cache, block_table, seq_lens, B, scale)
+    if derive:
+        mla_select_pages(st, layer, q, kv_c_and_k_pe_cache, block_table, seq_lens, B, scale)
+    else:
+        mla_score_only(st, layer, q, kv_c_and_k_pe_cache, block_table, B, scale)
+        mla_select_only(st, B)
     mla_decode(st, q, kv_c_and_k_pe_cache, block_table, seq_lens, B, scale, out, lse)
     return out, lse
