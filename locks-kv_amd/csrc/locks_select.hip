@@ -251,6 +251,103 @@ __device__ void finish_row(long rk, int n_pages, int n_sel_hi, int n_sink, int b
 }
 
 // ---------------------------------------------------------------------------
+// register-resident exact top-k: thread t holds keys[E] (valid flags) of
+// consecutive items; 12 + 12 + 8-bit MSD radix over an LDS histogram (4096
+// ints), then ordered emission with one packed (greater | equal << 16)
+// block scan.  Items must number < 65536.
+// ---------------------------------------------------------------------------
+struct RadixSel {
+    uint32_t prefix, kmask;
+    int k;              // keys == prefix still to take (exact mode)
+    bool whole_bin;     // every key whose masked bits >= prefix is kept
+};
+
+template <int BLK, int E>
+__device__ RadixSel reg_kth_largest(const uint32_t (&key)[E], const bool (&val)[E], int k,
+                                    int* hist, int* wtot, int* s3) {
+    constexpr int NW = BLK / kWave;
+    constexpr int BPL = 4096 / BLK;                     // histogram bins per lane
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    RadixSel rs{0u, 0u, k, false};
+#pragma unroll 1
+    for (int pass = 0; pass < 3; ++pass) {
+        const int shift = pass == 0 ? 20 : pass == 1 ? 8 : 0;
+        const int nb = pass < 2 ? 4096 : 256;
+        for (int i = tid; i < nb; i += BLK) hist[i] = 0;
+        __syncthreads();
+#pragma unroll
+        for (int e = 0; e < E; ++e)
+            hist_add(hist, (int)((key[e] >> shift) & (uint32_t)(nb - 1)),
+                     val[e] && (key[e] & rs.kmask) == rs.prefix);
+        __syncthreads();
+        // thread t: bins top .. top-BPL+1, top = nb-1-BPL*t (ascending thread
+        // order = descending bin order)
+        const int top = nb - 1 - BPL * tid;
+        int c = 0;
+#pragma unroll
+        for (int j = 0; j < BPL; ++j) c += (top - j >= 0) ? hist[top - j] : 0;
+        int incl = c;
+#pragma unroll
+        for (int o = 1; o < kWave; o <<= 1) {
+            const int t = __shfl_up(incl, o, kWave);
+            if (lane >= o) incl += t;
+        }
+        if (lane == kWave - 1) wtot[wave] = incl;
+        __syncthreads();
+        int base = 0;
+        for (int w = 0; w < wave && w < NW; ++w) base += wtot[w];
+        const int above0 = base + incl - c;
+        if (c > 0 && above0 < rs.k && rs.k <= base + incl) {
+            int above = above0;
+#pragma unroll
+            for (int j = 0; j < BPL; ++j) {
+                const int cb = (top - j >= 0) ? hist[top - j] : 0;
+                if (above + cb >= rs.k) { s3[0] = top - j; s3[1] = rs.k - above; s3[2] = cb; break; }
+                above += cb;
+            }
+        }
+        __syncthreads();
+        rs.prefix |= ((uint32_t)s3[0]) << shift;
+        rs.kmask |= ((uint32_t)(nb - 1)) << shift;
+        const int cb = s3[2];
+        rs.k = s3[1];
+        if (rs.k == cb) { rs.whole_bin = true; break; }
+    }
+    return rs;
+}
+
+// Emission in item order: out(pos, e) is called for every kept item of
+// this thread with its rank among all kept items.  Returns the kept count.
+template <int BLK, int E, class Out>
+__device__ int reg_emit(const uint32_t (&key)[E], const bool (&val)[E], const RadixSel& rs,
+                        int* wsum, Out out) {
+    int gt = 0, eq = 0;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        if (!val[e]) continue;
+        if (rs.whole_bin) gt += (key[e] & rs.kmask) >= rs.prefix;
+        else { gt += key[e] > rs.prefix; eq += key[e] == rs.prefix; }
+    }
+    int tot;
+    const int ex = block_excl_scan<BLK>(gt | (eq << 16), wsum, tot);
+    const int quota = rs.whole_bin ? 0 : rs.k;
+    int pos = (ex & 0xFFFF) + min(ex >> 16, quota);
+    int er = ex >> 16;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        if (!val[e]) continue;
+        bool kp;
+        if (rs.whole_bin) kp = (key[e] & rs.kmask) >= rs.prefix;
+        else {
+            kp = key[e] > rs.prefix;
+            if (key[e] == rs.prefix) { kp = er < quota; ++er; }
+        }
+        if (kp) out(pos++, e);
+    }
+    return (tot & 0xFFFF) + min(tot >> 16, quota);
+}
+
+// ---------------------------------------------------------------------------
 // whole-row kernel (max_pages <= ROW_MAXP): one 1024-thread workgroup per
 // (request, kv head) does combine, exact top-b and the page table in one
 // launch.  Thread t owns pages [E t, E t + E) (contiguous, so one packed
@@ -365,77 +462,8 @@ __global__ __launch_bounds__(ROW_BLK) void sel_row_kernel(
         val[e] = (p >= n_sink) && (p < n_sel_hi);
         key[e] = f2u(acc[e]);
     }
-    uint32_t prefix = 0u, kmask = 0u;
-    int k = b;
-    bool whole_bin = false;
-#pragma unroll 1
-    for (int pass = 0; pass < 3; ++pass) {
-        const int shift = pass == 0 ? 20 : pass == 1 ? 8 : 0;
-        const int nb = pass < 2 ? 4096 : 256;
-        for (int i = tid; i < nb; i += ROW_BLK) hist[i] = 0;
-        __syncthreads();
-#pragma unroll
-        for (int e = 0; e < E; ++e)
-            hist_add(hist, (int)((key[e] >> shift) & (uint32_t)(nb - 1)), val[e] && (key[e] & kmask) == prefix);
-        __syncthreads();
-        // wave w, lane l: bins top, top-1, top-2, top-3 with top = nb-1-256w-4l
-        // (ascending lane order = descending bin order)
-        const int top = nb - 1 - 256 * wave - 4 * lane;
-        int c = 0;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) c += (top - j >= 0) ? hist[top - j] : 0;
-        int incl = c;
-#pragma unroll
-        for (int o = 1; o < kWave; o <<= 1) {
-            const int t = __shfl_up(incl, o, kWave);
-            if (lane >= o) incl += t;
-        }
-        if (lane == kWave - 1) wtot[wave] = incl;
-        __syncthreads();
-        int base = 0;
-        for (int w = 0; w < wave; ++w) base += wtot[w];
-        const int above0 = base + incl - c;
-        if (c > 0 && above0 < k && k <= base + incl) {
-            int above = above0;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int cb = hist[top - j];
-                if (above + cb >= k) { s3[0] = top - j; s3[1] = k - above; s3[2] = cb; break; }
-                above += cb;
-            }
-        }
-        __syncthreads();
-        prefix |= ((uint32_t)s3[0]) << shift;
-        kmask |= ((uint32_t)(nb - 1)) << shift;
-        const int cb = s3[2];
-        k = s3[1];
-        if (k == cb) { whole_bin = true; break; }     // every key of the bin is kept
-    }
-
-    // ---- ordered emission: one packed (greater, equal) block scan --------
-    int gt = 0, eq = 0;
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-        if (!val[e]) continue;
-        if (whole_bin) gt += (key[e] & kmask) >= prefix;    // == prefix bin or above
-        else { gt += key[e] > prefix; eq += key[e] == prefix; }
-    }
-    int tot;
-    const int ex = block_excl_scan<ROW_BLK>(gt | (eq << 16), wsum, tot);
-    const int quota = whole_bin ? 0 : k;
-    int pos = (ex & 0xFFFF) + min(ex >> 16, quota);
-    int er = ex >> 16;
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-        if (!val[e]) continue;
-        bool kp;
-        if (whole_bin) kp = (key[e] & kmask) >= prefix;
-        else {
-            kp = key[e] > prefix;
-            if (key[e] == prefix) { kp = er < quota; ++er; }
-        }
-        if (kp) trow[n_sink + pos++] = p0 + e;
-    }
+    const RadixSel rs = reg_kth_largest<ROW_BLK, E>(key, val, b, hist, wtot, s3);
+    reg_emit<ROW_BLK, E>(key, val, rs, wsum, [&](int pos, int e) { trow[n_sink + pos] = p0 + e; });
     const int cnt = n_sink + b + (n_pages - n_sel_hi);
     if (p0 >= cnt && p0 + E <= MP) {                      // padding only
 #pragma unroll
@@ -612,6 +640,182 @@ __global__ __launch_bounds__(FIN_BLK) void sel_finish_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// page-parallel route with register-resident keys (rows > ROW_MAXP pages):
+// sel_chunk2_kernel: one 512-thread workgroup per 2048-page chunk, 4 pages
+// per thread; sel_finish2_kernel: one 1024-thread workgroup per row holds up
+// to 4096 candidates (4 per thread) in registers.
+// ---------------------------------------------------------------------------
+constexpr int C2_BLK = 512;
+constexpr int C2_E = SEL_CH / C2_BLK;                  // 4
+constexpr int F2_BLK = 1024;
+constexpr int F2_E = 4;
+constexpr int F2_CAP = F2_BLK * F2_E;                  // 4096 candidates
+
+__global__ __launch_bounds__(C2_BLK) void sel_chunk2_kernel(
+    const float* __restrict__ score_h, const float* __restrict__ pmax, int Zs,
+    const int* __restrict__ npg, const int* __restrict__ nsh, const int* __restrict__ bfix,
+    float* __restrict__ score, int* __restrict__ page_table,
+    uint32_t* __restrict__ cand_key, int* __restrict__ cand_page, int* __restrict__ cand_cnt,
+    int n_sink, int MP, int G, int combine)
+{
+    const int z = blockIdx.x, kh = blockIdx.y, r = blockIdx.z;
+    const int n_kv = gridDim.y, Z1 = gridDim.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const long rk = (long)r * n_kv + kh;
+    const int n_sel_hi = min(nsh[r], MP);
+    const int c0 = z * SEL_CH;
+    const int p0 = c0 + C2_E * tid;                     // this thread's 4 pages
+
+    __shared__ float hm[16];
+    __shared__ int hist[4096];
+    __shared__ int wtot[C2_BLK / kWave];
+    __shared__ int s3[4];
+    __shared__ int wsum[C2_BLK / kWave + 1];
+
+    // score_h of every head in flight first (row-bounded, no parameter wait)
+    const float* shb = score_h + rk * (long)G * MP;
+    float4 xv[16];
+#pragma unroll
+    for (int g = 0; g < 16; ++g)
+        xv[g] = (g < G && p0 + 3 < MP) ? *reinterpret_cast<const float4*>(shb + (long)g * MP + p0)
+                                       : make_float4(0.f, 0.f, 0.f, 0.f);
+    int* trow = page_table + rk * (long)MP;
+#pragma unroll
+    for (int e = 0; e < C2_E; ++e)
+        if (p0 + e < MP) trow[p0 + e] = -1;
+    if (combine == 0) {
+        for (int g = wave; g < G; g += C2_BLK / kWave) {
+            const float m = wave_max(chunk_max(pmax + rk * Zs * 16 + g, Zs));
+            if (lane == 0) hm[g] = m;
+        }
+        __syncthreads();
+    }
+    float acc[C2_E];
+#pragma unroll
+    for (int e = 0; e < C2_E; ++e) acc[e] = (combine == 0) ? 0.f : -INFINITY;
+#pragma unroll
+    for (int g = 0; g < 16; ++g) {
+        if (g < G) {
+            const float x4[4] = {xv[g].x, xv[g].y, xv[g].z, xv[g].w};
+#pragma unroll
+            for (int e = 0; e < C2_E; ++e) {
+                if (combine == 0) acc[e] += __expf(x4[e] - hm[g]);
+                else acc[e] = (g == 0) ? x4[e] : fmaxf(acc[e], x4[e]);
+            }
+        }
+    }
+    const int pend = max(n_sel_hi, 0);
+    float* srow = score + rk * (long)MP;
+    if (p0 + C2_E <= pend) {
+        *reinterpret_cast<float4*>(srow + p0) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    } else {
+#pragma unroll
+        for (int e = 0; e < C2_E; ++e)
+            if (p0 + e < pend) srow[p0 + e] = acc[e];
+    }
+    const int n_sel = n_sel_hi - n_sink;
+    int b = bfix[r];
+    b = max(1, min(b, max(n_sel, 1)));
+    uint32_t key[C2_E];
+    bool val[C2_E];
+    int nv = 0;
+#pragma unroll
+    for (int e = 0; e < C2_E; ++e) {
+        const int p = p0 + e;
+        val[e] = (n_sel > 1) && p >= n_sink && p < n_sel_hi;
+        key[e] = f2u(acc[e]);
+        nv += val[e];
+    }
+    int n_loc;
+    block_excl_scan<C2_BLK>(nv, wsum, n_loc);
+    uint32_t* ck = cand_key + (rk * Z1 + z) * (long)SEL_CH;
+    int* cp = cand_page + (rk * Z1 + z) * (long)SEL_CH;
+    int ncand = 0;
+    if (n_loc > 0) {
+        const int k_loc = min(b, n_loc);
+        RadixSel rs{0u, 0u, 0, true};                    // k_loc == n_loc: keep every valid key
+        if (k_loc < n_loc) rs = reg_kth_largest<C2_BLK, C2_E>(key, val, k_loc, hist, wtot, s3);
+        ncand = reg_emit<C2_BLK, C2_E>(key, val, rs, wsum, [&](int pos, int e) {
+            ck[pos] = key[e];
+            cp[pos] = p0 + e;
+        });
+    }
+    if (tid == 0) cand_cnt[rk * Z1 + z] = ncand;
+}
+
+__global__ __launch_bounds__(F2_BLK) void sel_finish2_kernel(
+    const int* __restrict__ npg, const int* __restrict__ nsh, const int* __restrict__ bfix,
+    int* __restrict__ page_table, int* __restrict__ page_cnt,
+    const uint32_t* __restrict__ cand_key, const int* __restrict__ cand_page,
+    const int* __restrict__ cand_cnt, uint32_t* __restrict__ spill_key, int* __restrict__ spill_page,
+    int n_sink, int MP, int Z1)
+{
+    const int kh = blockIdx.y, r = blockIdx.z;
+    const long rk = (long)r * gridDim.y + kh;
+    const int tid = threadIdx.x;
+    const int n_pages = min(npg[r], MP);
+    const int n_sel_hi = min(nsh[r], MP);
+    const int n_sel = n_sel_hi - n_sink;
+    int b = bfix[r];
+    b = max(1, min(b, max(n_sel, 1)));
+    int* trow = page_table + rk * (long)MP;
+    if (n_sel <= 1 || b >= n_sel) {
+        for (int i = tid; i < max(n_pages, 0); i += F2_BLK) trow[i] = i;
+        if (tid == 0) page_cnt[rk] = max(n_pages, 0);
+        return;
+    }
+    __shared__ int offs[FIN_MAXZ + 1];
+    __shared__ int hist[4096];
+    __shared__ int wtot[F2_BLK / kWave];
+    __shared__ int s3[4];
+    __shared__ int wsum[F2_BLK / kWave + 1];
+    {
+        const int c = (tid < Z1) ? cand_cnt[rk * Z1 + tid] : 0;
+        int tot;
+        const int ex = block_excl_scan<F2_BLK>(c, wsum, tot);
+        if (tid < Z1) offs[tid] = ex;
+        if (tid == 0) offs[Z1] = tot;
+        __syncthreads();
+    }
+    const int N = offs[Z1];
+    if (N > F2_CAP) {                                   // many / large candidate lists
+        __shared__ uint32_t lkey[FIN_CAP];
+        __shared__ int lpage[FIN_CAP];
+        finish_row<F2_BLK>(rk, n_pages, n_sel_hi, n_sink, b, MP, Z1, trow, page_cnt + rk, cand_key,
+                           cand_page, cand_cnt, spill_key, spill_page, offs, lkey, lpage, hist, s3,
+                           wsum);
+        return;
+    }
+    // candidates j = 4 t .. 4 t + 3 of the chunk-ordered (= page-ordered) list
+    uint32_t key[F2_E];
+    int page[F2_E];
+    bool val[F2_E];
+#pragma unroll
+    for (int e = 0; e < F2_E; ++e) {
+        const int j = F2_E * tid + e;
+        val[e] = j < N;
+        key[e] = 0u;
+        page[e] = 0;
+        if (val[e]) {
+            int lo = 0, hi = Z1;                            // offs[lo] <= j < offs[hi]
+            while (hi - lo > 1) {
+                const int mid = (lo + hi) >> 1;
+                if (offs[mid] <= j) lo = mid; else hi = mid;
+            }
+            const long src = (rk * Z1 + lo) * (long)SEL_CH + (j - offs[lo]);
+            key[e] = cand_key[src];
+            page[e] = cand_page[src];
+        }
+    }
+    const RadixSel rs = reg_kth_largest<F2_BLK, F2_E>(key, val, b, hist, wtot, s3);
+    reg_emit<F2_BLK, F2_E>(key, val, rs, wsum, [&](int pos, int e) { trow[n_sink + pos] = page[e]; });
+    const int cnt = n_sink + b + (n_pages - n_sel_hi);
+    for (int i = tid; i < n_sink; i += F2_BLK) trow[i] = i;
+    for (int i = n_sink + b + tid; i < cnt; i += F2_BLK) trow[i] = n_sel_hi + (i - n_sink - b);
+    if (tid == 0) page_cnt[rk] = cnt;
+}
+
+// ---------------------------------------------------------------------------
 // derive (select.py:28-58)
 // ---------------------------------------------------------------------------
 __global__ void derive_kernel(const int* __restrict__ seq_lens, int n_req, int page, int window,
@@ -692,6 +896,17 @@ extern "C" int32_t locks_select_nrm_topb(
         else ROW_LAUNCH(16);
 #undef ROW_LAUNCH
         return check_launch("sel_row_kernel");
+    }
+    if (Z1 > 1 && max_pages % 4 == 0) {
+        hipLaunchKernelGGL(sel_chunk2_kernel, dim3(Z1, n_kv, n_req), dim3(C2_BLK), 0, st,
+                           score_h, page_max, score_chunks, n_pages, n_sel_hi, b_fix, score,
+                           page_table, cand_key, cand_page, cand_cnt, n_sink, max_pages, G, combine);
+        int rc = check_launch("sel_chunk2_kernel");
+        if (rc) return rc;
+        hipLaunchKernelGGL(sel_finish2_kernel, dim3(1, n_kv, n_req), dim3(F2_BLK), 0, st,
+                           n_pages, n_sel_hi, b_fix, page_table, page_cnt, cand_key, cand_page,
+                           cand_cnt, spill_key, spill_page, n_sink, max_pages, Z1);
+        return check_launch("sel_finish2_kernel");
     }
     hipLaunchKernelGGL(sel_chunk_kernel, dim3(Z1, n_kv, n_req), dim3(SEL_BLK), 0, st,
                        score_h, page_max, score_chunks, n_pages, n_sel_hi, b_fix, score,

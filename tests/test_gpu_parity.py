@@ -131,6 +131,7 @@ def _random_select_inputs(seed, n_kv, G, seq_lens, MP, st, ties=None):
     ([1 << 20], 2, 16, 126),         # 1M context, 32 chunks
     ([262144, 196608, 131072, 65536], 2, 16, 126),   # ragged batch
     ([100000], 2, 4, 5000),          # large b (spills past the LDS cap)
+    ([400000], 2, 4, 5000),          # register chunks, finish over > 4096 candidates (spill)
     ([40, 17, 0, 33], 2, 4, 126),    # short rows, padded row, keep-all
 ])
 def test_select_matches_oracle(combine, seq_lens, n_kv, G, bp):
