@@ -37,16 +37,20 @@ constexpr int ML_WAVES = 4;
 constexpr int ML_BLK = ML_WAVES * kWave;
 constexpr int ML_VROW = ML_RNK * ML_D / 2;   // 2048 B packed V per page
 constexpr int ML_MAX_CHUNK = 1024;
-// per-wave LDS stage of one unit (2 pages)
-constexpr int MS_V = 0;                      // 2 x 2048 packed V
-constexpr int MS_MU = 4096;                  // 2 x 512 centroid
-constexpr int MS_C8 = 5120;                  // 2 x 128 coefficients
-constexpr int MS_CS = 5376;                  // 2 x 32 token scales
-constexpr int MS_VS = 5440;                  // 2 x 16 column scales
-constexpr int MS_MUS = 5472;                 // 2 dwords: centroid scales (bf16 in the low half)
-constexpr int MS_RP = 5504;                  // 2 x 16 x 128 B RoPE keys
-constexpr int MS_MD = 9600;                  // 2 x 16 fp32 centroid terms
-constexpr int MS_BYTES = 9728;
+// per-wave LDS stage of one unit (2 pages).  V rows (256 B) and RoPE token
+// rows (128 B) are padded by 16 B so that the MFMA-order reads of 16 rows at
+// once hit distinct banks.
+constexpr int MS_VROWB = 272;                // padded (page, column) V row
+constexpr int MS_RROWB = 144;                // padded (page, token) RoPE row
+constexpr int MS_V = 0;                      // 2 x 8 x 272 packed V
+constexpr int MS_MU = 16 * MS_VROWB;         // 2 x 512 centroid
+constexpr int MS_C8 = MS_MU + 1024;          // 2 x 128 coefficients
+constexpr int MS_CS = MS_C8 + 256;           // 2 x 32 token scales
+constexpr int MS_VS = MS_CS + 64;            // 2 x 16 column scales
+constexpr int MS_MUS = MS_VS + 32;           // 2 dwords: centroid scales (bf16 in the low half)
+constexpr int MS_RP = MS_MUS + 16;           // 2 x 16 x 144 B RoPE keys
+constexpr int MS_MD = MS_RP + 32 * MS_RROWB; // 2 x 16 fp32 centroid terms
+constexpr int MS_BYTES = MS_MD + 128;
 
 __device__ __forceinline__ v4i perm_even_odd(const uint4 n) {
     // 16 int8 in d order -> even d of the window first, then odd d (the
@@ -165,10 +169,12 @@ __global__ __launch_bounds__(ML_BLK) void mla_score_kernel(
         fr0 = rload(lane); fr1 = rload(lane + 64); fr2 = rload(lane + 128); fr3 = rload(lane + 192);
     };
     auto store_unit = [&](uint8_t* st) {
-        *reinterpret_cast<uint4*>(st + MS_V + lane * 16) = fv0;
-        *reinterpret_cast<uint4*>(st + MS_V + (lane + 64) * 16) = fv1;
-        *reinterpret_cast<uint4*>(st + MS_V + (lane + 128) * 16) = fv2;
-        *reinterpret_cast<uint4*>(st + MS_V + (lane + 192) * 16) = fv3;
+        // V chunk i: page i >> 7, column (i >> 4) & 7, 16-byte part i & 15
+        auto vofs = [&](int i) { return MS_V + ((i >> 7) * 8 + ((i >> 4) & 7)) * MS_VROWB + (i & 15) * 16; };
+        *reinterpret_cast<uint4*>(st + vofs(lane)) = fv0;
+        *reinterpret_cast<uint4*>(st + vofs(lane + 64)) = fv1;
+        *reinterpret_cast<uint4*>(st + vofs(lane + 128)) = fv2;
+        *reinterpret_cast<uint4*>(st + vofs(lane + 192)) = fv3;
         *reinterpret_cast<uint4*>(st + MS_MU + lane * 16) = fmu;
         if (lane < 16) *reinterpret_cast<uint4*>(st + MS_C8 + lane * 16) = fc8;
         if (lane < 4) *reinterpret_cast<uint4*>(st + MS_CS + lane * 16) = fcs;
@@ -176,10 +182,12 @@ __global__ __launch_bounds__(ML_BLK) void mla_score_kernel(
             *reinterpret_cast<uint4*>(st + MS_VS + lane * 16) = fvs;
             *reinterpret_cast<uint32_t*>(st + MS_MUS + lane * 4) = fmus;
         }
-        *reinterpret_cast<uint4*>(st + MS_RP + lane * 16) = fr0;
-        *reinterpret_cast<uint4*>(st + MS_RP + (lane + 64) * 16) = fr1;
-        *reinterpret_cast<uint4*>(st + MS_RP + (lane + 128) * 16) = fr2;
-        *reinterpret_cast<uint4*>(st + MS_RP + (lane + 192) * 16) = fr3;
+        // RoPE chunk i: (page, token) row i >> 3, 16-byte part i & 7
+        auto rofs = [&](int i) { return MS_RP + (i >> 3) * MS_RROWB + (i & 7) * 16; };
+        *reinterpret_cast<uint4*>(st + rofs(lane)) = fr0;
+        *reinterpret_cast<uint4*>(st + rofs(lane + 64)) = fr1;
+        *reinterpret_cast<uint4*>(st + rofs(lane + 128)) = fr2;
+        *reinterpret_cast<uint4*>(st + rofs(lane + 192)) = fr3;
     };
 
     uint8_t* st = stage_l[wave];
@@ -198,7 +206,7 @@ __global__ __launch_bounds__(ML_BLK) void mla_score_kernel(
         v4i acc = {0, 0, 0, 0}, accm = {0, 0, 0, 0};
 #pragma unroll
         for (int k4 = 0; k4 < 4; ++k4) {
-            const uint4 w = *reinterpret_cast<const uint4*>(st + MS_V + i_pg * ML_VROW + i_c * (ML_D / 2) + k4 * 64 + kg * 16);
+            const uint4 w = *reinterpret_cast<const uint4*>(st + MS_V + (i_pg * 8 + i_c) * MS_VROWB + k4 * 64 + kg * 16);
             const v4i a0 = {(int)((w.x << 4) & MH), (int)((w.y << 4) & MH), (int)(w.x & MH), (int)(w.y & MH)};
             const v4i a1 = {(int)((w.z << 4) & MH), (int)((w.w << 4) & MH), (int)(w.z & MH), (int)(w.w & MH)};
             acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, Bq[k4][0], acc, 0, 0, 0);
@@ -249,7 +257,7 @@ __global__ __launch_bounds__(ML_BLK) void mla_score_kernel(
 #pragma unroll
             for (int s = 0; s < 2; ++s) {
                 const v8bf a = __builtin_bit_cast(v8bf, *reinterpret_cast<const uint4*>(
-                    st + MS_RP + (pg * 16 + r16) * 128 + (32 * s + 8 * kg) * 2));
+                    st + MS_RP + (pg * 16 + r16) * MS_RROWB + (32 * s + 8 * kg) * 2));
                 rp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, Br[s], rp, 0, 0, 0);
             }
             const uint2 csw = *reinterpret_cast<const uint2*>(st + MS_CS + pg * 32 + kg * 8);
@@ -277,8 +285,8 @@ __global__ __launch_bounds__(ML_BLK) void mla_score_kernel(
 // the 512-d output for O^T += V^T P^T.  All stage and partial accesses are
 // inline-asm LDS ops: the compiler cannot tell them from the DMA in flight
 // and would otherwise wait for it before every access.
-constexpr int MD_PAGE_B = ML_PG * ML_HS * 2;          // 18432 B
-constexpr int MD_CHUNKS = MD_PAGE_B / 16;             // 1152 16-byte DMA chunks
+constexpr int MD_ROWB = ML_HS * 2 + 16;               // padded token row (1168 B)
+constexpr int MD_PAGE_B = ML_PG * MD_ROWB;            // 18688 B per stage
 constexpr int MD_IDS = 256;                           // page ids staged per batch
 constexpr int MD_MAX_SPLIT = 512;
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
@@ -346,17 +354,19 @@ __global__ __launch_bounds__(ML_BLK) void mla_decode_split_kernel(
 
     const uint32_t st0 = lds_addr(&stg[0][0]);
     const uint32_t sp_base = lds_addr(&spart[0][0]);
+    // DMA of one page: wave w fills token rows 4w .. 4w+3, each row as one
+    // 64-chunk and one 8-chunk instruction (rows are padded in LDS, so an
+    // instruction never crosses a row)
     auto issue = [&](int slot, int blk) {
         const uint16_t* base = cache + (long)blk * c_sb;
 #pragma unroll
-        for (int mm = 0; mm < 5; ++mm) {
-            const int i0 = 256 * mm + 64 * wave;             // first chunk of this wave's instruction
-            if (i0 < MD_CHUNKS) {
-                const int i = i0 + lane;
-                const int t = i / 72, part = i % 72;
-                __builtin_amdgcn_global_load_lds(base + (long)t * c_st + 8 * part,
-                                                 (lds_ptr_t)(&stg[slot][16 * i0]), 16, 0, 0);
-            }
+        for (int q4 = 0; q4 < 4; ++q4) {
+            const int t = 4 * wave + q4;
+            const uint16_t* row = base + (long)t * c_st;
+            __builtin_amdgcn_global_load_lds(row + 8 * lane, (lds_ptr_t)(&stg[slot][t * MD_ROWB]), 16, 0, 0);
+            if (lane < 8)
+                __builtin_amdgcn_global_load_lds(row + 8 * (64 + lane), (lds_ptr_t)(&stg[slot][t * MD_ROWB + 1024]),
+                                                 16, 0, 0);
         }
     };
 
@@ -383,7 +393,7 @@ __global__ __launch_bounds__(ML_BLK) void mla_decode_split_kernel(
             v4i ka[5];
 #pragma unroll
             for (int k = 0; k < 5; ++k)
-                if (k < s_n) ka[k] = ds_read16(sb + r16 * (ML_HS * 2) + (32 * (s_lo + k) + 8 * kg) * 2);
+                if (k < s_n) ka[k] = ds_read16(sb + r16 * MD_ROWB + (32 * (s_lo + k) + 8 * kg) * 2);
             lgkm_wait(ka[0], ka[1], ka[2], ka[3], ka[4]);
 #pragma unroll
             for (int k = 0; k < 5; ++k)
@@ -419,7 +429,7 @@ __global__ __launch_bounds__(ML_BLK) void mla_decode_split_kernel(
             v4i vi[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                vi[j] = ds_read16(sb + (4 * kg + j) * (ML_HS * 2) + (128 * wave + 8 * r16) * 2);
+                vi[j] = ds_read16(sb + (4 * kg + j) * MD_ROWB + (128 * wave + 8 * r16) * 2);
             lgkm_wait(vi[0], vi[1], vi[2], vi[3]);
             uint4 vr[4];
 #pragma unroll

@@ -41,14 +41,20 @@ constexpr int SC_VROW = SC_RNK * SC_D / 2;   // 512 B of packed V per row
 constexpr int SC_MAX_CHUNK = 1024;          // pages per workgroup, upper bound
 constexpr int SC_MAXKV = 16;                // kv heads per request
 constexpr int SC_MAXHQ = 128;               // query heads per request (n_kv * G)
-// per-wave LDS staging of one (tile, kv head) unit, filled by LDS DMA
-constexpr int ST_V = 0;                     // 8 pages x 512 B packed V  (-> qt after use)
-constexpr int ST_C8 = 4096;                 // 8 pages x 128 B coefficients
-constexpr int ST_MU = 5120;                 // 8 pages x 128 B centroid  (-> mud after use)
-constexpr int ST_CS = 6144;                 // 8 pages x 32 B token scales
-constexpr int ST_VS = 6400;                 // 8 pages x 16 B column scales
-constexpr int ST_MUS = 6528;                // 8 dwords: the pages' centroid scales (bf16 in the low half)
-constexpr int ST_BYTES = 6560;
+// per-wave LDS stage of one (tile, kv head) unit.  Rows are padded (V: 80 B
+// per 64-B basis row, mu: 144 B per 128-B row) so the MFMA-order reads of 16
+// rows at once hit distinct banks.
+constexpr int ST_VROWB = 80;                 // padded stride of one (page, column) V row
+constexpr int ST_VPAIR = 16 * ST_VROWB;      // 2 pages x 8 columns
+constexpr int ST_MUROWB = 144;               // padded stride of one page's mu row
+constexpr int ST_V = 0;                      // 4 pairs x 1280 B packed V
+constexpr int ST_C8 = 4 * ST_VPAIR;          // 8 pages x 128 B coefficients
+constexpr int ST_MU = ST_C8 + 1024;          // 8 pages x 144 B centroid (-> mud after use)
+constexpr int ST_CS = ST_MU + 8 * ST_MUROWB; // 8 pages x 32 B token scales
+constexpr int ST_VS = ST_CS + 256;           // 8 pages x 16 B column scales
+constexpr int ST_MUS = ST_VS + 128;          // 8 dwords: centroid scales (bf16 in the low half)
+constexpr int ST_BYTES = ST_MUS + 32;
+constexpr int SC_QROW = SC_D + 16;           // padded int8 q row (bank-conflict free reads)
 
 __device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d) {
     return (uint32_t)(uint8_t)a | ((uint32_t)(uint8_t)b << 8) |
@@ -86,8 +92,8 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
     __shared__ uint32_t wmax[SC_MAXKV][16];
     // dynamic LDS: int8 q rows of every head (+16 zero rows), chunk block ids
     extern __shared__ __attribute__((aligned(16))) uint8_t dyn_l[];
-    int8_t (*q8s)[SC_D] = reinterpret_cast<int8_t (*)[SC_D]>(dyn_l);
-    int* bt_l = reinterpret_cast<int*>(dyn_l + (size_t)(HQ + 16) * SC_D);
+    int8_t (*q8s)[SC_QROW] = reinterpret_cast<int8_t (*)[SC_QROW]>(dyn_l);
+    int* bt_l = reinterpret_cast<int*>(dyn_l + (size_t)(HQ + 16) * SC_QROW);
 
     // ---- prologue: q rows and block ids are fetched together; the first
     // unit's summary loads are issued before q is quantized, so the
@@ -108,7 +114,7 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
         wmax[i / 16][i % 16] = 0x007FFFFFu;                    // f2u(-inf)
         qsp[i / 16][i % 16] = 0.f;
     }
-    for (int i = tid; i < 16 * SC_D / 4; i += SC_BLOCK)
+    for (int i = tid; i < 16 * SC_QROW / 4; i += SC_BLOCK)
         reinterpret_cast<int*>(&q8s[HQ][0])[i] = 0;            // zero rows after the last head
     __syncthreads();
 
@@ -155,12 +161,14 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
         }
     };
     auto store_unit = [&](uint8_t* stg) {
-        *reinterpret_cast<uint4*>(stg + ST_V + 0 * 1024 + lane * 16) = fv0;
-        *reinterpret_cast<uint4*>(stg + ST_V + 1 * 1024 + lane * 16) = fv1;
-        *reinterpret_cast<uint4*>(stg + ST_V + 2 * 1024 + lane * 16) = fv2;
-        *reinterpret_cast<uint4*>(stg + ST_V + 3 * 1024 + lane * 16) = fv3;
+        // natural lane L of a pair: page L >> 5, column (L >> 2) & 7, chunk L & 3
+        const int vofs = ((lane >> 5) * 8 + ((lane >> 2) & 7)) * ST_VROWB + (lane & 3) * 16;
+        *reinterpret_cast<uint4*>(stg + ST_V + 0 * ST_VPAIR + vofs) = fv0;
+        *reinterpret_cast<uint4*>(stg + ST_V + 1 * ST_VPAIR + vofs) = fv1;
+        *reinterpret_cast<uint4*>(stg + ST_V + 2 * ST_VPAIR + vofs) = fv2;
+        *reinterpret_cast<uint4*>(stg + ST_V + 3 * ST_VPAIR + vofs) = fv3;
         *reinterpret_cast<uint4*>(stg + ST_C8 + lane * 16) = fc8;
-        *reinterpret_cast<uint4*>(stg + ST_MU + lane * 16) = fmu;
+        *reinterpret_cast<uint4*>(stg + ST_MU + (lane >> 3) * ST_MUROWB + (lane & 7) * 16) = fmu;
         if (lane < 16) *reinterpret_cast<uint4*>(stg + ST_CS + lane * 16) = fcs;
         if (lane < 8) {
             *reinterpret_cast<uint4*>(stg + ST_VS + lane * 16) = fvs;
@@ -231,7 +239,7 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
         uint32_t vsw[4][2];
 #pragma unroll
         for (int pp = 0; pp < 4; ++pp) {
-            vv[pp] = *reinterpret_cast<const uint4*>(stg + ST_V + pp * 1024 + i_pg * 512 + i_c * 64 + kg * 16);
+            vv[pp] = *reinterpret_cast<const uint4*>(stg + ST_V + pp * ST_VPAIR + (i_pg * 8 + i_c) * ST_VROWB + kg * 16);
 #pragma unroll
             for (int pg = 0; pg < 2; ++pg)          // column scales (2kg, 2kg+1) of page 2pp+pg
                 vsw[pp][pg] = *reinterpret_cast<const uint32_t*>(stg + ST_VS + (2 * pp + pg) * 16 + kg * 4);
@@ -240,8 +248,8 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
         float musf = 0.f;
         if ((lane & 15) < 8) {
             const int pg = lane & 15;
-            mu0 = *reinterpret_cast<const v4i*>(stg + ST_MU + pg * 128 + kg * 32);
-            mu1 = *reinterpret_cast<const v4i*>(stg + ST_MU + pg * 128 + kg * 32 + 16);
+            mu0 = *reinterpret_cast<const v4i*>(stg + ST_MU + pg * ST_MUROWB + kg * 32);
+            mu1 = *reinterpret_cast<const v4i*>(stg + ST_MU + pg * ST_MUROWB + kg * 32 + 16);
             musf = bf16lo(*reinterpret_cast<const uint32_t*>(stg + ST_MUS + pg * 4));
         }
         wave_lds_sync();                               // mu consumed: reuse as mud
@@ -402,7 +410,7 @@ extern "C" int32_t locks_score_rki4(
     if (n_req == 0) return 0;
     const int Z = cdiv(max_pages, chunk);
     dim3 grid(Z, n_req);
-    const size_t dyn = (size_t)(n_kv * G + 16) * SC_D + (size_t)chunk * sizeof(int);
+    const size_t dyn = (size_t)(n_kv * G + 16) * SC_QROW + (size_t)chunk * sizeof(int);
     hipStream_t st = (hipStream_t)stream;
 #define LAUNCH(GWV)                                                                    \
     hipLaunchKernelGGL((rki4_score_kernel<GWV>), grid, dim3(SC_BLOCK), dyn, st, q, \
