@@ -45,22 +45,49 @@ __device__ __forceinline__ uint32_t bf16_word(const uint4& w, int e) {
 }
 
 // Merge the first n_act split partials of row rk into out (one workgroup,
-// DC_BLK threads).  scratch: >= MAX_SPLIT * 16 floats of LDS.
+// DC_BLK threads).  w_s: >= 2 * MAX_SPLIT * 16 floats of LDS.
 __device__ void merge_row(const float* __restrict__ m_part, const float* __restrict__ l_part,
                           const float* __restrict__ acc_part, long rk, int r, int kh, int n_act,
                           int G, int split, void* __restrict__ out, long o_sr, long o_sh,
                           int out_f32, float* w_s, float* lt_s) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     constexpr int NWV = DC_BLK / kWave;
+    constexpr int PF = 8;                               // splits of acc prefetched per item
+    // the first PF split partials of this thread's (head, 4-dim) items are
+    // loaded before anything waits (they do not depend on the weights)
+    float4 pre[2][PF];
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+        const int i = tid + it * DC_BLK;
+        const int g = i / (DC_D / 4), d4 = (i % (DC_D / 4)) * 4;
+        const float* ap = acc_part + (rk * split * G + g) * DC_D + d4;
+#pragma unroll
+        for (int k = 0; k < PF; ++k)
+            pre[it][k] = (i < G * (DC_D / 4) && k < split)
+                             ? *reinterpret_cast<const float4*>(ap + (long)k * G * DC_D)
+                             : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    // every (split, head) m and l in one pass (all loads in flight), then the
+    // per-head max / weights / denominator from LDS
+    float* m_s = w_s;                                   // [s * 16 + g], reused for the weights
+    float* l_s = w_s + MAX_SPLIT * 16;
+    for (int i = tid; i < n_act * G; i += DC_BLK) {
+        const int sidx = i / G, g = i - sidx * G;
+        const long src = (rk * split + sidx) * G + g;
+        m_s[sidx * 16 + g] = m_part[src];
+        l_s[sidx * 16 + g] = l_part[src];
+    }
+    __syncthreads();
     for (int g = wave; g < G; g += NWV) {
         float mm = -INFINITY;
-        for (int s = lane; s < n_act; s += kWave) mm = fmaxf(mm, m_part[(rk * split + s) * G + g]);
+        for (int sidx = lane; sidx < n_act; sidx += kWave)
+            if (l_s[sidx * 16 + g] > 0.f) mm = fmaxf(mm, m_s[sidx * 16 + g]);
         mm = wave_max(mm);
         float lt = 0.f;
-        for (int s = lane; s < n_act; s += kWave) {
-            const float l = l_part[(rk * split + s) * G + g];
-            const float w = (l > 0.f) ? __expf(m_part[(rk * split + s) * G + g] - mm) : 0.f;
-            w_s[s * 16 + g] = w;
+        for (int sidx = lane; sidx < n_act; sidx += kWave) {
+            const float l = l_s[sidx * 16 + g];
+            const float w = (l > 0.f) ? __expf(m_s[sidx * 16 + g] - mm) : 0.f;
+            m_s[sidx * 16 + g] = w;                     // this lane read it last
             lt += l * w;
         }
 #pragma unroll
@@ -68,12 +95,23 @@ __device__ void merge_row(const float* __restrict__ m_part, const float* __restr
         if (lane == 0) lt_s[g] = lt;
     }
     __syncthreads();
-    for (int i = tid; i < G * (DC_D / 4); i += DC_BLK) {
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+        const int i = tid + it * DC_BLK;
+        if (i >= G * (DC_D / 4)) break;
         const int g = i / (DC_D / 4), d4 = (i % (DC_D / 4)) * 4;
         float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int k = 0; k < PF; ++k) {
+            if (k < n_act) {
+                const float w = w_s[k * 16 + g];
+                const float4 a = pre[it][k];
+                acc.x += w * a.x; acc.y += w * a.y; acc.z += w * a.z; acc.w += w * a.w;
+            }
+        }
         const float* ap = acc_part + (rk * split * G + g) * DC_D + d4;
-#pragma unroll 4
-        for (int s = 0; s < n_act; ++s) {
+#pragma unroll 8
+        for (int s = PF; s < n_act; ++s) {
             const float w = w_s[s * 16 + g];
             const float4 a = *reinterpret_cast<const float4*>(ap + (long)s * G * DC_D);
             acc.x += w * a.x; acc.y += w * a.y; acc.z += w * a.z; acc.w += w * a.w;
@@ -297,7 +335,7 @@ __global__ __launch_bounds__(DC_BLK) void decode_merge_kernel(
     const int cnt = pcnt[(long)r * cnt_sr + kh];
     const int pps = max(cdiv(cnt, split), pps_min);
     const int n_act = cnt > 0 ? min(cdiv(cnt, pps), split) : 0;
-    __shared__ float w_s[MAX_SPLIT * 16];
+    __shared__ float w_s[2 * MAX_SPLIT * 16];
     __shared__ float lt_s[16];
     merge_row(m_part, l_part, acc_part, rk, r, kh, n_act, G, split, out, o_sr, o_sh, out_f32,
               w_s, lt_s);

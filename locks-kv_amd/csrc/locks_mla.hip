@@ -486,6 +486,17 @@ __global__ __launch_bounds__(MG_BLK) void mla_merge_kernel(
     __shared__ float red[MG_BLK / kWave];
     __shared__ __attribute__((aligned(16))) float4 part[MG_GRP][32];
     const long rb = (long)r * split;
+    const int c = tid & 31, g = tid >> 5;
+    const int d0 = 128 * zc + 4 * c;
+    // the first 4 partials of this thread's split group, loaded before any
+    // wait (they do not depend on the weights)
+    float4 pre[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int s = g + k * MG_GRP;
+        pre[k] = (s < split) ? *reinterpret_cast<const float4*>(acc_part + ((rb + s) * ML_H + h) * ML_D + d0)
+                             : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
     // M = max over live splits; weights; L = sum w l (fixed reduction tree)
     float mx = -INFINITY;
     for (int s = tid; s < n_act; s += MG_BLK) {
@@ -515,10 +526,16 @@ __global__ __launch_bounds__(MG_BLK) void mla_merge_kernel(
 #pragma unroll
     for (int w = 0; w < MG_BLK / kWave; ++w) L += red[w];
     // acc over this slice: column c (4 dims), split group g
-    const int c = tid & 31, g = tid >> 5;
-    const int d0 = 128 * zc + 4 * c;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    int s = g;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int s = g + k * MG_GRP;
+        if (s < n_act) {
+            const float w = w_s[s];
+            acc.x += w * pre[k].x; acc.y += w * pre[k].y; acc.z += w * pre[k].z; acc.w += w * pre[k].w;
+        }
+    }
+    int s = g + 4 * MG_GRP;
     for (; s + 3 * MG_GRP < n_act; s += 4 * MG_GRP) {
         float4 a[4];
         float w[4];
