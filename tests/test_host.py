@@ -123,3 +123,30 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "_LIB_PATH", str(tmp_path / "nope.so"))
     with pytest.raises(_lib.LocksLibraryError):
         _lib.load()
+
+
+def test_mla_entries_reject_bad_geometry_without_device():
+    from locks import _lib
+    lib = _lib.load()
+    # locks_mla_score: kv_lora_rank 256 is outside this build
+    args = [1, 16 * 576, 576] + [1] * 7 + [16 * 576, 576, 8, 1, 64, 64, 1, 1, 64, 64, 64, 1, 16,
+                                             256, 64, 16, 0.1, None]
+    assert lib.locks_mla_score(*args) == -1 and b"geometry" in lib.locks_last_error()
+    args[22] = 17                                       # 17 heads
+    args[23] = 512
+    assert lib.locks_mla_score(*args) == -1 and b"n_heads=17" in lib.locks_last_error()
+    args[22] = 16
+    args[20] = 3                                        # odd chunk
+    assert lib.locks_mla_score(*args) == -1 and b"chunk 3" in lib.locks_last_error()
+    # decode: split above the partial buffers' bound
+    dargs = [1, 16 * 576, 576, 1, 16 * 576, 576, 8, 1, 64, 64, 1, 64, 64, 1, 1, 1, 1, 1,
+             1, 16, 512, 64, 16, 513, 4, 0.1, None]
+    assert lib.locks_mla_decode_splitk(*dargs) == -1 and b"split=513" in lib.locks_last_error()
+    margs = [1, 1, 1, 1, 64, 1, 16 * 512, 510, 0, None, 16, 1, 16, 512, 8, 4, None]
+    assert lib.locks_mla_decode_merge(*margs) == -1 and b"multiples of 4" in lib.locks_last_error()
+    assert 2 <= lib.locks_mla_score_auto_chunk(1, 8192) <= 1024
+    assert lib.locks_mla_score_auto_chunk(1, 8192) % 2 == 0
+    # the latent build accepts d = 512 geometry but not d = 256
+    bargs = [1, 16 * 576, 576, 0, 8, 1, 1, 1, 256, 16] + [1] * 7 + [None]
+    assert lib.locks_build_rki4(*bargs) == -1 and b"d=256" in lib.locks_last_error()
+
