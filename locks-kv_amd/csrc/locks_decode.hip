@@ -50,7 +50,7 @@ __device__ void merge_row(const float* __restrict__ m_part, const float* __restr
                           const float* __restrict__ acc_part, long rk, int r, int kh, int n_act,
                           int G, int split, void* __restrict__ out, long o_sr, long o_sh,
                           int out_f32, float* w_s, float* lt_s) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     constexpr int NWV = DC_BLK / kWave;
     constexpr int PF = 8;                               // splits of acc prefetched per item
     // the first PF split partials of this thread's (head, 4-dim) items are
@@ -158,7 +158,7 @@ __global__ __launch_bounds__(DC_BLK) void decode_split_kernel(
     if (j0 >= cnt) return;                        // inactive split: no store
     const int j1 = min(j0 + pps, cnt);
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int c16 = lane & 15, kg = lane >> 4;
     const int seq_len = seq_lens[r];
 

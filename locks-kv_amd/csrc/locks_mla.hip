@@ -73,7 +73,7 @@ __global__ __launch_bounds__(ML_BLK) void mla_score_kernel(
     int H, float scale, int chunk)
 {
     const int z = blockIdx.x, r = blockIdx.y;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int P = min(nsh[r], MP);
     const int c0 = z * chunk;
     const int c1 = min(c0 + chunk, P);
@@ -326,7 +326,7 @@ __global__ __launch_bounds__(ML_BLK) void mla_decode_split_kernel(
     const int j0 = sp * pps;
     if (j0 >= cnt) return;                               // inactive split: no store
     const int j1 = min(j0 + pps, cnt);
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r16 = lane & 15, kg = lane >> 4;
     const int seq_len = seq_lens[r];
 
@@ -478,7 +478,7 @@ __global__ __launch_bounds__(MG_BLK) void mla_merge_kernel(
     float* __restrict__ lse, long lse_sr, int split, int pps_min)
 {
     const int h = blockIdx.x, r = blockIdx.y, zc = blockIdx.z, tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int cnt = min(pcnt[r], pt_cols);
     const int pps = max(cdiv(cnt, split), pps_min);
     const int n_act = cnt > 0 ? cdiv(cnt, pps) : 0;

@@ -75,7 +75,7 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
     constexpr int NGRP = SC_TILE / PPM;     // token-stage groups per tile
     const int z = blockIdx.x, r = blockIdx.y;
     const int Z = gridDim.x;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int P = min(nsh[r], MP);          // never score past the score_h row
     const int c0 = z * chunk;
     const int c1 = min(c0 + chunk, P);

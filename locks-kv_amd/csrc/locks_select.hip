@@ -214,7 +214,7 @@ __device__ void finish_row(long rk, int n_pages, int n_sel_hi, int n_sink, int b
                            int* __restrict__ spill_page, int* offs, uint32_t* lkey, int* lpage,
                            int* hist, int* s3, int* wsum) {
     constexpr int NWV = BLK / kWave;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     {
         int run = 0;
         for (int base = 0; base < Z1; base += BLK) {
@@ -267,7 +267,7 @@ __device__ RadixSel reg_kth_largest(const uint32_t (&key)[E], const bool (&val)[
                                     int* hist, int* wtot, int* s3) {
     constexpr int NW = BLK / kWave;
     constexpr int BPL = 4096 / BLK;                     // histogram bins per lane
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     RadixSel rs{0u, 0u, k, false};
 #pragma unroll 1
     for (int pass = 0; pass < 3; ++pass) {
@@ -367,7 +367,7 @@ __global__ __launch_bounds__(ROW_BLK) void sel_row_kernel(
 {
     static_assert(E % 4 == 0, "pages per thread must be a multiple of 4");
     const int kh = blockIdx.x, r = blockIdx.y, n_kv = gridDim.x;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const long rk = (long)r * n_kv + kh;
     const int n_pages = max(min(npg[r], MP), 0);
     const int n_sel_hi = min(nsh[r], MP);
@@ -493,7 +493,7 @@ __global__ __launch_bounds__(SEL_BLK) void sel_chunk_kernel(
 {
     const int z = blockIdx.x, kh = blockIdx.y, r = blockIdx.z;
     const int n_kv = gridDim.y, Z1 = gridDim.x;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const long rk = (long)r * n_kv + kh;
     const int n_pages = min(npg[r], MP);
     const int n_sel_hi = min(nsh[r], MP);
@@ -660,7 +660,7 @@ __global__ __launch_bounds__(C2_BLK) void sel_chunk2_kernel(
 {
     const int z = blockIdx.x, kh = blockIdx.y, r = blockIdx.z;
     const int n_kv = gridDim.y, Z1 = gridDim.x;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const long rk = (long)r * n_kv + kh;
     const int n_sel_hi = min(nsh[r], MP);
     const int c0 = z * SEL_CH;
