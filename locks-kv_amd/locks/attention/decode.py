@@ -49,12 +49,14 @@ PPS_MIN_OVERRIDE = None        # set by bench sweeps; None = the table below
 
 
 def _pps_min(n_req: int, n_kv: int = 8) -> int:
-    """Minimum pages per split workgroup (4 waves x 2 pages at bs=1): amortises
-    the q load, the 4-wave LDS merge and the partial store."""
+    """Minimum pages per split workgroup (4 waves, 1-2 pages each at bs=1):
+    amortises the q load, the 4-wave LDS merge and the partial store.
+    Measured on MI355X at 128 attended pages: 4 for >= 4 kv heads (Llama,
+    256 workgroups), 8 for 2 kv heads (GLM)."""
     if PPS_MIN_OVERRIDE:
         return int(PPS_MIN_OVERRIDE)
     if n_req == 1:
-        return 8
+        return 4 if n_kv >= 4 else 8
     return 16 if n_req < 16 else 32
 
 
