@@ -27,11 +27,16 @@ COMMON = ["-O3", "-fPIC", "-std=c++17", f"-I{CSRC}", f"-I{os.path.join(ROOT, 'in
 DEVICE = [f"--offload-arch={ARCH}", "-x", "hip",
           # packed-fp32 instructions stay off on this pool (silent wrong results)
           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+# per-source extra flags: the scorer keeps its MFMA accumulators in VGPRs (no
+# accvgpr moves before the VALU epilogues; measured ~2 % faster).  Not for
+# sources whose inline-asm LDS stores read MFMA results: the compiler's
+# MFMA-to-asm wait states are only guaranteed through the accvgpr moves.
+EXTRA = {"locks_score.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def _compile(src: str) -> str:
     obj = os.path.join(OUT_DIR, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *COMMON, *DEVICE, "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [HIPCC, *COMMON, *DEVICE, *EXTRA.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stdout}\n{r.stderr}")
