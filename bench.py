@@ -492,6 +492,8 @@ def main():
     ap.add_argument("--no-dense", action="store_true")
     ap.add_argument("--zsplit", type=int, default=0, help="scorer chunks per (req, kv head)")
     ap.add_argument("--pps-min", type=int, default=0, help="override the decode pps_min table")
+    ap.add_argument("--fused-decode", type=int, default=-1,
+                    help="1: one-launch decode (last split merges), 0: split + merge launches")
     ap.add_argument("--calib-copy", type=int, default=0,
                     help="only run N device copies of 1 GiB (PMC byte-counter calibration)")
     ap.add_argument("--profile-scorer", type=int, default=0,
@@ -513,9 +515,11 @@ def main():
     if wl.get("mla"):
         run_mla(a, wl)
         return
+    from locks.attention import decode as _dec
     if a.pps_min:
-        from locks.attention import decode as _dec
         _dec.PPS_MIN_OVERRIDE = a.pps_min
+    if a.fused_decode >= 0:
+        _dec.FUSED_MERGE = bool(a.fused_decode)
     t0 = time.perf_counter()
     m = make_model(wl, a.budget_pages, summaries=a.summaries, zsplit=a.zsplit or None)
     log(f"model ready in {time.perf_counter() - t0:.1f}s (summary build {m['build_s']:.1f}s)")

@@ -157,6 +157,31 @@ int32_t locks_decode_merge(const float* m_part, const float* l_part, const float
                            int32_t split, int32_t pps_min, void* stream);
 
 /*
+ * locks_decode_splitk and locks_decode_merge in one launch: the last split
+ * workgroup of each (request, kv head) row to finish merges that row into
+ * out.  Replaces the same pair of launches
+ * (attention/decode.py:328-387 -> attention/merge.py:105-152); same
+ * arguments plus
+ *   counters (n_req * n_kv) i32 arrival counts: zero before the first call,
+ *     left zero by every call; calls that share counters must not overlap;
+ *   out / out_stride_* / out_is_f32 as locks_decode_merge.
+ * Writes the same bits as locks_decode_splitk + locks_decode_merge.
+ */
+int32_t locks_decode_fused(const uint16_t* q, int64_t q_stride_req, int64_t q_stride_head,
+                           const uint16_t* k_cache, int64_t k_stride_block, int64_t k_stride_tok,
+                           int64_t k_stride_head, const uint16_t* v_cache, int64_t v_stride_block,
+                           int64_t v_stride_tok, int64_t v_stride_head, int32_t num_blocks,
+                           const int32_t* block_table, int64_t bt_stride, int32_t bt_cols,
+                           const int32_t* page_table, int64_t pt_stride_req,
+                           int64_t pt_stride_head, int32_t pt_cols, const int32_t* page_cnt,
+                           int64_t cnt_stride, const int32_t* seq_lens, float* m_part,
+                           float* l_part, float* acc_part, int32_t* counters, void* out,
+                           int64_t out_stride_req, int64_t out_stride_head, int32_t out_is_f32,
+                           int32_t n_req, int32_t n_kv, int32_t G, int32_t head_dim,
+                           int32_t page, int32_t split, int32_t pps_min, float sm_scale,
+                           void* stream);
+
+/*
  * rki4 summary build on the GPU for the listed physical blocks of ONE layer
  * (head_dim 128: GQA K heads; head_dim 512: the MLA latent, n_kv 1).
  * Replaces the reference build chain _write_pre -> _eigh_chunked ->

@@ -44,12 +44,37 @@ __device__ __forceinline__ uint32_t bf16_word(const uint4& w, int e) {
     return (e & 1) ? (x >> 16) : (x & 0xFFFFu);
 }
 
+// Device-coherent partials for the fused decode: 16-byte buffer loads and
+// stores with the SC1 cache policy (the gfx950 encoding of device-scope
+// relaxed atomics) -- written by one workgroup, read by another of the same
+// launch after an arrival count, with no cache write-back or invalidate.
+constexpr int CPOL_SC1 = 16;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t part_rsrc(const float* base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, 0x7fffffff, 0x00020000);
+}
+template <bool COHERENT>
+__device__ __forceinline__ float4 ld_part4(const float* base, long idx) {
+    if constexpr (COHERENT) {
+        const v4i v = __builtin_amdgcn_raw_buffer_load_b128(part_rsrc(base), (int)(idx * 4), 0, CPOL_SC1);
+        return __builtin_bit_cast(float4, v);
+    } else {
+        return *reinterpret_cast<const float4*>(base + idx);
+    }
+}
+template <bool COHERENT>
+__device__ __forceinline__ float ld_part(const float* base, long idx) {
+    if constexpr (COHERENT)
+        return __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(part_rsrc(base), (int)(idx * 4), 0, CPOL_SC1));
+    else return base[idx];
+}
+
 // Merge the first n_act split partials of row rk into out (one workgroup,
-// DC_BLK threads).  w_s: >= 2 * MAX_SPLIT * 16 floats of LDS.
+// DC_BLK threads).  w_s, l_s: >= MAX_SPLIT * 16 floats of LDS each.
+template <bool COHERENT = false>
 __device__ void merge_row(const float* __restrict__ m_part, const float* __restrict__ l_part,
                           const float* __restrict__ acc_part, long rk, int r, int kh, int n_act,
                           int G, int split, void* __restrict__ out, long o_sr, long o_sh,
-                          int out_f32, float* w_s, float* lt_s) {
+                          int out_f32, float* w_s, float* l_s, float* lt_s) {
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     constexpr int NWV = DC_BLK / kWave;
     constexpr int PF = 8;                               // splits of acc prefetched per item
@@ -60,22 +85,20 @@ __device__ void merge_row(const float* __restrict__ m_part, const float* __restr
     for (int it = 0; it < 2; ++it) {
         const int i = tid + it * DC_BLK;
         const int g = i / (DC_D / 4), d4 = (i % (DC_D / 4)) * 4;
-        const float* ap = acc_part + (rk * split * G + g) * DC_D + d4;
 #pragma unroll
         for (int k = 0; k < PF; ++k)
             pre[it][k] = (i < G * (DC_D / 4) && k < split)
-                             ? *reinterpret_cast<const float4*>(ap + (long)k * G * DC_D)
+                             ? ld_part4<COHERENT>(acc_part, (rk * split * G + g) * DC_D + d4 + (long)k * G * DC_D)
                              : make_float4(0.f, 0.f, 0.f, 0.f);
     }
     // every (split, head) m and l in one pass (all loads in flight), then the
     // per-head max / weights / denominator from LDS
     float* m_s = w_s;                                   // [s * 16 + g], reused for the weights
-    float* l_s = w_s + MAX_SPLIT * 16;
     for (int i = tid; i < n_act * G; i += DC_BLK) {
         const int sidx = i / G, g = i - sidx * G;
         const long src = (rk * split + sidx) * G + g;
-        m_s[sidx * 16 + g] = m_part[src];
-        l_s[sidx * 16 + g] = l_part[src];
+        m_s[sidx * 16 + g] = ld_part<COHERENT>(m_part, src);
+        l_s[sidx * 16 + g] = ld_part<COHERENT>(l_part, src);
     }
     __syncthreads();
     for (int g = wave; g < G; g += NWV) {
@@ -109,11 +132,10 @@ __device__ void merge_row(const float* __restrict__ m_part, const float* __restr
                 acc.x += w * a.x; acc.y += w * a.y; acc.z += w * a.z; acc.w += w * a.w;
             }
         }
-        const float* ap = acc_part + (rk * split * G + g) * DC_D + d4;
 #pragma unroll 8
         for (int s = PF; s < n_act; ++s) {
             const float w = w_s[s * 16 + g];
-            const float4 a = *reinterpret_cast<const float4*>(ap + (long)s * G * DC_D);
+            const float4 a = ld_part4<COHERENT>(acc_part, (rk * split * G + g) * DC_D + d4 + (long)s * G * DC_D);
             acc.x += w * a.x; acc.y += w * a.y; acc.z += w * a.z; acc.w += w * a.w;
         }
         const float lt = lt_s[g];
@@ -139,6 +161,7 @@ __device__ void merge_row(const float* __restrict__ m_part, const float* __restr
 // stages ping-pong so one page is always in flight while the other is
 // consumed.  The 4 wave states are then merged in LDS into the split's
 // partial.
+template <bool FUSED>
 __global__ __launch_bounds__(DC_BLK) void decode_split_kernel(
     const uint16_t* __restrict__ q, long q_sr, long q_sh,
     const uint16_t* __restrict__ kc, long k_sb, long k_st, long k_sh,
@@ -147,7 +170,8 @@ __global__ __launch_bounds__(DC_BLK) void decode_split_kernel(
     const int* __restrict__ ptab, long pt_sr, long pt_sh, int pt_cols,
     const int* __restrict__ pcnt, long cnt_sr, const int* __restrict__ seq_lens,
     float* __restrict__ m_part, float* __restrict__ l_part, float* __restrict__ acc_part,
-    int G, int split, int pps_min, float sm_scale)
+    int G, int split, int pps_min, float sm_scale,
+    int* __restrict__ counters, void* __restrict__ out, long o_sr, long o_sh, int out_f32)
 {
     const int sp = blockIdx.x, kh = blockIdx.y, r = blockIdx.z;
     const int n_kv = gridDim.y;
@@ -155,6 +179,17 @@ __global__ __launch_bounds__(DC_BLK) void decode_split_kernel(
     const int cnt = min(pcnt[(long)r * cnt_sr + kh], pt_cols);
     const int pps = max(cdiv(cnt, split), pps_min);
     const int j0 = sp * pps;
+    if constexpr (FUSED) {
+        if (cnt <= 0) {                           // nothing selected: the output row is 0
+            if (sp == 0)
+                for (int i = threadIdx.x; i < G * DC_D; i += DC_BLK) {
+                    const long oi = (long)r * o_sr + (long)(kh * G + i / DC_D) * o_sh + i % DC_D;
+                    if (out_f32) static_cast<float*>(out)[oi] = 0.f;
+                    else static_cast<uint16_t*>(out)[oi] = 0;
+                }
+            return;
+        }
+    }
     if (j0 >= cnt) return;                        // inactive split: no store
     const int j1 = min(j0 + pps, cnt);
 
@@ -306,21 +341,53 @@ __global__ __launch_bounds__(DC_BLK) void decode_split_kernel(
     }
     __syncthreads();
     const long base = (rk * split + sp) * G;
-    for (int i = tid; i < G * DC_D; i += DC_BLK) {
-        const int g = i / DC_D, d = i % DC_D;
+    for (int i = tid; i < G * (DC_D / 4); i += DC_BLK) {
+        const int g = i / (DC_D / 4), d = (i % (DC_D / 4)) * 4;
         float M = wm[0][g];
 #pragma unroll
         for (int w = 1; w < DC_WAVES; ++w) M = fmaxf(M, wm[w][g]);
         const float Mr = (M == -INFINITY) ? 0.f : M;
-        float acc = 0.f, l = 0.f;
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+        float l = 0.f;
 #pragma unroll
         for (int w = 0; w < DC_WAVES; ++w) {
             const float e = __expf(wm[w][g] - Mr);
-            acc += e * red[(w * 16 + g) * DC_D + d];
+            const float4 x = *reinterpret_cast<const float4*>(red + (w * 16 + g) * DC_D + d);
+            acc.x += e * x.x; acc.y += e * x.y; acc.z += e * x.z; acc.w += e * x.w;
             l += e * wl[w][g];
         }
-        acc_part[(base + g) * DC_D + d] = acc;
-        if (d == 0) { m_part[base + g] = M; l_part[base + g] = l; }
+        if constexpr (FUSED) {
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i, acc), part_rsrc(acc_part),
+                                                   (int)(((base + g) * DC_D + d) * 4), 0, CPOL_SC1);
+            if (d == 0) {
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(M), part_rsrc(m_part), (int)((base + g) * 4), 0, CPOL_SC1);
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(l), part_rsrc(l_part), (int)((base + g) * 4), 0, CPOL_SC1);
+            }
+        } else {
+            *reinterpret_cast<float4*>(acc_part + (base + g) * DC_D + d) = acc;
+            if (d == 0) { m_part[base + g] = M; l_part[base + g] = l; }
+        }
+    }
+    if constexpr (FUSED) {
+        // The last of the row's active splits to finish merges them all: its
+        // SC1 partial stores are complete (vmcnt) before the arrival count is
+        // bumped, and the merge reads the partials with SC1 loads.  The
+        // merging workgroup resets the counter for the next call.
+        __shared__ int last_s;
+        __shared__ float lt_s[16];
+        __builtin_amdgcn_s_waitcnt(0x0070);
+        __syncthreads();
+        const int n_act = min(cdiv(cnt, pps), split);
+        if (tid == 0) {
+            const int old = __hip_atomic_fetch_add(counters + rk, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            last_s = (old == n_act - 1);
+        }
+        __syncthreads();
+        if (!last_s) return;
+        if (tid == 0) __hip_atomic_store(counters + rk, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        merge_row<true>(m_part, l_part, acc_part, rk, r, kh, n_act, G, split, out, o_sr, o_sh,
+                        out_f32, reinterpret_cast<float*>(&stA[0][0]),
+                        reinterpret_cast<float*>(&stB[0][0]), lt_s);
     }
 }
 
@@ -335,10 +402,10 @@ __global__ __launch_bounds__(DC_BLK) void decode_merge_kernel(
     const int cnt = pcnt[(long)r * cnt_sr + kh];
     const int pps = max(cdiv(cnt, split), pps_min);
     const int n_act = cnt > 0 ? min(cdiv(cnt, pps), split) : 0;
-    __shared__ float w_s[2 * MAX_SPLIT * 16];
+    __shared__ float w_s[MAX_SPLIT * 16], l_s[MAX_SPLIT * 16];
     __shared__ float lt_s[16];
     merge_row(m_part, l_part, acc_part, rk, r, kh, n_act, G, split, out, o_sr, o_sh, out_f32,
-              w_s, lt_s);
+              w_s, l_s, lt_s);
 }
 
 }  // namespace locks
@@ -369,14 +436,55 @@ extern "C" int32_t locks_decode_splitk(
     LOCKS_REQUIRE(q && k_cache && v_cache && block_table && page_table && page_cnt && seq_lens &&
                   m_part && l_part && acc_part, "locks_decode_splitk: null pointer argument");
     if (n_req == 0) return 0;
-    hipLaunchKernelGGL(decode_split_kernel, dim3(split, n_kv, n_req), dim3(DC_BLK), 0,
+    hipLaunchKernelGGL(decode_split_kernel<false>, dim3(split, n_kv, n_req), dim3(DC_BLK), 0,
                        (hipStream_t)stream, q, (long)q_stride_req, (long)q_stride_head, k_cache,
                        (long)k_stride_block, (long)k_stride_tok, (long)k_stride_head, v_cache,
                        (long)v_stride_block, (long)v_stride_tok, (long)v_stride_head, num_blocks,
                        block_table, (long)bt_stride, bt_cols, page_table, (long)pt_stride_req,
                        (long)pt_stride_head, pt_cols, page_cnt, (long)cnt_stride, seq_lens,
-                       m_part, l_part, acc_part, G, split, pps_min, sm_scale);
+                       m_part, l_part, acc_part, G, split, pps_min, sm_scale,
+                       nullptr, nullptr, 0L, 0L, 0);
     return check_launch("decode_split_kernel");
+}
+
+extern "C" int32_t locks_decode_fused(
+    const uint16_t* q, int64_t q_stride_req, int64_t q_stride_head,
+    const uint16_t* k_cache, int64_t k_stride_block, int64_t k_stride_tok, int64_t k_stride_head,
+    const uint16_t* v_cache, int64_t v_stride_block, int64_t v_stride_tok, int64_t v_stride_head,
+    int32_t num_blocks, const int32_t* block_table, int64_t bt_stride, int32_t bt_cols,
+    const int32_t* page_table, int64_t pt_stride_req, int64_t pt_stride_head, int32_t pt_cols,
+    const int32_t* page_cnt, int64_t cnt_stride, const int32_t* seq_lens,
+    float* m_part, float* l_part, float* acc_part, int32_t* counters,
+    void* out, int64_t out_stride_req, int64_t out_stride_head, int32_t out_is_f32,
+    int32_t n_req, int32_t n_kv, int32_t G, int32_t head_dim, int32_t page,
+    int32_t split, int32_t pps_min, float sm_scale, void* stream)
+{
+    LOCKS_REQUIRE(head_dim == DC_D, "locks_decode_fused: head_dim %d unsupported (this build: 128)", head_dim);
+    LOCKS_REQUIRE(page == DC_PG, "locks_decode_fused: page %d unsupported (this build: 16)", page);
+    LOCKS_REQUIRE(G >= 1 && G <= 16, "locks_decode_fused: G=%d outside [1, 16]", G);
+    LOCKS_REQUIRE(split >= 1 && split <= MAX_SPLIT, "locks_decode_fused: split %d outside [1, %d]", split, MAX_SPLIT);
+    LOCKS_REQUIRE(pps_min >= 1, "locks_decode_fused: pps_min %d < 1", pps_min);
+    LOCKS_REQUIRE(num_blocks >= 1 && bt_cols >= 1 && pt_cols >= 1, "locks_decode_fused: empty geometry");
+    LOCKS_REQUIRE(k_stride_tok % 8 == 0 && v_stride_tok % 8 == 0 && k_stride_block % 8 == 0 &&
+                  v_stride_block % 8 == 0 && k_stride_head % 8 == 0 && v_stride_head % 8 == 0 &&
+                  q_stride_req % 8 == 0 && q_stride_head % 8 == 0,
+                  "locks_decode_fused: q/K/V strides must be multiples of 8 elements (16-byte loads)");
+    LOCKS_REQUIRE(out_stride_req % 4 == 0 && out_stride_head % 4 == 0,
+                  "locks_decode_fused: out strides must be multiples of 4 elements");
+    LOCKS_REQUIRE((int64_t)n_req * n_kv * split * G * DC_D * 4 < 0x7fffffffLL,
+                  "locks_decode_fused: partials exceed 2 GiB");
+    LOCKS_REQUIRE(q && k_cache && v_cache && block_table && page_table && page_cnt && seq_lens &&
+                  m_part && l_part && acc_part && counters && out, "locks_decode_fused: null pointer argument");
+    if (n_req == 0) return 0;
+    hipLaunchKernelGGL(decode_split_kernel<true>, dim3(split, n_kv, n_req), dim3(DC_BLK), 0,
+                       (hipStream_t)stream, q, (long)q_stride_req, (long)q_stride_head, k_cache,
+                       (long)k_stride_block, (long)k_stride_tok, (long)k_stride_head, v_cache,
+                       (long)v_stride_block, (long)v_stride_tok, (long)v_stride_head, num_blocks,
+                       block_table, (long)bt_stride, bt_cols, page_table, (long)pt_stride_req,
+                       (long)pt_stride_head, pt_cols, page_cnt, (long)cnt_stride, seq_lens,
+                       m_part, l_part, acc_part, G, split, pps_min, sm_scale,
+                       counters, out, (long)out_stride_req, (long)out_stride_head, out_is_f32);
+    return check_launch("decode_split_kernel<fused>");
 }
 
 extern "C" int32_t locks_decode_merge(

@@ -31,6 +31,10 @@ SIGNATURES = {
                                    _i32, _p, _i64, _i32, _p, _i64, _i64, _i32, _p, _i64, _p,
                                    _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32,
                                    _p]),
+    "locks_decode_fused": (_i32, [_p, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64,
+                                  _i32, _p, _i64, _i32, _p, _i64, _i64, _i32, _p, _i64, _p,
+                                  _p, _p, _p, _p, _p, _i64, _i64, _i32,
+                                  _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _p]),
     "locks_build_rki4": (_i32, [_p, _i64, _i64, _i64, _i32, _p, _i32, _i32, _i32, _i32,
                                 _p, _p, _p, _p, _p, _p, _p, _p]),
     "locks_pack_rki4": (_i32, [_p, _p, _p, _p, _p, _i32, _i32, _i32, _p, _p, _p, _p, _p, _p, _p]),

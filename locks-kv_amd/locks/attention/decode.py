@@ -45,6 +45,7 @@ class ResidentVSource:
         return v, v.stride(0), v.stride(1), v.stride(2)
 
 
+FUSED_MERGE = True            # one launch: the last split of a row merges it
 PPS_MIN_OVERRIDE = None        # set by bench sweeps; None = the table below
 
 
@@ -81,6 +82,8 @@ def ensure_stage_b_buffers(st, device, split: int) -> None:
     st.m_part = torch.empty(R, n_kv, split, G, device=device, dtype=torch.float32)
     st.l_part = torch.empty(R, n_kv, split, G, device=device, dtype=torch.float32)
     st.acc_part = torch.empty(R, n_kv, split, G, D, device=device, dtype=torch.float32)
+    # arrival counts of the fused decode; every call leaves them at zero
+    st.dec_counters = torch.zeros(R, n_kv, device=device, dtype=torch.int32)
 
 
 def decode_splitk(q, k, v, block_table, seq_lens, page_table, page_cnt, m_part, l_part,
@@ -102,6 +105,29 @@ def decode_splitk(q, k, v, block_table, seq_lens, page_table, page_cnt, m_part, 
         _lib.stream_ptr(q.device)), "decode_splitk")
 
 
+def decode_fused(q, k, v, block_table, seq_lens, page_table, page_cnt, m_part, l_part,
+                 acc_part, counters, out, *, n_req: int, G: int, split: int, pps_min: int,
+                 scale: float) -> None:
+    """Split kernel whose last-arriving split of each (request, kv head) row
+    merges the row into ``out`` (one launch).  ``counters`` (R, n_kv) i32
+    must be zero on the first call; each call leaves it zero."""
+    if out.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"out must be bf16 or fp32, got {out.dtype}")
+    NB, page, n_kv, d = k.shape
+    lib = _lib.load()
+    _lib.check(lib.locks_decode_fused(
+        _lib.ptr(q), q.stride(0), q.stride(1),
+        _lib.ptr(k), k.stride(0), k.stride(1), k.stride(2),
+        _lib.ptr(v), v.stride(0), v.stride(1), v.stride(2), int(NB),
+        _lib.ptr(block_table), block_table.stride(0), int(block_table.shape[1]),
+        _lib.ptr(page_table), page_table.stride(0), page_table.stride(1),
+        int(page_table.shape[2]), _lib.ptr(page_cnt), page_cnt.stride(0), _lib.ptr(seq_lens),
+        _lib.ptr(m_part), _lib.ptr(l_part), _lib.ptr(acc_part), _lib.ptr(counters),
+        _lib.ptr(out), out.stride(0), out.stride(1), 1 if out.dtype == torch.float32 else 0,
+        int(n_req), int(n_kv), int(G), int(d), int(page), int(split), int(pps_min),
+        float(scale), _lib.stream_ptr(q.device)), "decode_fused")
+
+
 def decode_merge(m_part, l_part, acc_part, page_cnt, out, *, n_req: int, n_kv: int, G: int,
                  split: int, pps_min: int) -> None:
     if out.dtype not in (torch.bfloat16, torch.float32):
@@ -117,7 +143,8 @@ def decode_merge(m_part, l_part, acc_part, page_cnt, out, *, n_req: int, n_kv: i
 
 def sparse_paged_decode_batched(q, kv_cache, block_table, seq_lens, st, out,
                                 vsource=None, *, scale: float = None) -> None:
-    """Batched Stage B (decode.py:328-387): 2 fixed-shape launches."""
+    """Batched Stage B (decode.py:328-387): one fixed-shape launch (the
+    split kernel whose last split per row merges it), or split + merge."""
     if scale is None:
         scale = st.scale
     n_req = seq_lens.shape[0]
@@ -128,6 +155,11 @@ def sparse_paged_decode_batched(q, kv_cache, block_table, seq_lens, st, out,
         raise NotImplementedError("only the resident V source exists in this build")
     v = vsource.args()[0]
     pps = _pps_min(n_req, st.n_kv)
+    if FUSED_MERGE:
+        decode_fused(q, k, v, block_table, seq_lens, st.page_table, st.page_cnt, st.m_part,
+                     st.l_part, st.acc_part, st.dec_counters, out, n_req=n_req, G=st.G,
+                     split=st.split, pps_min=pps, scale=scale)
+        return
     decode_splitk(q, k, v, block_table, seq_lens, st.page_table, st.page_cnt, st.m_part,
                   st.l_part, st.acc_part, n_req=n_req, G=st.G, split=st.split,
                   pps_min=pps, scale=scale)

@@ -252,6 +252,47 @@ def test_decode_matches_oracle(n_kv, G, seq_lens, split):
         _decode_check(case, st, d, out, tab, cnt)
 
 
+@pytest.mark.parametrize("n_kv,G,seq_lens,split", [
+    (8, 4, [16384], 128), (2, 16, [131072], 128), (4, 5, [1000, 7, 0, 4099], 32),
+    (2, 16, [65536, 49152, 32768, 16384], 64), (2, 16, [20000], 1)])
+def test_fused_decode_equals_split_and_merge(n_kv, G, seq_lens, split):
+    """The one-launch decode (last split of a row merges it) writes the same
+    bits as split + merge, on repeated calls (the arrival counts return to
+    zero) and for rows with nothing selected."""
+    import torch
+    from locks.attention import decode_merge, decode_splitk
+    from locks.attention.decode import _pps_min, _split_kv, decode_fused
+    say("fused decode", n_kv, G, seq_lens, split)
+    MP = max(1, max((s + 15) // 16 for s in seq_lens))
+    case = make_case(9, n_kv, G, seq_lens, MP=MP, build=False)
+    rng = np.random.default_rng(10)
+    npg, nsh, b = O.derive_page_params(seq_lens, 16, 1, 1, 126, 0.1)
+    st = _state(case, split=split)
+    d = to_dev(case)
+    k, v = _split_kv(d["kv"])
+    pps = _pps_min(case.R, n_kv)
+    for call in range(3):
+        sc = rng.random((case.R, n_kv, MP)).astype(np.float32)
+        tab, cnt = O.topb_select(sc, npg, nsh, b, 1, MP)
+        st.page_table.copy_(torch.from_numpy(tab))
+        st.page_cnt.copy_(torch.from_numpy(cnt))
+        dt = torch.float32 if call == 1 else torch.bfloat16
+        ref = torch.full((case.R, n_kv * G, 128), float("nan"), dtype=dt, device="cuda")
+        out = torch.full_like(ref, float("nan"))
+        decode_splitk(d["q"], k, v, d["bt"], d["sl"], st.page_table, st.page_cnt, st.m_part,
+                      st.l_part, st.acc_part, n_req=case.R, G=G, split=st.split,
+                      pps_min=pps, scale=case.scale)
+        decode_merge(st.m_part, st.l_part, st.acc_part, st.page_cnt, ref, n_req=case.R,
+                     n_kv=n_kv, G=G, split=st.split, pps_min=pps)
+        decode_fused(d["q"], k, v, d["bt"], d["sl"], st.page_table, st.page_cnt, st.m_part,
+                     st.l_part, st.acc_part, st.dec_counters, out, n_req=case.R, G=G,
+                     split=st.split, pps_min=pps, scale=case.scale)
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16 if dt == torch.bfloat16 else torch.int32),
+                           ref.view(torch.int16 if dt == torch.bfloat16 else torch.int32))
+        assert int(st.dec_counters.abs().sum()) == 0
+
+
 def test_dense_equality_and_split_invariance():
     """Selecting every page reproduces dense attention; any split count gives
     the same result up to fp32 reassociation."""
