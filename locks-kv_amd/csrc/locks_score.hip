@@ -51,8 +51,8 @@ constexpr int ST_V = 0;                      // 4 pairs x 1280 B packed V
 constexpr int ST_C8 = 4 * ST_VPAIR;          // 8 pages x 128 B coefficients
 constexpr int ST_MU = ST_C8 + 1024;          // 8 pages x 144 B centroid (-> mud after use)
 constexpr int ST_CS = ST_MU + 8 * ST_MUROWB; // 8 pages x 32 B token scales
-constexpr int ST_VS = ST_CS + 256;           // 8 pages x 16 B column scales
-constexpr int ST_MUS = ST_VS + 128;          // 8 dwords: centroid scales (bf16 in the low half)
+constexpr int ST_VS = ST_CS + 256;           // 8 pages x 8 column scales (f32)
+constexpr int ST_MUS = ST_VS + 256;          // 8 dwords: centroid scales (bf16 in the low half)
 constexpr int ST_BYTES = ST_MUS + 32;
 constexpr int SC_QROW = SC_D + 16;           // padded int8 q row (bank-conflict free reads)
 
@@ -98,13 +98,18 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
     // ---- prologue: q rows and block ids are fetched together; the first
     // unit's summary loads are issued before q is quantized, so the
     // quantization overlaps them.
-    constexpr int QPW = SC_MAXHQ / SC_WAVES;                  // q rows per wave, max
-    uint32_t qw[QPW];
+    // q: 8 consecutive lanes per head, 16 dims (two 16-byte loads) per lane
+    constexpr int QCH = SC_MAXHQ * 8 / SC_BLOCK;              // 16-dim chunks per thread, max
+    uint4 qa[QCH][2];
 #pragma unroll
-    for (int i = 0; i < QPW; ++i) {
-        const int hq = wave + SC_WAVES * i;
-        qw[i] = 0u;
-        if (hq < HQ) qw[i] = *reinterpret_cast<const uint32_t*>(q + (long)r * q_sr + (long)hq * q_sh + 2 * lane);
+    for (int i = 0; i < QCH; ++i) {
+        const int c = tid + SC_BLOCK * i, hq = c >> 3;
+        qa[i][0] = qa[i][1] = make_uint4(0u, 0u, 0u, 0u);
+        if (hq < HQ) {
+            const uint4* qp = reinterpret_cast<const uint4*>(q + (long)r * q_sr + (long)hq * q_sh + (c & 7) * 16);
+            qa[i][0] = qp[0];
+            qa[i][1] = qp[1];
+        }
     }
     for (int i = tid; i < c1 - c0; i += SC_BLOCK) {
         const int b = bt[(long)r * bt_sr + min(c0 + i, bt_cols - 1)];
@@ -170,8 +175,11 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
         *reinterpret_cast<uint4*>(stg + ST_C8 + lane * 16) = fc8;
         *reinterpret_cast<uint4*>(stg + ST_MU + (lane >> 3) * ST_MUROWB + (lane & 7) * 16) = fmu;
         if (lane < 16) *reinterpret_cast<uint4*>(stg + ST_CS + lane * 16) = fcs;
-        if (lane < 8) {
-            *reinterpret_cast<uint4*>(stg + ST_VS + lane * 16) = fvs;
+        if (lane < 8) {                               // column scales widened to f32 once
+            *reinterpret_cast<float4*>(stg + ST_VS + lane * 32) =
+                make_float4(bf16lo(fvs.x), bf16hi(fvs.x), bf16lo(fvs.y), bf16hi(fvs.y));
+            *reinterpret_cast<float4*>(stg + ST_VS + lane * 32 + 16) =
+                make_float4(bf16lo(fvs.z), bf16hi(fvs.z), bf16lo(fvs.w), bf16hi(fvs.w));
             *reinterpret_cast<uint32_t*>(stg + ST_MUS + lane * 4) = fmus;
         }
     };
@@ -179,19 +187,48 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
     if (wave < n_units) load_unit(wave);
 
     // ---- quantize q (the first unit's loads are in flight) --------------
+    // q8 = rint(q / qs) with the correctly rounded quotient: q * (1 / qs) is
+    // within 2 ulp of it, which decides the rounding unless the product lies
+    // within 2^-15 of a half-integer; those (rare) lanes redo the division.
     const float s2 = sm_scale * 1.4426950408889634f;           // tokens in log2 units
 #pragma unroll
-    for (int i = 0; i < QPW; ++i) {
-        const int hq = wave + SC_WAVES * i;
-        if (hq >= HQ) break;
-        const float a0 = bf16lo(qw[i]), a1 = bf16hi(qw[i]);
-        const float am = wave_max(fmaxf(fabsf(a0), fabsf(a1)));
+    for (int i = 0; i < QCH; ++i) {
+        const int c = tid + SC_BLOCK * i, hq = c >> 3;
+        if (SC_BLOCK * i >= HQ * 8) break;                      // no head left for any lane
+        const uint32_t w[8] = {qa[i][0].x, qa[i][0].y, qa[i][0].z, qa[i][0].w,
+                               qa[i][1].x, qa[i][1].y, qa[i][1].z, qa[i][1].w};
+        float f[16];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) { f[2 * k] = bf16lo(w[k]); f[2 * k + 1] = bf16hi(w[k]); }
+        float am = 0.f;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) am = fmaxf(am, fabsf(f[k]));
+        am = fmaxf(am, __shfl_xor(am, 1, kWave));
+        am = fmaxf(am, __shfl_xor(am, 2, kWave));
+        am = fmaxf(am, __shfl_xor(am, 4, kWave));
         const float qs = fmaxf(am, 1e-8f) / 127.f;
-        const int i0 = (int)rintf(__fdiv_rn(a0, qs));
-        const int i1 = (int)rintf(__fdiv_rn(a1, qs));
-        q8s[hq][2 * lane] = (int8_t)i0;
-        q8s[hq][2 * lane + 1] = (int8_t)i1;
-        if (lane == 0) qsp[hq / G][hq % G] = qs * s2;
+        const float inv = 1.f / qs;
+        int iq[16];
+        bool near = false;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const float y = f[k] * inv;
+            const float ry = rintf(y);
+            near |= fabsf(fabsf(y - ry) - 0.5f) < 0x1p-15f;
+            iq[k] = (int)ry;
+        }
+        if (__builtin_expect(__ballot(near) != 0ull, 0)) {
+            if (near) {
+#pragma unroll
+                for (int k = 0; k < 16; ++k) iq[k] = (int)rintf(__fdiv_rn(f[k], qs));
+            }
+        }
+        if (hq < HQ) {
+            *reinterpret_cast<uint4*>(&q8s[hq][(c & 7) * 16]) =
+                make_uint4(pack4_i8(iq[0], iq[1], iq[2], iq[3]), pack4_i8(iq[4], iq[5], iq[6], iq[7]),
+                           pack4_i8(iq[8], iq[9], iq[10], iq[11]), pack4_i8(iq[12], iq[13], iq[14], iq[15]));
+            if ((c & 7) == 0) qsp[hq / G][hq % G] = qs * s2;
+        }
     }
     __syncthreads();
 
@@ -224,7 +261,15 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
                         (int)__builtin_amdgcn_perm(n1.y, n1.x, 0x07050301u), (int)__builtin_amdgcn_perm(n1.w, n1.z, 0x07050301u)};
         }
         const float4 qsl = *reinterpret_cast<const float4*>(&qsp[h][4 * kg]);   // rows 4kg.. (mud)
-        const float qsj = qsp[h][r16 % GW];                                    // column head (qt)
+        // column head's q scale x 1/16 (the nibble shift), zeroed where the
+        // token stage's block-diagonal B has no entry for this lane's column:
+        // qt of page p feeds page slot p % PPM only
+        float qsjm[PPM];
+        {
+            const float qsj = qsp[h][r16 % GW] * 0.0625f;
+#pragma unroll
+            for (int ps = 0; ps < PPM; ++ps) qsjm[ps] = (psub_l == ps) ? qsj : 0.f;
+        }
         wave_lds_sync();
 
         // ---- projection: qt (8 basis columns x GQA group) per page -------
@@ -236,13 +281,13 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
         // kg, step hh reads column 2kg + hh), so qt never goes through LDS.
         const int i_pg = r16 & 1, i_c = 2 * (r16 >> 2) + ((r16 >> 1) & 1);
         uint4 vv[4];
-        uint32_t vsw[4][2];
+        float2 vsf[4][2];
 #pragma unroll
         for (int pp = 0; pp < 4; ++pp) {
             vv[pp] = *reinterpret_cast<const uint4*>(stg + ST_V + pp * ST_VPAIR + (i_pg * 8 + i_c) * ST_VROWB + kg * 16);
 #pragma unroll
             for (int pg = 0; pg < 2; ++pg)          // column scales (2kg, 2kg+1) of page 2pp+pg
-                vsw[pp][pg] = *reinterpret_cast<const uint32_t*>(stg + ST_VS + (2 * pp + pg) * 16 + kg * 4);
+                vsf[pp][pg] = *reinterpret_cast<const float2*>(stg + ST_VS + (2 * pp + pg) * 32 + kg * 8);
         }
         v4i mu0 = {0, 0, 0, 0}, mu1 = {0, 0, 0, 0};
         float musf = 0.f;
@@ -268,9 +313,8 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
             // the column scale, a power of two, so qt is exact to the same bits
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const uint32_t w = vsw[pp][v & 1];
-                const float vsc = ((v >> 1) ? bf16hi(w) : bf16lo(w)) * 0.0625f;
-                qt[pp][v] = (float)acc[v] * qsj * vsc;
+                const float2 w = vsf[pp][v & 1];
+                qt[pp][v] = (float)acc[v] * ((v >> 1) ? w.y : w.x) * qsjm[(2 * pp + (v & 1)) % PPM];
             }
         }
         {
@@ -296,12 +340,10 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
             for (int ps = 0; ps < PPM; ++ps) {
                 const int page = gi * PPM + ps;
                 const uint32_t cw = *reinterpret_cast<const uint16_t*>(stg + ST_C8 + page * 128 + r16 * 8 + 2 * kg);
-#pragma unroll
-                for (int hh = 0; hh < 2; ++hh) {
-                    const float a = (float)(int8_t)(cw >> (8 * hh));
-                    const float b = (psub_l == ps) ? qt[page >> 1][2 * hh + (page & 1)] : 0.f;
-                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc, 0, 0, 0);
-                }
+                const float a0 = (float)(int8_t)cw, a1 = (float)(int8_t)(cw >> 8);
+                // qt is already zero where this lane's column is not page slot ps
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, qt[page >> 1][page & 1], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, qt[page >> 1][2 + (page & 1)], acc, 0, 0, 0);
             }
             const uint2 csw = *reinterpret_cast<const uint2*>(stg + ST_CS + (gi * PPM + psub_l) * 32 + kg * 8);
             return v4f{acc[0] * bf16lo(csw.x), acc[1] * bf16hi(csw.x), acc[2] * bf16lo(csw.y),
@@ -396,7 +438,8 @@ extern "C" int32_t locks_score_rki4(
     LOCKS_REQUIRE(n_req >= 0 && n_kv >= 1 && n_kv <= SC_MAXKV && n_kv * G <= SC_MAXHQ,
                   "locks_score_rki4: n_kv=%d G=%d outside this build (n_kv <= %d, n_kv*G <= %d)",
                   n_kv, G, SC_MAXKV, SC_MAXHQ);
-    LOCKS_REQUIRE(q_stride_head % 2 == 0, "locks_score_rki4: q head stride must be even");
+    LOCKS_REQUIRE(q_stride_head % 8 == 0 && q_stride_req % 8 == 0,
+                  "locks_score_rki4: q strides must be multiples of 8 elements (16-byte loads)");
     LOCKS_REQUIRE((long)num_blocks * n_kv * SC_VROW < (1L << 32),
                   "locks_score_rki4: slab too large for 32-bit offsets");
     LOCKS_REQUIRE(num_blocks >= 1 && bt_cols >= 1 && max_pages >= 1,
