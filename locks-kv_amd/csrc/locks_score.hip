@@ -50,8 +50,8 @@ constexpr int ST_MUROWB = 144;               // padded stride of one page's mu r
 constexpr int ST_V = 0;                      // 4 pairs x 1280 B packed V
 constexpr int ST_C8 = 4 * ST_VPAIR;          // 8 pages x 128 B coefficients
 constexpr int ST_MU = ST_C8 + 1024;          // 8 pages x 144 B centroid (-> mud after use)
-constexpr int ST_CS = ST_MU + 8 * ST_MUROWB; // 8 pages x 32 B token scales
-constexpr int ST_VS = ST_CS + 256;           // 8 pages x 8 column scales (f32)
+constexpr int ST_CS = ST_MU + 8 * ST_MUROWB; // 8 pages x 16 token scales (f32)
+constexpr int ST_VS = ST_CS + 512;           // 8 pages x 8 column scales (f32)
 constexpr int ST_MUS = ST_VS + 256;          // 8 dwords: centroid scales (bf16 in the low half)
 constexpr int ST_BYTES = ST_MUS + 32;
 constexpr int SC_QROW = SC_D + 16;           // padded int8 q row (bank-conflict free reads)
@@ -174,7 +174,12 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
         *reinterpret_cast<uint4*>(stg + ST_V + 3 * ST_VPAIR + vofs) = fv3;
         *reinterpret_cast<uint4*>(stg + ST_C8 + lane * 16) = fc8;
         *reinterpret_cast<uint4*>(stg + ST_MU + (lane >> 3) * ST_MUROWB + (lane & 7) * 16) = fmu;
-        if (lane < 16) *reinterpret_cast<uint4*>(stg + ST_CS + lane * 16) = fcs;
+        if (lane < 16) {                              // token scales widened to f32 once
+            *reinterpret_cast<float4*>(stg + ST_CS + lane * 32) =
+                make_float4(bf16lo(fcs.x), bf16hi(fcs.x), bf16lo(fcs.y), bf16hi(fcs.y));
+            *reinterpret_cast<float4*>(stg + ST_CS + lane * 32 + 16) =
+                make_float4(bf16lo(fcs.z), bf16hi(fcs.z), bf16lo(fcs.w), bf16hi(fcs.w));
+        }
         if (lane < 8) {                               // column scales widened to f32 once
             *reinterpret_cast<float4*>(stg + ST_VS + lane * 32) =
                 make_float4(bf16lo(fvs.x), bf16hi(fvs.x), bf16lo(fvs.y), bf16hi(fvs.y));
@@ -345,31 +350,56 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
                 acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, qt[page >> 1][page & 1], acc, 0, 0, 0);
                 acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, qt[page >> 1][2 + (page & 1)], acc, 0, 0, 0);
             }
-            const uint2 csw = *reinterpret_cast<const uint2*>(stg + ST_CS + (gi * PPM + psub_l) * 32 + kg * 8);
-            return v4f{acc[0] * bf16lo(csw.x), acc[1] * bf16hi(csw.x), acc[2] * bf16lo(csw.y),
-                       acc[3] * bf16hi(csw.y)};
+            const float4 csf = *reinterpret_cast<const float4*>(stg + ST_CS + (gi * PPM + psub_l) * 64 + kg * 16);
+            return v4f{acc[0] * csf.x, acc[1] * csf.y, acc[2] * csf.z, acc[3] * csf.w};
         };
         // 16-token LSE taken relative to the centroid term: tok - mud =
         // cs * acc.  The exp2 sum is exact whenever it lies in [2^-60, 2^60]
         // (no overflow; flushed terms < 2^-62 of the sum).  All groups are
         // formed first (independent matrix-core chains interleave), then one
         // wave-wide test picks this fast form or the exact-max recomputation.
-        float ev[NGRP], Sv[NGRP];
-        bool ok = true;
+        // Per-lane partial sums (4 tokens) of every group, then one
+        // transposing reduction per 4 groups: two row-pair swaps and one
+        // half swap leave group 4s + kg's 16-token total in row kg (same
+        // pairing and order as a per-group butterfly, so the same bits).
+        // Each lane then finishes only its own row's group.
+        constexpr int NSET = (NGRP + 3) / 4;
+        float ev[NGRP];
 #pragma unroll
         for (int gi = 0; gi < NGRP; ++gi) {
             const v4f x = tok_group(gi);
-            float e = __builtin_amdgcn_exp2f(x[0]) + __builtin_amdgcn_exp2f(x[1]) +
-                      __builtin_amdgcn_exp2f(x[2]) + __builtin_amdgcn_exp2f(x[3]);
-            e = xor32_sum(xor16_sum(e));
-            ev[gi] = e;
-            ok = ok && (e >= 0x1p-60f) && (e <= 0x1p60f);
+            ev[gi] = __builtin_amdgcn_exp2f(x[0]) + __builtin_amdgcn_exp2f(x[1]) +
+                     __builtin_amdgcn_exp2f(x[2]) + __builtin_amdgcn_exp2f(x[3]);
         }
+        float tot[NSET];
+#pragma unroll
+        for (int st = 0; st < NSET; ++st) {
+            auto pair16 = [](float u, float v) {
+                const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(u), __float_as_uint(v), false, false);
+                return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+            };
+            if constexpr (NGRP >= 4) {
+                const float A = pair16(ev[4 * st], ev[4 * st + 1]);      // rows: g0 01, g1 01, g0 23, g1 23
+                const float B = pair16(ev[4 * st + 2], ev[4 * st + 3]);  // rows: g2 01, g3 01, g2 23, g3 23
+                const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(A), __float_as_uint(B), false, false);
+                tot[st] = __uint_as_float(r[0]) + __uint_as_float(r[1]); // row k: group 4 st + k
+            } else {
+                tot[st] = xor32_sum(pair16(ev[0], ev[1]));               // row k: group k & 1
+            }
+        }
+        auto grp_of = [&](int st) { return (NGRP >= 4) ? 4 * st + kg : (kg & 1); };
+        bool ok = true;
+#pragma unroll
+        for (int st = 0; st < NSET; ++st) ok = ok && (tot[st] >= 0x1p-60f) && (tot[st] <= 0x1p60f);
+        float Sv[NSET];
         if (__builtin_expect(__ballot(!ok) == 0ull, 1)) {
 #pragma unroll
-            for (int gi = 0; gi < NGRP; ++gi)
-                Sv[gi] = (mud_w[(gi * PPM + psub_l) * 16 + g_l] + __builtin_amdgcn_logf(ev[gi])) * 0.6931471805599453f;
+            for (int st = 0; st < NSET; ++st)
+                Sv[st] = (mud_w[(grp_of(st) * PPM + psub_l) * 16 + g_l] + __builtin_amdgcn_logf(tot[st])) *
+                         0.6931471805599453f;
         } else {
+            // exact-max form (rare): every lane computes every group
+            float Sa[NGRP];
 #pragma unroll
             for (int gi = 0; gi < NGRP; ++gi) {
                 const v4f x = tok_group(gi);
@@ -377,23 +407,32 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
                 float f = __builtin_amdgcn_exp2f(x[0] - m) + __builtin_amdgcn_exp2f(x[1] - m) +
                           __builtin_amdgcn_exp2f(x[2] - m) + __builtin_amdgcn_exp2f(x[3] - m);
                 f = xor32_sum(xor16_sum(f));
-                Sv[gi] = ((mud_w[(gi * PPM + psub_l) * 16 + g_l] + m) + __builtin_amdgcn_logf(f)) * 0.6931471805599453f;
+                Sa[gi] = ((mud_w[(gi * PPM + psub_l) * 16 + g_l] + m) + __builtin_amdgcn_logf(f)) * 0.6931471805599453f;
+            }
+#pragma unroll
+            for (int st = 0; st < NSET; ++st) {
+                float v = Sa[0];
+#pragma unroll
+                for (int gi = 1; gi < NGRP; ++gi) v = (grp_of(st) == gi) ? Sa[gi] : v;
+                Sv[st] = v;
             }
         }
         float tmax = -INFINITY;
+        const bool row_owner = (NGRP >= 4) || (kg < 2);      // rows 2, 3 repeat rows 0, 1
 #pragma unroll
-        for (int gi = 0; gi < NGRP; ++gi) {
-            const int page = gi * PPM + psub_l;
-            if ((page < nvalid) && (g_l < G)) {
-                tmax = fmaxf(tmax, Sv[gi]);
-                if (lane < 16) score_h[(((long)r * n_kv + h) * G + g_l) * (long)MP + p0 + page] = Sv[gi];
+        for (int st = 0; st < NSET; ++st) {
+            const int page = grp_of(st) * PPM + psub_l;
+            if (row_owner && (page < nvalid) && (g_l < G)) {
+                tmax = fmaxf(tmax, Sv[st]);
+                score_h[(((long)r * n_kv + h) * G + g_l) * (long)MP + p0 + page] = Sv[st];
             }
         }
-        // this unit's per-head maxima -> LDS (ordered-uint atomic max)
+        // this unit's per-head maxima -> LDS (ordered-uint atomic max), one
+        // atomic per head column per row
 #pragma unroll
         for (int o = GW; o < 16; o <<= 1)    // max over the lanes of one head column
             tmax = fmaxf(tmax, o == 4 ? row_ror<4>(tmax) : o == 8 ? row_ror<8>(tmax) : row_ror<2>(tmax));
-        if (lane < GW && lane < G) atomicMax(&wmax[h][lane], f2u(tmax));
+        if (row_owner && (lane & 15) < GW && (lane & 15) < G) atomicMax(&wmax[h][lane & 15], f2u(tmax));
         wave_lds_sync();                               // staging reused by the next unit
     }
     __syncthreads();

@@ -96,6 +96,41 @@ def test_score_matches_oracle(n_kv, G, ctx):
                 assert pm[0, kh, z, g] == exp
 
 
+@pytest.mark.parametrize("n_kv,G", [(8, 4), (2, 16)])
+def test_score_q_quantisation_ties(n_kv, G):
+    """q rows whose q / qs quotients are exact half-integers (qs = 2^-4): the
+    scorer must round them to even exactly as the reference's rint does.  A
+    half-away-from-zero quantiser would move the scores by far more than the
+    tolerance (checked on the oracle), so the test pins the tie path."""
+    import torch
+    from locks.selection import derive_page_params, rki4_score_only
+    say("score q ties", n_kv, G)
+    case = make_case(11, n_kv, G, [4096])
+    rng = np.random.default_rng(12)
+    H, d = n_kv * G, case.d
+    k = rng.integers(-120, 120, size=(1, H, d))
+    qv = (k + 0.5) / 16.0                                 # every quotient a tie
+    qv[:, :, 0] = 127.0 / 16.0                             # row max -> qs = 2^-4
+    away = np.where(k >= 0, k + 1, k) / 16.0               # ties rounded away from 0
+    away[:, :, 0] = 127.0 / 16.0
+    case.q = O.f32_to_bf16(qv.astype(np.float32))
+    assert np.array_equal(O.bf16_to_f32(case.q), qv.astype(np.float32))   # bf16-exact
+    q_away = O.f32_to_bf16(away.astype(np.float32))
+    st = _state(case)
+    load_slabs(st, 0, case.slabs)
+    dv = to_dev(case)
+    derive_page_params(st, dv["sl"], case.R)
+    rki4_score_only(st, 0, dv["q"], dv["bt"], dv["sl"], case.R, case.scale)
+    torch.cuda.synchronize()
+    npg, nsh, b = _derive_np(case, st)
+    P = int(nsh[0])
+    ref = O.score_rki4_twin(case.q, case.slabs, case.bt, nsh, n_kv, G, case.scale, case.MP)
+    ref_away = O.score_rki4_twin(q_away, case.slabs, case.bt, nsh, n_kv, G, case.scale, case.MP)
+    got = st.score_h.cpu().numpy()
+    assert np.abs(ref_away[..., :P] - ref[..., :P]).max() > 1e-3
+    assert np.abs(got[..., :P] - ref[..., :P]).max() <= 2e-5
+
+
 def _random_select_inputs(seed, n_kv, G, seq_lens, MP, st, ties=None):
     """Upload a synthetic score_h + consistent per-chunk maxima."""
     import torch
