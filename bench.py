@@ -480,6 +480,33 @@ def run_mla(a, wl):
     print(json.dumps(line), flush=True)
 
 
+def run_ladder(a, wl):
+    """Sparse vs dense decode step over a context ladder (BASELINE configs[2]'s
+    dense comparison at 16K..1M): one JSON line per context, same model shape."""
+    import torch
+    for ctx in [int(c) for c in a.ladder.split(",") if c]:
+        w = dict(wl, seq_lens=[ctx])
+        m = make_model(w, a.budget_pages, summaries=a.summaries, zsplit=a.zsplit or None)
+        out = [torch.empty(m["R"], m["n_kv"] * m["G"], D, dtype=torch.bfloat16, device="cuda")
+               for _ in range(m["L"])]
+        g_sparse = capture(lambda: sparse_step(m, out))
+        ms = time_graph(g_sparse, a.steps, a.warmup)
+        dn = make_dense(m)
+        outd = [torch.empty_like(o) for o in out]
+        g_dense = capture(lambda: dense_step(m, dn, outd))
+        ms_dense = time_graph(g_dense, max(3, a.steps // 5), 2)
+        by = step_bytes(m)
+        print(json.dumps({"ladder": a.workload, "ctx": ctx, "layers": m["L"],
+                          "attended_pages_per_kv_head": int(m["st"].page_cnt[0, 0].item()),
+                          "sparse_ms_per_step": round(ms, 4), "dense_ms_per_step": round(ms_dense, 4),
+                          "speedup_vs_dense": round(ms_dense / ms, 3),
+                          "dense_achieved_GBps": round(by["dense"] / (ms_dense * 1e-3) / 1e9, 1)}),
+              flush=True)
+        del g_sparse, g_dense, dn, outd, out, m
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -496,6 +523,9 @@ def main():
                     help="1: one-launch decode (last split merges), 0: split + merge launches")
     ap.add_argument("--calib-copy", type=int, default=0,
                     help="only run N device copies of 1 GiB (PMC byte-counter calibration)")
+    ap.add_argument("--ladder", default="",
+                    help="comma-separated contexts (tokens): one sparse + dense line per context, "
+                         "e.g. 16384,131072,262144,524288,1048576 (single-request GQA workloads)")
     ap.add_argument("--profile-scorer", type=int, default=0,
                     help="only launch the scorer N times per layer (for rocprof)")
     a = ap.parse_args()
@@ -520,6 +550,9 @@ def main():
         _dec.PPS_MIN_OVERRIDE = a.pps_min
     if a.fused_decode >= 0:
         _dec.FUSED_MERGE = bool(a.fused_decode)
+    if a.ladder:
+        run_ladder(a, wl)
+        return
     t0 = time.perf_counter()
     m = make_model(wl, a.budget_pages, summaries=a.summaries, zsplit=a.zsplit or None)
     log(f"model ready in {time.perf_counter() - t0:.1f}s (summary build {m['build_s']:.1f}s)")

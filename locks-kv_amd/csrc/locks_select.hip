@@ -356,7 +356,10 @@ __device__ int reg_emit(const uint32_t (&key)[E], const bool (&val)[E], const Ra
 // ---------------------------------------------------------------------------
 constexpr int ROW_BLK = 1024;
 constexpr int ROW_NW = ROW_BLK / kWave;
-constexpr int ROW_MAXP = 16 * ROW_BLK;
+// Above 8192 pages a row's score_h (G x pages x 4 B) through one CU is
+// slower than the page-parallel route (measured: 16384 pages, G = 4: 22.4 vs
+// 20.5 us; G = 16: 44.8 vs 25.7 us).
+constexpr int ROW_MAXP = 8 * ROW_BLK;
 
 template <int E>
 __global__ __launch_bounds__(ROW_BLK) void sel_row_kernel(
@@ -892,8 +895,7 @@ extern "C" int32_t locks_select_nrm_topb(
                            page_max, score_chunks, n_pages, n_sel_hi, b_fix, score, page_table, \
                            page_cnt, n_sink, max_pages, G, combine)
         if (max_pages <= 4 * ROW_BLK) ROW_LAUNCH(4);
-        else if (max_pages <= 8 * ROW_BLK) ROW_LAUNCH(8);
-        else ROW_LAUNCH(16);
+        else ROW_LAUNCH(8);
 #undef ROW_LAUNCH
         return check_launch("sel_row_kernel");
     }
