@@ -108,10 +108,29 @@ __global__ __launch_bounds__(ML_BLK) void mla_score_kernel(
         for (int e = 0; e < 8; ++e) am = fmaxf(am, fabsf(a[e]));
         am = wave_max(am);
         const float qs = fmaxf(am, 1e-8f) / 127.f;
+        // rint(a / qs) with the correctly rounded quotient: a * (1 / qs) is
+        // within 2 ulp of it and decides the rounding unless it lies within
+        // 2^-15 of a half-integer; those (rare) lanes redo the division
+        const float inv = 1.f / qs;
+        int iv[8];
+        bool near = false;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float y = a[e] * inv;
+            const float ry = rintf(y);
+            near |= fabsf(fabsf(y - ry) - 0.5f) < 0x1p-15f;
+            iv[e] = (int)ry;
+        }
+        if (__builtin_expect(__ballot(near) != 0ull, 0)) {
+            if (near) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) iv[e] = (int)rintf(__fdiv_rn(a[e], qs));
+            }
+        }
         uint32_t pk[2] = {0u, 0u};
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const int v = (h < H) ? (int)rintf(__fdiv_rn(a[e], qs)) : 0;
+            const int v = (h < H) ? iv[e] : 0;
             pk[e >> 2] |= ((uint32_t)(uint8_t)v) << (8 * (e & 3));
         }
         *reinterpret_cast<uint2*>(&q8s[h][8 * lane]) = make_uint2(pk[0], pk[1]);

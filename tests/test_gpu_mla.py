@@ -86,6 +86,42 @@ def test_mla_score_matches_oracle(seq_lens, H):
         assert np.all(got[r, P:] == 123.0)                       # never written past n_sel_hi
 
 
+def test_mla_score_q_quantisation_ties():
+    """Latent q rows whose q / qs quotients are exact half-integers (qs =
+    2^-4) must round to even like the reference's rint; rounding half away
+    from zero would move the page scores ~50x past the tolerance (checked on
+    the oracle)."""
+    import torch
+    from locks.selection import mla_derive, mla_score_only
+    say("score q ties")
+    c = _case(13, [16 * 40 + 5], 16)
+    rng = np.random.default_rng(14)
+    k = rng.integers(-120, 120, size=(1, 16, LKV))
+    q = O.bf16_to_f32(c["q"]).copy()
+    q_tie, q_away = q.copy(), q.copy()
+    q_tie[:, :, :LKV] = (k + 0.5) / 16.0
+    q_away[:, :, :LKV] = np.where(k >= 0, k + 1, k) / 16.0
+    q_tie[:, :, 0] = q_away[:, :, 0] = 127.0 / 16.0        # row max -> qs = 2^-4
+    c["q"] = O.f32_to_bf16(q_tie.astype(np.float32))
+    assert np.array_equal(O.bf16_to_f32(c["q"])[:, :, :LKV], q_tie[:, :, :LKV].astype(np.float32))
+    d = _dev(c)
+    st = _state(c, budget=32)
+    slabs = M.mla_build_summaries(c["cache"], _blocks_of(c), c["NB"])
+    _upload_slabs(st, slabs)
+    mla_derive(st, d["sl"], c["R"])
+    mla_score_only(st, 0, d["q"], d["cache"], d["bt"], c["R"], 0.07)
+    torch.cuda.synchronize()
+    npg, nsh, b = M.mla_derive(c["sl"], PAGE, 10, 1, 32)
+    P = int(nsh[0])
+    ref = M.mla_score_rki4(c["q"], slabs, c["cache"], c["bt"], nsh, 0.07, c["MP"])[0, :P]
+    away = M.mla_score_rki4(O.f32_to_bf16(q_away.astype(np.float32)), slabs, c["cache"], c["bt"],
+                            nsh, 0.07, c["MP"])[0, :P]
+    tol = 2e-4 * max(1.0, np.abs(ref).max())
+    assert np.abs(away - ref).max() > 10 * tol
+    got = st.score_h[0, 0, 0, :P].cpu().numpy()
+    assert np.abs(got - ref).max() <= tol
+
+
 def test_mla_build_matches_oracle_through_the_score():
     """Eigenvectors agree only up to sign/rotation, so the GPU-built latent
     summary is compared through the oracle score it produces."""
