@@ -176,6 +176,12 @@ __global__ __launch_bounds__(DC_BLK) void decode_split_kernel(
     const int sp = blockIdx.x, kh = blockIdx.y, r = blockIdx.z;
     const int n_kv = gridDim.y;
     const long rk = (long)r * n_kv + kh;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int* prow = ptab + (long)r * pt_sr + (long)kh * pt_sh;
+    // This wave's first page ids assuming pps == pps_min (the usual sparse
+    // case), loaded together with the page count instead of after it.
+    const int js = sp * pps_min + wave + DC_WAVES * lane;
+    const int pt_spec = (js < pt_cols) ? prow[js] : 0;
     const int cnt = min(pcnt[(long)r * cnt_sr + kh], pt_cols);
     const int pps = max(cdiv(cnt, split), pps_min);
     const int j0 = sp * pps;
@@ -193,7 +199,6 @@ __global__ __launch_bounds__(DC_BLK) void decode_split_kernel(
     if (j0 >= cnt) return;                        // inactive split: no store
     const int j1 = min(j0 + pps, cnt);
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int c16 = lane & 15, kg = lane >> 4;
     const int seq_len = seq_lens[r];
 
@@ -214,19 +219,18 @@ __global__ __launch_bounds__(DC_BLK) void decode_split_kernel(
         }
     }
 
-    const int* prow = ptab + (long)r * pt_sr + (long)kh * pt_sh;
     // DMA page j into stage `st`: K slot s (0..3) = K[t = lane&15][32 s + 8 kg ..],
     // V slot v (0..3) = V[4 kg + v][8 (lane&15) ..]
     // Page and block ids of up to 64 steps of this wave are fetched up front
     // (lane i holds step i), so no dependent id load sits behind a stage's
     // DMA in the in-order vmcnt queue.
     int ptv = 0, blkv = 0;
-    auto fetch_ids = [&](int jb) {
+    auto fetch_ids = [&](int jb, bool spec) {
         const int jj = jb + DC_WAVES * lane;
         ptv = 0;
         blkv = 0;
         if (jj < j1) {
-            ptv = prow[jj];
+            ptv = spec ? pt_spec : prow[jj];
             const int ptc = min(max(ptv, 0), bt_cols - 1);
             blkv = min(max(bt[(long)r * bt_sr + ptc], 0), NB - 1);
         }
@@ -307,7 +311,7 @@ __global__ __launch_bounds__(DC_BLK) void decode_split_kernel(
     // ping-pong over the two stages: iteration s issues step s+1 into one
     // stage and consumes step s from the other (one page always in flight)
     for (int jb = j0 + wave; jb < j1; jb += DC_WAVES * kWave) {
-        fetch_ids(jb);
+        fetch_ids(jb, pps == pps_min && jb == j0 + wave);
         __builtin_amdgcn_s_waitcnt(0x0070);   // ids (and q) resident before any DMA
         const int ns = min(kWave, cdiv(j1 - jb, DC_WAVES));   // steps of this batch
         int pt_cur = 0;

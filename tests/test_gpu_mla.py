@@ -175,13 +175,14 @@ def test_mla_select_matches_topb_middle(seq_lens, budget):
         assert cnt[r] == min(P, budget)
 
 
-@pytest.mark.parametrize("seq_lens,budget", [([16 * 60 + 5], 24), ([16 * 30, 16 * 7 + 2], 16),
-                                             ([16 * 2048], 128)])
-def test_mla_decode_matches_oracle(seq_lens, budget):
+@pytest.mark.parametrize("seq_lens,budget,H", [([16 * 60 + 5], 24, 16), ([16 * 30, 16 * 7 + 2], 16, 16),
+                                               ([16 * 2048], 128, 16), ([16 * 90 + 3, 16 * 33], 20, 5),
+                                               ([16 * 64], 32, 1)])
+def test_mla_decode_matches_oracle(seq_lens, budget, H):
     import torch
     from locks.backend.mla_attn import mla_forward_mqa
-    say("decode", seq_lens, budget)
-    c = _case(14, seq_lens)
+    say("decode", seq_lens, budget, H)
+    c = _case(14, seq_lens, H)
     d = _dev(c)
     st = _state(c, budget=budget)
     slabs = M.mla_build_summaries(c["cache"], _blocks_of(c), c["NB"])
