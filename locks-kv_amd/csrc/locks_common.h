@@ -85,6 +85,13 @@ __device__ __forceinline__ float wave_max(float v) {
     v = fmaxf(v, row_ror<1>(v));
     return xor32_max(xor16_max(v));
 }
+__device__ __forceinline__ float wave_sum(float v) {
+    v += row_ror<8>(v);
+    v += row_ror<4>(v);
+    v += row_ror<2>(v);
+    v += row_ror<1>(v);
+    return xor32_sum(xor16_sum(v));
+}
 __device__ __forceinline__ int wave_sum_i(int v) {
     v += row_ror<8>(v);
     v += row_ror<4>(v);
@@ -94,6 +101,20 @@ __device__ __forceinline__ int wave_sum_i(int v) {
     v = (int)a[0] + (int)a[1];
     const auto b = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
     return (int)b[0] + (int)b[1];
+}
+
+// Whole-wave inclusive integer prefix sum on DPP (no LDS crossbar trips):
+// Hillis-Steele within each 16-lane row (row_shr 1, 2, 4, 8; lanes whose
+// source falls outside the row keep 0), then row_bcast:15 adds row 0 / 2's
+// totals to rows 1 / 3 and row_bcast:31 adds rows 0-1's total to rows 2-3.
+__device__ __forceinline__ int wave_incl_scan_i(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);
+    return v;
 }
 
 // Order LDS traffic between lanes of ONE wave (no cross-wave barrier).

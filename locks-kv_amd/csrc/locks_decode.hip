@@ -113,8 +113,7 @@ __device__ void merge_row(const float* __restrict__ m_part, const float* __restr
             m_s[sidx * 16 + g] = w;                     // this lane read it last
             lt += l * w;
         }
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) lt += __shfl_xor(lt, o, kWave);
+        lt = wave_sum(lt);
         if (lane == 0) lt_s[g] = lt;
     }
     __syncthreads();

@@ -49,22 +49,12 @@ template <int BLK>
 __device__ __forceinline__ int block_excl_scan(int v, int* wsum, int& total) {
     constexpr int NW = BLK / kWave;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    int incl = v;
-#pragma unroll
-    for (int o = 1; o < kWave; o <<= 1) {
-        const int t = __shfl_up(incl, o, kWave);
-        if (lane >= o) incl += t;
-    }
+    const int incl = wave_incl_scan_i(v);
     if (lane == kWave - 1) wsum[w] = incl;
     __syncthreads();
     if (w == 0) {
         const int x = (lane < NW) ? wsum[lane] : 0;
-        int xi = x;
-#pragma unroll
-        for (int o = 1; o < kWave; o <<= 1) {
-            const int t = __shfl_up(xi, o, kWave);
-            if (lane >= o) xi += t;
-        }
+        const int xi = wave_incl_scan_i(x);
         if (lane < NW) wsum[lane] = xi - x;
         if (lane == NW - 1) wsum[NW] = xi;
     }
@@ -82,8 +72,8 @@ __device__ __forceinline__ void hist_add(int* hist, int bin, bool valid) {
     const int lane = threadIdx.x & 63;
     const unsigned long long act = __ballot(valid);
     if (act == 0ull) return;
-    const int leader = __ffsll((long long)act) - 1;
-    const int b0 = __shfl(bin, leader, kWave);
+    const int leader = __ffsll((long long)act) - 1;       // wave-uniform
+    const int b0 = __builtin_amdgcn_readlane(bin, leader);
     const bool same = valid && bin == b0;
     const unsigned long long m = __ballot(same);
     if (lane == leader) atomicAdd(&hist[b0], __popcll(m));
@@ -286,16 +276,12 @@ __device__ RadixSel reg_kth_largest(const uint32_t (&key)[E], const bool (&val)[
         int c = 0;
 #pragma unroll
         for (int j = 0; j < BPL; ++j) c += (top - j >= 0) ? hist[top - j] : 0;
-        int incl = c;
-#pragma unroll
-        for (int o = 1; o < kWave; o <<= 1) {
-            const int t = __shfl_up(incl, o, kWave);
-            if (lane >= o) incl += t;
-        }
+        const int incl = wave_incl_scan_i(c);
         if (lane == kWave - 1) wtot[wave] = incl;
         __syncthreads();
-        int base = 0;
-        for (int w = 0; w < wave && w < NW; ++w) base += wtot[w];
+        // counts of the waves before this one: one parallel LDS read and a
+        // wave sum (a serial loop would chain up to NW - 1 LDS latencies)
+        const int base = wave_sum_i((lane < wave) ? wtot[lane] : 0);
         const int above0 = base + incl - c;
         if (c > 0 && above0 < rs.k && rs.k <= base + incl) {
             int above = above0;
