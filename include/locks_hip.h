@@ -28,7 +28,7 @@
 
 #include <stdint.h>
 
-#define LOCKS_ABI_VERSION 1
+#define LOCKS_ABI_VERSION 2
 
 #ifdef __cplusplus
 extern "C" {
@@ -107,17 +107,25 @@ int64_t locks_select_workspace_bytes(int32_t n_req, int32_t n_kv, int32_t max_pa
  *   score      (n_req, n_kv, max_pages) f32, written for p < n_sel_hi
  *   page_table (n_req, n_kv, max_pages) i32: kept pages ascending, -1 after
  *   page_cnt   (n_req, n_kv) i32
- *   workspace  >= locks_select_workspace_bytes(...) bytes (unused when
- *              max_pages <= 2048); calls that overlap on one workspace race.
- * Launches: one chunk kernel (combine + local top-b candidates, or the whole
- * selection when max_pages <= 2048) and one finishing kernel otherwise.
+ *   workspace  >= locks_select_workspace_bytes(...) bytes, zero-filled once
+ *              before its first use (every call leaves its histogram part
+ *              zero again; unused when max_pages <= 2048); calls that
+ *              overlap on one workspace race.
+ *   b_max      host-side upper bound of b_fix (0 = unknown).  Only picks the
+ *              route for rows above 8192 pages: when b_max * chunks exceeds
+ *              4096 candidates, the 2048-page chunks build a row key
+ *              histogram and a second pass emits the pages at or above the
+ *              b-th largest key's bin (one more launch) instead of per-chunk
+ *              top-b lists.  Either route gives the same page tables.
+ * Launches: one kernel for rows of <= 8192 pages; otherwise a chunk kernel
+ * (+ the band pass on the histogram route) and one finishing kernel.
  */
 int32_t locks_select_nrm_topb(const float* score_h, const float* page_max, int32_t score_chunks,
                               const int32_t* n_pages, const int32_t* n_sel_hi,
                               const int32_t* b_fix, float* score, int32_t* page_table,
                               int32_t* page_cnt, void* workspace, int64_t workspace_bytes,
                               int32_t n_req, int32_t n_kv, int32_t G, int32_t n_sink,
-                              int32_t max_pages, int32_t combine, void* stream);
+                              int32_t max_pages, int32_t combine, int32_t b_max, void* stream);
 
 /*
  * Split-K sparse paged decode over the selected pages.

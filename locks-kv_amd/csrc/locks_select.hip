@@ -91,10 +91,18 @@ __device__ uint32_t block_kth_largest(const uint32_t* keys, int n, int k, int* h
         const int shift = 24 - 8 * digit;
         for (int i = tid; i < 256; i += BLK) hist[i] = 0;
         __syncthreads();
-        for (int i = tid; i < n; i += BLK) {
-            const uint32_t u = keys[i];
-            const bool in = (u & kmask) == prefix;
-            hist_add(hist, (u >> shift) & 0xFF, in);
+        // 16 keys per thread in flight per batch (keys may live in global
+        // memory: a key-at-a-time loop would serialize one latency per key)
+        for (int i0 = tid; i0 < n; i0 += 16 * BLK) {
+            uint32_t u[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const int i = i0 + j * BLK;
+                u[j] = (i < n) ? keys[i] : 0u;
+            }
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+                hist_add(hist, (u[j] >> shift) & 0xFF, (i0 + j * BLK < n) && (u[j] & kmask) == prefix);
         }
         __syncthreads();
         if (tid < kWave) {
@@ -141,10 +149,15 @@ __device__ int emit_topk(const uint32_t* keys, int n, int k, uint32_t tau, PageO
     const int E = cdiv(n, BLK);
     const int i0 = min(tid * E, n), i1 = min(i0 + E, n);
     int gt = 0, eq = 0;
-    for (int i = i0; i < i1; ++i) {
-        const uint32_t u = keys[i];
-        gt += (u > tau);
-        eq += (u == tau);
+    for (int b0 = i0; b0 < i1; b0 += 16) {              // 16 loads in flight
+        uint32_t u[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) u[j] = (b0 + j < i1) ? keys[b0 + j] : 0u;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            gt += (b0 + j < i1) && (u[j] > tau);
+            eq += (b0 + j < i1) && (u[j] == tau);
+        }
     }
     int gt_tot, eq_tot;
     block_excl_scan<BLK>(gt, wsum, gt_tot);
@@ -154,14 +167,24 @@ __device__ int emit_topk(const uint32_t* keys, int n, int k, uint32_t tau, PageO
     int total;
     int pos = block_excl_scan<BLK>(mine, wsum, total);
     int er = eq_excl;
-    for (int i = i0; i < i1; ++i) {
-        const uint32_t u = keys[i];
-        bool kp = u > tau;
-        if (u == tau) { kp = er < quota; ++er; }
-        if (kp) {
-            out_page[pos] = page_of(i);
-            if (out_key) out_key[pos] = u;
-            ++pos;
+    for (int b0 = i0; b0 < i1; b0 += 16) {
+        uint32_t u[16];
+        int pg[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            u[j] = (b0 + j < i1) ? keys[b0 + j] : 0u;
+            pg[j] = (b0 + j < i1) ? page_of(b0 + j) : 0;
+        }
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const bool in = b0 + j < i1;
+            bool kp = in && u[j] > tau;
+            if (in && u[j] == tau) { kp = er < quota; ++er; }
+            if (kp) {
+                out_page[pos] = pg[j];
+                if (out_key) out_key[pos] = u[j];
+                ++pos;
+            }
         }
     }
     return total;
@@ -195,14 +218,15 @@ __device__ __forceinline__ void fill_all_pages(int* row, int n_pages, int MP, bo
 
 // Finish one row from the chunk candidates (ascending page order per chunk):
 // exact b-th largest key over all candidates, ordered emission, sink/window.
-// LDS arguments: offs[FIN_MAXZ+1], lkey/lpage[FIN_CAP], hist[256], s3[4], wsum.
+// LDS arguments: offs[FIN_MAXZ+1], lkey/lpage[cap] (more candidates spill to
+// the global workspace), hist[256], s3[4], wsum.
 template <int BLK>
 __device__ void finish_row(long rk, int n_pages, int n_sel_hi, int n_sink, int b, int MP, int Z1,
                            int* __restrict__ trow, int* __restrict__ cnt_out,
                            const uint32_t* __restrict__ cand_key, const int* __restrict__ cand_page,
                            const int* __restrict__ cand_cnt, uint32_t* __restrict__ spill_key,
                            int* __restrict__ spill_page, int* offs, uint32_t* lkey, int* lpage,
-                           int* hist, int* s3, int* wsum) {
+                           int* hist, int* s3, int* wsum, int cap = FIN_CAP) {
     constexpr int NWV = BLK / kWave;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     {
@@ -219,15 +243,26 @@ __device__ void finish_row(long rk, int n_pages, int n_sel_hi, int n_sink, int b
         __syncthreads();
     }
     const int N = offs[Z1];
-    uint32_t* kk = (N <= FIN_CAP) ? lkey : spill_key + rk * (long)MP;
-    int* pp = (N <= FIN_CAP) ? lpage : spill_page + rk * (long)MP;
+    uint32_t* kk = (N <= cap) ? lkey : spill_key + rk * (long)MP;
+    int* pp = (N <= cap) ? lpage : spill_page + rk * (long)MP;
     for (int zz = wave; zz < Z1; zz += NWV) {                 // chunk order == page order
         const int o = offs[zz], c = offs[zz + 1] - o;
         const uint32_t* sk = cand_key + (rk * Z1 + zz) * (long)SEL_CH;
         const int* sp = cand_page + (rk * Z1 + zz) * (long)SEL_CH;
-        for (int i = lane; i < c; i += kWave) {
-            kk[o + i] = sk[i];
-            pp[o + i] = sp[i];
+        for (int i0 = lane; i0 < c; i0 += 8 * kWave) {      // 8 loads in flight
+            uint32_t kv[8];
+            int pv[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int i = i0 + j * kWave;
+                kv[j] = (i < c) ? sk[i] : 0u;
+                pv[j] = (i < c) ? sp[i] : 0;
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int i = i0 + j * kWave;
+                if (i < c) { kk[o + i] = kv[j]; pp[o + i] = pv[j]; }
+            }
         }
     }
     __syncthreads();
@@ -637,15 +672,19 @@ __global__ __launch_bounds__(FIN_BLK) void sel_finish_kernel(
 constexpr int C2_BLK = 512;
 constexpr int C2_E = SEL_CH / C2_BLK;                  // 4
 constexpr int F2_BLK = 1024;
-constexpr int F2_E = 4;
-constexpr int F2_CAP = F2_BLK * F2_E;                  // 4096 candidates
+constexpr int F2_CAP = F2_BLK * 16;                    // register-resident candidates
 
+// BAND = false: emit the chunk's local top-min(b, n) candidates.
+// BAND = true (large budgets): add the chunk's key histogram (top 12 bits)
+// into the row's global histogram instead; sel_band_kernel then emits the
+// candidates at or above the row's boundary bin.
+template <bool BAND>
 __global__ __launch_bounds__(C2_BLK) void sel_chunk2_kernel(
     const float* __restrict__ score_h, const float* __restrict__ pmax, int Zs,
     const int* __restrict__ npg, const int* __restrict__ nsh, const int* __restrict__ bfix,
     float* __restrict__ score, int* __restrict__ page_table,
     uint32_t* __restrict__ cand_key, int* __restrict__ cand_page, int* __restrict__ cand_cnt,
-    int n_sink, int MP, int G, int combine)
+    int* __restrict__ ghist, int n_sink, int MP, int G, int combine)
 {
     const int z = blockIdx.x, kh = blockIdx.y, r = blockIdx.z;
     const int n_kv = gridDim.y, Z1 = gridDim.x;
@@ -715,6 +754,17 @@ __global__ __launch_bounds__(C2_BLK) void sel_chunk2_kernel(
         key[e] = f2u(acc[e]);
         nv += val[e];
     }
+    if constexpr (BAND) {
+        for (int i = tid; i < 4096; i += C2_BLK) hist[i] = 0;
+        __syncthreads();
+#pragma unroll
+        for (int e = 0; e < C2_E; ++e) hist_add(hist, (int)(key[e] >> 20), val[e]);
+        __syncthreads();
+        int* gh = ghist + rk * 4096;
+        for (int i = tid; i < 4096; i += C2_BLK)
+            if (hist[i]) __hip_atomic_fetch_add(gh + i, hist[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
     int n_loc;
     block_excl_scan<C2_BLK>(nv, wsum, n_loc);
     uint32_t* ck = cand_key + (rk * Z1 + z) * (long)SEL_CH;
@@ -732,16 +782,126 @@ __global__ __launch_bounds__(C2_BLK) void sel_chunk2_kernel(
     if (tid == 0) cand_cnt[rk * Z1 + z] = ncand;
 }
 
+// Register-resident finish of one row: candidates j = E t .. E t + E - 1 of
+// the chunk-ordered (= page-ordered) list, located by a binary search over
+// the chunk offsets; exact b-th largest, ordered emission, sink / window.
+template <int E>
+__device__ void finish2_regs(long rk, int N, int Z1, int b, int n_sink, int n_pages,
+                             int n_sel_hi, int* __restrict__ trow, int* __restrict__ page_cnt,
+                             const uint32_t* __restrict__ cand_key, const int* __restrict__ cand_page,
+                             const int* offs, int* hist, int* wtot, int* s3, int* wsum) {
+    const int tid = threadIdx.x;
+    uint32_t key[E];
+    int page[E];
+    bool val[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const int j = E * tid + e;
+        val[e] = j < N;
+        key[e] = 0u;
+        page[e] = 0;
+        if (val[e]) {
+            int lo = 0, hi = Z1;                            // offs[lo] <= j < offs[hi]
+            while (hi - lo > 1) {
+                const int mid = (lo + hi) >> 1;
+                if (offs[mid] <= j) lo = mid; else hi = mid;
+            }
+            const long src = (rk * Z1 + lo) * (long)SEL_CH + (j - offs[lo]);
+            key[e] = cand_key[src];
+            page[e] = cand_page[src];
+        }
+    }
+    const RadixSel rs = reg_kth_largest<F2_BLK, E>(key, val, b, hist, wtot, s3);
+    reg_emit<F2_BLK, E>(key, val, rs, wsum, [&](int pos, int e) { trow[n_sink + pos] = page[e]; });
+    const int cnt = n_sink + b + (n_pages - n_sel_hi);
+    for (int i = tid; i < n_sink; i += F2_BLK) trow[i] = i;
+    for (int i = n_sink + b + tid; i < cnt; i += F2_BLK) trow[i] = n_sel_hi + (i - n_sink - b);
+    if (tid == 0) page_cnt[rk] = cnt;
+}
+
+
+// Large-budget route, second pass: every chunk reads its row's key histogram
+// (complete after sel_chunk2_kernel<true>), finds the boundary bin T (the bin
+// holding the b-th largest key) and emits, in page order, its pages whose
+// key's top 12 bits are >= T -- every globally kept page plus the rest of
+// bin T -- for sel_finish2_kernel.  Keys are re-read from `score`.
+__global__ __launch_bounds__(C2_BLK) void sel_band_kernel(
+    const int* __restrict__ nsh, const int* __restrict__ bfix, const float* __restrict__ score,
+    uint32_t* __restrict__ cand_key, int* __restrict__ cand_page, int* __restrict__ cand_cnt,
+    const int* __restrict__ ghist, int n_sink, int MP)
+{
+    const int z = blockIdx.x, kh = blockIdx.y, r = blockIdx.z;
+    const int n_kv = gridDim.y, Z1 = gridDim.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const long rk = (long)r * n_kv + kh;
+    const int n_sel_hi = min(nsh[r], MP);
+    const int n_sel = n_sel_hi - n_sink;
+    int b = bfix[r];
+    b = max(1, min(b, max(n_sel, 1)));
+    __shared__ int wtot[C2_BLK / kWave];
+    __shared__ int wsum[C2_BLK / kWave + 1];
+    __shared__ int tbin;
+    if (n_sel <= 1 || b >= n_sel) {                     // keep-all rows need no candidates
+        if (tid == 0) cand_cnt[rk * Z1 + z] = 0;
+        return;
+    }
+    // boundary bin: thread t holds bins top .. top - 7 (top = 4095 - 8 t),
+    // ascending threads = descending bins
+    constexpr int BPT = 4096 / C2_BLK;
+    const int top = 4095 - BPT * tid;
+    int c = 0, hb[BPT];
+    const int* gh = ghist + rk * 4096;
+#pragma unroll
+    for (int j = 0; j < BPT; ++j) { hb[j] = gh[top - j]; c += hb[j]; }
+    const int incl = wave_incl_scan_i(c);
+    if (lane == kWave - 1) wtot[wave] = incl;
+    __syncthreads();
+    const int base = wave_sum_i((lane < wave) ? wtot[lane] : 0);
+    const int above0 = base + incl - c;
+    if (c > 0 && above0 < b && b <= base + incl) {
+        int above = above0;
+#pragma unroll
+        for (int j = 0; j < BPT; ++j) {
+            if (above + hb[j] >= b) { tbin = top - j; break; }
+            above += hb[j];
+        }
+    }
+    __syncthreads();
+    const uint32_t T = (uint32_t)tbin;
+    const int p0 = z * SEL_CH + C2_E * tid;
+    uint32_t key[C2_E];
+    int nv = 0;
+    bool kp[C2_E];
+    const float* srow = score + rk * (long)MP;
+#pragma unroll
+    for (int e = 0; e < C2_E; ++e) {
+        const int p = p0 + e;
+        const bool v = p >= n_sink && p < n_sel_hi;
+        key[e] = v ? f2u(srow[p]) : 0u;
+        kp[e] = v && (key[e] >> 20) >= T;
+        nv += kp[e];
+    }
+    int tot;
+    int pos = block_excl_scan<C2_BLK>(nv, wsum, tot);
+    const long cb = (rk * Z1 + z) * (long)SEL_CH;
+#pragma unroll
+    for (int e = 0; e < C2_E; ++e)
+        if (kp[e]) { cand_key[cb + pos] = key[e]; cand_page[cb + pos] = p0 + e; ++pos; }
+    if (tid == 0) cand_cnt[rk * Z1 + z] = tot;
+}
+
 __global__ __launch_bounds__(F2_BLK) void sel_finish2_kernel(
     const int* __restrict__ npg, const int* __restrict__ nsh, const int* __restrict__ bfix,
     int* __restrict__ page_table, int* __restrict__ page_cnt,
     const uint32_t* __restrict__ cand_key, const int* __restrict__ cand_page,
     const int* __restrict__ cand_cnt, uint32_t* __restrict__ spill_key, int* __restrict__ spill_page,
-    int n_sink, int MP, int Z1)
+    int* __restrict__ ghist, int n_sink, int MP, int Z1)
 {
     const int kh = blockIdx.y, r = blockIdx.z;
     const long rk = (long)r * gridDim.y + kh;
     const int tid = threadIdx.x;
+    if (ghist)                          // large-budget route: leave the row histogram zeroed
+        for (int i = tid; i < 4096; i += F2_BLK) ghist[rk * 4096 + i] = 0;
     const int n_pages = min(npg[r], MP);
     const int n_sel_hi = min(nsh[r], MP);
     const int n_sel = n_sel_hi - n_sink;
@@ -767,41 +927,18 @@ __global__ __launch_bounds__(F2_BLK) void sel_finish2_kernel(
         __syncthreads();
     }
     const int N = offs[Z1];
-    if (N > F2_CAP) {                                   // many / large candidate lists
-        __shared__ uint32_t lkey[FIN_CAP];
-        __shared__ int lpage[FIN_CAP];
+    if (N > F2_CAP) {                   // more candidates than registers: global spill
         finish_row<F2_BLK>(rk, n_pages, n_sel_hi, n_sink, b, MP, Z1, trow, page_cnt + rk, cand_key,
-                           cand_page, cand_cnt, spill_key, spill_page, offs, lkey, lpage, hist, s3,
-                           wsum);
+                           cand_page, cand_cnt, spill_key, spill_page, offs, nullptr, nullptr, hist,
+                           s3, wsum, 0);
         return;
     }
-    // candidates j = 4 t .. 4 t + 3 of the chunk-ordered (= page-ordered) list
-    uint32_t key[F2_E];
-    int page[F2_E];
-    bool val[F2_E];
-#pragma unroll
-    for (int e = 0; e < F2_E; ++e) {
-        const int j = F2_E * tid + e;
-        val[e] = j < N;
-        key[e] = 0u;
-        page[e] = 0;
-        if (val[e]) {
-            int lo = 0, hi = Z1;                            // offs[lo] <= j < offs[hi]
-            while (hi - lo > 1) {
-                const int mid = (lo + hi) >> 1;
-                if (offs[mid] <= j) lo = mid; else hi = mid;
-            }
-            const long src = (rk * Z1 + lo) * (long)SEL_CH + (j - offs[lo]);
-            key[e] = cand_key[src];
-            page[e] = cand_page[src];
-        }
-    }
-    const RadixSel rs = reg_kth_largest<F2_BLK, F2_E>(key, val, b, hist, wtot, s3);
-    reg_emit<F2_BLK, F2_E>(key, val, rs, wsum, [&](int pos, int e) { trow[n_sink + pos] = page[e]; });
-    const int cnt = n_sink + b + (n_pages - n_sel_hi);
-    for (int i = tid; i < n_sink; i += F2_BLK) trow[i] = i;
-    for (int i = n_sink + b + tid; i < cnt; i += F2_BLK) trow[i] = n_sel_hi + (i - n_sink - b);
-    if (tid == 0) page_cnt[rk] = cnt;
+    if (N <= F2_BLK * 4)
+        finish2_regs<4>(rk, N, Z1, b, n_sink, n_pages, n_sel_hi, trow, page_cnt, cand_key,
+                        cand_page, offs, hist, wtot, s3, wsum);
+    else
+        finish2_regs<16>(rk, N, Z1, b, n_sink, n_pages, n_sel_hi, trow, page_cnt, cand_key,
+                         cand_page, offs, hist, wtot, s3, wsum);
 }
 
 // ---------------------------------------------------------------------------
@@ -840,7 +977,8 @@ extern "C" int64_t locks_select_workspace_bytes(int32_t n_req, int32_t n_kv, int
     const long cand = rows * Z1 * SEL_CH;               // key + page per slot
     const long spill = rows * (long)max_pages;           // key + page per page
     const long counts = rows * Z1;
-    long bytes = cand * 8 + spill * 8 + counts * 4;
+    const long hists = rows * 4096;                      // large-budget row histograms
+    long bytes = cand * 8 + spill * 8 + counts * 4 + hists * 4;
     return (bytes + 255) / 256 * 256;
 }
 
@@ -850,7 +988,7 @@ extern "C" int32_t locks_select_nrm_topb(
     float* score, int32_t* page_table, int32_t* page_cnt,
     void* workspace, int64_t workspace_bytes,
     int32_t n_req, int32_t n_kv, int32_t G, int32_t n_sink, int32_t max_pages,
-    int32_t combine, void* stream)
+    int32_t combine, int32_t b_max, void* stream)
 {
     LOCKS_REQUIRE(G >= 1 && G <= 16, "locks_select_nrm_topb: G=%d outside [1, 16]", G);
     LOCKS_REQUIRE(n_req >= 0 && n_kv >= 1 && max_pages >= 1, "locks_select_nrm_topb: bad geometry");
@@ -875,6 +1013,7 @@ extern "C" int32_t locks_select_nrm_topb(
     uint32_t* spill_key = (uint32_t*)(ws + rows * Z1 * SEL_CH * 8);
     int* spill_page = (int*)(ws + rows * Z1 * SEL_CH * 8 + rows * (long)max_pages * 4);
     int* cand_cnt = (int*)(ws + rows * Z1 * SEL_CH * 8 + rows * (long)max_pages * 8);
+    int* ghist = cand_cnt + rows * Z1;
     if (max_pages <= ROW_MAXP && max_pages % 4 == 0 && max_pages > SEL_CH) {
 #define ROW_LAUNCH(EV)                                                                     \
         hipLaunchKernelGGL((sel_row_kernel<EV>), dim3(n_kv, n_req), dim3(ROW_BLK), 0, st, score_h, \
@@ -886,14 +1025,34 @@ extern "C" int32_t locks_select_nrm_topb(
         return check_launch("sel_row_kernel");
     }
     if (Z1 > 1 && max_pages % 4 == 0) {
-        hipLaunchKernelGGL(sel_chunk2_kernel, dim3(Z1, n_kv, n_req), dim3(C2_BLK), 0, st,
-                           score_h, page_max, score_chunks, n_pages, n_sel_hi, b_fix, score,
-                           page_table, cand_key, cand_page, cand_cnt, n_sink, max_pages, G, combine);
-        int rc = check_launch("sel_chunk2_kernel");
-        if (rc) return rc;
+        // Local top-b lists of every chunk past the 4-per-thread finisher:
+        // the histogram (band) route is faster (measured at 256K..1M with
+        // b = 1638..6553: 25-36 us against 40-160 us).
+        const bool band = (long)b_max * Z1 > F2_BLK * 4;
+        if (band) {
+            hipLaunchKernelGGL(sel_chunk2_kernel<true>, dim3(Z1, n_kv, n_req), dim3(C2_BLK), 0, st,
+                               score_h, page_max, score_chunks, n_pages, n_sel_hi, b_fix, score,
+                               page_table, cand_key, cand_page, cand_cnt, ghist, n_sink, max_pages,
+                               G, combine);
+            int rc = check_launch("sel_chunk2_kernel<band>");
+            if (rc) return rc;
+            hipLaunchKernelGGL(sel_band_kernel, dim3(Z1, n_kv, n_req), dim3(C2_BLK), 0, st,
+                               n_sel_hi, b_fix, score, cand_key, cand_page, cand_cnt, ghist, n_sink,
+                               max_pages);
+            rc = check_launch("sel_band_kernel");
+            if (rc) return rc;
+        } else {
+            hipLaunchKernelGGL(sel_chunk2_kernel<false>, dim3(Z1, n_kv, n_req), dim3(C2_BLK), 0, st,
+                               score_h, page_max, score_chunks, n_pages, n_sel_hi, b_fix, score,
+                               page_table, cand_key, cand_page, cand_cnt, nullptr, n_sink, max_pages,
+                               G, combine);
+            int rc = check_launch("sel_chunk2_kernel");
+            if (rc) return rc;
+        }
         hipLaunchKernelGGL(sel_finish2_kernel, dim3(1, n_kv, n_req), dim3(F2_BLK), 0, st,
                            n_pages, n_sel_hi, b_fix, page_table, page_cnt, cand_key, cand_page,
-                           cand_cnt, spill_key, spill_page, n_sink, max_pages, Z1);
+                           cand_cnt, spill_key, spill_page, band ? ghist : nullptr, n_sink,
+                           max_pages, Z1);
         return check_launch("sel_finish2_kernel");
     }
     hipLaunchKernelGGL(sel_chunk_kernel, dim3(Z1, n_kv, n_req), dim3(SEL_BLK), 0, st,

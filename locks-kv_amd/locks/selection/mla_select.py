@@ -83,7 +83,7 @@ def mla_select_only(st, n_req: int) -> None:
         _lib.ptr(st.score_h), None, 0, _lib.ptr(st.n_pages), _lib.ptr(st.n_sel_hi),
         _lib.ptr(st.b_fix), _lib.ptr(st.score), _lib.ptr(st.page_table), _lib.ptr(st.page_cnt),
         _lib.ptr(st.sel_ws), st.sel_ws.numel(), int(n_req), 1, 1, int(st.sink_pages),
-        int(st.max_pages), 1, _lib.stream_ptr(st.score.device)), "mla select")
+        int(st.max_pages), 1, int(st.budget_abs), _lib.stream_ptr(st.score.device)), "mla select")
 
 
 def mla_select_pages(st, layer: int, q, kv_cache, block_table, seq_lens, n_req: int,

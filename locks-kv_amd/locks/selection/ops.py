@@ -66,7 +66,8 @@ def rki4_select_only(st, n_req: int) -> None:
         _lib.ptr(st.n_pages), _lib.ptr(st.n_sel_hi), _lib.ptr(st.b_fix),
         _lib.ptr(st.score), _lib.ptr(st.page_table), _lib.ptr(st.page_cnt),
         _lib.ptr(st.sel_ws), st.sel_ws.numel(), int(n_req), int(st.n_kv), int(st.G),
-        int(st.sink_pages), int(st.max_pages), combine, _lib.stream_ptr(st.score.device)),
+        int(st.sink_pages), int(st.max_pages), combine, int(st.b_max),
+        _lib.stream_ptr(st.score.device)),
         "select_nrm_topb")
 
 

@@ -22,6 +22,8 @@ d=128, page 16) + 16 B tag (rki4_state.py:18-22, record_bytes :124-141).
 """
 from __future__ import annotations
 
+import math
+
 import torch
 
 from .. import _lib
@@ -59,6 +61,10 @@ class Rki4State:
         self.max_reqs, self.max_pages = R, MP
         self.budget = float(budget)
         self.budget_abs = int(budget_pages or 0)
+        # upper bound of the per-row budget b (derive_page_params), passed to
+        # the selector so that large budgets take its histogram route
+        self.b_max = self.budget_abs if self.budget_abs > 0 else \
+            int(math.ceil(self.budget * max_pages))
         self.sink_pages, self.window_pages = int(sink_pages), int(window_pages)
         self.combine = combine
         self.device = torch.device(device)

@@ -166,7 +166,9 @@ def _random_select_inputs(seed, n_kv, G, seq_lens, MP, st, ties=None):
     ([1 << 20], 2, 16, 126),         # 1M context, 32 chunks
     ([262144, 196608, 131072, 65536], 2, 16, 126),   # ragged batch
     ([100000], 2, 4, 5000),          # large b (spills past the LDS cap)
-    ([400000], 2, 4, 5000),          # register chunks, finish over > 4096 candidates (spill)
+    ([400000], 2, 4, 5000),          # histogram (band) route: b * chunks > register finisher
+    ([1 << 20], 2, 16, 6553),        # 1M at the default 10 % budget: band route
+    ([262144], 2, 16, 1638),         # 16 candidates per thread in the finisher
     ([40, 17, 0, 33], 2, 4, 126),    # short rows, padded row, keep-all
 ])
 def test_select_matches_oracle(combine, seq_lens, n_kv, G, bp):
@@ -218,15 +220,15 @@ def test_select_matches_oracle(combine, seq_lens, n_kv, G, bp):
 
 
 @pytest.mark.parametrize("ties", ["all_equal", "bands", "underflow"])
-@pytest.mark.parametrize("ctx", [16384, 131072, 1 << 19])
-def test_select_tie_batteries(ties, ctx):
+@pytest.mark.parametrize("ctx,bp", [(16384, 126), (131072, 126), (1 << 19, 126), (1 << 19, 3000)])
+def test_select_tie_batteries(ties, ctx, bp):
     import torch
     from locks.selection import derive_page_params, rki4_select_only
-    say("ties", ties, ctx)
+    say("ties", ties, ctx, bp)
     n_kv, G = 2, 8
     case = make_case(3, n_kv, G, [ctx], kv=False)
     for combine in ("max", "nrm"):
-        st = _state(case, budget_pages=126, combine=combine)
+        st = _state(case, budget_pages=bp, combine=combine)
         d = to_dev(case)
         derive_page_params(st, d["sl"], 1)
         sh, npg, nsh, b = _random_select_inputs(4, n_kv, G, [ctx], case.MP, st, ties=ties)

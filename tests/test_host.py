@@ -41,7 +41,7 @@ def test_rejects_bad_geometry_without_device():
                                    8, 1, 1, 1, 1, 1, 2, 17, 128, 16, 4, 1, 0.1, None]))
     assert rc == -1 and b"G=17" in lib.locks_last_error()
     # two chunks (max_pages 4096) need the candidate workspace: rejected pre-launch
-    rc = lib.locks_select_nrm_topb(*([1, 1, 1] + [1] * 7 + [0, 1, 2, 4, 1, 4096, 0, None]))
+    rc = lib.locks_select_nrm_topb(*([1, 1, 1] + [1] * 7 + [0, 1, 2, 4, 1, 4096, 0, 0, None]))
     assert rc == -1 and b"workspace" in lib.locks_last_error()
     rc = lib.locks_derive_params(1, 1, 16, 0, 1, 0, 0.1, 1, 1, 1, None)
     assert rc == -1 and b"window" in lib.locks_last_error()
