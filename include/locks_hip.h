@@ -79,7 +79,7 @@ int32_t locks_score_num_chunks(int32_t max_pages, int32_t chunk);
  *   score_h    (n_req, n_kv, G, max_pages) f32 -- written for p < n_sel_hi only
  *   page_max   (n_req, n_kv, chunks, 16) f32 -- per-chunk per-head maxima
  *   chunk      pages per workgroup (locks_score_auto_chunk); one workgroup
- *              scores its chunk for every kv head (n_kv <= 16, n_kv*G <= 128)
+ *              scores its chunk for one kv head (grid: chunks x n_kv x n_req)
  * Block ids are clamped to [0, num_blocks) and page ids to [0, bt_cols).
  */
 int32_t locks_score_rki4(const uint16_t* q, int64_t q_stride_req, int64_t q_stride_head,

@@ -39,8 +39,6 @@ constexpr int SC_WAVES = 4;
 constexpr int SC_BLOCK = SC_WAVES * kWave;
 constexpr int SC_VROW = SC_RNK * SC_D / 2;   // 512 B of packed V per row
 constexpr int SC_MAX_CHUNK = 1024;          // pages per workgroup, upper bound
-constexpr int SC_MAXKV = 16;                // kv heads per request
-constexpr int SC_MAXHQ = 128;               // query heads per request (n_kv * G)
 // per-wave LDS stage of one (tile, kv head) unit.  Rows are padded (V: 80 B
 // per 64-B basis row, mu: 144 B per 128-B row) so the MFMA-order reads of 16
 // rows at once hit distinct banks.
@@ -73,54 +71,50 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
 {
     constexpr int PPM = 16 / GW;            // pages per token-stage MFMA
     constexpr int NGRP = SC_TILE / PPM;     // token-stage groups per tile
-    const int z = blockIdx.x, r = blockIdx.y;
+    const int z = blockIdx.x, h = blockIdx.y, r = blockIdx.z;   // page chunk, kv head, request
     const int Z = gridDim.x;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int P = min(nsh[r], MP);          // never score past the score_h row
     const int c0 = z * chunk;
     const int c1 = min(c0 + chunk, P);
-    const int HQ = n_kv * G;
+    float* pm_out = pmax + (((long)r * n_kv + h) * Z + z) * 16;
 
     if (c0 >= P) {                          // no page of this chunk is scored
-        for (int i = tid; i < n_kv * 16; i += SC_BLOCK)
-            pmax[(((long)r * n_kv + i / 16) * Z + z) * 16 + (i % 16)] = -INFINITY;
+        if (tid < 16) pm_out[tid] = -INFINITY;
         return;
     }
 
-    __shared__ __attribute__((aligned(16))) float qsp[SC_MAXKV][16];
+    __shared__ __attribute__((aligned(16))) float qsp[16];
     __shared__ __attribute__((aligned(16))) uint8_t stage_l[SC_WAVES][ST_BYTES];
-    __shared__ uint32_t wmax[SC_MAXKV][16];
-    // dynamic LDS: int8 q rows of every head (+16 zero rows), chunk block ids
+    __shared__ uint32_t wmax[16];
+    // dynamic LDS: int8 q rows of this kv head's G query heads (+16 zero
+    // rows), chunk block ids
     extern __shared__ __attribute__((aligned(16))) uint8_t dyn_l[];
     int8_t (*q8s)[SC_QROW] = reinterpret_cast<int8_t (*)[SC_QROW]>(dyn_l);
-    int* bt_l = reinterpret_cast<int*>(dyn_l + (size_t)(HQ + 16) * SC_QROW);
+    int* bt_l = reinterpret_cast<int*>(dyn_l + (size_t)(G + 16) * SC_QROW);
 
     // ---- prologue: q rows and block ids are fetched together; the first
     // unit's summary loads are issued before q is quantized, so the
     // quantization overlaps them.
     // q: 8 consecutive lanes per head, 16 dims (two 16-byte loads) per lane
-    constexpr int QCH = SC_MAXHQ * 8 / SC_BLOCK;              // 16-dim chunks per thread, max
-    uint4 qa[QCH][2];
-#pragma unroll
-    for (int i = 0; i < QCH; ++i) {
-        const int c = tid + SC_BLOCK * i, hq = c >> 3;
-        qa[i][0] = qa[i][1] = make_uint4(0u, 0u, 0u, 0u);
-        if (hq < HQ) {
-            const uint4* qp = reinterpret_cast<const uint4*>(q + (long)r * q_sr + (long)hq * q_sh + (c & 7) * 16);
-            qa[i][0] = qp[0];
-            qa[i][1] = qp[1];
-        }
+    // (G <= 16 heads x 8 chunks <= 128 threads)
+    const int qg = tid >> 3;                                  // this thread's head in the group
+    uint4 qa0 = make_uint4(0u, 0u, 0u, 0u), qa1 = qa0;
+    if (qg < G) {
+        const uint4* qp = reinterpret_cast<const uint4*>(q + (long)r * q_sr + (long)(h * G + qg) * q_sh + (tid & 7) * 16);
+        qa0 = qp[0];
+        qa1 = qp[1];
     }
     for (int i = tid; i < c1 - c0; i += SC_BLOCK) {
         const int b = bt[(long)r * bt_sr + min(c0 + i, bt_cols - 1)];
         bt_l[i] = min(max(b, 0), NB - 1);
     }
-    for (int i = tid; i < SC_MAXKV * 16; i += SC_BLOCK) {
-        wmax[i / 16][i % 16] = 0x007FFFFFu;                    // f2u(-inf)
-        qsp[i / 16][i % 16] = 0.f;
+    if (tid < 16) {
+        wmax[tid] = 0x007FFFFFu;                               // f2u(-inf)
+        qsp[tid] = 0.f;
     }
     for (int i = tid; i < 16 * SC_QROW / 4; i += SC_BLOCK)
-        reinterpret_cast<int*>(&q8s[HQ][0])[i] = 0;            // zero rows after the last head
+        reinterpret_cast<int*>(&q8s[G][0])[i] = 0;             // zero rows after the last head
     __syncthreads();
 
     const int r16 = lane & 15, kg = lane >> 4;
@@ -129,7 +123,7 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
     const int g_l = jcol % GW;               // head of this lane's column
     const uint32_t MH = 0xF0F0F0F0u;
     const int n_tiles = cdiv(c1 - c0, SC_TILE);
-    const int n_units = n_tiles * n_kv;      // (tile, kv head) units of the chunk
+    const int n_units = n_tiles;             // (8-page tile) units of the chunk
 
     // Each (8-page tile, kv head) unit is fetched into VGPRs in natural
     // (contiguous) lane order -- fully coalesced 16-byte loads -- one unit
@@ -139,8 +133,7 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
     uint4 fv0, fv1, fv2, fv3, fc8, fmu, fcs, fvs;
     uint32_t fmus;
     auto load_unit = [&](int u) {
-        const int t = u / n_kv, h = u - t * n_kv;
-        const int p0 = t * SC_TILE;
+        const int p0 = u * SC_TILE;
         const int last = min(SC_TILE, c1 - c0 - p0) - 1;
         const int* bl = bt_l + p0;
         auto row_of = [&](int i) -> uint32_t { return (uint32_t)bl[min(i, last)] * (uint32_t)n_kv + (uint32_t)h; };
@@ -196,12 +189,9 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
     // within 2 ulp of it, which decides the rounding unless the product lies
     // within 2^-15 of a half-integer; those (rare) lanes redo the division.
     const float s2 = sm_scale * 1.4426950408889634f;           // tokens in log2 units
-#pragma unroll
-    for (int i = 0; i < QCH; ++i) {
-        const int c = tid + SC_BLOCK * i, hq = c >> 3;
-        if (SC_BLOCK * i >= HQ * 8) break;                      // no head left for any lane
-        const uint32_t w[8] = {qa[i][0].x, qa[i][0].y, qa[i][0].z, qa[i][0].w,
-                               qa[i][1].x, qa[i][1].y, qa[i][1].z, qa[i][1].w};
+    if (wave < 2) {                                           // threads 0..127: 16 heads x 8 chunks
+        const int c = tid, hq = qg;
+        const uint32_t w[8] = {qa0.x, qa0.y, qa0.z, qa0.w, qa1.x, qa1.y, qa1.z, qa1.w};
         float f[16];
 #pragma unroll
         for (int k = 0; k < 8; ++k) { f[2 * k] = bf16lo(w[k]); f[2 * k + 1] = bf16hi(w[k]); }
@@ -228,53 +218,54 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
                 for (int k = 0; k < 16; ++k) iq[k] = (int)rintf(__fdiv_rn(f[k], qs));
             }
         }
-        if (hq < HQ) {
+        if (hq < G) {
             *reinterpret_cast<uint4*>(&q8s[hq][(c & 7) * 16]) =
                 make_uint4(pack4_i8(iq[0], iq[1], iq[2], iq[3]), pack4_i8(iq[4], iq[5], iq[6], iq[7]),
                            pack4_i8(iq[8], iq[9], iq[10], iq[11]), pack4_i8(iq[12], iq[13], iq[14], iq[15]));
-            if ((c & 7) == 0) qsp[hq / G][hq % G] = qs * s2;
+            if ((c & 7) == 0) qsp[hq] = qs * s2;
         }
     }
     __syncthreads();
+
+    // int8 q rows of this kv head's GQA group as matrix-core operands (the
+    // same for every unit of the workgroup):
+    // Bq = projection B (column j <-> head j % GW, replicated over the
+    // GW-wide page slots), Amu = centroid A (row <-> head, zero padded)
+    v4i Bq[2], Amu[2];
+    {
+        const int gq = r16 % GW;
+        const int rowq = (gq < G) ? gq : G;                   // G.. = zero rows
+        const int rowm = (r16 < G) ? r16 : G;
+        const uint4 n0 = *reinterpret_cast<const uint4*>(&q8s[rowq][32 * kg]);
+        const uint4 n1 = *reinterpret_cast<const uint4*>(&q8s[rowq][32 * kg + 16]);
+        const uint4 m0 = *reinterpret_cast<const uint4*>(&q8s[rowm][32 * kg]);
+        const uint4 m1 = *reinterpret_cast<const uint4*>(&q8s[rowm][32 * kg + 16]);
+        Amu[0] = v4i{(int)m0.x, (int)m0.y, (int)m0.z, (int)m0.w};
+        Amu[1] = v4i{(int)m1.x, (int)m1.y, (int)m1.z, (int)m1.w};
+        // V operand order inside a 16-d window: even d (low nibbles), then odd d
+        Bq[0] = v4i{(int)__builtin_amdgcn_perm(n0.y, n0.x, 0x06040200u), (int)__builtin_amdgcn_perm(n0.w, n0.z, 0x06040200u),
+                    (int)__builtin_amdgcn_perm(n0.y, n0.x, 0x07050301u), (int)__builtin_amdgcn_perm(n0.w, n0.z, 0x07050301u)};
+        Bq[1] = v4i{(int)__builtin_amdgcn_perm(n1.y, n1.x, 0x06040200u), (int)__builtin_amdgcn_perm(n1.w, n1.z, 0x06040200u),
+                    (int)__builtin_amdgcn_perm(n1.y, n1.x, 0x07050301u), (int)__builtin_amdgcn_perm(n1.w, n1.z, 0x07050301u)};
+    }
+    const float4 qsl = *reinterpret_cast<const float4*>(&qsp[4 * kg]);   // rows 4kg.. (mud)
+    // column head's q scale x 1/16 (the nibble shift), zeroed where the
+    // token stage's block-diagonal B has no entry for this lane's column:
+    // qt of page p feeds page slot p % PPM only
+    float qsjm[PPM];
+    {
+        const float qsj = qsp[r16 % GW] * 0.0625f;
+#pragma unroll
+        for (int ps = 0; ps < PPM; ++ps) qsjm[ps] = (psub_l == ps) ? qsj : 0.f;
+    }
 
     uint8_t* stg = stage_l[wave];
     for (int u = wave; u < n_units; u += SC_WAVES) {
         store_unit(stg);
         if (u + SC_WAVES < n_units) load_unit(u + SC_WAVES);   // next unit in flight
-        const int t = u / n_kv, h = u - t * n_kv;
-        const int p0 = c0 + t * SC_TILE;
+        const int p0 = c0 + u * SC_TILE;
         const int nvalid = min(SC_TILE, c1 - p0);
 
-        // int8 q rows of this kv head's GQA group as matrix-core operands:
-        // Bq = projection B (column j <-> head j % GW, replicated over the
-        // GW-wide page slots), Amu = centroid A (row <-> head, zero padded)
-        v4i Bq[2], Amu[2];
-        {
-            const int gq = r16 % GW;
-            const int rowq = (gq < G) ? h * G + gq : HQ;          // HQ.. = zero rows
-            const int rowm = (r16 < G) ? h * G + r16 : HQ;
-            const uint4 n0 = *reinterpret_cast<const uint4*>(&q8s[rowq][32 * kg]);
-            const uint4 n1 = *reinterpret_cast<const uint4*>(&q8s[rowq][32 * kg + 16]);
-            const uint4 m0 = *reinterpret_cast<const uint4*>(&q8s[rowm][32 * kg]);
-            const uint4 m1 = *reinterpret_cast<const uint4*>(&q8s[rowm][32 * kg + 16]);
-            Amu[0] = v4i{(int)m0.x, (int)m0.y, (int)m0.z, (int)m0.w};
-            Amu[1] = v4i{(int)m1.x, (int)m1.y, (int)m1.z, (int)m1.w};
-            // V operand order inside a 16-d window: even d (low nibbles), then odd d
-            Bq[0] = v4i{(int)__builtin_amdgcn_perm(n0.y, n0.x, 0x06040200u), (int)__builtin_amdgcn_perm(n0.w, n0.z, 0x06040200u),
-                        (int)__builtin_amdgcn_perm(n0.y, n0.x, 0x07050301u), (int)__builtin_amdgcn_perm(n0.w, n0.z, 0x07050301u)};
-            Bq[1] = v4i{(int)__builtin_amdgcn_perm(n1.y, n1.x, 0x06040200u), (int)__builtin_amdgcn_perm(n1.w, n1.z, 0x06040200u),
-                        (int)__builtin_amdgcn_perm(n1.y, n1.x, 0x07050301u), (int)__builtin_amdgcn_perm(n1.w, n1.z, 0x07050301u)};
-        }
-        const float4 qsl = *reinterpret_cast<const float4*>(&qsp[h][4 * kg]);   // rows 4kg.. (mud)
-        // column head's q scale x 1/16 (the nibble shift), zeroed where the
-        // token stage's block-diagonal B has no entry for this lane's column:
-        // qt of page p feeds page slot p % PPM only
-        float qsjm[PPM];
-        {
-            const float qsj = qsp[h][r16 % GW] * 0.0625f;
-#pragma unroll
-            for (int ps = 0; ps < PPM; ++ps) qsjm[ps] = (psub_l == ps) ? qsj : 0.f;
-        }
         wave_lds_sync();
 
         // ---- projection: qt (8 basis columns x GQA group) per page -------
@@ -432,12 +423,11 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
 #pragma unroll
         for (int o = GW; o < 16; o <<= 1)    // max over the lanes of one head column
             tmax = fmaxf(tmax, o == 4 ? row_ror<4>(tmax) : o == 8 ? row_ror<8>(tmax) : row_ror<2>(tmax));
-        if (row_owner && (lane & 15) < GW && (lane & 15) < G) atomicMax(&wmax[h][lane & 15], f2u(tmax));
+        if (row_owner && (lane & 15) < GW && (lane & 15) < G) atomicMax(&wmax[lane & 15], f2u(tmax));
         wave_lds_sync();                               // staging reused by the next unit
     }
     __syncthreads();
-    for (int i = tid; i < n_kv * 16; i += SC_BLOCK)
-        pmax[(((long)r * n_kv + i / 16) * Z + z) * 16 + (i % 16)] = u2f(wmax[i / 16][i % 16]);
+    if (tid < 16) pm_out[tid] = u2f(wmax[tid]);
 }
 
 }  // namespace locks
@@ -445,12 +435,11 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
 using namespace locks;
 
 extern "C" int32_t locks_score_auto_chunk(int32_t n_req, int32_t n_kv, int32_t max_pages) {
-    // ~512 workgroups (2 per CU on a 256-CU MI355X, the VGPR-limited
-    // occupancy) over all (request, 8-page tile, kv head) units, in whole tiles.
+    // ~512 workgroups (2 per CU on a 256-CU MI355X) over all (request, kv
+    // head, 8-page tile) units; a workgroup scores whole tiles of one kv head.
     const long tiles = (long)cdiv(max_pages > 0 ? max_pages : 1, SC_TILE);
     const long units = tiles * (n_kv > 0 ? n_kv : 1) * (n_req > 0 ? n_req : 1);
-    const long per_wg = (units + 511) / 512;
-    long ct = (per_wg + (n_kv > 0 ? n_kv : 1) - 1) / (n_kv > 0 ? n_kv : 1);
+    long ct = (units + 511) / 512;                       // tiles per workgroup (one kv head)
     if (ct < 1) ct = 1;
     if (ct > SC_MAX_CHUNK / SC_TILE) ct = SC_MAX_CHUNK / SC_TILE;
     return (int32_t)(ct * SC_TILE);
@@ -474,9 +463,8 @@ extern "C" int32_t locks_score_rki4(
     LOCKS_REQUIRE(head_dim == SC_D, "locks_score_rki4: head_dim %d unsupported (this build: 128)", head_dim);
     LOCKS_REQUIRE(page == SC_PG, "locks_score_rki4: page %d unsupported (this build: 16)", page);
     LOCKS_REQUIRE(G >= 1 && G <= 16, "locks_score_rki4: G=%d outside [1, 16]", G);
-    LOCKS_REQUIRE(n_req >= 0 && n_kv >= 1 && n_kv <= SC_MAXKV && n_kv * G <= SC_MAXHQ,
-                  "locks_score_rki4: n_kv=%d G=%d outside this build (n_kv <= %d, n_kv*G <= %d)",
-                  n_kv, G, SC_MAXKV, SC_MAXHQ);
+    LOCKS_REQUIRE(n_req >= 0 && n_req <= 65535 && n_kv >= 1 && n_kv <= 65535,
+                  "locks_score_rki4: n_req=%d / n_kv=%d outside the grid limits", n_req, n_kv);
     LOCKS_REQUIRE(q_stride_head % 8 == 0 && q_stride_req % 8 == 0,
                   "locks_score_rki4: q strides must be multiples of 8 elements (16-byte loads)");
     LOCKS_REQUIRE((long)num_blocks * n_kv * SC_VROW < (1L << 32),
@@ -491,8 +479,8 @@ extern "C" int32_t locks_score_rki4(
                   "locks_score_rki4: null pointer argument");
     if (n_req == 0) return 0;
     const int Z = cdiv(max_pages, chunk);
-    dim3 grid(Z, n_req);
-    const size_t dyn = (size_t)(n_kv * G + 16) * SC_QROW + (size_t)chunk * sizeof(int);
+    dim3 grid(Z, n_kv, n_req);
+    const size_t dyn = (size_t)(G + 16) * SC_QROW + (size_t)chunk * sizeof(int);
     hipStream_t st = (hipStream_t)stream;
 #define LAUNCH(GWV)                                                                    \
     hipLaunchKernelGGL((rki4_score_kernel<GWV>), grid, dim3(SC_BLOCK), dyn, st, q, \
