@@ -782,9 +782,24 @@ __global__ __launch_bounds__(C2_BLK) void sel_chunk2_kernel(
     if (tid == 0) cand_cnt[rk * Z1 + z] = ncand;
 }
 
-// Register-resident finish of one row: candidates j = E t .. E t + E - 1 of
-// the chunk-ordered (= page-ordered) list, located by a binary search over
-// the chunk offsets; exact b-th largest, ordered emission, sink / window.
+// Exact b-th largest over register-resident candidates (thread order = page
+// order), ordered emission, sink / window, page count.
+template <int E>
+__device__ void finish2_select(long rk, int b, int n_sink, int n_pages, int n_sel_hi,
+                               int* __restrict__ trow, int* __restrict__ page_cnt,
+                               const uint32_t (&key)[E], const int (&page)[E], const bool (&val)[E],
+                               int* hist, int* wtot, int* s3, int* wsum) {
+    const int tid = threadIdx.x;
+    const RadixSel rs = reg_kth_largest<F2_BLK, E>(key, val, b, hist, wtot, s3);
+    reg_emit<F2_BLK, E>(key, val, rs, wsum, [&](int pos, int e) { trow[n_sink + pos] = page[e]; });
+    const int cnt = n_sink + b + (n_pages - n_sel_hi);
+    for (int i = tid; i < n_sink; i += F2_BLK) trow[i] = i;
+    for (int i = n_sink + b + tid; i < cnt; i += F2_BLK) trow[i] = n_sel_hi + (i - n_sink - b);
+    if (tid == 0) page_cnt[rk] = cnt;
+}
+
+// Candidates j = E t .. E t + E - 1 of the chunk-ordered (= page-ordered)
+// list, located by a binary search over the chunk offsets.
 template <int E>
 __device__ void finish2_regs(long rk, int N, int Z1, int b, int n_sink, int n_pages,
                              int n_sel_hi, int* __restrict__ trow, int* __restrict__ page_cnt,
@@ -811,12 +826,8 @@ __device__ void finish2_regs(long rk, int N, int Z1, int b, int n_sink, int n_pa
             page[e] = cand_page[src];
         }
     }
-    const RadixSel rs = reg_kth_largest<F2_BLK, E>(key, val, b, hist, wtot, s3);
-    reg_emit<F2_BLK, E>(key, val, rs, wsum, [&](int pos, int e) { trow[n_sink + pos] = page[e]; });
-    const int cnt = n_sink + b + (n_pages - n_sel_hi);
-    for (int i = tid; i < n_sink; i += F2_BLK) trow[i] = i;
-    for (int i = n_sink + b + tid; i < cnt; i += F2_BLK) trow[i] = n_sel_hi + (i - n_sink - b);
-    if (tid == 0) page_cnt[rk] = cnt;
+    finish2_select<E>(rk, b, n_sink, n_pages, n_sel_hi, trow, page_cnt, key, page, val, hist, wtot,
+                      s3, wsum);
 }
 
 
@@ -918,6 +929,34 @@ __global__ __launch_bounds__(F2_BLK) void sel_finish2_kernel(
     __shared__ int wtot[F2_BLK / kWave];
     __shared__ int s3[4];
     __shared__ int wsum[F2_BLK / kWave + 1];
+    // Slotted layout (the usual small budget): chunk z's local top-b list (at
+    // most min(b, SEL_CH) candidates, page-ordered) maps onto ceil(that / 4)
+    // consecutive threads, 4 slots each, so thread order is page order and the
+    // counts load in the same round trip as the candidates (no offset scan).
+    // Only on the local-top-b route (no histogram): band lists can be longer.
+    const int tpc = cdiv(min(b, SEL_CH), 4);          // threads per chunk list
+    if (!ghist && (long)Z1 * tpc <= F2_BLK) {
+        const int z = tid / tpc, sl = (tid - z * tpc) * 4;
+        const bool zin = z < Z1;
+        const long src = (rk * Z1 + (zin ? z : 0)) * (long)SEL_CH + sl;
+        const int cz = zin ? cand_cnt[rk * Z1 + z] : 0;
+        uint32_t key[4];
+        int page[4];
+        bool val[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            key[e] = zin ? cand_key[src + e] : 0u;          // slots past the count are masked
+            page[e] = zin ? cand_page[src + e] : 0;
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            val[e] = zin && sl + e < cz;
+            if (!val[e]) key[e] = 0u;
+        }
+        finish2_select<4>(rk, b, n_sink, n_pages, n_sel_hi, trow, page_cnt, key, page, val, hist,
+                          wtot, s3, wsum);
+        return;
+    }
     {
         const int c = (tid < Z1) ? cand_cnt[rk * Z1 + tid] : 0;
         int tot;
