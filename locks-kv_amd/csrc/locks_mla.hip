@@ -85,23 +85,81 @@ __global__ __launch_bounds__(ML_BLK) void mla_score_kernel(
     __shared__ int bt_l[ML_MAX_CHUNK];
     __shared__ __attribute__((aligned(16))) uint8_t stage_l[ML_WAVES][MS_BYTES];
 
-    // ---- prologue: block ids, q quantized per head (absmax / 127) --------
+    // ---- prologue: q rows of this wave's heads and the block ids in one
+    // round trip; the first unit's summary loads are issued before q is
+    // quantized (absmax / 127 per head), so the quantization overlaps them
+    constexpr int QH = ML_H / ML_WAVES;
+    uint4 qw[QH], qrw[QH];
+#pragma unroll
+    for (int i = 0; i < QH; ++i) {
+        const int h = wave + ML_WAVES * i;
+        const uint16_t* qh = q + (long)r * q_sr + (long)h * q_sh;
+        qw[i] = qrw[i] = make_uint4(0u, 0u, 0u, 0u);
+        if (h < H) {
+            qw[i] = *reinterpret_cast<const uint4*>(qh + 8 * lane);
+            if (lane < ML_DR / 8) qrw[i] = *reinterpret_cast<const uint4*>(qh + ML_D + 8 * lane);
+        }
+    }
     for (int i = tid; i < c1 - c0; i += ML_BLK) {
         const int b = bt[(long)r * bt_sr + min(c0 + i, bt_cols - 1)];
         bt_l[i] = min(max(b, 0), NB - 1);
     }
     for (int i = tid; i < ML_D / 4; i += ML_BLK) reinterpret_cast<int*>(&q8s[ML_H][0])[i] = 0;
-    for (int h = wave; h < ML_H; h += ML_WAVES) {
-        const uint16_t* qh = q + (long)r * q_sr + (long)h * q_sh;
+    __syncthreads();
+    const int r16 = lane & 15, kg = lane >> 4;
+    const int n_units = cdiv(c1 - c0, 2);
+    uint4 fv0, fv1, fv2, fv3, fmu, fc8, fcs, fvs, fr0, fr1, fr2, fr3;
+    uint32_t fmus = 0u;
+    // natural-order (coalesced) loads of unit u into registers
+    auto load_unit = [&](int u) {
+        const int p0 = 2 * u;
+        const int last = c1 - c0 - 1;
+        auto blk_of = [&](int pg) -> long { return (long)bt_l[min(p0 + pg, last)]; };
+        // 16-byte chunk i = lane + 64 m of the 2 V rows
+        auto vload = [&](int i) { return *reinterpret_cast<const uint4*>(v4 + blk_of(i >> 7) * ML_VROW + (i & 127) * 16); };
+        fv0 = vload(lane); fv1 = vload(lane + 64); fv2 = vload(lane + 128); fv3 = vload(lane + 192);
+        fmu = *reinterpret_cast<const uint4*>(mu8 + blk_of(lane >> 5) * ML_D + (lane & 31) * 16);
+        fc8 = *reinterpret_cast<const uint4*>(c8 + blk_of((lane >> 3) & 1) * (ML_PG * ML_RNK) + (lane & 7) * 16);
+        fcs = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(cs) + blk_of((lane >> 1) & 1) * (ML_PG * 2) + (lane & 1) * 16);
+        fvs = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(vs) + blk_of(lane & 1) * (ML_RNK * 2));
+        fmus = (uint32_t)mus[blk_of(lane & 1)];
+        // RoPE chunk i = (page i >> 7, token (i >> 3) & 15, 16-byte part i & 7)
+        auto rload = [&](int i) {
+            return *reinterpret_cast<const uint4*>(cache + blk_of(i >> 7) * c_sb + (long)((i >> 3) & 15) * c_st + ML_D + 8 * (i & 7));
+        };
+        fr0 = rload(lane); fr1 = rload(lane + 64); fr2 = rload(lane + 128); fr3 = rload(lane + 192);
+    };
+    auto store_unit = [&](uint8_t* st) {
+        // V chunk i: page i >> 7, column (i >> 4) & 7, 16-byte part i & 15
+        auto vofs = [&](int i) { return MS_V + ((i >> 7) * 8 + ((i >> 4) & 7)) * MS_VROWB + (i & 15) * 16; };
+        *reinterpret_cast<uint4*>(st + vofs(lane)) = fv0;
+        *reinterpret_cast<uint4*>(st + vofs(lane + 64)) = fv1;
+        *reinterpret_cast<uint4*>(st + vofs(lane + 128)) = fv2;
+        *reinterpret_cast<uint4*>(st + vofs(lane + 192)) = fv3;
+        *reinterpret_cast<uint4*>(st + MS_MU + lane * 16) = fmu;
+        if (lane < 16) *reinterpret_cast<uint4*>(st + MS_C8 + lane * 16) = fc8;
+        if (lane < 4) *reinterpret_cast<uint4*>(st + MS_CS + lane * 16) = fcs;
+        if (lane < 2) {
+            *reinterpret_cast<uint4*>(st + MS_VS + lane * 16) = fvs;
+            *reinterpret_cast<uint32_t*>(st + MS_MUS + lane * 4) = fmus;
+        }
+        // RoPE chunk i: (page, token) row i >> 3, 16-byte part i & 7
+        auto rofs = [&](int i) { return MS_RP + (i >> 3) * MS_RROWB + (i & 7) * 16; };
+        *reinterpret_cast<uint4*>(st + rofs(lane)) = fr0;
+        *reinterpret_cast<uint4*>(st + rofs(lane + 64)) = fr1;
+        *reinterpret_cast<uint4*>(st + rofs(lane + 128)) = fr2;
+        *reinterpret_cast<uint4*>(st + rofs(lane + 192)) = fr3;
+    };
+
+    load_unit(min(wave, n_units - 1));          // every lane loads (exact wait counts)
+#pragma unroll
+    for (int i = 0; i < QH; ++i) {
+        const int h = wave + ML_WAVES * i;
         float a[8];
-        if (h < H) {
-            const uint4 w = *reinterpret_cast<const uint4*>(qh + 8 * lane);
-            const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+        {
+            const uint32_t ws[4] = {qw[i].x, qw[i].y, qw[i].z, qw[i].w};
 #pragma unroll
             for (int e = 0; e < 4; ++e) { a[2 * e] = bf16lo(ws[e]); a[2 * e + 1] = bf16hi(ws[e]); }
-        } else {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) a[e] = 0.f;
         }
         float am = 0.f;
 #pragma unroll
@@ -134,16 +192,10 @@ __global__ __launch_bounds__(ML_BLK) void mla_score_kernel(
             pk[e >> 2] |= ((uint32_t)(uint8_t)v) << (8 * (e & 3));
         }
         *reinterpret_cast<uint2*>(&q8s[h][8 * lane]) = make_uint2(pk[0], pk[1]);
-        if (lane < ML_DR / 8) {
-            uint4 w = make_uint4(0u, 0u, 0u, 0u);
-            if (h < H) w = *reinterpret_cast<const uint4*>(qh + ML_D + 8 * lane);
-            *reinterpret_cast<uint4*>(&qrs[h][8 * lane]) = w;
-        }
+        if (lane < ML_DR / 8) *reinterpret_cast<uint4*>(&qrs[h][8 * lane]) = qrw[i];
         if (lane == 0) qss[h] = (h < H) ? qs : 0.f;
     }
     __syncthreads();
-
-    const int r16 = lane & 15, kg = lane >> 4;
     const uint32_t MH = 0xF0F0F0F0u;
     // q operands shared by every unit: projection B (column j = head j),
     // RoPE B (column = head), per-head scale of this lane's column
@@ -163,54 +215,7 @@ __global__ __launch_bounds__(ML_BLK) void mla_score_kernel(
     const float qsj = qss[r16];
     const bool col_ok = r16 < H;
 
-    const int n_units = cdiv(c1 - c0, 2);
-    uint4 fv0, fv1, fv2, fv3, fmu, fc8, fcs, fvs, fr0, fr1, fr2, fr3;
-    uint32_t fmus = 0u;
-    // natural-order (coalesced) loads of unit u into registers
-    auto load_unit = [&](int u) {
-        const int p0 = 2 * u;
-        const int last = c1 - c0 - 1;
-        auto blk_of = [&](int pg) -> long { return (long)bt_l[min(p0 + pg, last)]; };
-        // 16-byte chunk i = lane + 64 m of the 2 V rows
-        auto vload = [&](int i) { return *reinterpret_cast<const uint4*>(v4 + blk_of(i >> 7) * ML_VROW + (i & 127) * 16); };
-        fv0 = vload(lane); fv1 = vload(lane + 64); fv2 = vload(lane + 128); fv3 = vload(lane + 192);
-        fmu = *reinterpret_cast<const uint4*>(mu8 + blk_of(lane >> 5) * ML_D + (lane & 31) * 16);
-        if (lane < 16) fc8 = *reinterpret_cast<const uint4*>(c8 + blk_of(lane >> 3) * (ML_PG * ML_RNK) + (lane & 7) * 16);
-        if (lane < 4) fcs = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(cs) + blk_of(lane >> 1) * (ML_PG * 2) + (lane & 1) * 16);
-        if (lane < 2) {
-            fvs = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(vs) + blk_of(lane) * (ML_RNK * 2));
-            fmus = (uint32_t)mus[blk_of(lane)];
-        }
-        // RoPE chunk i = (page i >> 7, token (i >> 3) & 15, 16-byte part i & 7)
-        auto rload = [&](int i) {
-            return *reinterpret_cast<const uint4*>(cache + blk_of(i >> 7) * c_sb + (long)((i >> 3) & 15) * c_st + ML_D + 8 * (i & 7));
-        };
-        fr0 = rload(lane); fr1 = rload(lane + 64); fr2 = rload(lane + 128); fr3 = rload(lane + 192);
-    };
-    auto store_unit = [&](uint8_t* st) {
-        // V chunk i: page i >> 7, column (i >> 4) & 7, 16-byte part i & 15
-        auto vofs = [&](int i) { return MS_V + ((i >> 7) * 8 + ((i >> 4) & 7)) * MS_VROWB + (i & 15) * 16; };
-        *reinterpret_cast<uint4*>(st + vofs(lane)) = fv0;
-        *reinterpret_cast<uint4*>(st + vofs(lane + 64)) = fv1;
-        *reinterpret_cast<uint4*>(st + vofs(lane + 128)) = fv2;
-        *reinterpret_cast<uint4*>(st + vofs(lane + 192)) = fv3;
-        *reinterpret_cast<uint4*>(st + MS_MU + lane * 16) = fmu;
-        if (lane < 16) *reinterpret_cast<uint4*>(st + MS_C8 + lane * 16) = fc8;
-        if (lane < 4) *reinterpret_cast<uint4*>(st + MS_CS + lane * 16) = fcs;
-        if (lane < 2) {
-            *reinterpret_cast<uint4*>(st + MS_VS + lane * 16) = fvs;
-            *reinterpret_cast<uint32_t*>(st + MS_MUS + lane * 4) = fmus;
-        }
-        // RoPE chunk i: (page, token) row i >> 3, 16-byte part i & 7
-        auto rofs = [&](int i) { return MS_RP + (i >> 3) * MS_RROWB + (i & 7) * 16; };
-        *reinterpret_cast<uint4*>(st + rofs(lane)) = fr0;
-        *reinterpret_cast<uint4*>(st + rofs(lane + 64)) = fr1;
-        *reinterpret_cast<uint4*>(st + rofs(lane + 128)) = fr2;
-        *reinterpret_cast<uint4*>(st + rofs(lane + 192)) = fr3;
-    };
-
     uint8_t* st = stage_l[wave];
-    if (wave < n_units) load_unit(wave);
     for (int u = wave; u < n_units; u += ML_WAVES) {
         store_unit(st);
         if (u + ML_WAVES < n_units) load_unit(u + ML_WAVES);   // next unit in flight
