@@ -98,13 +98,12 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
     // quantization overlaps them.
     // q: 8 consecutive lanes per head, 16 dims (two 16-byte loads) per lane
     // (G <= 16 heads x 8 chunks <= 128 threads)
+    // Unconditional loads (threads past the group re-read its last head and
+    // are never stored): a guarded load would make the compiler wait for it
+    // at the branch join, before the block ids below are even requested.
     const int qg = tid >> 3;                                  // this thread's head in the group
-    uint4 qa0 = make_uint4(0u, 0u, 0u, 0u), qa1 = qa0;
-    if (qg < G) {
-        const uint4* qp = reinterpret_cast<const uint4*>(q + (long)r * q_sr + (long)(h * G + qg) * q_sh + (tid & 7) * 16);
-        qa0 = qp[0];
-        qa1 = qp[1];
-    }
+    const uint4* qp = reinterpret_cast<const uint4*>(q + (long)r * q_sr + (long)(h * G + min(qg, G - 1)) * q_sh + (tid & 7) * 16);
+    const uint4 qa0 = qp[0], qa1 = qp[1];
     for (int i = tid; i < c1 - c0; i += SC_BLOCK) {
         const int b = bt[(long)r * bt_sr + min(c0 + i, bt_cols - 1)];
         bt_l[i] = min(max(b, 0), NB - 1);
