@@ -80,25 +80,42 @@ __device__ void merge_row(const float* __restrict__ m_part, const float* __restr
     constexpr int PF = 8;                               // splits of acc prefetched per item
     // the first PF split partials of this thread's (head, 4-dim) items are
     // loaded before anything waits (they do not depend on the weights)
+    // Loads are unconditional (indices clamped into the buffers, surplus
+    // values never used): a guarded load merges with its default at a branch
+    // join, where the compiler waits for it -- splitting one round trip in two.
     float4 pre[2][PF];
 #pragma unroll
     for (int it = 0; it < 2; ++it) {
-        const int i = tid + it * DC_BLK;
+        const int i = min(tid + it * DC_BLK, G * (DC_D / 4) - 1);
         const int g = i / (DC_D / 4), d4 = (i % (DC_D / 4)) * 4;
 #pragma unroll
         for (int k = 0; k < PF; ++k)
-            pre[it][k] = (i < G * (DC_D / 4) && k < split)
-                             ? ld_part4<COHERENT>(acc_part, (rk * split * G + g) * DC_D + d4 + (long)k * G * DC_D)
-                             : make_float4(0.f, 0.f, 0.f, 0.f);
+            pre[it][k] = ld_part4<COHERENT>(acc_part, (rk * split * G + g) * DC_D + d4 +
+                                                          (long)min(k, split - 1) * G * DC_D);
     }
-    // every (split, head) m and l in one pass (all loads in flight), then the
+    // every (split, head) m and l, up to 4 per thread in flight, then the
     // per-head max / weights / denominator from LDS
     float* m_s = w_s;                                   // [s * 16 + g], reused for the weights
-    for (int i = tid; i < n_act * G; i += DC_BLK) {
-        const int sidx = i / G, g = i - sidx * G;
-        const long src = (rk * split + sidx) * G + g;
-        m_s[sidx * 16 + g] = ld_part<COHERENT>(m_part, src);
-        l_s[sidx * 16 + g] = ld_part<COHERENT>(l_part, src);
+    const int nml = n_act * G;
+    for (int i0 = tid; i0 < nml; i0 += 4 * DC_BLK) {
+        float mv[4], lv[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int i = min(i0 + j * DC_BLK, nml - 1);
+            const int sidx = i / G, g = i - sidx * G;
+            const long src = (rk * split + sidx) * G + g;
+            mv[j] = ld_part<COHERENT>(m_part, src);
+            lv[j] = ld_part<COHERENT>(l_part, src);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int i = i0 + j * DC_BLK;
+            if (i < nml) {
+                const int sidx = i / G, g = i - sidx * G;
+                m_s[sidx * 16 + g] = mv[j];
+                l_s[sidx * 16 + g] = lv[j];
+            }
+        }
     }
     __syncthreads();
     for (int g = wave; g < G; g += NWV) {
