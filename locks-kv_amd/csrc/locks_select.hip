@@ -199,10 +199,8 @@ __device__ __forceinline__ float chunk_max(const float* __restrict__ p, int n) {
     for (int z0 = lane; z0 < n; z0 += 8 * kWave) {
         float t[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int z = z0 + j * kWave;
-            t[j] = (z < n) ? p[(long)z * 16] : -INFINITY;
-        }
+        for (int j = 0; j < 8; ++j)                    // clamped: a repeat leaves the max
+            t[j] = p[(long)min(z0 + j * kWave, n - 1) * 16];
 #pragma unroll
         for (int j = 0; j < 8; ++j) m = fmaxf(m, t[j]);
     }
@@ -419,9 +417,11 @@ __global__ __launch_bounds__(ROW_BLK) void sel_row_kernel(
         for (int j = 0; j < HB; ++j)
 #pragma unroll
             for (int v = 0; v < E / 4; ++v) {
-                const int g = g0 + j, p = p0 + 4 * v;
-                xv[j][v] = (g < G && p < MP) ? *reinterpret_cast<const float4*>(shb + (long)g * MP + p)
-                                             : make_float4(0.f, 0.f, 0.f, 0.f);
+                // unconditional (clamped) loads: surplus heads / pages are
+                // never combined or kept, and a guarded load would make the
+                // compiler wait for it before the page maxima are requested
+                const int g = min(g0 + j, G - 1), p = min(p0 + 4 * v, MP - 4);
+                xv[j][v] = *reinterpret_cast<const float4*>(shb + (long)g * MP + p);
             }
     };
     load_batch(0);
@@ -704,9 +704,8 @@ __global__ __launch_bounds__(C2_BLK) void sel_chunk2_kernel(
     const float* shb = score_h + rk * (long)G * MP;
     float4 xv[16];
 #pragma unroll
-    for (int g = 0; g < 16; ++g)
-        xv[g] = (g < G && p0 + 3 < MP) ? *reinterpret_cast<const float4*>(shb + (long)g * MP + p0)
-                                       : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int g = 0; g < 16; ++g)                         // clamped, unconditional (see the row kernel)
+        xv[g] = *reinterpret_cast<const float4*>(shb + (long)min(g, G - 1) * MP + min(p0, MP - 4));
     int* trow = page_table + rk * (long)MP;
 #pragma unroll
     for (int e = 0; e < C2_E; ++e)
@@ -939,15 +938,16 @@ __global__ __launch_bounds__(F2_BLK) void sel_finish2_kernel(
         const int z = tid / tpc, sl = (tid - z * tpc) * 4;
         const bool zin = z < Z1;
         const long src = (rk * Z1 + (zin ? z : 0)) * (long)SEL_CH + sl;
-        const int cz = zin ? cand_cnt[rk * Z1 + z] : 0;
+        const int czl = cand_cnt[rk * Z1 + (zin ? z : 0)];
         uint32_t key[4];
         int page[4];
         bool val[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            key[e] = zin ? cand_key[src + e] : 0u;          // slots past the count are masked
-            page[e] = zin ? cand_page[src + e] : 0;
+        for (int e = 0; e < 4; ++e) {                     // slots past the count are masked
+            key[e] = cand_key[src + e];
+            page[e] = cand_page[src + e];
         }
+        const int cz = zin ? czl : 0;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             val[e] = zin && sl + e < cz;
