@@ -211,22 +211,29 @@ def scorer_traffic(workload):
 
 
 def scorer_roofline(m, reps=3):
-    """Average scorer launch duration (HIP events on the launch stream) over
-    every layer's slabs, cold across layers."""
+    """Average scorer launch duration over every layer's slabs (cold across
+    layers): the launches are captured in one HIP graph and its replays are
+    timed with HIP events on the capture stream, so host-side launch latency
+    does not starve the GPU between launches."""
     import torch
     from locks.selection import rki4_score_only
     st = m["st"]
-    s = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    n = 0
-    e0.record(s)
-    for _ in range(reps):
+
+    def launches():
         for layer in range(m["L"]):
             rki4_score_only(st, layer, m["q"][layer], m["bt"], m["sl"], m["R"], m["scale"])
-            n += 1
+
+    g = capture(launches)
+    s = torch.cuda.current_stream()
+    g.replay()                                  # warm-up replay
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    for _ in range(reps):
+        g.replay()
     e1.record(s)
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) * 1e3 / n       # us per launch
+    return e0.elapsed_time(e1) * 1e3 / (reps * m["L"])       # us per launch
 
 
 def cpu_baseline(m, sample_pages=4096):
@@ -367,12 +374,19 @@ def mla_scorer_us(m, reps=3):
     from locks.selection import mla_derive, mla_score_only
     st = m["st"]
     mla_derive(st, m["sl"], m["R"])
+
+    def launches():
+        for layer in range(m["L"]):
+            mla_score_only(st, layer, m["q"][layer], m["cache"][layer], m["bt"], m["R"], m["scale"])
+
+    g = capture(launches)                       # timed as graph replays, like scorer_roofline
     s = torch.cuda.current_stream()
+    g.replay()
+    torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(s)
     for _ in range(reps):
-        for layer in range(m["L"]):
-            mla_score_only(st, layer, m["q"][layer], m["cache"][layer], m["bt"], m["R"], m["scale"])
+        g.replay()
     e1.record(s)
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) * 1e3 / (reps * m["L"])
