@@ -494,6 +494,43 @@ def run_mla(a, wl):
     print(json.dumps(line), flush=True)
 
 
+def run_refresh(a, m):
+    """Summary refresh lifecycle on the bench model (one JSON line): bulk
+    rebuild of every finalized page in every layer, the delta tag scan with
+    nothing stale, and the one-row tail of a page-crossing decode step."""
+    import torch
+    from locks.selection import rki4_build_bulk, rki4_build_delta, rki4_build_tail
+
+    st, ks, R = m["st"], [kv[:, 0] for kv in m["kv"]], m["R"]
+    sl = (m["sl"] - 1).clamp(min=0)                      # settled lengths
+    max_fin = int(sl.max().item()) // PAGE
+    rows = torch.zeros(1, dtype=torch.int32, device="cuda")
+    s = torch.cuda.current_stream()
+
+    def ms(fn, reps):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for _ in range(reps):
+            fn()
+        e1.record(s)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    bulk = ms(lambda: rki4_build_bulk(st, ks, m["bt"], sl, R, max_fin), 2)
+    delta = ms(lambda: rki4_build_delta(st, ks, m["bt"], sl, R, max_fin), 10)
+    tail = ms(lambda: rki4_build_tail(st, ks, m["bt"], sl, R, rows), 20)
+    pages = int((sl // PAGE).sum().item())
+    print(json.dumps({
+        "metric": "summary refresh ms", "unit": "ms", "higher_is_better": False,
+        "config": {"workload": a.workload, "layers": m["L"], "n_kv": m["n_kv"],
+                   "finalized_pages": pages},
+        "bulk_ms": round(bulk, 3), "delta_nothing_stale_ms": round(delta, 4),
+        "tail_one_row_ms": round(tail, 4),
+        "bulk_us_per_gram": round(bulk * 1e3 / (pages * m["L"] * m["n_kv"]), 4)}), flush=True)
+
+
 def run_ladder(a, wl):
     """Sparse vs dense decode step over a context ladder (BASELINE configs[2]'s
     dense comparison at 16K..1M): one JSON line per context, same model shape."""
@@ -540,6 +577,8 @@ def main():
     ap.add_argument("--ladder", default="",
                     help="comma-separated contexts (tokens): one sparse + dense line per context, "
                          "e.g. 16384,131072,262144,524288,1048576 (single-request GQA workloads)")
+    ap.add_argument("--refresh", action="store_true",
+                    help="time the summary refresh lifecycle (bulk / delta / tail) instead")
     ap.add_argument("--profile-scorer", type=int, default=0,
                     help="only launch the scorer N times per layer (for rocprof)")
     a = ap.parse_args()
@@ -570,6 +609,9 @@ def main():
     t0 = time.perf_counter()
     m = make_model(wl, a.budget_pages, summaries=a.summaries, zsplit=a.zsplit or None)
     log(f"model ready in {time.perf_counter() - t0:.1f}s (summary build {m['build_s']:.1f}s)")
+    if a.refresh:
+        run_refresh(a, m)
+        return
     if a.profile_scorer:
         from locks.selection import derive_page_params
         derive_page_params(m["st"], m["sl"], m["R"])

@@ -28,7 +28,7 @@
 
 #include <stdint.h>
 
-#define LOCKS_ABI_VERSION 2
+#define LOCKS_ABI_VERSION 3
 
 #ifdef __cplusplus
 extern "C" {
@@ -221,6 +221,59 @@ int32_t locks_pack_rki4(const float* mu, const float* dc, const float* S2, const
                         const int32_t* rows, int32_t n, int32_t head_dim, int32_t page,
                         uint8_t* v4, uint16_t* vs, int8_t* c8, uint16_t* cs, int8_t* mu8,
                         uint16_t* mus, void* stream);
+
+/*
+ * Summary refresh lifecycle, step 1: the physical blocks to (re)build, as a
+ * device list `blocks` plus a device count `count` (no host sync; entries
+ * are distinct, in no particular order).  Replaces the block producers of
+ * the reference's batched refreshes (selection/build.py:372-384
+ * _tail_blocks, :415-427 _bulk_blocks, :472-488 _delta_select, called by
+ * rki4_build_tail / _bulk / _delta, selection/rki4_build.py:264-315):
+ *   LOCKS_REFRESH_TAIL   the last finalized page (max(sl/page - 1, 0)) of
+ *                        rows[0..n_rows) (rows NULL: rows 0..n_rows-1)
+ *   LOCKS_REFRESH_BULK   every finalized page p < sl/page, p < max_fin
+ *   LOCKS_REFRESH_DELTA  the finalized pages whose content tag
+ *                        K[page-1, kh, 0:8] differs (as bf16 numbers; the
+ *                        NaN initial tag always does) from the stored tag in
+ *                        ANY layer or kv head
+ *   seq_lens    (n_req,) i32 SETTLED token counts (written K only)
+ *   num_blocks  bound of valid block ids: min(state blocks, K blocks); ids
+ *               outside [0, num_blocks) are skipped (rki4_build.py:133-144)
+ *   k_layers    (n_layers,) device array of per-layer K base addresses with
+ *               common element strides (DELTA only; NULL otherwise)
+ *   tag         the state's (n_layers, tag_blocks, n_kv, 8) bf16 tag slab
+ *   mark        (num_blocks,) u8, zero-filled once; every call leaves it zero
+ *   blocks      (num_blocks,) i32 output list; count (1,) i32 output
+ * The reference's bulk path clamps invalid slots to block 0 and rebuilds it;
+ * here they are skipped (a non-finalized block's summary is never scored).
+ */
+#define LOCKS_REFRESH_TAIL 0
+#define LOCKS_REFRESH_BULK 1
+#define LOCKS_REFRESH_DELTA 2
+int32_t locks_refresh_blocks(int32_t mode, const int32_t* block_table, int64_t bt_stride,
+                             const int32_t* seq_lens, int32_t n_req, const int32_t* rows,
+                             int32_t n_rows, int32_t max_fin, int32_t page, int32_t num_blocks,
+                             const uint64_t* k_layers, int32_t n_layers, int64_t k_stride_block,
+                             int64_t k_stride_tok, int64_t k_stride_head, int32_t n_kv,
+                             const uint16_t* tag, int64_t tag_blocks, uint8_t* mark,
+                             int32_t* blocks, int32_t* count, void* stream);
+
+/*
+ * Summary refresh lifecycle, step 2: locks_build_rki4 over ALL layers in one
+ * launch (the reference loops layers / layer groups through torch ops,
+ * selection/build.py:430-453 _build_blocks).  Layer l reads K from
+ * k_layers[l] and writes the slabs at layer offset l * slab_blocks * n_kv
+ * rows (slabs laid out (n_layers, slab_blocks, n_kv, ...), pointers to layer
+ * 0).  count (nullable) is a device count of valid `blocks` entries, at most
+ * n_blocks, as written by locks_refresh_blocks.
+ */
+int32_t locks_build_rki4_layers(const uint64_t* k_layers, int32_t n_layers,
+                                int64_t k_stride_block, int64_t k_stride_tok,
+                                int64_t k_stride_head, int32_t num_blocks, const int32_t* blocks,
+                                const int32_t* count, int32_t n_blocks, int32_t n_kv,
+                                int32_t head_dim, int32_t page, int64_t slab_blocks, uint8_t* v4,
+                                uint16_t* vs, int8_t* c8, uint16_t* cs, int8_t* mu8,
+                                uint16_t* mus, uint16_t* tag, void* stream);
 
 
 /* ---------------------------------------------------------------------------

@@ -22,6 +22,8 @@
 // eigenpairs from the caller and is bit-exact to the reference op order
 // (V accumulated over t in ascending order with separately rounded multiply
 // and add, IEEE division, round-half-even).
+#include <algorithm>
+
 #include "locks_common.h"
 #include "locks_hip.h"
 
@@ -30,6 +32,8 @@ namespace locks {
 constexpr int BD_PG = 16;
 constexpr int BD_RNK = 8;
 constexpr int BD_SWEEPS = 12;
+// build grid cap (waves stride over the rest): a few resident rounds on 256 CUs
+constexpr long BD_MAX_GRID = 4096;
 // waves per workgroup: the per-wave LDS image of a d = 512 page is ~37 KB
 template <int D> constexpr int bd_waves() { return D <= 128 ? 4 : 1; }
 
@@ -142,7 +146,11 @@ __device__ void jacobi16(W& L) {
             off += __shfl_xor(off, o, kWave);
             dia += __shfl_xor(dia, o, kWave);
         }
-        if (!(off > 1e-14f * dia) ) break;      // wave-uniform (also exits on 0/0)
+        // wave-uniform (also exits on 0/0).  fp32 rounding leaves off/dia
+        // near 1e-14 (asymmetric residues of order eps * |lambda|), so the
+        // bound sits above that floor: 5-6 sweeps instead of running out the
+        // sweep limit, with the same top-8 eigenvalue accuracy (~3e-6 rel).
+        if (!(off > 1e-12f * dia)) break;
         for (int step = 0; step < BD_PG - 1; ++step) {
             // round-robin pairing: index 0 fixed, 1..15 rotate
             if (lane < BD_PG / 2) {
@@ -215,10 +223,17 @@ __device__ void select_top8(W& L) {
     wave_lds_sync();
 }
 
+// Grid: capped, waves stride over (layer, block, kv head).  Layer l reads K from
+// k_layers[l] (or kc for a single-layer call) and writes slab rows offset by
+// l * layer_rows.  n_dev, when given, is a device count of valid entries of
+// `blocks` (at most n_blocks): the refresh producers size the grid to the
+// host-known bound and the list is compacted on the device.
 template <int D>
 __global__ __launch_bounds__(bd_waves<D>() * kWave) void rki4_build_kernel(
-    const uint16_t* __restrict__ kc, long k_sb, long k_st, long k_sh, int NB,
-    const int* __restrict__ blocks, int n_blocks, int n_kv,
+    const uint16_t* __restrict__ kc, const uint64_t* __restrict__ k_layers,
+    long k_sb, long k_st, long k_sh, int NB,
+    const int* __restrict__ blocks, const int* __restrict__ n_dev, int n_blocks, int n_kv,
+    int n_layers, long layer_rows,
     uint8_t* __restrict__ v4, uint16_t* __restrict__ vs, int8_t* __restrict__ c8,
     uint16_t* __restrict__ cs, int8_t* __restrict__ mu8, uint16_t* __restrict__ mus,
     uint16_t* __restrict__ tag)
@@ -227,51 +242,58 @@ __global__ __launch_bounds__(bd_waves<D>() * kWave) void rki4_build_kernel(
     __shared__ WaveLds<D> lds[NW];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     WaveLds<D>& L = lds[wave];
-    const long item = (long)blockIdx.x * NW + wave;      // (block index, kv head)
-    if (item >= (long)n_blocks * n_kv) return;
-    const int bi = (int)(item / n_kv), kh = (int)(item % n_kv);
-    const int blk = blocks[bi];
-    if (blk < 0 || blk >= NB) return;                          // masked (profile pass)
-    const long row = (long)blk * n_kv + kh;
-    const uint16_t* kp = kc + (long)blk * k_sb + (long)kh * k_sh;
+    const int nb_valid = n_dev ? min(*n_dev, n_blocks) : n_blocks;
+    const long per_layer = (long)nb_valid * n_kv;
+    // one wave per (layer, block index, kv head), grid-stride
+    for (long item = (long)blockIdx.x * NW + wave; item < per_layer * n_layers;
+         item += (long)gridDim.x * NW) {
+        const int layer = (int)(item / per_layer);
+        const long rem = item - (long)layer * per_layer;
+        const int bi = (int)(rem / n_kv), kh = (int)(rem % n_kv);
+        const int blk = blocks[bi];
+        if (blk < 0 || blk >= NB) continue;                        // masked (profile pass)
+        const long row = (long)layer * layer_rows + (long)blk * n_kv + kh;
+        const uint16_t* kbase = k_layers ? reinterpret_cast<const uint16_t*>(k_layers[layer]) : kc;
+        const uint16_t* kp = kbase + (long)blk * k_sb + (long)kh * k_sh;
 
-    // stage K (fp32) and the centroid (sequential sum over t, then / 16)
-    for (int i = lane; i < BD_PG * D / 8; i += kWave) {
-        const int t = i / (D / 8), d0 = (i % (D / 8)) * 8;
-        const uint4 w = *reinterpret_cast<const uint4*>(kp + (long)t * k_st + d0);
-        const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+        // stage K (fp32) and the centroid (sequential sum over t, then / 16)
+        for (int i = lane; i < BD_PG * D / 8; i += kWave) {
+            const int t = i / (D / 8), d0 = (i % (D / 8)) * 8;
+            const uint4 w = *reinterpret_cast<const uint4*>(kp + (long)t * k_st + d0);
+            const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            L.dc[t][d0 + 2 * e] = bf16lo(ws[e]);
-            L.dc[t][d0 + 2 * e + 1] = bf16hi(ws[e]);
+            for (int e = 0; e < 4; ++e) {
+                L.dc[t][d0 + 2 * e] = bf16lo(ws[e]);
+                L.dc[t][d0 + 2 * e + 1] = bf16hi(ws[e]);
+            }
         }
-    }
-    if (lane < 8) tag[row * 8 + lane] = kp[(long)(BD_PG - 1) * k_st + lane];
-    wave_lds_sync();
-    for (int d = lane; d < D; d += kWave) {
-        float acc = 0.f;
-        for (int t = 0; t < BD_PG; ++t) acc = __fadd_rn(acc, L.dc[t][d]);
-        const float m = __fdiv_rn(acc, (float)BD_PG);
-        L.mu[d] = m;
-        for (int t = 0; t < BD_PG; ++t) L.dc[t][d] = __fsub_rn(L.dc[t][d], m);
-    }
-    wave_lds_sync();
+        if (lane < 8) tag[row * 8 + lane] = kp[(long)(BD_PG - 1) * k_st + lane];
+        wave_lds_sync();
+        for (int d = lane; d < D; d += kWave) {
+            float acc = 0.f;
+            for (int t = 0; t < BD_PG; ++t) acc = __fadd_rn(acc, L.dc[t][d]);
+            const float m = __fdiv_rn(acc, (float)BD_PG);
+            L.mu[d] = m;
+            for (int t = 0; t < BD_PG; ++t) L.dc[t][d] = __fsub_rn(L.dc[t][d], m);
+        }
+        wave_lds_sync();
 
-    // gram on the matrix core: Gm[i][j] = sum_d dc[i][d] dc[j][d]
-    {
-        const int i = lane & 15, kq = lane >> 4;
-        v4f g = {0.f, 0.f, 0.f, 0.f};
-        for (int s = 0; s < D / 4; ++s) {
-            const float a = L.dc[i][4 * s + kq];
-            g = __builtin_amdgcn_mfma_f32_16x16x4f32(a, a, g, 0, 0, 0);
-        }
+        // gram on the matrix core: Gm[i][j] = sum_d dc[i][d] dc[j][d]
+        {
+            const int i = lane & 15, kq = lane >> 4;
+            v4f g = {0.f, 0.f, 0.f, 0.f};
+            for (int s = 0; s < D / 4; ++s) {
+                const float a = L.dc[i][4 * s + kq];
+                g = __builtin_amdgcn_mfma_f32_16x16x4f32(a, a, g, 0, 0, 0);
+            }
 #pragma unroll
-        for (int v = 0; v < 4; ++v) L.A[4 * kq + v][i] = g[v];
+            for (int v = 0; v < 4; ++v) L.A[4 * kq + v][i] = g[v];
+        }
+        wave_lds_sync();
+        jacobi16(L);
+        select_top8(L);
+        pack_page<D>(L, row, v4, vs, c8, cs, mu8, mus);
     }
-    wave_lds_sync();
-    jacobi16(L);
-    select_top8(L);
-    pack_page<D>(L, row, v4, vs, c8, cs, mu8, mus);
 }
 
 // locks_pack_rki4: quantize + pack given the caller's eigen decomposition.
@@ -299,6 +321,80 @@ __global__ __launch_bounds__(4 * kWave) void rki4_pack_kernel(
     pack_page<BD_D>(L, rows[item], v4, vs, c8, cs, mu8, mus);
 }
 
+// ---- refresh lifecycle: which blocks to (re)build --------------------------
+// Reference producers: selection/build.py:372-384 _tail_blocks, :415-427
+// _bulk_blocks, :472-488 _delta_select (rki4_build.py:264-315 call them).
+// One thread per candidate page marks its physical block in a byte map
+// (duplicates collapse: pages shared by several requests are built once);
+// refresh_compact_kernel turns the map into a list plus a device count and
+// clears the map again.  No host sync on any mode.
+constexpr int RF_THREADS = 256;
+
+__device__ __forceinline__ bool tags_differ(uint4 a, uint4 b) {
+    // bf16 values compared as numbers, like the reference's float compare:
+    // NaN (the never-built tag) differs from everything, -0 equals +0
+    const uint32_t wa[4] = {a.x, a.y, a.z, a.w}, wb[4] = {b.x, b.y, b.z, b.w};
+    bool d = false;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+        d |= (bf16lo(wa[e]) != bf16lo(wb[e])) | (bf16hi(wa[e]) != bf16hi(wb[e]));
+    return d;
+}
+
+__global__ __launch_bounds__(RF_THREADS) void refresh_mark_kernel(
+    int mode, const int* __restrict__ bt, long bt_sr, const int* __restrict__ sl, int n_req,
+    const int* __restrict__ rows, int n_rows, int max_fin, int page, int NB,
+    const uint64_t* __restrict__ k_layers, long k_sb, long k_st, long k_sh, int n_kv,
+    const uint16_t* __restrict__ tag, long layer_rows, uint8_t* __restrict__ mark,
+    int* __restrict__ count)
+{
+    const long i = (long)blockIdx.x * RF_THREADS + threadIdx.x;
+    if (i == 0 && blockIdx.y == 0) *count = 0;           // compact runs after this kernel
+    // delta: one thread per (page, kv head), heads of one page adjacent
+    const int kh = mode == LOCKS_REFRESH_DELTA ? (int)(i % n_kv) : 0;
+    const long pi = mode == LOCKS_REFRESH_DELTA ? i / n_kv : i;
+    int blk;
+    if (mode == LOCKS_REFRESH_TAIL) {
+        if (pi >= n_rows) return;
+        const int r = rows ? rows[pi] : (int)pi;
+        if (r < 0 || r >= n_req) return;
+        const int fin1 = min(max(sl[r] / page - 1, 0), (int)bt_sr - 1);   // last finalized page
+        blk = bt[(long)r * bt_sr + fin1];
+    } else {
+        if (pi >= (long)n_req * max_fin) return;
+        const int r = (int)(pi / max_fin), p = (int)(pi % max_fin);
+        if (p >= sl[r] / page) return;                    // not finalized
+        blk = bt[(long)r * bt_sr + p];
+    }
+    if (blk < 0 || blk >= NB) return;
+    if (mode == LOCKS_REFRESH_DELTA) {
+        const int layer = blockIdx.y;
+        const uint16_t* kp = reinterpret_cast<const uint16_t*>(k_layers[layer]) +
+                             (long)blk * k_sb + (long)(page - 1) * k_st + (long)kh * k_sh;
+        const uint16_t* tp = tag + ((long)layer * layer_rows + (long)blk * n_kv + kh) * 8;
+        if (!tags_differ(*reinterpret_cast<const uint4*>(kp), *reinterpret_cast<const uint4*>(tp)))
+            return;
+    }
+    mark[blk] = 1;
+}
+
+__global__ __launch_bounds__(RF_THREADS) void refresh_compact_kernel(
+    uint8_t* __restrict__ mark, int NB, int* __restrict__ blocks, int* __restrict__ count)
+{
+    const int i = blockIdx.x * RF_THREADS + threadIdx.x;
+    const int lane = threadIdx.x & 63;
+    const bool m = i < NB && mark[i] != 0;
+    if (m) mark[i] = 0;
+    const uint64_t bal = __ballot(m);
+    if (bal == 0) return;
+    const int pre = __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                              __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+    int base = 0;
+    if (lane == 0) base = atomicAdd(count, __popcll(bal));
+    base = __shfl(base, 0);
+    if (m) blocks[base + pre] = i;
+}
+
 }  // namespace locks
 
 using namespace locks;
@@ -320,13 +416,12 @@ extern "C" int32_t locks_build_rki4(
     if (n_blocks == 0) return 0;
     const long items = (long)n_blocks * n_kv;
     const int nw = head_dim == 128 ? bd_waves<128>() : bd_waves<512>();
-    const long grid = (items + nw - 1) / nw;
-    LOCKS_REQUIRE(grid < (1L << 31), "locks_build_rki4: too many pages in one call");
+    const long grid = std::min((items + nw - 1) / nw, BD_MAX_GRID);
 #define BUILD_LAUNCH(DV)                                                                     \
     hipLaunchKernelGGL((rki4_build_kernel<DV>), dim3((unsigned)grid), dim3(nw * kWave), 0,  \
-                       (hipStream_t)stream, k_cache, (long)k_stride_block, (long)k_stride_tok, \
-                       (long)k_stride_head, num_blocks, blocks, n_blocks, n_kv, v4, vs, c8, cs, \
-                       mu8, mus, tag)
+                       (hipStream_t)stream, k_cache, nullptr, (long)k_stride_block,          \
+                       (long)k_stride_tok, (long)k_stride_head, num_blocks, blocks, nullptr,   \
+                       n_blocks, n_kv, 1, 0L, v4, vs, c8, cs, mu8, mus, tag)
     if (head_dim == 128) BUILD_LAUNCH(128);
     else BUILD_LAUNCH(512);
 #undef BUILD_LAUNCH
@@ -348,4 +443,79 @@ extern "C" int32_t locks_pack_rki4(const float* mu, const float* dc, const float
     hipLaunchKernelGGL(rki4_pack_kernel, dim3((n + 3) / 4), dim3(4 * kWave),
                        0, (hipStream_t)stream, mu, dc, S2, U, rows, n, v4, vs, c8, cs, mu8, mus);
     return check_launch("rki4_pack_kernel");
+}
+
+extern "C" int32_t locks_refresh_blocks(
+    int32_t mode, const int32_t* block_table, int64_t bt_stride, const int32_t* seq_lens,
+    int32_t n_req, const int32_t* rows, int32_t n_rows, int32_t max_fin, int32_t page,
+    int32_t num_blocks, const uint64_t* k_layers, int32_t n_layers, int64_t k_stride_block,
+    int64_t k_stride_tok, int64_t k_stride_head, int32_t n_kv, const uint16_t* tag,
+    int64_t tag_blocks, uint8_t* mark, int32_t* blocks, int32_t* count, void* stream)
+{
+    LOCKS_REQUIRE(mode == LOCKS_REFRESH_TAIL || mode == LOCKS_REFRESH_BULK ||
+                      mode == LOCKS_REFRESH_DELTA,
+                  "locks_refresh_blocks: unknown mode %d", mode);
+    LOCKS_REQUIRE(block_table && seq_lens && mark && blocks && count,
+                  "locks_refresh_blocks: null pointer argument");
+    LOCKS_REQUIRE(n_req >= 0 && n_rows >= 0 && max_fin >= 0 && page >= 1 && num_blocks >= 1 &&
+                      bt_stride >= 1,
+                  "locks_refresh_blocks: bad geometry");
+    if (mode == LOCKS_REFRESH_BULK || mode == LOCKS_REFRESH_DELTA)
+        LOCKS_REQUIRE(max_fin <= bt_stride, "locks_refresh_blocks: max_fin %d > block-table width %lld",
+                      max_fin, (long long)bt_stride);
+    if (mode == LOCKS_REFRESH_DELTA) {
+        LOCKS_REQUIRE(k_layers && tag && n_layers >= 1 && n_layers <= 65535 && n_kv >= 1 &&
+                          tag_blocks >= num_blocks,
+                      "locks_refresh_blocks: delta needs k_layers, tag, n_layers, n_kv");
+        LOCKS_REQUIRE(k_stride_tok % 8 == 0 && k_stride_block % 8 == 0 && k_stride_head % 8 == 0,
+                      "locks_refresh_blocks: K strides must be multiples of 8 elements");
+    }
+    const long items = mode == LOCKS_REFRESH_TAIL ? (long)n_rows
+                       : (long)n_req * max_fin * (mode == LOCKS_REFRESH_DELTA ? n_kv : 1);
+    const long gx = std::max<long>(1, (items + RF_THREADS - 1) / RF_THREADS);
+    LOCKS_REQUIRE(gx < (1L << 31), "locks_refresh_blocks: too many pages in one call");
+    const int gy = mode == LOCKS_REFRESH_DELTA ? n_layers : 1;
+    hipLaunchKernelGGL(refresh_mark_kernel, dim3((unsigned)gx, gy), dim3(RF_THREADS), 0,
+                       (hipStream_t)stream, mode, block_table, (long)bt_stride, seq_lens, n_req,
+                       rows, n_rows, max_fin, page, num_blocks, k_layers, (long)k_stride_block,
+                       (long)k_stride_tok, (long)k_stride_head, n_kv, tag,
+                       (long)tag_blocks * n_kv, mark, count);
+    int32_t rc = check_launch("refresh_mark_kernel");
+    if (rc) return rc;
+    hipLaunchKernelGGL(refresh_compact_kernel, dim3((num_blocks + RF_THREADS - 1) / RF_THREADS),
+                       dim3(RF_THREADS), 0, (hipStream_t)stream, mark, num_blocks, blocks, count);
+    return check_launch("refresh_compact_kernel");
+}
+
+extern "C" int32_t locks_build_rki4_layers(
+    const uint64_t* k_layers, int32_t n_layers, int64_t k_stride_block, int64_t k_stride_tok,
+    int64_t k_stride_head, int32_t num_blocks, const int32_t* blocks, const int32_t* count,
+    int32_t n_blocks, int32_t n_kv, int32_t head_dim, int32_t page, int64_t slab_blocks,
+    uint8_t* v4, uint16_t* vs, int8_t* c8, uint16_t* cs, int8_t* mu8, uint16_t* mus,
+    uint16_t* tag, void* stream)
+{
+    LOCKS_REQUIRE((head_dim == 128 || head_dim == 512) && page == BD_PG,
+                  "locks_build_rki4_layers: geometry d=%d page=%d unsupported (this build: d 128 or 512, page 16)",
+                  head_dim, page);
+    LOCKS_REQUIRE(n_kv >= 1 && num_blocks >= 1 && n_blocks >= 0 && n_layers >= 1 &&
+                      n_layers <= 65535 && slab_blocks >= num_blocks,
+                  "locks_build_rki4_layers: bad geometry");
+    LOCKS_REQUIRE(k_stride_tok % 8 == 0 && k_stride_block % 8 == 0 && k_stride_head % 8 == 0,
+                  "locks_build_rki4_layers: K strides must be multiples of 8 elements");
+    LOCKS_REQUIRE(k_layers && blocks && v4 && vs && c8 && cs && mu8 && mus && tag,
+                  "locks_build_rki4_layers: null pointer argument");
+    if (n_blocks == 0) return 0;
+    const long items = (long)n_blocks * n_kv * n_layers;
+    const int nw = head_dim == 128 ? bd_waves<128>() : bd_waves<512>();
+    const long grid = std::min((items + nw - 1) / nw, BD_MAX_GRID);
+    const long layer_rows = (long)slab_blocks * n_kv;
+#define BUILD_LAYERS_LAUNCH(DV)                                                              \
+    hipLaunchKernelGGL((rki4_build_kernel<DV>), dim3((unsigned)grid), dim3(nw * kWave),       \
+                       0, (hipStream_t)stream, nullptr, k_layers, (long)k_stride_block,        \
+                       (long)k_stride_tok, (long)k_stride_head, num_blocks, blocks, count,     \
+                       n_blocks, n_kv, n_layers, layer_rows, v4, vs, c8, cs, mu8, mus, tag)
+    if (head_dim == 128) BUILD_LAYERS_LAUNCH(128);
+    else BUILD_LAYERS_LAUNCH(512);
+#undef BUILD_LAYERS_LAUNCH
+    return check_launch("rki4_build_kernel");
 }
