@@ -236,6 +236,40 @@ def scorer_roofline(m, reps=3):
     return e0.elapsed_time(e1) * 1e3 / (reps * m["L"])       # us per launch
 
 
+def stream_read_us(nbytes, layers, reps=3):
+    """Practical read ceiling for a launch of `nbytes`: a plain streaming read
+    (`locks_calib_read`) over `layers` distinct buffers, captured and timed
+    like the scorer (so each launch is cold in the 256 MB Infinity Cache when
+    layers x nbytes exceeds it).  Returns us per launch."""
+    import torch
+    from locks import _lib
+    lib = _lib.load()
+    nb = (int(nbytes) + 15) // 16 * 16
+    buf = torch.ones(layers * nb, dtype=torch.uint8, device="cuda")
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+
+    def launches():
+        st = _lib.stream_ptr()
+        for layer in range(layers):
+            _lib.check(lib.locks_calib_read(buf.data_ptr() + layer * nb, nb, sink.data_ptr(), st),
+                       "calib_read")
+
+    g = capture(launches)
+    s = torch.cuda.current_stream()
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    for _ in range(reps):
+        g.replay()
+    e1.record(s)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (reps * layers)
+    del g, buf
+    torch.cuda.empty_cache()
+    return us
+
+
 def cpu_baseline(m, sample_pages=4096):
     """Oracle (numpy) timed on the host on a bounded sample: one layer,
     `sample_pages` selectable pages of every kv head; scaled to ms/step."""
@@ -457,6 +491,7 @@ def run_mla(a, wl):
     by = mla_step_bytes(m)
     score_us = mla_scorer_us(m)
     score_gbps = by["score_per_launch"] / (score_us * 1e-6) / 1e9
+    stream_us = stream_read_us(by["score_per_launch"], L)
     res = {}
     if not a.no_dense:
         dn = make_mla_dense(m)
@@ -488,7 +523,9 @@ def run_mla(a, wl):
                      "frac": round(score_gbps / HBM_PEAK_GBPS, 4),
                      "avg_launch_us": round(score_us, 3),
                      "bytes_per_launch": by["score_per_launch"],
-                     "traffic": scorer_traffic(a.workload)},
+                     "traffic": scorer_traffic(a.workload),
+                     "stream_read_same_bytes_us": round(stream_us, 3),
+                     "frac_of_stream_read": round(stream_us / score_us, 4)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
@@ -637,6 +674,7 @@ def main():
     log(f"sparse step {ms:.3f} ms")
     score_us = scorer_roofline(m)
     score_gbps = by["score_per_launch"] / (score_us * 1e-6) / 1e9
+    stream_us = stream_read_us(by["score_per_launch"], m["L"])
     res = {}
     if not a.no_dense:
         dn = make_dense(m)
@@ -670,7 +708,9 @@ def main():
                      "frac": round(score_gbps / HBM_PEAK_GBPS, 4),
                      "avg_launch_us": round(score_us, 3),
                      "bytes_per_launch": by["score_per_launch"],
-                     "traffic": scorer_traffic(a.workload)},
+                     "traffic": scorer_traffic(a.workload),
+                     "stream_read_same_bytes_us": round(stream_us, 3),
+                     "frac_of_stream_read": round(stream_us / score_us, 4)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -276,6 +276,16 @@ int32_t locks_build_rki4_layers(const uint64_t* k_layers, int32_t n_layers,
                                 uint16_t* mus, uint16_t* tag, void* stream);
 
 
+/*
+ * Measurement helper (no counterpart in the reference): one streaming read of
+ * `bytes` (a multiple of 16) from `src`, 2048 workgroups; `sink` receives a
+ * store only in a practically impossible case.  Benchmarks time it beside a
+ * kernel that moves the same bytes, as the practical read ceiling of a
+ * launch of that size.
+ */
+int32_t locks_calib_read(const void* src, int64_t bytes, uint32_t* sink, void* stream);
+
+
 /* ---------------------------------------------------------------------------
  * MLA (one latent KV head shared by all query heads; DeepSeek-V2-Lite:
  * kv_lora_rank 512 + 64 RoPE dims, 16 heads).  The cache is the engine's

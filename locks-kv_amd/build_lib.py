@@ -18,7 +18,8 @@ CSRC = os.path.join(HERE, "csrc")
 OUT_DIR = os.path.join(HERE, "locks", "_lib")
 LIB = os.path.join(OUT_DIR, "liblocks_hip.so")
 SOURCES = ["locks_capi.cpp", "locks_score.hip", "locks_select.hip", "locks_decode.hip", "locks_build.hip",
-           "locks_mla.hip"]
+           "locks_mla.hip",
+           "locks_calib.hip"]
 ARCH = "gfx950"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

@@ -41,6 +41,7 @@ SIGNATURES = {
                                     _i32, _i64, _i64, _i64, _i32, _p, _i64, _p, _p, _p, _p]),
     "locks_build_rki4_layers": (_i32, [_p, _i32, _i64, _i64, _i64, _i32, _p, _p, _i32, _i32,
                                        _i32, _i32, _i64, _p, _p, _p, _p, _p, _p, _p, _p]),
+    "locks_calib_read": (_i32, [_p, _i64, _p, _p]),
     "locks_pack_rki4": (_i32, [_p, _p, _p, _p, _p, _i32, _i32, _i32, _p, _p, _p, _p, _p, _p, _p]),
     "locks_mla_score": (_i32, [_p, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _p,
                                _i64, _i32, _p, _p, _i64, _i32, _i32, _i32, _i32, _i32, _i32,
