@@ -254,3 +254,37 @@ def test_gate_keeps_every_finalized_page_fresh():
             lens = [x + 1 for x in lens]
         qlen = [1] * n
     print(f"[case] gate steps ok, built_once={gate.built_once}", flush=True)
+
+
+def test_mla_latent_refresh_equals_per_layer_build():
+    """The batched producers serve the MLA latent summaries too (head_dim 512,
+    one latent head): bulk and delta over the latent views of the cache give
+    the bytes of the per-layer latent build."""
+    import torch
+    from locks.selection import MlaState, mla_build_blocks, rki4_build_bulk, rki4_build_delta
+    L, NB, MP = 2, 40, 16
+    g = torch.Generator().manual_seed(11)
+    caches = [torch.randn(NB, PAGE, 576, generator=g).to(torch.bfloat16).cuda() for _ in range(L)]
+    lat = [c[:, :, None, :512] for c in caches]            # (NB, page, 1, 512) views
+    perm = torch.randperm(NB, generator=g)[:2 * MP].view(2, MP).to(torch.int32)
+    bt = perm.cuda()
+    sl = torch.tensor([16 * 11 + 4, 16 * 6], dtype=torch.int32, device="cuda")
+
+    def state():
+        return MlaState("cuda", num_layers=L, num_blocks=NB, n_heads=16, max_reqs=2,
+                        max_pages=MP, budget_pages=8, sink_pages=1, window_pages=2)
+
+    print("[case] mla latent bulk/delta", flush=True)
+    a = state()
+    rki4_build_bulk(a, lat, bt, sl, 2, 11)
+    fin = sorted(set(perm[0, :11].tolist()) | set(perm[1, :6].tolist()))
+    b = state()
+    for layer in range(L):
+        mla_build_blocks(b, layer, caches[layer], torch.tensor(fin, dtype=torch.int32))
+    _assert_same(_slab_bytes(a), _slab_bytes(b))
+    assert rki4_build_delta(a, lat, bt, sl, 2, 11) == 0
+    caches[1][fin[2], PAGE - 1, 5] += 1.0                  # latent tag channel
+    assert rki4_build_delta(a, lat, bt, sl, 2, 11) == L
+    for layer in range(L):
+        mla_build_blocks(b, layer, caches[layer], torch.tensor([fin[2]], dtype=torch.int32))
+    _assert_same(_slab_bytes(a), _slab_bytes(b))
