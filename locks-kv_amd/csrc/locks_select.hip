@@ -665,12 +665,13 @@ __global__ __launch_bounds__(FIN_BLK) void sel_finish_kernel(
 
 // ---------------------------------------------------------------------------
 // page-parallel route with register-resident keys (rows > ROW_MAXP pages):
-// sel_chunk2_kernel: one 512-thread workgroup per 2048-page chunk, 4 pages
-// per thread; sel_finish2_kernel: one 1024-thread workgroup per row holds up
+// sel_chunk2_kernel: one 1024-thread workgroup per 2048-page chunk, 2 pages
+// per thread (measured faster than 512 x 4: less serial work per thread); sel_finish2_kernel: one 1024-thread workgroup per row holds up
 // to 4096 candidates (4 per thread) in registers.
 // ---------------------------------------------------------------------------
-constexpr int C2_BLK = 512;
-constexpr int C2_E = SEL_CH / C2_BLK;                  // 4
+constexpr int C2_BLK = 1024;
+constexpr int C2_E = SEL_CH / C2_BLK;                  // 2
+static_assert(C2_E == 2, "sel_chunk2_kernel loads and stores its pages as float2");
 constexpr int F2_BLK = 1024;
 constexpr int F2_CAP = F2_BLK * 16;                    // register-resident candidates
 
@@ -692,7 +693,7 @@ __global__ __launch_bounds__(C2_BLK) void sel_chunk2_kernel(
     const long rk = (long)r * n_kv + kh;
     const int n_sel_hi = min(nsh[r], MP);
     const int c0 = z * SEL_CH;
-    const int p0 = c0 + C2_E * tid;                     // this thread's 4 pages
+    const int p0 = c0 + C2_E * tid;                     // this thread's C2_E pages
 
     __shared__ float hm[16];
     __shared__ int hist[4096];
@@ -702,10 +703,10 @@ __global__ __launch_bounds__(C2_BLK) void sel_chunk2_kernel(
 
     // score_h of every head in flight first (row-bounded, no parameter wait)
     const float* shb = score_h + rk * (long)G * MP;
-    float4 xv[16];
+    float2 xv[16];
 #pragma unroll
     for (int g = 0; g < 16; ++g)                         // clamped, unconditional (see the row kernel)
-        xv[g] = *reinterpret_cast<const float4*>(shb + (long)min(g, G - 1) * MP + min(p0, MP - 4));
+        xv[g] = *reinterpret_cast<const float2*>(shb + (long)min(g, G - 1) * MP + min(p0, MP - 2));
     int* trow = page_table + rk * (long)MP;
 #pragma unroll
     for (int e = 0; e < C2_E; ++e)
@@ -723,7 +724,7 @@ __global__ __launch_bounds__(C2_BLK) void sel_chunk2_kernel(
 #pragma unroll
     for (int g = 0; g < 16; ++g) {
         if (g < G) {
-            const float x4[4] = {xv[g].x, xv[g].y, xv[g].z, xv[g].w};
+            const float x4[2] = {xv[g].x, xv[g].y};
 #pragma unroll
             for (int e = 0; e < C2_E; ++e) {
                 if (combine == 0) acc[e] += __expf(x4[e] - hm[g]);
@@ -734,7 +735,7 @@ __global__ __launch_bounds__(C2_BLK) void sel_chunk2_kernel(
     const int pend = max(n_sel_hi, 0);
     float* srow = score + rk * (long)MP;
     if (p0 + C2_E <= pend) {
-        *reinterpret_cast<float4*>(srow + p0) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+        *reinterpret_cast<float2*>(srow + p0) = make_float2(acc[0], acc[1]);
     } else {
 #pragma unroll
         for (int e = 0; e < C2_E; ++e)
@@ -855,7 +856,7 @@ __global__ __launch_bounds__(C2_BLK) void sel_band_kernel(
         if (tid == 0) cand_cnt[rk * Z1 + z] = 0;
         return;
     }
-    // boundary bin: thread t holds bins top .. top - 7 (top = 4095 - 8 t),
+    // boundary bin: thread t holds bins top .. top - BPT + 1 (top = 4095 - BPT t),
     // ascending threads = descending bins
     constexpr int BPT = 4096 / C2_BLK;
     const int top = 4095 - BPT * tid;
