@@ -54,7 +54,7 @@ struct WaveLds {
 // S8 (LDS), writing the six slab rows.  Lane l owns the packed bytes
 // j = l + 64 k (d = 2j, 2j + 1).
 template <int D>
-__device__ void pack_page(WaveLds<D>& L, long row, uint8_t* __restrict__ v4, uint16_t* __restrict__ vs,
+__device__ __forceinline__ void pack_page(WaveLds<D>& L, long row, uint8_t* __restrict__ v4, uint16_t* __restrict__ vs,
                           int8_t* __restrict__ c8, uint16_t* __restrict__ cs,
                           int8_t* __restrict__ mu8, uint16_t* __restrict__ mus) {
     constexpr int NK = D / 128;
@@ -68,6 +68,10 @@ __device__ void pack_page(WaveLds<D>& L, long row, uint8_t* __restrict__ v4, uin
             const int d = 2 * (lane + 64 * k) + e;
 #pragma unroll
             for (int r = 0; r < BD_RNK; ++r) {
+                // compiler barrier: one column's operands live at a time
+                // (hoisting all 16 x 8 basis values costs ~130 VGPRs and
+                // halves the build's occupancy)
+                asm volatile("" ::: "memory");
                 float acc = 0.f;
                 const int c = L.col[r];
                 for (int t = 0; t < BD_PG; ++t) acc = __fadd_rn(acc, __fmul_rn(L.dc[t][d], L.U[t][c]));
