@@ -534,7 +534,8 @@ def run_mla(a, wl):
 def run_refresh(a, m):
     """Summary refresh lifecycle on the bench model (one JSON line): bulk
     rebuild of every finalized page in every layer, the delta tag scan with
-    nothing stale, and the one-row tail of a page-crossing decode step."""
+    nothing stale, the one-row tail of a page-crossing decode step alone, and
+    what the tail adds to a captured decode step (tail + step vs step)."""
     import torch
     from locks.selection import rki4_build_bulk, rki4_build_delta, rki4_build_tail
 
@@ -558,6 +559,14 @@ def run_refresh(a, m):
     bulk = ms(lambda: rki4_build_bulk(st, ks, m["bt"], sl, R, max_fin), 2)
     delta = ms(lambda: rki4_build_delta(st, ks, m["bt"], sl, R, max_fin), 10)
     tail = ms(lambda: rki4_build_tail(st, ks, m["bt"], sl, R, rows), 20)
+    # in situ: a page-crossing decode step (tail + the sparse step) against
+    # the sparse step alone, both as graph replays on a busy GPU
+    out = [torch.empty(m["R"], m["n_kv"] * m["G"], D, dtype=torch.bfloat16, device="cuda")
+           for _ in range(m["L"])]
+    g_step = capture(lambda: sparse_step(m, out))
+    g_cross = capture(lambda: (rki4_build_tail(st, ks, m["bt"], sl, R, rows), sparse_step(m, out)))
+    t_step = time_graph(g_step, 30, 3)
+    t_cross = time_graph(g_cross, 30, 3)
     pages = int((sl // PAGE).sum().item())
     print(json.dumps({
         "metric": "summary refresh ms", "unit": "ms", "higher_is_better": False,
@@ -565,6 +574,8 @@ def run_refresh(a, m):
                    "finalized_pages": pages},
         "bulk_ms": round(bulk, 3), "delta_nothing_stale_ms": round(delta, 4),
         "tail_one_row_ms": round(tail, 4),
+        "step_ms": round(t_step, 4), "step_with_tail_ms": round(t_cross, 4),
+        "tail_in_step_ms": round(t_cross - t_step, 4),
         "bulk_us_per_gram": round(bulk * 1e3 / (pages * m["L"] * m["n_kv"]), 4)}), flush=True)
 
 

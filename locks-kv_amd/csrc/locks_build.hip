@@ -44,7 +44,6 @@ struct WaveLds {
     float A[BD_PG][BD_PG + 1];   // gram, rotated in place
     float U[BD_PG][BD_PG + 1];   // accumulated eigenvectors (columns)
     float cc[BD_PG], ss[BD_PG];
-    int partner[BD_PG];
     float S8[BD_RNK];
     int col[BD_RNK];             // eigen column of basis r (ascending top-8)
     float red[BD_RNK][kWave / 8];
@@ -133,9 +132,33 @@ __device__ __forceinline__ void pack_page(WaveLds<D>& L, long row, uint8_t* __re
 }
 
 // Parallel cyclic Jacobi on L.A (16x16 symmetric); eigenvectors -> L.U columns.
+// Round-robin pairing of step `step`: index 0 stays, 1..15 rotate; the
+// pair of position k (1 <= k <= 7) is (at(k), at(15 - k)), position 0 pairs
+// index 0 with at(0), where at(k) = 1 + (k + step) % 15.
+__device__ __forceinline__ int rr_at(int k, int step) { return 1 + (k + step) % (BD_PG - 1); }
+__device__ __forceinline__ int rr_partner(int i, int step) {
+    if (i == 0) return rr_at(0, step);
+    const int k = (i - 1 - step + (BD_PG - 1)) % (BD_PG - 1);
+    return k == 0 ? 0 : rr_at(BD_PG - 1 - k, step);
+}
+
+// Parallel cyclic Jacobi on the 16x16 symmetric matrix in L.A (eigenvalues
+// end on the diagonal, eigenvectors in the columns of L.U).  One step applies
+// the 8 disjoint rotations of the round-robin schedule as one two-sided update
+// A'' = J^T A J read entirely from the old A:
+//   A''[i][j] = c_j (c_i A[i][j] + s_i A[pi][j]) + s_j (c_i A[i][pj] + s_i A[pi][pj])
+//   U'[i][j]  = c_j U[i][j] + s_j U[i][pj]
+// Lane l owns column j = l & 15 of rows (l >> 4) + 4e.  A wave executes its
+// LDS instructions in order, so the old values every lane reads are read
+// before any lane writes (the asm barriers keep the compiler from moving the
+// accesses across each other): two dependent LDS round trips per step.
+// Rotation parameters use the hardware reciprocal and reciprocal square root
+// (~1 ulp): a rotation only has to reduce the off-diagonal mass, and the
+// result is checked through the quantised summary, not bit for bit.
 template <class W>
 __device__ void jacobi16(W& L) {
     const int lane = threadIdx.x & 63;
+    const int j = lane & 15, r0 = lane >> 4;
     for (int i = lane; i < BD_PG * BD_PG; i += kWave) L.U[i / BD_PG][i % BD_PG] = (i / BD_PG == i % BD_PG) ? 1.f : 0.f;
     wave_lds_sync();
     for (int sweep = 0; sweep < BD_SWEEPS; ++sweep) {
@@ -156,53 +179,40 @@ __device__ void jacobi16(W& L) {
         // sweep limit, with the same top-8 eigenvalue accuracy (~3e-6 rel).
         if (!(off > 1e-12f * dia)) break;
         for (int step = 0; step < BD_PG - 1; ++step) {
-            // round-robin pairing: index 0 fixed, 1..15 rotate
             if (lane < BD_PG / 2) {
-                auto at = [&](int k) { return 1 + ((k + step) % (BD_PG - 1)); };
-                const int p = lane == 0 ? 0 : at(lane);
-                const int q = lane == 0 ? at(0) : at(BD_PG - 1 - lane);
-                const float apq = L.A[p][q];
-                float c = 1.f, s = 0.f;
-                if (apq != 0.f) {
-                    const float theta = (L.A[q][q] - L.A[p][p]) / (2.f * apq);
-                    const float t = copysignf(1.f, theta) / (fabsf(theta) + sqrtf(theta * theta + 1.f));
-                    c = 1.f / sqrtf(t * t + 1.f);
-                    s = t * c;
+                const int p = lane == 0 ? 0 : rr_at(lane, step);
+                const int q = lane == 0 ? rr_at(0, step) : rr_at(BD_PG - 1 - lane, step);
+                const float apq = L.A[p][q], app = L.A[p][p], aqq = L.A[q][q];
+                float c = 1.f, sn = 0.f;
+                if (fabsf(apq) > 1e-30f) {                 // smaller: nothing to rotate away
+                    const float theta = (aqq - app) * __builtin_amdgcn_rcpf(2.f * apq);
+                    const float t = copysignf(__builtin_amdgcn_rcpf(fabsf(theta) +
+                                                                    __builtin_amdgcn_sqrtf(theta * theta + 1.f)),
+                                              theta);
+                    c = __builtin_amdgcn_rsqf(t * t + 1.f);
+                    sn = t * c;
                 }
-                L.cc[p] = c; L.ss[p] = -s; L.partner[p] = q;
-                L.cc[q] = c; L.ss[q] = s;  L.partner[q] = p;
+                L.cc[p] = c; L.ss[p] = -sn;
+                L.cc[q] = c; L.ss[q] = sn;
             }
-            wave_lds_sync();
-            // rows: A'[i][j] = cc[i] A[i][j] + ss[i] A[partner i][j]
-            float nv[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int idx = lane + e * kWave, i = idx / BD_PG, j = idx % BD_PG;
-                nv[e] = L.cc[i] * L.A[i][j] + L.ss[i] * L.A[L.partner[i]][j];
-            }
-            wave_lds_sync();
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int idx = lane + e * kWave;
-                L.A[idx / BD_PG][idx % BD_PG] = nv[e];
-            }
-            wave_lds_sync();
-            // columns of A and of U
+            asm volatile("" ::: "memory");
+            const int pj = rr_partner(j, step);
+            const float cj = L.cc[j], sj = L.ss[j];
             float na[4], nu[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const int idx = lane + e * kWave, i = idx / BD_PG, j = idx % BD_PG;
-                na[e] = L.cc[j] * L.A[i][j] + L.ss[j] * L.A[i][L.partner[j]];
-                nu[e] = L.cc[j] * L.U[i][j] + L.ss[j] * L.U[i][L.partner[j]];
+                const int i = r0 + 4 * e, pi = rr_partner(i, step);
+                const float ci = L.cc[i], si = L.ss[i];
+                na[e] = cj * (ci * L.A[i][j] + si * L.A[pi][j]) + sj * (ci * L.A[i][pj] + si * L.A[pi][pj]);
+                nu[e] = cj * L.U[i][j] + sj * L.U[i][pj];
             }
-            wave_lds_sync();
+            asm volatile("" ::: "memory");
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const int idx = lane + e * kWave;
-                L.A[idx / BD_PG][idx % BD_PG] = na[e];
-                L.U[idx / BD_PG][idx % BD_PG] = nu[e];
+                L.A[r0 + 4 * e][j] = na[e];
+                L.U[r0 + 4 * e][j] = nu[e];
             }
-            wave_lds_sync();
+            asm volatile("" ::: "memory");
         }
     }
 }
