@@ -150,3 +150,55 @@ def test_mla_entries_reject_bad_geometry_without_device():
     bargs = [1, 16 * 576, 576, 0, 8, 1, 1, 1, 256, 16] + [1] * 7 + [None]
     assert lib.locks_build_rki4(*bargs) == -1 and b"d=256" in lib.locks_last_error()
 
+
+
+def test_refresh_entries_reject_bad_arguments_without_device():
+    from locks import _lib
+    lib = _lib.load()
+    # locks_refresh_blocks(mode, bt, bt_stride, sl, n_req, rows, n_rows, max_fin, page, num_blocks,
+    #                      k_layers, n_layers, k_sb, k_st, k_sh, n_kv, tag, tag_blocks, mark,
+    #                      blocks, count, stream)
+    ok = [1, 1, 64, 1, 2, None, 0, 8, 16, 100, None, 0, 0, 0, 0, 1, None, 100, 1, 1, 1, None]
+    a = list(ok); a[0] = 7
+    assert lib.locks_refresh_blocks(*a) == -1 and b"unknown mode 7" in lib.locks_last_error()
+    a = list(ok); a[7] = 65                              # max_fin past the block-table width
+    assert lib.locks_refresh_blocks(*a) == -1 and b"max_fin 65" in lib.locks_last_error()
+    a = list(ok); a[0] = 2                               # delta needs K pointers and the tag slab
+    assert lib.locks_refresh_blocks(*a) == -1 and b"delta needs" in lib.locks_last_error()
+    a = list(ok); a[18] = None
+    assert lib.locks_refresh_blocks(*a) == -1 and b"null pointer" in lib.locks_last_error()
+    # locks_build_rki4_layers: geometry and the slab-blocks bound
+    bl = [1, 2, 16 * 8 * 128, 8 * 128, 128, 100, 1, None, 4, 8, 128, 16, 100] + [1] * 7 + [None]
+    b = list(bl); b[10] = 64
+    assert lib.locks_build_rki4_layers(*b) == -1 and b"d=64" in lib.locks_last_error()
+    b = list(bl); b[12] = 50                             # slab smaller than the K pool bound
+    assert lib.locks_build_rki4_layers(*b) == -1 and b"bad geometry" in lib.locks_last_error()
+    b = list(bl); b[3] = 12                              # token stride not a multiple of 8
+    assert lib.locks_build_rki4_layers(*b) == -1 and b"multiples of 8" in lib.locks_last_error()
+    assert lib.locks_calib_read(None, 64, None, None) == -1
+
+
+def test_engine_and_producers_validate_on_the_host():
+    import torch
+    from types import SimpleNamespace
+    from locks.backend.engine import LocksEngine
+    from locks.config import LocksConfig
+    from locks.selection import rki4_build_tail
+    with pytest.raises(ValueError):
+        LocksEngine(LocksConfig(variant="mem-v"), [torch.zeros(1)], num_heads_q=8,
+                    num_heads_kv=2, head_dim=128, block_size=16, max_num_seqs=1,
+                    max_model_len=64)
+    with pytest.raises(ValueError):
+        LocksEngine(LocksConfig(), [torch.zeros(1)], num_heads_q=6, num_heads_kv=4,
+                    head_dim=128, block_size=16, max_num_seqs=1, max_model_len=64)
+    with pytest.raises(ValueError):
+        LocksEngine(LocksConfig(), [], num_heads_q=8, num_heads_kv=2, head_dim=128,
+                    block_size=16, max_num_seqs=1, max_model_len=64)
+    st = SimpleNamespace(L=2, NB=4)
+    K = torch.zeros(4, 16, 2, 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):                      # one K view for a 2-layer state
+        rki4_build_tail(st, [K], torch.zeros(1, 4, dtype=torch.int32),
+                        torch.ones(1, dtype=torch.int32), 1)
+    with pytest.raises(TypeError):                       # layers of different strides
+        rki4_build_tail(st, [K, K.transpose(1, 2).contiguous().transpose(1, 2)],
+                        torch.zeros(1, 4, dtype=torch.int32), torch.ones(1, dtype=torch.int32), 1)
