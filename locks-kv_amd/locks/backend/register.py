@@ -7,7 +7,10 @@ FlashAttention backend resolves to the LOCKS backend.  On ROCm the selector
 lives on ``vllm.platforms.rocm.RocmPlatform`` (the reference patches the CUDA
 platform only).  When vLLM is not installed (as in this image) registration
 stops after loading the config: the hot path is then driven directly
-through ``backend._runtime`` (see tests/ and bench.py).
+through ``backend.engine.LocksEngine`` / ``backend._runtime``.  When vLLM-ROCm
+is importable but the vLLM backend class is not shipped (this build),
+registration refuses with ``NotImplementedError`` instead of patching the
+selector to a missing class.
 """
 from __future__ import annotations
 
@@ -41,6 +44,13 @@ def register(overrides: dict | None = None) -> None:
         print(f"[locks] registered config (variant={cfg.variant}); vLLM not importable, "
               "backend selector not patched", flush=True)
         return
+    import importlib.util
+    if importlib.util.find_spec(_OUR_PATH.rsplit(".", 1)[0]) is None:
+        # the vLLM attention-backend class is not shipped by this build:
+        # refuse here rather than let vLLM fail later on a missing import
+        raise NotImplementedError(
+            "locks: vLLM-ROCm is importable but this build ships no vLLM attention backend "
+            f"class ({_OUR_PATH}); drive the decode path with locks.backend.engine.LocksEngine")
     target = next(k for k in rocm.RocmPlatform.__mro__ if "get_attn_backend_cls" in k.__dict__)
     orig = target.__dict__["get_attn_backend_cls"].__func__
 

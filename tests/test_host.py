@@ -98,6 +98,34 @@ def test_register_inert_and_mem_refused(monkeypatch, capsys):
     assert _runtime.get_config().budget_pages == 126
 
 
+def test_register_refuses_vllm_without_backend_class(monkeypatch):
+    """vLLM-ROCm importable but no vLLM backend class shipped: refuse at
+    registration instead of patching the selector to a missing class."""
+    import sys
+    import types
+    import locks
+    from locks.backend import register as regmod
+    fake_vllm = types.ModuleType("vllm")
+    fake_platforms = types.ModuleType("vllm.platforms")
+    fake_rocm = types.ModuleType("vllm.platforms.rocm")
+
+    class RocmPlatform:
+        @classmethod
+        def get_attn_backend_cls(cls, *a, **k):
+            return "vllm.v1.attention.backends.flash_attn.FlashAttentionBackend"
+
+    fake_rocm.RocmPlatform = RocmPlatform
+    fake_platforms.rocm = fake_rocm
+    fake_vllm.platforms = fake_platforms
+    monkeypatch.setitem(sys.modules, "vllm", fake_vllm)
+    monkeypatch.setitem(sys.modules, "vllm.platforms", fake_platforms)
+    monkeypatch.setitem(sys.modules, "vllm.platforms.rocm", fake_rocm)
+    monkeypatch.setattr(regmod, "_APPLIED", False)
+    with pytest.raises(NotImplementedError, match="LocksEngine"):
+        locks.register({"budget_pages": 126})
+    assert RocmPlatform.get_attn_backend_cls().endswith("FlashAttentionBackend")   # untouched
+
+
 def test_geometry_contract():
     from locks.selection import Rki4State
     Rki4State.validate_geometry(head_dim=128, G=16, page=16)
