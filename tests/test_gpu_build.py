@@ -102,3 +102,58 @@ def test_refresh_is_tag_gated():
     n2 = rki4_build_refresh(st, 0, K, d["bt"], d["sl"], 1)
     torch.cuda.synchronize()
     assert n1 == 64 and n2 == 0          # only finalized pages; second pass: all fresh
+
+
+def test_build_degenerate_pages():
+    """Pages a Jacobi solver can trip on: constant, all-zero (zero gram), rank
+    1, exactly rank 8, one token 1000x the others.  Centroid bytes and tags
+    are exact; the zero-gram page gets zero V codes and the 1e-8 scale floor
+    (rki4_build.py:178-225); the others reconstruct the centred page as well
+    as the oracle's LAPACK build does."""
+    import torch
+    from locks.selection.rki4_build import rki4_build_blocks
+    rng = np.random.default_rng(3)
+    NB, n_kv, d = 6, 2, 128
+    k = rng.standard_normal((NB, 16, n_kv, d)).astype(np.float32)
+    k[0] = rng.standard_normal((1, n_kv, d))                       # constant page
+    k[4] = 0.0                                                     # all-zero page
+    a = rng.standard_normal((16, 1, 1))
+    k[1] = rng.standard_normal((1, n_kv, d)) + a * rng.standard_normal((1, n_kv, d))  # rank 1
+    basis = rng.standard_normal((8, n_kv, d))
+    k[3] = np.einsum("tr,rhd->thd", rng.standard_normal((16, 8)), basis)           # rank 8
+    k[2, 7] *= 1000.0                                              # one spiked token
+    kb = O.f32_to_bf16(k)
+    blocks = np.arange(NB, dtype=np.int64)
+    ref = O.build_state_slabs(kb, blocks, NB)
+
+    class C:
+        pass
+    case = C()
+    case.NB, case.n_kv, case.G, case.R, case.MP = NB, n_kv, 4, 1, 16
+    st = _state(case)
+    kt = torch.from_numpy(kb.view(np.int16)).view(torch.bfloat16).cuda()
+    print("[case] degenerate pages", flush=True)
+    rki4_build_blocks(st, 0, kt, torch.from_numpy(blocks))
+    torch.cuda.synchronize()
+    got = _slabs_np(st)
+    assert np.array_equal(got["mu8"], ref["mu8"]) and np.array_equal(got["mus"], ref["mus"])
+    assert np.array_equal(got["tag"], kb[:, 15, :, :8])
+    floor = O.f32_to_bf16(np.float32(1e-8))
+    assert not got["v4"][4].any()                                  # zero gram: zero codes,
+    assert (got["vs"][4] == floor).all()                           # scale at the floor
+
+    def recon(s, b):
+        V = O.unpack_i4(s["v4"][b]).astype(np.float64) * O.bf16_to_f32(s["vs"][b])[..., None]
+        Cm = s["c8"][b].astype(np.float64) * O.bf16_to_f32(s["cs"][b])[..., None]
+        return np.einsum("ktr,krd->ktd", Cm, V)
+    # the constant page centres to ~1-ulp residues (the fp32 mean of 16 equal
+    # values rounds): its reconstruction must stay at that level
+    r0 = recon(got, 0)
+    assert np.abs(r0).max() <= 1e-3 * np.abs(O.bf16_to_f32(kb[0])).max()
+    for b in (1, 2, 3, 5):
+        _, _, dc, _ = O.summary_pre(kb[b:b + 1])
+        dc = dc[0]
+        eg = np.linalg.norm(recon(got, b) - dc) / np.linalg.norm(dc)
+        er = np.linalg.norm(recon(ref, b) - dc) / np.linalg.norm(dc)
+        print(f"[case] block {b}: reconstruction gpu {eg:.4f} oracle {er:.4f}", flush=True)
+        assert np.isfinite(eg) and eg <= er + 0.02, (b, eg, er)
