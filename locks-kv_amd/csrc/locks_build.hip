@@ -67,10 +67,12 @@ __device__ __forceinline__ void pack_page(WaveLds<D>& L, long row, uint8_t* __re
             const int d = 2 * (lane + 64 * k) + e;
 #pragma unroll
             for (int r = 0; r < BD_RNK; ++r) {
-                // compiler barrier: one column's operands live at a time
-                // (hoisting all 16 x 8 basis values costs ~130 VGPRs and
-                // halves the build's occupancy)
-                asm volatile("" ::: "memory");
+                // d = 128: a compiler barrier keeps one column's operands
+                // live at a time (hoisting all 16 x 8 basis values costs ~130
+                // VGPRs and halves the occupancy).  d = 512 runs one wave per
+                // SIMD anyway (its LDS image), so there the hoisting is free
+                // and the barrier would only multiply the LDS reloads.
+                if constexpr (D <= 128) asm volatile("" ::: "memory");
                 float acc = 0.f;
                 const int c = L.col[r];
                 for (int t = 0; t < BD_PG; ++t) acc = __fadd_rn(acc, __fmul_rn(L.dc[t][d], L.U[t][c]));
