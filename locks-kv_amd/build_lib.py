@@ -21,6 +21,7 @@ SOURCES = ["locks_capi.cpp", "locks_score.hip", "locks_select.hip", "locks_decod
            "locks_mla.hip",
            "locks_calib.hip"]
 ARCH = "gfx950"
+EXAMPLES = [("examples/capi_decode.cpp", "capi_decode")]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 COMMON = ["-O3", "-fPIC", "-std=c++17", f"-I{CSRC}", f"-I{os.path.join(ROOT, 'include')}",
@@ -56,6 +57,16 @@ def build(verbose: bool = False) -> str:
     os.replace(tmp, LIB)
     for o in objs:
         os.remove(o)
+    # the C-ABI example (a non-Python host of the library), run by the GPU tests
+    for src, exe in EXAMPLES:
+        out = os.path.join(OUT_DIR, exe)
+        cmd = [HIPCC, "-O2", "-std=c++17", f"-I{os.path.join(ROOT, 'include')}",
+               f"--offload-arch={ARCH}", os.path.join(HERE, src), f"-L{OUT_DIR}", "-llocks_hip",
+               "-Wl,-rpath,$ORIGIN", "-o", out + ".tmp"]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"hipcc failed for {src}:\n{r.stdout}\n{r.stderr}")
+        os.replace(out + ".tmp", out)
     if verbose:
         print(f"[locks] built {LIB}")
     return LIB
