@@ -31,6 +31,44 @@ def test_library_exports_header_symbols():
     assert lib.locks_abi_version() == _lib.ABI_VERSION
 
 
+def _header_params():
+    """name -> list of C parameter types, parsed from include/locks_hip.h."""
+    text = open(os.path.join(ROOT, "include", "locks_hip.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    out = {}
+    for m in re.finditer(r"(?:const char\*|int32_t|int64_t)\s+(locks_\w+)\(([^)]*)\);", text):
+        params = [p.strip() for p in m.group(2).replace("\n", " ").split(",") if p.strip()]
+        out[m.group(1)] = [] if params == ["void"] else params
+    return out
+
+
+def test_ctypes_signatures_match_the_header():
+    """Every ctypes argtype list in locks/_lib.py has the header's parameter
+    count and kind (pointer / int32 / int64 / float / double), and the return
+    type matches: a drifted binding would pass arguments in the wrong slots."""
+    from locks import _lib
+    kinds = {"p": _lib._p, "i32": _lib._i32, "i64": _lib._i64, "f32": _lib._f32, "f64": _lib._f64}
+
+    def kind(decl):
+        if "*" in decl:
+            return "p"
+        t = decl.split()[0] if not decl.startswith("const ") else decl.split()[1]
+        return {"int32_t": "i32", "int64_t": "i64", "float": "f32", "double": "f64"}[t]
+
+    text = open(os.path.join(ROOT, "include", "locks_hip.h")).read()
+    params = _header_params()
+    assert set(params) == set(_lib.SIGNATURES)
+    for name, decls in params.items():
+        res, args = _lib.SIGNATURES[name]
+        assert len(args) == len(decls), f"{name}: {len(args)} ctypes args, header has {len(decls)}"
+        for i, (a, d) in enumerate(zip(args, decls)):
+            assert a is kinds[kind(d)], f"{name} arg {i} ({d}): ctypes {a}"
+        ret = re.search(r"(const char\*|int32_t|int64_t)\s+" + name + r"\(", text).group(1)
+        want = {"int32_t": _lib._i32, "int64_t": _lib._i64}.get(ret)
+        if want is not None:
+            assert res is want, f"{name} returns {ret}"
+
+
 def test_rejects_bad_geometry_without_device():
     from locks import _lib
     lib = _lib.load()
