@@ -38,7 +38,7 @@ def _attend(q, K, V, bt, sl, tab, cnt, r, kh, G, scale):
     return p @ v
 
 
-def _run(budget_pages, steps, check_fresh, full_budget=False):
+def _run(budget_pages, steps, check_fresh, full_budget=False, kv_first=False):
     import torch
     from locks.backend.engine import LocksEngine
     from locks.config import LocksConfig
@@ -49,8 +49,15 @@ def _run(budget_pages, steps, check_fresh, full_budget=False):
     MP = MAXLEN // PAGE
     NB = R * MP + 4
     g = torch.Generator().manual_seed(5)
-    caches = [torch.zeros(NB, 2, PAGE, n_kv, D, dtype=torch.bfloat16, device="cuda")
-              for _ in range(L)]
+    if kv_first:                                 # vLLM 0.11 layout (2, NB, page, n_kv, d)
+        caches = [torch.zeros(2, NB, PAGE, n_kv, D, dtype=torch.bfloat16, device="cuda")
+                  for _ in range(L)]
+    else:
+        caches = [torch.zeros(NB, 2, PAGE, n_kv, D, dtype=torch.bfloat16, device="cuda")
+                  for _ in range(L)]
+
+    def halves(c):
+        return (c[0], c[1]) if kv_first else (c[:, 0], c[:, 1])
     perm = torch.randperm(NB, generator=g)[: R * MP].view(R, MP).to(torch.int32)
     bt = perm.cuda()
     cfg = LocksConfig(budget_pages=budget_pages, sink_pages=1, window_pages=1)
@@ -61,7 +68,10 @@ def _run(budget_pages, steps, check_fresh, full_budget=False):
     def write(r, pos):
         b = int(perm[r, pos // PAGE])
         for c in caches:
-            c[b, :, pos % PAGE] = torch.randn(2, n_kv, D, generator=g).to(torch.bfloat16).cuda()
+            kv = torch.randn(2, n_kv, D, generator=g).to(torch.bfloat16).cuda()
+            Kc, Vc = halves(c)
+            Kc[b, pos % PAGE] = kv[0]
+            Vc[b, pos % PAGE] = kv[1]
 
     lens, qlen = [150], [150]                    # prefill of request 0
     worst = 0.0
@@ -96,13 +106,13 @@ def _run(budget_pages, steps, check_fresh, full_budget=False):
                                   head_dim=D, page=PAGE, max_reqs=R, max_pages=MP,
                                   budget=0.1, budget_pages=budget_pages)
                 fresh._layer_of = {c.data_ptr(): i for i, c in enumerate(caches)}
-                ks = [c[:, 0] for c in caches]
+                ks = [halves(c)[0] for c in caches]
                 settled = sl[:n] - 1
                 rki4_build_bulk(fresh, ks, bt, settled, n, int(settled.max()) // PAGE)
                 derive_page_params(fresh, sl, n)
             for layer in range(L):
                 out, tab, cnt = outs[layer]
-                K, V = caches[layer][:, 0], caches[layer][:, 1]
+                K, V = halves(caches[layer])
                 if check_fresh:
                     _runtime._rki4_select_adapter(q[layer], caches[layer], bt, sl, fresh, n,
                                                   scale, cfg)
@@ -139,3 +149,8 @@ def test_engine_decode_loop_selection_and_output():
 def test_engine_full_budget_equals_dense():
     """Every page selected: the sparse output is dense attention."""
     _run(budget_pages=64, steps=10, check_fresh=False, full_budget=True)
+
+
+def test_engine_kv_first_cache_layout():
+    """The (2, num_blocks, page, n_kv, d) cache layout of vLLM 0.11."""
+    _run(budget_pages=4, steps=12, check_fresh=True, kv_first=True)
