@@ -26,8 +26,9 @@ Two things are restated here (paths relative to the reference package
      mla_score_rki4       tok[h][t] = (q8.mu8)qs mus + cs_t sum_c c8[t][c]
                           (sum_d V4[c][d] q8[h][d]) qs vs_c + q_rope[h].k_rope[t]
                           page score = scale * max_{h, t} tok[h][t]
-   The reference ships no latent rki4 format (SURVEY: "new layout"); the
-   max-union score, the budget rule and the attention are the reference's.
+   The reference ships no latent rki4 format (this layout is new: the
+   reference scores with fp32 factors, mla_select.py:69-108); the max-union
+   score, the budget rule and the attention are the reference's.
 
 Ties: the reference's ``topb_middle`` uses ``torch.topk``, whose order among
 equal scores is unspecified; ``topb_middle`` here breaks ties by the lowest
