@@ -288,3 +288,38 @@ def test_mla_latent_refresh_equals_per_layer_build():
     for layer in range(L):
         mla_build_blocks(b, layer, caches[layer], torch.tensor([fin[2]], dtype=torch.int32))
     _assert_same(_slab_bytes(a), _slab_bytes(b))
+
+
+def test_bulk_replays_in_a_graph():
+    """The bulk producer is capturable too (no host sync): each replay
+    rebuilds every finalized page from the live K, which changes between
+    replays."""
+    import torch
+    from locks.selection import rki4_build_bulk
+    case = _case(26)
+    L = 2
+    d, ks = _layers(case, L, 6)
+    sl = np.array(case.seq_lens)
+    max_fin = int((sl // PAGE).max())
+    a = _state(case.NB, L, case.n_kv, 3, case.MP)
+    rki4_build_bulk(a, ks, d["bt"], d["sl"], 3, max_fin)      # allocates the buffers
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            rki4_build_bulk(a, ks, d["bt"], d["sl"], 3, max_fin)
+    torch.cuda.synchronize()
+    fin = _finalized(case.bt, sl)
+    some = sorted(fin)[:5]
+    for rep in range(3):
+        print(f"[case] bulk graph replay {rep}", flush=True)
+        for blk in some:
+            ks[rep % L][blk, 3, 1, :] -= 0.25
+        g.replay()
+        torch.cuda.synchronize()
+        b = _state(case.NB, L, case.n_kv, 3, case.MP)
+        _per_layer(b, ks, fin)
+        _assert_same(_slab_bytes(a), _slab_bytes(b))
+        assert int(a.refresh_mark.sum().item()) == 0
