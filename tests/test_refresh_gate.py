@@ -92,3 +92,108 @@ def test_mixed_step_counts_only_settled_tokens():
     # row 0 decodes, row 1 prefills a 300-token chunk on top of 100 settled
     p = g.plan([65, 400], _qs(1, 300), 2)
     assert p.kind == "bulk" and p.max_fin == 100 // 16
+
+
+# ---- property test: the gate keeps every finalized page fresh ---------------
+# A model of the cache and the summaries under the producers' semantics
+# (rki4_build_tail / _bulk / _delta, selection/rki4_build.py:264-315):
+#   bulk   rebuilds every finalized page of the batch;
+#   delta  rebuilds the finalized pages whose last key changed since their
+#          build (the content tag is that key's first channels);
+#   tail   rebuilds page max((seq_len - 1) // page - 1, 0) of each given row.
+# Keys of a step's query tokens are written after the prologue.  Invariant
+# after every prologue: each finalized page (p < settled // page) was built
+# after its last key write.
+
+from hypothesis import given, settings, strategies as hst  # noqa: E402
+
+PG = 16
+
+
+class _Model:
+    def __init__(self):
+        self.rows = []              # [row id, seq_len incl. in-flight, query_len]
+        self.next_id = 0
+        self.write_step = {}        # (row id, token) -> step of the last write
+        self.built = {}             # (row id, page) -> step of the last build
+        self.step = 0
+
+    def settled(self, row):
+        return max(row[1] - row[2], 0)
+
+    def page_last_write(self, rid, p):
+        return max(self.write_step.get((rid, p * PG + t), -1) for t in range(PG))
+
+    def run(self, plan):
+        n = len(self.rows)
+        if plan.kind == "skip":
+            return
+        if plan.kind == "tail":
+            for r in plan.rows:
+                rid, sl, _ = self.rows[int(r)]
+                self.built[(rid, max((sl - 1) // PG - 1, 0))] = self.step
+            return
+        for i in range(n):
+            rid = self.rows[i][0]
+            nf = self.settled(self.rows[i]) // PG
+            if plan.kind in ("bulk", "legacy"):
+                nf = min(nf, plan.max_fin) if plan.kind == "bulk" else nf
+            for p in range(nf):
+                key_step = self.write_step.get((rid, p * PG + PG - 1), -1)
+                if plan.kind == "delta" or plan.kind == "legacy":
+                    if self.built.get((rid, p), -2) > key_step:
+                        continue
+                self.built[(rid, p)] = self.step
+
+    def check(self):
+        for rid, sl, ql in self.rows:
+            for p in range(max(sl - ql, 0) // PG):
+                assert self.built.get((rid, p), -2) > self.page_last_write(rid, p), (rid, p, self.step)
+
+    def write(self):
+        for rid, sl, ql in self.rows:
+            for t in range(sl - ql, sl):
+                self.write_step[(rid, t)] = self.step
+
+
+_ACTIONS = hst.lists(hst.tuples(hst.sampled_from(
+    ["decode", "decode", "decode", "arrive", "prefill", "drop", "shuffle", "frozen", "pad"]),
+    hst.integers(1, 70)), min_size=1, max_size=60)
+
+
+@settings(max_examples=150, deadline=None)
+@given(_ACTIONS)
+def test_gate_keeps_finalized_pages_fresh(actions):
+    g = RefreshGate(PG)
+    m = _Model()
+    prev_lens = None
+    for act, k in actions:
+        if act == "arrive" or not m.rows:
+            m.rows.append([m.next_id, k, k])                 # prefill of k tokens
+            m.next_id += 1
+        elif act == "prefill":                               # a row continues a chunked prefill
+            r = m.rows[k % len(m.rows)]
+            r[1], r[2] = r[1] + k, k
+        elif act == "drop" and len(m.rows) > 1:
+            m.rows.pop(k % len(m.rows))
+        elif act == "shuffle":
+            m.rows = m.rows[k % len(m.rows):] + m.rows[:k % len(m.rows)]
+        elif act == "frozen" and prev_lens is not None and len(prev_lens) == len(m.rows):
+            for r, pl in zip(m.rows, prev_lens):             # drain replay: last step's lengths
+                r[1], r[2] = pl, (1 if pl > 0 else 0)
+        elif act == "pad":
+            m.rows.append([m.next_id, 0, 0])                 # padded uniform-decode row
+            m.next_id += 1
+        lens = [r[1] for r in m.rows]
+        qs = np.concatenate([[0], np.cumsum([r[2] for r in m.rows])])
+        plan = g.plan(np.array(lens), qs, len(m.rows))
+        if plan.kind == "bulk":
+            g.built_once = True
+        m.run(plan)
+        m.check()
+        m.write()
+        m.step += 1
+        prev_lens = lens
+        for r in m.rows:                                     # the next step decodes by default
+            if r[1] > 0:
+                r[1], r[2] = r[1] + 1, 1
