@@ -151,7 +151,8 @@ def dense_step(m, dn, out):
                       dn["l"], dn["acc"], n_req=m["R"], G=m["G"], split=dn["split"],
                       pps_min=1, scale=m["scale"])
         decode_merge(dn["m"], dn["l"], dn["acc"], dn["cnt"], out[layer], n_req=m["R"],
-                     n_kv=m["n_kv"], G=m["G"], split=dn["split"], pps_min=1)
+                     n_kv=m["n_kv"], G=m["G"], split=dn["split"], pps_min=1,
+                     pt_cols=dn["tab"].shape[2])
 
 
 def capture(fn):

@@ -28,7 +28,7 @@
 
 #include <stdint.h>
 
-#define LOCKS_ABI_VERSION 3
+#define LOCKS_ABI_VERSION 4
 
 #ifdef __cplusplus
 extern "C" {
@@ -110,7 +110,10 @@ int64_t locks_select_workspace_bytes(int32_t n_req, int32_t n_kv, int32_t max_pa
  *   workspace  >= locks_select_workspace_bytes(...) bytes, zero-filled once
  *              before its first use (every call leaves its histogram part
  *              zero again; unused when max_pages <= 2048); calls that
- *              overlap on one workspace race.
+ *              overlap on one workspace race.  Its layout is derived from
+ *              workspace_bytes (rows it can hold), not from n_req, so pass
+ *              the same workspace_bytes on every call with that workspace
+ *              whatever the batch size.
  *   b_max      host-side upper bound of b_fix (0 = unknown).  Only picks the
  *              route for rows above 8192 pages: when b_max * chunks exceeds
  *              4096 candidates, the 2048-page chunks build a row key
@@ -157,9 +160,12 @@ int32_t locks_decode_splitk(const uint16_t* q, int64_t q_stride_req, int64_t q_s
  *   out (n_req, n_kv*G, 128) bf16 (out_is_f32 = 0) or f32 (out_is_f32 = 1),
  *   strides (out_stride_req, out_stride_head, 1), multiples of 4 elements;
  *   rows with page_cnt 0 get 0.
+ *   pt_cols: the page-table width given to locks_decode_splitk; page_cnt is
+ *   clamped to it exactly as the split kernel clamps it, so both derive the
+ *   same pages per split and active split count.
  */
 int32_t locks_decode_merge(const float* m_part, const float* l_part, const float* acc_part,
-                           const int32_t* page_cnt, int64_t cnt_stride, void* out,
+                           const int32_t* page_cnt, int64_t cnt_stride, int32_t pt_cols, void* out,
                            int64_t out_stride_req, int64_t out_stride_head, int32_t out_is_f32,
                            int32_t n_req, int32_t n_kv, int32_t G, int32_t head_dim,
                            int32_t split, int32_t pps_min, void* stream);

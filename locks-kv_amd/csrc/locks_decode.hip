@@ -389,21 +389,25 @@ __global__ __launch_bounds__(DC_BLK) void decode_split_kernel(
         }
     }
     if constexpr (FUSED) {
-        // The last of the row's active splits to finish merges them all: its
-        // SC1 partial stores are complete (vmcnt) before the arrival count is
-        // bumped, and the merge reads the partials with SC1 loads.  The
-        // merging workgroup resets the counter for the next call.
+        // The last of the row's active splits to finish merges them all.
+        // Every thread releases its partial stores at agent scope before the
+        // workgroup barrier; the arrival count is an acq_rel agent-scope
+        // atomic, and the merging workgroup acquires at agent scope before
+        // it reads the partials (SC1 loads, so no stale L2 line of another
+        // XCD is read either way).  The merging workgroup resets the counter
+        // for the next call.
         __shared__ int last_s;
         __shared__ float lt_s[16];
-        __builtin_amdgcn_s_waitcnt(0x0070);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
         __syncthreads();
         const int n_act = min(cdiv(cnt, pps), split);
         if (tid == 0) {
-            const int old = __hip_atomic_fetch_add(counters + rk, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const int old = __hip_atomic_fetch_add(counters + rk, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
             last_s = (old == n_act - 1);
         }
         __syncthreads();
         if (!last_s) return;
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
         if (tid == 0) __hip_atomic_store(counters + rk, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         merge_row<true>(m_part, l_part, acc_part, rk, r, kh, n_act, G, split, out, o_sr, o_sh,
                         out_f32, reinterpret_cast<float*>(&stA[0][0]),
@@ -413,13 +417,14 @@ __global__ __launch_bounds__(DC_BLK) void decode_split_kernel(
 
 __global__ __launch_bounds__(DC_BLK) void decode_merge_kernel(
     const float* __restrict__ m_part, const float* __restrict__ l_part,
-    const float* __restrict__ acc_part, const int* __restrict__ pcnt, long cnt_sr,
+    const float* __restrict__ acc_part, const int* __restrict__ pcnt, long cnt_sr, int pt_cols,
     void* __restrict__ out, long o_sr, long o_sh, int out_f32, int G, int split, int pps_min)
 {
     const int kh = blockIdx.x, r = blockIdx.y;
     const int n_kv = gridDim.x;
     const long rk = (long)r * n_kv + kh;
-    const int cnt = pcnt[(long)r * cnt_sr + kh];
+    // the same clamp as decode_split_kernel, so both derive the same pps / n_act
+    const int cnt = min(pcnt[(long)r * cnt_sr + kh], pt_cols);
     const int pps = max(cdiv(cnt, split), pps_min);
     const int n_act = cnt > 0 ? min(cdiv(cnt, pps), split) : 0;
     __shared__ float w_s[MAX_SPLIT * 16], l_s[MAX_SPLIT * 16];
@@ -509,10 +514,11 @@ extern "C" int32_t locks_decode_fused(
 
 extern "C" int32_t locks_decode_merge(
     const float* m_part, const float* l_part, const float* acc_part,
-    const int32_t* page_cnt, int64_t cnt_stride, void* out, int64_t out_stride_req,
+    const int32_t* page_cnt, int64_t cnt_stride, int32_t pt_cols, void* out, int64_t out_stride_req,
     int64_t out_stride_head, int32_t out_is_f32, int32_t n_req, int32_t n_kv, int32_t G,
     int32_t head_dim, int32_t split, int32_t pps_min, void* stream)
 {
+    LOCKS_REQUIRE(pt_cols >= 1, "locks_decode_merge: pt_cols %d < 1", pt_cols);
     LOCKS_REQUIRE(head_dim == DC_D, "locks_decode_merge: head_dim %d unsupported (this build: 128)", head_dim);
     LOCKS_REQUIRE(G >= 1 && G <= 16, "locks_decode_merge: G=%d outside [1, 16]", G);
     LOCKS_REQUIRE(split >= 1 && split <= MAX_SPLIT, "locks_decode_merge: split %d outside [1, %d]", split, MAX_SPLIT);
@@ -522,7 +528,7 @@ extern "C" int32_t locks_decode_merge(
                   "locks_decode_merge: out strides must be multiples of 4 elements");
     if (n_req == 0) return 0;
     hipLaunchKernelGGL(decode_merge_kernel, dim3(n_kv, n_req), dim3(DC_BLK), 0, (hipStream_t)stream,
-                       m_part, l_part, acc_part, page_cnt, (long)cnt_stride, out, (long)out_stride_req,
+                       m_part, l_part, acc_part, page_cnt, (long)cnt_stride, pt_cols, out, (long)out_stride_req,
                        (long)out_stride_head, out_is_f32, G, split, pps_min);
     return check_launch("decode_merge_kernel");
 }

@@ -1010,15 +1010,18 @@ __global__ void derive_kernel(const int* __restrict__ seq_lens, int n_req, int p
 
 using namespace locks;
 
+// Workspace bytes of one (request, kv head) row: candidate keys + pages per
+// chunk slot, spill keys + pages per page, per-chunk counts, and the
+// large-budget route's 4096-bin row histogram.
+static long sel_row_bytes(long Z1, long max_pages) {
+    return Z1 * SEL_CH * 8 + max_pages * 8 + Z1 * 4 + 4096 * 4;
+}
+
 extern "C" int64_t locks_select_workspace_bytes(int32_t n_req, int32_t n_kv, int32_t max_pages) {
     if (n_req < 0 || n_kv < 1 || max_pages < 1) return -1;
     const long Z1 = cdiv(max_pages, SEL_CH);
     const long rows = (long)n_req * n_kv;
-    const long cand = rows * Z1 * SEL_CH;               // key + page per slot
-    const long spill = rows * (long)max_pages;           // key + page per page
-    const long counts = rows * Z1;
-    const long hists = rows * 4096;                      // large-budget row histograms
-    long bytes = cand * 8 + spill * 8 + counts * 4 + hists * 4;
+    const long bytes = rows * sel_row_bytes(Z1, max_pages);
     return (bytes + 255) / 256 * 256;
 }
 
@@ -1046,14 +1049,18 @@ extern "C" int32_t locks_select_nrm_topb(
                   (long long)workspace_bytes, (long long)need);
     if (n_req == 0) return 0;
     hipStream_t st = (hipStream_t)stream;
-    const long rows = (long)n_req * n_kv;
+    // Every region is laid out for the workspace's row capacity, not for this
+    // call's n_req: the band route's row histograms must stay zero between
+    // calls (the finisher clears them), so they may never move onto bytes a
+    // call with another batch size used for candidates.
+    const long cap = workspace ? (long)(workspace_bytes / sel_row_bytes(Z1, max_pages)) : 0;
     uint8_t* ws = (uint8_t*)workspace;
     uint32_t* cand_key = (uint32_t*)ws;
-    int* cand_page = (int*)(ws + rows * Z1 * SEL_CH * 4);
-    uint32_t* spill_key = (uint32_t*)(ws + rows * Z1 * SEL_CH * 8);
-    int* spill_page = (int*)(ws + rows * Z1 * SEL_CH * 8 + rows * (long)max_pages * 4);
-    int* cand_cnt = (int*)(ws + rows * Z1 * SEL_CH * 8 + rows * (long)max_pages * 8);
-    int* ghist = cand_cnt + rows * Z1;
+    int* cand_page = (int*)(ws + cap * Z1 * SEL_CH * 4);
+    uint32_t* spill_key = (uint32_t*)(ws + cap * Z1 * SEL_CH * 8);
+    int* spill_page = (int*)(ws + cap * Z1 * SEL_CH * 8 + cap * (long)max_pages * 4);
+    int* cand_cnt = (int*)(ws + cap * Z1 * SEL_CH * 8 + cap * (long)max_pages * 8);
+    int* ghist = cand_cnt + cap * Z1;
     if (max_pages <= ROW_MAXP && max_pages % 4 == 0 && max_pages > SEL_CH) {
 #define ROW_LAUNCH(EV)                                                                     \
         hipLaunchKernelGGL((sel_row_kernel<EV>), dim3(n_kv, n_req), dim3(ROW_BLK), 0, st, score_h, \

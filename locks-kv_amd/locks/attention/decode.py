@@ -105,14 +105,22 @@ def decode_splitk(q, k, v, block_table, seq_lens, page_table, page_cnt, m_part, 
         _lib.stream_ptr(q.device)), "decode_splitk")
 
 
+def _check_out(out) -> None:
+    """The kernels write 4-element runs along the last dim of ``out``."""
+    if out.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"out must be bf16 or fp32, got {out.dtype}")
+    if out.dim() != 3 or out.stride(-1) != 1:
+        raise TypeError(f"out must be (n_req, heads, d) with a contiguous last dim, got shape "
+                        f"{tuple(out.shape)} strides {tuple(out.stride())}")
+
+
 def decode_fused(q, k, v, block_table, seq_lens, page_table, page_cnt, m_part, l_part,
                  acc_part, counters, out, *, n_req: int, G: int, split: int, pps_min: int,
                  scale: float) -> None:
     """Split kernel whose last-arriving split of each (request, kv head) row
     merges the row into ``out`` (one launch).  ``counters`` (R, n_kv) i32
     must be zero on the first call; each call leaves it zero."""
-    if out.dtype not in (torch.bfloat16, torch.float32):
-        raise TypeError(f"out must be bf16 or fp32, got {out.dtype}")
+    _check_out(out)
     NB, page, n_kv, d = k.shape
     lib = _lib.load()
     _lib.check(lib.locks_decode_fused(
@@ -129,13 +137,14 @@ def decode_fused(q, k, v, block_table, seq_lens, page_table, page_cnt, m_part, l
 
 
 def decode_merge(m_part, l_part, acc_part, page_cnt, out, *, n_req: int, n_kv: int, G: int,
-                 split: int, pps_min: int) -> None:
-    if out.dtype not in (torch.bfloat16, torch.float32):
-        raise TypeError(f"out must be bf16 or fp32, got {out.dtype}")
+                 split: int, pps_min: int, pt_cols: int) -> None:
+    """LSE merge of the split partials into ``out``; ``pt_cols`` is the page
+    table width the split kernel was given (page_cnt is clamped to it)."""
+    _check_out(out)
     lib = _lib.load()
     _lib.check(lib.locks_decode_merge(
         _lib.ptr(m_part), _lib.ptr(l_part), _lib.ptr(acc_part), _lib.ptr(page_cnt),
-        page_cnt.stride(0), _lib.ptr(out), out.stride(0), out.stride(1),
+        page_cnt.stride(0), int(pt_cols), _lib.ptr(out), out.stride(0), out.stride(1),
         1 if out.dtype == torch.float32 else 0, int(n_req), int(n_kv), int(G),
         int(acc_part.shape[-1]), int(split), int(pps_min), _lib.stream_ptr(out.device)),
         "decode_merge")
@@ -164,4 +173,5 @@ def sparse_paged_decode_batched(q, kv_cache, block_table, seq_lens, st, out,
                   st.l_part, st.acc_part, n_req=n_req, G=st.G, split=st.split,
                   pps_min=pps, scale=scale)
     decode_merge(st.m_part, st.l_part, st.acc_part, st.page_cnt, out, n_req=n_req,
-                 n_kv=st.n_kv, G=st.G, split=st.split, pps_min=pps)
+                 n_kv=st.n_kv, G=st.G, split=st.split, pps_min=pps,
+                 pt_cols=st.page_table.shape[2])

@@ -83,3 +83,44 @@ def load_slabs(st, layer, slabs):
     for name, attr in (("vs", "pp_vs"), ("cs", "pp_cs"), ("mus", "pp_mus")):
         getattr(st, attr)[layer].copy_(
             torch.from_numpy(slabs[name].view(np.int16)).view(torch.bfloat16))
+
+
+def random_slabs(rng: np.random.Generator, NB: int, n_kv: int, d: int = 128, page: int = 16,
+                 rank: int = 8) -> dict:
+    """Seeded rki4 slab bytes for scorer-only cases at full row lengths.
+
+    The scorer is a function of the slab bytes alone, so long rows (128K,
+    1M) are covered without running the O(pages) eigen build: every int4
+    nibble and int8 code value is drawn uniformly over its full range, and
+    the bf16 scales over the magnitudes a build of N(0, 1) keys with x8
+    outlier channels produces (vs ~ |V|max/7, cs ~ |C|max/127, mus ~
+    |mu|max/127)."""
+    bf = lambda lo, hi, shape: O.f32_to_bf16(rng.uniform(lo, hi, shape).astype(np.float32))
+    return dict(
+        v4=rng.integers(0, 256, (NB, n_kv, rank, d // 2), dtype=np.uint8),
+        vs=bf(0.005, 0.06, (NB, n_kv, rank)),
+        c8=rng.integers(-127, 128, (NB, n_kv, page, rank), dtype=np.int8),
+        cs=bf(0.01, 0.3, (NB, n_kv, page)),
+        mu8=rng.integers(-127, 128, (NB, n_kv, d), dtype=np.int8),
+        mus=bf(0.005, 0.08, (NB, n_kv)),
+    )
+
+
+def score_oracle_chunked(q, slabs, bt, nsh, n_kv, G, scale, MP, chunk=8192, dtype=None):
+    """O.score_rki4_twin (or, with dtype, O.score_rki4_intpath) over page
+    slices of at most `chunk` pages: a page's score depends on that page
+    alone, so the slices concatenate to the full row's result."""
+    R = q.shape[0]
+    out = np.zeros((R, n_kv, G, MP), np.float32)
+    for r in range(R):
+        P = int(nsh[r])
+        for lo in range(0, max(P, 0), chunk):
+            hi = min(lo + chunk, P)
+            sub_bt = np.ascontiguousarray(bt[r:r + 1, lo:hi])
+            args = (q[r:r + 1], slabs, sub_bt, np.array([hi - lo]), n_kv, G, scale, hi - lo)
+            if dtype is None:
+                s = O.score_rki4_twin(*args)
+            else:
+                s = O.score_rki4_intpath(*args, dtype=dtype)
+            out[r, :, :, lo:hi] = s[0]
+    return out

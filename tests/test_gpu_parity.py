@@ -219,6 +219,39 @@ def test_select_matches_oracle(combine, seq_lens, n_kv, G, bp):
     assert np.array_equal(gtab, tab2) and np.array_equal(gcnt, cnt2)
 
 
+@pytest.mark.parametrize("combine", ["max", "nrm"])
+def test_select_band_route_batch_size_changes(combine):
+    """One state on the histogram (band) route called with n_req = 4, then 1,
+    then 4: the row histograms must be zero on entry to every call whatever
+    the previous call's batch size (the workspace layout is fixed by its
+    capacity, not by n_req).  Every call is checked against the oracle."""
+    import torch
+    from locks.selection import derive_page_params, rki4_select_only
+    seq_all = [400000, 300000, 350000, 380000]
+    n_kv, G, bp = 2, 4, 5000
+    MP = max((s + 15) // 16 for s in seq_all)
+    case = make_case(5, n_kv, G, seq_all, MP=MP, kv=False)
+    st = _state(case, budget_pages=bp, combine=combine)
+    for it, R in enumerate((4, 1, 4, 1)):
+        seq = seq_all[:R] if it < 2 else seq_all[::-1][:R]
+        say("band route", combine, "call", it, "n_req", R, seq)
+        sl = torch.tensor(seq, dtype=torch.int32, device="cuda")
+        derive_page_params(st, sl, R)
+        sh, npg, nsh, b = _random_select_inputs(40 + it, n_kv, G, seq, MP, st)
+        st.page_table.fill_(7)
+        rki4_select_only(st, R)
+        torch.cuda.synchronize()
+        gtab = st.page_table[:R].cpu().numpy()
+        gcnt = st.page_cnt[:R].cpu().numpy()
+        gsc = st.score[:R].cpu().numpy()
+        tab2, cnt2 = O.topb_select(gsc, npg, nsh, b, st.sink_pages, MP)
+        assert np.array_equal(gtab, tab2) and np.array_equal(gcnt, cnt2), f"call {it}"
+        if combine == "max":
+            comb = O.combine_max(sh[:R], nsh)
+            tab, cnt = O.topb_select(comb, npg, nsh, b, st.sink_pages, MP)
+            assert np.array_equal(gtab, tab) and np.array_equal(gcnt, cnt)
+
+
 @pytest.mark.parametrize("ties", ["all_equal", "bands", "underflow"])
 @pytest.mark.parametrize("ctx,bp", [(16384, 126), (131072, 126), (1 << 19, 126), (1 << 19, 3000)])
 def test_select_tie_batteries(ties, ctx, bp):
@@ -284,7 +317,8 @@ def test_decode_matches_oracle(n_kv, G, seq_lens, split):
                       st.l_part, st.acc_part, n_req=case.R, G=G, split=st.split,
                       pps_min=pps, scale=case.scale)
         decode_merge(st.m_part, st.l_part, st.acc_part, st.page_cnt, out, n_req=case.R,
-                     n_kv=n_kv, G=G, split=st.split, pps_min=pps)
+                     n_kv=n_kv, G=G, split=st.split, pps_min=pps,
+                     pt_cols=st.page_table.shape[2])
         torch.cuda.synchronize()
         _decode_check(case, st, d, out, tab, cnt)
 
@@ -320,7 +354,8 @@ def test_fused_decode_equals_split_and_merge(n_kv, G, seq_lens, split):
                       st.l_part, st.acc_part, n_req=case.R, G=G, split=st.split,
                       pps_min=pps, scale=case.scale)
         decode_merge(st.m_part, st.l_part, st.acc_part, st.page_cnt, ref, n_req=case.R,
-                     n_kv=n_kv, G=G, split=st.split, pps_min=pps)
+                     n_kv=n_kv, G=G, split=st.split, pps_min=pps,
+                     pt_cols=st.page_table.shape[2])
         decode_fused(d["q"], k, v, d["bt"], d["sl"], st.page_table, st.page_cnt, st.m_part,
                      st.l_part, st.acc_part, st.dec_counters, out, n_req=case.R, G=G,
                      split=st.split, pps_min=pps, scale=case.scale)
@@ -355,7 +390,8 @@ def test_dense_equality_and_split_invariance():
                       st.l_part, st.acc_part, n_req=1, G=G, split=split, pps_min=1,
                       scale=case.scale)
         decode_merge(st.m_part, st.l_part, st.acc_part, st.page_cnt, out, n_req=1,
-                     n_kv=n_kv, G=G, split=split, pps_min=1)
+                     n_kv=n_kv, G=G, split=split, pps_min=1,
+                     pt_cols=st.page_table.shape[2])
         torch.cuda.synchronize()
         outs.append(out.cpu().numpy())
     # dense reference through torch SDPA in float64 (independent of the oracle)
