@@ -98,7 +98,7 @@ def test_score_forced_chunks_16k(zsplit, chunk):
     _run(21, 8, 4, [16384], zsplit=zsplit, expect_chunk=chunk)
 
 
-@pytest.mark.parametrize("zsplit,chunk", [(16, 64), (2, 512)])
+@pytest.mark.parametrize("zsplit,chunk", [(4, 64), (1, 256)])
 def test_score_forced_chunks_g16(zsplit, chunk):
     """GLM-shaped group (G = 16: one page per token-stage MFMA) over several
     units per wave, with a ragged last tile (4000 tokens -> 249 pages)."""
