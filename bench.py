@@ -127,32 +127,35 @@ def sparse_step(m, out):
                                  m["scale"], None)
 
 
-def make_dense(m, split=512):
+def dense_split(m, split=0):
+    """Dense comparator split count: about two workgroups per CU over the
+    (request, kv head) rows (the dense kernel holds one per CU: 128 KB of
+    page stages)."""
+    if split:
+        return int(split)
+    rows = m["R"] * m["n_kv"]
+    return max(1, min(512, -(-512 // rows)))
+
+
+def make_dense(m, split=0):
     import torch
-    R, n_kv, MP, G = m["R"], m["n_kv"], m["MP"], m["G"]
-    tab = torch.full((R, n_kv, MP), -1, dtype=torch.int32, device="cuda")
-    cnt = torch.zeros(R, n_kv, dtype=torch.int32, device="cuda")
-    for r, s in enumerate(m["sl"].tolist()):
-        n = (s + PAGE - 1) // PAGE
-        tab[r, :, :n] = torch.arange(n, dtype=torch.int32, device="cuda")
-        cnt[r, :] = n
+    R, n_kv, G = m["R"], m["n_kv"], m["G"]
+    split = dense_split(m, split)
     mp = torch.empty(R, n_kv, split, G, device="cuda")
     lp = torch.empty_like(mp)
     ap = torch.empty(R, n_kv, split, G, D, device="cuda")
-    return dict(tab=tab, cnt=cnt, m=mp, l=lp, acc=ap, split=split)
+    return dict(m=mp, l=lp, acc=ap, split=split)
 
 
 def dense_step(m, dn, out):
-    from locks.attention import decode_merge, decode_splitk
+    """Dense full-KV decode of every layer: every page of every row, through
+    the dense kernel (block table only, four page stages per wave)."""
+    from locks.attention import decode_dense
     from locks.attention.decode import _split_kv
     for layer in range(m["L"]):
         k, v = _split_kv(m["kv"][layer])
-        decode_splitk(m["q"][layer], k, v, m["bt"], m["sl"], dn["tab"], dn["cnt"], dn["m"],
-                      dn["l"], dn["acc"], n_req=m["R"], G=m["G"], split=dn["split"],
-                      pps_min=1, scale=m["scale"])
-        decode_merge(dn["m"], dn["l"], dn["acc"], dn["cnt"], out[layer], n_req=m["R"],
-                     n_kv=m["n_kv"], G=m["G"], split=dn["split"], pps_min=1,
-                     pt_cols=dn["tab"].shape[2])
+        decode_dense(m["q"][layer], k, v, m["bt"], m["sl"], dn["m"], dn["l"], dn["acc"],
+                     out[layer], n_req=m["R"], G=m["G"], split=dn["split"], scale=m["scale"])
 
 
 def capture(fn):
@@ -271,53 +274,93 @@ def stream_read_us(nbytes, layers, reps=3):
     return us
 
 
-def cpu_baseline(m, sample_pages=4096):
-    """Oracle (numpy) timed on the host on a bounded sample: one layer,
-    `sample_pages` selectable pages of every kv head; scaled to ms/step."""
-    import numpy as np
+def host_cores():
+    """Host threads this process may use: its CPU affinity, capped by
+    OMP_NUM_THREADS (the GPU box's per-GPU CPU share)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    omp = os.environ.get("OMP_NUM_THREADS")
+    if omp and omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return max(1, n)
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(a, runs=10, warmup=2):
+    """BASELINE configs[0] (one GQA layer, 32 q / 8 kv heads, d 128, 16K
+    context, bs=1, b = 126 + sink + window pages) through the torch CPU
+    restatement of the reference's CPU path (oracle/torch_ref.py: twin
+    scorer, nrm combine, torch.topk exact top-b, fp32 gather attention), at
+    full size, on the host cores: median of `runs` timed runs after `warmup`
+    untimed ones, per stage.  The same config's sparse step is timed on the
+    GPU (HIP graph) for the ratio."""
+    import statistics
+
     import torch
 
-    from oracle import locks_oracle as O
-    st, n_kv, G = m["st"], m["n_kv"], m["G"]
-    P = min(sample_pages, int(m["sl"][0].item()) // PAGE - 1)
-    bt = m["bt"][:1, :P + 1].cpu().numpy()
-    blocks = np.unique(bt[0])
-    to_np = lambda t: t.cpu().numpy()
-    slabs = {}
-    for name, attr, bf in (("v4", "pp_v4", 0), ("vs", "pp_vs", 1), ("c8", "pp_c8", 0),
-                           ("cs", "pp_cs", 1), ("mu8", "pp_mu8", 0), ("mus", "pp_mus", 1)):
-        t = getattr(st, attr)[0]
-        a = to_np(t.view(torch.int16) if bf else t)
-        slabs[name] = a.view(np.uint16) if bf else a
-    kv = m["kv"][0]
-    k = to_np(kv[:, 0].view(torch.int16)).view(np.uint16)
-    v = to_np(kv[:, 1].view(torch.int16)).view(np.uint16)
-    q = to_np(m["q"][0][:1].view(torch.int16)).view(np.uint16)
-    sl = [(P + 1) * PAGE]
-    t0 = time.perf_counter()
-    npg, nsh, b = O.derive_page_params(sl, PAGE, 1, 1, st.budget_abs, st.budget)
-    sh = O.score_rki4_twin(q, slabs, bt, nsh, n_kv, G, m["scale"], P + 1)
-    t1 = time.perf_counter()
-    comb = O.combine_nrm(sh, nsh)
-    tab, cnt = O.topb_select(comb, npg, nsh, b, 1, P + 1)
-    t2 = time.perf_counter()
-    O.decode_attention(q, k, v, bt, sl, tab, cnt, G, m["scale"])
-    t3 = time.perf_counter()
-    full_P = (m["sl"][0].item() + PAGE - 1) // PAGE - 1
-    f = full_P / P
-    per_layer = (t1 - t0) * f + (t2 - t1) * f + (t3 - t2)
+    from oracle import torch_ref as T
+    wl = dict(layers=1, n_kv=8, G=4, seq_lens=[16384])
+    m = make_model(wl, a.budget_pages, seed=0)
+    st = m["st"]
+    out = [torch.empty(1, 32, D, dtype=torch.bfloat16, device="cuda")]
+    g = capture(lambda: sparse_step(m, out))
+    gpu_ms = time_graph(g, 200, 20)
+    cpu = lambda t: t.detach().cpu()
+    slabs = {k: cpu(getattr(st, "pp_" + k)[0]) for k in ("v4", "vs", "c8", "cs", "mu8", "mus")}
+    kv = cpu(m["kv"][0])
+    k, v = kv[:, 0].contiguous(), kv[:, 1].contiguous()
+    q, bt, sl = cpu(m["q"][0]), cpu(m["bt"]), [int(x) for x in m["sl"].tolist()]
+    npg = torch.tensor([(x + PAGE - 1) // PAGE for x in sl], dtype=torch.int32)
+    nsh = npg - st.window_pages
+    b = torch.clamp(torch.clamp(nsh - st.sink_pages, min=1), max=st.budget_abs)
+    threads = host_cores()
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    stages = {"score": [], "select": [], "decode": []}
     try:
-        from threadpoolctl import threadpool_info
-        cores = max([i.get("num_threads", 1) for i in threadpool_info()] + [1])
-    except Exception:
-        cores = 1
-    return dict(value=round(per_layer * m["L"] * 1e3, 3), unit="ms/step", cores=cores,
-                kind="port",
-                sample=(f"numpy oracle, layer 0, {P} of {full_P} selectable pages x {n_kv} kv "
-                        f"heads (score+select scaled x{f:.1f}), decode over the selected "
-                        f"pages, x{m['L']} layers"),
-                stages_s=dict(score=round(t1 - t0, 3), select=round(t2 - t1, 3),
-                              decode=round(t3 - t2, 3)))
+        for it in range(warmup + runs):
+            t0 = time.perf_counter()
+            sh = T.score_rki4(q, slabs, bt, nsh, 8, 4, m["scale"], m["MP"])
+            t1 = time.perf_counter()
+            comb = T.combine_nrm(sh, nsh)
+            tab, cnt = T.topb_select(comb, npg, nsh, b, st.sink_pages, m["MP"])
+            t2 = time.perf_counter()
+            T.decode_attention(q, k, v, bt, sl, tab, cnt, 4, m["scale"])
+            t3 = time.perf_counter()
+            if it >= warmup:
+                stages["score"].append(t1 - t0)
+                stages["select"].append(t2 - t1)
+                stages["decode"].append(t3 - t2)
+    finally:
+        torch.set_num_threads(prev)
+    # the CPU path's selection must equal the GPU's on this config up to the
+    # documented fp32 near-ties; report how many kept pages differ
+    gtab = st.page_table.cpu()
+    diff = sum(len(set(gtab[0, h, :int(st.page_cnt[0, h])].tolist())
+                   ^ set(tab[0, h, :int(cnt[0, h])].tolist())) for h in range(8))
+    tot = [sum(x) for x in zip(stages["score"], stages["select"], stages["decode"])]
+    med = lambda xs: round(statistics.median(xs) * 1e3, 3)
+    cpu_ms = med(tot)
+    del g, m, out
+    torch.cuda.empty_cache()
+    return dict(value=cpu_ms, unit="ms/step", cores=threads, kind="port",
+                sample=("BASELINE configs[0] at full size: one layer, 8 kv x 4 q heads, 16K "
+                        "tokens, 1023 scored pages, b=126+2; torch CPU restatement of the "
+                        f"reference CPU path; median of {runs} runs after {warmup} warm-ups"),
+                cpu_model=cpu_model(), torch_threads=threads,
+                stages_ms={k_: med(v_) for k_, v_ in stages.items()},
+                gpu_ms_same_config=round(gpu_ms, 4),
+                cpu_over_gpu=round(cpu_ms / gpu_ms, 1),
+                selection_pages_differing=int(diff))
 
 
 # --------------------------------------------------------------------------- #
@@ -617,6 +660,10 @@ def main():
     ap.add_argument("--summaries", default="build", choices=["build", "copy"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-dense", action="store_true")
+    ap.add_argument("--no-1m", action="store_true",
+                    help="default workload only: skip the GLM-4-9B 1M north-star point")
+    ap.add_argument("--dense-split", type=int, default=0,
+                    help="dense comparator split count (0: about two workgroups per CU)")
     ap.add_argument("--zsplit", type=int, default=0, help="scorer chunks per (req, kv head)")
     ap.add_argument("--pps-min", type=int, default=0, help="override the decode pps_min table")
     ap.add_argument("--fused-decode", type=int, default=-1,
@@ -655,18 +702,42 @@ def main():
     if a.ladder:
         run_ladder(a, wl)
         return
+    res = measure_gqa(a, wl, a.workload, quickstart=(a.workload == "llama8b-128k"))
+    if res is None:
+        return
+    line, ms = res
+    if a.workload == "llama8b-128k" and not a.no_1m:
+        # the north-star target point (1M, bs=1, b=2048)
+        # in the same JSON line: sparse and dense steps, scorer roofline
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        g1m, _ = measure_gqa(a, WORKLOADS["glm9b-1m"], "glm9b-1m", summaries="copy",
+                             quickstart=False)
+        keep = ("ms_per_step", "tokens_per_s", "achieved_GBps", "step_algorithmic_bytes",
+                "dense_ms_per_step", "dense_achieved_GBps", "dense_ideal_ms_per_step",
+                "speedup_vs_dense", "speedup_vs_ideal_dense", "roofline", "config")
+        line["glm9b_1m"] = {k: g1m[k] for k in keep if k in g1m}
+    line["cpu_baseline"] = None if a.no_cpu else cpu_baseline(a)
+    print(json.dumps(line), flush=True)
+
+
+def measure_gqa(a, wl, workload, summaries=None, quickstart=False):
+    """One GQA workload: the captured sparse step (value), the dense
+    comparator, the scorer roofline and, for the quickstart, the README
+    budget_pages=128 point.  Returns (line, ms) or None (special modes)."""
+    import torch
     t0 = time.perf_counter()
-    m = make_model(wl, a.budget_pages, summaries=a.summaries, zsplit=a.zsplit or None)
-    log(f"model ready in {time.perf_counter() - t0:.1f}s (summary build {m['build_s']:.1f}s)")
+    m = make_model(wl, a.budget_pages, summaries=summaries or a.summaries, zsplit=a.zsplit or None)
+    log(f"{workload}: model ready in {time.perf_counter() - t0:.1f}s (summary build {m['build_s']:.1f}s)")
     if a.refresh:
         run_refresh(a, m)
-        return
+        return None
     if a.profile_scorer:
         from locks.selection import derive_page_params
         derive_page_params(m["st"], m["sl"], m["R"])
         us = scorer_roofline(m, reps=a.profile_scorer)
         log(f"scorer avg {us:.2f} us/launch")
-        return
+        return None
     out = [torch.empty(m["R"], m["n_kv"] * m["G"], D, dtype=torch.bfloat16, device="cuda")
            for _ in range(m["L"])]
     # eager vs graph consistency (graph replays must reproduce the eager step)
@@ -683,34 +754,50 @@ def main():
     ms = time_graph(g_sparse, a.steps, a.warmup)
     by = step_bytes(m)
     sparse_bytes = by["score"] + by["select"] + by["decode"]
-    log(f"sparse step {ms:.3f} ms")
+    log(f"{workload}: sparse step {ms:.3f} ms")
+    attended = int(m["st"].page_cnt[0, 0].item())
+    del g_sparse
+    res = {}
+    if quickstart and a.budget_pages != 128:
+        # README quickstart budget (budget_pages=128: 130 attended pages)
+        st = m["st"]
+        keep_b = st.budget_abs
+        st.budget_abs = 128
+        gq = capture(lambda: sparse_step(m, out))
+        ms128 = time_graph(gq, a.steps, a.warmup)
+        res["budget_pages_128"] = dict(ms_per_step=round(ms128, 4),
+                                       attended_pages_per_kv_head=int(st.page_cnt[0, 0].item()))
+        log(f"{workload}: budget_pages=128 step {ms128:.3f} ms")
+        st.budget_abs = keep_b
+        del gq
+        sparse_step(m, out)                  # restore the headline budget's page tables
+        torch.cuda.synchronize()
     score_us = scorer_roofline(m)
     score_gbps = by["score_per_launch"] / (score_us * 1e-6) / 1e9
     stream_us = stream_read_us(by["score_per_launch"], m["L"])
-    res = {}
     if not a.no_dense:
-        dn = make_dense(m)
+        dn = make_dense(m, a.dense_split)
         outd = [torch.empty_like(o) for o in out]
         g_dense = capture(lambda: dense_step(m, dn, outd))
         ms_dense = time_graph(g_dense, max(3, a.steps // 5), 2)
-        res = dict(dense_ms_per_step=round(ms_dense, 4),
+        ideal = by["dense"] / (HBM_PEAK_GBPS * 1e9) * 1e3
+        res.update(dense_ms_per_step=round(ms_dense, 4),
                    dense_achieved_GBps=round(by["dense"] / (ms_dense * 1e-3) / 1e9, 1),
-                   speedup_vs_dense=round(ms_dense / ms, 3))
-        log(f"dense step {ms_dense:.3f} ms")
-    cpu = None
-    if not a.no_cpu:
-        cpu = cpu_baseline(m)
-        log(f"cpu baseline {cpu}")
+                   dense_split=dn["split"],
+                   dense_ideal_ms_per_step=round(ideal, 4),
+                   speedup_vs_dense=round(ms_dense / ms, 3),
+                   speedup_vs_ideal_dense=round(ideal / ms, 3))
+        log(f"{workload}: dense step {ms_dense:.3f} ms (split {dn['split']})")
+        del g_dense, dn, outd
     line = {
         "metric": "decode ms/step + achieved HBM GB/s, bs=1 @128K/1M ctx, b=2048",
         "value": round(ms, 4), "unit": "ms/step", "n_gpus": 1, "steps": a.steps,
         "warmup": a.warmup, "ms_per_step": round(ms, 4), "higher_is_better": False,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
-        "config": {"workload": a.workload, "layers": m["L"], "n_kv": m["n_kv"], "G": m["G"],
+        "config": {"workload": workload, "layers": m["L"], "n_kv": m["n_kv"], "G": m["G"],
                    "seq_lens": wl["seq_lens"], "page": PAGE, "head_dim": D,
-                   "budget_pages": a.budget_pages, "attended_pages_per_kv_head":
-                       int(m["st"].page_cnt[0, 0].item()), "summaries": a.summaries,
-                   "parallelism": "single-gpu"},
+                   "budget_pages": a.budget_pages, "attended_pages_per_kv_head": attended,
+                   "summaries": summaries or a.summaries, "parallelism": "single-gpu"},
         "tokens_per_s": round(m["R"] * 1e3 / ms, 2),
         "achieved_GBps": round(sparse_bytes / (ms * 1e-3) / 1e9, 1),
         "step_algorithmic_bytes": sparse_bytes,
@@ -720,13 +807,14 @@ def main():
                      "frac": round(score_gbps / HBM_PEAK_GBPS, 4),
                      "avg_launch_us": round(score_us, 3),
                      "bytes_per_launch": by["score_per_launch"],
-                     "traffic": scorer_traffic(a.workload),
+                     "traffic": scorer_traffic(workload),
                      "stream_read_same_bytes_us": round(stream_us, 3),
                      "frac_of_stream_read": round(stream_us / score_us, 4)},
-        "cpu_baseline": cpu,
     }
-    print(json.dumps(line), flush=True)
-
+    del m, out
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return line, ms
 
 if __name__ == "__main__":
     main()

@@ -196,6 +196,28 @@ int32_t locks_decode_fused(const uint16_t* q, int64_t q_stride_req, int64_t q_st
                            void* stream);
 
 /*
+ * Dense full-KV decode: attention of each (request, kv head) group over
+ * EVERY page of the row (pages 0 .. ceil(seq_len / page) - 1, no selection),
+ * the dense comparator the sparse step is measured against.  No reference
+ * kernel is replaced: the reference compares against FlashAttention-3 /
+ * FlashInfer decode (README.md:80-90), which are not part of LOCKS.
+ * Two launches: the split kernel in its dense form (page ids implicit, four
+ * page stages per wave) writes the split partials, then one merge workgroup
+ * per query head folds them.  Argument meanings as locks_decode_splitk and
+ * locks_decode_merge; the partial buffers hold (n_req, n_kv, split, G[, 128]).
+ */
+int32_t locks_decode_dense(const uint16_t* q, int64_t q_stride_req, int64_t q_stride_head,
+                           const uint16_t* k_cache, int64_t k_stride_block, int64_t k_stride_tok,
+                           int64_t k_stride_head, const uint16_t* v_cache, int64_t v_stride_block,
+                           int64_t v_stride_tok, int64_t v_stride_head, int32_t num_blocks,
+                           const int32_t* block_table, int64_t bt_stride, int32_t bt_cols,
+                           const int32_t* seq_lens, float* m_part, float* l_part, float* acc_part,
+                           void* out, int64_t out_stride_req, int64_t out_stride_head,
+                           int32_t out_is_f32, int32_t n_req, int32_t n_kv, int32_t G,
+                           int32_t head_dim, int32_t page, int32_t split, float sm_scale,
+                           void* stream);
+
+/*
  * rki4 summary build on the GPU for the listed physical blocks of ONE layer
  * (head_dim 128: GQA K heads; head_dim 512: the MLA latent, n_kv 1).
  * Replaces the reference build chain _write_pre -> _eigh_chunked ->

@@ -38,6 +38,7 @@ constexpr int DC_PAGE_BYTES = 8192;       // K + V of one (page, kv head)
 typedef __attribute__((address_space(3))) void* lds_ptr;
 typedef __attribute__((address_space(3))) const uint8_t* lds_u8_ptr;
 constexpr int MAX_SPLIT = 512;
+constexpr int DENSE_NST = 4;           // page stages per wave of the dense comparator
 
 __device__ __forceinline__ uint32_t bf16_word(const uint4& w, int e) {
     const uint32_t x = (e >> 1) == 0 ? w.x : (e >> 1) == 1 ? w.y : (e >> 1) == 2 ? w.z : w.w;
@@ -177,7 +178,24 @@ __device__ void merge_row(const float* __restrict__ m_part, const float* __restr
 // stages ping-pong so one page is always in flight while the other is
 // consumed.  The 4 wave states are then merged in LDS into the split's
 // partial.
-template <bool FUSED>
+// DENSE: every page of the row in logical order (page count from seq_len,
+// no page table) -- the dense full-KV comparator.  NST: page stages per
+// wave (NST - 1 pages in flight while one is consumed).
+template <int NST>
+__device__ __forceinline__ void wait_vm_pages(int ahead) {
+    // vmcnt(8 * ahead) with lgkmcnt(0); vmcnt is bits [3:0] + [15:14]
+    switch (ahead) {
+        case 0: __builtin_amdgcn_s_waitcnt(0x0070); break;
+        case 1: __builtin_amdgcn_s_waitcnt(0x0078); break;
+        case 2: if constexpr (NST > 2) __builtin_amdgcn_s_waitcnt(0x4070); break;
+        case 3: if constexpr (NST > 3) __builtin_amdgcn_s_waitcnt(0x4078); break;
+        case 4: if constexpr (NST > 4) __builtin_amdgcn_s_waitcnt(0x8070); break;
+        case 5: if constexpr (NST > 5) __builtin_amdgcn_s_waitcnt(0x8078); break;
+        default: if constexpr (NST > 6) __builtin_amdgcn_s_waitcnt(0xC070); break;
+    }
+}
+
+template <bool FUSED, bool DENSE = false, int NST = 2>
 __global__ __launch_bounds__(DC_BLK) void decode_split_kernel(
     const uint16_t* __restrict__ q, long q_sr, long q_sh,
     const uint16_t* __restrict__ kc, long k_sb, long k_st, long k_sh,
@@ -193,12 +211,19 @@ __global__ __launch_bounds__(DC_BLK) void decode_split_kernel(
     const int n_kv = gridDim.y;
     const long rk = (long)r * n_kv + kh;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    static_assert(NST >= 2 && NST <= 7, "page stages per wave");
+    static_assert(!(FUSED && DENSE), "the dense comparator merges in its own launch");
     const int* prow = ptab + (long)r * pt_sr + (long)kh * pt_sh;
     // This wave's first page ids assuming pps == pps_min (the usual sparse
     // case), loaded together with the page count instead of after it.
     const int js = sp * pps_min + wave + DC_WAVES * lane;
-    const int pt_spec = (js < pt_cols) ? prow[js] : 0;
-    const int cnt = min(pcnt[(long)r * cnt_sr + kh], pt_cols);
+    int pt_spec = 0, cnt;
+    if constexpr (DENSE) {
+        cnt = min(cdiv(seq_lens[r], DC_PG), bt_cols);
+    } else {
+        pt_spec = (js < pt_cols) ? prow[js] : 0;
+        cnt = min(pcnt[(long)r * cnt_sr + kh], pt_cols);
+    }
     const int pps = max(cdiv(cnt, split), pps_min);
     const int j0 = sp * pps;
     if constexpr (FUSED) {
@@ -218,9 +243,10 @@ __global__ __launch_bounds__(DC_BLK) void decode_split_kernel(
     const int c16 = lane & 15, kg = lane >> 4;
     const int seq_len = seq_lens[r];
 
-    // two page stages per wave (distinct arrays), later reused for the merge
+    // NST page stages per wave (stage 0 in stA, the others in stB), later
+    // reused for the merge
     __shared__ __attribute__((aligned(16))) uint8_t stA[DC_WAVES][DC_PAGE_BYTES];
-    __shared__ __attribute__((aligned(16))) uint8_t stB[DC_WAVES][DC_PAGE_BYTES];
+    __shared__ __attribute__((aligned(16))) uint8_t stB[(NST - 1) * DC_WAVES][DC_PAGE_BYTES];
     __shared__ float wm[DC_WAVES][16], wl[DC_WAVES][16];
 
     // B operand of QK, k-slot (kg, s) <-> d = 32*s + 8*kg + 0..7
@@ -246,7 +272,8 @@ __global__ __launch_bounds__(DC_BLK) void decode_split_kernel(
         ptv = 0;
         blkv = 0;
         if (jj < j1) {
-            ptv = spec ? pt_spec : prow[jj];
+            if constexpr (DENSE) ptv = jj;
+            else ptv = spec ? pt_spec : prow[jj];
             const int ptc = min(max(ptv, 0), bt_cols - 1);
             blkv = min(max(bt[(long)r * bt_sr + ptc], 0), NB - 1);
         }
@@ -330,6 +357,25 @@ __global__ __launch_bounds__(DC_BLK) void decode_split_kernel(
         fetch_ids(jb, pps == pps_min && jb == j0 + wave);
         __builtin_amdgcn_s_waitcnt(0x0070);   // ids (and q) resident before any DMA
         const int ns = min(kWave, cdiv(j1 - jb, DC_WAVES));   // steps of this batch
+        if constexpr (NST > 2) {
+            // ring of NST stages: step s + NST - 1 is issued before step s is
+            // consumed, so up to NST - 1 pages stream while one is scored
+            auto stage = [&](int i) { return i == 0 ? stA[wave] : stB[(i - 1) * DC_WAVES + wave]; };
+#pragma unroll
+            for (int i = 0; i < NST - 1; ++i)
+                if (i < ns) issue(i, stage(i));
+            int si = 0, ii = NST - 1;
+            for (int s = 0; s < ns; ++s) {
+                if (s + NST - 1 < ns) issue(s + NST - 1, stage(ii));
+                wait_vm_pages<NST>(min(NST - 1, ns - 1 - s));
+                __builtin_amdgcn_wave_barrier();
+                consume(stage(si), __builtin_amdgcn_readlane(ptv, s));
+                __builtin_amdgcn_wave_barrier();
+                si = (si + 1 == NST) ? 0 : si + 1;
+                ii = (ii + 1 == NST) ? 0 : ii + 1;
+            }
+            continue;
+        }
         int pt_cur = 0;
         for (int s = -1; s < ns; ++s) {
             const bool nxt = s + 1 < ns;
@@ -444,6 +490,83 @@ __global__ __launch_bounds__(DC_BLK) void decode_merge_kernel(
               w_s, l_s, lt_s);
 }
 
+// LSE merge of one (request, kv head, query head) row of split partials,
+// one workgroup per head: 8 split streams x 32 float4 columns, so a row of
+// hundreds of splits (the dense comparator) is merged by G workgroups
+// instead of one.  The page count is the dense one (every page of the row).
+constexpr int MH_BLK = 256, MH_STREAMS = MH_BLK / 32;
+__global__ __launch_bounds__(MH_BLK) void decode_merge_heads_kernel(
+    const float* __restrict__ m_part, const float* __restrict__ l_part,
+    const float* __restrict__ acc_part, const int* __restrict__ seq_lens, int bt_cols,
+    void* __restrict__ out, long o_sr, long o_sh, int out_f32, int G, int split, int pps_min)
+{
+    const int g = blockIdx.x, kh = blockIdx.y, r = blockIdx.z;
+    const int n_kv = gridDim.y;
+    const long rk = (long)r * n_kv + kh;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int cnt = min(cdiv(seq_lens[r], DC_PG), bt_cols);
+    const int pps = max(cdiv(cnt, split), pps_min);
+    const int n_act = cnt > 0 ? min(cdiv(cnt, pps), split) : 0;
+    __shared__ float w_s[MAX_SPLIT];
+    __shared__ float red[MH_BLK / kWave];
+    __shared__ float4 part[MH_STREAMS][32];
+    // head max over the splits that hold mass
+    float mm = -INFINITY;
+    for (int s = tid; s < n_act; s += MH_BLK) {
+        const long i = (rk * split + s) * G + g;
+        if (l_part[i] > 0.f) mm = fmaxf(mm, m_part[i]);
+    }
+    mm = wave_max(mm);
+    if (lane == 0) red[wave] = mm;
+    __syncthreads();
+    mm = red[0];
+#pragma unroll
+    for (int w = 1; w < MH_BLK / kWave; ++w) mm = fmaxf(mm, red[w]);
+    __syncthreads();
+    float lt = 0.f;
+    for (int s = tid; s < n_act; s += MH_BLK) {
+        const long i = (rk * split + s) * G + g;
+        const float l = l_part[i];
+        const float w = (l > 0.f) ? __expf(m_part[i] - mm) : 0.f;
+        w_s[s] = w;
+        lt += l * w;
+    }
+    lt = wave_sum(lt);
+    if (lane == 0) red[wave] = lt;
+    __syncthreads();
+    lt = 0.f;
+#pragma unroll
+    for (int w = 0; w < MH_BLK / kWave; ++w) lt += red[w];
+    const int col = tid & 31, strm = tid >> 5;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 4
+    for (int s = strm; s < n_act; s += MH_STREAMS) {
+        const float w = w_s[s];
+        const float4 a = *reinterpret_cast<const float4*>(acc_part + ((rk * split + s) * G + g) * DC_D + col * 4);
+        acc.x += w * a.x; acc.y += w * a.y; acc.z += w * a.z; acc.w += w * a.w;
+    }
+    part[strm][col] = acc;
+    __syncthreads();
+    if (tid < 32) {
+        float4 t = part[0][col];
+#pragma unroll
+        for (int k = 1; k < MH_STREAMS; ++k) {
+            const float4 a = part[k][col];
+            t.x += a.x; t.y += a.y; t.z += a.z; t.w += a.w;
+        }
+        const float inv = (lt > 0.f) ? 1.f / lt : 0.f;
+        const float o[4] = {t.x * inv, t.y * inv, t.z * inv, t.w * inv};
+        const long oi = (long)r * o_sr + (long)(kh * G + g) * o_sh + col * 4;
+        if (out_f32) {
+            *reinterpret_cast<float4*>(reinterpret_cast<float*>(out) + oi) = make_float4(o[0], o[1], o[2], o[3]);
+        } else {
+            uint16_t* ob = reinterpret_cast<uint16_t*>(out) + oi;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) ob[e] = f32_to_bf16(o[e]);
+        }
+    }
+}
+
 }  // namespace locks
 
 using namespace locks;
@@ -544,3 +667,43 @@ extern "C" int32_t locks_decode_merge(
     return check_launch("decode_merge_kernel");
 }
 
+
+extern "C" int32_t locks_decode_dense(
+    const uint16_t* q, int64_t q_stride_req, int64_t q_stride_head,
+    const uint16_t* k_cache, int64_t k_stride_block, int64_t k_stride_tok, int64_t k_stride_head,
+    const uint16_t* v_cache, int64_t v_stride_block, int64_t v_stride_tok, int64_t v_stride_head,
+    int32_t num_blocks, const int32_t* block_table, int64_t bt_stride, int32_t bt_cols,
+    const int32_t* seq_lens, float* m_part, float* l_part, float* acc_part,
+    void* out, int64_t out_stride_req, int64_t out_stride_head, int32_t out_is_f32,
+    int32_t n_req, int32_t n_kv, int32_t G, int32_t head_dim, int32_t page,
+    int32_t split, float sm_scale, void* stream)
+{
+    LOCKS_REQUIRE(head_dim == DC_D, "locks_decode_dense: head_dim %d unsupported (this build: 128)", head_dim);
+    LOCKS_REQUIRE(page == DC_PG, "locks_decode_dense: page %d unsupported (this build: 16)", page);
+    LOCKS_REQUIRE(G >= 1 && G <= 16, "locks_decode_dense: G=%d outside [1, 16]", G);
+    LOCKS_REQUIRE(split >= 1 && split <= MAX_SPLIT, "locks_decode_dense: split %d outside [1, %d]", split, MAX_SPLIT);
+    LOCKS_REQUIRE(num_blocks >= 1 && bt_cols >= 1, "locks_decode_dense: empty geometry");
+    LOCKS_REQUIRE(k_stride_tok % 8 == 0 && v_stride_tok % 8 == 0 && k_stride_block % 8 == 0 &&
+                  v_stride_block % 8 == 0 && k_stride_head % 8 == 0 && v_stride_head % 8 == 0 &&
+                  q_stride_req % 8 == 0 && q_stride_head % 8 == 0,
+                  "locks_decode_dense: q/K/V strides must be multiples of 8 elements (16-byte loads)");
+    LOCKS_REQUIRE(out_stride_req % 4 == 0 && out_stride_head % 4 == 0,
+                  "locks_decode_dense: out strides must be multiples of 4 elements");
+    LOCKS_REQUIRE(q && k_cache && v_cache && block_table && seq_lens && m_part && l_part && acc_part && out,
+                  "locks_decode_dense: null pointer argument");
+    if (n_req == 0) return 0;
+    hipStream_t st = (hipStream_t)stream;
+    hipLaunchKernelGGL((decode_split_kernel<false, true, DENSE_NST>), dim3(split, n_kv, n_req), dim3(DC_BLK),
+                       0, st, q, (long)q_stride_req, (long)q_stride_head, k_cache,
+                       (long)k_stride_block, (long)k_stride_tok, (long)k_stride_head, v_cache,
+                       (long)v_stride_block, (long)v_stride_tok, (long)v_stride_head, num_blocks,
+                       block_table, (long)bt_stride, bt_cols, nullptr, 0L, 0L, 1, nullptr, 0L,
+                       seq_lens, m_part, l_part, acc_part, G, split, 1, sm_scale,
+                       nullptr, nullptr, 0L, 0L, 0);
+    int rc = check_launch("decode_split_kernel<dense>");
+    if (rc) return rc;
+    hipLaunchKernelGGL(decode_merge_heads_kernel, dim3(G, n_kv, n_req), dim3(MH_BLK), 0, st,
+                       m_part, l_part, acc_part, seq_lens, bt_cols, out, (long)out_stride_req,
+                       (long)out_stride_head, out_is_f32, G, split, 1);
+    return check_launch("decode_merge_heads_kernel");
+}

@@ -150,6 +150,25 @@ def decode_merge(m_part, l_part, acc_part, page_cnt, out, *, n_req: int, n_kv: i
         "decode_merge")
 
 
+def decode_dense(q, k, v, block_table, seq_lens, m_part, l_part, acc_part, out, *, n_req: int,
+                 G: int, split: int, scale: float) -> None:
+    """Dense full-KV decode over every page of each row (the comparator of
+    the sparse step): split partials in (R, n_kv, split, G[, d]) buffers,
+    then a per-head merge into ``out``."""
+    _check_out(out)
+    NB, page, n_kv, d = k.shape
+    lib = _lib.load()
+    _lib.check(lib.locks_decode_dense(
+        _lib.ptr(q), q.stride(0), q.stride(1),
+        _lib.ptr(k), k.stride(0), k.stride(1), k.stride(2),
+        _lib.ptr(v), v.stride(0), v.stride(1), v.stride(2), int(NB),
+        _lib.ptr(block_table), block_table.stride(0), int(block_table.shape[1]),
+        _lib.ptr(seq_lens), _lib.ptr(m_part), _lib.ptr(l_part), _lib.ptr(acc_part),
+        _lib.ptr(out), out.stride(0), out.stride(1), 1 if out.dtype == torch.float32 else 0,
+        int(n_req), int(n_kv), int(G), int(d), int(page), int(split), float(scale),
+        _lib.stream_ptr(q.device)), "decode_dense")
+
+
 def sparse_paged_decode_batched(q, kv_cache, block_table, seq_lens, st, out,
                                 vsource=None, *, scale: float = None) -> None:
     """Batched Stage B (decode.py:328-387): one fixed-shape launch (the

@@ -410,6 +410,48 @@ def test_dense_equality_and_split_invariance():
         assert np.abs(o - outs[0]).max() <= 1e-3
 
 
+@pytest.mark.parametrize("n_kv,G,seq_lens", [(2, 16, [9000, 4097, 16, 1]), (8, 4, [20000])])
+@pytest.mark.parametrize("split", [1, 37, 256])
+def test_dense_comparator_matches_sdpa(n_kv, G, seq_lens, split):
+    """The dense full-KV decode (every page of the row, no page table) equals
+    float64 SDPA over the row's first seq_len tokens, for ragged rows
+    (partial last page, a one-page row, a one-token row) and any split."""
+    import torch
+    from locks.attention import decode_dense
+    from locks.attention.decode import _split_kv
+    say("dense comparator", n_kv, G, seq_lens, split)
+    case = make_case(8, n_kv, G, seq_lens, build=False)
+    d = to_dev(case)
+    k, v = _split_kv(d["kv"])
+    R = case.R
+    mp = torch.empty(R, n_kv, split, G, device="cuda")
+    lp = torch.empty_like(mp)
+    ap = torch.empty(R, n_kv, split, G, 128, device="cuda")
+    for dt in (torch.float32, torch.bfloat16):
+        out = torch.full((R, n_kv * G, 128), float("nan"), dtype=dt, device="cuda")
+        decode_dense(d["q"], k, v, d["bt"], d["sl"], mp, lp, ap, out, n_req=R, G=G,
+                     split=split, scale=case.scale)
+        torch.cuda.synchronize()
+        got = out.float().cpu().numpy()
+        for r, sl in enumerate(seq_lens):
+            npg = (sl + 15) // 16
+            K = O.bf16_to_f32(case.k[case.bt[r, :npg]]).reshape(-1, n_kv, 128)[:sl]
+            V = O.bf16_to_f32(case.v[case.bt[r, :npg]]).reshape(-1, n_kv, 128)[:sl]
+            Q = O.bf16_to_f32(case.q[r]).reshape(n_kv, G, 128)
+            qt = torch.from_numpy(Q).double()
+            kt = torch.from_numpy(K).double().permute(1, 0, 2)[:, None]
+            vt = torch.from_numpy(V).double().permute(1, 0, 2)[:, None]
+            ref = torch.nn.functional.scaled_dot_product_attention(
+                qt[:, :, None], kt.expand(-1, G, -1, -1), vt.expand(-1, G, -1, -1),
+                scale=float(case.scale))
+            ref = ref[:, :, 0].reshape(n_kv * G, 128).numpy()
+            # north-star bar for both output types: P is fp16 (the reference's
+            # P.V precision), ~2^-11 |v| per token, unaveraged on short rows
+            rb = ref if dt == torch.float32 else O.bf16_round(ref.astype(np.float32))
+            e = np.abs(got[r] - rb)
+            assert e.max() <= 2e-2 and e.sum() / np.abs(rb).sum() <= 1e-3, f"row {r}: {e.max()}"
+
+
 def test_end_to_end_runtime_path():
     """The reference's call sites (select adapter + decode dispatch) on one
     layer vs the oracle pipeline."""
