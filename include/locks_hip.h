@@ -196,6 +196,38 @@ int32_t locks_decode_fused(const uint16_t* q, int64_t q_stride_req, int64_t q_st
                            void* stream);
 
 /*
+ * locks_decode_fused without caller buffers, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference: its
+ * decode always takes caller-owned partials (attention/decode_cuda.py:960-965).
+ * Same arguments as locks_decode_fused minus m_part / l_part / acc_part /
+ * counters: those live in a file-scope device array of
+ * LOCKS_NOALLOC_SCRATCH_BYTES (one copy per GPU, held until the process
+ * ends), laid out as the arrival counters (n_req * n_kv i32, 256-B aligned)
+ * followed by the m, l (n_req * n_kv * split * G f32 each) and acc
+ * (n_req * n_kv * split * G * 128 f32) partials.  Calls needing more scratch
+ * fail with -1 and a message.  Each call clears the counters (a fill kernel)
+ * and launches the fused decode; nothing is allocated or freed.  Every call
+ * on one GPU shares the array, so calls that overlap on one GPU (other
+ * streams, other host threads) race.  Writes the same bits as
+ * locks_decode_fused on the same inputs.
+ */
+#define LOCKS_NOALLOC_SCRATCH_BYTES (16 * 1024 * 1024)
+int32_t locks_decode_fused_noalloc(const uint16_t* q, int64_t q_stride_req, int64_t q_stride_head,
+                                   const uint16_t* k_cache, int64_t k_stride_block,
+                                   int64_t k_stride_tok, int64_t k_stride_head,
+                                   const uint16_t* v_cache, int64_t v_stride_block,
+                                   int64_t v_stride_tok, int64_t v_stride_head, int32_t num_blocks,
+                                   const int32_t* block_table, int64_t bt_stride, int32_t bt_cols,
+                                   const int32_t* page_table, int64_t pt_stride_req,
+                                   int64_t pt_stride_head, int32_t pt_cols,
+                                   const int32_t* page_cnt, int64_t cnt_stride,
+                                   const int32_t* seq_lens, void* out, int64_t out_stride_req,
+                                   int64_t out_stride_head, int32_t out_is_f32, int32_t n_req,
+                                   int32_t n_kv, int32_t G, int32_t head_dim, int32_t page,
+                                   int32_t split, int32_t pps_min, float sm_scale, void* stream);
+
+/*
  * Dense full-KV decode: attention of each (request, kv head) group over
  * EVERY page of the row (pages 0 .. ceil(seq_len / page) - 1, no selection),
  * the dense comparator the sparse step is measured against.  No reference

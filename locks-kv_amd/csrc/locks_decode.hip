@@ -28,6 +28,8 @@
 #include "locks_common.h"
 #include "locks_hip.h"
 
+#include <mutex>
+
 namespace locks {
 
 constexpr int DC_D = 128;
@@ -567,6 +569,16 @@ __global__ __launch_bounds__(MH_BLK) void decode_merge_heads_kernel(
     }
 }
 
+// ---- no-allocation variant of the fused decode ----------------------------
+// Scratch of locks_decode_fused_noalloc: the arrival counters (first 256-B
+// aligned block), then the m, l and acc split partials.  One copy per GPU,
+// held until the process ends; every call on a GPU shares it.
+static __device__ __align__(256) uint8_t scratch[LOCKS_NOALLOC_SCRATCH_BYTES];
+
+__global__ __launch_bounds__(256) void zero_i32_kernel(int* __restrict__ p, int n) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0;
+}
+
 }  // namespace locks
 
 using namespace locks;
@@ -706,4 +718,69 @@ extern "C" int32_t locks_decode_dense(
                        m_part, l_part, acc_part, seq_lens, bt_cols, out, (long)out_stride_req,
                        (long)out_stride_head, out_is_f32, G, split, 1);
     return check_launch("decode_merge_heads_kernel");
+}
+
+// Device address of `scratch` per device (the array's host-side name is not
+// a device address).  Resolved once per device with that device current.
+static std::mutex g_scratch_mu;
+static uint8_t* g_scratch_ptr[64];
+
+static int scratch_on_current_device(uint8_t** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    LOCKS_REQUIRE(e == hipSuccess && dev >= 0 && dev < 64,
+                  "locks_decode_fused_noalloc: hipGetDevice failed (%s)", hipGetErrorString(e));
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        LOCKS_REQUIRE(e == hipSuccess && p, "locks_decode_fused_noalloc: hipGetSymbolAddress(scratch) "
+                      "failed on device %d (%s)", dev, hipGetErrorString(e));
+        g_scratch_ptr[dev] = static_cast<uint8_t*>(p);
+    }
+    *out = g_scratch_ptr[dev];
+    return 0;
+}
+
+extern "C" int32_t locks_decode_fused_noalloc(
+    const uint16_t* q, int64_t q_stride_req, int64_t q_stride_head,
+    const uint16_t* k_cache, int64_t k_stride_block, int64_t k_stride_tok, int64_t k_stride_head,
+    const uint16_t* v_cache, int64_t v_stride_block, int64_t v_stride_tok, int64_t v_stride_head,
+    int32_t num_blocks, const int32_t* block_table, int64_t bt_stride, int32_t bt_cols,
+    const int32_t* page_table, int64_t pt_stride_req, int64_t pt_stride_head, int32_t pt_cols,
+    const int32_t* page_cnt, int64_t cnt_stride, const int32_t* seq_lens,
+    void* out, int64_t out_stride_req, int64_t out_stride_head, int32_t out_is_f32,
+    int32_t n_req, int32_t n_kv, int32_t G, int32_t head_dim, int32_t page,
+    int32_t split, int32_t pps_min, float sm_scale, void* stream)
+{
+    LOCKS_REQUIRE(n_req >= 0 && n_kv >= 1 && G >= 1 && G <= 16 && split >= 1 && split <= MAX_SPLIT,
+                  "locks_decode_fused_noalloc: bad geometry (n_req=%d n_kv=%d G=%d split=%d)",
+                  n_req, n_kv, G, split);
+    const long rows = (long)n_req * n_kv;
+    const long cnt_bytes = (rows * 4 + 255) / 256 * 256;
+    const long ml = rows * split * G;                    // m or l floats
+    const long need = cnt_bytes + ml * 4 * 2 + ml * DC_D * 4;
+    LOCKS_REQUIRE(need <= LOCKS_NOALLOC_SCRATCH_BYTES,
+                  "locks_decode_fused_noalloc: n_req=%d x n_kv=%d x split=%d x G=%d needs %ld B of "
+                  "scratch, more than its %ld B (use locks_decode_fused with caller buffers)",
+                  n_req, n_kv, split, G, need, (long)LOCKS_NOALLOC_SCRATCH_BYTES);
+    uint8_t* base = nullptr;
+    if (int rc = scratch_on_current_device(&base)) return rc;
+    if (n_req == 0) return 0;
+    int* counters = reinterpret_cast<int*>(base);
+    float* m_part = reinterpret_cast<float*>(base + cnt_bytes);
+    float* l_part = m_part + ml;
+    float* acc_part = l_part + ml;
+    // the counters must start at zero: a previous call leaves them zero, but
+    // this array is shared by every call on the GPU, so clear them here (a
+    // fill kernel, which a HIP graph may capture)
+    hipLaunchKernelGGL(zero_i32_kernel, dim3((unsigned)cdiv((int)rows, 256)), dim3(256), 0,
+                       (hipStream_t)stream, counters, (int)rows);
+    if (int rc = check_launch("zero_i32_kernel")) return rc;
+    return locks_decode_fused(q, q_stride_req, q_stride_head, k_cache, k_stride_block, k_stride_tok,
+                              k_stride_head, v_cache, v_stride_block, v_stride_tok, v_stride_head,
+                              num_blocks, block_table, bt_stride, bt_cols, page_table, pt_stride_req,
+                              pt_stride_head, pt_cols, page_cnt, cnt_stride, seq_lens, m_part, l_part,
+                              acc_part, counters, out, out_stride_req, out_stride_head, out_is_f32,
+                              n_req, n_kv, G, head_dim, page, split, pps_min, sm_scale, stream);
 }

@@ -52,6 +52,10 @@ SIGNATURES = {
                                        _i32, _i32, _i32, _f32, _p]),
     "locks_mla_decode_merge": (_i32, [_p, _p, _p, _p, _i32, _p, _i64, _i64, _i32, _p, _i64, _i32,
                                       _i32, _i32, _i32, _i32, _p]),
+    "locks_decode_fused_noalloc": (_i32, [_p, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64,
+                                          _i64, _i32, _p, _i64, _i32, _p, _i64, _i64, _i32, _p,
+                                          _i64, _p, _p, _i64, _i64, _i32, _i32, _i32, _i32, _i32,
+                                          _i32, _i32, _i32, _f32, _p]),
     "locks_decode_dense": (_i32, [_p, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64,
                                   _i32, _p, _i64, _i32, _p, _p, _p, _p, _p, _i64, _i64, _i32,
                                   _i32, _i32, _i32, _i32, _i32, _i32, _f32, _p]),

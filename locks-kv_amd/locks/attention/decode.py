@@ -136,6 +136,26 @@ def decode_fused(q, k, v, block_table, seq_lens, page_table, page_cnt, m_part, l
         float(scale), _lib.stream_ptr(q.device)), "decode_fused")
 
 
+def decode_fused_noalloc(q, k, v, block_table, seq_lens, page_table, page_cnt, out, *,
+                         n_req: int, G: int, split: int, pps_min: int, scale: float) -> None:
+    """decode_fused with its split partials and arrival counters in the
+    library's fixed per-GPU scratch (LOCKS_NOALLOC_SCRATCH_BYTES): no buffer
+    arguments, nothing allocated.  Calls overlapping on one GPU race."""
+    _check_out(out)
+    NB, page, n_kv, d = k.shape
+    lib = _lib.load()
+    _lib.check(lib.locks_decode_fused_noalloc(
+        _lib.ptr(q), q.stride(0), q.stride(1),
+        _lib.ptr(k), k.stride(0), k.stride(1), k.stride(2),
+        _lib.ptr(v), v.stride(0), v.stride(1), v.stride(2), int(NB),
+        _lib.ptr(block_table), block_table.stride(0), int(block_table.shape[1]),
+        _lib.ptr(page_table), page_table.stride(0), page_table.stride(1),
+        int(page_table.shape[2]), _lib.ptr(page_cnt), page_cnt.stride(0), _lib.ptr(seq_lens),
+        _lib.ptr(out), out.stride(0), out.stride(1), 1 if out.dtype == torch.float32 else 0,
+        int(n_req), int(n_kv), int(G), int(d), int(page), int(split), int(pps_min),
+        float(scale), _lib.stream_ptr(q.device)), "decode_fused_noalloc")
+
+
 def decode_merge(m_part, l_part, acc_part, page_cnt, out, *, n_req: int, n_kv: int, G: int,
                  split: int, pps_min: int, pt_cols: int) -> None:
     """LSE merge of the split partials into ``out``; ``pt_cols`` is the page
