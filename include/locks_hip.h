@@ -28,7 +28,7 @@
 
 #include <stdint.h>
 
-#define LOCKS_ABI_VERSION 4
+#define LOCKS_ABI_VERSION 5
 
 #ifdef __cplusplus
 extern "C" {
@@ -139,7 +139,11 @@ int32_t locks_select_nrm_topb(const float* score_h, const float* page_max, int32
  *   (vLLM kv_cache (NB, 2, page, n_kv, d) halves, attention/decode.py:64-73)
  *   page_table (n_req, n_kv, pt_cols) i32; page_cnt (n_req, n_kv) i32
  *   m_part, l_part (n_req, n_kv, split, G) f32; acc_part (..., G, 128) f32
- *   pps = max(ceil(cnt / split), pps_min); inactive splits store nothing.
+ *   max_cnt: the caller's upper bound of page_cnt (b_max + sink + window
+ *   for a selection; 0 = none).  min(split, ceil(max_cnt / pps_min)) splits
+ *   are launched ("nsplit"); pps = max(ceil(cnt / nsplit), pps_min), so a
+ *   count above the bound is still decoded in full.  split remains the
+ *   partial buffers' stride.  Inactive splits store nothing.
  */
 int32_t locks_decode_splitk(const uint16_t* q, int64_t q_stride_req, int64_t q_stride_head,
                             const uint16_t* k_cache, int64_t k_stride_block,
@@ -152,23 +156,25 @@ int32_t locks_decode_splitk(const uint16_t* q, int64_t q_stride_req, int64_t q_s
                             int64_t cnt_stride, const int32_t* seq_lens, float* m_part,
                             float* l_part, float* acc_part, int32_t n_req, int32_t n_kv,
                             int32_t G, int32_t head_dim, int32_t page, int32_t split,
-                            int32_t pps_min, float sm_scale, void* stream);
+                            int32_t pps_min, int32_t max_cnt, float sm_scale, void* stream);
 
 /*
  * LSE merge of the split-K partials into the attention output.
- * Replaces merge_splits_kernel (attention/merge.py:105-152).
+ * Replaces merge_splits_kernel (attention/merge.py:105-152).  One workgroup
+ * per (request, kv head, query head), so a row's partials are read by G
+ * CUs in parallel.
  *   out (n_req, n_kv*G, 128) bf16 (out_is_f32 = 0) or f32 (out_is_f32 = 1),
  *   strides (out_stride_req, out_stride_head, 1), multiples of 4 elements;
  *   rows with page_cnt 0 get 0.
- *   pt_cols: the page-table width given to locks_decode_splitk; page_cnt is
- *   clamped to it exactly as the split kernel clamps it, so both derive the
- *   same pages per split and active split count.
+ *   pt_cols, max_cnt: as given to locks_decode_splitk (page_cnt is clamped
+ *   to pt_cols and the split count derived from max_cnt exactly as there),
+ *   so both derive the same pages per split and active split count.
  */
 int32_t locks_decode_merge(const float* m_part, const float* l_part, const float* acc_part,
                            const int32_t* page_cnt, int64_t cnt_stride, int32_t pt_cols, void* out,
                            int64_t out_stride_req, int64_t out_stride_head, int32_t out_is_f32,
                            int32_t n_req, int32_t n_kv, int32_t G, int32_t head_dim,
-                           int32_t split, int32_t pps_min, void* stream);
+                           int32_t split, int32_t pps_min, int32_t max_cnt, void* stream);
 
 /*
  * locks_decode_splitk and locks_decode_merge in one launch: the last split
@@ -176,11 +182,15 @@ int32_t locks_decode_merge(const float* m_part, const float* l_part, const float
  * out.  Replaces the same pair of launches
  * (attention/decode.py:328-387 -> attention/merge.py:105-152); same
  * arguments plus
- *   counters (n_req * n_kv) i32 arrival counts: zero before the first call,
+ *   counters (n_req * n_kv * LOCKS_DECODE_COUNTER_STRIDE) i32 arrival
+ *     counts, one per row at a stride of LOCKS_DECODE_COUNTER_STRIDE ints
+ *     (256 B: rows never share a cache line): zero before the first call,
  *     left zero by every call; calls that share counters must not overlap;
  *   out / out_stride_* / out_is_f32 as locks_decode_merge.
- * Writes the same bits as locks_decode_splitk + locks_decode_merge.
+ * Same values as locks_decode_splitk + locks_decode_merge up to fp32
+ * reassociation (the last split merges the whole row in one workgroup).
  */
+#define LOCKS_DECODE_COUNTER_STRIDE 64
 int32_t locks_decode_fused(const uint16_t* q, int64_t q_stride_req, int64_t q_stride_head,
                            const uint16_t* k_cache, int64_t k_stride_block, int64_t k_stride_tok,
                            int64_t k_stride_head, const uint16_t* v_cache, int64_t v_stride_block,
@@ -192,7 +202,8 @@ int32_t locks_decode_fused(const uint16_t* q, int64_t q_stride_req, int64_t q_st
                            float* l_part, float* acc_part, int32_t* counters, void* out,
                            int64_t out_stride_req, int64_t out_stride_head, int32_t out_is_f32,
                            int32_t n_req, int32_t n_kv, int32_t G, int32_t head_dim,
-                           int32_t page, int32_t split, int32_t pps_min, float sm_scale,
+                           int32_t page, int32_t split, int32_t pps_min, int32_t max_cnt,
+                           float sm_scale,
                            void* stream);
 
 /*
@@ -203,8 +214,8 @@ int32_t locks_decode_fused(const uint16_t* q, int64_t q_stride_req, int64_t q_st
  * Same arguments as locks_decode_fused minus m_part / l_part / acc_part /
  * counters: those live in a file-scope device array of
  * LOCKS_NOALLOC_SCRATCH_BYTES (one copy per GPU, held until the process
- * ends), laid out as the arrival counters (n_req * n_kv i32, 256-B aligned)
- * followed by the m, l (n_req * n_kv * split * G f32 each) and acc
+ * ends), laid out as the arrival counters (n_req * n_kv *
+ * LOCKS_DECODE_COUNTER_STRIDE i32) followed by the m, l (n_req * n_kv * split * G f32 each) and acc
  * (n_req * n_kv * split * G * 128 f32) partials.  Calls needing more scratch
  * fail with -1 and a message.  Each call clears the counters (a fill kernel)
  * and launches the fused decode; nothing is allocated or freed.  Every call
@@ -225,7 +236,8 @@ int32_t locks_decode_fused_noalloc(const uint16_t* q, int64_t q_stride_req, int6
                                    const int32_t* seq_lens, void* out, int64_t out_stride_req,
                                    int64_t out_stride_head, int32_t out_is_f32, int32_t n_req,
                                    int32_t n_kv, int32_t G, int32_t head_dim, int32_t page,
-                                   int32_t split, int32_t pps_min, float sm_scale, void* stream);
+                                   int32_t split, int32_t pps_min, int32_t max_cnt,
+                                   float sm_scale, void* stream);
 
 /*
  * Dense full-KV decode: attention of each (request, kv head) group over

@@ -28,6 +28,7 @@
 #include "locks_common.h"
 #include "locks_hip.h"
 
+#include <algorithm>
 #include <mutex>
 
 namespace locks {
@@ -73,6 +74,13 @@ __device__ __forceinline__ float ld_part(const float* base, long idx) {
 
 // Merge the first n_act split partials of row rk into out (one workgroup,
 // DC_BLK threads).  w_s, l_s: >= MAX_SPLIT * 16 floats of LDS each.
+// Work split: the row's G * 32 float4 output columns ("items") times `grp`
+// split streams fill the workgroup (G <= 8; G > 8: two items per thread).
+// Every thread issues the loads of its first MR_PF splits' partials before
+// anything waits, together with the m / l loads, so a row of up to
+// grp * MR_PF splits costs one memory round trip; the streams are summed in
+// LDS at the end.
+constexpr int MR_PF = 16;
 template <bool COHERENT = false>
 __device__ void merge_row(const float* __restrict__ m_part, const float* __restrict__ l_part,
                           const float* __restrict__ acc_part, long rk, int r, int kh, int n_act,
@@ -80,21 +88,26 @@ __device__ void merge_row(const float* __restrict__ m_part, const float* __restr
                           int out_f32, float* w_s, float* l_s, float* lt_s) {
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     constexpr int NWV = DC_BLK / kWave;
-    constexpr int PF = 8;                               // splits of acc prefetched per item
-    // the first PF split partials of this thread's (head, 4-dim) items are
-    // loaded before anything waits (they do not depend on the weights)
-    // Loads are unconditional (indices clamped into the buffers, surplus
-    // values never used): a guarded load merges with its default at a branch
-    // join, where the compiler waits for it -- splitting one round trip in two.
-    float4 pre[2][PF];
+    const int n_items = G * (DC_D / 4);
+    const int grp = n_items >= DC_BLK ? 1 : DC_BLK / n_items;
+    const int stream = n_items >= DC_BLK ? 0 : tid / n_items;
+    const int item0 = n_items >= DC_BLK ? tid : tid % n_items;
+    const bool two = n_items > DC_BLK;                  // G > 8: items tid and tid + DC_BLK
+    const bool live = stream < grp;                     // threads past grp * n_items idle
+    // partial index of (item, split s): ((rk * split + s) * G + g) * 32 + c
+    //   = rk * split * n_items + s * n_items + item
+    const long rowbase = rk * split * (long)n_items;
+    float4 pre[2][MR_PF];
 #pragma unroll
     for (int it = 0; it < 2; ++it) {
-        const int i = min(tid + it * DC_BLK, G * (DC_D / 4) - 1);
-        const int g = i / (DC_D / 4), d4 = (i % (DC_D / 4)) * 4;
+        const int item = min(item0 + it * DC_BLK, n_items - 1);
 #pragma unroll
-        for (int k = 0; k < PF; ++k)
-            pre[it][k] = ld_part4<COHERENT>(acc_part, (rk * split * G + g) * DC_D + d4 +
-                                                          (long)min(k, split - 1) * G * DC_D);
+        for (int k = 0; k < MR_PF; ++k) {
+            const int sidx = min(stream + k * grp, split - 1);
+            pre[it][k] = (it == 0 || two)
+                ? ld_part4<COHERENT>(acc_part, (rowbase + (long)sidx * n_items + item) * 4)
+                : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
     }
     // every (split, head) m and l, up to 4 per thread in flight, then the
     // per-head max / weights / denominator from LDS
@@ -137,26 +150,58 @@ __device__ void merge_row(const float* __restrict__ m_part, const float* __restr
         if (lane == 0) lt_s[g] = lt;
     }
     __syncthreads();
+    float4 accs[2];
 #pragma unroll
     for (int it = 0; it < 2; ++it) {
-        const int i = tid + it * DC_BLK;
-        if (i >= G * (DC_D / 4)) break;
-        const int g = i / (DC_D / 4), d4 = (i % (DC_D / 4)) * 4;
+        const int item = min(item0 + it * DC_BLK, n_items - 1);
+        const int g = item >> 5;
         float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-        for (int k = 0; k < PF; ++k) {
-            if (k < n_act) {
-                const float w = w_s[k * 16 + g];
+        for (int k = 0; k < MR_PF; ++k) {
+            const int sidx = stream + k * grp;
+            if (sidx < n_act) {
+                const float w = w_s[sidx * 16 + g];
                 const float4 a = pre[it][k];
                 acc.x += w * a.x; acc.y += w * a.y; acc.z += w * a.z; acc.w += w * a.w;
             }
         }
-#pragma unroll 8
-        for (int s = PF; s < n_act; ++s) {
-            const float w = w_s[s * 16 + g];
-            const float4 a = ld_part4<COHERENT>(acc_part, (rk * split * G + g) * DC_D + d4 + (long)s * G * DC_D);
-            acc.x += w * a.x; acc.y += w * a.y; acc.z += w * a.z; acc.w += w * a.w;
+        // splits past the prefetched ones (rows of more than grp * MR_PF
+        // splits): batches of 8 loads, then their FMAs
+        for (int k0 = MR_PF; stream + k0 * grp < n_act; k0 += 8) {
+            float4 b[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const int sidx = min(stream + (k0 + k) * grp, split - 1);
+                b[k] = ld_part4<COHERENT>(acc_part, (rowbase + (long)sidx * n_items + item) * 4);
+            }
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const int sidx = stream + (k0 + k) * grp;
+                if (sidx < n_act) {
+                    const float w = w_s[sidx * 16 + g];
+                    acc.x += w * b[k].x; acc.y += w * b[k].y; acc.z += w * b[k].z; acc.w += w * b[k].w;
+                }
+            }
         }
+        accs[it] = acc;
+    }
+    float4* red = reinterpret_cast<float4*>(l_s);        // [stream][item], after the weights
+    if (grp > 1) {
+        if (live) red[stream * n_items + item0] = accs[0];
+        __syncthreads();
+    }
+    if (stream != 0 || !live) return;
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+        if (it == 1 && !two) break;
+        const int item = item0 + it * DC_BLK;
+        if (item >= n_items) break;
+        float4 acc = accs[it];
+        for (int sg = 1; sg < grp; ++sg) {
+            const float4 a = red[sg * n_items + item];
+            acc.x += a.x; acc.y += a.y; acc.z += a.z; acc.w += a.w;
+        }
+        const int g = item >> 5, d4 = (item & 31) * 4;
         const float lt = lt_s[g];
         const float inv = (lt > 0.f) ? 1.f / lt : 0.f;
         const float o[4] = {acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv};
@@ -226,7 +271,9 @@ __global__ __launch_bounds__(DC_BLK) void decode_split_kernel(
         pt_spec = (js < pt_cols) ? prow[js] : 0;
         cnt = min(pcnt[(long)r * cnt_sr + kh], pt_cols);
     }
-    const int pps = max(cdiv(cnt, split), pps_min);
+    // gridDim.x = the launched split count (<= split, the buffers' stride)
+    const int nsplit = gridDim.x;
+    const int pps = max(cdiv(cnt, nsplit), pps_min);
     const int j0 = sp * pps;
     if constexpr (FUSED) {
         if (cnt <= 0) {                           // nothing selected: the output row is 0
@@ -450,6 +497,10 @@ __global__ __launch_bounds__(DC_BLK) void decode_split_kernel(
         //      the last one acquires (workgroup fence after the barrier) and
         //      reads the partials with SC1 loads, which cannot hit a stale
         //      L2 line.
+        // Each row's counter sits in its own 256-B block: with the counters
+        // of all rows packed in one cache line, every arrival of the launch
+        // serialised on that line (measured +1.7 us per launch at Llama
+        // 128K: 256 arrivals).
         // Agent-scope release / acquire fences would add an L2 write-back
         // (buffer_wbl2) and an L2 invalidate (buffer_inv) to every workgroup:
         // measured +8 us per layer at Llama 128K (step 1.35 -> 1.62 ms), for
@@ -459,56 +510,42 @@ __global__ __launch_bounds__(DC_BLK) void decode_split_kernel(
         __builtin_amdgcn_s_waitcnt(0x0070);           // vmcnt(0): SC1 stores acknowledged
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
         __syncthreads();
-        const int n_act = min(cdiv(cnt, pps), split);
+        const int n_act = min(cdiv(cnt, pps), nsplit);
         if (tid == 0) {
-            const int old = __hip_atomic_fetch_add(counters + rk, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const int old = __hip_atomic_fetch_add(counters + rk * LOCKS_DECODE_COUNTER_STRIDE, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             last_s = (old == n_act - 1);
         }
         __syncthreads();
         if (!last_s) return;
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-        if (tid == 0) __hip_atomic_store(counters + rk, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (tid == 0) __hip_atomic_store(counters + rk * LOCKS_DECODE_COUNTER_STRIDE, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         merge_row<true>(m_part, l_part, acc_part, rk, r, kh, n_act, G, split, out, o_sr, o_sh,
                         out_f32, reinterpret_cast<float*>(&stA[0][0]),
                         reinterpret_cast<float*>(&stB[0][0]), lt_s);
     }
 }
 
-__global__ __launch_bounds__(DC_BLK) void decode_merge_kernel(
-    const float* __restrict__ m_part, const float* __restrict__ l_part,
-    const float* __restrict__ acc_part, const int* __restrict__ pcnt, long cnt_sr, int pt_cols,
-    void* __restrict__ out, long o_sr, long o_sh, int out_f32, int G, int split, int pps_min)
-{
-    const int kh = blockIdx.x, r = blockIdx.y;
-    const int n_kv = gridDim.x;
-    const long rk = (long)r * n_kv + kh;
-    // the same clamp as decode_split_kernel, so both derive the same pps / n_act
-    const int cnt = min(pcnt[(long)r * cnt_sr + kh], pt_cols);
-    const int pps = max(cdiv(cnt, split), pps_min);
-    const int n_act = cnt > 0 ? min(cdiv(cnt, pps), split) : 0;
-    __shared__ float w_s[MAX_SPLIT * 16], l_s[MAX_SPLIT * 16];
-    __shared__ float lt_s[16];
-    merge_row(m_part, l_part, acc_part, rk, r, kh, n_act, G, split, out, o_sr, o_sh, out_f32,
-              w_s, l_s, lt_s);
-}
-
 // LSE merge of one (request, kv head, query head) row of split partials,
-// one workgroup per head: 8 split streams x 32 float4 columns, so a row of
-// hundreds of splits (the dense comparator) is merged by G workgroups
-// instead of one.  The page count is the dense one (every page of the row).
+// one workgroup per head: 8 split streams x 32 float4 columns, so a row is
+// merged by G workgroups (G CUs' memory parallelism) instead of one.  The
+// page count is page_cnt (clamped to pt_cols, as the split kernel) or, with
+// pcnt == nullptr, the dense one (every page of the row).
 constexpr int MH_BLK = 256, MH_STREAMS = MH_BLK / 32;
 __global__ __launch_bounds__(MH_BLK) void decode_merge_heads_kernel(
     const float* __restrict__ m_part, const float* __restrict__ l_part,
-    const float* __restrict__ acc_part, const int* __restrict__ seq_lens, int bt_cols,
-    void* __restrict__ out, long o_sr, long o_sh, int out_f32, int G, int split, int pps_min)
+    const float* __restrict__ acc_part, const int* __restrict__ pcnt, long cnt_sr, int pt_cols,
+    const int* __restrict__ seq_lens, int bt_cols,
+    void* __restrict__ out, long o_sr, long o_sh, int out_f32, int G, int split, int nsplit,
+    int pps_min)
 {
     const int g = blockIdx.x, kh = blockIdx.y, r = blockIdx.z;
     const int n_kv = gridDim.y;
     const long rk = (long)r * n_kv + kh;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int cnt = min(cdiv(seq_lens[r], DC_PG), bt_cols);
-    const int pps = max(cdiv(cnt, split), pps_min);
-    const int n_act = cnt > 0 ? min(cdiv(cnt, pps), split) : 0;
+    const int cnt = pcnt ? min(pcnt[(long)r * cnt_sr + kh], pt_cols)
+                         : min(cdiv(seq_lens[r], DC_PG), bt_cols);
+    const int pps = max(cdiv(cnt, nsplit), pps_min);
+    const int n_act = cnt > 0 ? min(cdiv(cnt, pps), nsplit) : 0;
     __shared__ float w_s[MAX_SPLIT];
     __shared__ float red[MH_BLK / kWave];
     __shared__ float4 part[MH_STREAMS][32];
@@ -583,6 +620,14 @@ __global__ __launch_bounds__(256) void zero_i32_kernel(int* __restrict__ p, int 
 
 using namespace locks;
 
+// Splits launched: enough for max_cnt pages at pps_min pages each (max_cnt
+// is the caller's bound on page_cnt; 0 = none), at most `split`.  The
+// kernels derive pps from the launched count, so a count above the bound is
+// still decoded in full, in fewer, longer splits.
+static int launched_splits(int split, int pps_min, int max_cnt) {
+    return max_cnt > 0 ? std::min(split, std::max(1, cdiv(max_cnt, pps_min))) : split;
+}
+
 extern "C" int32_t locks_decode_splitk(
     const uint16_t* q, int64_t q_stride_req, int64_t q_stride_head,
     const uint16_t* k_cache, int64_t k_stride_block, int64_t k_stride_tok, int64_t k_stride_head,
@@ -592,7 +637,7 @@ extern "C" int32_t locks_decode_splitk(
     const int32_t* page_cnt, int64_t cnt_stride, const int32_t* seq_lens,
     float* m_part, float* l_part, float* acc_part,
     int32_t n_req, int32_t n_kv, int32_t G, int32_t head_dim, int32_t page,
-    int32_t split, int32_t pps_min, float sm_scale, void* stream)
+    int32_t split, int32_t pps_min, int32_t max_cnt, float sm_scale, void* stream)
 {
     LOCKS_REQUIRE(head_dim == DC_D, "locks_decode_splitk: head_dim %d unsupported (this build: 128)", head_dim);
     LOCKS_REQUIRE(page == DC_PG, "locks_decode_splitk: page %d unsupported (this build: 16)", page);
@@ -607,7 +652,7 @@ extern "C" int32_t locks_decode_splitk(
     LOCKS_REQUIRE(q && k_cache && v_cache && block_table && page_table && page_cnt && seq_lens &&
                   m_part && l_part && acc_part, "locks_decode_splitk: null pointer argument");
     if (n_req == 0) return 0;
-    hipLaunchKernelGGL(decode_split_kernel<false>, dim3(split, n_kv, n_req), dim3(DC_BLK), 0,
+    hipLaunchKernelGGL(decode_split_kernel<false>, dim3(launched_splits(split, pps_min, max_cnt), n_kv, n_req), dim3(DC_BLK), 0,
                        (hipStream_t)stream, q, (long)q_stride_req, (long)q_stride_head, k_cache,
                        (long)k_stride_block, (long)k_stride_tok, (long)k_stride_head, v_cache,
                        (long)v_stride_block, (long)v_stride_tok, (long)v_stride_head, num_blocks,
@@ -628,7 +673,7 @@ extern "C" int32_t locks_decode_fused(
     float* m_part, float* l_part, float* acc_part, int32_t* counters,
     void* out, int64_t out_stride_req, int64_t out_stride_head, int32_t out_is_f32,
     int32_t n_req, int32_t n_kv, int32_t G, int32_t head_dim, int32_t page,
-    int32_t split, int32_t pps_min, float sm_scale, void* stream)
+    int32_t split, int32_t pps_min, int32_t max_cnt, float sm_scale, void* stream)
 {
     LOCKS_REQUIRE(head_dim == DC_D, "locks_decode_fused: head_dim %d unsupported (this build: 128)", head_dim);
     LOCKS_REQUIRE(page == DC_PG, "locks_decode_fused: page %d unsupported (this build: 16)", page);
@@ -647,7 +692,7 @@ extern "C" int32_t locks_decode_fused(
     LOCKS_REQUIRE(q && k_cache && v_cache && block_table && page_table && page_cnt && seq_lens &&
                   m_part && l_part && acc_part && counters && out, "locks_decode_fused: null pointer argument");
     if (n_req == 0) return 0;
-    hipLaunchKernelGGL(decode_split_kernel<true>, dim3(split, n_kv, n_req), dim3(DC_BLK), 0,
+    hipLaunchKernelGGL(decode_split_kernel<true>, dim3(launched_splits(split, pps_min, max_cnt), n_kv, n_req), dim3(DC_BLK), 0,
                        (hipStream_t)stream, q, (long)q_stride_req, (long)q_stride_head, k_cache,
                        (long)k_stride_block, (long)k_stride_tok, (long)k_stride_head, v_cache,
                        (long)v_stride_block, (long)v_stride_tok, (long)v_stride_head, num_blocks,
@@ -662,7 +707,7 @@ extern "C" int32_t locks_decode_merge(
     const float* m_part, const float* l_part, const float* acc_part,
     const int32_t* page_cnt, int64_t cnt_stride, int32_t pt_cols, void* out, int64_t out_stride_req,
     int64_t out_stride_head, int32_t out_is_f32, int32_t n_req, int32_t n_kv, int32_t G,
-    int32_t head_dim, int32_t split, int32_t pps_min, void* stream)
+    int32_t head_dim, int32_t split, int32_t pps_min, int32_t max_cnt, void* stream)
 {
     LOCKS_REQUIRE(pt_cols >= 1, "locks_decode_merge: pt_cols %d < 1", pt_cols);
     LOCKS_REQUIRE(head_dim == DC_D, "locks_decode_merge: head_dim %d unsupported (this build: 128)", head_dim);
@@ -673,9 +718,10 @@ extern "C" int32_t locks_decode_merge(
     LOCKS_REQUIRE(out_stride_req % 4 == 0 && out_stride_head % 4 == 0,
                   "locks_decode_merge: out strides must be multiples of 4 elements");
     if (n_req == 0) return 0;
-    hipLaunchKernelGGL(decode_merge_kernel, dim3(n_kv, n_req), dim3(DC_BLK), 0, (hipStream_t)stream,
-                       m_part, l_part, acc_part, page_cnt, (long)cnt_stride, pt_cols, out, (long)out_stride_req,
-                       (long)out_stride_head, out_is_f32, G, split, pps_min);
+    hipLaunchKernelGGL(decode_merge_heads_kernel, dim3(G, n_kv, n_req), dim3(MH_BLK), 0,
+                       (hipStream_t)stream, m_part, l_part, acc_part, page_cnt, (long)cnt_stride,
+                       pt_cols, nullptr, 1, out, (long)out_stride_req, (long)out_stride_head,
+                       out_is_f32, G, split, launched_splits(split, pps_min, max_cnt), pps_min);
     return check_launch("decode_merge_kernel");
 }
 
@@ -715,8 +761,8 @@ extern "C" int32_t locks_decode_dense(
     int rc = check_launch("decode_split_kernel<dense>");
     if (rc) return rc;
     hipLaunchKernelGGL(decode_merge_heads_kernel, dim3(G, n_kv, n_req), dim3(MH_BLK), 0, st,
-                       m_part, l_part, acc_part, seq_lens, bt_cols, out, (long)out_stride_req,
-                       (long)out_stride_head, out_is_f32, G, split, 1);
+                       m_part, l_part, acc_part, nullptr, 0L, 1, seq_lens, bt_cols, out,
+                       (long)out_stride_req, (long)out_stride_head, out_is_f32, G, split, split, 1);
     return check_launch("decode_merge_heads_kernel");
 }
 
@@ -751,13 +797,13 @@ extern "C" int32_t locks_decode_fused_noalloc(
     const int32_t* page_cnt, int64_t cnt_stride, const int32_t* seq_lens,
     void* out, int64_t out_stride_req, int64_t out_stride_head, int32_t out_is_f32,
     int32_t n_req, int32_t n_kv, int32_t G, int32_t head_dim, int32_t page,
-    int32_t split, int32_t pps_min, float sm_scale, void* stream)
+    int32_t split, int32_t pps_min, int32_t max_cnt, float sm_scale, void* stream)
 {
     LOCKS_REQUIRE(n_req >= 0 && n_kv >= 1 && G >= 1 && G <= 16 && split >= 1 && split <= MAX_SPLIT,
                   "locks_decode_fused_noalloc: bad geometry (n_req=%d n_kv=%d G=%d split=%d)",
                   n_req, n_kv, G, split);
     const long rows = (long)n_req * n_kv;
-    const long cnt_bytes = (rows * 4 + 255) / 256 * 256;
+    const long cnt_bytes = rows * LOCKS_DECODE_COUNTER_STRIDE * 4;
     const long ml = rows * split * G;                    // m or l floats
     const long need = cnt_bytes + ml * 4 * 2 + ml * DC_D * 4;
     LOCKS_REQUIRE(need <= LOCKS_NOALLOC_SCRATCH_BYTES,
@@ -774,13 +820,15 @@ extern "C" int32_t locks_decode_fused_noalloc(
     // the counters must start at zero: a previous call leaves them zero, but
     // this array is shared by every call on the GPU, so clear them here (a
     // fill kernel, which a HIP graph may capture)
-    hipLaunchKernelGGL(zero_i32_kernel, dim3((unsigned)cdiv((int)rows, 256)), dim3(256), 0,
-                       (hipStream_t)stream, counters, (int)rows);
+    const int n_ctr = (int)(rows * LOCKS_DECODE_COUNTER_STRIDE);
+    hipLaunchKernelGGL(zero_i32_kernel, dim3((unsigned)cdiv(n_ctr, 256)), dim3(256), 0,
+                       (hipStream_t)stream, counters, n_ctr);
     if (int rc = check_launch("zero_i32_kernel")) return rc;
     return locks_decode_fused(q, q_stride_req, q_stride_head, k_cache, k_stride_block, k_stride_tok,
                               k_stride_head, v_cache, v_stride_block, v_stride_tok, v_stride_head,
                               num_blocks, block_table, bt_stride, bt_cols, page_table, pt_stride_req,
                               pt_stride_head, pt_cols, page_cnt, cnt_stride, seq_lens, m_part, l_part,
                               acc_part, counters, out, out_stride_req, out_stride_head, out_is_f32,
-                              n_req, n_kv, G, head_dim, page, split, pps_min, sm_scale, stream);
+                              n_req, n_kv, G, head_dim, page, split, pps_min, max_cnt, sm_scale,
+                              stream);
 }

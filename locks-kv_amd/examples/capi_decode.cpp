@@ -104,7 +104,7 @@ int main() {
         dev_alloc(&d_score, (size_t)R * NKV * MP, 0) || dev_alloc(&d_tab, (size_t)R * NKV * MP, 0) ||
         dev_alloc(&d_cnt, (size_t)R * NKV, 0) || dev_alloc(&d_ws, (size_t)(wsb > 256 ? wsb : 256), 0) ||
         dev_alloc(&d_m, (size_t)R * NKV * SPLIT * G, 0) || dev_alloc(&d_l, (size_t)R * NKV * SPLIT * G, 0) ||
-        dev_alloc(&d_acc, (size_t)R * NKV * SPLIT * G * D, 0) || dev_alloc(&d_ctr, (size_t)R * NKV, 0) ||
+        dev_alloc(&d_acc, (size_t)R * NKV * SPLIT * G * D, 0) || dev_alloc(&d_ctr, (size_t)R * NKV * LOCKS_DECODE_COUNTER_STRIDE, 0) ||
         dev_alloc(&d_out, (size_t)R * H * D, 0)) {
         std::printf("allocation failed\n");
         return 1;
@@ -131,7 +131,8 @@ int main() {
     LOCKS_OK(locks_decode_fused(d_q, (long)H * D, D, d_kv, s_blk, s_tok, D, d_kv + s_half, s_blk,
                                 s_tok, D, NB, d_bt, MP, MP, d_tab, (long)NKV * MP, MP, MP, d_cnt,
                                 NKV, d_seq, d_m, d_l, d_acc, d_ctr, d_out, (long)H * D, D, 0, R,
-                                NKV, G, D, PAGE, SPLIT, PPS_MIN, scale, stream));
+                                NKV, G, D, PAGE, SPLIT, PPS_MIN, BUDGET + SINK + WINDOW, scale,
+                                stream));
     HIP_OK(hipStreamSynchronize(stream));
 
     std::vector<int32_t> tab((size_t)NKV * MP), cnt(NKV);

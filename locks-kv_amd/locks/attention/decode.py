@@ -45,7 +45,12 @@ class ResidentVSource:
         return v, v.stride(0), v.stride(1), v.stride(2)
 
 
-FUSED_MERGE = True            # one launch: the last split of a row merges it
+COUNTER_STRIDE = 64          # ints between rows' arrival counters (LOCKS_DECODE_COUNTER_STRIDE)
+# False (default): the split kernel, then one merge workgroup per query head
+# (measured faster per step: 1.306 vs 1.321 ms Llama 128K, 2.529 vs 2.612 ms
+# GLM 1M -- the fused form merges a whole row's partials through one CU);
+# True: one launch whose last split per row merges the row
+FUSED_MERGE = False
 PPS_MIN_OVERRIDE = None        # set by bench sweeps; None = the table below
 
 
@@ -83,12 +88,12 @@ def ensure_stage_b_buffers(st, device, split: int) -> None:
     st.l_part = torch.empty(R, n_kv, split, G, device=device, dtype=torch.float32)
     st.acc_part = torch.empty(R, n_kv, split, G, D, device=device, dtype=torch.float32)
     # arrival counts of the fused decode; every call leaves them at zero
-    st.dec_counters = torch.zeros(R, n_kv, device=device, dtype=torch.int32)
+    st.dec_counters = torch.zeros(R, n_kv, COUNTER_STRIDE, device=device, dtype=torch.int32)
 
 
 def decode_splitk(q, k, v, block_table, seq_lens, page_table, page_cnt, m_part, l_part,
                   acc_part, *, n_req: int, G: int, split: int, pps_min: int,
-                  scale: float) -> None:
+                  scale: float, max_cnt: int = 0) -> None:
     """Launch the split kernel on explicit tensors.  k, v: (NB, page, n_kv, d)
     views; page_table (R, n_kv, MP) i32; page_cnt (R, n_kv) i32."""
     NB, page, n_kv, d = k.shape
@@ -101,7 +106,7 @@ def decode_splitk(q, k, v, block_table, seq_lens, page_table, page_cnt, m_part, 
         _lib.ptr(page_table), page_table.stride(0), page_table.stride(1),
         int(page_table.shape[2]), _lib.ptr(page_cnt), page_cnt.stride(0), _lib.ptr(seq_lens),
         _lib.ptr(m_part), _lib.ptr(l_part), _lib.ptr(acc_part), int(n_req), int(n_kv), int(G),
-        int(d), int(page), int(split), int(pps_min), float(scale),
+        int(d), int(page), int(split), int(pps_min), int(max_cnt), float(scale),
         _lib.stream_ptr(q.device)), "decode_splitk")
 
 
@@ -116,10 +121,13 @@ def _check_out(out) -> None:
 
 def decode_fused(q, k, v, block_table, seq_lens, page_table, page_cnt, m_part, l_part,
                  acc_part, counters, out, *, n_req: int, G: int, split: int, pps_min: int,
-                 scale: float) -> None:
+                 scale: float, max_cnt: int = 0) -> None:
     """Split kernel whose last-arriving split of each (request, kv head) row
-    merges the row into ``out`` (one launch).  ``counters`` (R, n_kv) i32
-    must be zero on the first call; each call leaves it zero."""
+    merges the row into ``out`` (one launch).  ``counters`` (R, n_kv,
+    COUNTER_STRIDE) i32 must be zero on the first call; each call leaves it
+    zero."""
+    if counters.numel() < int(n_req) * k.shape[2] * COUNTER_STRIDE:
+        raise ValueError(f"counters needs n_req * n_kv * {COUNTER_STRIDE} int32 entries")
     _check_out(out)
     NB, page, n_kv, d = k.shape
     lib = _lib.load()
@@ -133,11 +141,12 @@ def decode_fused(q, k, v, block_table, seq_lens, page_table, page_cnt, m_part, l
         _lib.ptr(m_part), _lib.ptr(l_part), _lib.ptr(acc_part), _lib.ptr(counters),
         _lib.ptr(out), out.stride(0), out.stride(1), 1 if out.dtype == torch.float32 else 0,
         int(n_req), int(n_kv), int(G), int(d), int(page), int(split), int(pps_min),
-        float(scale), _lib.stream_ptr(q.device)), "decode_fused")
+        int(max_cnt), float(scale), _lib.stream_ptr(q.device)), "decode_fused")
 
 
 def decode_fused_noalloc(q, k, v, block_table, seq_lens, page_table, page_cnt, out, *,
-                         n_req: int, G: int, split: int, pps_min: int, scale: float) -> None:
+                         n_req: int, G: int, split: int, pps_min: int, scale: float,
+                         max_cnt: int = 0) -> None:
     """decode_fused with its split partials and arrival counters in the
     library's fixed per-GPU scratch (LOCKS_NOALLOC_SCRATCH_BYTES): no buffer
     arguments, nothing allocated.  Calls overlapping on one GPU race."""
@@ -153,11 +162,11 @@ def decode_fused_noalloc(q, k, v, block_table, seq_lens, page_table, page_cnt, o
         int(page_table.shape[2]), _lib.ptr(page_cnt), page_cnt.stride(0), _lib.ptr(seq_lens),
         _lib.ptr(out), out.stride(0), out.stride(1), 1 if out.dtype == torch.float32 else 0,
         int(n_req), int(n_kv), int(G), int(d), int(page), int(split), int(pps_min),
-        float(scale), _lib.stream_ptr(q.device)), "decode_fused_noalloc")
+        int(max_cnt), float(scale), _lib.stream_ptr(q.device)), "decode_fused_noalloc")
 
 
 def decode_merge(m_part, l_part, acc_part, page_cnt, out, *, n_req: int, n_kv: int, G: int,
-                 split: int, pps_min: int, pt_cols: int) -> None:
+                 split: int, pps_min: int, pt_cols: int, max_cnt: int = 0) -> None:
     """LSE merge of the split partials into ``out``; ``pt_cols`` is the page
     table width the split kernel was given (page_cnt is clamped to it)."""
     _check_out(out)
@@ -166,7 +175,8 @@ def decode_merge(m_part, l_part, acc_part, page_cnt, out, *, n_req: int, n_kv: i
         _lib.ptr(m_part), _lib.ptr(l_part), _lib.ptr(acc_part), _lib.ptr(page_cnt),
         page_cnt.stride(0), int(pt_cols), _lib.ptr(out), out.stride(0), out.stride(1),
         1 if out.dtype == torch.float32 else 0, int(n_req), int(n_kv), int(G),
-        int(acc_part.shape[-1]), int(split), int(pps_min), _lib.stream_ptr(out.device)),
+        int(acc_part.shape[-1]), int(split), int(pps_min), int(max_cnt),
+        _lib.stream_ptr(out.device)),
         "decode_merge")
 
 
@@ -191,8 +201,9 @@ def decode_dense(q, k, v, block_table, seq_lens, m_part, l_part, acc_part, out, 
 
 def sparse_paged_decode_batched(q, kv_cache, block_table, seq_lens, st, out,
                                 vsource=None, *, scale: float = None) -> None:
-    """Batched Stage B (decode.py:328-387): one fixed-shape launch (the
-    split kernel whose last split per row merges it), or split + merge."""
+    """Batched Stage B (decode.py:328-387): the split kernel + the
+    head-parallel merge, or (FUSED_MERGE) one launch whose last split per row
+    merges it."""
     if scale is None:
         scale = st.scale
     n_req = seq_lens.shape[0]
@@ -203,14 +214,22 @@ def sparse_paged_decode_batched(q, kv_cache, block_table, seq_lens, st, out,
         raise NotImplementedError("only the resident V source exists in this build")
     v = vsource.args()[0]
     pps = _pps_min(n_req, st.n_kv)
+    mc = page_cnt_bound(st)
     if FUSED_MERGE:
         decode_fused(q, k, v, block_table, seq_lens, st.page_table, st.page_cnt, st.m_part,
                      st.l_part, st.acc_part, st.dec_counters, out, n_req=n_req, G=st.G,
-                     split=st.split, pps_min=pps, scale=scale)
+                     split=st.split, pps_min=pps, scale=scale, max_cnt=mc)
         return
     decode_splitk(q, k, v, block_table, seq_lens, st.page_table, st.page_cnt, st.m_part,
                   st.l_part, st.acc_part, n_req=n_req, G=st.G, split=st.split,
-                  pps_min=pps, scale=scale)
+                  pps_min=pps, scale=scale, max_cnt=mc)
     decode_merge(st.m_part, st.l_part, st.acc_part, st.page_cnt, out, n_req=n_req,
                  n_kv=st.n_kv, G=st.G, split=st.split, pps_min=pps,
-                 pt_cols=st.page_table.shape[2])
+                 pt_cols=st.page_table.shape[2], max_cnt=mc)
+
+
+def page_cnt_bound(st) -> int:
+    """Upper bound of any row's page_cnt under the state's budget: b_max
+    selected pages plus the sink and window pages (a keep-all row has at most
+    sink + 1 + window pages, and b >= 1).  Sizes the decode grid."""
+    return int(st.b_max) + int(st.sink_pages) + int(st.window_pages)

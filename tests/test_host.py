@@ -76,7 +76,7 @@ def test_rejects_bad_geometry_without_device():
     rc = lib.locks_score_rki4(*args)           # head_dim 64 is outside the contract
     assert rc == -1 and b"head_dim 64" in lib.locks_last_error()
     rc = lib.locks_decode_splitk(*([1, 8, 8] + [1, 8, 8, 8] * 2 + [1, 1, 8, 1, 1, 8, 8, 1, 1,
-                                   8, 1, 1, 1, 1, 1, 2, 17, 128, 16, 4, 1, 0.1, None]))
+                                   8, 1, 1, 1, 1, 1, 2, 17, 128, 16, 4, 1, 0, 0.1, None]))
     assert rc == -1 and b"G=17" in lib.locks_last_error()
     # two chunks (max_pages 4096) need the candidate workspace: rejected pre-launch
     rc = lib.locks_select_nrm_topb(*([1, 1, 1] + [1] * 7 + [0, 1, 2, 4, 1, 4096, 0, 0, None]))

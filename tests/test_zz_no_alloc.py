@@ -39,7 +39,7 @@ def _pair(case, d, split, pps_min, dtype):
     mp = torch.empty(R, n_kv, split, G, device="cuda")
     lp = torch.empty_like(mp)
     ap = torch.empty(R, n_kv, split, G, 128, device="cuda")
-    ctr = torch.zeros(R, n_kv, dtype=torch.int32, device="cuda")
+    ctr = torch.zeros(R, n_kv, D.COUNTER_STRIDE, dtype=torch.int32, device="cuda")
     ref = torch.full((R, n_kv * G, 128), float("nan"), dtype=dtype, device="cuda")
     out = torch.full_like(ref, float("nan"))
     D.decode_fused(d["q"], k, v, d["bt"], d["sl"], d["tab"], d["cnt"], mp, lp, ap, ctr, ref,
