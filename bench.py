@@ -128,13 +128,15 @@ def sparse_step(m, out):
 
 
 def dense_split(m, split=0):
-    """Dense comparator split count: about two workgroups per CU over the
-    (request, kv head) rows (the dense kernel holds one per CU: 128 KB of
-    page stages)."""
+    """Dense comparator split count (the dense kernel holds two workgroups
+    per CU).  Measured on MI355X: 512 workgroups for the 2-row GLM 1M step
+    (split 256: 5.97 TB/s; 512: 5.62), 1024 for the 8-row Llama 128K step
+    (split 128 beat 64)."""
     if split:
         return int(split)
     rows = m["R"] * m["n_kv"]
-    return max(1, min(512, -(-512 // rows)))
+    target = 512 if rows <= 2 else 1024
+    return max(1, min(512, -(-target // rows)))
 
 
 def make_dense(m, split=0):

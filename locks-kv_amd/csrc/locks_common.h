@@ -12,6 +12,16 @@ namespace locks {
 
 constexpr int kWave = 64;
 
+// Workgroup barrier that orders LDS only: each wave waits for its own LDS
+// accesses, not for its outstanding global stores (__syncthreads() also
+// waits vmcnt(0) on gfx950, which stalls a barrier behind stores that no
+// other thread of the workgroup reads).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));

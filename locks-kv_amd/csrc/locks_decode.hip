@@ -41,7 +41,11 @@ constexpr int DC_PAGE_BYTES = 8192;       // K + V of one (page, kv head)
 typedef __attribute__((address_space(3))) void* lds_ptr;
 typedef __attribute__((address_space(3))) const uint8_t* lds_u8_ptr;
 constexpr int MAX_SPLIT = 512;
-constexpr int DENSE_NST = 4;           // page stages per wave of the dense comparator
+constexpr int DENSE_NST = 2;           // page stages per wave of the dense comparator
+// K/V DMA cache policy: NT (non-temporal: every page is read once) measured
+// 5.58 -> 5.97 TB/s for the dense comparator at 1M (SC1 did not help); the
+// sparse decode measured the same step time with and without it.
+constexpr int CPOL_NT = 2;
 
 __device__ __forceinline__ uint32_t bf16_word(const uint4& w, int e) {
     const uint32_t x = (e >> 1) == 0 ? w.x : (e >> 1) == 1 ? w.y : (e >> 1) == 2 ? w.z : w.w;
@@ -227,7 +231,8 @@ __device__ void merge_row(const float* __restrict__ m_part, const float* __restr
 // partial.
 // DENSE: every page of the row in logical order (page count from seq_len,
 // no page table) -- the dense full-KV comparator.  NST: page stages per
-// wave (NST - 1 pages in flight while one is consumed).
+// wave (NST - 1 pages in flight while one is consumed).  KVPOL: cache policy
+// bits of the K/V page DMA.
 template <int NST>
 __device__ __forceinline__ void wait_vm_pages(int ahead) {
     // vmcnt(8 * ahead) with lgkmcnt(0); vmcnt is bits [3:0] + [15:14]
@@ -242,7 +247,7 @@ __device__ __forceinline__ void wait_vm_pages(int ahead) {
     }
 }
 
-template <bool FUSED, bool DENSE = false, int NST = 2>
+template <bool FUSED, bool DENSE = false, int NST = 2, int KVPOL = 0>
 __global__ __launch_bounds__(DC_BLK) void decode_split_kernel(
     const uint16_t* __restrict__ q, long q_sr, long q_sh,
     const uint16_t* __restrict__ kc, long k_sb, long k_st, long k_sh,
@@ -336,10 +341,10 @@ __global__ __launch_bounds__(DC_BLK) void decode_split_kernel(
         const uint16_t* vp = vc + (long)blk * v_sb + (long)kh * v_sh + 8 * c16;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            __builtin_amdgcn_global_load_lds(kp + 32 * i, (lds_ptr)(st + i * 1024), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(kp + 32 * i, (lds_ptr)(st + i * 1024), 16, 0, KVPOL);
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            __builtin_amdgcn_global_load_lds(vp + (long)(4 * kg + i) * v_st, (lds_ptr)(st + 4096 + i * 1024), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(vp + (long)(4 * kg + i) * v_st, (lds_ptr)(st + 4096 + i * 1024), 16, 0, KVPOL);
         return pt;
     };
 
@@ -751,7 +756,7 @@ extern "C" int32_t locks_decode_dense(
                   "locks_decode_dense: null pointer argument");
     if (n_req == 0) return 0;
     hipStream_t st = (hipStream_t)stream;
-    hipLaunchKernelGGL((decode_split_kernel<false, true, DENSE_NST>), dim3(split, n_kv, n_req), dim3(DC_BLK),
+    hipLaunchKernelGGL((decode_split_kernel<false, true, DENSE_NST, CPOL_NT>), dim3(split, n_kv, n_req), dim3(DC_BLK),
                        0, st, q, (long)q_stride_req, (long)q_stride_head, k_cache,
                        (long)k_stride_block, (long)k_stride_tok, (long)k_stride_head, v_cache,
                        (long)v_stride_block, (long)v_stride_tok, (long)v_stride_head, num_blocks,

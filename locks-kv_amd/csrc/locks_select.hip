@@ -51,17 +51,17 @@ __device__ __forceinline__ int block_excl_scan(int v, int* wsum, int& total) {
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int incl = wave_incl_scan_i(v);
     if (lane == kWave - 1) wsum[w] = incl;
-    __syncthreads();
+    lds_barrier();
     if (w == 0) {
         const int x = (lane < NW) ? wsum[lane] : 0;
         const int xi = wave_incl_scan_i(x);
         if (lane < NW) wsum[lane] = xi - x;
         if (lane == NW - 1) wsum[NW] = xi;
     }
-    __syncthreads();
+    lds_barrier();
     const int res = wsum[w] + incl - v;
     total = wsum[NW];
-    __syncthreads();
+    lds_barrier();
     return res;
 }
 
@@ -90,7 +90,7 @@ __device__ uint32_t block_kth_largest(const uint32_t* keys, int n, int k, int* h
     for (int digit = 0; digit < 4; ++digit) {
         const int shift = 24 - 8 * digit;
         for (int i = tid; i < 256; i += BLK) hist[i] = 0;
-        __syncthreads();
+        lds_barrier();
         // 16 keys per thread in flight per batch (keys may live in global
         // memory: a key-at-a-time loop would serialize one latency per key)
         for (int i0 = tid; i0 < n; i0 += 16 * BLK) {
@@ -104,7 +104,7 @@ __device__ uint32_t block_kth_largest(const uint32_t* keys, int n, int k, int* h
             for (int j = 0; j < 16; ++j)
                 hist_add(hist, (u[j] >> shift) & 0xFF, (i0 + j * BLK < n) && (u[j] & kmask) == prefix);
         }
-        __syncthreads();
+        lds_barrier();
         if (tid < kWave) {
             const int lane = tid;
             const int seg = hist[4 * lane] + hist[4 * lane + 1] + hist[4 * lane + 2] + hist[4 * lane + 3];
@@ -127,12 +127,12 @@ __device__ uint32_t block_kth_largest(const uint32_t* keys, int n, int k, int* h
                 s3[2] = cb;
             }
         }
-        __syncthreads();
+        lds_barrier();
         prefix |= ((uint32_t)s3[0]) << shift;
         k = s3[1];
         const int cb = s3[2];
         kmask |= 0xFFu << shift;
-        __syncthreads();
+        lds_barrier();
         if (k == cb) break;
     }
     return prefix;
@@ -238,7 +238,7 @@ __device__ void finish_row(long rk, int n_pages, int n_sel_hi, int n_sink, int b
             run += tot;
         }
         if (tid == 0) offs[Z1] = run;
-        __syncthreads();
+        lds_barrier();
     }
     const int N = offs[Z1];
     uint32_t* kk = (N <= cap) ? lkey : spill_key + rk * (long)MP;
@@ -263,7 +263,7 @@ __device__ void finish_row(long rk, int n_pages, int n_sel_hi, int n_sink, int b
             }
         }
     }
-    __syncthreads();
+    __syncthreads();                    // candidates may be in global spill memory
     const uint32_t tau = block_kth_largest<BLK>(kk, N, b, hist, s3);
     const int nsel_w = emit_topk<BLK>(kk, N, b, tau, [&](int i) { return pp[i]; },
                                       trow + n_sink, nullptr, wsum);
@@ -297,12 +297,12 @@ __device__ RadixSel reg_kth_largest(const uint32_t (&key)[E], const bool (&val)[
         const int shift = pass == 0 ? 20 : pass == 1 ? 8 : 0;
         const int nb = pass < 2 ? 4096 : 256;
         for (int i = tid; i < nb; i += BLK) hist[i] = 0;
-        __syncthreads();
+        lds_barrier();
 #pragma unroll
         for (int e = 0; e < E; ++e)
             hist_add(hist, (int)((key[e] >> shift) & (uint32_t)(nb - 1)),
                      val[e] && (key[e] & rs.kmask) == rs.prefix);
-        __syncthreads();
+        lds_barrier();
         // thread t: bins top .. top-BPL+1, top = nb-1-BPL*t (ascending thread
         // order = descending bin order)
         const int top = nb - 1 - BPL * tid;
@@ -311,7 +311,7 @@ __device__ RadixSel reg_kth_largest(const uint32_t (&key)[E], const bool (&val)[
         for (int j = 0; j < BPL; ++j) c += (top - j >= 0) ? hist[top - j] : 0;
         const int incl = wave_incl_scan_i(c);
         if (lane == kWave - 1) wtot[wave] = incl;
-        __syncthreads();
+        lds_barrier();
         // counts of the waves before this one: one parallel LDS read and a
         // wave sum (a serial loop would chain up to NW - 1 LDS latencies)
         const int base = wave_sum_i((lane < wave) ? wtot[lane] : 0);
@@ -325,7 +325,7 @@ __device__ RadixSel reg_kth_largest(const uint32_t (&key)[E], const bool (&val)[
                 above += cb;
             }
         }
-        __syncthreads();
+        lds_barrier();
         rs.prefix |= ((uint32_t)s3[0]) << shift;
         rs.kmask |= ((uint32_t)(nb - 1)) << shift;
         const int cb = s3[2];
@@ -432,7 +432,7 @@ __global__ __launch_bounds__(ROW_BLK) void sel_row_kernel(
             m = wave_max(m);
             if (lane == 0) hm[wave] = m;
         }
-        __syncthreads();
+        lds_barrier();
     }
     float acc[E];
 #pragma unroll
@@ -561,7 +561,7 @@ __global__ __launch_bounds__(SEL_BLK) void sel_chunk_kernel(
             m = wave_max(m);
             if (lane == 0) hm[g] = m;
         }
-        __syncthreads();
+        lds_barrier();
     }
 
     // ---- combine: score[p] for p < nsh, keys for the selectable slice ----
@@ -584,7 +584,7 @@ __global__ __launch_bounds__(SEL_BLK) void sel_chunk_kernel(
         score[rk * (long)MP + p] = acc;
         keys[p - c0] = f2u(acc);
     }
-    __syncthreads();
+    lds_barrier();
 
     const int lo_c = min(max(n_sink, c0), c1) - c0;       // selectable slice of
     const int hi_c = max(min(n_sel_hi, c1), c0) - c0;     // this chunk, local idx
@@ -716,7 +716,7 @@ __global__ __launch_bounds__(C2_BLK) void sel_chunk2_kernel(
             const float m = wave_max(chunk_max(pmax + rk * Zs * 16 + g, Zs));
             if (lane == 0) hm[g] = m;
         }
-        __syncthreads();
+        lds_barrier();
     }
     float acc[C2_E];
 #pragma unroll
@@ -756,10 +756,10 @@ __global__ __launch_bounds__(C2_BLK) void sel_chunk2_kernel(
     }
     if constexpr (BAND) {
         for (int i = tid; i < 4096; i += C2_BLK) hist[i] = 0;
-        __syncthreads();
+        lds_barrier();
 #pragma unroll
         for (int e = 0; e < C2_E; ++e) hist_add(hist, (int)(key[e] >> 20), val[e]);
-        __syncthreads();
+        lds_barrier();
         int* gh = ghist + rk * 4096;
         for (int i = tid; i < 4096; i += C2_BLK)
             if (hist[i]) __hip_atomic_fetch_add(gh + i, hist[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -866,7 +866,7 @@ __global__ __launch_bounds__(C2_BLK) void sel_band_kernel(
     for (int j = 0; j < BPT; ++j) { hb[j] = gh[top - j]; c += hb[j]; }
     const int incl = wave_incl_scan_i(c);
     if (lane == kWave - 1) wtot[wave] = incl;
-    __syncthreads();
+    lds_barrier();
     const int base = wave_sum_i((lane < wave) ? wtot[lane] : 0);
     const int above0 = base + incl - c;
     if (c > 0 && above0 < b && b <= base + incl) {
@@ -877,7 +877,7 @@ __global__ __launch_bounds__(C2_BLK) void sel_band_kernel(
             above += hb[j];
         }
     }
-    __syncthreads();
+    lds_barrier();
     const uint32_t T = (uint32_t)tbin;
     const int p0 = z * SEL_CH + C2_E * tid;
     uint32_t key[C2_E];
@@ -964,7 +964,7 @@ __global__ __launch_bounds__(F2_BLK) void sel_finish2_kernel(
         const int ex = block_excl_scan<F2_BLK>(c, wsum, tot);
         if (tid < Z1) offs[tid] = ex;
         if (tid == 0) offs[Z1] = tot;
-        __syncthreads();
+        lds_barrier();
     }
     const int N = offs[Z1];
     if (N > F2_CAP) {                   // more candidates than registers: global spill
