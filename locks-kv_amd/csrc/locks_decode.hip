@@ -536,6 +536,7 @@ __global__ __launch_bounds__(DC_BLK) void decode_split_kernel(
 // page count is page_cnt (clamped to pt_cols, as the split kernel) or, with
 // pcnt == nullptr, the dense one (every page of the row).
 constexpr int MH_BLK = 256, MH_STREAMS = MH_BLK / 32;
+constexpr int MH_PF = 8;                   // partials prefetched per thread (64 splits)
 __global__ __launch_bounds__(MH_BLK) void decode_merge_heads_kernel(
     const float* __restrict__ m_part, const float* __restrict__ l_part,
     const float* __restrict__ acc_part, const int* __restrict__ pcnt, long cnt_sr, int pt_cols,
@@ -547,28 +548,44 @@ __global__ __launch_bounds__(MH_BLK) void decode_merge_heads_kernel(
     const int n_kv = gridDim.y;
     const long rk = (long)r * n_kv + kh;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int cnt = pcnt ? min(pcnt[(long)r * cnt_sr + kh], pt_cols)
-                         : min(cdiv(seq_lens[r], DC_PG), bt_cols);
+    const int col = tid & 31, strm = tid >> 5;
+    // Every load is issued before anything waits: the page count, this
+    // thread's (split, m, l) and its first MH_PF partial columns, at split
+    // indices clamped into the buffers (entries past the active count are
+    // masked below, never combined), so the merge costs one round trip.
+    const int cnt_raw = pcnt ? pcnt[(long)r * cnt_sr + kh] : seq_lens[r];
+    float4 pre[MH_PF];
+#pragma unroll
+    for (int k = 0; k < MH_PF; ++k) {
+        const int sidx = min(strm + k * MH_STREAMS, split - 1);
+        pre[k] = *reinterpret_cast<const float4*>(acc_part + ((rk * split + sidx) * G + g) * DC_D + col * 4);
+    }
+    const long ml0 = (rk * split + min(tid, split - 1)) * G + g;
+    const float m0 = m_part[ml0], l0 = l_part[ml0];
+    const int cnt = pcnt ? min(cnt_raw, pt_cols) : min(cdiv(cnt_raw, DC_PG), bt_cols);
     const int pps = max(cdiv(cnt, nsplit), pps_min);
     const int n_act = cnt > 0 ? min(cdiv(cnt, pps), nsplit) : 0;
     __shared__ float w_s[MAX_SPLIT];
     __shared__ float red[MH_BLK / kWave];
     __shared__ float4 part[MH_STREAMS][32];
     // head max over the splits that hold mass
-    float mm = -INFINITY;
-    for (int s = tid; s < n_act; s += MH_BLK) {
+    const bool has0 = tid < n_act && l0 > 0.f;
+    float mm = has0 ? m0 : -INFINITY;
+    for (int s = tid + MH_BLK; s < n_act; s += MH_BLK) {   // rows of more than MH_BLK splits
         const long i = (rk * split + s) * G + g;
         if (l_part[i] > 0.f) mm = fmaxf(mm, m_part[i]);
     }
     mm = wave_max(mm);
     if (lane == 0) red[wave] = mm;
-    __syncthreads();
+    lds_barrier();
     mm = red[0];
 #pragma unroll
     for (int w = 1; w < MH_BLK / kWave; ++w) mm = fmaxf(mm, red[w]);
-    __syncthreads();
-    float lt = 0.f;
-    for (int s = tid; s < n_act; s += MH_BLK) {
+    lds_barrier();
+    const float w0 = has0 ? __expf(m0 - mm) : 0.f;
+    if (tid < n_act) w_s[tid] = w0;
+    float lt = has0 ? l0 * w0 : 0.f;
+    for (int s = tid + MH_BLK; s < n_act; s += MH_BLK) {
         const long i = (rk * split + s) * G + g;
         const float l = l_part[i];
         const float w = (l > 0.f) ? __expf(m_part[i] - mm) : 0.f;
@@ -577,20 +594,27 @@ __global__ __launch_bounds__(MH_BLK) void decode_merge_heads_kernel(
     }
     lt = wave_sum(lt);
     if (lane == 0) red[wave] = lt;
-    __syncthreads();
+    lds_barrier();
     lt = 0.f;
 #pragma unroll
     for (int w = 0; w < MH_BLK / kWave; ++w) lt += red[w];
-    const int col = tid & 31, strm = tid >> 5;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int k = 0; k < MH_PF; ++k) {
+        const int sidx = strm + k * MH_STREAMS;
+        if (sidx < n_act) {
+            const float w = w_s[sidx];
+            acc.x += w * pre[k].x; acc.y += w * pre[k].y; acc.z += w * pre[k].z; acc.w += w * pre[k].w;
+        }
+    }
 #pragma unroll 4
-    for (int s = strm; s < n_act; s += MH_STREAMS) {
+    for (int s = strm + MH_PF * MH_STREAMS; s < n_act; s += MH_STREAMS) {
         const float w = w_s[s];
         const float4 a = *reinterpret_cast<const float4*>(acc_part + ((rk * split + s) * G + g) * DC_D + col * 4);
         acc.x += w * a.x; acc.y += w * a.y; acc.z += w * a.z; acc.w += w * a.w;
     }
     part[strm][col] = acc;
-    __syncthreads();
+    lds_barrier();
     if (tid < 32) {
         float4 t = part[0][col];
 #pragma unroll

@@ -521,21 +521,28 @@ __global__ __launch_bounds__(MG_BLK) void mla_merge_kernel(
         pre[k] = (s < split) ? *reinterpret_cast<const float4*>(acc_part + ((rb + s) * ML_H + h) * ML_D + d0)
                              : make_float4(0.f, 0.f, 0.f, 0.f);
     }
+    // this thread's split (m, l) in the same round trip (clamped index;
+    // masked by the active count below)
+    const long ml0 = (rb + min(tid, split - 1)) * ML_H + h;
+    const float m0 = m_part[ml0], l0 = l_part[ml0];
+    const bool has0 = tid < n_act && l0 > 0.f;
     // M = max over live splits; weights; L = sum w l (fixed reduction tree)
-    float mx = -INFINITY;
-    for (int s = tid; s < n_act; s += MG_BLK) {
+    float mx = has0 ? m0 : -INFINITY;
+    for (int s = tid + MG_BLK; s < n_act; s += MG_BLK) {
         const long i = (rb + s) * ML_H + h;
         if (l_part[i] > 0.f) mx = fmaxf(mx, m_part[i]);
     }
     mx = wave_max(mx);
     if (lane == 0) red[wave] = mx;
-    __syncthreads();
+    lds_barrier();
     float M = red[0];
 #pragma unroll
     for (int w = 1; w < MG_BLK / kWave; ++w) M = fmaxf(M, red[w]);
-    __syncthreads();
-    float lp = 0.f;
-    for (int s = tid; s < n_act; s += MG_BLK) {
+    lds_barrier();
+    const float w0 = has0 ? __expf(m0 - M) : 0.f;
+    if (tid < n_act) w_s[tid] = w0;
+    float lp = has0 ? w0 * l0 : 0.f;
+    for (int s = tid + MG_BLK; s < n_act; s += MG_BLK) {
         const long i = (rb + s) * ML_H + h;
         const float l = l_part[i];
         const float w = (l > 0.f) ? __expf(m_part[i] - M) : 0.f;
@@ -545,7 +552,7 @@ __global__ __launch_bounds__(MG_BLK) void mla_merge_kernel(
     lp += row_ror<8>(lp); lp += row_ror<4>(lp); lp += row_ror<2>(lp); lp += row_ror<1>(lp);
     lp = xor32_sum(xor16_sum(lp));
     if (lane == 0) red[wave] = lp;
-    __syncthreads();
+    lds_barrier();
     float L = 0.f;
 #pragma unroll
     for (int w = 0; w < MG_BLK / kWave; ++w) L += red[w];
@@ -579,7 +586,7 @@ __global__ __launch_bounds__(MG_BLK) void mla_merge_kernel(
         acc.x += w * a.x; acc.y += w * a.y; acc.z += w * a.z; acc.w += w * a.w;
     }
     part[g][c] = acc;
-    __syncthreads();
+    lds_barrier();
     if (g == 0) {
         float4 o = part[0][c];
 #pragma unroll
