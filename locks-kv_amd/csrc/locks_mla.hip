@@ -59,6 +59,13 @@ __device__ __forceinline__ v4i perm_even_odd(const uint4 n) {
                (int)__builtin_amdgcn_perm(n.y, n.x, 0x07050301u), (int)__builtin_amdgcn_perm(n.w, n.z, 0x07050301u)};
 }
 
+// 16-byte non-temporal load (global_load_dwordx4 ... nt)
+__device__ __forceinline__ uint4 ld_nt16(const void* p) {
+    typedef unsigned v4u __attribute__((ext_vector_type(4)));
+    const v4u x = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p));
+    return make_uint4(x.x, x.y, x.z, x.w);
+}
+
 // ---------------------------------------------------------------------------
 // latent page scorer: grid (chunks, requests), 4 waves; unit = 2 pages
 // ---------------------------------------------------------------------------
@@ -116,16 +123,19 @@ __global__ __launch_bounds__(ML_BLK) void mla_score_kernel(
         const int last = c1 - c0 - 1;
         auto blk_of = [&](int pg) -> long { return (long)bt_l[min(p0 + pg, last)]; };
         // 16-byte chunk i = lane + 64 m of the 2 V rows
-        auto vload = [&](int i) { return *reinterpret_cast<const uint4*>(v4 + blk_of(i >> 7) * ML_VROW + (i & 127) * 16); };
+        // Rows read once by this workgroup (packed V, centroid, coefficients,
+        // RoPE keys) load non-temporally; the small scale rows, whose cache
+        // lines neighbouring blocks share, with the default policy.
+        auto vload = [&](int i) { return ld_nt16(v4 + blk_of(i >> 7) * ML_VROW + (i & 127) * 16); };
         fv0 = vload(lane); fv1 = vload(lane + 64); fv2 = vload(lane + 128); fv3 = vload(lane + 192);
-        fmu = *reinterpret_cast<const uint4*>(mu8 + blk_of(lane >> 5) * ML_D + (lane & 31) * 16);
-        fc8 = *reinterpret_cast<const uint4*>(c8 + blk_of((lane >> 3) & 1) * (ML_PG * ML_RNK) + (lane & 7) * 16);
+        fmu = ld_nt16(mu8 + blk_of(lane >> 5) * ML_D + (lane & 31) * 16);
+        fc8 = ld_nt16(c8 + blk_of((lane >> 3) & 1) * (ML_PG * ML_RNK) + (lane & 7) * 16);
         fcs = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(cs) + blk_of((lane >> 1) & 1) * (ML_PG * 2) + (lane & 1) * 16);
         fvs = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(vs) + blk_of(lane & 1) * (ML_RNK * 2));
         fmus = (uint32_t)mus[blk_of(lane & 1)];
         // RoPE chunk i = (page i >> 7, token (i >> 3) & 15, 16-byte part i & 7)
         auto rload = [&](int i) {
-            return *reinterpret_cast<const uint4*>(cache + blk_of(i >> 7) * c_sb + (long)((i >> 3) & 15) * c_st + ML_D + 8 * (i & 7));
+            return ld_nt16(cache + blk_of(i >> 7) * c_sb + (long)((i >> 3) & 15) * c_st + ML_D + 8 * (i & 7));
         };
         fr0 = rload(lane); fr1 = rload(lane + 64); fr2 = rload(lane + 128); fr3 = rload(lane + 192);
     };
