@@ -14,12 +14,13 @@
  *   - return 0 on success, <0 on a rejected argument (-1) or a failed launch
  *     (-2); locks_last_error() then describes the failure (thread-local).
  *
- * Geometry contract of this build: head_dim 128, page 16, summary rank 8,
- * int4 basis, 1 <= G <= 16 query heads per kv head; MLA: kv_lora_rank 512 +
- * 64 RoPE dims, <= 16 query heads.  (The reference's rki4
- * state asserts d in {64,128,256}, page in {16,32,64}, G <= 8:
- * src/locks/selection/rki4_state.py:288-334; G up to 16 is needed by the
- * GLM-4-9B 32q/2kv geometry.)
+ * Geometry contract of this build: summary rank 8, int4 basis, 1 <= G <= 16
+ * query heads per kv head; the decode entries (split, fused, merge, dense)
+ * take head_dim in {64, 128, 256} and page in {16, 32, 64}, the reference's
+ * domain (src/locks/selection/rki4_state.py:288-334: d in {64,128,256},
+ * page in {16,32,64}, G <= 8; G up to 16 is needed by the GLM-4-9B
+ * 32q/2kv geometry); the summary entries (build, score) head_dim 128 and
+ * page 16; MLA: kv_lora_rank 512 + 64 RoPE dims, <= 16 query heads.
  *
  * Reference interfaces each entry replaces (paths under src/locks/):
  */
@@ -138,7 +139,9 @@ int32_t locks_select_nrm_topb(const float* score_h, const float* page_max, int32
  *   k_cache / v_cache: element strides of (block, token, kv head); d contiguous
  *   (vLLM kv_cache (NB, 2, page, n_kv, d) halves, attention/decode.py:64-73)
  *   page_table (n_req, n_kv, pt_cols) i32; page_cnt (n_req, n_kv) i32
- *   m_part, l_part (n_req, n_kv, split, G) f32; acc_part (..., G, 128) f32
+ *   m_part, l_part (n_req, n_kv, split, G) f32; acc_part (..., G, head_dim) f32
+ *   head_dim 64 / 128 / 256; page 16 / 32 / 64 tokens (a page runs as
+ *   page / 16 steps of 16 tokens)
  *   max_cnt: the caller's upper bound of page_cnt (b_max + sink + window
  *   for a selection; 0 = none).  min(split, ceil(max_cnt / pps_min)) splits
  *   are launched ("nsplit"); pps = max(ceil(cnt / nsplit), pps_min), so a
@@ -163,7 +166,7 @@ int32_t locks_decode_splitk(const uint16_t* q, int64_t q_stride_req, int64_t q_s
  * Replaces merge_splits_kernel (attention/merge.py:105-152).  One workgroup
  * per (request, kv head, query head), so a row's partials are read by G
  * CUs in parallel.
- *   out (n_req, n_kv*G, 128) bf16 (out_is_f32 = 0) or f32 (out_is_f32 = 1),
+ *   out (n_req, n_kv*G, head_dim) bf16 (out_is_f32 = 0) or f32 (out_is_f32 = 1),
  *   strides (out_stride_req, out_stride_head, 1), multiples of 4 elements;
  *   rows with page_cnt 0 get 0.
  *   pt_cols, max_cnt: as given to locks_decode_splitk (page_cnt is clamped
@@ -216,7 +219,7 @@ int32_t locks_decode_fused(const uint16_t* q, int64_t q_stride_req, int64_t q_st
  * LOCKS_NOALLOC_SCRATCH_BYTES (one copy per GPU, held until the process
  * ends), laid out as the arrival counters (n_req * n_kv *
  * LOCKS_DECODE_COUNTER_STRIDE i32) followed by the m, l (n_req * n_kv * split * G f32 each) and acc
- * (n_req * n_kv * split * G * 128 f32) partials.  Calls needing more scratch
+ * (n_req * n_kv * split * G * head_dim f32) partials.  Calls needing more scratch
  * fail with -1 and a message.  Each call clears the counters (a fill kernel)
  * and launches the fused decode; nothing is allocated or freed.  Every call
  * on one GPU shares the array, so calls that overlap on one GPU (other
@@ -248,7 +251,7 @@ int32_t locks_decode_fused_noalloc(const uint16_t* q, int64_t q_stride_req, int6
  * Two launches: the split kernel in its dense form (page ids implicit, four
  * page stages per wave) writes the split partials, then one merge workgroup
  * per query head folds them.  Argument meanings as locks_decode_splitk and
- * locks_decode_merge; the partial buffers hold (n_req, n_kv, split, G[, 128]).
+ * locks_decode_merge; the partial buffers hold (n_req, n_kv, split, G[, head_dim]).
  */
 int32_t locks_decode_dense(const uint16_t* q, int64_t q_stride_req, int64_t q_stride_head,
                            const uint16_t* k_cache, int64_t k_stride_block, int64_t k_stride_tok,

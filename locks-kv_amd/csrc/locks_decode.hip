@@ -33,13 +33,12 @@
 
 namespace locks {
 
-constexpr int DC_D = 128;
 constexpr int DC_PG = 16;
 constexpr int DC_WAVES = 4;
 constexpr int DC_BLK = DC_WAVES * kWave;
-constexpr int DC_PAGE_BYTES = 8192;       // K + V of one (page, kv head)
 typedef __attribute__((address_space(3))) void* lds_ptr;
 typedef __attribute__((address_space(3))) const uint8_t* lds_u8_ptr;
+typedef int v2i __attribute__((ext_vector_type(2)));
 constexpr int MAX_SPLIT = 512;
 constexpr int DENSE_NST = 2;           // page stages per wave of the dense comparator
 // K/V DMA cache policy: NT (non-temporal: every page is read once) measured
@@ -78,27 +77,28 @@ __device__ __forceinline__ float ld_part(const float* base, long idx) {
 
 // Merge the first n_act split partials of row rk into out (one workgroup,
 // DC_BLK threads).  w_s, l_s: >= MAX_SPLIT * 16 floats of LDS each.
-// Work split: the row's G * 32 float4 output columns ("items") times `grp`
-// split streams fill the workgroup (G <= 8; G > 8: two items per thread).
+// Work split: the row's G * D / 4 float4 output columns ("items") times
+// `grp` split streams fill the workgroup (at most two items per thread).
 // Every thread issues the loads of its first MR_PF splits' partials before
 // anything waits, together with the m / l loads, so a row of up to
 // grp * MR_PF splits costs one memory round trip; the streams are summed in
 // LDS at the end.
 constexpr int MR_PF = 16;
-template <bool COHERENT = false>
+template <bool COHERENT = false, int D = 128>
 __device__ void merge_row(const float* __restrict__ m_part, const float* __restrict__ l_part,
                           const float* __restrict__ acc_part, long rk, int r, int kh, int n_act,
                           int G, int split, void* __restrict__ out, long o_sr, long o_sh,
                           int out_f32, float* w_s, float* l_s, float* lt_s) {
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     constexpr int NWV = DC_BLK / kWave;
-    const int n_items = G * (DC_D / 4);
+    constexpr int CPR = D / 4;                          // float4 columns per head
+    const int n_items = G * CPR;
     const int grp = n_items >= DC_BLK ? 1 : DC_BLK / n_items;
     const int stream = n_items >= DC_BLK ? 0 : tid / n_items;
     const int item0 = n_items >= DC_BLK ? tid : tid % n_items;
     const bool two = n_items > DC_BLK;                  // G > 8: items tid and tid + DC_BLK
     const bool live = stream < grp;                     // threads past grp * n_items idle
-    // partial index of (item, split s): ((rk * split + s) * G + g) * 32 + c
+    // partial index of (item, split s): ((rk * split + s) * G + g) * CPR + c
     //   = rk * split * n_items + s * n_items + item
     const long rowbase = rk * split * (long)n_items;
     float4 pre[2][MR_PF];
@@ -158,7 +158,7 @@ __device__ void merge_row(const float* __restrict__ m_part, const float* __restr
 #pragma unroll
     for (int it = 0; it < 2; ++it) {
         const int item = min(item0 + it * DC_BLK, n_items - 1);
-        const int g = item >> 5;
+        const int g = item / CPR;
         float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
         for (int k = 0; k < MR_PF; ++k) {
@@ -205,7 +205,7 @@ __device__ void merge_row(const float* __restrict__ m_part, const float* __restr
             const float4 a = red[sg * n_items + item];
             acc.x += a.x; acc.y += a.y; acc.z += a.z; acc.w += a.w;
         }
-        const int g = item >> 5, d4 = (item & 31) * 4;
+        const int g = item / CPR, d4 = (item % CPR) * 4;
         const float lt = lt_s[g];
         const float inv = (lt > 0.f) ? 1.f / lt : 0.f;
         const float o[4] = {acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv};
@@ -221,33 +221,43 @@ __device__ void merge_row(const float* __restrict__ m_part, const float* __restr
     }
 }
 
-// One workgroup = 4 waves per split; wave w takes pages j0+w, j0+w+4, ...
-// Pages are DMA'd into per-wave LDS stages with global_load_lds_dwordx4 in
-// the exact lane order the MFMA operands need, so each lane later reads
-// back only the 16-byte slots it loaded itself (conflict-free, coalesced
-// 64/256-byte row segments in HBM) and in-flight pages cost no VGPRs; two
-// stages ping-pong so one page is always in flight while the other is
-// consumed.  The 4 wave states are then merged in LDS into the split's
-// partial.
-// DENSE: every page of the row in logical order (page count from seq_len,
-// no page table) -- the dense full-KV comparator.  NST: page stages per
-// wave (NST - 1 pages in flight while one is consumed).  KVPOL: cache policy
-// bits of the K/V page DMA.
-template <int NST>
-__device__ __forceinline__ void wait_vm_pages(int ahead) {
-    // vmcnt(8 * ahead) with lgkmcnt(0); vmcnt is bits [3:0] + [15:14]
+// Per-head_dim constants of the split kernel.  A step is 16 tokens of one
+// (page, kv head): K 16 x D and V 16 x D bf16 in one LDS stage.
+template <int D>
+struct DcGeom {
+    static_assert(D == 64 || D == 128 || D == 256, "head_dim 64, 128 or 256");
+    static constexpr int KS = D / 32;                   // QK k-slots: one 16-byte DMA per lane each
+    static constexpr int DPL = D / 16;                  // V columns per lane (PV output blocks)
+    static constexpr int VI = D == 64 ? 2 : 4 * (DPL / 8);   // V DMA instructions per step
+    static constexpr int NI = KS + VI;                  // DMA instructions per step
+    static constexpr int KBYTES = 16 * D * 2;
+    static constexpr int STEP_BYTES = 2 * KBYTES;
+};
+
+constexpr int vm_wait_imm(int n) {                       // s_waitcnt vmcnt(n) lgkmcnt(0)
+    return 0x0070 | (n & 15) | ((n >> 4) << 14);
+}
+template <int NI, int NST>
+__device__ __forceinline__ void wait_vm_steps(int ahead) {
+    // vmcnt(NI * ahead): the steps issued after the one to consume
     switch (ahead) {
-        case 0: __builtin_amdgcn_s_waitcnt(0x0070); break;
-        case 1: __builtin_amdgcn_s_waitcnt(0x0078); break;
-        case 2: if constexpr (NST > 2) __builtin_amdgcn_s_waitcnt(0x4070); break;
-        case 3: if constexpr (NST > 3) __builtin_amdgcn_s_waitcnt(0x4078); break;
-        case 4: if constexpr (NST > 4) __builtin_amdgcn_s_waitcnt(0x8070); break;
-        case 5: if constexpr (NST > 5) __builtin_amdgcn_s_waitcnt(0x8078); break;
-        default: if constexpr (NST > 6) __builtin_amdgcn_s_waitcnt(0xC070); break;
+        case 0: __builtin_amdgcn_s_waitcnt(vm_wait_imm(0)); break;
+        case 1: __builtin_amdgcn_s_waitcnt(vm_wait_imm(NI)); break;
+        case 2: if constexpr (NST > 2) __builtin_amdgcn_s_waitcnt(vm_wait_imm(2 * NI)); break;
+        default: if constexpr (NST > 3) __builtin_amdgcn_s_waitcnt(vm_wait_imm(3 * NI)); break;
     }
 }
 
-template <bool FUSED, bool DENSE = false, int NST = 2, int KVPOL = 0>
+// One workgroup = 4 waves per split; wave w takes the split's 16-token steps
+// s0+w, s0+w+4, ... (a page of PG tokens is PG/16 consecutive steps).
+// Steps are DMA'd into per-wave LDS stages with global_load_lds_dwordx4 in
+// the lane order the MFMA operands need, so in-flight steps cost no VGPRs;
+// NST stages form a ring (NST - 1 steps in flight while one is consumed).
+// The 4 wave states are then merged in LDS into the split's partial.
+// DENSE: every page of the row in logical order (page count from seq_len,
+// no page table) -- the dense full-KV comparator.  KVPOL: cache policy bits
+// of the K/V DMA.  pg_sh: log2(page / 16).
+template <bool FUSED, bool DENSE = false, int NST = 2, int KVPOL = 0, int D = 128>
 __global__ __launch_bounds__(DC_BLK) void decode_split_kernel(
     const uint16_t* __restrict__ q, long q_sr, long q_sh,
     const uint16_t* __restrict__ kc, long k_sb, long k_st, long k_sh,
@@ -256,24 +266,27 @@ __global__ __launch_bounds__(DC_BLK) void decode_split_kernel(
     const int* __restrict__ ptab, long pt_sr, long pt_sh, int pt_cols,
     const int* __restrict__ pcnt, long cnt_sr, const int* __restrict__ seq_lens,
     float* __restrict__ m_part, float* __restrict__ l_part, float* __restrict__ acc_part,
-    int G, int split, int pps_min, float sm_scale,
+    int G, int split, int pps_min, float sm_scale, int pg_sh,
     int* __restrict__ counters, void* __restrict__ out, long o_sr, long o_sh, int out_f32)
 {
+    using GM = DcGeom<D>;
+    constexpr int KS = GM::KS, DPL = GM::DPL, NI = GM::NI, KB = GM::KBYTES, SB = GM::STEP_BYTES;
     const int sp = blockIdx.x, kh = blockIdx.y, r = blockIdx.z;
     const int n_kv = gridDim.y;
     const long rk = (long)r * n_kv + kh;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    static_assert(NST >= 2 && NST <= 7, "page stages per wave");
+    static_assert(NST >= 2 && NST <= 4, "page stages per wave");
     static_assert(!(FUSED && DENSE), "the dense comparator merges in its own launch");
+    const int PG = DC_PG << pg_sh, smask = (1 << pg_sh) - 1;
     const int* prow = ptab + (long)r * pt_sr + (long)kh * pt_sh;
     // This wave's first page ids assuming pps == pps_min (the usual sparse
     // case), loaded together with the page count instead of after it.
-    const int js = sp * pps_min + wave + DC_WAVES * lane;
+    const int js = ((sp * pps_min) << pg_sh) + wave + DC_WAVES * lane;
     int pt_spec = 0, cnt;
     if constexpr (DENSE) {
-        cnt = min(cdiv(seq_lens[r], DC_PG), bt_cols);
+        cnt = min(cdiv(seq_lens[r], PG), bt_cols);
     } else {
-        pt_spec = (js < pt_cols) ? prow[js] : 0;
+        pt_spec = ((js >> pg_sh) < pt_cols) ? prow[js >> pg_sh] : 0;
         cnt = min(pcnt[(long)r * cnt_sr + kh], pt_cols);
     }
     // gridDim.x = the launched split count (<= split, the buffers' stride)
@@ -283,8 +296,8 @@ __global__ __launch_bounds__(DC_BLK) void decode_split_kernel(
     if constexpr (FUSED) {
         if (cnt <= 0) {                           // nothing selected: the output row is 0
             if (sp == 0)
-                for (int i = threadIdx.x; i < G * DC_D; i += DC_BLK) {
-                    const long oi = (long)r * o_sr + (long)(kh * G + i / DC_D) * o_sh + i % DC_D;
+                for (int i = threadIdx.x; i < G * D; i += DC_BLK) {
+                    const long oi = (long)r * o_sr + (long)(kh * G + i / D) * o_sh + i % D;
                     if (out_f32) static_cast<float*>(out)[oi] = 0.f;
                     else static_cast<uint16_t*>(out)[oi] = 0;
                 }
@@ -293,30 +306,36 @@ __global__ __launch_bounds__(DC_BLK) void decode_split_kernel(
     }
     if (j0 >= cnt) return;                        // inactive split: no store
     const int j1 = min(j0 + pps, cnt);
+    const int s0 = j0 << pg_sh, s1 = j1 << pg_sh; // this split's 16-token steps
 
     const int c16 = lane & 15, kg = lane >> 4;
     const int seq_len = seq_lens[r];
 
-    // NST page stages per wave (stage 0 in stA, the others in stB), later
-    // reused for the merge
-    __shared__ __attribute__((aligned(16))) uint8_t stA[DC_WAVES][DC_PAGE_BYTES];
-    __shared__ __attribute__((aligned(16))) uint8_t stB[(NST - 1) * DC_WAVES][DC_PAGE_BYTES];
+    // NST step stages per wave (stage 0 in stA, the others in stB), later
+    // reused for the merges (the fused merge needs MAX_SPLIT x 16 floats in each)
+    constexpr int MIN_REGION = FUSED ? MAX_SPLIT * 16 * 4 : 0;
+    constexpr int A_BYTES = DC_WAVES * SB > MIN_REGION ? DC_WAVES * SB : MIN_REGION;
+    constexpr int B_BYTES = (NST - 1) * DC_WAVES * SB > MIN_REGION ? (NST - 1) * DC_WAVES * SB : MIN_REGION;
+    static_assert(A_BYTES >= DC_WAVES * 16 * D * 4, "wave-merge buffer fits stage A");
+    __shared__ __attribute__((aligned(16))) uint8_t stA[A_BYTES];
+    __shared__ __attribute__((aligned(16))) uint8_t stB[B_BYTES];
     __shared__ float wm[DC_WAVES][16], wl[DC_WAVES][16];
+    auto stage = [&](int i) -> uint8_t* {
+        return i == 0 ? stA + wave * SB : stB + ((i - 1) * DC_WAVES + wave) * SB;
+    };
 
     // B operand of QK, k-slot (kg, s) <-> d = 32*s + 8*kg + 0..7
-    v8bf qb[4];
+    v8bf qb[KS];
     {
         const uint16_t* qp = q + (long)r * q_sr + (long)(kh * G + c16) * q_sh + 8 * kg;
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
+        for (int s = 0; s < KS; ++s) {
             uint4 w = make_uint4(0u, 0u, 0u, 0u);
             if (c16 < G) w = *reinterpret_cast<const uint4*>(qp + 32 * s);
             qb[s] = __builtin_bit_cast(v8bf, w);
         }
     }
 
-    // DMA page j into stage `st`: K slot s (0..3) = K[t = lane&15][32 s + 8 kg ..],
-    // V slot v (0..3) = V[4 kg + v][8 (lane&15) ..]
     // Page and block ids of up to 64 steps of this wave are fetched up front
     // (lane i holds step i), so no dependent id load sits behind a stage's
     // DMA in the in-order vmcnt queue.
@@ -325,60 +344,130 @@ __global__ __launch_bounds__(DC_BLK) void decode_split_kernel(
         const int jj = jb + DC_WAVES * lane;
         ptv = 0;
         blkv = 0;
-        if (jj < j1) {
-            if constexpr (DENSE) ptv = jj;
-            else ptv = spec ? pt_spec : prow[jj];
+        if (jj < s1) {
+            if constexpr (DENSE) ptv = jj >> pg_sh;
+            else ptv = spec ? pt_spec : prow[jj >> pg_sh];
             const int ptc = min(max(ptv, 0), bt_cols - 1);
             blkv = min(max(bt[(long)r * bt_sr + ptc], 0), NB - 1);
         }
     };
-    // DMA step s of the current id batch into stage `st`:
-    // K slot i (0..3) = K[t = lane&15][32 i + 8 kg ..], V slot i = V[4 kg + i][8 (lane&15) ..]
-    auto issue = [&](int s, uint8_t* st) -> int {
+    // DMA step s of the current id batch (16 tokens from token 16 * sub of
+    // its page) into stage `st`:
+    //   K slot i (< KS) = K[t = lane&15][32 i + 8 kg ..], 1 KB per slot;
+    //   V (D >= 128) slot (i, hh) = V[4 kg + i][DPL (lane&15) + 8 hh ..];
+    //   V (D == 64) in natural row order (8 lanes per 128-byte row).
+    auto issue = [&](int s, int sub, uint8_t* st) -> int {
         const int pt = __builtin_amdgcn_readlane(ptv, s);
         const int blk = __builtin_amdgcn_readlane(blkv, s);
-        const uint16_t* kp = kc + (long)blk * k_sb + (long)kh * k_sh + (long)c16 * k_st + 8 * kg;
-        const uint16_t* vp = vc + (long)blk * v_sb + (long)kh * v_sh + 8 * c16;
+        const long t0 = (long)sub * 16;
+        const uint16_t* kp = kc + (long)blk * k_sb + (long)kh * k_sh + (t0 + c16) * k_st + 8 * kg;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < KS; ++i)
             __builtin_amdgcn_global_load_lds(kp + 32 * i, (lds_ptr)(st + i * 1024), 16, 0, KVPOL);
+        const uint16_t* vb = vc + (long)blk * v_sb + (long)kh * v_sh + t0 * v_st;
+        if constexpr (D == 64) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            __builtin_amdgcn_global_load_lds(vp + (long)(4 * kg + i) * v_st, (lds_ptr)(st + 4096 + i * 1024), 16, 0, KVPOL);
+            for (int i = 0; i < 2; ++i)
+                __builtin_amdgcn_global_load_lds(vb + (long)(8 * i + (lane >> 3)) * v_st + 8 * (lane & 7),
+                                                 (lds_ptr)(st + KB + i * 1024), 16, 0, KVPOL);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int hh = 0; hh < DPL / 8; ++hh)
+                    __builtin_amdgcn_global_load_lds(vb + (long)(4 * kg + i) * v_st + DPL * c16 + 8 * hh,
+                                                     (lds_ptr)(st + KB + (i * (DPL / 8) + hh) * 1024), 16, 0, KVPOL);
+        }
         return pt;
     };
 
     float m = -INFINITY, lsum = 0.f;
-    v4f o[8];
+    v4f o[DPL];
 #pragma unroll
-    for (int b = 0; b < 8; ++b) o[b] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int b = 0; b < DPL; ++b) o[b] = v4f{0.f, 0.f, 0.f, 0.f};
 
-    auto consume = [&](const uint8_t* st, int pt) {
+    auto consume = [&](const uint8_t* st, int pt, int sub) {
         // The stage is read with ds_read in inline asm: the compiler cannot
-        // tell these reads from the other stage's DMA still in flight and
+        // tell these reads from the other stages' DMA still in flight and
         // would otherwise wait for every outstanding load (vmcnt(0)) here.
-        // The caller has already waited for this stage's own DMA.
-        v4i kr[4], vr[4];
-        const uint32_t la = (uint32_t)(uintptr_t)(lds_u8_ptr)(st) + lane * 16;
-        asm volatile(
-            "ds_read_b128 %0, %8\n\t"
-            "ds_read_b128 %1, %8 offset:1024\n\t"
-            "ds_read_b128 %2, %8 offset:2048\n\t"
-            "ds_read_b128 %3, %8 offset:3072\n\t"
-            "ds_read_b128 %4, %8 offset:4096\n\t"
-            "ds_read_b128 %5, %8 offset:5120\n\t"
-            "ds_read_b128 %6, %8 offset:6144\n\t"
-            "ds_read_b128 %7, %8 offset:7168\n\t"
-            "s_waitcnt lgkmcnt(0)"
-            : "=v"(kr[0]), "=v"(kr[1]), "=v"(kr[2]), "=v"(kr[3]),
-              "=v"(vr[0]), "=v"(vr[1]), "=v"(vr[2]), "=v"(vr[3])
-            : "v"(la));
+        // The caller has already waited for this stage's own DMA.  One asm
+        // block per head_dim, so nothing uses a result before the wait.
+        v4i kr[KS];
+        uint32_t vw[4][DPL / 2];                     // V row v: DPL bf16 columns
+        const uint32_t sbase = (uint32_t)(uintptr_t)(lds_u8_ptr)(st);
+        const uint32_t la = sbase + lane * 16;
+        if constexpr (D == 64) {
+            v2i v64[4];
+            const uint32_t lv = sbase + KB + kg * 512 + c16 * 8;   // row 4 kg, columns 4 c16 ..
+            asm volatile(
+                "ds_read_b128 %0, %6\n\t"
+                "ds_read_b128 %1, %6 offset:1024\n\t"
+                "ds_read_b64 %2, %7\n\t"
+                "ds_read_b64 %3, %7 offset:128\n\t"
+                "ds_read_b64 %4, %7 offset:256\n\t"
+                "ds_read_b64 %5, %7 offset:384\n\t"
+                "s_waitcnt lgkmcnt(0)"
+                : "=v"(kr[0]), "=v"(kr[1]), "=v"(v64[0]), "=v"(v64[1]), "=v"(v64[2]), "=v"(v64[3])
+                : "v"(la), "v"(lv));
+#pragma unroll
+            for (int v = 0; v < 4; ++v) { vw[v][0] = (uint32_t)v64[v][0]; vw[v][1] = (uint32_t)v64[v][1]; }
+        } else if constexpr (D == 128) {
+            v4i vr[4];
+            asm volatile(
+                "ds_read_b128 %0, %8\n\t"
+                "ds_read_b128 %1, %8 offset:1024\n\t"
+                "ds_read_b128 %2, %8 offset:2048\n\t"
+                "ds_read_b128 %3, %8 offset:3072\n\t"
+                "ds_read_b128 %4, %8 offset:4096\n\t"
+                "ds_read_b128 %5, %8 offset:5120\n\t"
+                "ds_read_b128 %6, %8 offset:6144\n\t"
+                "ds_read_b128 %7, %8 offset:7168\n\t"
+                "s_waitcnt lgkmcnt(0)"
+                : "=v"(kr[0]), "=v"(kr[1]), "=v"(kr[2]), "=v"(kr[3]),
+                  "=v"(vr[0]), "=v"(vr[1]), "=v"(vr[2]), "=v"(vr[3])
+                : "v"(la));
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) vw[v][e] = (uint32_t)vr[v][e];
+        } else {
+            v4i vr[8];
+            const uint32_t la2 = la + 8192;          // the second 8 KB of the stage
+            asm volatile(
+                "ds_read_b128 %0, %16\n\t"
+                "ds_read_b128 %1, %16 offset:1024\n\t"
+                "ds_read_b128 %2, %16 offset:2048\n\t"
+                "ds_read_b128 %3, %16 offset:3072\n\t"
+                "ds_read_b128 %4, %16 offset:4096\n\t"
+                "ds_read_b128 %5, %16 offset:5120\n\t"
+                "ds_read_b128 %6, %16 offset:6144\n\t"
+                "ds_read_b128 %7, %16 offset:7168\n\t"
+                "ds_read_b128 %8, %17\n\t"
+                "ds_read_b128 %9, %17 offset:1024\n\t"
+                "ds_read_b128 %10, %17 offset:2048\n\t"
+                "ds_read_b128 %11, %17 offset:3072\n\t"
+                "ds_read_b128 %12, %17 offset:4096\n\t"
+                "ds_read_b128 %13, %17 offset:5120\n\t"
+                "ds_read_b128 %14, %17 offset:6144\n\t"
+                "ds_read_b128 %15, %17 offset:7168\n\t"
+                "s_waitcnt lgkmcnt(0)"
+                : "=v"(kr[0]), "=v"(kr[1]), "=v"(kr[2]), "=v"(kr[3]),
+                  "=v"(kr[4]), "=v"(kr[5]), "=v"(kr[6]), "=v"(kr[7]),
+                  "=v"(vr[0]), "=v"(vr[1]), "=v"(vr[2]), "=v"(vr[3]),
+                  "=v"(vr[4]), "=v"(vr[5]), "=v"(vr[6]), "=v"(vr[7])
+                : "v"(la), "v"(la2));
+            // slot (v, hh) = vr[2 v + hh]: columns 16 c16 + 8 hh ..
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) vw[v][e] = (uint32_t)vr[2 * v + (e >> 2)][e & 3];
+        }
         // ---- S^T[t][g] = K[t] . q[g] ------------------------------------
         v4f s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < KS; ++i)
             s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, kr[i]), qb[i], s, 0, 0, 0);
-        const int pos0 = pt * DC_PG + 4 * kg;
+        const int pos0 = pt * PG + sub * 16 + 4 * kg;
         float sv[4];
 #pragma unroll
         for (int v = 0; v < 4; ++v) sv[v] = (pos0 + v < seq_len) ? s[v] * sm_scale : -INFINITY;
@@ -394,75 +483,61 @@ __global__ __launch_bounds__(DC_BLK) void decode_split_kernel(
         lsum = lsum * alpha + (p[0] + p[1] + p[2] + p[3]);
         m = m_new;
         const v4h pb = {(_Float16)p[0], (_Float16)p[1], (_Float16)p[2], (_Float16)p[3]};
-        // ---- O^T[d][g] += V^T P^T ---------------------------------------
+        // ---- O^T[d][g] += V^T P^T: block b holds d = DPL * row + b --------
 #pragma unroll
-        for (int b = 0; b < 8; ++b) {
+        for (int b = 0; b < DPL; ++b) {
             v4h a;
 #pragma unroll
-            for (int v = 0; v < 4; ++v) a[v] = (_Float16)bf16_to_f32((uint16_t)bf16_word(__builtin_bit_cast(uint4, vr[v]), b));
+            for (int v = 0; v < 4; ++v) {
+                const uint32_t w = vw[v][b >> 1];
+                a[v] = (_Float16)bf16_to_f32((uint16_t)((b & 1) ? (w >> 16) : (w & 0xFFFFu)));
+            }
             o[b] = o[b] * alpha;
             o[b] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, pb, o[b], 0, 0, 0);
         }
     };
 
-    // ping-pong over the two stages: iteration s issues step s+1 into one
-    // stage and consumes step s from the other (one page always in flight)
-    for (int jb = j0 + wave; jb < j1; jb += DC_WAVES * kWave) {
-        fetch_ids(jb, pps == pps_min && jb == j0 + wave);
+    for (int jb = s0 + wave; jb < s1; jb += DC_WAVES * kWave) {
+        fetch_ids(jb, pps == pps_min && jb == s0 + wave);
         __builtin_amdgcn_s_waitcnt(0x0070);   // ids (and q) resident before any DMA
-        const int ns = min(kWave, cdiv(j1 - jb, DC_WAVES));   // steps of this batch
-        if constexpr (NST > 2) {
-            // ring of NST stages: step s + NST - 1 is issued before step s is
-            // consumed, so up to NST - 1 pages stream while one is scored
-            auto stage = [&](int i) { return i == 0 ? stA[wave] : stB[(i - 1) * DC_WAVES + wave]; };
+        const int ns = min(kWave, cdiv(s1 - jb, DC_WAVES));   // steps of this batch
+        auto sub_of = [&](int s) { return (jb + DC_WAVES * s) & smask; };
+        // ring of NST stages: step s + NST - 1 is issued before step s is
+        // consumed, so up to NST - 1 steps stream while one is scored
 #pragma unroll
-            for (int i = 0; i < NST - 1; ++i)
-                if (i < ns) issue(i, stage(i));
-            int si = 0, ii = NST - 1;
-            for (int s = 0; s < ns; ++s) {
-                if (s + NST - 1 < ns) issue(s + NST - 1, stage(ii));
-                wait_vm_pages<NST>(min(NST - 1, ns - 1 - s));
-                __builtin_amdgcn_wave_barrier();
-                consume(stage(si), __builtin_amdgcn_readlane(ptv, s));
-                __builtin_amdgcn_wave_barrier();
-                si = (si + 1 == NST) ? 0 : si + 1;
-                ii = (ii + 1 == NST) ? 0 : ii + 1;
-            }
-            continue;
-        }
-        int pt_cur = 0;
-        for (int s = -1; s < ns; ++s) {
-            const bool nxt = s + 1 < ns;
-            int pt_nxt = 0;
-            if (nxt) pt_nxt = issue(s + 1, ((s + 1) & 1) ? stB[wave] : stA[wave]);
-            if (s >= 0) {
-                if (nxt) __builtin_amdgcn_s_waitcnt(0x0078);   // vmcnt(8): step s landed
-                else __builtin_amdgcn_s_waitcnt(0x0070);      // vmcnt(0)
-                __builtin_amdgcn_wave_barrier();
-                consume((s & 1) ? stB[wave] : stA[wave], pt_cur);
-                __builtin_amdgcn_wave_barrier();
-            }
-            pt_cur = pt_nxt;
+        for (int i = 0; i < NST - 1; ++i)
+            if (i < ns) issue(i, sub_of(i), stage(i));
+        int si = 0, ii = NST - 1;
+        for (int s = 0; s < ns; ++s) {
+            if (s + NST - 1 < ns) issue(s + NST - 1, sub_of(s + NST - 1), stage(ii));
+            wait_vm_steps<NI, NST>(min(NST - 1, ns - 1 - s));
+            __builtin_amdgcn_wave_barrier();
+            consume(stage(si), __builtin_amdgcn_readlane(ptv, s), sub_of(s));
+            __builtin_amdgcn_wave_barrier();
+            si = (si + 1 == NST) ? 0 : si + 1;
+            ii = (ii + 1 == NST) ? 0 : ii + 1;
         }
     }
     lsum = xor32_sum(xor16_sum(lsum));
 
     // ---- merge the 4 wave states of this split in LDS --------------------
     __syncthreads();                              // every stage consumed
-    float* red = reinterpret_cast<float*>(&stA[0][0]);   // [wave][g][d], 32 KB
+    float* red = reinterpret_cast<float*>(stA);   // [wave][g][d]
     if (kg == 0) { wm[wave][c16] = m; wl[wave][c16] = lsum; }
     {
-        float* ow = red + (wave * 16 + c16) * DC_D + 32 * kg;
+        // lane (g = c16, kg), row v of block b <-> d = DPL * (4 kg + v) + b
+        float* ow = red + (wave * 16 + c16) * D + DPL * 4 * kg;
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            *reinterpret_cast<float4*>(ow + 8 * v) = make_float4(o[0][v], o[1][v], o[2][v], o[3][v]);
-            *reinterpret_cast<float4*>(ow + 8 * v + 4) = make_float4(o[4][v], o[5][v], o[6][v], o[7][v]);
-        }
+        for (int v = 0; v < 4; ++v)
+#pragma unroll
+            for (int j = 0; j < DPL / 4; ++j)
+                *reinterpret_cast<float4*>(ow + DPL * v + 4 * j) =
+                    make_float4(o[4 * j][v], o[4 * j + 1][v], o[4 * j + 2][v], o[4 * j + 3][v]);
     }
     __syncthreads();
     const long base = (rk * split + sp) * G;
-    for (int i = tid; i < G * (DC_D / 4); i += DC_BLK) {
-        const int g = i / (DC_D / 4), d = (i % (DC_D / 4)) * 4;
+    for (int i = tid; i < G * (D / 4); i += DC_BLK) {
+        const int g = i / (D / 4), d = (i % (D / 4)) * 4;
         float M = wm[0][g];
 #pragma unroll
         for (int w = 1; w < DC_WAVES; ++w) M = fmaxf(M, wm[w][g]);
@@ -472,19 +547,19 @@ __global__ __launch_bounds__(DC_BLK) void decode_split_kernel(
 #pragma unroll
         for (int w = 0; w < DC_WAVES; ++w) {
             const float e = __expf(wm[w][g] - Mr);
-            const float4 x = *reinterpret_cast<const float4*>(red + (w * 16 + g) * DC_D + d);
+            const float4 x = *reinterpret_cast<const float4*>(red + (w * 16 + g) * D + d);
             acc.x += e * x.x; acc.y += e * x.y; acc.z += e * x.z; acc.w += e * x.w;
             l += e * wl[w][g];
         }
         if constexpr (FUSED) {
             __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i, acc), part_rsrc(acc_part),
-                                                   (int)(((base + g) * DC_D + d) * 4), 0, CPOL_SC1);
+                                                   (int)(((base + g) * D + d) * 4), 0, CPOL_SC1);
             if (d == 0) {
                 __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(M), part_rsrc(m_part), (int)((base + g) * 4), 0, CPOL_SC1);
                 __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(l), part_rsrc(l_part), (int)((base + g) * 4), 0, CPOL_SC1);
             }
         } else {
-            *reinterpret_cast<float4*>(acc_part + (base + g) * DC_D + d) = acc;
+            *reinterpret_cast<float4*>(acc_part + (base + g) * D + d) = acc;
             if (d == 0) { m_part[base + g] = M; l_part[base + g] = l; }
         }
     }
@@ -524,31 +599,32 @@ __global__ __launch_bounds__(DC_BLK) void decode_split_kernel(
         if (!last_s) return;
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
         if (tid == 0) __hip_atomic_store(counters + rk * LOCKS_DECODE_COUNTER_STRIDE, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        merge_row<true>(m_part, l_part, acc_part, rk, r, kh, n_act, G, split, out, o_sr, o_sh,
-                        out_f32, reinterpret_cast<float*>(&stA[0][0]),
-                        reinterpret_cast<float*>(&stB[0][0]), lt_s);
+        merge_row<true, D>(m_part, l_part, acc_part, rk, r, kh, n_act, G, split, out, o_sr, o_sh,
+                           out_f32, reinterpret_cast<float*>(stA), reinterpret_cast<float*>(stB), lt_s);
     }
 }
 
 // LSE merge of one (request, kv head, query head) row of split partials,
-// one workgroup per head: 8 split streams x 32 float4 columns, so a row is
+// one workgroup per head: D / 4 float4 columns x 1024 / D split streams, so a row is
 // merged by G workgroups (G CUs' memory parallelism) instead of one.  The
 // page count is page_cnt (clamped to pt_cols, as the split kernel) or, with
 // pcnt == nullptr, the dense one (every page of the row).
-constexpr int MH_BLK = 256, MH_STREAMS = MH_BLK / 32;
-constexpr int MH_PF = 8;                   // partials prefetched per thread (64 splits)
+constexpr int MH_BLK = 256;
+constexpr int MH_PF = 8;                   // partials prefetched per thread
+template <int D>
 __global__ __launch_bounds__(MH_BLK) void decode_merge_heads_kernel(
     const float* __restrict__ m_part, const float* __restrict__ l_part,
     const float* __restrict__ acc_part, const int* __restrict__ pcnt, long cnt_sr, int pt_cols,
     const int* __restrict__ seq_lens, int bt_cols,
     void* __restrict__ out, long o_sr, long o_sh, int out_f32, int G, int split, int nsplit,
-    int pps_min)
+    int pps_min, int pg)
 {
+    constexpr int MH_COLS = D / 4, MH_STREAMS = MH_BLK / MH_COLS;   // float4 columns x split streams
     const int g = blockIdx.x, kh = blockIdx.y, r = blockIdx.z;
     const int n_kv = gridDim.y;
     const long rk = (long)r * n_kv + kh;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int col = tid & 31, strm = tid >> 5;
+    const int col = tid % MH_COLS, strm = tid / MH_COLS;
     // Every load is issued before anything waits: the page count, this
     // thread's (split, m, l) and its first MH_PF partial columns, at split
     // indices clamped into the buffers (entries past the active count are
@@ -558,16 +634,16 @@ __global__ __launch_bounds__(MH_BLK) void decode_merge_heads_kernel(
 #pragma unroll
     for (int k = 0; k < MH_PF; ++k) {
         const int sidx = min(strm + k * MH_STREAMS, split - 1);
-        pre[k] = *reinterpret_cast<const float4*>(acc_part + ((rk * split + sidx) * G + g) * DC_D + col * 4);
+        pre[k] = *reinterpret_cast<const float4*>(acc_part + ((rk * split + sidx) * G + g) * D + col * 4);
     }
     const long ml0 = (rk * split + min(tid, split - 1)) * G + g;
     const float m0 = m_part[ml0], l0 = l_part[ml0];
-    const int cnt = pcnt ? min(cnt_raw, pt_cols) : min(cdiv(cnt_raw, DC_PG), bt_cols);
+    const int cnt = pcnt ? min(cnt_raw, pt_cols) : min(cdiv(cnt_raw, pg), bt_cols);
     const int pps = max(cdiv(cnt, nsplit), pps_min);
     const int n_act = cnt > 0 ? min(cdiv(cnt, pps), nsplit) : 0;
     __shared__ float w_s[MAX_SPLIT];
     __shared__ float red[MH_BLK / kWave];
-    __shared__ float4 part[MH_STREAMS][32];
+    __shared__ float4 part[MH_STREAMS][MH_COLS];
     // head max over the splits that hold mass
     const bool has0 = tid < n_act && l0 > 0.f;
     float mm = has0 ? m0 : -INFINITY;
@@ -610,12 +686,12 @@ __global__ __launch_bounds__(MH_BLK) void decode_merge_heads_kernel(
 #pragma unroll 4
     for (int s = strm + MH_PF * MH_STREAMS; s < n_act; s += MH_STREAMS) {
         const float w = w_s[s];
-        const float4 a = *reinterpret_cast<const float4*>(acc_part + ((rk * split + s) * G + g) * DC_D + col * 4);
+        const float4 a = *reinterpret_cast<const float4*>(acc_part + ((rk * split + s) * G + g) * D + col * 4);
         acc.x += w * a.x; acc.y += w * a.y; acc.z += w * a.z; acc.w += w * a.w;
     }
     part[strm][col] = acc;
     lds_barrier();
-    if (tid < 32) {
+    if (tid < MH_COLS) {
         float4 t = part[0][col];
 #pragma unroll
         for (int k = 1; k < MH_STREAMS; ++k) {
@@ -657,6 +733,22 @@ static int launched_splits(int split, int pps_min, int max_cnt) {
     return max_cnt > 0 ? std::min(split, std::max(1, cdiv(max_cnt, pps_min))) : split;
 }
 
+// head_dim in {64, 128, 256}, page in {16, 32, 64} (the reference's geometry
+// domain, rki4_state.py:295-324); pg_sh = log2(page / 16)
+static bool dc_geometry(int head_dim, int page, int* pg_sh) {
+    if (head_dim != 64 && head_dim != 128 && head_dim != 256) return false;
+    if (page != 16 && page != 32 && page != 64) return false;
+    *pg_sh = page == 16 ? 0 : page == 32 ? 1 : 2;
+    return true;
+}
+// launch KERNEL<..., D> for the runtime head_dim
+#define DC_BY_D(HD, LAUNCH_D)                               \
+    do {                                                     \
+        if ((HD) == 64) { LAUNCH_D(64); }                    \
+        else if ((HD) == 128) { LAUNCH_D(128); }             \
+        else { LAUNCH_D(256); }                              \
+    } while (0)
+
 extern "C" int32_t locks_decode_splitk(
     const uint16_t* q, int64_t q_stride_req, int64_t q_stride_head,
     const uint16_t* k_cache, int64_t k_stride_block, int64_t k_stride_tok, int64_t k_stride_head,
@@ -668,8 +760,9 @@ extern "C" int32_t locks_decode_splitk(
     int32_t n_req, int32_t n_kv, int32_t G, int32_t head_dim, int32_t page,
     int32_t split, int32_t pps_min, int32_t max_cnt, float sm_scale, void* stream)
 {
-    LOCKS_REQUIRE(head_dim == DC_D, "locks_decode_splitk: head_dim %d unsupported (this build: 128)", head_dim);
-    LOCKS_REQUIRE(page == DC_PG, "locks_decode_splitk: page %d unsupported (this build: 16)", page);
+    int pg_sh = 0;
+    LOCKS_REQUIRE(dc_geometry(head_dim, page, &pg_sh),
+                  "locks_decode_splitk: head_dim %d / page %d outside {64,128,256} x {16,32,64}", head_dim, page);
     LOCKS_REQUIRE(G >= 1 && G <= 16, "locks_decode_splitk: G=%d outside [1, 16]", G);
     LOCKS_REQUIRE(split >= 1 && split <= MAX_SPLIT, "locks_decode_splitk: split %d outside [1, %d]", split, MAX_SPLIT);
     LOCKS_REQUIRE(pps_min >= 1, "locks_decode_splitk: pps_min %d < 1", pps_min);
@@ -681,14 +774,18 @@ extern "C" int32_t locks_decode_splitk(
     LOCKS_REQUIRE(q && k_cache && v_cache && block_table && page_table && page_cnt && seq_lens &&
                   m_part && l_part && acc_part, "locks_decode_splitk: null pointer argument");
     if (n_req == 0) return 0;
-    hipLaunchKernelGGL(decode_split_kernel<false>, dim3(launched_splits(split, pps_min, max_cnt), n_kv, n_req), dim3(DC_BLK), 0,
-                       (hipStream_t)stream, q, (long)q_stride_req, (long)q_stride_head, k_cache,
-                       (long)k_stride_block, (long)k_stride_tok, (long)k_stride_head, v_cache,
-                       (long)v_stride_block, (long)v_stride_tok, (long)v_stride_head, num_blocks,
-                       block_table, (long)bt_stride, bt_cols, page_table, (long)pt_stride_req,
-                       (long)pt_stride_head, pt_cols, page_cnt, (long)cnt_stride, seq_lens,
-                       m_part, l_part, acc_part, G, split, pps_min, sm_scale,
-                       nullptr, nullptr, 0L, 0L, 0);
+#define LAUNCH_D(DV)                                                                                   \
+    hipLaunchKernelGGL((decode_split_kernel<false, false, 2, 0, DV>),                                  \
+                       dim3(launched_splits(split, pps_min, max_cnt), n_kv, n_req), dim3(DC_BLK), 0,    \
+                       (hipStream_t)stream, q, (long)q_stride_req, (long)q_stride_head, k_cache,       \
+                       (long)k_stride_block, (long)k_stride_tok, (long)k_stride_head, v_cache,         \
+                       (long)v_stride_block, (long)v_stride_tok, (long)v_stride_head, num_blocks,      \
+                       block_table, (long)bt_stride, bt_cols, page_table, (long)pt_stride_req,         \
+                       (long)pt_stride_head, pt_cols, page_cnt, (long)cnt_stride, seq_lens,            \
+                       m_part, l_part, acc_part, G, split, pps_min, sm_scale, pg_sh,                   \
+                       nullptr, nullptr, 0L, 0L, 0)
+    DC_BY_D(head_dim, LAUNCH_D);
+#undef LAUNCH_D
     return check_launch("decode_split_kernel");
 }
 
@@ -704,8 +801,9 @@ extern "C" int32_t locks_decode_fused(
     int32_t n_req, int32_t n_kv, int32_t G, int32_t head_dim, int32_t page,
     int32_t split, int32_t pps_min, int32_t max_cnt, float sm_scale, void* stream)
 {
-    LOCKS_REQUIRE(head_dim == DC_D, "locks_decode_fused: head_dim %d unsupported (this build: 128)", head_dim);
-    LOCKS_REQUIRE(page == DC_PG, "locks_decode_fused: page %d unsupported (this build: 16)", page);
+    int pg_sh = 0;
+    LOCKS_REQUIRE(dc_geometry(head_dim, page, &pg_sh),
+                  "locks_decode_fused: head_dim %d / page %d outside {64,128,256} x {16,32,64}", head_dim, page);
     LOCKS_REQUIRE(G >= 1 && G <= 16, "locks_decode_fused: G=%d outside [1, 16]", G);
     LOCKS_REQUIRE(split >= 1 && split <= MAX_SPLIT, "locks_decode_fused: split %d outside [1, %d]", split, MAX_SPLIT);
     LOCKS_REQUIRE(pps_min >= 1, "locks_decode_fused: pps_min %d < 1", pps_min);
@@ -716,19 +814,23 @@ extern "C" int32_t locks_decode_fused(
                   "locks_decode_fused: q/K/V strides must be multiples of 8 elements (16-byte loads)");
     LOCKS_REQUIRE(out_stride_req % 4 == 0 && out_stride_head % 4 == 0,
                   "locks_decode_fused: out strides must be multiples of 4 elements");
-    LOCKS_REQUIRE((int64_t)n_req * n_kv * split * G * DC_D * 4 < 0x7fffffffLL,
+    LOCKS_REQUIRE((int64_t)n_req * n_kv * split * G * head_dim * 4 < 0x7fffffffLL,
                   "locks_decode_fused: partials exceed 2 GiB");
     LOCKS_REQUIRE(q && k_cache && v_cache && block_table && page_table && page_cnt && seq_lens &&
                   m_part && l_part && acc_part && counters && out, "locks_decode_fused: null pointer argument");
     if (n_req == 0) return 0;
-    hipLaunchKernelGGL(decode_split_kernel<true>, dim3(launched_splits(split, pps_min, max_cnt), n_kv, n_req), dim3(DC_BLK), 0,
-                       (hipStream_t)stream, q, (long)q_stride_req, (long)q_stride_head, k_cache,
-                       (long)k_stride_block, (long)k_stride_tok, (long)k_stride_head, v_cache,
-                       (long)v_stride_block, (long)v_stride_tok, (long)v_stride_head, num_blocks,
-                       block_table, (long)bt_stride, bt_cols, page_table, (long)pt_stride_req,
-                       (long)pt_stride_head, pt_cols, page_cnt, (long)cnt_stride, seq_lens,
-                       m_part, l_part, acc_part, G, split, pps_min, sm_scale,
-                       counters, out, (long)out_stride_req, (long)out_stride_head, out_is_f32);
+#define LAUNCH_D(DV)                                                                                   \
+    hipLaunchKernelGGL((decode_split_kernel<true, false, 2, 0, DV>),                                   \
+                       dim3(launched_splits(split, pps_min, max_cnt), n_kv, n_req), dim3(DC_BLK), 0,    \
+                       (hipStream_t)stream, q, (long)q_stride_req, (long)q_stride_head, k_cache,       \
+                       (long)k_stride_block, (long)k_stride_tok, (long)k_stride_head, v_cache,         \
+                       (long)v_stride_block, (long)v_stride_tok, (long)v_stride_head, num_blocks,      \
+                       block_table, (long)bt_stride, bt_cols, page_table, (long)pt_stride_req,         \
+                       (long)pt_stride_head, pt_cols, page_cnt, (long)cnt_stride, seq_lens,            \
+                       m_part, l_part, acc_part, G, split, pps_min, sm_scale, pg_sh,                   \
+                       counters, out, (long)out_stride_req, (long)out_stride_head, out_is_f32)
+    DC_BY_D(head_dim, LAUNCH_D);
+#undef LAUNCH_D
     return check_launch("decode_split_kernel<fused>");
 }
 
@@ -739,7 +841,8 @@ extern "C" int32_t locks_decode_merge(
     int32_t head_dim, int32_t split, int32_t pps_min, int32_t max_cnt, void* stream)
 {
     LOCKS_REQUIRE(pt_cols >= 1, "locks_decode_merge: pt_cols %d < 1", pt_cols);
-    LOCKS_REQUIRE(head_dim == DC_D, "locks_decode_merge: head_dim %d unsupported (this build: 128)", head_dim);
+    LOCKS_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256,
+                  "locks_decode_merge: head_dim %d outside {64, 128, 256}", head_dim);
     LOCKS_REQUIRE(G >= 1 && G <= 16, "locks_decode_merge: G=%d outside [1, 16]", G);
     LOCKS_REQUIRE(split >= 1 && split <= MAX_SPLIT, "locks_decode_merge: split %d outside [1, %d]", split, MAX_SPLIT);
     LOCKS_REQUIRE(pps_min >= 1, "locks_decode_merge: pps_min %d < 1", pps_min);
@@ -747,10 +850,13 @@ extern "C" int32_t locks_decode_merge(
     LOCKS_REQUIRE(out_stride_req % 4 == 0 && out_stride_head % 4 == 0,
                   "locks_decode_merge: out strides must be multiples of 4 elements");
     if (n_req == 0) return 0;
-    hipLaunchKernelGGL(decode_merge_heads_kernel, dim3(G, n_kv, n_req), dim3(MH_BLK), 0,
-                       (hipStream_t)stream, m_part, l_part, acc_part, page_cnt, (long)cnt_stride,
-                       pt_cols, nullptr, 1, out, (long)out_stride_req, (long)out_stride_head,
-                       out_is_f32, G, split, launched_splits(split, pps_min, max_cnt), pps_min);
+#define LAUNCH_D(DV)                                                                                \
+    hipLaunchKernelGGL(decode_merge_heads_kernel<DV>, dim3(G, n_kv, n_req), dim3(MH_BLK), 0,        \
+                       (hipStream_t)stream, m_part, l_part, acc_part, page_cnt, (long)cnt_stride,   \
+                       pt_cols, nullptr, 1, out, (long)out_stride_req, (long)out_stride_head,       \
+                       out_is_f32, G, split, launched_splits(split, pps_min, max_cnt), pps_min, 16)
+    DC_BY_D(head_dim, LAUNCH_D);
+#undef LAUNCH_D
     return check_launch("decode_merge_kernel");
 }
 
@@ -765,8 +871,9 @@ extern "C" int32_t locks_decode_dense(
     int32_t n_req, int32_t n_kv, int32_t G, int32_t head_dim, int32_t page,
     int32_t split, float sm_scale, void* stream)
 {
-    LOCKS_REQUIRE(head_dim == DC_D, "locks_decode_dense: head_dim %d unsupported (this build: 128)", head_dim);
-    LOCKS_REQUIRE(page == DC_PG, "locks_decode_dense: page %d unsupported (this build: 16)", page);
+    int pg_sh = 0;
+    LOCKS_REQUIRE(dc_geometry(head_dim, page, &pg_sh),
+                  "locks_decode_dense: head_dim %d / page %d outside {64,128,256} x {16,32,64}", head_dim, page);
     LOCKS_REQUIRE(G >= 1 && G <= 16, "locks_decode_dense: G=%d outside [1, 16]", G);
     LOCKS_REQUIRE(split >= 1 && split <= MAX_SPLIT, "locks_decode_dense: split %d outside [1, %d]", split, MAX_SPLIT);
     LOCKS_REQUIRE(num_blocks >= 1 && bt_cols >= 1, "locks_decode_dense: empty geometry");
@@ -780,18 +887,25 @@ extern "C" int32_t locks_decode_dense(
                   "locks_decode_dense: null pointer argument");
     if (n_req == 0) return 0;
     hipStream_t st = (hipStream_t)stream;
-    hipLaunchKernelGGL((decode_split_kernel<false, true, DENSE_NST, CPOL_NT>), dim3(split, n_kv, n_req), dim3(DC_BLK),
-                       0, st, q, (long)q_stride_req, (long)q_stride_head, k_cache,
-                       (long)k_stride_block, (long)k_stride_tok, (long)k_stride_head, v_cache,
-                       (long)v_stride_block, (long)v_stride_tok, (long)v_stride_head, num_blocks,
-                       block_table, (long)bt_stride, bt_cols, nullptr, 0L, 0L, 1, nullptr, 0L,
-                       seq_lens, m_part, l_part, acc_part, G, split, 1, sm_scale,
-                       nullptr, nullptr, 0L, 0L, 0);
+#define LAUNCH_D(DV)                                                                                \
+    hipLaunchKernelGGL((decode_split_kernel<false, true, DENSE_NST, CPOL_NT, DV>), dim3(split, n_kv, n_req), \
+                       dim3(DC_BLK), 0, st, q, (long)q_stride_req, (long)q_stride_head, k_cache,    \
+                       (long)k_stride_block, (long)k_stride_tok, (long)k_stride_head, v_cache,      \
+                       (long)v_stride_block, (long)v_stride_tok, (long)v_stride_head, num_blocks,   \
+                       block_table, (long)bt_stride, bt_cols, nullptr, 0L, 0L, 1, nullptr, 0L,      \
+                       seq_lens, m_part, l_part, acc_part, G, split, 1, sm_scale, pg_sh,            \
+                       nullptr, nullptr, 0L, 0L, 0)
+    DC_BY_D(head_dim, LAUNCH_D);
+#undef LAUNCH_D
     int rc = check_launch("decode_split_kernel<dense>");
     if (rc) return rc;
-    hipLaunchKernelGGL(decode_merge_heads_kernel, dim3(G, n_kv, n_req), dim3(MH_BLK), 0, st,
-                       m_part, l_part, acc_part, nullptr, 0L, 1, seq_lens, bt_cols, out,
-                       (long)out_stride_req, (long)out_stride_head, out_is_f32, G, split, split, 1);
+#define LAUNCH_D(DV)                                                                                \
+    hipLaunchKernelGGL(decode_merge_heads_kernel<DV>, dim3(G, n_kv, n_req), dim3(MH_BLK), 0, st,    \
+                       m_part, l_part, acc_part, nullptr, 0L, 1, seq_lens, bt_cols, out,            \
+                       (long)out_stride_req, (long)out_stride_head, out_is_f32, G, split, split, 1, \
+                       page)
+    DC_BY_D(head_dim, LAUNCH_D);
+#undef LAUNCH_D
     return check_launch("decode_merge_heads_kernel");
 }
 
@@ -834,7 +948,7 @@ extern "C" int32_t locks_decode_fused_noalloc(
     const long rows = (long)n_req * n_kv;
     const long cnt_bytes = rows * LOCKS_DECODE_COUNTER_STRIDE * 4;
     const long ml = rows * split * G;                    // m or l floats
-    const long need = cnt_bytes + ml * 4 * 2 + ml * DC_D * 4;
+    const long need = cnt_bytes + ml * 4 * 2 + ml * (long)head_dim * 4;
     LOCKS_REQUIRE(need <= LOCKS_NOALLOC_SCRATCH_BYTES,
                   "locks_decode_fused_noalloc: n_req=%d x n_kv=%d x split=%d x G=%d needs %ld B of "
                   "scratch, more than its %ld B (use locks_decode_fused with caller buffers)",
