@@ -29,35 +29,40 @@
 
 namespace locks {
 
-constexpr int BD_PG = 16;
 constexpr int BD_RNK = 8;
-constexpr int BD_SWEEPS = 12;
 // build grid cap (waves stride over the rest): a few resident rounds on 256 CUs
 constexpr long BD_MAX_GRID = 4096;
-// waves per workgroup: the per-wave LDS image of a d = 512 page is ~37 KB
-template <int D> constexpr int bd_waves() { return D <= 128 ? 4 : 1; }
 
-template <int D>
+// Per-wave LDS image of one (block, kv head) page of PG tokens x D dims.
+template <int D, int PG>
 struct WaveLds {
-    float dc[BD_PG][D + 1];      // centred page (padded rows)
+    float dc[PG][D + 1];         // centred page (padded rows)
     float mu[D];
-    float A[BD_PG][BD_PG + 1];   // gram, rotated in place
-    float U[BD_PG][BD_PG + 1];   // accumulated eigenvectors (columns)
-    float cc[BD_PG], ss[BD_PG];
+    float A[PG][PG + 1];         // gram, rotated in place
+    float U[PG][PG + 1];         // accumulated eigenvectors (columns)
+    float cc[PG], ss[PG];
     float S8[BD_RNK];
     int col[BD_RNK];             // eigen column of basis r (ascending top-8)
     float red[BD_RNK][kWave / 8];
 };
+// waves per workgroup: as many page images as fit 160 KB of LDS, at most 4;
+// d = 512 (the MLA latent, ~37 KB per image) runs one
+template <int D, int PG> constexpr int bd_waves() {
+    if (D >= 512) return 1;
+    constexpr int n = (160 * 1024) / (int)sizeof(WaveLds<D, PG>);
+    return n >= 4 ? 4 : n;
+}
 
 // quantize + pack one page from mu (LDS), dc (LDS), U8 = U[:, col[r]],
 // S8 (LDS), writing the six slab rows.  Lane l owns the packed bytes
 // j = l + 64 k (d = 2j, 2j + 1).
-template <int D>
-__device__ __forceinline__ void pack_page(WaveLds<D>& L, long row, uint8_t* __restrict__ v4, uint16_t* __restrict__ vs,
+template <int D, int PG>
+__device__ __forceinline__ void pack_page(WaveLds<D, PG>& L, long row, uint8_t* __restrict__ v4, uint16_t* __restrict__ vs,
                           int8_t* __restrict__ c8, uint16_t* __restrict__ cs,
                           int8_t* __restrict__ mu8, uint16_t* __restrict__ mus) {
-    constexpr int NK = D / 128;
+    constexpr int NK = (D / 2 + 63) / 64;      // packed bytes per lane (d = 64: lanes < 32)
     const int lane = threadIdx.x & 63;
+    auto own = [&](int k) { return lane + 64 * k < D / 2; };
     // V[d][r]: sequential over t, separately rounded
     float V[NK][2][BD_RNK];
 #pragma unroll
@@ -67,15 +72,16 @@ __device__ __forceinline__ void pack_page(WaveLds<D>& L, long row, uint8_t* __re
             const int d = 2 * (lane + 64 * k) + e;
 #pragma unroll
             for (int r = 0; r < BD_RNK; ++r) {
-                // d = 128: a compiler barrier keeps one column's operands
+                // d <= 256: a compiler barrier keeps one column's operands
                 // live at a time (hoisting all 16 x 8 basis values costs ~130
                 // VGPRs and halves the occupancy).  d = 512 runs one wave per
                 // SIMD anyway (its LDS image), so there the hoisting is free
                 // and the barrier would only multiply the LDS reloads.
-                if constexpr (D <= 128) asm volatile("" ::: "memory");
+                if constexpr (D <= 256) asm volatile("" ::: "memory");
                 float acc = 0.f;
                 const int c = L.col[r];
-                for (int t = 0; t < BD_PG; ++t) acc = __fadd_rn(acc, __fmul_rn(L.dc[t][d], L.U[t][c]));
+                if (own(k))
+                    for (int t = 0; t < PG; ++t) acc = __fadd_rn(acc, __fmul_rn(L.dc[t][d], L.U[t][c]));
                 V[k][e][r] = __fdiv_rn(acc, L.S8[r]);
             }
         }
@@ -96,11 +102,11 @@ __device__ __forceinline__ void pack_page(WaveLds<D>& L, long row, uint8_t* __re
         for (int k = 0; k < NK; ++k) {
             const int lo = (int)fminf(fmaxf(rintf(__fdiv_rn(V[k][0][r], vsc[r])), -8.f), 7.f);
             const int hi = (int)fminf(fmaxf(rintf(__fdiv_rn(V[k][1][r], vsc[r])), -8.f), 7.f);
-            vrow[r * (D / 2) + lane + 64 * k] = (uint8_t)((lo & 15) | ((hi & 15) << 4));
+            if (own(k)) vrow[r * (D / 2) + lane + 64 * k] = (uint8_t)((lo & 15) | ((hi & 15) << 4));
         }
     if (lane < BD_RNK) vs[row * BD_RNK + lane] = f32_to_bf16(vsc[lane]);
-    // coefficients: lane t < 16 owns token t
-    if (lane < BD_PG) {
+    // coefficients: lane t < PG owns token t
+    if (lane < PG) {
         const int t = lane;
         float C[BD_RNK];
         float am = 0.f;
@@ -110,17 +116,17 @@ __device__ __forceinline__ void pack_page(WaveLds<D>& L, long row, uint8_t* __re
             am = fmaxf(am, fabsf(C[r]));
         }
         const float csc = fmaxf(__fdiv_rn(am, 127.f), 1e-8f);
-        int8_t* crow = c8 + (row * BD_PG + t) * BD_RNK;
+        int8_t* crow = c8 + (row * PG + t) * BD_RNK;
 #pragma unroll
         for (int r = 0; r < BD_RNK; ++r)
             crow[r] = (int8_t)fminf(fmaxf(rintf(__fdiv_rn(C[r], csc)), -127.f), 127.f);
-        cs[row * BD_PG + t] = f32_to_bf16(csc);
+        cs[row * PG + t] = f32_to_bf16(csc);
     }
     // centroid
     float am = 0.f;
 #pragma unroll
     for (int k = 0; k < NK; ++k)
-        am = fmaxf(am, fmaxf(fabsf(L.mu[2 * (lane + 64 * k)]), fabsf(L.mu[2 * (lane + 64 * k) + 1])));
+        if (own(k)) am = fmaxf(am, fmaxf(fabsf(L.mu[2 * (lane + 64 * k)]), fabsf(L.mu[2 * (lane + 64 * k) + 1])));
     am = wave_max(am);
     const float msc = fmaxf(__fdiv_rn(am, 127.f), 1e-8f);
 #pragma unroll
@@ -128,47 +134,53 @@ __device__ __forceinline__ void pack_page(WaveLds<D>& L, long row, uint8_t* __re
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
             const int d = 2 * (lane + 64 * k) + e;
-            mu8[row * D + d] = (int8_t)fminf(fmaxf(rintf(__fdiv_rn(L.mu[d], msc)), -127.f), 127.f);
+            if (own(k)) mu8[row * D + d] = (int8_t)fminf(fmaxf(rintf(__fdiv_rn(L.mu[d], msc)), -127.f), 127.f);
         }
     if (lane == 0) mus[row] = f32_to_bf16(msc);
 }
 
-// Parallel cyclic Jacobi on L.A (16x16 symmetric); eigenvectors -> L.U columns.
-// Round-robin pairing of step `step`: index 0 stays, 1..15 rotate; the
-// pair of position k (1 <= k <= 7) is (at(k), at(15 - k)), position 0 pairs
-// index 0 with at(0), where at(k) = 1 + (k + step) % 15.
-__device__ __forceinline__ int rr_at(int k, int step) { return 1 + (k + step) % (BD_PG - 1); }
+// Parallel cyclic Jacobi on L.A (N x N symmetric, N = page = 16 or 32);
+// eigenvectors -> L.U columns.  Round-robin pairing of step `step`: index 0
+// stays, 1..N-1 rotate; the pair of position k (1 <= k < N/2) is
+// (at(k), at(N-1-k)), position 0 pairs index 0 with at(0), where
+// at(k) = 1 + (k + step) % (N - 1).
+template <int N>
+__device__ __forceinline__ int rr_at(int k, int step) { return 1 + (k + step) % (N - 1); }
+template <int N>
 __device__ __forceinline__ int rr_partner(int i, int step) {
-    if (i == 0) return rr_at(0, step);
-    const int k = (i - 1 - step + (BD_PG - 1)) % (BD_PG - 1);
-    return k == 0 ? 0 : rr_at(BD_PG - 1 - k, step);
+    if (i == 0) return rr_at<N>(0, step);
+    const int k = (i - 1 - step + (N - 1)) % (N - 1);
+    return k == 0 ? 0 : rr_at<N>(N - 1 - k, step);
 }
 
-// Parallel cyclic Jacobi on the 16x16 symmetric matrix in L.A (eigenvalues
+// Parallel cyclic Jacobi on the N x N symmetric matrix in L.A (eigenvalues
 // end on the diagonal, eigenvectors in the columns of L.U).  One step applies
-// the 8 disjoint rotations of the round-robin schedule as one two-sided update
-// A'' = J^T A J read entirely from the old A:
+// the N/2 disjoint rotations of the round-robin schedule as one two-sided
+// update A'' = J^T A J read entirely from the old A:
 //   A''[i][j] = c_j (c_i A[i][j] + s_i A[pi][j]) + s_j (c_i A[i][pj] + s_i A[pi][pj])
 //   U'[i][j]  = c_j U[i][j] + s_j U[i][pj]
-// Lane l owns column j = l & 15 of rows (l >> 4) + 4e.  A wave executes its
-// LDS instructions in order, so the old values every lane reads are read
+// Lane l owns column j = l % N of rows l / N + (64 / N) e.  A wave executes
+// its LDS instructions in order, so the old values every lane reads are read
 // before any lane writes (the asm barriers keep the compiler from moving the
 // accesses across each other): two dependent LDS round trips per step.
 // Rotation parameters use the hardware reciprocal and reciprocal square root
 // (~1 ulp): a rotation only has to reduce the off-diagonal mass, and the
 // result is checked through the quantised summary, not bit for bit.
-template <class W>
-__device__ void jacobi16(W& L) {
+template <int N, class W>
+__device__ void jacobi(W& L) {
+    static_assert(N == 16 || N == 32, "page 16 or 32");
+    constexpr int RS = kWave / N, RPL = N * N / kWave;   // row stride, rows per lane
+    constexpr int SWEEPS = N == 16 ? 12 : 16;
     const int lane = threadIdx.x & 63;
-    const int j = lane & 15, r0 = lane >> 4;
-    for (int i = lane; i < BD_PG * BD_PG; i += kWave) L.U[i / BD_PG][i % BD_PG] = (i / BD_PG == i % BD_PG) ? 1.f : 0.f;
+    const int j = lane % N, r0 = lane / N;
+    for (int i = lane; i < N * N; i += kWave) L.U[i / N][i % N] = (i / N == i % N) ? 1.f : 0.f;
     wave_lds_sync();
-    for (int sweep = 0; sweep < BD_SWEEPS; ++sweep) {
+    for (int sweep = 0; sweep < SWEEPS; ++sweep) {
         // convergence test: off-diagonal mass vs diagonal
         float off = 0.f, dia = 0.f;
-        for (int i = lane; i < BD_PG * BD_PG; i += kWave) {
-            const float a = L.A[i / BD_PG][i % BD_PG];
-            if (i / BD_PG == i % BD_PG) dia += a * a; else off += a * a;
+        for (int i = lane; i < N * N; i += kWave) {
+            const float a = L.A[i / N][i % N];
+            if (i / N == i % N) dia += a * a; else off += a * a;
         }
 #pragma unroll
         for (int o = 32; o >= 1; o >>= 1) {
@@ -177,13 +189,14 @@ __device__ void jacobi16(W& L) {
         }
         // wave-uniform (also exits on 0/0).  fp32 rounding leaves off/dia
         // near 1e-14 (asymmetric residues of order eps * |lambda|), so the
-        // bound sits above that floor: 5-6 sweeps instead of running out the
-        // sweep limit, with the same top-8 eigenvalue accuracy (~3e-6 rel).
+        // bound sits above that floor: 5-6 sweeps at N = 16 instead of
+        // running out the sweep limit, with the same top-8 eigenvalue
+        // accuracy (~3e-6 rel).
         if (!(off > 1e-12f * dia)) break;
-        for (int step = 0; step < BD_PG - 1; ++step) {
-            if (lane < BD_PG / 2) {
-                const int p = lane == 0 ? 0 : rr_at(lane, step);
-                const int q = lane == 0 ? rr_at(0, step) : rr_at(BD_PG - 1 - lane, step);
+        for (int step = 0; step < N - 1; ++step) {
+            if (lane < N / 2) {
+                const int p = lane == 0 ? 0 : rr_at<N>(lane, step);
+                const int q = lane == 0 ? rr_at<N>(0, step) : rr_at<N>(N - 1 - lane, step);
                 const float apq = L.A[p][q], app = L.A[p][p], aqq = L.A[q][q];
                 float c = 1.f, sn = 0.f;
                 if (fabsf(apq) > 1e-30f) {                 // smaller: nothing to rotate away
@@ -198,21 +211,21 @@ __device__ void jacobi16(W& L) {
                 L.cc[q] = c; L.ss[q] = sn;
             }
             asm volatile("" ::: "memory");
-            const int pj = rr_partner(j, step);
+            const int pj = rr_partner<N>(j, step);
             const float cj = L.cc[j], sj = L.ss[j];
-            float na[4], nu[4];
+            float na[RPL], nu[RPL];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int i = r0 + 4 * e, pi = rr_partner(i, step);
+            for (int e = 0; e < RPL; ++e) {
+                const int i = r0 + RS * e, pi = rr_partner<N>(i, step);
                 const float ci = L.cc[i], si = L.ss[i];
                 na[e] = cj * (ci * L.A[i][j] + si * L.A[pi][j]) + sj * (ci * L.A[i][pj] + si * L.A[pi][pj]);
                 nu[e] = cj * L.U[i][j] + sj * L.U[i][pj];
             }
             asm volatile("" ::: "memory");
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                L.A[r0 + 4 * e][j] = na[e];
-                L.U[r0 + 4 * e][j] = nu[e];
+            for (int e = 0; e < RPL; ++e) {
+                L.A[r0 + RS * e][j] = na[e];
+                L.U[r0 + RS * e][j] = nu[e];
             }
             asm volatile("" ::: "memory");
         }
@@ -220,18 +233,18 @@ __device__ void jacobi16(W& L) {
 }
 
 // eigenvalues on the diagonal of L.A -> ascending ranks -> top-8 columns
-template <class W>
+template <int N, class W>
 __device__ void select_top8(W& L) {
     const int lane = threadIdx.x & 63;
-    if (lane < BD_PG) {
+    if (lane < N) {
         const float li = L.A[lane][lane];
         int rank = 0;
-        for (int j = 0; j < BD_PG; ++j) {
+        for (int j = 0; j < N; ++j) {
             const float lj = L.A[j][j];
             rank += (lj < li) || (lj == li && j < lane);
         }
-        if (rank >= BD_PG - BD_RNK) {
-            const int r = rank - (BD_PG - BD_RNK);
+        if (rank >= N - BD_RNK) {
+            const int r = rank - (N - BD_RNK);
             L.col[r] = lane;
             L.S8[r] = __fsqrt_rn(fmaxf(li, 1e-10f));
         }
@@ -244,8 +257,8 @@ __device__ void select_top8(W& L) {
 // l * layer_rows.  n_dev, when given, is a device count of valid entries of
 // `blocks` (at most n_blocks): the refresh producers size the grid to the
 // host-known bound and the list is compacted on the device.
-template <int D>
-__global__ __launch_bounds__(bd_waves<D>() * kWave) void rki4_build_kernel(
+template <int D, int PG = 16>
+__global__ __launch_bounds__((bd_waves<D, PG>() * kWave)) void rki4_build_kernel(
     const uint16_t* __restrict__ kc, const uint64_t* __restrict__ k_layers,
     long k_sb, long k_st, long k_sh, int NB,
     const int* __restrict__ blocks, const int* __restrict__ n_dev, int n_blocks, int n_kv,
@@ -254,10 +267,10 @@ __global__ __launch_bounds__(bd_waves<D>() * kWave) void rki4_build_kernel(
     uint16_t* __restrict__ cs, int8_t* __restrict__ mu8, uint16_t* __restrict__ mus,
     uint16_t* __restrict__ tag)
 {
-    constexpr int NW = bd_waves<D>();
-    __shared__ WaveLds<D> lds[NW];
+    constexpr int NW = bd_waves<D, PG>();
+    __shared__ WaveLds<D, PG> lds[NW];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    WaveLds<D>& L = lds[wave];
+    WaveLds<D, PG>& L = lds[wave];
     const int nb_valid = n_dev ? min(*n_dev, n_blocks) : n_blocks;
     const long per_layer = (long)nb_valid * n_kv;
     // one wave per (layer, block index, kv head), grid-stride
@@ -272,8 +285,8 @@ __global__ __launch_bounds__(bd_waves<D>() * kWave) void rki4_build_kernel(
         const uint16_t* kbase = k_layers ? reinterpret_cast<const uint16_t*>(k_layers[layer]) : kc;
         const uint16_t* kp = kbase + (long)blk * k_sb + (long)kh * k_sh;
 
-        // stage K (fp32) and the centroid (sequential sum over t, then / 16)
-        for (int i = lane; i < BD_PG * D / 8; i += kWave) {
+        // stage K (fp32) and the centroid (sequential sum over t, then / PG)
+        for (int i = lane; i < PG * D / 8; i += kWave) {
             const int t = i / (D / 8), d0 = (i % (D / 8)) * 8;
             const uint4 w = *reinterpret_cast<const uint4*>(kp + (long)t * k_st + d0);
             const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
@@ -283,32 +296,39 @@ __global__ __launch_bounds__(bd_waves<D>() * kWave) void rki4_build_kernel(
                 L.dc[t][d0 + 2 * e + 1] = bf16hi(ws[e]);
             }
         }
-        if (lane < 8) tag[row * 8 + lane] = kp[(long)(BD_PG - 1) * k_st + lane];
+        if (lane < 8) tag[row * 8 + lane] = kp[(long)(PG - 1) * k_st + lane];
         wave_lds_sync();
         for (int d = lane; d < D; d += kWave) {
             float acc = 0.f;
-            for (int t = 0; t < BD_PG; ++t) acc = __fadd_rn(acc, L.dc[t][d]);
-            const float m = __fdiv_rn(acc, (float)BD_PG);
+            for (int t = 0; t < PG; ++t) acc = __fadd_rn(acc, L.dc[t][d]);
+            const float m = __fdiv_rn(acc, (float)PG);
             L.mu[d] = m;
-            for (int t = 0; t < BD_PG; ++t) L.dc[t][d] = __fsub_rn(L.dc[t][d], m);
+            for (int t = 0; t < PG; ++t) L.dc[t][d] = __fsub_rn(L.dc[t][d], m);
         }
         wave_lds_sync();
 
-        // gram on the matrix core: Gm[i][j] = sum_d dc[i][d] dc[j][d]
+        // gram on the matrix core: Gm[i][j] = sum_d dc[i][d] dc[j][d], in
+        // 16 x 16 blocks (bi, bj) of the PG x PG matrix
         {
             const int i = lane & 15, kq = lane >> 4;
-            v4f g = {0.f, 0.f, 0.f, 0.f};
-            for (int s = 0; s < D / 4; ++s) {
-                const float a = L.dc[i][4 * s + kq];
-                g = __builtin_amdgcn_mfma_f32_16x16x4f32(a, a, g, 0, 0, 0);
-            }
 #pragma unroll
-            for (int v = 0; v < 4; ++v) L.A[4 * kq + v][i] = g[v];
+            for (int bi = 0; bi < PG / 16; ++bi)
+#pragma unroll
+                for (int bj = 0; bj < PG / 16; ++bj) {
+                    v4f g = {0.f, 0.f, 0.f, 0.f};
+                    for (int s = 0; s < D / 4; ++s) {
+                        const float a = L.dc[16 * bi + i][4 * s + kq];
+                        const float b = L.dc[16 * bj + i][4 * s + kq];
+                        g = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, g, 0, 0, 0);
+                    }
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) L.A[16 * bi + 4 * kq + v][16 * bj + i] = g[v];
+                }
         }
         wave_lds_sync();
-        jacobi16(L);
-        select_top8(L);
-        pack_page<D>(L, row, v4, vs, c8, cs, mu8, mus);
+        jacobi<PG>(L);
+        select_top8<PG>(L);
+        pack_page<D, PG>(L, row, v4, vs, c8, cs, mu8, mus);
     }
 }
 
@@ -319,10 +339,10 @@ __global__ __launch_bounds__(4 * kWave) void rki4_pack_kernel(
     uint8_t* __restrict__ v4, uint16_t* __restrict__ vs, int8_t* __restrict__ c8,
     uint16_t* __restrict__ cs, int8_t* __restrict__ mu8, uint16_t* __restrict__ mus)
 {
-    constexpr int BD_D = 128;
-    __shared__ WaveLds<BD_D> lds[4];
+    constexpr int BD_D = 128, BD_PG = 16;
+    __shared__ WaveLds<BD_D, BD_PG> lds[4];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    WaveLds<BD_D>& L = lds[wave];
+    WaveLds<BD_D, BD_PG>& L = lds[wave];
     const long item = (long)blockIdx.x * 4 + wave;
     if (item >= n) return;
     for (int i = lane; i < BD_PG * BD_D; i += kWave) L.dc[i / BD_D][i % BD_D] = dc[item * BD_PG * BD_D + i];
@@ -334,7 +354,7 @@ __global__ __launch_bounds__(4 * kWave) void rki4_pack_kernel(
         L.S8[lane] = __fsqrt_rn(fmaxf(S2[item * BD_PG + c], 1e-10f));
     }
     wave_lds_sync();
-    pack_page<BD_D>(L, rows[item], v4, vs, c8, cs, mu8, mus);
+    pack_page<BD_D, BD_PG>(L, rows[item], v4, vs, c8, cs, mu8, mus);
 }
 
 // ---- refresh lifecycle: which blocks to (re)build --------------------------
@@ -415,33 +435,53 @@ __global__ __launch_bounds__(RF_THREADS) void refresh_compact_kernel(
 
 using namespace locks;
 
+// (head_dim, page) of the summary builder: {64, 128, 256} x {16, 32} (the
+// reference's rki4 geometry domain, rki4_state.py:295-324, without page 64)
+// plus the MLA latent (512, 16).
+static bool bd_geometry(int head_dim, int page) {
+    if (head_dim == 512) return page == 16;
+    return (head_dim == 64 || head_dim == 128 || head_dim == 256) && (page == 16 || page == 32);
+}
+template <int D, int PG>
+static int bd_launch(const uint16_t* kc, const uint64_t* k_layers, long k_sb, long k_st, long k_sh,
+                     int NB, const int* blocks, const int* count, int n_blocks, int n_kv,
+                     int n_layers, long layer_rows, uint8_t* v4, uint16_t* vs, int8_t* c8,
+                     uint16_t* cs, int8_t* mu8, uint16_t* mus, uint16_t* tag, hipStream_t st) {
+    constexpr int nw = bd_waves<D, PG>();
+    const long items = (long)n_blocks * n_kv * n_layers;
+    const long grid = std::min((items + nw - 1) / nw, BD_MAX_GRID);
+    hipLaunchKernelGGL((rki4_build_kernel<D, PG>), dim3((unsigned)grid), dim3(nw * kWave), 0, st,
+                       kc, k_layers, k_sb, k_st, k_sh, NB, blocks, count, n_blocks, n_kv,
+                       n_layers, layer_rows, v4, vs, c8, cs, mu8, mus, tag);
+    return check_launch("rki4_build_kernel");
+}
+#define BD_DISPATCH(HD, PGV, ...)                                              \
+    ((HD) == 512 ? bd_launch<512, 16>(__VA_ARGS__)                               \
+     : (PGV) == 16 ? ((HD) == 128 ? bd_launch<128, 16>(__VA_ARGS__)              \
+                      : (HD) == 64 ? bd_launch<64, 16>(__VA_ARGS__)              \
+                                   : bd_launch<256, 16>(__VA_ARGS__))            \
+                   : ((HD) == 128 ? bd_launch<128, 32>(__VA_ARGS__)              \
+                      : (HD) == 64 ? bd_launch<64, 32>(__VA_ARGS__)              \
+                                   : bd_launch<256, 32>(__VA_ARGS__)))
+
 extern "C" int32_t locks_build_rki4(
     const uint16_t* k_cache, int64_t k_stride_block, int64_t k_stride_tok, int64_t k_stride_head,
     int32_t num_blocks, const int32_t* blocks, int32_t n_blocks, int32_t n_kv, int32_t head_dim,
     int32_t page, uint8_t* v4, uint16_t* vs, int8_t* c8, uint16_t* cs, int8_t* mu8,
     uint16_t* mus, uint16_t* tag, void* stream)
 {
-    LOCKS_REQUIRE((head_dim == 128 || head_dim == 512) && page == BD_PG,
-                  "locks_build_rki4: geometry d=%d page=%d unsupported (this build: d 128 or 512, page 16)",
-                  head_dim, page);
+    LOCKS_REQUIRE(bd_geometry(head_dim, page),
+                  "locks_build_rki4: geometry d=%d page=%d unsupported (d 64/128/256 with page 16/32, "
+                  "or d 512 with page 16)", head_dim, page);
     LOCKS_REQUIRE(n_kv >= 1 && num_blocks >= 1 && n_blocks >= 0, "locks_build_rki4: bad geometry");
     LOCKS_REQUIRE(k_stride_tok % 8 == 0 && k_stride_block % 8 == 0 && k_stride_head % 8 == 0,
                   "locks_build_rki4: K strides must be multiples of 8 elements");
     LOCKS_REQUIRE(k_cache && blocks && v4 && vs && c8 && cs && mu8 && mus && tag,
                   "locks_build_rki4: null pointer argument");
     if (n_blocks == 0) return 0;
-    const long items = (long)n_blocks * n_kv;
-    const int nw = head_dim == 128 ? bd_waves<128>() : bd_waves<512>();
-    const long grid = std::min((items + nw - 1) / nw, BD_MAX_GRID);
-#define BUILD_LAUNCH(DV)                                                                     \
-    hipLaunchKernelGGL((rki4_build_kernel<DV>), dim3((unsigned)grid), dim3(nw * kWave), 0,  \
-                       (hipStream_t)stream, k_cache, nullptr, (long)k_stride_block,          \
-                       (long)k_stride_tok, (long)k_stride_head, num_blocks, blocks, nullptr,   \
-                       n_blocks, n_kv, 1, 0L, v4, vs, c8, cs, mu8, mus, tag)
-    if (head_dim == 128) BUILD_LAUNCH(128);
-    else BUILD_LAUNCH(512);
-#undef BUILD_LAUNCH
-    return check_launch("rki4_build_kernel");
+    return BD_DISPATCH(head_dim, page, k_cache, nullptr, (long)k_stride_block, (long)k_stride_tok,
+                       (long)k_stride_head, num_blocks, blocks, nullptr, n_blocks, n_kv, 1, 0L,
+                       v4, vs, c8, cs, mu8, mus, tag, (hipStream_t)stream);
 }
 
 extern "C" int32_t locks_pack_rki4(const float* mu, const float* dc, const float* S2,
@@ -450,8 +490,8 @@ extern "C" int32_t locks_pack_rki4(const float* mu, const float* dc, const float
                                    int8_t* c8, uint16_t* cs, int8_t* mu8, uint16_t* mus,
                                    void* stream)
 {
-    LOCKS_REQUIRE(head_dim == 128 && page == BD_PG,
-                  "locks_pack_rki4: geometry d=%d page=%d unsupported (this build: 128/16)", head_dim, page);
+    LOCKS_REQUIRE(head_dim == 128 && page == 16,
+                  "locks_pack_rki4: geometry d=%d page=%d unsupported (this entry: 128/16)", head_dim, page);
     LOCKS_REQUIRE(n >= 0, "locks_pack_rki4: n=%d < 0", n);
     LOCKS_REQUIRE(mu && dc && S2 && U && rows && v4 && vs && c8 && cs && mu8 && mus,
                   "locks_pack_rki4: null pointer argument");
@@ -510,9 +550,9 @@ extern "C" int32_t locks_build_rki4_layers(
     uint8_t* v4, uint16_t* vs, int8_t* c8, uint16_t* cs, int8_t* mu8, uint16_t* mus,
     uint16_t* tag, void* stream)
 {
-    LOCKS_REQUIRE((head_dim == 128 || head_dim == 512) && page == BD_PG,
-                  "locks_build_rki4_layers: geometry d=%d page=%d unsupported (this build: d 128 or 512, page 16)",
-                  head_dim, page);
+    LOCKS_REQUIRE(bd_geometry(head_dim, page),
+                  "locks_build_rki4_layers: geometry d=%d page=%d unsupported (d 64/128/256 with page "
+                  "16/32, or d 512 with page 16)", head_dim, page);
     LOCKS_REQUIRE(n_kv >= 1 && num_blocks >= 1 && n_blocks >= 0 && n_layers >= 1 &&
                       n_layers <= 65535 && slab_blocks >= num_blocks,
                   "locks_build_rki4_layers: bad geometry");
@@ -521,17 +561,8 @@ extern "C" int32_t locks_build_rki4_layers(
     LOCKS_REQUIRE(k_layers && blocks && v4 && vs && c8 && cs && mu8 && mus && tag,
                   "locks_build_rki4_layers: null pointer argument");
     if (n_blocks == 0) return 0;
-    const long items = (long)n_blocks * n_kv * n_layers;
-    const int nw = head_dim == 128 ? bd_waves<128>() : bd_waves<512>();
-    const long grid = std::min((items + nw - 1) / nw, BD_MAX_GRID);
     const long layer_rows = (long)slab_blocks * n_kv;
-#define BUILD_LAYERS_LAUNCH(DV)                                                              \
-    hipLaunchKernelGGL((rki4_build_kernel<DV>), dim3((unsigned)grid), dim3(nw * kWave),       \
-                       0, (hipStream_t)stream, nullptr, k_layers, (long)k_stride_block,        \
-                       (long)k_stride_tok, (long)k_stride_head, num_blocks, blocks, count,     \
-                       n_blocks, n_kv, n_layers, layer_rows, v4, vs, c8, cs, mu8, mus, tag)
-    if (head_dim == 128) BUILD_LAYERS_LAUNCH(128);
-    else BUILD_LAYERS_LAUNCH(512);
-#undef BUILD_LAYERS_LAUNCH
-    return check_launch("rki4_build_kernel");
+    return BD_DISPATCH(head_dim, page, nullptr, k_layers, (long)k_stride_block, (long)k_stride_tok,
+                       (long)k_stride_head, num_blocks, blocks, count, n_blocks, n_kv, n_layers,
+                       layer_rows, v4, vs, c8, cs, mu8, mus, tag, (hipStream_t)stream);
 }

@@ -31,36 +31,47 @@
 
 namespace locks {
 
-constexpr int SC_D = 128;     // head dim (geometry contract of this build)
-constexpr int SC_PG = 16;     // page size
 constexpr int SC_RNK = 8;     // summary rank
 constexpr int SC_TILE = 8;    // pages per wave tile
 constexpr int SC_WAVES = 4;
 constexpr int SC_BLOCK = SC_WAVES * kWave;
-constexpr int SC_VROW = SC_RNK * SC_D / 2;   // 512 B of packed V per row
 constexpr int SC_MAX_CHUNK = 1024;          // pages per workgroup, upper bound
 constexpr int SC_CPOL_NT = 2;                // buffer-load cache policy: non-temporal
-// per-wave LDS stage of one (tile, kv head) unit.  Rows are padded (V: 80 B
-// per 64-B basis row, mu: 144 B per 128-B row) so the MFMA-order reads of 16
-// rows at once hit distinct banks.
-constexpr int ST_VROWB = 80;                 // padded stride of one (page, column) V row
-constexpr int ST_VPAIR = 16 * ST_VROWB;      // 2 pages x 8 columns
-constexpr int ST_MUROWB = 144;               // padded stride of one page's mu row
-constexpr int ST_V = 0;                      // 4 pairs x 1280 B packed V
-constexpr int ST_C8 = 4 * ST_VPAIR;          // 8 pages x 128 B coefficients
-constexpr int ST_MU = ST_C8 + 1024;          // 8 pages x 144 B centroid (-> mud after use)
-constexpr int ST_CS = ST_MU + 8 * ST_MUROWB; // 8 pages x 16 token scales (f32)
-constexpr int ST_VS = ST_CS + 512;           // 8 pages x 8 column scales (f32)
-constexpr int ST_MUS = ST_VS + 256;          // 8 dwords: centroid scales (bf16 in the low half)
-constexpr int ST_BYTES = ST_MUS + 32;
-constexpr int SC_QROW = SC_D + 16;           // padded int8 q row (bank-conflict free reads)
+
+// Per-geometry layout (head_dim D in {64, 128, 256}, page PG in {16, 32}):
+// slab rows and the per-wave LDS stage of one (8-page tile, kv head) unit.
+// Stage rows are padded (+16 B) so the MFMA-order reads of 16 rows at once
+// hit distinct banks.
+template <int D, int PG>
+struct ScGeom {
+    static_assert(D == 64 || D == 128 || D == 256, "head_dim 64, 128 or 256");
+    static_assert(PG == 16 || PG == 32, "page 16 or 32");
+    static constexpr int VROW = SC_RNK * D / 2;        // packed V bytes per slab row
+    static constexpr int NVL = D / 32;                 // 1-KB V loads per unit
+    static constexpr int NCL = PG / 16;                // 1-KB coefficient loads per unit
+    static constexpr int NML = D >= 128 ? D / 128 : 1; // centroid loads per unit (D = 64: half)
+    static constexpr int NWIN = D / 64;                // 16-d windows per lane (projection MFMAs)
+    static constexpr int NTB = PG / 16;                // 16-token blocks per page
+    static constexpr int VROWB = D / 2 + 16;           // one (page, column) V row, padded
+    static constexpr int VPAIR = 16 * VROWB;           // 2 pages x 8 columns
+    static constexpr int MUROWB = D + 16;              // one page's centroid row, padded
+    static constexpr int ST_V = 0;                     // 4 pairs of packed V
+    static constexpr int ST_C8 = 4 * VPAIR;            // 8 pages x PG x 8 coefficients
+    static constexpr int ST_MU = ST_C8 + 64 * PG;      // 8 centroid rows (-> mud after use)
+    static constexpr int ST_CS = ST_MU + 8 * MUROWB;   // 8 pages x PG token scales (f32)
+    static constexpr int ST_VS = ST_CS + 32 * PG;      // 8 pages x 8 column scales (f32)
+    static constexpr int ST_MUS = ST_VS + 256;         // 8 dwords: centroid scales
+    static constexpr int ST_BYTES = ST_MUS + 32;
+    static constexpr int QROW = D + 16;                // padded int8 q row
+    static_assert(8 * MUROWB >= 8 * 16 * 4, "mud fits the centroid rows");
+};
 
 __device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d) {
     return (uint32_t)(uint8_t)a | ((uint32_t)(uint8_t)b << 8) |
            ((uint32_t)(uint8_t)c << 16) | ((uint32_t)(uint8_t)d << 24);
 }
 
-template <int GW>
+template <int GW, int D = 128, int PG = 16>
 __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
     const uint16_t* __restrict__ q, long q_sr, long q_sh,
     const uint8_t* __restrict__ v4, const uint16_t* __restrict__ vs,
@@ -70,8 +81,14 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
     const int* __restrict__ nsh, float* __restrict__ score_h, int MP,
     float* __restrict__ pmax, int n_kv, int G, float sm_scale, int chunk)
 {
+    using GM = ScGeom<D, PG>;
     constexpr int PPM = 16 / GW;            // pages per token-stage MFMA
     constexpr int NGRP = SC_TILE / PPM;     // token-stage groups per tile
+    constexpr int NVL = GM::NVL, NCL = GM::NCL, NML = GM::NML, NWIN = GM::NWIN, NTB = GM::NTB;
+    constexpr int SC_VROW = GM::VROW, ST_VROWB = GM::VROWB, ST_VPAIR = GM::VPAIR, ST_MUROWB = GM::MUROWB;
+    constexpr int ST_V = GM::ST_V, ST_C8 = GM::ST_C8, ST_MU = GM::ST_MU, ST_CS = GM::ST_CS,
+                  ST_VS = GM::ST_VS, ST_MUS = GM::ST_MUS, ST_BYTES = GM::ST_BYTES, SC_QROW = GM::QROW;
+    constexpr int LPH = D / 16;             // q lanes per head (16 dims each)
     const int z = blockIdx.x, h = blockIdx.y, r = blockIdx.z;   // page chunk, kv head, request
     const int Z = gridDim.x;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -97,13 +114,13 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
     // ---- prologue: q rows and block ids are fetched together; the first
     // unit's summary loads are issued before q is quantized, so the
     // quantization overlaps them.
-    // q: 8 consecutive lanes per head, 16 dims (two 16-byte loads) per lane
-    // (G <= 16 heads x 8 chunks <= 128 threads)
+    // q: D / 16 consecutive lanes per head, 16 dims (two 16-byte loads) per
+    // lane (G <= 16 heads x D / 16 lanes <= 256 threads)
     // Unconditional loads (threads past the group re-read its last head and
     // are never stored): a guarded load would make the compiler wait for it
     // at the branch join, before the block ids below are even requested.
-    const int qg = tid >> 3;                                  // this thread's head in the group
-    const uint4* qp = reinterpret_cast<const uint4*>(q + (long)r * q_sr + (long)(h * G + min(qg, G - 1)) * q_sh + (tid & 7) * 16);
+    const int qg = tid / LPH;                                 // this thread's head in the group
+    const uint4* qp = reinterpret_cast<const uint4*>(q + (long)r * q_sr + (long)(h * G + min(qg, G - 1)) * q_sh + (tid % LPH) * 16);
     const uint4 qa0 = qp[0], qa1 = qp[1];
     for (int i = tid; i < c1 - c0; i += SC_BLOCK) {
         const int b = bt[(long)r * bt_sr + min(c0 + i, bt_cols - 1)];
@@ -130,7 +147,7 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
     // ahead of the one being scored, then written to this wave's LDS stage
     // and read back in MFMA operand order.  Consecutive units are the kv
     // heads of one tile, whose slab rows are adjacent.
-    uint4 fv0, fv1, fv2, fv3, fc8, fmu, fcs, fvs;
+    uint4 fv[NVL], fc8[NCL], fmu[NML], fcs, fvs;
     uint32_t fmus;
     // The six slabs are read through buffer loads: the large rows (packed V,
     // coefficients, centroid: 768 of 818 B per row) with the non-temporal
@@ -153,20 +170,26 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
         const int last = min(SC_TILE, c1 - c0 - p0) - 1;
         const int* bl = bt_l + p0;
         auto row_of = [&](int i) -> uint32_t { return (uint32_t)bl[min(i, last)] * (uint32_t)n_kv + (uint32_t)h; };
-        // 2 pages x 512 B of packed V per load
-        const uint32_t vo = (lane & 31) * 16;
-        fv0 = ld_big(rs_v4, row_of(0 + (lane >> 5)) * SC_VROW + vo);
-        fv1 = ld_big(rs_v4, row_of(2 + (lane >> 5)) * SC_VROW + vo);
-        fv2 = ld_big(rs_v4, row_of(4 + (lane >> 5)) * SC_VROW + vo);
-        fv3 = ld_big(rs_v4, row_of(6 + (lane >> 5)) * SC_VROW + vo);
-        {
-            const uint32_t row = row_of(lane >> 3);   // 8 pages x 128 B
-            fc8 = ld_big(rs_c8, row * (SC_PG * SC_RNK) + (lane & 7) * 16);
-            fmu = ld_big(rs_mu, row * SC_D + (lane & 7) * 16);
+        // 1 KB per load in natural order: byte o = 1024 i + 16 lane of the
+        // unit's (page-major) rows
+#pragma unroll
+        for (int i = 0; i < NVL; ++i) {                 // packed V: 8 pages x SC_VROW
+            const int o = 1024 * i + 16 * lane;
+            fv[i] = ld_big(rs_v4, row_of(o / SC_VROW) * SC_VROW + o % SC_VROW);
         }
-        if (lane < 16) {                              // 8 pages x 32 B token scales
-            const uint32_t row = row_of(lane >> 1);
-            fcs = ld_small(rs_cs, row * (SC_PG * 2) + (lane & 1) * 16);
+#pragma unroll
+        for (int i = 0; i < NCL; ++i) {                 // coefficients: 8 pages x PG x 8
+            const int o = 1024 * i + 16 * lane;
+            fc8[i] = ld_big(rs_c8, row_of(o / (PG * SC_RNK)) * (PG * SC_RNK) + o % (PG * SC_RNK));
+        }
+#pragma unroll
+        for (int i = 0; i < NML; ++i) {                 // centroid: 8 pages x D
+            const int o = 1024 * i + 16 * lane;
+            if (D >= 128 || lane < 32) fmu[i] = ld_big(rs_mu, row_of(o / D) * D + o % D);
+        }
+        if (lane < PG) {                              // 8 pages x PG x 2 B token scales
+            const int o = 16 * lane;
+            fcs = ld_small(rs_cs, row_of(o / (2 * PG)) * (2 * PG) + o % (2 * PG));
         }
         if (lane < 8) {                               // 8 pages x 16 B column scales
             const uint32_t row = row_of(lane);
@@ -175,15 +198,23 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
         }
     };
     auto store_unit = [&](uint8_t* stg) {
-        // natural lane L of a pair: page L >> 5, column (L >> 2) & 7, chunk L & 3
-        const int vofs = ((lane >> 5) * 8 + ((lane >> 2) & 7)) * ST_VROWB + (lane & 3) * 16;
-        *reinterpret_cast<uint4*>(stg + ST_V + 0 * ST_VPAIR + vofs) = fv0;
-        *reinterpret_cast<uint4*>(stg + ST_V + 1 * ST_VPAIR + vofs) = fv1;
-        *reinterpret_cast<uint4*>(stg + ST_V + 2 * ST_VPAIR + vofs) = fv2;
-        *reinterpret_cast<uint4*>(stg + ST_V + 3 * ST_VPAIR + vofs) = fv3;
-        *reinterpret_cast<uint4*>(stg + ST_C8 + lane * 16) = fc8;
-        *reinterpret_cast<uint4*>(stg + ST_MU + (lane >> 3) * ST_MUROWB + (lane & 7) * 16) = fmu;
-        if (lane < 16) {                              // token scales widened to f32 once
+#pragma unroll
+        for (int i = 0; i < NVL; ++i) {               // byte o -> page, basis column, chunk
+            const int o = 1024 * i + 16 * lane;
+            const int pg = o / SC_VROW, w = o % SC_VROW;
+            *reinterpret_cast<uint4*>(stg + ST_V + (pg >> 1) * ST_VPAIR +
+                                      ((pg & 1) * 8 + w / (D / 2)) * ST_VROWB + w % (D / 2)) = fv[i];
+        }
+#pragma unroll
+        for (int i = 0; i < NCL; ++i)
+            *reinterpret_cast<uint4*>(stg + ST_C8 + 1024 * i + lane * 16) = fc8[i];
+#pragma unroll
+        for (int i = 0; i < NML; ++i) {
+            const int o = 1024 * i + 16 * lane;
+            if (D >= 128 || lane < 32)
+                *reinterpret_cast<uint4*>(stg + ST_MU + (o / D) * ST_MUROWB + o % D) = fmu[i];
+        }
+        if (lane < PG) {                              // token scales widened to f32 once
             *reinterpret_cast<float4*>(stg + ST_CS + lane * 32) =
                 make_float4(bf16lo(fcs.x), bf16hi(fcs.x), bf16lo(fcs.y), bf16hi(fcs.y));
             *reinterpret_cast<float4*>(stg + ST_CS + lane * 32 + 16) =
@@ -205,7 +236,7 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
     // within 2 ulp of it, which decides the rounding unless the product lies
     // within 2^-15 of a half-integer; those (rare) lanes redo the division.
     const float s2 = sm_scale * 1.4426950408889634f;           // tokens in log2 units
-    if (wave < 2) {                                           // threads 0..127: 16 heads x 8 chunks
+    if (tid < 16 * LPH) {                                     // 16 heads x D / 16 lanes
         const int c = tid, hq = qg;
         const uint32_t w[8] = {qa0.x, qa0.y, qa0.z, qa0.w, qa1.x, qa1.y, qa1.z, qa1.w};
         float f[16];
@@ -214,9 +245,8 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
         float am = 0.f;
 #pragma unroll
         for (int k = 0; k < 16; ++k) am = fmaxf(am, fabsf(f[k]));
-        am = fmaxf(am, __shfl_xor(am, 1, kWave));
-        am = fmaxf(am, __shfl_xor(am, 2, kWave));
-        am = fmaxf(am, __shfl_xor(am, 4, kWave));
+#pragma unroll
+        for (int o = 1; o < LPH; o <<= 1) am = fmaxf(am, __shfl_xor(am, o, kWave));
         const float qs = fmaxf(am, 1e-8f) / 127.f;
         const float inv = 1.f / qs;
         int iq[16];
@@ -235,10 +265,10 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
             }
         }
         if (hq < G) {
-            *reinterpret_cast<uint4*>(&q8s[hq][(c & 7) * 16]) =
+            *reinterpret_cast<uint4*>(&q8s[hq][(c % LPH) * 16]) =
                 make_uint4(pack4_i8(iq[0], iq[1], iq[2], iq[3]), pack4_i8(iq[4], iq[5], iq[6], iq[7]),
                            pack4_i8(iq[8], iq[9], iq[10], iq[11]), pack4_i8(iq[12], iq[13], iq[14], iq[15]));
-            if ((c & 7) == 0) qsp[hq] = qs * s2;
+            if (c % LPH == 0) qsp[hq] = qs * s2;
         }
     }
     __syncthreads();
@@ -247,22 +277,21 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
     // same for every unit of the workgroup):
     // Bq = projection B (column j <-> head j % GW, replicated over the
     // GW-wide page slots), Amu = centroid A (row <-> head, zero padded)
-    v4i Bq[2], Amu[2];
+    v4i Bq[NWIN], Amu[NWIN];
     {
+        // lane group kg covers d in [kg D / 4, (kg + 1) D / 4): NWIN windows of 16
         const int gq = r16 % GW;
         const int rowq = (gq < G) ? gq : G;                   // G.. = zero rows
         const int rowm = (r16 < G) ? r16 : G;
-        const uint4 n0 = *reinterpret_cast<const uint4*>(&q8s[rowq][32 * kg]);
-        const uint4 n1 = *reinterpret_cast<const uint4*>(&q8s[rowq][32 * kg + 16]);
-        const uint4 m0 = *reinterpret_cast<const uint4*>(&q8s[rowm][32 * kg]);
-        const uint4 m1 = *reinterpret_cast<const uint4*>(&q8s[rowm][32 * kg + 16]);
-        Amu[0] = v4i{(int)m0.x, (int)m0.y, (int)m0.z, (int)m0.w};
-        Amu[1] = v4i{(int)m1.x, (int)m1.y, (int)m1.z, (int)m1.w};
-        // V operand order inside a 16-d window: even d (low nibbles), then odd d
-        Bq[0] = v4i{(int)__builtin_amdgcn_perm(n0.y, n0.x, 0x06040200u), (int)__builtin_amdgcn_perm(n0.w, n0.z, 0x06040200u),
-                    (int)__builtin_amdgcn_perm(n0.y, n0.x, 0x07050301u), (int)__builtin_amdgcn_perm(n0.w, n0.z, 0x07050301u)};
-        Bq[1] = v4i{(int)__builtin_amdgcn_perm(n1.y, n1.x, 0x06040200u), (int)__builtin_amdgcn_perm(n1.w, n1.z, 0x06040200u),
-                    (int)__builtin_amdgcn_perm(n1.y, n1.x, 0x07050301u), (int)__builtin_amdgcn_perm(n1.w, n1.z, 0x07050301u)};
+#pragma unroll
+        for (int w = 0; w < NWIN; ++w) {
+            const uint4 n0 = *reinterpret_cast<const uint4*>(&q8s[rowq][kg * (D / 4) + 16 * w]);
+            const uint4 m0 = *reinterpret_cast<const uint4*>(&q8s[rowm][kg * (D / 4) + 16 * w]);
+            Amu[w] = v4i{(int)m0.x, (int)m0.y, (int)m0.z, (int)m0.w};
+            // V operand order inside a 16-d window: even d (low nibbles), then odd d
+            Bq[w] = v4i{(int)__builtin_amdgcn_perm(n0.y, n0.x, 0x06040200u), (int)__builtin_amdgcn_perm(n0.w, n0.z, 0x06040200u),
+                        (int)__builtin_amdgcn_perm(n0.y, n0.x, 0x07050301u), (int)__builtin_amdgcn_perm(n0.w, n0.z, 0x07050301u)};
+        }
     }
     const float4 qsl = *reinterpret_cast<const float4*>(&qsp[4 * kg]);   // rows 4kg.. (mud)
     // column head's q scale x 1/16 (the nibble shift), zeroed where the
@@ -292,21 +321,35 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
         // which is exactly the B operand the token stage needs (its k-slot
         // kg, step hh reads column 2kg + hh), so qt never goes through LDS.
         const int i_pg = r16 & 1, i_c = 2 * (r16 >> 2) + ((r16 >> 1) & 1);
-        uint4 vv[4];
+        // lane group kg reads D / 8 packed bytes (d in [kg D / 4, (kg + 1) D / 4))
+        uint32_t vv[4][D / 32];
         float2 vsf[4][2];
 #pragma unroll
         for (int pp = 0; pp < 4; ++pp) {
-            vv[pp] = *reinterpret_cast<const uint4*>(stg + ST_V + pp * ST_VPAIR + (i_pg * 8 + i_c) * ST_VROWB + kg * 16);
+            const uint8_t* vp = stg + ST_V + pp * ST_VPAIR + (i_pg * 8 + i_c) * ST_VROWB + kg * (D / 8);
+            if constexpr (D == 64) {
+                const uint2 x = *reinterpret_cast<const uint2*>(vp);
+                vv[pp][0] = x.x; vv[pp][1] = x.y;
+            } else {
+#pragma unroll
+                for (int k = 0; k < D / 128; ++k) {
+                    const uint4 x = *reinterpret_cast<const uint4*>(vp + 16 * k);
+                    vv[pp][4 * k] = x.x; vv[pp][4 * k + 1] = x.y; vv[pp][4 * k + 2] = x.z; vv[pp][4 * k + 3] = x.w;
+                }
+            }
 #pragma unroll
             for (int pg = 0; pg < 2; ++pg)          // column scales (2kg, 2kg+1) of page 2pp+pg
                 vsf[pp][pg] = *reinterpret_cast<const float2*>(stg + ST_VS + (2 * pp + pg) * 32 + kg * 8);
         }
-        v4i mu0 = {0, 0, 0, 0}, mu1 = {0, 0, 0, 0};
+        v4i mu[NWIN];
         float musf = 0.f;
+#pragma unroll
+        for (int w = 0; w < NWIN; ++w) mu[w] = v4i{0, 0, 0, 0};
         if ((lane & 15) < 8) {
             const int pg = lane & 15;
-            mu0 = *reinterpret_cast<const v4i*>(stg + ST_MU + pg * ST_MUROWB + kg * 32);
-            mu1 = *reinterpret_cast<const v4i*>(stg + ST_MU + pg * ST_MUROWB + kg * 32 + 16);
+#pragma unroll
+            for (int w = 0; w < NWIN; ++w)
+                mu[w] = *reinterpret_cast<const v4i*>(stg + ST_MU + pg * ST_MUROWB + kg * (D / 4) + 16 * w);
             musf = bf16lo(*reinterpret_cast<const uint32_t*>(stg + ST_MUS + pg * 4));
         }
         wave_lds_sync();                               // mu consumed: reuse as mud
@@ -315,12 +358,13 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
 #pragma unroll
         for (int pp = 0; pp < 4; ++pp) {
             // signed nibbles moved to the high half of each byte: 16 * V as int8
-            const uint32_t w0 = vv[pp].x, w1 = vv[pp].y, w2 = vv[pp].z, w3 = vv[pp].w;
-            const v4i a0 = {(int)((w0 << 4) & MH), (int)((w1 << 4) & MH), (int)(w0 & MH), (int)(w1 & MH)};
-            const v4i a1 = {(int)((w2 << 4) & MH), (int)((w3 << 4) & MH), (int)(w2 & MH), (int)(w3 & MH)};
             v4i acc = {0, 0, 0, 0};
-            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, Bq[0], acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, Bq[1], acc, 0, 0, 0);
+#pragma unroll
+            for (int w = 0; w < NWIN; ++w) {
+                const uint32_t w0 = vv[pp][2 * w], w1 = vv[pp][2 * w + 1];
+                const v4i a = {(int)((w0 << 4) & MH), (int)((w1 << 4) & MH), (int)(w0 & MH), (int)(w1 & MH)};
+                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, Bq[w], acc, 0, 0, 0);
+            }
             // acc = 16 * sum_d V q8 exactly (|acc| < 2^22): the 1/16 rides on
             // the column scale, a power of two, so qt is exact to the same bits
 #pragma unroll
@@ -331,8 +375,9 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
         }
         {
             v4i accm = {0, 0, 0, 0};
-            accm = __builtin_amdgcn_mfma_i32_16x16x64_i8(Amu[0], mu0, accm, 0, 0, 0);
-            accm = __builtin_amdgcn_mfma_i32_16x16x64_i8(Amu[1], mu1, accm, 0, 0, 0);
+#pragma unroll
+            for (int w = 0; w < NWIN; ++w)
+                accm = __builtin_amdgcn_mfma_i32_16x16x64_i8(Amu[w], mu[w], accm, 0, 0, 0);
             if ((lane & 15) < 8) {
                 float4 md;
                 md.x = (float)accm[0] * qsl.x * musf;
@@ -344,20 +389,22 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
         }
         wave_lds_sync();
 
-        // ---- token reconstruction + 16-token LSE per (page, head) --------
-        // k-slot kg, step hh <-> basis column 2kg + hh (both operands)
-        auto tok_group = [&](int gi) -> v4f {        // cs * (C8 qt) of group gi, 4 tokens
+        // ---- token reconstruction + PG-token LSE per (page, head) --------
+        // k-slot kg, step hh <-> basis column 2kg + hh (both operands);
+        // tokens in blocks of 16 (tb < PG / 16)
+        auto tok_group = [&](int gi, int tb) -> v4f {   // cs * (C8 qt) of group gi, 4 tokens
             v4f acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ps = 0; ps < PPM; ++ps) {
                 const int page = gi * PPM + ps;
-                const uint32_t cw = *reinterpret_cast<const uint16_t*>(stg + ST_C8 + page * 128 + r16 * 8 + 2 * kg);
+                const uint32_t cw = *reinterpret_cast<const uint16_t*>(stg + ST_C8 + page * (PG * SC_RNK) +
+                                                                       (16 * tb + r16) * 8 + 2 * kg);
                 const float a0 = (float)(int8_t)cw, a1 = (float)(int8_t)(cw >> 8);
                 // qt is already zero where this lane's column is not page slot ps
                 acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, qt[page >> 1][page & 1], acc, 0, 0, 0);
                 acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, qt[page >> 1][2 + (page & 1)], acc, 0, 0, 0);
             }
-            const float4 csf = *reinterpret_cast<const float4*>(stg + ST_CS + (gi * PPM + psub_l) * 64 + kg * 16);
+            const float4 csf = *reinterpret_cast<const float4*>(stg + ST_CS + ((gi * PPM + psub_l) * PG + 16 * tb) * 4 + kg * 16);
             return v4f{acc[0] * csf.x, acc[1] * csf.y, acc[2] * csf.z, acc[3] * csf.w};
         };
         // 16-token LSE taken relative to the centroid term: tok - mud =
@@ -374,9 +421,13 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
         float ev[NGRP];
 #pragma unroll
         for (int gi = 0; gi < NGRP; ++gi) {
-            const v4f x = tok_group(gi);
-            ev[gi] = __builtin_amdgcn_exp2f(x[0]) + __builtin_amdgcn_exp2f(x[1]) +
-                     __builtin_amdgcn_exp2f(x[2]) + __builtin_amdgcn_exp2f(x[3]);
+            ev[gi] = 0.f;
+#pragma unroll
+            for (int tb = 0; tb < NTB; ++tb) {
+                const v4f x = tok_group(gi, tb);
+                ev[gi] += __builtin_amdgcn_exp2f(x[0]) + __builtin_amdgcn_exp2f(x[1]) +
+                          __builtin_amdgcn_exp2f(x[2]) + __builtin_amdgcn_exp2f(x[3]);
+            }
         }
         float tot[NSET];
 #pragma unroll
@@ -409,10 +460,19 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
             float Sa[NGRP];
 #pragma unroll
             for (int gi = 0; gi < NGRP; ++gi) {
-                const v4f x = tok_group(gi);
-                const float m = xor32_max(xor16_max(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]))));
-                float f = __builtin_amdgcn_exp2f(x[0] - m) + __builtin_amdgcn_exp2f(x[1] - m) +
-                          __builtin_amdgcn_exp2f(x[2] - m) + __builtin_amdgcn_exp2f(x[3] - m);
+                v4f x[NTB];
+                float m = -INFINITY;
+#pragma unroll
+                for (int tb = 0; tb < NTB; ++tb) {
+                    x[tb] = tok_group(gi, tb);
+                    m = fmaxf(m, fmaxf(fmaxf(x[tb][0], x[tb][1]), fmaxf(x[tb][2], x[tb][3])));
+                }
+                m = xor32_max(xor16_max(m));
+                float f = 0.f;
+#pragma unroll
+                for (int tb = 0; tb < NTB; ++tb)
+                    f += __builtin_amdgcn_exp2f(x[tb][0] - m) + __builtin_amdgcn_exp2f(x[tb][1] - m) +
+                         __builtin_amdgcn_exp2f(x[tb][2] - m) + __builtin_amdgcn_exp2f(x[tb][3] - m);
                 f = xor32_sum(xor16_sum(f));
                 Sa[gi] = ((mud_w[(gi * PPM + psub_l) * 16 + g_l] + m) + __builtin_amdgcn_logf(f)) * 0.6931471805599453f;
             }
@@ -480,14 +540,14 @@ extern "C" int32_t locks_score_rki4(
     int32_t n_req, int32_t n_kv, int32_t G, int32_t head_dim, int32_t page,
     float sm_scale, void* stream)
 {
-    LOCKS_REQUIRE(head_dim == SC_D, "locks_score_rki4: head_dim %d unsupported (this build: 128)", head_dim);
-    LOCKS_REQUIRE(page == SC_PG, "locks_score_rki4: page %d unsupported (this build: 16)", page);
+    LOCKS_REQUIRE((head_dim == 64 || head_dim == 128 || head_dim == 256) && (page == 16 || page == 32),
+                  "locks_score_rki4: head_dim %d / page %d outside {64,128,256} x {16,32}", head_dim, page);
     LOCKS_REQUIRE(G >= 1 && G <= 16, "locks_score_rki4: G=%d outside [1, 16]", G);
     LOCKS_REQUIRE(n_req >= 0 && n_req <= 65535 && n_kv >= 1 && n_kv <= 65535,
                   "locks_score_rki4: n_req=%d / n_kv=%d outside the grid limits", n_req, n_kv);
     LOCKS_REQUIRE(q_stride_head % 8 == 0 && q_stride_req % 8 == 0,
                   "locks_score_rki4: q strides must be multiples of 8 elements (16-byte loads)");
-    LOCKS_REQUIRE((long)num_blocks * n_kv * SC_VROW < (1L << 32),
+    LOCKS_REQUIRE((long)num_blocks * n_kv * (SC_RNK * head_dim / 2) < (1L << 32),
                   "locks_score_rki4: slab too large for 32-bit offsets");
     LOCKS_REQUIRE(num_blocks >= 1 && bt_cols >= 1 && max_pages >= 1,
                   "locks_score_rki4: empty geometry (num_blocks=%d bt_cols=%d max_pages=%d)",
@@ -500,16 +560,29 @@ extern "C" int32_t locks_score_rki4(
     if (n_req == 0) return 0;
     const int Z = cdiv(max_pages, chunk);
     dim3 grid(Z, n_kv, n_req);
-    const size_t dyn = (size_t)(G + 16) * SC_QROW + (size_t)chunk * sizeof(int);
+    const size_t dyn = (size_t)(G + 16) * (head_dim + 16) + (size_t)chunk * sizeof(int);
     hipStream_t st = (hipStream_t)stream;
-#define LAUNCH(GWV)                                                                    \
-    hipLaunchKernelGGL((rki4_score_kernel<GWV>), grid, dim3(SC_BLOCK), dyn, st, q, \
-                       (long)q_stride_req, (long)q_stride_head, v4, vs, c8, cs, mu8, mus, \
-                       num_blocks, block_table, (long)bt_stride, bt_cols, n_sel_hi,       \
+#define LAUNCH(GWV, DV, PGV)                                                                   \
+    hipLaunchKernelGGL((rki4_score_kernel<GWV, DV, PGV>), grid, dim3(SC_BLOCK), dyn, st, q, \
+                       (long)q_stride_req, (long)q_stride_head, v4, vs, c8, cs, mu8, mus,      \
+                       num_blocks, block_table, (long)bt_stride, bt_cols, n_sel_hi,            \
                        score_h, max_pages, page_max, n_kv, G, sm_scale, chunk)
-    if (G <= 4) LAUNCH(4);
-    else if (G <= 8) LAUNCH(8);
-    else LAUNCH(16);
+#define LAUNCH_G(DV, PGV)                     \
+    do {                                      \
+        if (G <= 4) LAUNCH(4, DV, PGV);       \
+        else if (G <= 8) LAUNCH(8, DV, PGV);  \
+        else LAUNCH(16, DV, PGV);             \
+    } while (0)
+    if (page == 16) {
+        if (head_dim == 128) LAUNCH_G(128, 16);
+        else if (head_dim == 64) LAUNCH_G(64, 16);
+        else LAUNCH_G(256, 16);
+    } else {
+        if (head_dim == 128) LAUNCH_G(128, 32);
+        else if (head_dim == 64) LAUNCH_G(64, 32);
+        else LAUNCH_G(256, 32);
+    }
+#undef LAUNCH_G
 #undef LAUNCH
     return check_launch("rki4_score_kernel");
 }

@@ -1,7 +1,7 @@
 """rki4 summary build (off the hot path): finalized K pages -> six slabs.
 
 Runs on the GPU through ``locks_build_rki4`` (gram on the matrix core,
-16x16 parallel Jacobi eigensolver, quantize/pack), following the reference
+page x page parallel Jacobi eigensolver, quantize/pack), following the reference
 builder's op sequence (src/locks/selection/rki4_build.py:147-158 _write_pre,
 :93-129 eigh, :178-225 _write_post, :161-175 int4 pack).  The lifecycle
 entry ``rki4_build_refresh`` mirrors rki4_build.py:318-364 (content-tag

@@ -114,3 +114,142 @@ def test_dense_geometry(hd, page):
                  scale=case.scale)
     torch.cuda.synchronize()
     _check(case, out, tab, cnt)
+
+
+# ---- summaries (build + scorer) and the whole step at the other geometries ----
+SUMMARY_GEOMS = [(64, 16), (256, 16), (128, 32), (64, 32), (256, 32)]
+
+
+def _state(case, *, L=1, budget_pages=40, split=64):
+    import torch
+    from locks.attention import ensure_stage_b_buffers
+    from locks.selection import Rki4State
+    st = Rki4State("cuda", num_layers=L, num_blocks=case.NB, n_kv=case.n_kv, G=case.G,
+                   head_dim=case.d, page=case.page, max_reqs=case.R, max_pages=case.MP,
+                   budget=0.1, budget_pages=budget_pages, sink_pages=1, window_pages=1)
+    ensure_stage_b_buffers(st, torch.device("cuda"), split)
+    return st
+
+
+@pytest.mark.parametrize("hd,page", SUMMARY_GEOMS)
+@pytest.mark.parametrize("n_kv,G,seq_lens", [(2, 4, [6000]), (2, 16, [4100, 700, 33])])
+def test_score_geometry(hd, page, n_kv, G, seq_lens):
+    """Scorer vs the oracle's fp32 twin and its exact (float64) integer path,
+    same bar as at d = 128 / page 16 (2e-5), plus the per-chunk maxima."""
+    import torch
+    from locks.selection import derive_page_params, rki4_score_only
+    from tests.cases import load_slabs
+    say("score geometry", hd, page, n_kv, G, seq_lens)
+    case = make_case(31, n_kv, G, seq_lens, page=page, d=hd)
+    st = _state(case)
+    load_slabs(st, 0, case.slabs)
+    d = to_dev(case)
+    derive_page_params(st, d["sl"], case.R)
+    rki4_score_only(st, 0, d["q"], d["bt"], d["sl"], case.R, case.scale)
+    torch.cuda.synchronize()
+    npg, nsh, b = O.derive_page_params(case.seq_lens, page, 1, 1, 40, 0.1)
+    ref = O.score_rki4_twin(case.q, case.slabs, case.bt, nsh, n_kv, G, case.scale, case.MP)
+    ref64 = O.score_rki4_intpath(case.q, case.slabs, case.bt, nsh, n_kv, G, case.scale,
+                                 case.MP, dtype=np.float64)
+    got = st.score_h.cpu().numpy()
+    pm = st.page_max.cpu().numpy()
+    for r in range(case.R):
+        P = int(nsh[r])
+        err = np.abs(got[r, ..., :P] - ref[r, ..., :P]).max() if P else 0.0
+        err64 = np.abs(got[r, ..., :P] - ref64[r, ..., :P]).max() if P else 0.0
+        say(f"row {r}: max|gpu-twin|={err:.3e} max|gpu-exact|={err64:.3e}")
+        assert err <= 2e-5 and err64 <= 2e-5
+        for z in range(st.score_chunks):
+            lo, hi = z * st.score_chunk, min((z + 1) * st.score_chunk, P)
+            for kh in range(n_kv):
+                for g in range(G):
+                    exp = got[r, kh, g, lo:hi].max() if hi > lo else -np.inf
+                    assert pm[r, kh, z, g] == exp
+
+
+@pytest.mark.parametrize("hd,page", SUMMARY_GEOMS)
+def test_build_geometry(hd, page):
+    """GPU summary build vs the oracle build (LAPACK eigh): the centroid bytes
+    and the tag exactly; the reconstruction C V^T within 0.01 of the oracle
+    build's relative error; the page scores of the two builds close."""
+    import torch
+    from locks.selection.rki4_build import rki4_build_blocks
+    say("build geometry", hd, page)
+    n_kv, G, npages = 2, 4, 300
+    case = make_case(32, n_kv, G, [page * npages], page=page, d=hd)
+    d = to_dev(case)
+    st = _state(case)
+    b = np.unique(case.bt[0, :npages]).astype(np.int64)
+    rki4_build_blocks(st, 0, d["kv"][:, 0], torch.from_numpy(b))
+    torch.cuda.synchronize()
+    got = {}
+    for n, a, bf in (("v4", "pp_v4", 0), ("vs", "pp_vs", 1), ("c8", "pp_c8", 0),
+                     ("cs", "pp_cs", 1), ("mu8", "pp_mu8", 0), ("mus", "pp_mus", 1),
+                     ("tag", "pp_tag", 1)):
+        t = getattr(st, a)[0]
+        x = (t.view(torch.int16) if bf else t).cpu().numpy()
+        got[n] = x.view(np.uint16) if bf else x
+    ref = case.slabs
+    assert np.array_equal(got["mu8"][b], ref["mu8"][b]) and np.array_equal(got["mus"][b], ref["mus"][b])
+    assert np.array_equal(got["tag"][b], case.k[b, page - 1, :, :8])
+
+    def recon(s):
+        V = O.unpack_i4(s["v4"][b]).astype(np.float64) * O.bf16_to_f32(s["vs"][b])[..., None]
+        C = s["c8"][b].astype(np.float64) * O.bf16_to_f32(s["cs"][b])[..., None]
+        return np.einsum("nktr,nkrd->nktd", C, V)
+    _, _, dc, _ = O.summary_pre(case.k[b])
+    eg = np.linalg.norm(recon(got) - dc) / np.linalg.norm(dc)
+    er = np.linalg.norm(recon(ref) - dc) / np.linalg.norm(dc)
+    say(f"reconstruction error gpu {eg:.4f} oracle {er:.4f}")
+    assert abs(eg - er) < 0.01 and eg < 0.9
+    npg, nsh, _ = O.derive_page_params(case.seq_lens, page, 1, 1, 40, 0.1)
+    sg = O.score_rki4_twin(case.q, got, case.bt, nsh, n_kv, G, case.scale, case.MP)
+    so = O.score_rki4_twin(case.q, ref, case.bt, nsh, n_kv, G, case.scale, case.MP)
+    P = int(nsh[0])
+    diff = np.abs(sg[..., :P] - so[..., :P])
+    say(f"score |gpu-build - oracle-build| max {diff.max():.3e} mean {diff.mean():.3e}")
+    assert diff.mean() < 0.02 and diff.max() < 0.5
+
+
+@pytest.mark.parametrize("hd,page", [(64, 16), (256, 32), (128, 32)])
+def test_step_geometry(hd, page):
+    """The reference's call sites (select adapter + decode dispatch) on one
+    layer at another geometry vs the oracle pipeline: page tables equal up
+    to near-ties of the b-th score, attention within the bf16 bar."""
+    import torch
+    from locks.backend import _runtime
+    from locks.config import LocksConfig
+    from locks.selection import derive_page_params
+    from tests.cases import load_slabs
+    say("step geometry", hd, page)
+    n_kv, G, sl = 2, 8, [9000, 2500]
+    case = make_case(33, n_kv, G, sl, page=page, d=hd)
+    st = _state(case, L=2)
+    load_slabs(st, 1, case.slabs)
+    d = to_dev(case)
+    kv = d["kv"]
+    st._layer_of = {kv.data_ptr(): 1}
+    cfg = LocksConfig(budget_pages=40)
+    derive_page_params(st, d["sl"], case.R)
+    out = torch.zeros((case.R, n_kv * G, hd), dtype=torch.bfloat16, device="cuda")
+    _runtime._rki4_select_adapter(d["q"], kv, d["bt"], d["sl"], st, case.R, case.scale, cfg)
+    _runtime.decode_dispatch(d["q"], kv, d["bt"], d["sl"], st, out, None, case.scale, cfg)
+    torch.cuda.synchronize()
+    npg, nsh, b = O.derive_page_params(case.seq_lens, page, 1, 1, 40, 0.1)
+    sh = O.score_rki4_twin(case.q, case.slabs, case.bt, nsh, n_kv, G, case.scale, case.MP)
+    comb = O.combine_nrm(sh, nsh)
+    tab, cnt = O.topb_select(comb, npg, nsh, b, 1, case.MP)
+    gtab, gcnt = st.page_table.cpu().numpy(), st.page_cnt.cpu().numpy()
+    n_diff = 0
+    for r in range(case.R):
+        for kh in range(n_kv):
+            a = set(gtab[r, kh, :gcnt[r, kh]].tolist())
+            e = set(tab[r, kh, :cnt[r, kh]].tolist())
+            if a != e:
+                assert gcnt[r, kh] == cnt[r, kh]
+                tau = np.sort(comb[r, kh, 1:nsh[r]])[::-1][b[r] - 1]
+                for p in a ^ e:
+                    assert abs(comb[r, kh, p] - tau) <= 1e-5 * max(abs(tau), 1e-30)
+                    n_diff += 1
+    say("near-tie differences:", n_diff)
+    _check(case, out, gtab, gcnt)

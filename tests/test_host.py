@@ -72,9 +72,13 @@ def test_ctypes_signatures_match_the_header():
 def test_rejects_bad_geometry_without_device():
     from locks import _lib
     lib = _lib.load()
-    args = [0, 0, 0] + [1] * 6 + [1, 1, 0, 1, 1, 1, 16, 1, 32, 1, 2, 4, 64, 16, 0.1, None]
-    rc = lib.locks_score_rki4(*args)           # head_dim 64 is outside the contract
-    assert rc == -1 and b"head_dim 64" in lib.locks_last_error()
+    args = [0, 0, 0] + [1] * 6 + [1, 1, 0, 1, 1, 1, 16, 1, 32, 1, 2, 4, 96, 16, 0.1, None]
+    rc = lib.locks_score_rki4(*args)           # head_dim 96 is outside the contract
+    assert rc == -1 and b"head_dim 96" in lib.locks_last_error()
+    args[-4] = 64
+    args[-3] = 64                              # page 64: decode only, no summary scorer
+    rc = lib.locks_score_rki4(*args)
+    assert rc == -1 and b"page 64" in lib.locks_last_error()
     rc = lib.locks_decode_splitk(*([1, 8, 8] + [1, 8, 8, 8] * 2 + [1, 1, 8, 1, 1, 8, 8, 1, 1,
                                    8, 1, 1, 1, 1, 1, 2, 17, 128, 16, 4, 1, 0, 0.1, None]))
     assert rc == -1 and b"G=17" in lib.locks_last_error()
@@ -166,9 +170,12 @@ def test_register_refuses_vllm_without_backend_class(monkeypatch):
 
 def test_geometry_contract():
     from locks.selection import Rki4State
-    Rki4State.validate_geometry(head_dim=128, G=16, page=16)
-    for kw in (dict(head_dim=64, G=4, page=16), dict(head_dim=128, G=17, page=16),
-               dict(head_dim=128, G=4, page=32)):
+    for d in (64, 128, 256):
+        for page in (16, 32):
+            Rki4State.validate_geometry(head_dim=d, G=16, page=page)
+    for kw in (dict(head_dim=96, G=4, page=16), dict(head_dim=128, G=17, page=16),
+               dict(head_dim=128, G=4, page=64), dict(head_dim=512, G=4, page=16),
+               dict(head_dim=128, G=4, page=8)):
         with pytest.raises(AssertionError):
             Rki4State.validate_geometry(**kw)
 
@@ -212,9 +219,11 @@ def test_mla_entries_reject_bad_geometry_without_device():
     assert lib.locks_mla_decode_merge(*margs) == -1 and b"multiples of 4" in lib.locks_last_error()
     assert 2 <= lib.locks_mla_score_auto_chunk(1, 8192) <= 1024
     assert lib.locks_mla_score_auto_chunk(1, 8192) % 2 == 0
-    # the latent build accepts d = 512 geometry but not d = 256
-    bargs = [1, 16 * 576, 576, 0, 8, 1, 1, 1, 256, 16] + [1] * 7 + [None]
-    assert lib.locks_build_rki4(*bargs) == -1 and b"d=256" in lib.locks_last_error()
+    # the build takes d = 512 (the latent) only at page 16, and no d = 96
+    bargs = [1, 16 * 576, 576, 0, 8, 1, 1, 1, 96, 16] + [1] * 7 + [None]
+    assert lib.locks_build_rki4(*bargs) == -1 and b"d=96" in lib.locks_last_error()
+    bargs[8:10] = [512, 32]
+    assert lib.locks_build_rki4(*bargs) == -1 and b"d=512 page=32" in lib.locks_last_error()
 
 
 
@@ -235,8 +244,10 @@ def test_refresh_entries_reject_bad_arguments_without_device():
     assert lib.locks_refresh_blocks(*a) == -1 and b"null pointer" in lib.locks_last_error()
     # locks_build_rki4_layers: geometry and the slab-blocks bound
     bl = [1, 2, 16 * 8 * 128, 8 * 128, 128, 100, 1, None, 4, 8, 128, 16, 100] + [1] * 7 + [None]
-    b = list(bl); b[10] = 64
-    assert lib.locks_build_rki4_layers(*b) == -1 and b"d=64" in lib.locks_last_error()
+    b = list(bl); b[10] = 96
+    assert lib.locks_build_rki4_layers(*b) == -1 and b"d=96" in lib.locks_last_error()
+    b = list(bl); b[11] = 64                             # page 64: decode only
+    assert lib.locks_build_rki4_layers(*b) == -1 and b"page=64" in lib.locks_last_error()
     b = list(bl); b[12] = 50                             # slab smaller than the K pool bound
     assert lib.locks_build_rki4_layers(*b) == -1 and b"bad geometry" in lib.locks_last_error()
     b = list(bl); b[3] = 12                              # token stride not a multiple of 8
