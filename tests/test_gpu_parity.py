@@ -463,22 +463,24 @@ def test_dense_comparator_matches_sdpa(n_kv, G, seq_lens, split):
             assert e.max() <= 2e-2 and e.sum() / np.abs(rb).sum() <= 1e-3, f"row {r}: {e.max()}"
 
 
-def test_end_to_end_runtime_path():
+@pytest.mark.parametrize("budget_pages", [126, 128])
+def test_end_to_end_runtime_path(budget_pages):
     """The reference's call sites (select adapter + decode dispatch) on one
-    layer vs the oracle pipeline."""
+    layer vs the oracle pipeline; budget 126 (+ sink + window = 128 attended
+    pages) and the quickstart budget_pages=128."""
     import torch
     from locks.backend import _runtime
     from locks.config import LocksConfig
     from locks.selection import derive_page_params
-    say("e2e runtime")
+    say("e2e runtime", budget_pages)
     n_kv, G, sl = 2, 16, [16384, 5000]
     case = make_case(9, n_kv, G, sl)
-    st = _state(case, L=2)
+    st = _state(case, L=2, budget_pages=budget_pages)
     load_slabs(st, 1, case.slabs)
     d = to_dev(case)
     kv = d["kv"]
     st._layer_of = {kv.data_ptr(): 1}
-    cfg = LocksConfig(budget_pages=126)
+    cfg = LocksConfig(budget_pages=budget_pages)
     derive_page_params(st, d["sl"], case.R)
     out = torch.zeros((case.R, n_kv * G, 128), dtype=torch.bfloat16, device="cuda")
     _runtime._rki4_select_adapter(d["q"], kv, d["bt"], d["sl"], st, case.R, case.scale, cfg)

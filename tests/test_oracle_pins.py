@@ -316,3 +316,102 @@ def test_merge_split_invariance():
         out = O.merge_partials(m, l, acc, np.array([[cnt, 0]]), split, 1)
         assert np.abs(out[0, :G] - direct).max() < 1e-5
         assert (out[0, G:] == 0).all()
+
+
+# ---- the other geometries (rki4_state.py:295-324: d 64/128/256, page 16/32) ----
+GEOMS = [(64, 16), (256, 16), (128, 32), (64, 32), (256, 32)]
+
+
+@pytest.mark.parametrize("d,page", GEOMS)
+def test_geometry_pre_and_low_rank(d, page):
+    """Centre / tag at float64, and an exact rank-5 page reproduced to the
+    int4/int8 quantization floor (the build's eigh + pack at this shape)."""
+    rng = np.random.default_rng(40)
+    A = rng.standard_normal((3, 2, page, 5)) @ rng.standard_normal((3, 2, 5, d))
+    A += rng.standard_normal((3, 2, 1, d))
+    kp = O.f32_to_bf16(A.transpose(0, 2, 1, 3).astype(np.float32))
+    tag, mu, dc, _ = O.summary_pre(kp)
+    K = O.bf16_to_f32(kp).astype(np.float64).transpose(0, 2, 1, 3)
+    assert np.abs(mu - K.mean(2)).max() < 1e-5
+    assert np.array_equal(tag, kp[:, page - 1, :, :8])
+    s = O.build_summaries(kp)
+    assert s["v4"].shape[-2:] == (8, d // 2) and s["c8"].shape[-2:] == (page, 8)
+    V = O.unpack_i4(s["v4"]).astype(np.float64) * O.bf16_to_f32(s["vs"])[..., None]
+    C = s["c8"].astype(np.float64) * O.bf16_to_f32(s["cs"])[..., None]
+    rec = np.einsum("nktr,nkrd->nktd", C, V)
+    assert np.linalg.norm(rec - dc) / np.linalg.norm(dc) < 0.2
+
+
+@pytest.mark.parametrize("d,page", GEOMS)
+@pytest.mark.parametrize("G", [1, 8])
+def test_geometry_score_vs_reconstructed_keys(d, page, G):
+    """Twin and integer-path scores equal the float64 LSE over the page's
+    keys rebuilt from the dequantized summary, at each geometry."""
+    rng = np.random.default_rng(41)
+    n_kv, npages = 2, 12
+    NB = npages + 2
+    k, _, _ = O.synth_kv(rng, NB, page, n_kv, d)
+    slabs = O.build_state_slabs(k, np.arange(NB), NB)
+    q = O.f32_to_bf16(rng.standard_normal((1, n_kv * G, d)).astype(np.float32))
+    bt = rng.permutation(NB)[None, :npages].astype(np.int32)
+    P, s = 11, 1 / math.sqrt(d)
+    twin = O.score_rki4_twin(q, slabs, bt, np.array([P]), n_kv, G, s, npages)
+    intp = O.score_rki4_intpath(q, slabs, bt, np.array([P]), n_kv, G, s, npages)
+    q8, qs = O.quantize_q(q.reshape(1, n_kv, G, d))
+    qd = q8.astype(np.float64) * qs[..., None]
+    for p in range(P):
+        b = bt[0, p]
+        for kh in range(n_kv):
+            V = O.unpack_i4(slabs["v4"][b, kh]).astype(np.float64) * O.bf16_to_f32(slabs["vs"][b, kh])[:, None]
+            C = slabs["c8"][b, kh].astype(np.float64) * O.bf16_to_f32(slabs["cs"][b, kh])[:, None]
+            mu = slabs["mu8"][b, kh].astype(np.float64) * float(O.bf16_to_f32(slabs["mus"][b, kh:kh + 1])[0])
+            keys = mu[None, :] + C @ V                                   # (page, d)
+            assert keys.shape == (page, d)
+            for g in range(G):
+                ref = O.log_sum_exp(list(s * (keys @ qd[0, kh, g])))
+                assert abs(twin[0, kh, g, p] - ref) < 1e-5 and abs(intp[0, kh, g, p] - ref) < 1e-5
+
+
+@pytest.mark.parametrize("d,page", GEOMS)
+def test_geometry_rank0_closed_form(d, page):
+    """V = 0 -> every token logit is s*mud, so LSE = s*mud + log(page)."""
+    rng = np.random.default_rng(42)
+    NB, n_kv, G = 6, 2, 4
+    k, _, _ = O.synth_kv(rng, NB, page, n_kv, d)
+    slabs = dict(O.build_state_slabs(k, np.arange(NB), NB))
+    slabs["v4"] = np.zeros_like(slabs["v4"])
+    q = O.f32_to_bf16(rng.standard_normal((1, n_kv * G, d)).astype(np.float32))
+    bt = np.arange(NB, dtype=np.int32)[None]
+    s = 0.3
+    out = O.score_rki4_twin(q, slabs, bt, np.array([NB]), n_kv, G, s, NB)
+    q8, qs = O.quantize_q(q.reshape(1, n_kv, G, d))
+    for p in range(NB):
+        for kh in range(n_kv):
+            mud = (slabs["mu8"][p, kh].astype(np.float64) @ q8[0, kh].T.astype(np.float64)) \
+                * qs[0, kh] * float(O.bf16_to_f32(slabs["mus"][p, kh:kh + 1])[0])
+            assert np.allclose(out[0, kh, :, p], s * mud + math.log(page), atol=1e-5)
+
+
+@pytest.mark.parametrize("d,page", GEOMS + [(128, 64)])
+def test_geometry_decode_matches_sdpa(d, page):
+    """decode_attention over every page of a ragged row equals float64 SDPA."""
+    import torch
+    rng = np.random.default_rng(43)
+    n_kv, G, sl = 2, 3, 5 * page + 7
+    npg = -(-sl // page)
+    NB = npg + 2
+    k, v, _ = O.synth_kv(rng, NB, page, n_kv, d)
+    bt = rng.permutation(NB)[None, :npg].astype(np.int32)
+    q = O.f32_to_bf16(rng.standard_normal((1, n_kv * G, d)).astype(np.float32))
+    tab = np.full((1, n_kv, npg), -1, np.int32)
+    tab[..., :npg] = np.arange(npg)
+    cnt = np.full((1, n_kv), npg, np.int32)
+    sc = 1 / math.sqrt(d)
+    out, _ = O.decode_attention(q, k, v, bt, [sl], tab, cnt, G, sc, dtype=np.float64)
+    K = torch.from_numpy(O.bf16_to_f32(k[bt[0]]).reshape(-1, n_kv, d)[:sl]).double()
+    V = torch.from_numpy(O.bf16_to_f32(v[bt[0]]).reshape(-1, n_kv, d)[:sl]).double()
+    Q = torch.from_numpy(O.bf16_to_f32(q[0])).double().reshape(n_kv, G, d)
+    ref = torch.nn.functional.scaled_dot_product_attention(
+        Q[:, :, None], K.permute(1, 0, 2)[:, None].expand(-1, G, -1, -1),
+        V.permute(1, 0, 2)[:, None].expand(-1, G, -1, -1), scale=sc)[:, :, 0]
+    assert np.abs(out[0] - ref.reshape(-1, d).numpy()).max() < 1e-10
