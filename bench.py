@@ -414,24 +414,24 @@ def mla_sparse_step(m, out, lse):
                         out=out[layer], lse=lse[layer], layer=layer, derive=(layer == 0))
 
 
-def make_mla_dense(m):
+def make_mla_dense(m, split=0):
+    """Partials of the dense MLA comparator (locks_mla_decode_dense): about
+    two workgroups per CU over the batch's rows."""
     import torch
-    from locks.selection import MlaState
-    dn = MlaState("cuda", num_layers=1, num_blocks=8, n_heads=m["H"], max_reqs=m["R"],
-                  max_pages=m["MP"], budget_pages=m["MP"] + 1, split=512)
-    for r, s in enumerate(m["sl"].tolist()):
-        n = (s + PAGE - 1) // PAGE
-        dn.page_table[r, 0, :n] = torch.arange(n, dtype=torch.int32, device="cuda")
-        dn.page_cnt[r, 0] = n
-    dn.NB = m["NB"]
-    return dn
+    R = m["R"]
+    split = split or max(1, min(512, 512 // R))
+    return dict(split=split,
+                m=torch.empty(R, split, 16, device="cuda"),
+                l=torch.empty(R, split, 16, device="cuda"),
+                acc=torch.empty(R, split, 16, MLA_LKV, device="cuda"))
 
 
 def mla_dense_step(m, dn, out, lse):
-    from locks.attention import mla_decode
+    from locks.attention import mla_decode_dense
     for layer in range(m["L"]):
-        mla_decode(dn, m["q"][layer], m["cache"][layer], m["bt"], m["sl"], m["R"], m["scale"],
-                   out[layer], lse[layer])
+        mla_decode_dense(m["q"][layer], m["cache"][layer], m["bt"], m["sl"], dn["m"], dn["l"],
+                         dn["acc"], out[layer], n_req=m["R"], split=dn["split"],
+                         scale=m["scale"], num_blocks=m["NB"], lse=lse[layer])
 
 
 def mla_step_bytes(m):
@@ -540,7 +540,7 @@ def run_mla(a, wl):
     stream_us = stream_read_us(by["score_per_launch"], L)
     res = {}
     if not a.no_dense:
-        dn = make_mla_dense(m)
+        dn = make_mla_dense(m, a.dense_split)
         outd = [torch.empty_like(o) for o in out]
         lsed = [torch.empty_like(x) for x in lse]
         gd = capture(lambda: mla_dense_step(m, dn, outd, lsed))
@@ -694,6 +694,9 @@ def main():
         return
     wl = WORKLOADS[a.workload]
     if wl.get("mla"):
+        if a.pps_min:
+            from locks.attention import mla_decode as _mdec
+            _mdec.PPS_MIN_OVERRIDE = a.pps_min
         run_mla(a, wl)
         return
     from locks.attention import decode as _dec

@@ -30,7 +30,7 @@
 
 #include <stdint.h>
 
-#define LOCKS_ABI_VERSION 5
+#define LOCKS_ABI_VERSION 6
 
 #ifdef __cplusplus
 extern "C" {
@@ -432,6 +432,27 @@ int32_t locks_mla_decode_merge(const float* m_part, const float* l_part, const f
                                int32_t out_is_f32, float* lse, int64_t lse_stride_req,
                                int32_t n_req, int32_t n_heads, int32_t kv_lora_rank,
                                int32_t split, int32_t pps_min, void* stream);
+
+/*
+ * Dense full-cache MLA decode (the comparator of the sparse step): every
+ * page of each request's row, in logical order (page count from seq_len,
+ * no page table), split-K over `split` workgroups per request with three
+ * page stages in flight and non-temporal page DMA, then the same LSE merge
+ * into out (n_req, H, 512) and lse (n_req, H) (lse may be NULL).  Partials
+ * as for locks_mla_decode_splitk (split <= 512).  No counterpart kernel in
+ * the reference, whose dense baseline is FlashMLA (backend/mla_attn.py);
+ * it exists so the sparse step is compared with a dense decode of the same
+ * quality on the same GPU.
+ */
+int32_t locks_mla_decode_dense(const uint16_t* q, int64_t q_stride_req, int64_t q_stride_head,
+                               const uint16_t* cache, int64_t c_stride_block, int64_t c_stride_tok,
+                               int32_t num_blocks, const int32_t* block_table, int64_t bt_stride,
+                               int32_t bt_cols, const int32_t* seq_lens, float* m_part,
+                               float* l_part, float* acc_part, void* out, int64_t out_stride_req,
+                               int64_t out_stride_head, int32_t out_is_f32, float* lse,
+                               int64_t lse_stride_req, int32_t n_req, int32_t n_heads,
+                               int32_t kv_lora_rank, int32_t rope_dim, int32_t page,
+                               int32_t split, float scale, void* stream);
 
 #ifdef __cplusplus
 }

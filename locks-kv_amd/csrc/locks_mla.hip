@@ -323,6 +323,7 @@ constexpr int MD_ROWB = ML_HS * 2 + 16;               // padded token row (1168 
 constexpr int MD_PAGE_B = ML_PG * MD_ROWB;            // 18688 B per stage
 constexpr int MD_IDS = 256;                           // page ids staged per batch
 constexpr int MD_MAX_SPLIT = 512;
+constexpr int CPOL_NT_MLA = 2;                        // non-temporal DMA (dense: every page read once)
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
@@ -346,6 +347,14 @@ __device__ __forceinline__ void lgkm_wait(v4i& a, v4i& b, v4i& c, v4i& d, v4i& e
     asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d), "+v"(e) :: "memory");
 }
 
+// DENSE: every page of the row in logical order (page count from seq_len, no
+// page table) -- the dense full-cache comparator.  NST: page stages per
+// workgroup (NST - 1 pages in flight while one is consumed).  KVPOL: cache
+// policy bits of the page DMA.
+constexpr int vm_wait_imm(int n) {                       // s_waitcnt vmcnt(n) lgkmcnt(0)
+    return 0x0070 | (n & 15) | ((n >> 4) << 14);
+}
+template <bool DENSE = false, int NST = 2, int KVPOL = 0>
 __global__ __launch_bounds__(ML_BLK) void mla_decode_split_kernel(
     const uint16_t* __restrict__ q, long q_sr, long q_sh,
     const uint16_t* __restrict__ cache, long c_sb, long c_st, int NB,
@@ -354,8 +363,9 @@ __global__ __launch_bounds__(ML_BLK) void mla_decode_split_kernel(
     const int* __restrict__ seq_lens, float* __restrict__ m_part, float* __restrict__ l_part,
     float* __restrict__ acc_part, int H, int split, int pps_min, float scale)
 {
+    static_assert(NST >= 2 && NST <= 4, "page stages");
     const int sp = blockIdx.x, r = blockIdx.y;
-    const int cnt = min(pcnt[r], pt_cols);
+    const int cnt = DENSE ? min(cdiv(seq_lens[r], ML_PG), bt_cols) : min(pcnt[r], pt_cols);
     const int pps = max(cdiv(cnt, split), pps_min);
     const int j0 = sp * pps;
     if (j0 >= cnt) return;                               // inactive split: no store
@@ -364,7 +374,7 @@ __global__ __launch_bounds__(ML_BLK) void mla_decode_split_kernel(
     const int r16 = lane & 15, kg = lane >> 4;
     const int seq_len = seq_lens[r];
 
-    __shared__ __attribute__((aligned(16))) uint8_t stg[2][MD_PAGE_B];
+    __shared__ __attribute__((aligned(16))) uint8_t stg[NST][MD_PAGE_B];
     __shared__ __attribute__((aligned(16))) float spart[ML_WAVES][kWave * 4];
     __shared__ int ids_pt[MD_IDS], ids_blk[MD_IDS];
 
@@ -397,10 +407,10 @@ __global__ __launch_bounds__(ML_BLK) void mla_decode_split_kernel(
         for (int q4 = 0; q4 < 4; ++q4) {
             const int t = 4 * wave + q4;
             const uint16_t* row = base + (long)t * c_st;
-            __builtin_amdgcn_global_load_lds(row + 8 * lane, (lds_ptr_t)(&stg[slot][t * MD_ROWB]), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(row + 8 * lane, (lds_ptr_t)(&stg[slot][t * MD_ROWB]), 16, 0, KVPOL);
             if (lane < 8)
                 __builtin_amdgcn_global_load_lds(row + 8 * (64 + lane), (lds_ptr_t)(&stg[slot][t * MD_ROWB + 1024]),
-                                                 16, 0, 0);
+                                                 16, 0, KVPOL);
         }
     };
 
@@ -408,18 +418,27 @@ __global__ __launch_bounds__(ML_BLK) void mla_decode_split_kernel(
         const int nb = min(MD_IDS, j1 - jb);
         __syncthreads();                                      // previous batch fully consumed
         for (int i = tid; i < nb; i += ML_BLK) {
-            const int pt = ptab[(long)r * pt_sr + jb + i];
+            const int pt = DENSE ? jb + i : ptab[(long)r * pt_sr + jb + i];
             const int ptc = min(max(pt, 0), bt_cols - 1);
             ids_pt[i] = pt;
             ids_blk[i] = min(max(bt[(long)r * bt_sr + ptc], 0), NB - 1);
         }
         __syncthreads();
-        issue(0, ids_blk[0]);
+        // ring of NST stages: page i + NST - 1 is issued (into the slot of
+        // page i - 1) once every wave is past page i - 1
+#pragma unroll
+        for (int k = 0; k < NST - 1; ++k)
+            if (k < nb) issue(k, ids_blk[k]);
         for (int i = 0; i < nb; ++i) {
-            const int slot = i & 1;
-            __builtin_amdgcn_s_waitcnt(0x0070);               // this wave's part of page i landed
+            const int slot = i % NST;
+            // this wave's part of page i landed: 8 DMA instructions per page
+            // per wave, min(NST - 2, nb - 1 - i) pages issued after it
+            const int ahead = min(NST - 2, nb - 1 - i);
+            if (ahead <= 0) __builtin_amdgcn_s_waitcnt(vm_wait_imm(0));
+            else if (NST > 2 && ahead == 1) __builtin_amdgcn_s_waitcnt(vm_wait_imm(8));
+            else if (NST > 3) __builtin_amdgcn_s_waitcnt(vm_wait_imm(16));
             __builtin_amdgcn_s_barrier();                     // every part landed; page i-1 consumed
-            if (i + 1 < nb) issue(slot ^ 1, ids_blk[i + 1]);
+            if (i + NST - 1 < nb) issue((i + NST - 1) % NST, ids_blk[i + NST - 1]);
             const int pt = ids_pt[i];
             const uint32_t sb = st0 + slot * MD_PAGE_B;
             // ---- partial S^T[t][h] over this wave's k-steps ----------------
@@ -499,34 +518,42 @@ __global__ __launch_bounds__(ML_BLK) void mla_decode_split_kernel(
 }
 
 // LSE merge of the active splits (merge.py:105-152 rule) into o (R, H, 512)
-// and lse (R, H).  Grid (H, R, 4 slices of 128 dims); 256 threads = 32
-// float4 columns x 8 split groups, so hundreds of split partials (dense
-// decode) are read with 8 independent streams per column and reduced in LDS.
+// and lse (R, H).  Grid (H, R, 512 / (4 COLS) slices); 256 threads = COLS
+// float4 columns x 256 / COLS split groups, each group's first PF partials
+// loaded before anything waits, the rest in batches of PF, reduced in LDS.
+// Sparse rows (tens of splits): COLS 32 (4 slices of 128 dims).  The dense
+// comparator (hundreds of splits): COLS 8 (16 slices of 32 dims, 256
+// workgroups per request instead of 64) and PF 8, so a 512-split row is
+// two rounds of loads per thread instead of sixteen.
 constexpr int MG_BLK = 256;
-constexpr int MG_GRP = MG_BLK / 32;
 
+template <int COLS, int PF>
 __global__ __launch_bounds__(MG_BLK) void mla_merge_kernel(
     const float* __restrict__ m_part, const float* __restrict__ l_part,
     const float* __restrict__ acc_part, const int* __restrict__ pcnt, int pt_cols,
+    const int* __restrict__ seq_lens, int bt_cols,
     void* __restrict__ out, long o_sr, long o_sh, int out_f32,
     float* __restrict__ lse, long lse_sr, int split, int pps_min)
 {
     const int h = blockIdx.x, r = blockIdx.y, zc = blockIdx.z, tid = threadIdx.x;
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int cnt = min(pcnt[r], pt_cols);
+    // page count: the selection's (clamped to the table) or, with pcnt ==
+    // nullptr, every page of the row (the dense comparator)
+    const int cnt = pcnt ? min(pcnt[r], pt_cols) : min(cdiv(seq_lens[r], ML_PG), bt_cols);
     const int pps = max(cdiv(cnt, split), pps_min);
     const int n_act = cnt > 0 ? cdiv(cnt, pps) : 0;
     __shared__ float w_s[MD_MAX_SPLIT];
     __shared__ float red[MG_BLK / kWave];
-    __shared__ __attribute__((aligned(16))) float4 part[MG_GRP][32];
+    constexpr int MG_GRP = MG_BLK / COLS;
+    __shared__ __attribute__((aligned(16))) float4 part[MG_GRP][COLS];
     const long rb = (long)r * split;
-    const int c = tid & 31, g = tid >> 5;
-    const int d0 = 128 * zc + 4 * c;
-    // the first 4 partials of this thread's split group, loaded before any
+    const int c = tid % COLS, g = tid / COLS;
+    const int d0 = 4 * COLS * zc + 4 * c;
+    // the first PF partials of this thread's split group, loaded before any
     // wait (they do not depend on the weights)
-    float4 pre[4];
+    float4 pre[PF];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
+    for (int k = 0; k < PF; ++k) {
         const int s = g + k * MG_GRP;
         pre[k] = (s < split) ? *reinterpret_cast<const float4*>(acc_part + ((rb + s) * ML_H + h) * ML_D + d0)
                              : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -569,24 +596,24 @@ __global__ __launch_bounds__(MG_BLK) void mla_merge_kernel(
     // acc over this slice: column c (4 dims), split group g
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
+    for (int k = 0; k < PF; ++k) {
         const int s = g + k * MG_GRP;
         if (s < n_act) {
             const float w = w_s[s];
             acc.x += w * pre[k].x; acc.y += w * pre[k].y; acc.z += w * pre[k].z; acc.w += w * pre[k].w;
         }
     }
-    int s = g + 4 * MG_GRP;
-    for (; s + 3 * MG_GRP < n_act; s += 4 * MG_GRP) {
-        float4 a[4];
-        float w[4];
+    int s = g + PF * MG_GRP;
+    for (; s + (PF - 1) * MG_GRP < n_act; s += PF * MG_GRP) {
+        float4 a[PF];
+        float w[PF];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
+        for (int k = 0; k < PF; ++k) {
             a[k] = *reinterpret_cast<const float4*>(acc_part + ((rb + s + k * MG_GRP) * ML_H + h) * ML_D + d0);
             w[k] = w_s[s + k * MG_GRP];
         }
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
+        for (int k = 0; k < PF; ++k) {
             acc.x += w[k] * a[k].x; acc.y += w[k] * a[k].y; acc.z += w[k] * a[k].z; acc.w += w[k] * a[k].w;
         }
     }
@@ -683,7 +710,7 @@ extern "C" int32_t locks_mla_decode_splitk(
     LOCKS_REQUIRE(q && cache && block_table && page_table && page_cnt && seq_lens && m_part && l_part && acc_part,
                   "locks_mla_decode_splitk: null pointer argument");
     if (n_req == 0) return 0;
-    hipLaunchKernelGGL(mla_decode_split_kernel, dim3(split, n_req), dim3(ML_BLK), 0, (hipStream_t)stream,
+    hipLaunchKernelGGL((mla_decode_split_kernel<false, 2, 0>), dim3(split, n_req), dim3(ML_BLK), 0, (hipStream_t)stream,
                        q, (long)q_stride_req, (long)q_stride_head, cache, (long)c_stride_block,
                        (long)c_stride_tok, num_blocks, block_table, (long)bt_stride, bt_cols,
                        page_table, (long)pt_stride, pt_cols, page_cnt, seq_lens, m_part, l_part,
@@ -705,8 +732,47 @@ extern "C" int32_t locks_mla_decode_merge(
                   "locks_mla_decode_merge: out strides must be multiples of 4 elements");
     LOCKS_REQUIRE(m_part && l_part && acc_part && page_cnt && out, "locks_mla_decode_merge: null pointer argument");
     if (n_req == 0) return 0;
-    hipLaunchKernelGGL(mla_merge_kernel, dim3(n_heads, n_req, ML_D / 128), dim3(MG_BLK), 0, (hipStream_t)stream,
-                       m_part, l_part, acc_part, page_cnt, pt_cols, out, (long)out_stride_req,
+    hipLaunchKernelGGL((mla_merge_kernel<32, 4>), dim3(n_heads, n_req, ML_D / 128), dim3(MG_BLK), 0, (hipStream_t)stream,
+                       m_part, l_part, acc_part, page_cnt, pt_cols, nullptr, 1, out, (long)out_stride_req,
                        (long)out_stride_head, out_is_f32, lse, (long)lse_stride_req, split, pps_min);
+    return check_launch("mla_merge_kernel");
+}
+
+#ifndef LOCKS_MLA_DENSE_NST
+#define LOCKS_MLA_DENSE_NST 3
+#endif
+extern "C" int32_t locks_mla_decode_dense(
+    const uint16_t* q, int64_t q_stride_req, int64_t q_stride_head, const uint16_t* cache,
+    int64_t c_stride_block, int64_t c_stride_tok, int32_t num_blocks, const int32_t* block_table,
+    int64_t bt_stride, int32_t bt_cols, const int32_t* seq_lens, float* m_part, float* l_part,
+    float* acc_part, void* out, int64_t out_stride_req, int64_t out_stride_head, int32_t out_is_f32,
+    float* lse, int64_t lse_stride_req, int32_t n_req, int32_t n_heads, int32_t kv_lora_rank,
+    int32_t rope_dim, int32_t page, int32_t split, float scale, void* stream)
+{
+    LOCKS_REQUIRE(kv_lora_rank == ML_D && rope_dim == ML_DR && page == ML_PG,
+                  "locks_mla_decode_dense: geometry (%d, %d, page %d) unsupported (this build: 512 + 64, page 16)",
+                  kv_lora_rank, rope_dim, page);
+    LOCKS_REQUIRE(n_heads >= 1 && n_heads <= ML_H, "locks_mla_decode_dense: n_heads=%d outside [1, %d]",
+                  n_heads, ML_H);
+    LOCKS_REQUIRE(split >= 1 && split <= MD_MAX_SPLIT, "locks_mla_decode_dense: split=%d outside [1, %d]",
+                  split, MD_MAX_SPLIT);
+    LOCKS_REQUIRE(q_stride_head % 8 == 0 && q_stride_req % 8 == 0 && c_stride_tok % 8 == 0 &&
+                  c_stride_block % 8 == 0, "locks_mla_decode_dense: strides must be multiples of 8 elements");
+    LOCKS_REQUIRE(out_stride_req % 4 == 0 && out_stride_head % 4 == 0,
+                  "locks_mla_decode_dense: out strides must be multiples of 4 elements");
+    LOCKS_REQUIRE(n_req >= 0 && num_blocks >= 1 && bt_cols >= 1, "locks_mla_decode_dense: empty geometry");
+    LOCKS_REQUIRE(q && cache && block_table && seq_lens && m_part && l_part && acc_part && out,
+                  "locks_mla_decode_dense: null pointer argument");
+    if (n_req == 0) return 0;
+    hipStream_t st = (hipStream_t)stream;
+    hipLaunchKernelGGL((mla_decode_split_kernel<true, LOCKS_MLA_DENSE_NST, CPOL_NT_MLA>), dim3(split, n_req),
+                       dim3(ML_BLK), 0, st, q, (long)q_stride_req, (long)q_stride_head, cache,
+                       (long)c_stride_block, (long)c_stride_tok, num_blocks, block_table, (long)bt_stride,
+                       bt_cols, nullptr, 0L, 1, nullptr, seq_lens, m_part, l_part, acc_part, n_heads,
+                       split, 1, scale);
+    if (int rc = check_launch("mla_decode_split_kernel<dense>")) return rc;
+    hipLaunchKernelGGL((mla_merge_kernel<8, 8>), dim3(n_heads, n_req, ML_D / 32), dim3(MG_BLK), 0, st,
+                       m_part, l_part, acc_part, nullptr, 1, seq_lens, bt_cols, out, (long)out_stride_req,
+                       (long)out_stride_head, out_is_f32, lse, (long)lse_stride_req, split, 1);
     return check_launch("mla_merge_kernel");
 }

@@ -10,7 +10,7 @@ import ctypes
 import os
 
 _LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "liblocks_hip.so")
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _c = ctypes
 _i32, _i64, _f32, _f64, _p = _c.c_int32, _c.c_int64, _c.c_float, _c.c_double, _c.c_void_p
@@ -52,6 +52,9 @@ SIGNATURES = {
                                        _i32, _i32, _i32, _f32, _p]),
     "locks_mla_decode_merge": (_i32, [_p, _p, _p, _p, _i32, _p, _i64, _i64, _i32, _p, _i64, _i32,
                                       _i32, _i32, _i32, _i32, _p]),
+    "locks_mla_decode_dense": (_i32, [_p, _i64, _i64, _p, _i64, _i64, _i32, _p, _i64, _i32, _p,
+                                      _p, _p, _p, _p, _i64, _i64, _i32, _p, _i64, _i32, _i32,
+                                      _i32, _i32, _i32, _i32, _f32, _p]),
     "locks_decode_fused_noalloc": (_i32, [_p, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64,
                                           _i64, _i32, _p, _i64, _i32, _p, _i64, _i64, _i32, _p,
                                           _i64, _p, _p, _i64, _i64, _i32, _i32, _i32, _i32, _i32,
