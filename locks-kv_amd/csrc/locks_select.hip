@@ -275,23 +275,57 @@ __device__ void finish_row(long rk, int n_pages, int n_sel_hi, int n_sink, int b
 
 // ---------------------------------------------------------------------------
 // register-resident exact top-k: thread t holds keys[E] (valid flags) of
-// consecutive items; 12 + 12 + 8-bit MSD radix over an LDS histogram (4096
-// ints), then ordered emission with one packed (greater | equal << 16)
-// block scan.  Items must number < 65536.
+// consecutive items.  Result: either a whole bin (every key >= lo is kept)
+// or an exact threshold (keys > tau kept, then keys == tau up to k).
+// Items must number < 65536.
 // ---------------------------------------------------------------------------
 struct RadixSel {
-    uint32_t prefix, kmask;
-    int k;              // keys == prefix still to take (exact mode)
-    bool whole_bin;     // every key whose masked bits >= prefix is kept
+    uint32_t lo, tau;
+    int k;              // keys == tau still to take (exact mode)
+    bool whole_bin;     // every key >= lo is kept
 };
 
-template <int BLK, int E>
-__device__ RadixSel reg_kth_largest(const uint32_t (&key)[E], const bool (&val)[E], int k,
-                                    int* hist, int* wtot, int* s3) {
+// Boundary search over an LDS histogram of nb bins (nb = 4096 or 256): the
+// bin B holding the k-th largest (bins counted from the top), the keys still
+// needed from it (k - #above) and its count, in s3[0..2].
+template <int BLK, int NB>
+__device__ __forceinline__ void hist_boundary(const int* hist, int k, int* wtot, int* s3) {
     constexpr int NW = BLK / kWave;
-    constexpr int BPL = 4096 / BLK;                     // histogram bins per lane
+    constexpr int nb = NB;
+    constexpr int bpl = NB / BLK > 0 ? NB / BLK : 1;    // histogram bins per lane
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    RadixSel rs{0u, 0u, k, false};
+    // thread t: bins top .. top-bpl+1, top = nb-1-bpl*t (ascending thread
+    // order = descending bin order)
+    const int top = nb - 1 - bpl * tid;
+    int c = 0;
+#pragma unroll
+    for (int j = 0; j < bpl; ++j) c += (top - j >= 0) ? hist[top - j] : 0;
+    const int incl = wave_incl_scan_i(c);
+    if (lane == kWave - 1) wtot[wave] = incl;
+    lds_barrier();
+    // counts of the waves before this one: one parallel LDS read and a
+    // wave sum (a serial loop would chain up to NW - 1 LDS latencies)
+    const int base = wave_sum_i((lane < wave && lane < NW) ? wtot[lane] : 0);
+    const int above0 = base + incl - c;
+    if (c > 0 && above0 < k && k <= base + incl) {
+        int above = above0;
+#pragma unroll
+        for (int j = 0; j < bpl; ++j) {
+            const int cb = (top - j >= 0) ? hist[top - j] : 0;
+            if (above + cb >= k) { s3[0] = top - j; s3[1] = k - above; s3[2] = cb; break; }
+            above += cb;
+        }
+    }
+    lds_barrier();
+}
+
+// 12 + 12 + 8-bit MSD radix on the absolute key bits (the fallback of
+// reg_kth_largest below).
+template <int BLK, int E>
+__device__ RadixSel reg_kth_largest_abs(const uint32_t (&key)[E], const bool (&val)[E], int k,
+                                        int* hist, int* wtot, int* s3) {
+    const int tid = threadIdx.x;
+    uint32_t prefix = 0u, kmask = 0u;
 #pragma unroll 1
     for (int pass = 0; pass < 3; ++pass) {
         const int shift = pass == 0 ? 20 : pass == 1 ? 8 : 0;
@@ -301,38 +335,85 @@ __device__ RadixSel reg_kth_largest(const uint32_t (&key)[E], const bool (&val)[
 #pragma unroll
         for (int e = 0; e < E; ++e)
             hist_add(hist, (int)((key[e] >> shift) & (uint32_t)(nb - 1)),
-                     val[e] && (key[e] & rs.kmask) == rs.prefix);
+                     val[e] && (key[e] & kmask) == prefix);
         lds_barrier();
-        // thread t: bins top .. top-BPL+1, top = nb-1-BPL*t (ascending thread
-        // order = descending bin order)
-        const int top = nb - 1 - BPL * tid;
-        int c = 0;
-#pragma unroll
-        for (int j = 0; j < BPL; ++j) c += (top - j >= 0) ? hist[top - j] : 0;
-        const int incl = wave_incl_scan_i(c);
-        if (lane == kWave - 1) wtot[wave] = incl;
-        lds_barrier();
-        // counts of the waves before this one: one parallel LDS read and a
-        // wave sum (a serial loop would chain up to NW - 1 LDS latencies)
-        const int base = wave_sum_i((lane < wave) ? wtot[lane] : 0);
-        const int above0 = base + incl - c;
-        if (c > 0 && above0 < rs.k && rs.k <= base + incl) {
-            int above = above0;
-#pragma unroll
-            for (int j = 0; j < BPL; ++j) {
-                const int cb = (top - j >= 0) ? hist[top - j] : 0;
-                if (above + cb >= rs.k) { s3[0] = top - j; s3[1] = rs.k - above; s3[2] = cb; break; }
-                above += cb;
-            }
-        }
-        lds_barrier();
-        rs.prefix |= ((uint32_t)s3[0]) << shift;
-        rs.kmask |= ((uint32_t)(nb - 1)) << shift;
+        if (pass < 2) hist_boundary<BLK, 4096>(hist, k, wtot, s3);
+        else hist_boundary<BLK, 256>(hist, k, wtot, s3);
+        prefix |= ((uint32_t)s3[0]) << shift;
+        kmask |= ((uint32_t)(nb - 1)) << shift;
         const int cb = s3[2];
-        rs.k = s3[1];
-        if (rs.k == cb) { rs.whole_bin = true; break; }
+        k = s3[1];
+        if (k == cb) return RadixSel{prefix, prefix, k, true};   // keys >= prefix (low bits 0)
     }
-    return rs;
+    return RadixSel{prefix, prefix, k, false};
+}
+
+// Exact k-th largest with a first pass relative to the row maximum mk: bin
+// = 4095 - min(4095, (mk - key) >> 15), i.e. 4096 bins of 2^15 key steps
+// (about 2^-8 of a binade) covering the 16 binades below the maximum, keys
+// further down clamped into bin 0.  The top keys spread over many bins
+// instead of the few that the absolute leading bits give, so the boundary
+// bin usually holds the last needed key alone and the select ends after
+// one pass; otherwise a second pass splits the 2^15-step bin into 4096 bins
+// of 8 steps and a third pass resolves the 8.  A boundary in the clamped
+// bin 0 (the k-th key more than 16 binades below the maximum) falls back to
+// the absolute radix.
+template <int BLK, int E>
+__device__ RadixSel reg_kth_largest(const uint32_t (&key)[E], const bool (&val)[E], int k,
+                                    int* hist, int* wtot, int* s3) {
+    constexpr int NW = BLK / kWave;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // row maximum over the valid keys (0 when none: every valid key >= 0)
+    uint32_t mx = 0u;
+#pragma unroll
+    for (int e = 0; e < E; ++e) mx = val[e] ? max(mx, key[e]) : mx;
+    for (int i = tid; i < 4096; i += BLK) hist[i] = 0;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, o, kWave));
+    if (lane == 0) wtot[wave] = (int)mx;
+    lds_barrier();
+    uint32_t mk = 0u;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) mk = max(mk, (uint32_t)wtot[w]);
+    // pass 0: bins relative to mk
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const uint32_t d = (mk - key[e]) >> 15;
+        hist_add(hist, 4095 - (int)min(d, 4095u), val[e]);
+    }
+    lds_barrier();
+    hist_boundary<BLK, 4096>(hist, k, wtot, s3);
+    const int B = s3[0];
+    if (B == 0) return reg_kth_largest_abs<BLK, E>(key, val, k, hist, wtot, s3);
+    // bin B holds keys with (mk - key) >> 15 == 4095 - B: [lo, hi] (a
+    // non-empty bin implies mk >= (4095 - B) << 15, so hi does not wrap;
+    // lo saturates at 0)
+    const uint32_t span = (uint32_t)(4096 - B) << 15;
+    uint32_t hi = mk - ((uint32_t)(4095 - B) << 15);
+    uint32_t lo = (mk + 1u > span) ? mk + 1u - span : 0u;
+    k = s3[1];
+    if (k == s3[2]) return RadixSel{lo, lo, k, true};
+    // passes 1 and 2: bins of 8 steps inside [lo, hi] (< 2^15 steps), then
+    // the (<= 8) steps of the boundary bin
+#pragma unroll 1
+    for (int pass = 1; pass < 3; ++pass) {
+        const int shift = pass == 1 ? 3 : 0;
+        const int nb = pass == 1 ? 4096 : 8;
+        for (int i = tid; i < nb; i += BLK) hist[i] = 0;
+        lds_barrier();
+#pragma unroll
+        for (int e = 0; e < E; ++e)
+            hist_add(hist, (int)((key[e] - lo) >> shift) & (nb - 1), val[e] && key[e] >= lo && key[e] <= hi);
+        lds_barrier();
+        if (pass == 1) hist_boundary<BLK, 4096>(hist, k, wtot, s3);
+        else hist_boundary<BLK, 8>(hist, k, wtot, s3);
+        lo += (uint32_t)s3[0] << shift;
+        hi = min(hi, lo + ((1u << shift) - 1u));
+        const int cb = s3[2];
+        k = s3[1];
+        if (k == cb) return RadixSel{lo, lo, k, true};
+    }
+    return RadixSel{lo, lo, k, false};                        // exact: tau = lo
 }
 
 // Emission in item order: out(pos, e) is called for every kept item of
@@ -344,8 +425,8 @@ __device__ int reg_emit(const uint32_t (&key)[E], const bool (&val)[E], const Ra
 #pragma unroll
     for (int e = 0; e < E; ++e) {
         if (!val[e]) continue;
-        if (rs.whole_bin) gt += (key[e] & rs.kmask) >= rs.prefix;
-        else { gt += key[e] > rs.prefix; eq += key[e] == rs.prefix; }
+        if (rs.whole_bin) gt += key[e] >= rs.lo;
+        else { gt += key[e] > rs.tau; eq += key[e] == rs.tau; }
     }
     int tot;
     const int ex = block_excl_scan<BLK>(gt | (eq << 16), wsum, tot);
@@ -356,10 +437,10 @@ __device__ int reg_emit(const uint32_t (&key)[E], const bool (&val)[E], const Ra
     for (int e = 0; e < E; ++e) {
         if (!val[e]) continue;
         bool kp;
-        if (rs.whole_bin) kp = (key[e] & rs.kmask) >= rs.prefix;
+        if (rs.whole_bin) kp = key[e] >= rs.lo;
         else {
-            kp = key[e] > rs.prefix;
-            if (key[e] == rs.prefix) { kp = er < quota; ++er; }
+            kp = key[e] > rs.tau;
+            if (key[e] == rs.tau) { kp = er < quota; ++er; }
         }
         if (kp) out(pos++, e);
     }
@@ -772,7 +853,7 @@ __global__ __launch_bounds__(C2_BLK) void sel_chunk2_kernel(
     int ncand = 0;
     if (n_loc > 0) {
         const int k_loc = min(b, n_loc);
-        RadixSel rs{0u, 0u, 0, true};                    // k_loc == n_loc: keep every valid key
+        RadixSel rs{0u, 0u, 0, true};                    // k_loc == n_loc: keep every valid key (>= 0)
         if (k_loc < n_loc) rs = reg_kth_largest<C2_BLK, C2_E>(key, val, k_loc, hist, wtot, s3);
         ncand = reg_emit<C2_BLK, C2_E>(key, val, rs, wsum, [&](int pos, int e) {
             ck[pos] = key[e];

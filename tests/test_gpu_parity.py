@@ -144,6 +144,16 @@ def _random_select_inputs(seed, n_kv, G, seq_lens, MP, st, ties=None):
     elif ties == "underflow":
         sh[..., ::7] = -200.0                         # exp underflows to +0
         sh = np.where(rng.random(sh.shape) < 0.5, -300.0, sh).astype(np.float32)
+    elif ties == "sparse_peaks":
+        # fewer normal pages than the budget: the b-th key sits far below
+        # the row maximum (the selector's absolute-radix fallback)
+        keep = np.zeros(sh.shape, bool)
+        for idx in np.ndindex(*sh.shape[:3]):
+            keep[idx][rng.choice(MP, size=min(40, MP), replace=False)] = True
+        sh = np.where(keep, sh, -300.0).astype(np.float32)
+    elif ties == "far":
+        # a second cluster ~40 units (about 58 binades of exp) below
+        sh = np.where(rng.random(sh.shape) < 0.025, sh, sh - 40.0).astype(np.float32)
     npg, nsh, b = O.derive_page_params(seq_lens, 16, st.window_pages, st.sink_pages,
                                        st.budget_abs, st.budget)
     pm = np.full((R, n_kv, st.score_chunks, 16), -np.inf, np.float32)
@@ -252,7 +262,7 @@ def test_select_band_route_batch_size_changes(combine):
             assert np.array_equal(gtab, tab) and np.array_equal(gcnt, cnt)
 
 
-@pytest.mark.parametrize("ties", ["all_equal", "bands", "underflow"])
+@pytest.mark.parametrize("ties", ["all_equal", "bands", "underflow", "sparse_peaks", "far"])
 @pytest.mark.parametrize("ctx,bp", [(16384, 126), (131072, 126), (1 << 19, 126), (1 << 19, 3000)])
 def test_select_tie_batteries(ties, ctx, bp):
     import torch
