@@ -574,17 +574,17 @@ __global__ __launch_bounds__(DC_BLK) void decode_split_kernel(
         //      thread 0's arrival (it also keeps the compiler from moving any
         //      store past the barrier);
         //   3. an agent-scope atomic counts arrivals; the workgroup that sees
-        //      the last one acquires (workgroup fence after the barrier) and
-        //      reads the partials with SC1 loads, which cannot hit a stale
-        //      L2 line.
+        //      the last one acquires (agent-scope fence after the barrier)
+        //      and reads the partials with SC1 loads, which cannot hit a
+        //      stale L2 line.
         // Each row's counter sits in its own 256-B block: with the counters
         // of all rows packed in one cache line, every arrival of the launch
         // serialised on that line (measured +1.7 us per launch at Llama
         // 128K: 256 arrivals).
-        // Agent-scope release / acquire fences would add an L2 write-back
-        // (buffer_wbl2) and an L2 invalidate (buffer_inv) to every workgroup:
-        // measured +8 us per layer at Llama 128K (step 1.35 -> 1.62 ms), for
-        // data that never goes through the L2 here.
+        // An agent-scope release on every arrival would add an L2 write-back
+        // (buffer_wbl2) to every workgroup: measured +8 us per layer at Llama
+        // 128K (step 1.35 -> 1.62 ms, with the acquire side in every
+        // workgroup too), for data that never goes through the L2 here.
         __shared__ int last_s;
         __shared__ float lt_s[16];
         __builtin_amdgcn_s_waitcnt(0x0070);           // vmcnt(0): SC1 stores acknowledged
@@ -597,7 +597,10 @@ __global__ __launch_bounds__(DC_BLK) void decode_split_kernel(
         }
         __syncthreads();
         if (!last_s) return;
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        // the reader side under the memory model: an agent-scope acquire in
+        // the row's last workgroup only (one per row, so its L2 invalidate
+        // is not paid by every split)
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
         if (tid == 0) __hip_atomic_store(counters + rk * LOCKS_DECODE_COUNTER_STRIDE, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         merge_row<true, D>(m_part, l_part, acc_part, rk, r, kh, n_act, G, split, out, o_sr, o_sh,
                            out_f32, reinterpret_cast<float*>(stA), reinterpret_cast<float*>(stB), lt_s);
