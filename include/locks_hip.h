@@ -19,9 +19,9 @@
  * take head_dim in {64, 128, 256} and page in {16, 32, 64}, the reference's
  * domain (src/locks/selection/rki4_state.py:288-334: d in {64,128,256},
  * page in {16,32,64}, G <= 8; G up to 16 is needed by the GLM-4-9B
- * 32q/2kv geometry); the summary entries (build, score) head_dim 64, 128
- * or 256 with page 16 or 32 (locks_pack_rki4: 128 / 16); MLA: kv_lora_rank
- * 512 + 64 RoPE dims, <= 16 query heads.
+ * 32q/2kv geometry); the summary entries (build, score) the same domain
+ * (locks_pack_rki4: 128 / 16); MLA: kv_lora_rank 512 + 64 RoPE dims, <= 16
+ * query heads.
  *
  * Reference interfaces each entry replaces (paths under src/locks/):
  */
@@ -69,7 +69,7 @@ int32_t locks_score_num_chunks(int32_t max_pages, int32_t chunk);
  * rki4 per-head page LSE scores.
  * Replaces rki4_score_bt(q, v4, vs, c8, cs, mu8, mus, bt, nsh, S, sm_scale,
  * zsplit, n_req) (selection/rki4_score_cuda.py:2518-2619; math :653-722).
- *   (d = head_dim in {64, 128, 256}, P = page in {16, 32})
+ *   (d = head_dim in {64, 128, 256}, P = page in {16, 32, 64})
  *   q          (n_req, n_kv*G, d) bf16, strides (q_stride_req, q_stride_head, 1)
  *   v4         (num_blocks, n_kv, 8, d/2) u8  int4 column-major basis
  *   vs         (num_blocks, n_kv, 8)     bf16 per-column scales
@@ -268,8 +268,8 @@ int32_t locks_decode_dense(const uint16_t* q, int64_t q_stride_req, int64_t q_st
 
 /*
  * rki4 summary build on the GPU for the listed physical blocks of ONE layer
- * (head_dim 64 / 128 / 256 with page 16 or 32: GQA K heads; head_dim 512
- * with page 16: the MLA latent, n_kv 1).
+ * (head_dim 64 / 128 / 256 with page 16, 32 or 64: GQA K heads; head_dim
+ * 512 with page 16: the MLA latent, n_kv 1).
  * Replaces the reference build chain _write_pre -> _eigh_chunked ->
  * _write_post (selection/rki4_build.py:147-158, :93-129, :178-225, the
  * `rki4_build_{tail,bulk,delta,refresh}` producers :264-364 call it):

@@ -40,6 +40,10 @@ struct WaveLds {
     float mu[D];
     float A[PG][PG + 1];         // gram, rotated in place
     float U[PG][PG + 1];         // accumulated eigenvectors (columns)
+    // second buffers of the page-64 Jacobi step (one element per row 1 x 1
+    // otherwise)
+    float A2[PG == 64 ? PG : 1][PG + 1];
+    float U2[PG == 64 ? PG : 1][PG + 1];
     float cc[PG], ss[PG];
     float S8[BD_RNK];
     int col[BD_RNK];             // eigen column of basis r (ascending top-8)
@@ -139,7 +143,7 @@ __device__ __forceinline__ void pack_page(WaveLds<D, PG>& L, long row, uint8_t* 
     if (lane == 0) mus[row] = f32_to_bf16(msc);
 }
 
-// Parallel cyclic Jacobi on L.A (N x N symmetric, N = page = 16 or 32);
+// Parallel cyclic Jacobi on L.A (N x N symmetric, N = page = 16, 32 or 64);
 // eigenvectors -> L.U columns.  Round-robin pairing of step `step`: index 0
 // stays, 1..N-1 rotate; the pair of position k (1 <= k < N/2) is
 // (at(k), at(N-1-k)), position 0 pairs index 0 with at(0), where
@@ -168,9 +172,9 @@ __device__ __forceinline__ int rr_partner(int i, int step) {
 // result is checked through the quantised summary, not bit for bit.
 template <int N, class W>
 __device__ void jacobi(W& L) {
-    static_assert(N == 16 || N == 32, "page 16 or 32");
+    static_assert(N == 16 || N == 32 || N == 64, "page 16, 32 or 64");
     constexpr int RS = kWave / N, RPL = N * N / kWave;   // row stride, rows per lane
-    constexpr int SWEEPS = N == 16 ? 12 : 16;
+    constexpr int SWEEPS = N == 16 ? 12 : N == 32 ? 16 : 20;
     const int lane = threadIdx.x & 63;
     const int j = lane % N, r0 = lane / N;
     for (int i = lane; i < N * N; i += kWave) L.U[i / N][i % N] = (i / N == i % N) ? 1.f : 0.f;
@@ -194,10 +198,12 @@ __device__ void jacobi(W& L) {
         // accuracy (~3e-6 rel).
         if (!(off > 1e-12f * dia)) break;
         for (int step = 0; step < N - 1; ++step) {
+            // page 64: A / U alternate between the two buffers step by step
+            float (*Ac)[N + 1] = (N == 64 && (step & 1)) ? L.A2 : L.A;
             if (lane < N / 2) {
                 const int p = lane == 0 ? 0 : rr_at<N>(lane, step);
                 const int q = lane == 0 ? rr_at<N>(0, step) : rr_at<N>(N - 1 - lane, step);
-                const float apq = L.A[p][q], app = L.A[p][p], aqq = L.A[q][q];
+                const float apq = Ac[p][q], app = Ac[p][p], aqq = Ac[q][q];
                 float c = 1.f, sn = 0.f;
                 if (fabsf(apq) > 1e-30f) {                 // smaller: nothing to rotate away
                     const float theta = (aqq - app) * __builtin_amdgcn_rcpf(2.f * apq);
@@ -213,6 +219,22 @@ __device__ void jacobi(W& L) {
             asm volatile("" ::: "memory");
             const int pj = rr_partner<N>(j, step);
             const float cj = L.cc[j], sj = L.ss[j];
+            if constexpr (N == 64) {
+                // 64 rows per lane: read the current buffers, write the
+                // other ones (the old values are never overwritten inside the
+                // step, so nothing has to be held in registers), then swap
+                float (*Uc)[N + 1] = (step & 1) ? L.U2 : L.U;
+                float (*An)[N + 1] = (step & 1) ? L.A : L.A2;
+                float (*Un)[N + 1] = (step & 1) ? L.U : L.U2;
+                for (int i = 0; i < N; ++i) {
+                    const int pi = rr_partner<N>(i, step);
+                    const float ci = L.cc[i], si = L.ss[i];
+                    An[i][j] = cj * (ci * Ac[i][j] + si * Ac[pi][j]) + sj * (ci * Ac[i][pj] + si * Ac[pi][pj]);
+                    Un[i][j] = cj * Uc[i][j] + sj * Uc[i][pj];
+                }
+                asm volatile("" ::: "memory");
+                continue;
+            }
             float na[RPL], nu[RPL];
 #pragma unroll
             for (int e = 0; e < RPL; ++e) {
@@ -226,6 +248,14 @@ __device__ void jacobi(W& L) {
             for (int e = 0; e < RPL; ++e) {
                 L.A[r0 + RS * e][j] = na[e];
                 L.U[r0 + RS * e][j] = nu[e];
+            }
+            asm volatile("" ::: "memory");
+        }
+        if constexpr (N == 64) {
+            // a sweep has 63 steps: the result sits in the second buffers
+            for (int i = 0; i < N; ++i) {
+                L.A[i][lane] = L.A2[i][lane];
+                L.U[i][lane] = L.U2[i][lane];
             }
             asm volatile("" ::: "memory");
         }
@@ -311,7 +341,7 @@ __global__ __launch_bounds__((bd_waves<D, PG>() * kWave)) void rki4_build_kernel
         // 16 x 16 blocks (bi, bj) of the PG x PG matrix
         {
             const int i = lane & 15, kq = lane >> 4;
-#pragma unroll
+#pragma unroll 1
             for (int bi = 0; bi < PG / 16; ++bi)
 #pragma unroll
                 for (int bj = 0; bj < PG / 16; ++bj) {
@@ -435,12 +465,12 @@ __global__ __launch_bounds__(RF_THREADS) void refresh_compact_kernel(
 
 using namespace locks;
 
-// (head_dim, page) of the summary builder: {64, 128, 256} x {16, 32} (the
-// reference's rki4 geometry domain, rki4_state.py:295-324, without page 64)
-// plus the MLA latent (512, 16).
+// (head_dim, page) of the summary builder: {64, 128, 256} x {16, 32, 64}
+// (the reference's rki4 geometry domain, rki4_state.py:295-324) plus the MLA
+// latent (512, 16).
 static bool bd_geometry(int head_dim, int page) {
     if (head_dim == 512) return page == 16;
-    return (head_dim == 64 || head_dim == 128 || head_dim == 256) && (page == 16 || page == 32);
+    return (head_dim == 64 || head_dim == 128 || head_dim == 256) && (page == 16 || page == 32 || page == 64);
 }
 template <int D, int PG>
 static int bd_launch(const uint16_t* kc, const uint64_t* k_layers, long k_sb, long k_st, long k_sh,
@@ -460,9 +490,12 @@ static int bd_launch(const uint16_t* kc, const uint64_t* k_layers, long k_sb, lo
      : (PGV) == 16 ? ((HD) == 128 ? bd_launch<128, 16>(__VA_ARGS__)              \
                       : (HD) == 64 ? bd_launch<64, 16>(__VA_ARGS__)              \
                                    : bd_launch<256, 16>(__VA_ARGS__))            \
-                   : ((HD) == 128 ? bd_launch<128, 32>(__VA_ARGS__)              \
+     : (PGV) == 32 ? ((HD) == 128 ? bd_launch<128, 32>(__VA_ARGS__)              \
                       : (HD) == 64 ? bd_launch<64, 32>(__VA_ARGS__)              \
-                                   : bd_launch<256, 32>(__VA_ARGS__)))
+                                   : bd_launch<256, 32>(__VA_ARGS__))            \
+                   : ((HD) == 128 ? bd_launch<128, 64>(__VA_ARGS__)              \
+                      : (HD) == 64 ? bd_launch<64, 64>(__VA_ARGS__)              \
+                                   : bd_launch<256, 64>(__VA_ARGS__)))
 
 extern "C" int32_t locks_build_rki4(
     const uint16_t* k_cache, int64_t k_stride_block, int64_t k_stride_tok, int64_t k_stride_head,
@@ -471,7 +504,7 @@ extern "C" int32_t locks_build_rki4(
     uint16_t* mus, uint16_t* tag, void* stream)
 {
     LOCKS_REQUIRE(bd_geometry(head_dim, page),
-                  "locks_build_rki4: geometry d=%d page=%d unsupported (d 64/128/256 with page 16/32, "
+                  "locks_build_rki4: geometry d=%d page=%d unsupported (d 64/128/256 with page 16/32/64, "
                   "or d 512 with page 16)", head_dim, page);
     LOCKS_REQUIRE(n_kv >= 1 && num_blocks >= 1 && n_blocks >= 0, "locks_build_rki4: bad geometry");
     LOCKS_REQUIRE(k_stride_tok % 8 == 0 && k_stride_block % 8 == 0 && k_stride_head % 8 == 0,
@@ -552,7 +585,7 @@ extern "C" int32_t locks_build_rki4_layers(
 {
     LOCKS_REQUIRE(bd_geometry(head_dim, page),
                   "locks_build_rki4_layers: geometry d=%d page=%d unsupported (d 64/128/256 with page "
-                  "16/32, or d 512 with page 16)", head_dim, page);
+                  "16/32/64, or d 512 with page 16)", head_dim, page);
     LOCKS_REQUIRE(n_kv >= 1 && num_blocks >= 1 && n_blocks >= 0 && n_layers >= 1 &&
                       n_layers <= 65535 && slab_blocks >= num_blocks,
                   "locks_build_rki4_layers: bad geometry");

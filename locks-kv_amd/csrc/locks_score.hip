@@ -38,14 +38,14 @@ constexpr int SC_BLOCK = SC_WAVES * kWave;
 constexpr int SC_MAX_CHUNK = 1024;          // pages per workgroup, upper bound
 constexpr int SC_CPOL_NT = 2;                // buffer-load cache policy: non-temporal
 
-// Per-geometry layout (head_dim D in {64, 128, 256}, page PG in {16, 32}):
+// Per-geometry layout (head_dim D in {64, 128, 256}, page PG in {16, 32, 64}):
 // slab rows and the per-wave LDS stage of one (8-page tile, kv head) unit.
 // Stage rows are padded (+16 B) so the MFMA-order reads of 16 rows at once
 // hit distinct banks.
 template <int D, int PG>
 struct ScGeom {
     static_assert(D == 64 || D == 128 || D == 256, "head_dim 64, 128 or 256");
-    static_assert(PG == 16 || PG == 32, "page 16 or 32");
+    static_assert(PG == 16 || PG == 32 || PG == 64, "page 16, 32 or 64");
     static constexpr int VROW = SC_RNK * D / 2;        // packed V bytes per slab row
     static constexpr int NVL = D / 32;                 // 1-KB V loads per unit
     static constexpr int NCL = PG / 16;                // 1-KB coefficient loads per unit
@@ -540,8 +540,8 @@ extern "C" int32_t locks_score_rki4(
     int32_t n_req, int32_t n_kv, int32_t G, int32_t head_dim, int32_t page,
     float sm_scale, void* stream)
 {
-    LOCKS_REQUIRE((head_dim == 64 || head_dim == 128 || head_dim == 256) && (page == 16 || page == 32),
-                  "locks_score_rki4: head_dim %d / page %d outside {64,128,256} x {16,32}", head_dim, page);
+    LOCKS_REQUIRE((head_dim == 64 || head_dim == 128 || head_dim == 256) && (page == 16 || page == 32 || page == 64),
+                  "locks_score_rki4: head_dim %d / page %d outside {64,128,256} x {16,32,64}", head_dim, page);
     LOCKS_REQUIRE(G >= 1 && G <= 16, "locks_score_rki4: G=%d outside [1, 16]", G);
     LOCKS_REQUIRE(n_req >= 0 && n_req <= 65535 && n_kv >= 1 && n_kv <= 65535,
                   "locks_score_rki4: n_req=%d / n_kv=%d outside the grid limits", n_req, n_kv);
@@ -577,10 +577,14 @@ extern "C" int32_t locks_score_rki4(
         if (head_dim == 128) LAUNCH_G(128, 16);
         else if (head_dim == 64) LAUNCH_G(64, 16);
         else LAUNCH_G(256, 16);
-    } else {
+    } else if (page == 32) {
         if (head_dim == 128) LAUNCH_G(128, 32);
         else if (head_dim == 64) LAUNCH_G(64, 32);
         else LAUNCH_G(256, 32);
+    } else {
+        if (head_dim == 128) LAUNCH_G(128, 64);
+        else if (head_dim == 64) LAUNCH_G(64, 64);
+        else LAUNCH_G(256, 64);
     }
 #undef LAUNCH_G
 #undef LAUNCH

@@ -19,7 +19,7 @@ per-chunk maxima -- and sel_ws, the selector's candidate workspace.
 
 Footprint per (page, kv head): 5d + 10*page + 18 bytes of summary (818 B at
 d=128, page 16) + 16 B tag (rki4_state.py:18-22, record_bytes :124-141).
-Geometry: d in {64, 128, 256}, page 16 or 32, G <= 16.
+Geometry: d in {64, 128, 256}, page 16, 32 or 64, G <= 16.
 """
 from __future__ import annotations
 
@@ -110,14 +110,13 @@ class Rki4State:
     @staticmethod
     def validate_geometry(*, head_dim: int, G: int, page: int, rank: int = RNK) -> None:
         """Supported set of the gfx950 kernels, checked at wiring time: the
-        reference's d in {64, 128, 256} (rki4_state.py:295-324) with page 16
-        or 32 (its page 64 is served by the decode kernels only, not by the
-        summary build and scorer of this build), G up to 16."""
+        reference's d in {64, 128, 256} and page in {16, 32, 64}
+        (rki4_state.py:295-324), G up to 16."""
         assert head_dim in (64, 128, 256), \
             f"rki4 supports d in {{64, 128, 256}}, model has d={head_dim}"
         assert 1 <= G <= 16, f"this build supports 1 <= G <= 16 query heads per kv head, got {G}"
-        assert page in (16, 32), \
-            f"this MI355X build supports page 16 or 32 for rki4 summaries, engine block_size={page}"
+        assert page in (16, 32, 64), \
+            f"rki4 supports page in {{16, 32, 64}}, engine block_size={page}"
         assert rank == RNK, f"rki4 rank is fixed at {RNK} in this build, got {rank}"
 
     @classmethod

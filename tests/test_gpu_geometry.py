@@ -117,7 +117,8 @@ def test_dense_geometry(hd, page):
 
 
 # ---- summaries (build + scorer) and the whole step at the other geometries ----
-SUMMARY_GEOMS = [(64, 16), (256, 16), (128, 32), (64, 32), (256, 32)]
+SUMMARY_GEOMS = [(64, 16), (256, 16), (128, 32), (64, 32), (256, 32), (128, 64), (64, 64),
+                 (256, 64)]
 
 
 def _state(case, *, L=1, budget_pages=40, split=64):
@@ -211,7 +212,7 @@ def test_build_geometry(hd, page):
     assert diff.mean() < 0.02 and diff.max() < 0.5
 
 
-@pytest.mark.parametrize("hd,page", [(64, 16), (256, 32), (128, 32)])
+@pytest.mark.parametrize("hd,page", [(64, 16), (256, 32), (128, 32), (128, 64)])
 def test_step_geometry(hd, page):
     """The reference's call sites (select adapter + decode dispatch) on one
     layer at another geometry vs the oracle pipeline: page tables equal up

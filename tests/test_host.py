@@ -76,9 +76,9 @@ def test_rejects_bad_geometry_without_device():
     rc = lib.locks_score_rki4(*args)           # head_dim 96 is outside the contract
     assert rc == -1 and b"head_dim 96" in lib.locks_last_error()
     args[-4] = 64
-    args[-3] = 64                              # page 64: decode only, no summary scorer
+    args[-3] = 128                             # page 128: outside the domain
     rc = lib.locks_score_rki4(*args)
-    assert rc == -1 and b"page 64" in lib.locks_last_error()
+    assert rc == -1 and b"page 128" in lib.locks_last_error()
     rc = lib.locks_decode_splitk(*([1, 8, 8] + [1, 8, 8, 8] * 2 + [1, 1, 8, 1, 1, 8, 8, 1, 1,
                                    8, 1, 1, 1, 1, 1, 2, 17, 128, 16, 4, 1, 0, 0.1, None]))
     assert rc == -1 and b"G=17" in lib.locks_last_error()
@@ -171,10 +171,10 @@ def test_register_refuses_vllm_without_backend_class(monkeypatch):
 def test_geometry_contract():
     from locks.selection import Rki4State
     for d in (64, 128, 256):
-        for page in (16, 32):
+        for page in (16, 32, 64):
             Rki4State.validate_geometry(head_dim=d, G=16, page=page)
     for kw in (dict(head_dim=96, G=4, page=16), dict(head_dim=128, G=17, page=16),
-               dict(head_dim=128, G=4, page=64), dict(head_dim=512, G=4, page=16),
+               dict(head_dim=128, G=4, page=128), dict(head_dim=512, G=4, page=16),
                dict(head_dim=128, G=4, page=8)):
         with pytest.raises(AssertionError):
             Rki4State.validate_geometry(**kw)
@@ -246,8 +246,8 @@ def test_refresh_entries_reject_bad_arguments_without_device():
     bl = [1, 2, 16 * 8 * 128, 8 * 128, 128, 100, 1, None, 4, 8, 128, 16, 100] + [1] * 7 + [None]
     b = list(bl); b[10] = 96
     assert lib.locks_build_rki4_layers(*b) == -1 and b"d=96" in lib.locks_last_error()
-    b = list(bl); b[11] = 64                             # page 64: decode only
-    assert lib.locks_build_rki4_layers(*b) == -1 and b"page=64" in lib.locks_last_error()
+    b = list(bl); b[11] = 8                              # page 8: outside the domain
+    assert lib.locks_build_rki4_layers(*b) == -1 and b"page=8" in lib.locks_last_error()
     b = list(bl); b[12] = 50                             # slab smaller than the K pool bound
     assert lib.locks_build_rki4_layers(*b) == -1 and b"bad geometry" in lib.locks_last_error()
     b = list(bl); b[3] = 12                              # token stride not a multiple of 8

@@ -319,7 +319,7 @@ def test_merge_split_invariance():
 
 
 # ---- the other geometries (rki4_state.py:295-324: d 64/128/256, page 16/32) ----
-GEOMS = [(64, 16), (256, 16), (128, 32), (64, 32), (256, 32)]
+GEOMS = [(64, 16), (256, 16), (128, 32), (64, 32), (256, 32), (128, 64), (256, 64)]
 
 
 @pytest.mark.parametrize("d,page", GEOMS)
@@ -392,7 +392,7 @@ def test_geometry_rank0_closed_form(d, page):
             assert np.allclose(out[0, kh, :, p], s * mud + math.log(page), atol=1e-5)
 
 
-@pytest.mark.parametrize("d,page", GEOMS + [(128, 64)])
+@pytest.mark.parametrize("d,page", GEOMS)
 def test_geometry_decode_matches_sdpa(d, page):
     """decode_attention over every page of a ragged row equals float64 SDPA."""
     import torch
