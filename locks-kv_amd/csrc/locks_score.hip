@@ -15,16 +15,17 @@
 // of one (request, kv head); a wave handles 8 pages per tile:
 //   * the int4 x int8 projection of the whole GQA group runs on the matrix
 //     core: v_mfma_i32_16x16x64_i8 with A = q8 (16 head rows, zero padded)
-//     and B = 2 pages x 8 basis columns.  The int4 nibbles are fed BIASED
-//     (n ^ 8 = V + 8, one AND per 4 values, no sign extension) and the
-//     +8 * sum_d q8 plane is removed exactly in int32 afterwards;
+//     and B = 2 pages x 8 basis columns.  Each int4 nibble is moved to the
+//     high half of its byte (one shift and one AND per 8 values), so the
+//     operand is 16 V as int8, no sign extension; the 1/16 rides on the
+//     column scale;
 //   * mu . q8 uses the same MFMA with B = one mu row per column (page);
 //   * the per-token reconstruction sum_c c8[t][c] qt[g][c] is a 16x8 by
 //     8xG product per page: v_mfma_f32_16x16x4_f32 with pages packed side by
 //     side when G < 16 (block-diagonal B), so the VALU only does the cs/mu
 //     epilogue and the 16-token LSE (4 tokens per lane + 2 cross-row steps).
-// Summary bytes are read exactly once, straight from the six slabs through
-// the block table.  Per-WG page maxima are published to `pmax` so the
+// Summary bytes are read exactly once, DMA'd straight from the six slabs
+// (through the block table) into per-wave LDS stages, one unit ahead.  Per-WG page maxima are published to `pmax` so the
 // selector can form the per-head max without re-reading score_h.
 #include "locks_common.h"
 #include "locks_hip.h"
@@ -38,10 +39,20 @@ constexpr int SC_BLOCK = SC_WAVES * kWave;
 constexpr int SC_MAX_CHUNK = 1024;          // pages per workgroup, upper bound
 constexpr int SC_CPOL_NT = 2;                // buffer-load cache policy: non-temporal
 
-// Per-geometry layout (head_dim D in {64, 128, 256}, page PG in {16, 32, 64}):
-// slab rows and the per-wave LDS stage of one (8-page tile, kv head) unit.
-// Stage rows are padded (+16 B) so the MFMA-order reads of 16 rows at once
-// hit distinct banks.
+// Per-geometry layout (head_dim D in {64, 128, 256}, page PG in {16, 32, 64})
+// of the slab rows and of one wave's LDS stage for an (8-page tile, kv head)
+// unit.  The stage is written by LDS DMA (global_load_lds_dwordx4: lane L of
+// an instruction fills bytes 16 L .. 16 L + 15 of a 1-KB block), so rows
+// cannot be padded; instead the 16-byte chunks of each packed-V and centroid
+// row are XOR-swizzled (chunk k of row R stored at k ^ swz(R)), which spreads
+// the MFMA-order reads of 16 (resp. 8) rows at the same column over all 64
+// banks.  Three separate LDS objects per wave:
+//   sv: packed V (8 pages x 8 columns x D/2 B) + centroids (8 x D B)
+//   sc: coefficients (8 pages x PG x 8 B) + token scales (bf16) + column scales (bf16)
+//   sm: per-page centroid terms mud (8 pages x 16 heads f32)
+// The next unit's sv DMA is issued as soon as sv has been read into
+// registers; the token stage then reads only sc and sm, which the compiler's
+// memory-counter tracking can tell apart from the DMA's destination.
 template <int D, int PG>
 struct ScGeom {
     static_assert(D == 64 || D == 128 || D == 256, "head_dim 64, 128 or 256");
@@ -52,19 +63,26 @@ struct ScGeom {
     static constexpr int NML = D >= 128 ? D / 128 : 1; // centroid loads per unit (D = 64: half)
     static constexpr int NWIN = D / 64;                // 16-d windows per lane (projection MFMAs)
     static constexpr int NTB = PG / 16;                // 16-token blocks per page
-    static constexpr int VROWB = D / 2 + 16;           // one (page, column) V row, padded
-    static constexpr int VPAIR = 16 * VROWB;           // 2 pages x 8 columns
-    static constexpr int MUROWB = D + 16;              // one page's centroid row, padded
-    static constexpr int ST_V = 0;                     // 4 pairs of packed V
-    static constexpr int ST_C8 = 4 * VPAIR;            // 8 pages x PG x 8 coefficients
-    static constexpr int ST_MU = ST_C8 + 64 * PG;      // 8 centroid rows (-> mud after use)
-    static constexpr int ST_CS = ST_MU + 8 * MUROWB;   // 8 pages x PG token scales (f32)
-    static constexpr int ST_VS = ST_CS + 32 * PG;      // 8 pages x 8 column scales (f32)
-    static constexpr int ST_MUS = ST_VS + 256;         // 8 dwords: centroid scales
-    static constexpr int ST_BYTES = ST_MUS + 32;
+    static constexpr int VCH = D / 32;                 // 16-B chunks per packed-V row (page, column)
+    static constexpr int MCH = D / 16;                 // 16-B chunks per centroid row
+    static constexpr int SV_MU = 8 * VROW;             // centroid rows after the packed V
+    static constexpr int SV_BYTES = SV_MU + 8 * D;
+    static constexpr int SC_C8 = 0;                    // 8 pages x PG x 8 int8
+    static constexpr int SC_CS = 64 * PG;              // 8 pages x PG bf16
+    static constexpr int SC_VS = SC_CS + 16 * PG;      // 8 pages x 8 bf16
+    static constexpr int SC_BYTES = SC_VS + 128;
     static constexpr int QROW = D + 16;                // padded int8 q row
-    static_assert(8 * MUROWB >= 8 * 16 * 4, "mud fits the centroid rows");
+    // rows R .. R + 16 / VCH - 1 share a 256-B bank period; distinct swizzles
+    // across the periods make 16 consecutive rows hit distinct banks
+    static constexpr int vswz(int R) { return (R / (16 / VCH)) & (VCH - 1); }
+    static constexpr int mswz(int R) { return (R / (16 / MCH)) & (MCH - 1); }
 };
+
+typedef __attribute__((address_space(3))) void* sc_lds_ptr;
+
+// One lane's byte offsets into the six slabs for one unit.
+template <int NVL, int NML, int NCL>
+struct ScUnitOff { uint32_t v[NVL], m[NML], c[NCL], cs, vs, mus; };
 
 __device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d) {
     return (uint32_t)(uint8_t)a | ((uint32_t)(uint8_t)b << 8) |
@@ -85,10 +103,10 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
     constexpr int PPM = 16 / GW;            // pages per token-stage MFMA
     constexpr int NGRP = SC_TILE / PPM;     // token-stage groups per tile
     constexpr int NVL = GM::NVL, NCL = GM::NCL, NML = GM::NML, NWIN = GM::NWIN, NTB = GM::NTB;
-    constexpr int SC_VROW = GM::VROW, ST_VROWB = GM::VROWB, ST_VPAIR = GM::VPAIR, ST_MUROWB = GM::MUROWB;
-    constexpr int ST_V = GM::ST_V, ST_C8 = GM::ST_C8, ST_MU = GM::ST_MU, ST_CS = GM::ST_CS,
-                  ST_VS = GM::ST_VS, ST_MUS = GM::ST_MUS, ST_BYTES = GM::ST_BYTES, SC_QROW = GM::QROW;
-    constexpr int LPH = D / 16;             // q lanes per head (16 dims each)
+    constexpr int SC_VROW = GM::VROW, VCH = GM::VCH, MCH = GM::MCH;
+    constexpr int SV_MU = GM::SV_MU, SC_C8 = GM::SC_C8, SC_CS = GM::SC_CS, SC_VS = GM::SC_VS, SC_QROW = GM::QROW;
+    constexpr int QDL = D <= 128 ? 8 : 16;  // q dims per lane in the quantize step
+    constexpr int LPH = D / QDL;            // q lanes per head (8 or 16: one DPP row group)
     const int z = blockIdx.x, h = blockIdx.y, r = blockIdx.z;   // page chunk, kv head, request
     const int Z = gridDim.x;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -103,10 +121,13 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
     }
 
     __shared__ __attribute__((aligned(16))) float qsp[16];
-    __shared__ __attribute__((aligned(16))) uint8_t stage_l[SC_WAVES][ST_BYTES];
+    __shared__ __attribute__((aligned(16))) uint8_t sv_l[SC_WAVES][GM::SV_BYTES];
+    __shared__ __attribute__((aligned(16))) uint8_t sc0_l[SC_WAVES][GM::SC_BYTES];
+    __shared__ __attribute__((aligned(16))) uint8_t sc1_l[SC_WAVES][GM::SC_BYTES];
+    __shared__ __attribute__((aligned(16))) float sm_l[SC_WAVES][SC_TILE * 16];
     __shared__ uint32_t wmax[16];
     // dynamic LDS: int8 q rows of this kv head's G query heads (+16 zero
-    // rows), chunk block ids
+    // rows), slab rows (block x n_kv + kv head) of the chunk
     extern __shared__ __attribute__((aligned(16))) uint8_t dyn_l[];
     int8_t (*q8s)[SC_QROW] = reinterpret_cast<int8_t (*)[SC_QROW]>(dyn_l);
     int* bt_l = reinterpret_cast<int*>(dyn_l + (size_t)(G + 16) * SC_QROW);
@@ -114,17 +135,17 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
     // ---- prologue: q rows and block ids are fetched together; the first
     // unit's summary loads are issued before q is quantized, so the
     // quantization overlaps them.
-    // q: D / 16 consecutive lanes per head, 16 dims (two 16-byte loads) per
-    // lane (G <= 16 heads x D / 16 lanes <= 256 threads)
+    // q: LPH consecutive lanes per head, QDL dims (one or two 16-byte loads)
+    // per lane (G <= 16 heads x LPH lanes <= 256 threads)
     // Unconditional loads (threads past the group re-read its last head and
     // are never stored): a guarded load would make the compiler wait for it
     // at the branch join, before the block ids below are even requested.
     const int qg = tid / LPH;                                 // this thread's head in the group
-    const uint4* qp = reinterpret_cast<const uint4*>(q + (long)r * q_sr + (long)(h * G + min(qg, G - 1)) * q_sh + (tid % LPH) * 16);
-    const uint4 qa0 = qp[0], qa1 = qp[1];
+    const uint4* qp = reinterpret_cast<const uint4*>(q + (long)r * q_sr + (long)(h * G + min(qg, G - 1)) * q_sh + (tid % LPH) * QDL);
+    const uint4 qa0 = qp[0], qa1 = (QDL == 16) ? qp[1] : qa0;
     for (int i = tid; i < c1 - c0; i += SC_BLOCK) {
         const int b = bt[(long)r * bt_sr + min(c0 + i, bt_cols - 1)];
-        bt_l[i] = min(max(b, 0), NB - 1);
+        bt_l[i] = min(max(b, 0), NB - 1) * n_kv + h;           // slab row of (block, kv head)
     }
     if (tid < 16) {
         wmax[tid] = 0x007FFFFFu;                               // f2u(-inf)
@@ -142,117 +163,118 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
     const int n_tiles = cdiv(c1 - c0, SC_TILE);
     const int n_units = n_tiles;             // (8-page tile) units of the chunk
 
-    // Each (8-page tile, kv head) unit is fetched into VGPRs in natural
-    // (contiguous) lane order -- fully coalesced 16-byte loads -- one unit
-    // ahead of the one being scored, then written to this wave's LDS stage
-    // and read back in MFMA operand order.  Consecutive units are the kv
-    // heads of one tile, whose slab rows are adjacent.
-    uint4 fv[NVL], fc8[NCL], fmu[NML], fcs, fvs;
-    uint32_t fmus;
-    // The six slabs are read through buffer loads: the large rows (packed V,
-    // coefficients, centroid: 768 of 818 B per row) with the non-temporal
-    // policy -- every row is read once -- and the small scale rows (16, 32
-    // and 2 B, whose cache lines are shared with the next kv head's or
-    // block's rows, read by another workgroup) with the default policy, so
-    // those lines stay in the L2 for it.  Measured per launch: Llama 128K
-    // 17.0 -> 15.8 us, GLM 1M 31.6 -> 30.5 us (NT on the small rows as well:
-    // 16.1 / 32.6 us).
-    auto rsv = [](const void* b) { return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(b), 0, -1, 0x00020000); };
-    const auto rs_v4 = rsv(v4), rs_c8 = rsv(c8), rs_mu = rsv(mu8), rs_cs = rsv(cs), rs_vs = rsv(vs), rs_mus = rsv(mus);
-    auto ld_big = [&](__amdgpu_buffer_rsrc_t rs, uint32_t off) -> uint4 {
-        return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)off, 0, SC_CPOL_NT));
-    };
-    auto ld_small = [&](__amdgpu_buffer_rsrc_t rs, uint32_t off) -> uint4 {
-        return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)off, 0, 0));
-    };
-    auto load_unit = [&](int u) {
+    // Each (8-page tile, kv head) unit's rows are DMA'd straight from the six
+    // slabs into this wave's LDS stage (no VGPR round trip).  Consecutive
+    // units are the kv heads of one tile, whose slab rows are adjacent.  The
+    // large rows (packed V, coefficients, centroid: 768 of 818 B per row) are
+    // read with the non-temporal policy -- every row is read once -- and the
+    // small scale rows (16, 32 and 2 B, whose cache lines are shared with the
+    // next kv head's or block's rows, read by another workgroup) with the
+    // default policy, so those lines stay in the L2 for it.
+    const uint8_t* const v4b = v4;
+    const uint8_t* const c8b = reinterpret_cast<const uint8_t*>(c8);
+    const uint8_t* const mub = reinterpret_cast<const uint8_t*>(mu8);
+    const uint8_t* const csb = reinterpret_cast<const uint8_t*>(cs);
+    const uint8_t* const vsb = reinterpret_cast<const uint8_t*>(vs);
+    const auto rs_mus = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(mus), 0, -1, 0x00020000);
+    uint8_t* const sv = sv_l[wave];
+    float* const mud_w = sm_l[wave];                 // [page][16 heads]
+    uint32_t fmus = 0;                               // centroid scale of page lane & 15 (lanes & 15 < 8)
+    // Every lane's slab offsets of one unit, read from the block ids in LDS
+    // while no DMA is outstanding (an LDS read issued behind a DMA waits for
+    // it) and pinned in registers before the first DMA of the unit.
+    using UnitOff = ScUnitOff<NVL, NML, NCL>;
+    auto unit_off = [&](int u) -> UnitOff {
         const int p0 = u * SC_TILE;
-        const int last = min(SC_TILE, c1 - c0 - p0) - 1;
-        const int* bl = bt_l + p0;
-        auto row_of = [&](int i) -> uint32_t { return (uint32_t)bl[min(i, last)] * (uint32_t)n_kv + (uint32_t)h; };
-        // 1 KB per load in natural order: byte o = 1024 i + 16 lane of the
-        // unit's (page-major) rows
+        const int last = min(SC_TILE, c1 - c0 - p0) - 1;   // tail pages repeat the last one
+        auto row = [&](int i) -> uint32_t { return (uint32_t)bt_l[p0 + min(i, last)]; };
+        UnitOff f;
 #pragma unroll
-        for (int i = 0; i < NVL; ++i) {                 // packed V: 8 pages x SC_VROW
-            const int o = 1024 * i + 16 * lane;
-            fv[i] = ld_big(rs_v4, row_of(o / SC_VROW) * SC_VROW + o % SC_VROW);
+        for (int i = 0; i < NVL; ++i) {              // LDS chunk s <- row R, chunk (s % VCH) ^ swz(R)
+            const int s = 64 * i + lane, R = s / VCH, k = (s % VCH) ^ GM::vswz(R);
+            f.v[i] = row(R >> 3) * SC_VROW + (R & 7) * (D / 2) + 16 * k;
         }
-#pragma unroll
-        for (int i = 0; i < NCL; ++i) {                 // coefficients: 8 pages x PG x 8
-            const int o = 1024 * i + 16 * lane;
-            fc8[i] = ld_big(rs_c8, row_of(o / (PG * SC_RNK)) * (PG * SC_RNK) + o % (PG * SC_RNK));
-        }
-#pragma unroll
-        for (int i = 0; i < NML; ++i) {                 // centroid: 8 pages x D
-            const int o = 1024 * i + 16 * lane;
-            if (D >= 128 || lane < 32) fmu[i] = ld_big(rs_mu, row_of(o / D) * D + o % D);
-        }
-        if (lane < PG) {                              // 8 pages x PG x 2 B token scales
-            const int o = 16 * lane;
-            fcs = ld_small(rs_cs, row_of(o / (2 * PG)) * (2 * PG) + o % (2 * PG));
-        }
-        if (lane < 8) {                               // 8 pages x 16 B column scales
-            const uint32_t row = row_of(lane);
-            fvs = ld_small(rs_vs, row * (SC_RNK * 2));
-            fmus = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs_mus, (int)(row * 2), 0, 0);   // centroid scale
-        }
-    };
-    auto store_unit = [&](uint8_t* stg) {
-#pragma unroll
-        for (int i = 0; i < NVL; ++i) {               // byte o -> page, basis column, chunk
-            const int o = 1024 * i + 16 * lane;
-            const int pg = o / SC_VROW, w = o % SC_VROW;
-            *reinterpret_cast<uint4*>(stg + ST_V + (pg >> 1) * ST_VPAIR +
-                                      ((pg & 1) * 8 + w / (D / 2)) * ST_VROWB + w % (D / 2)) = fv[i];
-        }
-#pragma unroll
-        for (int i = 0; i < NCL; ++i)
-            *reinterpret_cast<uint4*>(stg + ST_C8 + 1024 * i + lane * 16) = fc8[i];
 #pragma unroll
         for (int i = 0; i < NML; ++i) {
+            const int s = 64 * i + lane, R = (s / MCH) & 7, k = (s % MCH) ^ GM::mswz(R);
+            f.m[i] = row(R) * D + 16 * k;
+        }
+#pragma unroll
+        for (int i = 0; i < NCL; ++i) {
             const int o = 1024 * i + 16 * lane;
+            f.c[i] = row(o / (PG * SC_RNK)) * (PG * SC_RNK) + o % (PG * SC_RNK);
+        }
+        const int oc = 16 * (lane % PG);
+        f.cs = row(oc / (2 * PG)) * (2 * PG) + oc % (2 * PG);
+        f.vs = row(lane & 7) * (SC_RNK * 2);
+        f.mus = row(lane & 7) * 2;
+#pragma unroll
+        for (int i = 0; i < NVL; ++i) asm volatile("" :: "v"(f.v[i]));
+#pragma unroll
+        for (int i = 0; i < NML; ++i) asm volatile("" :: "v"(f.m[i]));
+#pragma unroll
+        for (int i = 0; i < NCL; ++i) asm volatile("" :: "v"(f.c[i]));
+        asm volatile("" :: "v"(f.cs), "v"(f.vs), "v"(f.mus));
+        return f;
+    };
+    auto issue_sv = [&](const UnitOff& f) {          // packed V + centroid rows, centroid scale
+#pragma unroll
+        for (int i = 0; i < NVL; ++i) {
+            const uint32_t o = f.v[i];               // copied out first: a member of f inside the builtin's
+                                                     // arguments makes the host pass drop the kernel stub
+            __builtin_amdgcn_global_load_lds(v4b + o, (sc_lds_ptr)(sv + 1024 * i), 16, 0, SC_CPOL_NT);
+        }
+#pragma unroll
+        for (int i = 0; i < NML; ++i) {
+            const uint32_t o = f.m[i];
             if (D >= 128 || lane < 32)
-                *reinterpret_cast<uint4*>(stg + ST_MU + (o / D) * ST_MUROWB + o % D) = fmu[i];
+                __builtin_amdgcn_global_load_lds(mub + o, (sc_lds_ptr)(sv + SV_MU + 1024 * i), 16, 0, SC_CPOL_NT);
         }
-        if (lane < PG) {                              // token scales widened to f32 once
-            *reinterpret_cast<float4*>(stg + ST_CS + lane * 32) =
-                make_float4(bf16lo(fcs.x), bf16hi(fcs.x), bf16lo(fcs.y), bf16hi(fcs.y));
-            *reinterpret_cast<float4*>(stg + ST_CS + lane * 32 + 16) =
-                make_float4(bf16lo(fcs.z), bf16hi(fcs.z), bf16lo(fcs.w), bf16hi(fcs.w));
+        if ((lane & 15) < 8)
+            fmus = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs_mus, (int)f.mus, 0, 0);
+    };
+    auto issue_sc = [&](const UnitOff& f, uint8_t* sc) {   // coefficients, token and column scales
+#pragma unroll
+        for (int i = 0; i < NCL; ++i) {
+            const uint32_t o = f.c[i];
+            __builtin_amdgcn_global_load_lds(c8b + o, (sc_lds_ptr)(sc + SC_C8 + 1024 * i), 16, 0, SC_CPOL_NT);
         }
-        if (lane < 8) {                               // column scales widened to f32 once
-            *reinterpret_cast<float4*>(stg + ST_VS + lane * 32) =
-                make_float4(bf16lo(fvs.x), bf16hi(fvs.x), bf16lo(fvs.y), bf16hi(fvs.y));
-            *reinterpret_cast<float4*>(stg + ST_VS + lane * 32 + 16) =
-                make_float4(bf16lo(fvs.z), bf16hi(fvs.z), bf16lo(fvs.w), bf16hi(fvs.w));
-            *reinterpret_cast<uint32_t*>(stg + ST_MUS + lane * 4) = fmus;
-        }
+        const uint32_t ocs = f.cs, ovs = f.vs;
+        if (lane < PG)                               // 8 pages x PG x 2 B
+            __builtin_amdgcn_global_load_lds(csb + ocs, (sc_lds_ptr)(sc + SC_CS), 16, 0, 0);
+        if (lane < 8)                                // 8 pages x 16 B
+            __builtin_amdgcn_global_load_lds(vsb + ovs, (sc_lds_ptr)(sc + SC_VS), 16, 0, 0);
     };
     __builtin_amdgcn_s_waitcnt(0x0070);      // q rows resident before the unit loads queue
-    if (wave < n_units) load_unit(wave);
+    if (wave < n_units) { const UnitOff f = unit_off(wave); issue_sv(f); issue_sc(f, sc0_l[wave]); }
 
     // ---- quantize q (the first unit's loads are in flight) --------------
     // q8 = rint(q / qs) with the correctly rounded quotient: q * (1 / qs) is
     // within 2 ulp of it, which decides the rounding unless the product lies
     // within 2^-15 of a half-integer; those (rare) lanes redo the division.
     const float s2 = sm_scale * 1.4426950408889634f;           // tokens in log2 units
-    if (tid < 16 * LPH) {                                     // 16 heads x D / 16 lanes
+    if (tid < G * LPH) {                                      // G heads x LPH lanes
         const int c = tid, hq = qg;
         const uint32_t w[8] = {qa0.x, qa0.y, qa0.z, qa0.w, qa1.x, qa1.y, qa1.z, qa1.w};
-        float f[16];
+        float f[QDL];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) { f[2 * k] = bf16lo(w[k]); f[2 * k + 1] = bf16hi(w[k]); }
+        for (int k = 0; k < QDL / 2; ++k) { f[2 * k] = bf16lo(w[k]); f[2 * k + 1] = bf16hi(w[k]); }
         float am = 0.f;
 #pragma unroll
-        for (int k = 0; k < 16; ++k) am = fmaxf(am, fabsf(f[k]));
-#pragma unroll
-        for (int o = 1; o < LPH; o <<= 1) am = fmaxf(am, __shfl_xor(am, o, kWave));
+        for (int k = 0; k < QDL; ++k) am = fmaxf(am, fabsf(f[k]));
+        // max over the head's LPH lanes (aligned groups of 8 or 16) by DPP:
+        // quad swaps, then the half-row and (16) row mirrors
+        am = fmaxf(am, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(am), 0xB1, 0xF, 0xF, false)));
+        am = fmaxf(am, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(am), 0x4E, 0xF, 0xF, false)));
+        am = fmaxf(am, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(am), 0x141, 0xF, 0xF, false)));
+        if constexpr (LPH == 16)
+            am = fmaxf(am, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(am), 0x140, 0xF, 0xF, false)));
         const float qs = fmaxf(am, 1e-8f) / 127.f;
         const float inv = 1.f / qs;
-        int iq[16];
+        int iq[QDL];
         bool near = false;
 #pragma unroll
-        for (int k = 0; k < 16; ++k) {
+        for (int k = 0; k < QDL; ++k) {
             const float y = f[k] * inv;
             const float ry = rintf(y);
             near |= fabsf(fabsf(y - ry) - 0.5f) < 0x1p-15f;
@@ -261,15 +283,14 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
         if (__builtin_expect(__ballot(near) != 0ull, 0)) {
             if (near) {
 #pragma unroll
-                for (int k = 0; k < 16; ++k) iq[k] = (int)rintf(__fdiv_rn(f[k], qs));
+                for (int k = 0; k < QDL; ++k) iq[k] = (int)rintf(__fdiv_rn(f[k], qs));
             }
         }
-        if (hq < G) {
-            *reinterpret_cast<uint4*>(&q8s[hq][(c % LPH) * 16]) =
-                make_uint4(pack4_i8(iq[0], iq[1], iq[2], iq[3]), pack4_i8(iq[4], iq[5], iq[6], iq[7]),
-                           pack4_i8(iq[8], iq[9], iq[10], iq[11]), pack4_i8(iq[12], iq[13], iq[14], iq[15]));
-            if (c % LPH == 0) qsp[hq] = qs * s2;
-        }
+        int8_t* qrow = &q8s[hq][(c % LPH) * QDL];
+        *reinterpret_cast<uint2*>(qrow) = make_uint2(pack4_i8(iq[0], iq[1], iq[2], iq[3]), pack4_i8(iq[4], iq[5], iq[6], iq[7]));
+        if constexpr (QDL == 16)
+            *reinterpret_cast<uint2*>(qrow + 8) = make_uint2(pack4_i8(iq[8], iq[9], iq[10], iq[11]), pack4_i8(iq[12], iq[13], iq[14], iq[15]));
+        if (c % LPH == 0) qsp[hq] = qs * s2;
     }
     __syncthreads();
 
@@ -304,10 +325,16 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
         for (int ps = 0; ps < PPM; ++ps) qsjm[ps] = (psub_l == ps) ? qsj : 0.f;
     }
 
-    uint8_t* stg = stage_l[wave];
-    for (int u = wave; u < n_units; u += SC_WAVES) {
-        store_unit(stg);
-        if (u + SC_WAVES < n_units) load_unit(u + SC_WAVES);   // next unit in flight
+    float wrun = -INFINITY;                          // running per-head max of this lane's column
+    // Two coefficient stages per wave, alternating between units, as separate
+    // LDS objects: the next unit's sc DMA never shares an object with the
+    // current unit's token-stage reads.
+    auto score_unit = [&](int u, const uint8_t* sc, uint8_t* sc_next) {
+        __builtin_amdgcn_s_waitcnt(0x0070);          // this unit's rows have landed in the stages
+        wave_lds_sync();
+        const bool more = u + SC_WAVES < n_units;
+        UnitOff nf;
+        if (more) nf = unit_off(u + SC_WAVES);
         const int p0 = c0 + u * SC_TILE;
         const int nvalid = min(SC_TILE, c1 - p0);
 
@@ -326,20 +353,23 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
         float2 vsf[4][2];
 #pragma unroll
         for (int pp = 0; pp < 4; ++pp) {
-            const uint8_t* vp = stg + ST_V + pp * ST_VPAIR + (i_pg * 8 + i_c) * ST_VROWB + kg * (D / 8);
+            const int R = 16 * pp + i_pg * 8 + i_c;            // (page 2pp + i_pg, column i_c)
+            const uint8_t* rp = sv + R * (D / 2);
             if constexpr (D == 64) {
-                const uint2 x = *reinterpret_cast<const uint2*>(vp);
+                const uint2 x = *reinterpret_cast<const uint2*>(rp + 16 * ((kg >> 1) ^ GM::vswz(R)) + 8 * (kg & 1));
                 vv[pp][0] = x.x; vv[pp][1] = x.y;
             } else {
 #pragma unroll
                 for (int k = 0; k < D / 128; ++k) {
-                    const uint4 x = *reinterpret_cast<const uint4*>(vp + 16 * k);
+                    const uint4 x = *reinterpret_cast<const uint4*>(rp + 16 * ((kg * (D / 128) + k) ^ GM::vswz(R)));
                     vv[pp][4 * k] = x.x; vv[pp][4 * k + 1] = x.y; vv[pp][4 * k + 2] = x.z; vv[pp][4 * k + 3] = x.w;
                 }
             }
 #pragma unroll
-            for (int pg = 0; pg < 2; ++pg)          // column scales (2kg, 2kg+1) of page 2pp+pg
-                vsf[pp][pg] = *reinterpret_cast<const float2*>(stg + ST_VS + (2 * pp + pg) * 32 + kg * 8);
+            for (int pg = 0; pg < 2; ++pg) {        // column scales (2kg, 2kg+1) of page 2pp+pg
+                const uint32_t w = *reinterpret_cast<const uint32_t*>(sc + SC_VS + (2 * pp + pg) * 16 + kg * 4);
+                vsf[pp][pg] = make_float2(bf16lo(w), bf16hi(w));
+            }
         }
         v4i mu[NWIN];
         float musf = 0.f;
@@ -349,11 +379,14 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
             const int pg = lane & 15;
 #pragma unroll
             for (int w = 0; w < NWIN; ++w)
-                mu[w] = *reinterpret_cast<const v4i*>(stg + ST_MU + pg * ST_MUROWB + kg * (D / 4) + 16 * w);
-            musf = bf16lo(*reinterpret_cast<const uint32_t*>(stg + ST_MUS + pg * 4));
+                mu[w] = *reinterpret_cast<const v4i*>(sv + SV_MU + pg * D + 16 * ((kg * (D / 64) + w) ^ GM::mswz(pg)));
+            musf = bf16lo(fmus);
         }
-        wave_lds_sync();                               // mu consumed: reuse as mud
-        float* mud_w = reinterpret_cast<float*>(stg + ST_MU);    // [page][16]
+        // sv is in registers: the next unit's packed V and centroid rows
+        // stream in under this unit's projection and token stages
+        __builtin_amdgcn_s_waitcnt(0xC07F);           // lgkmcnt(0): the sv reads have returned
+        wave_lds_sync();
+        if (more) { issue_sv(nf); issue_sc(nf, sc_next); }
         float qt[4][4];
 #pragma unroll
         for (int pp = 0; pp < 4; ++pp) {
@@ -397,15 +430,15 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
 #pragma unroll
             for (int ps = 0; ps < PPM; ++ps) {
                 const int page = gi * PPM + ps;
-                const uint32_t cw = *reinterpret_cast<const uint16_t*>(stg + ST_C8 + page * (PG * SC_RNK) +
+                const uint32_t cw = *reinterpret_cast<const uint16_t*>(sc + SC_C8 + page * (PG * SC_RNK) +
                                                                        (16 * tb + r16) * 8 + 2 * kg);
                 const float a0 = (float)(int8_t)cw, a1 = (float)(int8_t)(cw >> 8);
                 // qt is already zero where this lane's column is not page slot ps
                 acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, qt[page >> 1][page & 1], acc, 0, 0, 0);
                 acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, qt[page >> 1][2 + (page & 1)], acc, 0, 0, 0);
             }
-            const float4 csf = *reinterpret_cast<const float4*>(stg + ST_CS + ((gi * PPM + psub_l) * PG + 16 * tb) * 4 + kg * 16);
-            return v4f{acc[0] * csf.x, acc[1] * csf.y, acc[2] * csf.z, acc[3] * csf.w};
+            const uint2 cw4 = *reinterpret_cast<const uint2*>(sc + SC_CS + ((gi * PPM + psub_l) * PG + 16 * tb + 4 * kg) * 2);
+            return v4f{acc[0] * bf16lo(cw4.x), acc[1] * bf16hi(cw4.x), acc[2] * bf16lo(cw4.y), acc[3] * bf16hi(cw4.y)};
         };
         // 16-token LSE taken relative to the centroid term: tok - mud =
         // cs * acc.  The exp2 sum is exact whenever it lies in [2^-60, 2^60]
@@ -494,14 +527,19 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
                 score_h[(((long)r * n_kv + h) * G + g_l) * (long)MP + p0 + page] = Sv[st];
             }
         }
-        // this unit's per-head maxima -> LDS (ordered-uint atomic max), one
-        // atomic per head column per row
-#pragma unroll
-        for (int o = GW; o < 16; o <<= 1)    // max over the lanes of one head column
-            tmax = fmaxf(tmax, o == 4 ? row_ror<4>(tmax) : o == 8 ? row_ror<8>(tmax) : row_ror<2>(tmax));
-        if (row_owner && (lane & 15) < GW && (lane & 15) < G) atomicMax(&wmax[lane & 15], f2u(tmax));
-        wave_lds_sync();                               // staging reused by the next unit
+        wrun = fmaxf(wrun, tmax);
+        wave_lds_sync();                               // stages reused by the unit after next
+    };
+    for (int u = wave; u < n_units; u += 2 * SC_WAVES) {
+        score_unit(u, sc0_l[wave], sc1_l[wave]);
+        if (u + SC_WAVES < n_units) score_unit(u + SC_WAVES, sc1_l[wave], sc0_l[wave]);
     }
+    // per-head maxima of the workgroup -> LDS (ordered-uint atomic max), one
+    // atomic per head column per row
+#pragma unroll
+    for (int o = GW; o < 16; o <<= 1)        // max over the lanes of one head column
+        wrun = fmaxf(wrun, o == 4 ? row_ror<4>(wrun) : o == 8 ? row_ror<8>(wrun) : row_ror<2>(wrun));
+    if ((NGRP >= 4 || kg < 2) && (lane & 15) < GW && (lane & 15) < G) atomicMax(&wmax[lane & 15], f2u(wrun));
     __syncthreads();
     if (tid < 16) pm_out[tid] = u2f(wmax[tid]);
 }
