@@ -23,6 +23,17 @@
  * (locks_pack_rki4: 128 / 16); MLA: kv_lora_rank 512 + 64 RoPE dims, <= 16
  * query heads.
  *
+ * Summary slabs: the six rki4 slabs of one layer are passed as six base
+ * pointers plus `slab_row_bytes`, the byte stride between consecutive
+ * (block, kv head) rows of each (v4, vs, c8, cs, mu8, mus, in that order).
+ * NULL means contiguous slabs of the shapes below (strides 8 d/2, 16, 8 P,
+ * 2 P, d and 2 bytes); a state that keeps all six fields of a row together
+ * (this package's Rki4State, and the reference's AoS record
+ * selection/rki4_state.py:93-110: one record of 5d + 10P + 18 bytes rounded
+ * up to 64, fields in the order v4, mu8, c8, cs, vs, mus) passes that record
+ * size six times; the scorer then reads each page's record as one stream.  Bases and strides of v4, vs, c8, cs, mu8 are 16-byte aligned, mus
+ * 2-byte aligned.
+ *
  * Reference interfaces each entry replaces (paths under src/locks/):
  */
 #ifndef LOCKS_HIP_H_
@@ -30,7 +41,7 @@
 
 #include <stdint.h>
 
-#define LOCKS_ABI_VERSION 6
+#define LOCKS_ABI_VERSION 7
 
 #ifdef __cplusplus
 extern "C" {
@@ -77,6 +88,7 @@ int32_t locks_score_num_chunks(int32_t max_pages, int32_t chunk);
  *   cs         (num_blocks, n_kv, P)     bf16 per-token scales
  *   mu8        (num_blocks, n_kv, d)     i8   page centroid
  *   mus        (num_blocks, n_kv)        bf16 centroid scale
+ *   slab_row_bytes  NULL or the six row strides (see above)
  *   block_table (n_req, bt_cols) i32, row stride bt_stride; page p -> block
  *   n_sel_hi   (n_req,) i32: pages [0, n_sel_hi) are scored
  *   score_h    (n_req, n_kv, G, max_pages) f32 -- written for p < n_sel_hi only
@@ -88,6 +100,7 @@ int32_t locks_score_num_chunks(int32_t max_pages, int32_t chunk);
 int32_t locks_score_rki4(const uint16_t* q, int64_t q_stride_req, int64_t q_stride_head,
                          const uint8_t* v4, const uint16_t* vs, const int8_t* c8,
                          const uint16_t* cs, const int8_t* mu8, const uint16_t* mus,
+                         const int64_t* slab_row_bytes,
                          int32_t num_blocks, const int32_t* block_table, int64_t bt_stride,
                          int32_t bt_cols, const int32_t* n_sel_hi, float* score_h,
                          int32_t max_pages, float* page_max, int32_t chunk, int32_t n_req,
@@ -278,8 +291,9 @@ int32_t locks_decode_dense(const uint16_t* q, int64_t q_stride_req, int64_t q_st
  *   k_cache   K half of one layer, element strides of (block, token, kv head)
  *   blocks    (n_blocks,) i32 physical block ids; ids outside [0, num_blocks)
  *             are skipped (rki4_build.py:133-144)
- *   outputs   the layer's six slabs (as in locks_score_rki4) and the tag
- *             (num_blocks, n_kv, 8) bf16 = K[page-1, kh, 0:8]
+ *   outputs   the layer's six slabs with their row strides slab_row_bytes
+ *             (as in locks_score_rki4) and the tag (num_blocks, n_kv, 8)
+ *             bf16 = K[page-1, kh, 0:8]
  * Eigenvectors agree with any other eigensolver up to sign / rotation inside
  * degenerate eigenspaces, so bytes are comparable only through the score.
  */
@@ -287,19 +301,21 @@ int32_t locks_build_rki4(const uint16_t* k_cache, int64_t k_stride_block, int64_
                          int64_t k_stride_head, int32_t num_blocks, const int32_t* blocks,
                          int32_t n_blocks, int32_t n_kv, int32_t head_dim, int32_t page,
                          uint8_t* v4, uint16_t* vs, int8_t* c8, uint16_t* cs, int8_t* mu8,
-                         uint16_t* mus, uint16_t* tag, void* stream);
+                         uint16_t* mus, const int64_t* slab_row_bytes, uint16_t* tag,
+                         void* stream);
 
 /*
  * Quantize + pack from a given eigen decomposition (the _write_post half,
  * selection/rki4_build.py:178-225 with the int4 pack :161-175), bit-exact to
  * the reference op order.  Inputs per page i < n: mu (n, 128) f32, dc
  * (n, 16, 128) f32, S2 (n, 16) f32 ascending, U (n, 16, 16) f32 (columns =
- * eigenvectors); rows (n,) i32 = slab row (block * n_kv + kv head).
+ * eigenvectors); rows (n,) i32 = slab row (block * n_kv + kv head);
+ * slab_row_bytes as in locks_score_rki4.
  */
 int32_t locks_pack_rki4(const float* mu, const float* dc, const float* S2, const float* U,
                         const int32_t* rows, int32_t n, int32_t head_dim, int32_t page,
                         uint8_t* v4, uint16_t* vs, int8_t* c8, uint16_t* cs, int8_t* mu8,
-                        uint16_t* mus, void* stream);
+                        uint16_t* mus, const int64_t* slab_row_bytes, void* stream);
 
 /*
  * Summary refresh lifecycle, step 1: the physical blocks to (re)build, as a
@@ -342,8 +358,8 @@ int32_t locks_refresh_blocks(int32_t mode, const int32_t* block_table, int64_t b
  * launch (the reference loops layers / layer groups through torch ops,
  * selection/build.py:430-453 _build_blocks).  Layer l reads K from
  * k_layers[l] and writes the slabs at layer offset l * slab_blocks * n_kv
- * rows (slabs laid out (n_layers, slab_blocks, n_kv, ...), pointers to layer
- * 0).  count (nullable) is a device count of valid `blocks` entries, at most
+ * rows (slabs laid out (n_layers, slab_blocks, n_kv, ...) with row strides
+ * slab_row_bytes, pointers to layer 0).  count (nullable) is a device count of valid `blocks` entries, at most
  * n_blocks, as written by locks_refresh_blocks.
  */
 int32_t locks_build_rki4_layers(const uint64_t* k_layers, int32_t n_layers,
@@ -352,7 +368,8 @@ int32_t locks_build_rki4_layers(const uint64_t* k_layers, int32_t n_layers,
                                 const int32_t* count, int32_t n_blocks, int32_t n_kv,
                                 int32_t head_dim, int32_t page, int64_t slab_blocks, uint8_t* v4,
                                 uint16_t* vs, int8_t* c8, uint16_t* cs, int8_t* mu8,
-                                uint16_t* mus, uint16_t* tag, void* stream);
+                                uint16_t* mus, const int64_t* slab_row_bytes, uint16_t* tag,
+                                void* stream);
 
 
 /*

@@ -61,9 +61,7 @@ template <int D, int PG> constexpr int bd_waves() {
 // S8 (LDS), writing the six slab rows.  Lane l owns the packed bytes
 // j = l + 64 k (d = 2j, 2j + 1).
 template <int D, int PG>
-__device__ __forceinline__ void pack_page(WaveLds<D, PG>& L, long row, uint8_t* __restrict__ v4, uint16_t* __restrict__ vs,
-                          int8_t* __restrict__ c8, uint16_t* __restrict__ cs,
-                          int8_t* __restrict__ mu8, uint16_t* __restrict__ mus) {
+__device__ __forceinline__ void pack_page(WaveLds<D, PG>& L, long row, const SlabRows& S) {
     constexpr int NK = (D / 2 + 63) / 64;      // packed bytes per lane (d = 64: lanes < 32)
     const int lane = threadIdx.x & 63;
     auto own = [&](int k) { return lane + 64 * k < D / 2; };
@@ -99,7 +97,7 @@ __device__ __forceinline__ void pack_page(WaveLds<D, PG>& L, long row, uint8_t* 
         am = wave_max(am);
         vsc[r] = fmaxf(__fdiv_rn(am, 7.f), 1e-8f);
     }
-    uint8_t* vrow = v4 + row * (BD_RNK * D / 2);
+    uint8_t* vrow = S.v4 + row * S.sv4;
 #pragma unroll
     for (int r = 0; r < BD_RNK; ++r)
 #pragma unroll
@@ -108,7 +106,7 @@ __device__ __forceinline__ void pack_page(WaveLds<D, PG>& L, long row, uint8_t* 
             const int hi = (int)fminf(fmaxf(rintf(__fdiv_rn(V[k][1][r], vsc[r])), -8.f), 7.f);
             if (own(k)) vrow[r * (D / 2) + lane + 64 * k] = (uint8_t)((lo & 15) | ((hi & 15) << 4));
         }
-    if (lane < BD_RNK) vs[row * BD_RNK + lane] = f32_to_bf16(vsc[lane]);
+    if (lane < BD_RNK) reinterpret_cast<uint16_t*>(S.vs + row * S.svs)[lane] = f32_to_bf16(vsc[lane]);
     // coefficients: lane t < PG owns token t
     if (lane < PG) {
         const int t = lane;
@@ -120,11 +118,11 @@ __device__ __forceinline__ void pack_page(WaveLds<D, PG>& L, long row, uint8_t* 
             am = fmaxf(am, fabsf(C[r]));
         }
         const float csc = fmaxf(__fdiv_rn(am, 127.f), 1e-8f);
-        int8_t* crow = c8 + (row * PG + t) * BD_RNK;
+        int8_t* crow = reinterpret_cast<int8_t*>(S.c8 + row * S.sc8) + t * BD_RNK;
 #pragma unroll
         for (int r = 0; r < BD_RNK; ++r)
             crow[r] = (int8_t)fminf(fmaxf(rintf(__fdiv_rn(C[r], csc)), -127.f), 127.f);
-        cs[row * PG + t] = f32_to_bf16(csc);
+        reinterpret_cast<uint16_t*>(S.cs + row * S.scs)[t] = f32_to_bf16(csc);
     }
     // centroid
     float am = 0.f;
@@ -138,9 +136,9 @@ __device__ __forceinline__ void pack_page(WaveLds<D, PG>& L, long row, uint8_t* 
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
             const int d = 2 * (lane + 64 * k) + e;
-            if (own(k)) mu8[row * D + d] = (int8_t)fminf(fmaxf(rintf(__fdiv_rn(L.mu[d], msc)), -127.f), 127.f);
+            if (own(k)) reinterpret_cast<int8_t*>(S.mu + row * S.smu)[d] = (int8_t)fminf(fmaxf(rintf(__fdiv_rn(L.mu[d], msc)), -127.f), 127.f);
         }
-    if (lane == 0) mus[row] = f32_to_bf16(msc);
+    if (lane == 0) *reinterpret_cast<uint16_t*>(S.mus + row * S.smus) = f32_to_bf16(msc);
 }
 
 // Parallel cyclic Jacobi on L.A (N x N symmetric, N = page = 16, 32 or 64);
@@ -292,10 +290,7 @@ __global__ __launch_bounds__((bd_waves<D, PG>() * kWave)) void rki4_build_kernel
     const uint16_t* __restrict__ kc, const uint64_t* __restrict__ k_layers,
     long k_sb, long k_st, long k_sh, int NB,
     const int* __restrict__ blocks, const int* __restrict__ n_dev, int n_blocks, int n_kv,
-    int n_layers, long layer_rows,
-    uint8_t* __restrict__ v4, uint16_t* __restrict__ vs, int8_t* __restrict__ c8,
-    uint16_t* __restrict__ cs, int8_t* __restrict__ mu8, uint16_t* __restrict__ mus,
-    uint16_t* __restrict__ tag)
+    int n_layers, long layer_rows, SlabRows S, uint16_t* __restrict__ tag)
 {
     constexpr int NW = bd_waves<D, PG>();
     __shared__ WaveLds<D, PG> lds[NW];
@@ -358,16 +353,14 @@ __global__ __launch_bounds__((bd_waves<D, PG>() * kWave)) void rki4_build_kernel
         wave_lds_sync();
         jacobi<PG>(L);
         select_top8<PG>(L);
-        pack_page<D, PG>(L, row, v4, vs, c8, cs, mu8, mus);
+        pack_page<D, PG>(L, row, S);
     }
 }
 
 // locks_pack_rki4: quantize + pack given the caller's eigen decomposition.
 __global__ __launch_bounds__(4 * kWave) void rki4_pack_kernel(
     const float* __restrict__ mu, const float* __restrict__ dc, const float* __restrict__ S2,
-    const float* __restrict__ U, const int* __restrict__ rows, int n,
-    uint8_t* __restrict__ v4, uint16_t* __restrict__ vs, int8_t* __restrict__ c8,
-    uint16_t* __restrict__ cs, int8_t* __restrict__ mu8, uint16_t* __restrict__ mus)
+    const float* __restrict__ U, const int* __restrict__ rows, int n, SlabRows S)
 {
     constexpr int BD_D = 128, BD_PG = 16;
     __shared__ WaveLds<BD_D, BD_PG> lds[4];
@@ -384,7 +377,7 @@ __global__ __launch_bounds__(4 * kWave) void rki4_pack_kernel(
         L.S8[lane] = __fsqrt_rn(fmaxf(S2[item * BD_PG + c], 1e-10f));
     }
     wave_lds_sync();
-    pack_page<BD_D, BD_PG>(L, rows[item], v4, vs, c8, cs, mu8, mus);
+    pack_page<BD_D, BD_PG>(L, rows[item], S);
 }
 
 // ---- refresh lifecycle: which blocks to (re)build --------------------------
@@ -475,14 +468,13 @@ static bool bd_geometry(int head_dim, int page) {
 template <int D, int PG>
 static int bd_launch(const uint16_t* kc, const uint64_t* k_layers, long k_sb, long k_st, long k_sh,
                      int NB, const int* blocks, const int* count, int n_blocks, int n_kv,
-                     int n_layers, long layer_rows, uint8_t* v4, uint16_t* vs, int8_t* c8,
-                     uint16_t* cs, int8_t* mu8, uint16_t* mus, uint16_t* tag, hipStream_t st) {
+                     int n_layers, long layer_rows, const SlabRows& S, uint16_t* tag, hipStream_t st) {
     constexpr int nw = bd_waves<D, PG>();
     const long items = (long)n_blocks * n_kv * n_layers;
     const long grid = std::min((items + nw - 1) / nw, BD_MAX_GRID);
     hipLaunchKernelGGL((rki4_build_kernel<D, PG>), dim3((unsigned)grid), dim3(nw * kWave), 0, st,
                        kc, k_layers, k_sb, k_st, k_sh, NB, blocks, count, n_blocks, n_kv,
-                       n_layers, layer_rows, v4, vs, c8, cs, mu8, mus, tag);
+                       n_layers, layer_rows, S, tag);
     return check_launch("rki4_build_kernel");
 }
 #define BD_DISPATCH(HD, PGV, ...)                                              \
@@ -501,7 +493,7 @@ extern "C" int32_t locks_build_rki4(
     const uint16_t* k_cache, int64_t k_stride_block, int64_t k_stride_tok, int64_t k_stride_head,
     int32_t num_blocks, const int32_t* blocks, int32_t n_blocks, int32_t n_kv, int32_t head_dim,
     int32_t page, uint8_t* v4, uint16_t* vs, int8_t* c8, uint16_t* cs, int8_t* mu8,
-    uint16_t* mus, uint16_t* tag, void* stream)
+    uint16_t* mus, const int64_t* slab_row_bytes, uint16_t* tag, void* stream)
 {
     LOCKS_REQUIRE(bd_geometry(head_dim, page),
                   "locks_build_rki4: geometry d=%d page=%d unsupported (d 64/128/256 with page 16/32/64, "
@@ -511,26 +503,32 @@ extern "C" int32_t locks_build_rki4(
                   "locks_build_rki4: K strides must be multiples of 8 elements");
     LOCKS_REQUIRE(k_cache && blocks && v4 && vs && c8 && cs && mu8 && mus && tag,
                   "locks_build_rki4: null pointer argument");
+    const SlabRows S = slab_rows(v4, vs, c8, cs, mu8, mus, slab_row_bytes, head_dim, page);
+    LOCKS_REQUIRE(slab_rows_ok(S, head_dim, page),
+                  "locks_build_rki4: slab row strides below the field sizes or misaligned");
     if (n_blocks == 0) return 0;
     return BD_DISPATCH(head_dim, page, k_cache, nullptr, (long)k_stride_block, (long)k_stride_tok,
                        (long)k_stride_head, num_blocks, blocks, nullptr, n_blocks, n_kv, 1, 0L,
-                       v4, vs, c8, cs, mu8, mus, tag, (hipStream_t)stream);
+                       S, tag, (hipStream_t)stream);
 }
 
 extern "C" int32_t locks_pack_rki4(const float* mu, const float* dc, const float* S2,
                                    const float* U, const int32_t* rows, int32_t n,
                                    int32_t head_dim, int32_t page, uint8_t* v4, uint16_t* vs,
                                    int8_t* c8, uint16_t* cs, int8_t* mu8, uint16_t* mus,
-                                   void* stream)
+                                   const int64_t* slab_row_bytes, void* stream)
 {
     LOCKS_REQUIRE(head_dim == 128 && page == 16,
                   "locks_pack_rki4: geometry d=%d page=%d unsupported (this entry: 128/16)", head_dim, page);
     LOCKS_REQUIRE(n >= 0, "locks_pack_rki4: n=%d < 0", n);
     LOCKS_REQUIRE(mu && dc && S2 && U && rows && v4 && vs && c8 && cs && mu8 && mus,
                   "locks_pack_rki4: null pointer argument");
+    const SlabRows S = slab_rows(v4, vs, c8, cs, mu8, mus, slab_row_bytes, head_dim, page);
+    LOCKS_REQUIRE(slab_rows_ok(S, head_dim, page),
+                  "locks_pack_rki4: slab row strides below the field sizes or misaligned");
     if (n == 0) return 0;
     hipLaunchKernelGGL(rki4_pack_kernel, dim3((n + 3) / 4), dim3(4 * kWave),
-                       0, (hipStream_t)stream, mu, dc, S2, U, rows, n, v4, vs, c8, cs, mu8, mus);
+                       0, (hipStream_t)stream, mu, dc, S2, U, rows, n, S);
     return check_launch("rki4_pack_kernel");
 }
 
@@ -581,7 +579,7 @@ extern "C" int32_t locks_build_rki4_layers(
     int64_t k_stride_head, int32_t num_blocks, const int32_t* blocks, const int32_t* count,
     int32_t n_blocks, int32_t n_kv, int32_t head_dim, int32_t page, int64_t slab_blocks,
     uint8_t* v4, uint16_t* vs, int8_t* c8, uint16_t* cs, int8_t* mu8, uint16_t* mus,
-    uint16_t* tag, void* stream)
+    const int64_t* slab_row_bytes, uint16_t* tag, void* stream)
 {
     LOCKS_REQUIRE(bd_geometry(head_dim, page),
                   "locks_build_rki4_layers: geometry d=%d page=%d unsupported (d 64/128/256 with page "
@@ -593,9 +591,12 @@ extern "C" int32_t locks_build_rki4_layers(
                   "locks_build_rki4_layers: K strides must be multiples of 8 elements");
     LOCKS_REQUIRE(k_layers && blocks && v4 && vs && c8 && cs && mu8 && mus && tag,
                   "locks_build_rki4_layers: null pointer argument");
+    const SlabRows S = slab_rows(v4, vs, c8, cs, mu8, mus, slab_row_bytes, head_dim, page);
+    LOCKS_REQUIRE(slab_rows_ok(S, head_dim, page),
+                  "locks_build_rki4_layers: slab row strides below the field sizes or misaligned");
     if (n_blocks == 0) return 0;
     const long layer_rows = (long)slab_blocks * n_kv;
     return BD_DISPATCH(head_dim, page, nullptr, k_layers, (long)k_stride_block, (long)k_stride_tok,
                        (long)k_stride_head, num_blocks, blocks, count, n_blocks, n_kv, n_layers,
-                       layer_rows, v4, vs, c8, cs, mu8, mus, tag, (hipStream_t)stream);
+                       layer_rows, S, tag, (hipStream_t)stream);
 }

@@ -136,6 +136,48 @@ __device__ __forceinline__ void wave_lds_sync() {
 
 __host__ __device__ __forceinline__ int cdiv(int a, int b) { return (a + b - 1) / b; }
 
+// The six rki4 summary slabs of one layer as (base, row stride in bytes):
+// field f of the (block, kv head) row i lives at base_f + i * stride_f.
+// Contiguous slabs have the natural strides (8 d/2, 16, 8 page, 2 page, d,
+// 2 bytes); a state that packs all six fields of a row together gives every
+// field the same stride (the packed row size).
+struct SlabRows {
+    uint8_t* v4; uint8_t* vs; uint8_t* c8; uint8_t* cs; uint8_t* mu; uint8_t* mus;
+    long sv4, svs, sc8, scs, smu, smus;
+};
+
+// Host side: the natural strides of geometry (d, page), or the caller's
+// six (row_bytes != nullptr).
+inline SlabRows slab_rows(const void* v4, const void* vs, const void* c8, const void* cs,
+                          const void* mu, const void* mus, const int64_t* row_bytes, int d, int page) {
+    SlabRows s;
+    s.v4 = (uint8_t*)v4; s.vs = (uint8_t*)vs; s.c8 = (uint8_t*)c8;
+    s.cs = (uint8_t*)cs; s.mu = (uint8_t*)mu; s.mus = (uint8_t*)mus;
+    if (row_bytes) {
+        s.sv4 = row_bytes[0]; s.svs = row_bytes[1]; s.sc8 = row_bytes[2];
+        s.scs = row_bytes[3]; s.smu = row_bytes[4]; s.smus = row_bytes[5];
+    } else {
+        s.sv4 = 4L * d; s.svs = 16; s.sc8 = 8L * page; s.scs = 2L * page; s.smu = d; s.smus = 2;
+    }
+    return s;
+}
+
+// Host side: strides at least the field sizes, 16-byte aligned bases and
+// strides for the fields read with 16-byte loads (all but mus), even mus.
+inline bool slab_rows_ok(const SlabRows& s, int d, int page) {
+    auto a16 = [](const void* p, long st) { return ((uintptr_t)p % 16 == 0) && (st % 16 == 0); };
+    return s.sv4 >= 4L * d && s.svs >= 16 && s.sc8 >= 8L * page && s.scs >= 2L * page && s.smu >= d &&
+           s.smus >= 2 && a16(s.v4, s.sv4) && a16(s.vs, s.svs) && a16(s.c8, s.sc8) &&
+           a16(s.cs, s.scs) && a16(s.mu, s.smu) && ((uintptr_t)s.mus % 2 == 0) && (s.smus % 2 == 0);
+}
+
+// Largest byte offset a kernel forms into any slab for `rows` rows.
+inline long slab_rows_extent(const SlabRows& s, long rows) {
+    long m = s.sv4;
+    for (long v : {s.svs, s.sc8, s.scs, s.smu, s.smus}) m = v > m ? v : m;
+    return rows * m;
+}
+
 }  // namespace locks
 
 // ---- host-side error plumbing for the C ABI -------------------------------

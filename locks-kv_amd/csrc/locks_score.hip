@@ -39,72 +39,67 @@ constexpr int SC_BLOCK = SC_WAVES * kWave;
 constexpr int SC_MAX_CHUNK = 1024;          // pages per workgroup, upper bound
 constexpr int SC_CPOL_NT = 2;                // buffer-load cache policy: non-temporal
 
-// Per-geometry layout (head_dim D in {64, 128, 256}, page PG in {16, 32, 64})
-// of the slab rows and of one wave's LDS stage for an (8-page tile, kv head)
-// unit.  The stage is written by LDS DMA (global_load_lds_dwordx4: lane L of
-// an instruction fills bytes 16 L .. 16 L + 15 of a 1-KB block), so rows
-// cannot be padded; instead the 16-byte chunks of each packed-V and centroid
-// row are XOR-swizzled (chunk k of row R stored at k ^ swz(R)), which spreads
-// the MFMA-order reads of 16 (resp. 8) rows at the same column over all 64
-// banks.  Three separate LDS objects per wave:
-//   sv: packed V (8 pages x 8 columns x D/2 B) + centroids (8 x D B)
-//   sc: coefficients (8 pages x PG x 8 B) + token scales (bf16) + column scales (bf16)
-//   sm: per-page centroid terms mud (8 pages x 16 heads f32)
-// The next unit's sv DMA is issued as soon as sv has been read into
-// registers; the token stage then reads only sc and sm, which the compiler's
-// memory-counter tracking can tell apart from the DMA's destination.
+// Per-geometry layout (head_dim D in {64, 128, 256}, page PG in {16, 32, 64}).
+// A summary row (one page, one kv head) holds, in this order (the
+// reference's AoS record, selection/rki4_state.py:93-110, 198-219):
+//   v4  8 columns x D/2 B   int4 basis (column-major, low nibble = even d)
+//   mu  D B                 centroid
+//   c8  PG tokens x 8 B     coefficients
+//   cs  PG x bf16           token scales
+//   vs  8 x bf16            column scales
+//   mus bf16                centroid scale (+ pad)
+// i.e. 5D + 10PG + 18 bytes rounded up to 64 when the state packs the fields
+// together (RS; 832 B at D = 128, PG = 16).  One wave's unit is 8 such rows;
+// all fields but mus (RB = 5D + 10PG + 16 bytes per row) are DMA'd as ONE
+// byte stream (global_load_lds_dwordx4: lane L of
+// instruction i fetches stream chunk 64 i + L into LDS byte 16 (64 i + L))
+// into a row-major LDS stage, so each instruction reads ~1 KB of consecutive
+// row bytes -- measured 16-22 % faster than field-wise DMA of the same rows.
+// The centroid scale goes to a VGPR.  With separate slabs (the reference's
+// layout) each lane picks its chunk's slab instead; the stage is the same.
 template <int D, int PG>
 struct ScGeom {
     static_assert(D == 64 || D == 128 || D == 256, "head_dim 64, 128 or 256");
     static_assert(PG == 16 || PG == 32 || PG == 64, "page 16, 32 or 64");
-    static constexpr int VROW = SC_RNK * D / 2;        // packed V bytes per slab row
-    static constexpr int NVL = D / 32;                 // 1-KB V loads per unit
-    static constexpr int NCL = PG / 16;                // 1-KB coefficient loads per unit
-    static constexpr int NML = D >= 128 ? D / 128 : 1; // centroid loads per unit (D = 64: half)
     static constexpr int NWIN = D / 64;                // 16-d windows per lane (projection MFMAs)
     static constexpr int NTB = PG / 16;                // 16-token blocks per page
-    static constexpr int VCH = D / 32;                 // 16-B chunks per packed-V row (page, column)
-    static constexpr int MCH = D / 16;                 // 16-B chunks per centroid row
-    static constexpr int SV_MU = 8 * VROW;             // centroid rows after the packed V
-    static constexpr int SV_BYTES = SV_MU + 8 * D;
-    static constexpr int SC_C8 = 0;                    // 8 pages x PG x 8 int8
-    static constexpr int SC_CS = 64 * PG;              // 8 pages x PG bf16
-    static constexpr int SC_VS = SC_CS + 16 * PG;      // 8 pages x 8 bf16
-    static constexpr int SC_BYTES = SC_VS + 128;
+    static constexpr int O_MU = 4 * D;                 // field offsets inside a row
+    static constexpr int O_C8 = O_MU + D;
+    static constexpr int O_CS = O_C8 + 8 * PG;
+    static constexpr int O_VS = O_CS + 2 * PG;
+    static constexpr int RB = O_VS + 16;               // stage row bytes (all fields but mus)
+    static constexpr int CPR = RB / 16;                // 16-B chunks per stage row
+    static constexpr int NCK = SC_TILE * CPR;          // chunks per unit
+    static constexpr int NDI = (NCK + 63) / 64;        // DMA instructions per unit
+    static constexpr int ST_BYTES = SC_TILE * RB;
     static constexpr int QROW = D + 16;                // padded int8 q row
-    // rows R .. R + 16 / VCH - 1 share a 256-B bank period; distinct swizzles
-    // across the periods make 16 consecutive rows hit distinct banks
-    static constexpr int vswz(int R) { return (R / (16 / VCH)) & (VCH - 1); }
-    static constexpr int mswz(int R) { return (R / (16 / MCH)) & (MCH - 1); }
 };
 
 typedef __attribute__((address_space(3))) void* sc_lds_ptr;
 
-// One lane's byte offsets into the six slabs for one unit.
-template <int NVL, int NML, int NCL>
-struct ScUnitOff { uint32_t v[NVL], m[NML], c[NCL], cs, vs, mus; };
+// One lane's sources for one unit: per DMA instruction a byte offset from
+// the v4 base (packed rows) or a full address (separate slabs), and the
+// centroid scale's offset.
+template <int NDI, bool PK>
+struct ScUnitSrc { uint32_t off[PK ? NDI : 1]; const uint8_t* addr[PK ? 1 : NDI]; uint32_t mus; };
 
 __device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d) {
     return (uint32_t)(uint8_t)a | ((uint32_t)(uint8_t)b << 8) |
            ((uint32_t)(uint8_t)c << 16) | ((uint32_t)(uint8_t)d << 24);
 }
 
-template <int GW, int D = 128, int PG = 16>
+template <int GW, int D = 128, int PG = 16, bool PK = true>
 __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
-    const uint16_t* __restrict__ q, long q_sr, long q_sh,
-    const uint8_t* __restrict__ v4, const uint16_t* __restrict__ vs,
-    const int8_t* __restrict__ c8, const uint16_t* __restrict__ cs,
-    const int8_t* __restrict__ mu8, const uint16_t* __restrict__ mus,
-    int NB, const int* __restrict__ bt, long bt_sr, int bt_cols,
+    const uint16_t* __restrict__ q, long q_sr, long q_sh, SlabRows S, int NB, const int* __restrict__ bt, long bt_sr, int bt_cols,
     const int* __restrict__ nsh, float* __restrict__ score_h, int MP,
     float* __restrict__ pmax, int n_kv, int G, float sm_scale, int chunk)
 {
     using GM = ScGeom<D, PG>;
     constexpr int PPM = 16 / GW;            // pages per token-stage MFMA
     constexpr int NGRP = SC_TILE / PPM;     // token-stage groups per tile
-    constexpr int NVL = GM::NVL, NCL = GM::NCL, NML = GM::NML, NWIN = GM::NWIN, NTB = GM::NTB;
-    constexpr int SC_VROW = GM::VROW, VCH = GM::VCH, MCH = GM::MCH;
-    constexpr int SV_MU = GM::SV_MU, SC_C8 = GM::SC_C8, SC_CS = GM::SC_CS, SC_VS = GM::SC_VS, SC_QROW = GM::QROW;
+    constexpr int NWIN = GM::NWIN, NTB = GM::NTB, SC_QROW = GM::QROW;
+    constexpr int O_C8 = GM::O_C8, O_MU = GM::O_MU, O_CS = GM::O_CS, O_VS = GM::O_VS, RB = GM::RB;
+    constexpr int CPR = GM::CPR, NCK = GM::NCK, NDI = GM::NDI;
     constexpr int QDL = D <= 128 ? 8 : 16;  // q dims per lane in the quantize step
     constexpr int LPH = D / QDL;            // q lanes per head (8 or 16: one DPP row group)
     const int z = blockIdx.x, h = blockIdx.y, r = blockIdx.z;   // page chunk, kv head, request
@@ -121,9 +116,12 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
     }
 
     __shared__ __attribute__((aligned(16))) float qsp[16];
-    __shared__ __attribute__((aligned(16))) uint8_t sv_l[SC_WAVES][GM::SV_BYTES];
-    __shared__ __attribute__((aligned(16))) uint8_t sc0_l[SC_WAVES][GM::SC_BYTES];
-    __shared__ __attribute__((aligned(16))) uint8_t sc1_l[SC_WAVES][GM::SC_BYTES];
+    // two stages per wave, alternating between units, as separate LDS
+    // objects: the next unit's DMA never shares an object with the current
+    // unit's reads (the compiler's memory-counter tracking would otherwise
+    // wait for the DMA before every read)
+    __shared__ __attribute__((aligned(16))) uint8_t sa_l[SC_WAVES][GM::ST_BYTES];
+    __shared__ __attribute__((aligned(16))) uint8_t sb_l[SC_WAVES][GM::ST_BYTES];
     __shared__ __attribute__((aligned(16))) float sm_l[SC_WAVES][SC_TILE * 16];
     __shared__ uint32_t wmax[16];
     // dynamic LDS: int8 q rows of this kv head's G query heads (+16 zero
@@ -163,90 +161,69 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
     const int n_tiles = cdiv(c1 - c0, SC_TILE);
     const int n_units = n_tiles;             // (8-page tile) units of the chunk
 
-    // Each (8-page tile, kv head) unit's rows are DMA'd straight from the six
-    // slabs into this wave's LDS stage (no VGPR round trip).  Consecutive
-    // units are the kv heads of one tile, whose slab rows are adjacent.  The
-    // large rows (packed V, coefficients, centroid: 768 of 818 B per row) are
-    // read with the non-temporal policy -- every row is read once -- and the
-    // small scale rows (16, 32 and 2 B, whose cache lines are shared with the
-    // next kv head's or block's rows, read by another workgroup) with the
-    // default policy, so those lines stay in the L2 for it.
-    const uint8_t* const v4b = v4;
-    const uint8_t* const c8b = reinterpret_cast<const uint8_t*>(c8);
-    const uint8_t* const mub = reinterpret_cast<const uint8_t*>(mu8);
-    const uint8_t* const csb = reinterpret_cast<const uint8_t*>(cs);
-    const uint8_t* const vsb = reinterpret_cast<const uint8_t*>(vs);
-    const auto rs_mus = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(mus), 0, -1, 0x00020000);
-    uint8_t* const sv = sv_l[wave];
+    // Each (8-page tile, kv head) unit's rows are DMA'd straight from the
+    // slabs into this wave's LDS stage (no VGPR round trip), non-temporally:
+    // every row is read once.  Consecutive units are the kv heads of one
+    // tile, whose rows are adjacent.
+    const auto rs_mus = __builtin_amdgcn_make_buffer_rsrc(S.mus, 0, -1, 0x00020000);
+    // row strides (bytes) of the slabs: offsets below stay under 2^32
+    const uint32_t sv4 = (uint32_t)S.sv4, svs = (uint32_t)S.svs, sc8 = (uint32_t)S.sc8,
+                   scs = (uint32_t)S.scs, smu = (uint32_t)S.smu, smus = (uint32_t)S.smus;
     float* const mud_w = sm_l[wave];                 // [page][16 heads]
     uint32_t fmus = 0;                               // centroid scale of page lane & 15 (lanes & 15 < 8)
-    // Every lane's slab offsets of one unit, read from the block ids in LDS
-    // while no DMA is outstanding (an LDS read issued behind a DMA waits for
-    // it) and pinned in registers before the first DMA of the unit.
-    using UnitOff = ScUnitOff<NVL, NML, NCL>;
-    auto unit_off = [&](int u) -> UnitOff {
+    // Every lane's sources of one unit, read from the slab rows in LDS while
+    // no DMA is outstanding (an LDS read issued behind a DMA waits for it)
+    // and pinned in registers before the first DMA of the unit.
+    using UnitSrc = ScUnitSrc<NDI, PK>;
+    auto unit_src = [&](int u) -> UnitSrc {
         const int p0 = u * SC_TILE;
         const int last = min(SC_TILE, c1 - c0 - p0) - 1;   // tail pages repeat the last one
         auto row = [&](int i) -> uint32_t { return (uint32_t)bt_l[p0 + min(i, last)]; };
-        UnitOff f;
+        UnitSrc f;
+        uint32_t w[NDI];                             // all block-id reads first, then the math
 #pragma unroll
-        for (int i = 0; i < NVL; ++i) {              // LDS chunk s <- row R, chunk (s % VCH) ^ swz(R)
-            const int s = 64 * i + lane, R = s / VCH, k = (s % VCH) ^ GM::vswz(R);
-            f.v[i] = row(R >> 3) * SC_VROW + (R & 7) * (D / 2) + 16 * k;
+        for (int i = 0; i < NDI; ++i) w[i] = row(min(64 * i + lane, NCK - 1) / CPR);
+#pragma unroll
+        for (int i = 0; i < NDI; ++i) {
+            const int sk = min(64 * i + lane, NCK - 1);     // stream chunk (lanes past the end: idle)
+            const int o = 16 * (sk % CPR);                  // byte in the row
+            if constexpr (PK) {
+                f.off[i] = w[i] * sv4 + o;
+            } else {
+                const uint8_t* a;
+                if (o < O_MU) a = S.v4 + (size_t)w[i] * sv4 + o;
+                else if (o < O_C8) a = S.mu + (size_t)w[i] * smu + (o - O_MU);
+                else if (o < O_CS) a = S.c8 + (size_t)w[i] * sc8 + (o - O_C8);
+                else if (o < O_VS) a = S.cs + (size_t)w[i] * scs + (o - O_CS);
+                else a = S.vs + (size_t)w[i] * svs;
+                f.addr[i] = a;
+            }
         }
+        f.mus = row(lane & 7) * smus;
 #pragma unroll
-        for (int i = 0; i < NML; ++i) {
-            const int s = 64 * i + lane, R = (s / MCH) & 7, k = (s % MCH) ^ GM::mswz(R);
-            f.m[i] = row(R) * D + 16 * k;
-        }
+        for (int i = 0; i < (PK ? NDI : 1); ++i) asm volatile("" :: "v"(f.off[i]));
 #pragma unroll
-        for (int i = 0; i < NCL; ++i) {
-            const int o = 1024 * i + 16 * lane;
-            f.c[i] = row(o / (PG * SC_RNK)) * (PG * SC_RNK) + o % (PG * SC_RNK);
-        }
-        const int oc = 16 * (lane % PG);
-        f.cs = row(oc / (2 * PG)) * (2 * PG) + oc % (2 * PG);
-        f.vs = row(lane & 7) * (SC_RNK * 2);
-        f.mus = row(lane & 7) * 2;
-#pragma unroll
-        for (int i = 0; i < NVL; ++i) asm volatile("" :: "v"(f.v[i]));
-#pragma unroll
-        for (int i = 0; i < NML; ++i) asm volatile("" :: "v"(f.m[i]));
-#pragma unroll
-        for (int i = 0; i < NCL; ++i) asm volatile("" :: "v"(f.c[i]));
-        asm volatile("" :: "v"(f.cs), "v"(f.vs), "v"(f.mus));
+        for (int i = 0; i < (PK ? 1 : NDI); ++i) asm volatile("" :: "v"(f.addr[i]));
+        asm volatile("" :: "v"(f.mus));
         return f;
     };
-    auto issue_sv = [&](const UnitOff& f) {          // packed V + centroid rows, centroid scale
+    auto issue = [&](const UnitSrc& f, uint8_t* st) {
 #pragma unroll
-        for (int i = 0; i < NVL; ++i) {
-            const uint32_t o = f.v[i];               // copied out first: a member of f inside the builtin's
-                                                     // arguments makes the host pass drop the kernel stub
-            __builtin_amdgcn_global_load_lds(v4b + o, (sc_lds_ptr)(sv + 1024 * i), 16, 0, SC_CPOL_NT);
+        for (int i = 0; i < NDI; ++i) {
+            // copied out first: a member of f inside the builtin's arguments
+            // makes the host pass drop the kernel stub
+            const uint8_t* src;
+            if constexpr (PK) { const uint32_t o = f.off[i]; src = S.v4 + o; }
+            else src = f.addr[i];
+            if (NCK % 64 == 0 || i < NDI - 1 || lane < NCK - 64 * (NDI - 1))
+                __builtin_amdgcn_global_load_lds(src, (sc_lds_ptr)(st + 1024 * i), 16, 0, SC_CPOL_NT);
         }
-#pragma unroll
-        for (int i = 0; i < NML; ++i) {
-            const uint32_t o = f.m[i];
-            if (D >= 128 || lane < 32)
-                __builtin_amdgcn_global_load_lds(mub + o, (sc_lds_ptr)(sv + SV_MU + 1024 * i), 16, 0, SC_CPOL_NT);
-        }
+        const uint32_t om = f.mus;
         if ((lane & 15) < 8)
-            fmus = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs_mus, (int)f.mus, 0, 0);
-    };
-    auto issue_sc = [&](const UnitOff& f, uint8_t* sc) {   // coefficients, token and column scales
-#pragma unroll
-        for (int i = 0; i < NCL; ++i) {
-            const uint32_t o = f.c[i];
-            __builtin_amdgcn_global_load_lds(c8b + o, (sc_lds_ptr)(sc + SC_C8 + 1024 * i), 16, 0, SC_CPOL_NT);
-        }
-        const uint32_t ocs = f.cs, ovs = f.vs;
-        if (lane < PG)                               // 8 pages x PG x 2 B
-            __builtin_amdgcn_global_load_lds(csb + ocs, (sc_lds_ptr)(sc + SC_CS), 16, 0, 0);
-        if (lane < 8)                                // 8 pages x 16 B
-            __builtin_amdgcn_global_load_lds(vsb + ovs, (sc_lds_ptr)(sc + SC_VS), 16, 0, 0);
+            fmus = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs_mus, (int)om, 0, 0);
     };
     __builtin_amdgcn_s_waitcnt(0x0070);      // q rows resident before the unit loads queue
-    if (wave < n_units) { const UnitOff f = unit_off(wave); issue_sv(f); issue_sc(f, sc0_l[wave]); }
+    if (wave < n_units) issue(unit_src(wave), sa_l[wave]);
 
     // ---- quantize q (the first unit's loads are in flight) --------------
     // q8 = rint(q / qs) with the correctly rounded quotient: q * (1 / qs) is
@@ -326,15 +303,13 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
     }
 
     float wrun = -INFINITY;                          // running per-head max of this lane's column
-    // Two coefficient stages per wave, alternating between units, as separate
-    // LDS objects: the next unit's sc DMA never shares an object with the
-    // current unit's token-stage reads.
-    auto score_unit = [&](int u, const uint8_t* sc, uint8_t* sc_next) {
-        __builtin_amdgcn_s_waitcnt(0x0070);          // this unit's rows have landed in the stages
+    auto score_unit = [&](int u, const uint8_t* st, uint8_t* st_next) {
+        __builtin_amdgcn_s_waitcnt(0x0070);          // this unit's rows have landed in the stage
         wave_lds_sync();
+        const float musf = ((lane & 15) < 8) ? bf16lo(fmus) : 0.f;   // before the next unit's load
         const bool more = u + SC_WAVES < n_units;
-        UnitOff nf;
-        if (more) nf = unit_off(u + SC_WAVES);
+        UnitSrc nf;
+        if (more) nf = unit_src(u + SC_WAVES);
         const int p0 = c0 + u * SC_TILE;
         const int nvalid = min(SC_TILE, c1 - p0);
 
@@ -353,40 +328,37 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
         float2 vsf[4][2];
 #pragma unroll
         for (int pp = 0; pp < 4; ++pp) {
-            const int R = 16 * pp + i_pg * 8 + i_c;            // (page 2pp + i_pg, column i_c)
-            const uint8_t* rp = sv + R * (D / 2);
+            // (page 2pp + i_pg, column i_c); lane group kg: bytes kg D / 8 ..
+            const uint8_t* rp = st + (2 * pp + i_pg) * RB + i_c * (D / 2) + kg * (D / 8);
             if constexpr (D == 64) {
-                const uint2 x = *reinterpret_cast<const uint2*>(rp + 16 * ((kg >> 1) ^ GM::vswz(R)) + 8 * (kg & 1));
+                const uint2 x = *reinterpret_cast<const uint2*>(rp);
                 vv[pp][0] = x.x; vv[pp][1] = x.y;
             } else {
 #pragma unroll
                 for (int k = 0; k < D / 128; ++k) {
-                    const uint4 x = *reinterpret_cast<const uint4*>(rp + 16 * ((kg * (D / 128) + k) ^ GM::vswz(R)));
+                    const uint4 x = *reinterpret_cast<const uint4*>(rp + 16 * k);
                     vv[pp][4 * k] = x.x; vv[pp][4 * k + 1] = x.y; vv[pp][4 * k + 2] = x.z; vv[pp][4 * k + 3] = x.w;
                 }
             }
 #pragma unroll
             for (int pg = 0; pg < 2; ++pg) {        // column scales (2kg, 2kg+1) of page 2pp+pg
-                const uint32_t w = *reinterpret_cast<const uint32_t*>(sc + SC_VS + (2 * pp + pg) * 16 + kg * 4);
+                const uint32_t w = *reinterpret_cast<const uint32_t*>(st + (2 * pp + pg) * RB + O_VS + kg * 4);
                 vsf[pp][pg] = make_float2(bf16lo(w), bf16hi(w));
             }
         }
         v4i mu[NWIN];
-        float musf = 0.f;
 #pragma unroll
         for (int w = 0; w < NWIN; ++w) mu[w] = v4i{0, 0, 0, 0};
         if ((lane & 15) < 8) {
             const int pg = lane & 15;
 #pragma unroll
             for (int w = 0; w < NWIN; ++w)
-                mu[w] = *reinterpret_cast<const v4i*>(sv + SV_MU + pg * D + 16 * ((kg * (D / 64) + w) ^ GM::mswz(pg)));
-            musf = bf16lo(fmus);
+                mu[w] = *reinterpret_cast<const v4i*>(st + pg * RB + O_MU + kg * (D / 4) + 16 * w);
         }
-        // sv is in registers: the next unit's packed V and centroid rows
-        // stream in under this unit's projection and token stages
-        __builtin_amdgcn_s_waitcnt(0xC07F);           // lgkmcnt(0): the sv reads have returned
-        wave_lds_sync();
-        if (more) { issue_sv(nf); issue_sc(nf, sc_next); }
+        // the next unit's rows stream in under this unit's projection and
+        // token stages (issued after the V / centroid reads, which the
+        // compiler would otherwise hold behind the DMA)
+        if (more) issue(nf, st_next);
         float qt[4][4];
 #pragma unroll
         for (int pp = 0; pp < 4; ++pp) {
@@ -430,15 +402,17 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
 #pragma unroll
             for (int ps = 0; ps < PPM; ++ps) {
                 const int page = gi * PPM + ps;
-                const uint32_t cw = *reinterpret_cast<const uint16_t*>(sc + SC_C8 + page * (PG * SC_RNK) +
-                                                                       (16 * tb + r16) * 8 + 2 * kg);
-                const float a0 = (float)(int8_t)cw, a1 = (float)(int8_t)(cw >> 8);
+                const uint8_t* rp = st + page * RB;
+                const uint32_t cw = *reinterpret_cast<const uint16_t*>(rp + O_C8 + (16 * tb + r16) * 8 + 2 * kg);
+                // the token scale rides on the coefficient operand: int8 x
+                // bf16 is exact in fp32
+                const float cf = __uint_as_float((uint32_t)*reinterpret_cast<const uint16_t*>(rp + O_CS + (16 * tb + r16) * 2) << 16);
+                const float a0 = (float)(int8_t)cw * cf, a1 = (float)(int8_t)(cw >> 8) * cf;
                 // qt is already zero where this lane's column is not page slot ps
                 acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, qt[page >> 1][page & 1], acc, 0, 0, 0);
                 acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, qt[page >> 1][2 + (page & 1)], acc, 0, 0, 0);
             }
-            const uint2 cw4 = *reinterpret_cast<const uint2*>(sc + SC_CS + ((gi * PPM + psub_l) * PG + 16 * tb + 4 * kg) * 2);
-            return v4f{acc[0] * bf16lo(cw4.x), acc[1] * bf16hi(cw4.x), acc[2] * bf16lo(cw4.y), acc[3] * bf16hi(cw4.y)};
+            return acc;
         };
         // 16-token LSE taken relative to the centroid term: tok - mud =
         // cs * acc.  The exp2 sum is exact whenever it lies in [2^-60, 2^60]
@@ -528,11 +502,21 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
             }
         }
         wrun = fmaxf(wrun, tmax);
+        // the DMA source registers stay allocated until here: a VGPR that a
+        // pending DMA reads its address from is not reused (a later write to
+        // it would have to wait for the DMA)
+        if (more) {
+#pragma unroll
+            for (int i = 0; i < (PK ? NDI : 1); ++i) asm volatile("" :: "v"(nf.off[i]));
+#pragma unroll
+            for (int i = 0; i < (PK ? 1 : NDI); ++i) asm volatile("" :: "v"(nf.addr[i]));
+            asm volatile("" :: "v"(nf.mus));
+        }
         wave_lds_sync();                               // stages reused by the unit after next
     };
     for (int u = wave; u < n_units; u += 2 * SC_WAVES) {
-        score_unit(u, sc0_l[wave], sc1_l[wave]);
-        if (u + SC_WAVES < n_units) score_unit(u + SC_WAVES, sc1_l[wave], sc0_l[wave]);
+        score_unit(u, sa_l[wave], sb_l[wave]);
+        if (u + SC_WAVES < n_units) score_unit(u + SC_WAVES, sb_l[wave], sa_l[wave]);
     }
     // per-head maxima of the workgroup -> LDS (ordered-uint atomic max), one
     // atomic per head column per row
@@ -571,7 +555,7 @@ extern "C" int32_t locks_score_num_chunks(int32_t max_pages, int32_t chunk) {
 extern "C" int32_t locks_score_rki4(
     const uint16_t* q, int64_t q_stride_req, int64_t q_stride_head,
     const uint8_t* v4, const uint16_t* vs, const int8_t* c8, const uint16_t* cs,
-    const int8_t* mu8, const uint16_t* mus, int32_t num_blocks,
+    const int8_t* mu8, const uint16_t* mus, const int64_t* slab_row_bytes, int32_t num_blocks,
     const int32_t* block_table, int64_t bt_stride, int32_t bt_cols,
     const int32_t* n_sel_hi, float* score_h, int32_t max_pages,
     float* page_max, int32_t chunk,
@@ -585,7 +569,10 @@ extern "C" int32_t locks_score_rki4(
                   "locks_score_rki4: n_req=%d / n_kv=%d outside the grid limits", n_req, n_kv);
     LOCKS_REQUIRE(q_stride_head % 8 == 0 && q_stride_req % 8 == 0,
                   "locks_score_rki4: q strides must be multiples of 8 elements (16-byte loads)");
-    LOCKS_REQUIRE((long)num_blocks * n_kv * (SC_RNK * head_dim / 2) < (1L << 32),
+    const SlabRows S = slab_rows(v4, vs, c8, cs, mu8, mus, slab_row_bytes, head_dim, page);
+    LOCKS_REQUIRE(slab_rows_ok(S, head_dim, page),
+                  "locks_score_rki4: slab row strides below the field sizes or misaligned");
+    LOCKS_REQUIRE(slab_rows_extent(S, (long)num_blocks * n_kv) < (1L << 32),
                   "locks_score_rki4: slab too large for 32-bit offsets");
     LOCKS_REQUIRE(num_blocks >= 1 && bt_cols >= 1 && max_pages >= 1,
                   "locks_score_rki4: empty geometry (num_blocks=%d bt_cols=%d max_pages=%d)",
@@ -600,16 +587,29 @@ extern "C" int32_t locks_score_rki4(
     dim3 grid(Z, n_kv, n_req);
     const size_t dyn = (size_t)(G + 16) * (head_dim + 16) + (size_t)chunk * sizeof(int);
     hipStream_t st = (hipStream_t)stream;
-#define LAUNCH(GWV, DV, PGV)                                                                   \
-    hipLaunchKernelGGL((rki4_score_kernel<GWV, DV, PGV>), grid, dim3(SC_BLOCK), dyn, st, q, \
-                       (long)q_stride_req, (long)q_stride_head, v4, vs, c8, cs, mu8, mus,      \
+    // packed rows: all six fields of a row together, in the kernel's order,
+    // rows of one common stride (any stride >= the fields: the reference's
+    // AoS record rounds to 64 B)
+    const long RSB = S.sv4;
+    const bool packed = RSB >= 5L * head_dim + 10L * page + 18 && S.svs == RSB && S.sc8 == RSB &&
+                        S.scs == RSB && S.smu == RSB && S.smus == RSB &&
+                        S.mu == S.v4 + 4L * head_dim && S.c8 == S.mu + head_dim &&
+                        S.cs == S.c8 + 8L * page && S.vs == S.cs + 2L * page && S.mus == S.vs + 16;
+#define LAUNCH(GWV, DV, PGV, PKV)                                                               \
+    hipLaunchKernelGGL((rki4_score_kernel<GWV, DV, PGV, PKV>), grid, dim3(SC_BLOCK), dyn, st, q, \
+                       (long)q_stride_req, (long)q_stride_head, S,                             \
                        num_blocks, block_table, (long)bt_stride, bt_cols, n_sel_hi,            \
                        score_h, max_pages, page_max, n_kv, G, sm_scale, chunk)
-#define LAUNCH_G(DV, PGV)                     \
-    do {                                      \
-        if (G <= 4) LAUNCH(4, DV, PGV);       \
-        else if (G <= 8) LAUNCH(8, DV, PGV);  \
-        else LAUNCH(16, DV, PGV);             \
+#define LAUNCH_GP(DV, PGV, PKV)                    \
+    do {                                           \
+        if (G <= 4) LAUNCH(4, DV, PGV, PKV);       \
+        else if (G <= 8) LAUNCH(8, DV, PGV, PKV);  \
+        else LAUNCH(16, DV, PGV, PKV);             \
+    } while (0)
+#define LAUNCH_G(DV, PGV)                          \
+    do {                                           \
+        if (packed) LAUNCH_GP(DV, PGV, true);      \
+        else LAUNCH_GP(DV, PGV, false);            \
     } while (0)
     if (page == 16) {
         if (head_dim == 128) LAUNCH_G(128, 16);
@@ -625,6 +625,7 @@ extern "C" int32_t locks_score_rki4(
         else LAUNCH_G(256, 64);
     }
 #undef LAUNCH_G
+#undef LAUNCH_GP
 #undef LAUNCH
     return check_launch("rki4_score_kernel");
 }

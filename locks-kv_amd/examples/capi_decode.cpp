@@ -120,10 +120,10 @@ int main() {
     // ---- summaries of the finalized pages (settled tokens: SEQ - 1)
     const int n_fin = (SEQ - 1) / PAGE;
     LOCKS_OK(locks_build_rki4(d_kv, s_blk, s_tok, D, NB, d_blocks, n_fin, NKV, D, PAGE, d_v4,
-                              d_vs, d_c8, d_cs, d_mu8, d_mus, d_tag, stream));
+                              d_vs, d_c8, d_cs, d_mu8, d_mus, nullptr, d_tag, stream));
     LOCKS_OK(locks_derive_params(d_seq, R, PAGE, WINDOW, SINK, BUDGET, 0.1, d_npg, d_nsh, d_bfix,
                                  stream));
-    LOCKS_OK(locks_score_rki4(d_q, (long)H * D, D, d_v4, d_vs, d_c8, d_cs, d_mu8, d_mus, NB, d_bt,
+    LOCKS_OK(locks_score_rki4(d_q, (long)H * D, D, d_v4, d_vs, d_c8, d_cs, d_mu8, d_mus, nullptr, NB, d_bt,
                               MP, MP, d_nsh, d_sh, MP, d_pmax, chunk, R, NKV, G, D, PAGE, scale,
                               stream));
     LOCKS_OK(locks_select_nrm_topb(d_sh, d_pmax, chunks, d_npg, d_nsh, d_bfix, d_score, d_tab,

@@ -10,7 +10,7 @@ import ctypes
 import os
 
 _LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "liblocks_hip.so")
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _c = ctypes
 _i32, _i64, _f32, _f64, _p = _c.c_int32, _c.c_int64, _c.c_float, _c.c_double, _c.c_void_p
@@ -22,7 +22,7 @@ SIGNATURES = {
     "locks_derive_params": (_i32, [_p, _i32, _i32, _i32, _i32, _i32, _f64, _p, _p, _p, _p]),
     "locks_score_auto_chunk": (_i32, [_i32, _i32, _i32]),
     "locks_score_num_chunks": (_i32, [_i32, _i32]),
-    "locks_score_rki4": (_i32, [_p, _i64, _i64, _p, _p, _p, _p, _p, _p, _i32, _p, _i64, _i32,
+    "locks_score_rki4": (_i32, [_p, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _i32, _p, _i64, _i32,
                                 _p, _p, _i32, _p, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _p]),
     "locks_select_workspace_bytes": (_i64, [_i32, _i32, _i32]),
     "locks_select_nrm_topb": (_i32, [_p, _p, _i32, _p, _p, _p, _p, _p, _p, _p, _i64,
@@ -36,13 +36,13 @@ SIGNATURES = {
                                   _p, _p, _p, _p, _p, _i64, _i64, _i32,
                                   _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _p]),
     "locks_build_rki4": (_i32, [_p, _i64, _i64, _i64, _i32, _p, _i32, _i32, _i32, _i32,
-                                _p, _p, _p, _p, _p, _p, _p, _p]),
+                                _p, _p, _p, _p, _p, _p, _p, _p, _p]),
     "locks_refresh_blocks": (_i32, [_i32, _p, _i64, _p, _i32, _p, _i32, _i32, _i32, _i32, _p,
                                     _i32, _i64, _i64, _i64, _i32, _p, _i64, _p, _p, _p, _p]),
     "locks_build_rki4_layers": (_i32, [_p, _i32, _i64, _i64, _i64, _i32, _p, _p, _i32, _i32,
-                                       _i32, _i32, _i64, _p, _p, _p, _p, _p, _p, _p, _p]),
+                                       _i32, _i32, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p]),
     "locks_calib_read": (_i32, [_p, _i64, _p, _p]),
-    "locks_pack_rki4": (_i32, [_p, _p, _p, _p, _p, _i32, _i32, _i32, _p, _p, _p, _p, _p, _p, _p]),
+    "locks_pack_rki4": (_i32, [_p, _p, _p, _p, _p, _i32, _i32, _i32, _p, _p, _p, _p, _p, _p, _p, _p]),
     "locks_mla_score": (_i32, [_p, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _p,
                                _i64, _i32, _p, _p, _i64, _i32, _i32, _i32, _i32, _i32, _i32,
                                _i32, _f32, _p]),
@@ -108,6 +108,13 @@ def check(rc: int, what: str) -> None:
 def ptr(t) -> int:
     """Device pointer of a torch tensor (None -> NULL)."""
     return 0 if t is None else int(t.data_ptr())
+
+
+def rows_arg(st) -> int:
+    """slab_row_bytes argument for a summary state: the address of its six
+    row strides (a state with packed rows), or NULL (contiguous slabs)."""
+    rb = getattr(st, "slab_row_bytes", None)
+    return 0 if rb is None else _c.addressof(rb)
 
 
 def stream_ptr(device=None) -> int:

@@ -45,7 +45,8 @@ def mla_build_blocks(st, layer: int, kv_cache, blocks) -> int:
     _lib.check(lib.locks_build_rki4(
         _lib.ptr(cache), sb, stt, 0, int(min(st.NB, cache.shape[0])), _lib.ptr(b), n, 1, st.D,
         st.page, _lib.ptr(v4), _lib.ptr(vs), _lib.ptr(c8), _lib.ptr(cs), _lib.ptr(mu8),
-        _lib.ptr(mus), _lib.ptr(tag), _lib.stream_ptr(cache.device)), "build_rki4 (latent)")
+        _lib.ptr(mus), _lib.rows_arg(st), _lib.ptr(tag), _lib.stream_ptr(cache.device)),
+        "build_rki4 (latent)")
     return n
 
 

@@ -49,7 +49,7 @@ def rki4_score_only(st, layer: int, q, block_table, seq_lens, n_req: int,
     _lib.check(lib.locks_score_rki4(
         _lib.ptr(q3), q3.stride(0), q3.stride(1),
         _lib.ptr(v4), _lib.ptr(vs), _lib.ptr(c8), _lib.ptr(cs), _lib.ptr(mu8), _lib.ptr(mus),
-        int(st.NB), _lib.ptr(block_table), block_table.stride(0), int(block_table.shape[1]),
+        _lib.rows_arg(st), int(st.NB), _lib.ptr(block_table), block_table.stride(0), int(block_table.shape[1]),
         _lib.ptr(st.n_sel_hi), _lib.ptr(st.score_h), int(st.max_pages),
         _lib.ptr(st.page_max), int(st.score_chunk), int(n_req), int(st.n_kv), int(st.G),
         int(st.d), int(st.page), float(scale), _lib.stream_ptr(q.device)), "rki4_score")

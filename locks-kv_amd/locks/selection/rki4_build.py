@@ -40,7 +40,8 @@ def rki4_build_blocks(st, layer: int, K: torch.Tensor, blocks: torch.Tensor) -> 
     _lib.check(lib.locks_build_rki4(
         _lib.ptr(K), K.stride(0), K.stride(1), K.stride(2), nb, _lib.ptr(b), n, int(st.n_kv),
         int(st.d), int(st.page), _lib.ptr(v4), _lib.ptr(vs), _lib.ptr(c8), _lib.ptr(cs),
-        _lib.ptr(mu8), _lib.ptr(mus), _lib.ptr(tag), _lib.stream_ptr(K.device)), "build_rki4")
+        _lib.ptr(mu8), _lib.ptr(mus), _lib.rows_arg(st), _lib.ptr(tag), _lib.stream_ptr(K.device)),
+        "build_rki4")
     return n
 
 
@@ -56,7 +57,7 @@ def rki4_pack(st, layer: int, mu, dc, S2, U, rows) -> None:
     _lib.check(lib.locks_pack_rki4(
         *[_lib.ptr(t) for t in ts], _lib.ptr(rows), int(rows.numel()), int(st.d), int(st.page),
         _lib.ptr(v4), _lib.ptr(vs), _lib.ptr(c8), _lib.ptr(cs), _lib.ptr(mu8), _lib.ptr(mus),
-        _lib.stream_ptr(rows.device)), "pack_rki4")
+        _lib.rows_arg(st), _lib.stream_ptr(rows.device)), "pack_rki4")
 
 
 @torch.no_grad()
@@ -157,7 +158,8 @@ def _refresh(st, mode: str, K_layers, block_table, seq_lens, n_req: int, rows=No
         _lib.ptr(kptr), int(st.L), K0.stride(0), K0.stride(1), K0.stride(2), nb,
         _lib.ptr(st.refresh_blocks), _lib.ptr(st.refresh_count), bound, int(st.n_kv),
         int(st.d), int(st.page), int(st.NB), _lib.ptr(v4), _lib.ptr(vs), _lib.ptr(c8),
-        _lib.ptr(cs), _lib.ptr(mu8), _lib.ptr(mus), _lib.ptr(tag), stream), "build_rki4_layers")
+        _lib.ptr(cs), _lib.ptr(mu8), _lib.ptr(mus), _lib.rows_arg(st), _lib.ptr(tag), stream),
+        "build_rki4_layers")
     return bound
 
 

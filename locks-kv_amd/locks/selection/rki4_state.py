@@ -20,9 +20,24 @@ per-chunk maxima -- and sel_ws, the selector's candidate workspace.
 Footprint per (page, kv head): 5d + 10*page + 18 bytes of summary (818 B at
 d=128, page 16) + 16 B tag (rki4_state.py:18-22, record_bytes :124-141).
 Geometry: d in {64, 128, 256}, page 16, 32 or 64, G <= 16.
+
+Memory layout (this build): the six summary fields of one (block, kv head)
+are stored together in one record of ``pp_rows`` (L, NB, n_kv, row_bytes)
+u8, row_bytes = 5d + 10*page + 18 rounded up to 64 (832 B at d=128, page
+16), fields in the order v4 | mu8 | c8 | cs | vs | mus -- the reference's
+AoS record (rki4_state.py:93-110, 198-219; the reference builds it for
+d=128 / page 16 under RKI4_MMA_AOS, this build for every geometry).  The
+scorer reads a page's summary as one contiguous ~0.8 KB row instead of six
+rows in six arrays (16-, 32- and 2-byte rows each costing a cache line of
+their own).
+``pp_v4`` .. ``pp_mus`` are strided views with the reference's shapes and
+dtypes, so every tensor-level use (copies, comparisons) is unchanged; the
+kernels take each slab's row stride (``slab_row_bytes``).  The tag stays a
+separate slab (read only by the refresh lifecycle).
 """
 from __future__ import annotations
 
+import ctypes
 import math
 
 import torch
@@ -34,6 +49,44 @@ RNK = 8
 IBITS = 4
 QMAX = (1 << (IBITS - 1)) - 1
 QMIN = -(1 << (IBITS - 1))
+
+
+def packed_row_bytes(d: int, page: int) -> int:
+    """Bytes of one packed (block, kv head) summary record: 5d + 10*page + 18
+    rounded up to 64 (the reference's _rec_bytes_aos, rki4_state.py:106-109)."""
+    return -(-(5 * d + 10 * page + 18) // 64) * 64
+
+
+def packed_slab_views(rows: torch.Tensor, d: int, page: int):
+    """(v4, vs, c8, cs, mu8, mus) views of packed rows (..., row_bytes) u8,
+    with the reference's slab shapes and dtypes."""
+    P, i8, bf16 = page, torch.int8, torch.bfloat16
+    o_mu = RNK * d // 2
+    o_c8 = o_mu + d
+    o_cs = o_c8 + RNK * P
+    o_vs = o_cs + 2 * P
+    o_mus = o_vs + 2 * RNK
+    v4 = rows[..., 0:o_mu].unflatten(-1, (RNK, d // 2))
+    mu8 = rows[..., o_mu:o_c8].view(i8)
+    c8 = rows[..., o_c8:o_cs].view(i8).unflatten(-1, (P, RNK))
+    cs = rows[..., o_cs:o_vs].view(bf16)
+    vs = rows[..., o_vs:o_mus].view(bf16)
+    mus = rows[..., o_mus:o_mus + 2].view(bf16)[..., 0]
+    return v4, vs, c8, cs, mu8, mus
+
+
+def slab_row_bytes(slabs) -> "ctypes.Array":
+    """The C ABI's slab_row_bytes argument for (v4, vs, c8, cs, mu8, mus)
+    tensors shaped (..., NB, n_kv, field...): each slab's byte stride between
+    consecutive (block, kv head) rows."""
+    vals = []
+    for t, tail in zip(slabs, (2, 1, 2, 1, 1, 0)):    # field dims after (NB, n_kv)
+        kv_dim = t.dim() - tail - 1
+        rb = t.stride(kv_dim) * t.element_size()
+        assert t.stride(kv_dim - 1) * t.element_size() == rb * t.shape[kv_dim], \
+            "slab rows of one block must be consecutive over kv heads"
+        vals.append(rb)
+    return (ctypes.c_int64 * 6)(*vals)
 
 
 def record_bytes(d: int, page: int, tagw: int = TAGW) -> int:
@@ -73,12 +126,12 @@ class Rki4State:
         i32, f32 = torch.int32, torch.float32
         dev = self.device
 
-        self.pp_v4 = torch.zeros(L, NB, n_kv, RNK, D * IBITS // 8, device=dev, dtype=u8)
-        self.pp_vs = torch.zeros(L, NB, n_kv, RNK, device=dev, dtype=bf16)
-        self.pp_c8 = torch.zeros(L, NB, n_kv, page, RNK, device=dev, dtype=i8)
-        self.pp_cs = torch.zeros(L, NB, n_kv, page, device=dev, dtype=bf16)
-        self.pp_mu8 = torch.zeros(L, NB, n_kv, D, device=dev, dtype=i8)
-        self.pp_mus = torch.zeros(L, NB, n_kv, device=dev, dtype=bf16)
+        self.row_bytes = packed_row_bytes(D, page)
+        self.pp_rows = torch.zeros(L, NB, n_kv, self.row_bytes, device=dev, dtype=u8)
+        (self.pp_v4, self.pp_vs, self.pp_c8, self.pp_cs, self.pp_mu8,
+         self.pp_mus) = packed_slab_views(self.pp_rows, D, page)
+        self.slab_row_bytes = slab_row_bytes(
+            (self.pp_v4, self.pp_vs, self.pp_c8, self.pp_cs, self.pp_mu8, self.pp_mus))
         self.pp_tag = torch.full((L, NB, n_kv, tagw), float("nan"), device=dev, dtype=bf16)
 
         self.score = torch.zeros(R, n_kv, MP, device=dev, dtype=f32)

@@ -40,7 +40,7 @@ def _layers(case, L, seed):
 def _slab_bytes(st):
     import torch
     torch.cuda.synchronize()
-    return {n: getattr(st, n).view(torch.uint8).cpu().numpy() for n in SLABS}
+    return {n: getattr(st, n).contiguous().view(torch.uint8).cpu().numpy() for n in SLABS}
 
 
 def _assert_same(a, b):

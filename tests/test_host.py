@@ -72,7 +72,7 @@ def test_ctypes_signatures_match_the_header():
 def test_rejects_bad_geometry_without_device():
     from locks import _lib
     lib = _lib.load()
-    args = [0, 0, 0] + [1] * 6 + [1, 1, 0, 1, 1, 1, 16, 1, 32, 1, 2, 4, 96, 16, 0.1, None]
+    args = [0, 0, 0] + [1] * 6 + [None] + [1, 1, 0, 1, 1, 1, 16, 1, 32, 1, 2, 4, 96, 16, 0.1, None]
     rc = lib.locks_score_rki4(*args)           # head_dim 96 is outside the contract
     assert rc == -1 and b"head_dim 96" in lib.locks_last_error()
     args[-4] = 64
@@ -220,7 +220,7 @@ def test_mla_entries_reject_bad_geometry_without_device():
     assert 2 <= lib.locks_mla_score_auto_chunk(1, 8192) <= 1024
     assert lib.locks_mla_score_auto_chunk(1, 8192) % 2 == 0
     # the build takes d = 512 (the latent) only at page 16, and no d = 96
-    bargs = [1, 16 * 576, 576, 0, 8, 1, 1, 1, 96, 16] + [1] * 7 + [None]
+    bargs = [1, 16 * 576, 576, 0, 8, 1, 1, 1, 96, 16] + [1] * 6 + [None, 1, None]
     assert lib.locks_build_rki4(*bargs) == -1 and b"d=96" in lib.locks_last_error()
     bargs[8:10] = [512, 32]
     assert lib.locks_build_rki4(*bargs) == -1 and b"d=512 page=32" in lib.locks_last_error()
@@ -243,7 +243,7 @@ def test_refresh_entries_reject_bad_arguments_without_device():
     a = list(ok); a[18] = None
     assert lib.locks_refresh_blocks(*a) == -1 and b"null pointer" in lib.locks_last_error()
     # locks_build_rki4_layers: geometry and the slab-blocks bound
-    bl = [1, 2, 16 * 8 * 128, 8 * 128, 128, 100, 1, None, 4, 8, 128, 16, 100] + [1] * 7 + [None]
+    bl = [1, 2, 16 * 8 * 128, 8 * 128, 128, 100, 1, None, 4, 8, 128, 16, 100] + [1] * 6 + [None, 1, None]
     b = list(bl); b[10] = 96
     assert lib.locks_build_rki4_layers(*b) == -1 and b"d=96" in lib.locks_last_error()
     b = list(bl); b[11] = 8                              # page 8: outside the domain
