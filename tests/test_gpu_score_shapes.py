@@ -2,9 +2,9 @@
 
 The scorer's workgroup scores `chunk` pages of one kv head as 8-page units,
 4 waves each taking every 4th unit: with chunk >= 64 a wave scores several
-units, prefetching the next into registers while it scores the current one,
-reusing its LDS stage, and folding each unit's per-head maxima into the
-chunk's `page_max`.  These cases force those paths (explicit zsplit on the
+units, DMA'ing the next unit's summary records into its other LDS stage
+while it scores the current one, and folding each unit's per-head maxima
+into the chunk's `page_max`.  These cases force those paths (explicit zsplit on the
 16K Llama-shaped row: chunk 64 / 128 / 256 / 1024) and run the full rows of
 the benchmarked configurations at their automatic chunking: Llama 128K
 (8 kv x 8191 pages), GLM 1M (2 kv x 65535 pages, G = 16), the ragged GLM
@@ -16,6 +16,8 @@ page alone).  Bar: |score_h - oracle| <= 2e-5 on every scored page,
 page_max[r, kh, z, g] equal to the max of the chunk's scored pages, and no
 write past n_sel_hi.  Slab bytes are seeded random draws over the full
 code ranges (tests/cases.random_slabs): the scorer reads bytes, not keys.
+The same bytes as the reference's six separate contiguous slabs (C ABI,
+slab_row_bytes NULL) must score bit-identically to the state's AoS records.
 """
 from __future__ import annotations
 
@@ -123,6 +125,55 @@ def test_score_ragged_glm_batch():
     """{256K, 192K, 128K, 64K}, one grid sized for the
     longest row; the shorter rows' tail chunks score nothing."""
     _run(27, 2, 16, [262144, 196608, 131072, 65536], check64=False)
+
+
+@pytest.mark.parametrize("d,page,n_kv,G,seq,zsplit", [
+    (128, 16, 8, 4, 16384, 8),       # Llama shape, 2 units per wave
+    (128, 16, 2, 16, 4000, 1),       # G = 16, ragged last tile
+    (64, 32, 4, 8, 6000, 2),         # another geometry
+])
+def test_score_six_slabs_equal_records(d, page, n_kv, G, seq, zsplit):
+    """locks_score_rki4 over six separate contiguous slabs (the reference's
+    tensors; slab_row_bytes NULL: each row's fields gathered from six arrays)
+    returns bit-identical score_h and page_max to the state's AoS records
+    (one stream per record)."""
+    import ctypes
+    import torch
+    from locks import _lib
+    from locks.selection import Rki4State, derive_page_params, rki4_score_only
+    from tests.cases import load_slabs
+    rng = np.random.default_rng(31)
+    npg = (seq + page - 1) // page
+    MP, NB = npg, npg + 3
+    bt = O.synth_block_table(rng, [seq], page, NB, MP)
+    slabs = random_slabs(rng, NB, n_kv, d, page)
+    q = O.f32_to_bf16(rng.standard_normal((1, n_kv * G, d), dtype=np.float32))
+    scale = 1.0 / np.sqrt(d)
+    st = Rki4State("cuda", num_layers=1, num_blocks=NB, n_kv=n_kv, G=G, head_dim=d, page=page,
+                   max_reqs=1, max_pages=MP, budget_pages=16, zsplit=zsplit)
+    say(f"six slabs vs records: d={d} page={page} n_kv={n_kv} G={G} seq={seq} chunk={st.score_chunk}")
+    load_slabs(st, 0, slabs)
+    dq = torch.from_numpy(q.view(np.int16)).view(torch.bfloat16).cuda()
+    dbt = torch.from_numpy(bt).cuda()
+    dsl = torch.tensor([seq], dtype=torch.int32, device="cuda")
+    derive_page_params(st, dsl, 1)
+    st.score_h.fill_(SENTINEL)
+    rki4_score_only(st, 0, dq, dbt, dsl, 1, scale)
+    torch.cuda.synchronize()
+    rec_sh, rec_pm = st.score_h.clone(), st.page_max.clone()
+    six = [t[0].contiguous() for t in (st.pp_v4, st.pp_vs, st.pp_c8, st.pp_cs, st.pp_mu8, st.pp_mus)]
+    assert all(t.is_contiguous() for t in six)
+    sh = torch.full_like(st.score_h, SENTINEL)
+    pm = torch.full_like(st.page_max, float("nan"))
+    lib = _lib.load()
+    _lib.check(lib.locks_score_rki4(
+        _lib.ptr(dq), dq.stride(0), dq.stride(1), *[_lib.ptr(t) for t in six], None,
+        NB, _lib.ptr(dbt), dbt.stride(0), int(dbt.shape[1]), _lib.ptr(st.n_sel_hi), _lib.ptr(sh), MP,
+        _lib.ptr(pm), st.score_chunk, 1, n_kv, G, d, page, ctypes.c_float(scale).value,
+        _lib.stream_ptr()), "score (six slabs)")
+    torch.cuda.synchronize()
+    assert torch.equal(sh, rec_sh), "score_h differs between six slabs and records"
+    assert torch.equal(pm, rec_pm), "page_max differs between six slabs and records"
 
 
 def test_mla_score_8k_pages():
