@@ -86,6 +86,19 @@ __device__ __forceinline__ float xor32_max(float x) {
     return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
+// Whole-wave max of unsigned keys, result in every lane (DPP row rotations,
+// then the two pair swaps).
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, (uint32_t)row_ror<8>((int)v));
+    v = max(v, (uint32_t)row_ror<4>((int)v));
+    v = max(v, (uint32_t)row_ror<2>((int)v));
+    v = max(v, (uint32_t)row_ror<1>((int)v));
+    auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    v = max(r[0], r[1]);
+    r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return max(r[0], r[1]);
+}
+
 // Whole-wave max / integer sum, result in every lane: row rotations, then
 // the two pair swaps -- no LDS round trip.
 __device__ __forceinline__ float wave_max(float v) {
