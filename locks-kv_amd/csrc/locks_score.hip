@@ -122,13 +122,15 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
     // wait for the DMA before every read)
     __shared__ __attribute__((aligned(16))) uint8_t sa_l[SC_WAVES][GM::ST_BYTES];
     __shared__ __attribute__((aligned(16))) uint8_t sb_l[SC_WAVES][GM::ST_BYTES];
-    __shared__ __attribute__((aligned(16))) float sm_l[SC_WAVES][SC_TILE * 16];
     __shared__ uint32_t wmax[16];
-    // dynamic LDS: int8 q rows of this kv head's G query heads (+16 zero
-    // rows), slab rows (block x n_kv + kv head) of the chunk
-    extern __shared__ __attribute__((aligned(16))) uint8_t dyn_l[];
-    int8_t (*q8s)[SC_QROW] = reinterpret_cast<int8_t (*)[SC_QROW]>(dyn_l);
-    int* bt_l = reinterpret_cast<int*>(dyn_l + (size_t)(G + 16) * SC_QROW);
+    // dynamic LDS: slab rows (block x n_kv + kv head) of the chunk
+    extern __shared__ __attribute__((aligned(16))) int dyn_l[];
+    int* bt_l = dyn_l;
+    // int8 q rows of this kv head's G query heads (+16 zero rows) live in the
+    // second stages until the q operands are built: no DMA reaches them
+    // before the first unit, and the workgroup fits three to a CU
+    static_assert((16 + 16) * SC_QROW <= SC_WAVES * GM::ST_BYTES, "q rows fit the second stages");
+    int8_t (*q8s)[SC_QROW] = reinterpret_cast<int8_t (*)[SC_QROW]>(&sb_l[0][0]);
 
     // ---- prologue: q rows and block ids are fetched together; the first
     // unit's summary loads are issued before q is quantized, so the
@@ -169,7 +171,6 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
     // row strides (bytes) of the slabs: offsets below stay under 2^32
     const uint32_t sv4 = (uint32_t)S.sv4, svs = (uint32_t)S.svs, sc8 = (uint32_t)S.sc8,
                    scs = (uint32_t)S.scs, smu = (uint32_t)S.smu, smus = (uint32_t)S.smus;
-    float* const mud_w = sm_l[wave];                 // [page][16 heads]
     uint32_t fmus = 0;                               // centroid scale of page lane & 15 (lanes & 15 < 8)
     // Every lane's sources of one unit, read from the slab rows in LDS while
     // no DMA is outstanding (an LDS read issued behind a DMA waits for it)
@@ -292,6 +293,7 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
         }
     }
     const float4 qsl = *reinterpret_cast<const float4*>(&qsp[4 * kg]);   // rows 4kg.. (mud)
+    __syncthreads();                         // q rows consumed: the second stages are free
     // column head's q scale x 1/16 (the nibble shift), zeroed where the
     // token stage's block-diagonal B has no entry for this lane's column:
     // qt of page p feeds page slot p % PPM only
@@ -303,7 +305,10 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
     }
 
     float wrun = -INFINITY;                          // running per-head max of this lane's column
-    auto score_unit = [&](int u, const uint8_t* st, uint8_t* st_next) {
+    auto score_unit = [&](int u, uint8_t* st, uint8_t* st_next) {
+        // per-page centroid terms mud[page][head] go into the first 64 B of
+        // the page's stage row (packed V, consumed by then)
+        auto mud_at = [&](int page, int g) -> float* { return reinterpret_cast<float*>(st + page * RB) + g; };
         __builtin_amdgcn_s_waitcnt(0x0070);          // this unit's rows have landed in the stage
         wave_lds_sync();
         const float musf = ((lane & 15) < 8) ? bf16lo(fmus) : 0.f;   // before the next unit's load
@@ -389,7 +394,7 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
                 md.y = (float)accm[1] * qsl.y * musf;
                 md.z = (float)accm[2] * qsl.z * musf;
                 md.w = (float)accm[3] * qsl.w * musf;
-                *reinterpret_cast<float4*>(mud_w + (lane & 15) * 16 + 4 * kg) = md;
+                *reinterpret_cast<float4*>(mud_at(lane & 15, 4 * kg)) = md;
             }
         }
         wave_lds_sync();
@@ -438,29 +443,29 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
         }
         float tot[NSET];
 #pragma unroll
-        for (int st = 0; st < NSET; ++st) {
+        for (int sx = 0; sx < NSET; ++sx) {
             auto pair16 = [](float u, float v) {
                 const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(u), __float_as_uint(v), false, false);
                 return __uint_as_float(r[0]) + __uint_as_float(r[1]);
             };
             if constexpr (NGRP >= 4) {
-                const float A = pair16(ev[4 * st], ev[4 * st + 1]);      // rows: g0 01, g1 01, g0 23, g1 23
-                const float B = pair16(ev[4 * st + 2], ev[4 * st + 3]);  // rows: g2 01, g3 01, g2 23, g3 23
+                const float A = pair16(ev[4 * sx], ev[4 * sx + 1]);      // rows: g0 01, g1 01, g0 23, g1 23
+                const float B = pair16(ev[4 * sx + 2], ev[4 * sx + 3]);  // rows: g2 01, g3 01, g2 23, g3 23
                 const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(A), __float_as_uint(B), false, false);
-                tot[st] = __uint_as_float(r[0]) + __uint_as_float(r[1]); // row k: group 4 st + k
+                tot[sx] = __uint_as_float(r[0]) + __uint_as_float(r[1]); // row k: group 4 sx + k
             } else {
-                tot[st] = xor32_sum(pair16(ev[0], ev[1]));               // row k: group k & 1
+                tot[sx] = xor32_sum(pair16(ev[0], ev[1]));               // row k: group k & 1
             }
         }
-        auto grp_of = [&](int st) { return (NGRP >= 4) ? 4 * st + kg : (kg & 1); };
+        auto grp_of = [&](int sx) { return (NGRP >= 4) ? 4 * sx + kg : (kg & 1); };
         bool ok = true;
 #pragma unroll
-        for (int st = 0; st < NSET; ++st) ok = ok && (tot[st] >= 0x1p-60f) && (tot[st] <= 0x1p60f);
+        for (int sx = 0; sx < NSET; ++sx) ok = ok && (tot[sx] >= 0x1p-60f) && (tot[sx] <= 0x1p60f);
         float Sv[NSET];
         if (__builtin_expect(__ballot(!ok) == 0ull, 1)) {
 #pragma unroll
-            for (int st = 0; st < NSET; ++st)
-                Sv[st] = (mud_w[(grp_of(st) * PPM + psub_l) * 16 + g_l] + __builtin_amdgcn_logf(tot[st])) *
+            for (int sx = 0; sx < NSET; ++sx)
+                Sv[sx] = (*mud_at(grp_of(sx) * PPM + psub_l, g_l) + __builtin_amdgcn_logf(tot[sx])) *
                          0.6931471805599453f;
         } else {
             // exact-max form (rare): every lane computes every group
@@ -481,24 +486,24 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
                     f += __builtin_amdgcn_exp2f(x[tb][0] - m) + __builtin_amdgcn_exp2f(x[tb][1] - m) +
                          __builtin_amdgcn_exp2f(x[tb][2] - m) + __builtin_amdgcn_exp2f(x[tb][3] - m);
                 f = xor32_sum(xor16_sum(f));
-                Sa[gi] = ((mud_w[(gi * PPM + psub_l) * 16 + g_l] + m) + __builtin_amdgcn_logf(f)) * 0.6931471805599453f;
+                Sa[gi] = ((*mud_at(gi * PPM + psub_l, g_l) + m) + __builtin_amdgcn_logf(f)) * 0.6931471805599453f;
             }
 #pragma unroll
-            for (int st = 0; st < NSET; ++st) {
+            for (int sx = 0; sx < NSET; ++sx) {
                 float v = Sa[0];
 #pragma unroll
-                for (int gi = 1; gi < NGRP; ++gi) v = (grp_of(st) == gi) ? Sa[gi] : v;
-                Sv[st] = v;
+                for (int gi = 1; gi < NGRP; ++gi) v = (grp_of(sx) == gi) ? Sa[gi] : v;
+                Sv[sx] = v;
             }
         }
         float tmax = -INFINITY;
         const bool row_owner = (NGRP >= 4) || (kg < 2);      // rows 2, 3 repeat rows 0, 1
 #pragma unroll
-        for (int st = 0; st < NSET; ++st) {
-            const int page = grp_of(st) * PPM + psub_l;
+        for (int sx = 0; sx < NSET; ++sx) {
+            const int page = grp_of(sx) * PPM + psub_l;
             if (row_owner && (page < nvalid) && (g_l < G)) {
-                tmax = fmaxf(tmax, Sv[st]);
-                score_h[(((long)r * n_kv + h) * G + g_l) * (long)MP + p0 + page] = Sv[st];
+                tmax = fmaxf(tmax, Sv[sx]);
+                score_h[(((long)r * n_kv + h) * G + g_l) * (long)MP + p0 + page] = Sv[sx];
             }
         }
         wrun = fmaxf(wrun, tmax);
@@ -585,7 +590,7 @@ extern "C" int32_t locks_score_rki4(
     if (n_req == 0) return 0;
     const int Z = cdiv(max_pages, chunk);
     dim3 grid(Z, n_kv, n_req);
-    const size_t dyn = (size_t)(G + 16) * (head_dim + 16) + (size_t)chunk * sizeof(int);
+    const size_t dyn = (size_t)chunk * sizeof(int);
     hipStream_t st = (hipStream_t)stream;
     // packed rows: all six fields of a row together, in the kernel's order,
     // rows of one common stride (any stride >= the fields: the reference's
