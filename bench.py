@@ -368,7 +368,7 @@ def cpu_baseline(a, runs=10, warmup=2):
 # --------------------------------------------------------------------------- #
 # MLA (config 5)
 # --------------------------------------------------------------------------- #
-def make_mla_model(wl, seed=0):
+def make_mla_model(wl, seed=0, rope="exact"):
     import torch
     from locks.selection import MlaState, mla_build_blocks
     dev = torch.device("cuda")
@@ -385,7 +385,8 @@ def make_mla_model(wl, seed=0):
         bt[r, :n] = perm[off:off + n]
         off += n
     st = MlaState(dev, num_layers=L, num_blocks=NB, n_heads=H, max_reqs=R, max_pages=MP,
-                  budget_pages=wl["budget_pages"], sink_pages=1, window_pages=wl["window_pages"])
+                  budget_pages=wl["budget_pages"], sink_pages=1, window_pages=wl["window_pages"],
+                  rope=rope)
     fin = torch.cat([bt[r, : sls[r] // PAGE] for r in range(R)])
     caches, t_build = [], 0.0
     for layer in range(L):
@@ -519,7 +520,7 @@ def mla_cpu_baseline(m, sample_pages=1024):
 def run_mla(a, wl):
     import torch
     t0 = time.perf_counter()
-    m = make_mla_model(wl)
+    m = make_mla_model(wl, rope=a.mla_rope)
     log(f"MLA model ready in {time.perf_counter() - t0:.1f}s (latent summary build {m['build_s']:.1f}s)")
     R, H, L = m["R"], m["H"], m["L"]
     out = [torch.empty(R, H, MLA_LKV, dtype=torch.bfloat16, device="cuda") for _ in range(L)]
@@ -559,7 +560,7 @@ def run_mla(a, wl):
                    "rope_dim": MLA_DR, "seq_lens": wl["seq_lens"], "page": PAGE,
                    "budget_pages": wl["budget_pages"], "window_pages": wl["window_pages"],
                    "attended_pages": int(m["st"].page_cnt[0, 0].item()),
-                   "parallelism": "single-gpu"},
+                   "mla_rope": a.mla_rope, "parallelism": "single-gpu"},
         "tokens_per_s": round(R * 1e3 / ms, 2),
         "achieved_GBps": round(sparse_bytes / (ms * 1e-3) / 1e9, 1),
         "step_algorithmic_bytes": sparse_bytes,
@@ -569,7 +570,8 @@ def run_mla(a, wl):
                      "frac": round(score_gbps / HBM_PEAK_GBPS, 4),
                      "avg_launch_us": round(score_us, 3),
                      "bytes_per_launch": by["score_per_launch"],
-                     "traffic": scorer_traffic(a.workload),
+                     # the committed PMC traffic is the default (exact-key) scorer's
+                     "traffic": scorer_traffic(a.workload) if a.mla_rope == "exact" else None,
                      "stream_read_same_bytes_us": round(stream_us, 3),
                      "frac_of_stream_read": round(stream_us / score_us, 4)},
         "cpu_baseline": cpu,
@@ -661,6 +663,8 @@ def main():
     ap.add_argument("--budget-pages", type=int, default=126)
     ap.add_argument("--summaries", default="build", choices=["build", "copy"])
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--mla-rope", default="exact", choices=["exact", "int8"],
+                    help="MLA scorer RoPE term: int8 RoPE summary or the exact cache keys")
     ap.add_argument("--no-dense", action="store_true")
     ap.add_argument("--no-1m", action="store_true",
                     help="default workload only: skip the GLM-4-9B 1M north-star point")

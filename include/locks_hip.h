@@ -41,7 +41,7 @@
 
 #include <stdint.h>
 
-#define LOCKS_ABI_VERSION 7
+#define LOCKS_ABI_VERSION 8
 
 #ifdef __cplusplus
 extern "C" {
@@ -388,7 +388,10 @@ int32_t locks_calib_read(const void* src, int64_t bytes, uint32_t* sink, void* s
  * latent cache (num_blocks, page, 576) bf16.  Summaries are the rki4 record
  * of the latent block built by locks_build_rki4 with head_dim 512, n_kv 1
  * (v4 (NB,1,8,256), vs (NB,1,8), c8 (NB,1,16,8), cs (NB,1,16), mu8 (NB,1,512),
- * mus (NB,1)); the RoPE keys are read from the cache.  Selection reuses
+ * mus (NB,1)).  The RoPE term reads either the exact bf16 keys from the
+ * cache or the int8 RoPE summary built by locks_mla_build_rope (rk8
+ * (NB,16,64) int8, rks (NB,16) bf16: 1056 B per page instead of 2048 B).
+ * Selection reuses
  * locks_derive_params (budget_abs = budget_pages - sink - window) and
  * locks_select_nrm_topb (n_kv 1, G 1, combine 1 = max), which together
  * equal the reference's topb_middle (selection/mla_score_torch.py:51-73).
@@ -401,7 +404,10 @@ int32_t locks_calib_read(const void* src, int64_t bytes, uint32_t* sink, void* s
  *   score[r][p] = scale * max_{h < n_heads, t} (q_c8[h] . khat_t + q_rope[h] . k_rope_t)
  * for pages p < n_sel_hi[r] (full pages; written there only), where q_c is
  * int8-quantized per head and khat_t = mu + C_t V^T is the summary's
- * reconstruction of token t.
+ * reconstruction of token t.  With rk8 / rks (both non-NULL) the RoPE term
+ * is (qr8[h] . rk8_t) qrs[h] rks_t, q_rope int8-quantized per head like q_c
+ * (absmax / 127), and the cache is not read (it may be NULL); with both NULL
+ * it is q_rope[h] . k_rope_t on the cache's exact bf16 keys.
  *   q      (n_req, n_heads, 576) bf16, strides (q_stride_req, q_stride_head, 1)
  *   score  (n_req, score_stride) f32
  *   chunk  pages per workgroup (even, <= 1024; locks_mla_score_auto_chunk)
@@ -409,6 +415,7 @@ int32_t locks_calib_read(const void* src, int64_t bytes, uint32_t* sink, void* s
 int32_t locks_mla_score(const uint16_t* q, int64_t q_stride_req, int64_t q_stride_head,
                         const uint8_t* v4, const uint16_t* vs, const int8_t* c8,
                         const uint16_t* cs, const int8_t* mu8, const uint16_t* mus,
+                        const int8_t* rk8, const uint16_t* rks,
                         const uint16_t* cache, int64_t c_stride_block, int64_t c_stride_tok,
                         int32_t num_blocks, const int32_t* block_table, int64_t bt_stride,
                         int32_t bt_cols, const int32_t* n_sel_hi, float* score,
@@ -416,6 +423,22 @@ int32_t locks_mla_score(const uint16_t* q, int64_t q_stride_req, int64_t q_strid
                         int32_t n_heads, int32_t kv_lora_rank, int32_t rope_dim, int32_t page,
                         float scale, void* stream);
 int32_t locks_mla_score_auto_chunk(int32_t n_req, int32_t max_pages);
+
+/*
+ * int8 RoPE summary of the listed physical blocks (ids outside
+ * [0, num_blocks) are skipped; with n_blocks_dev non-NULL only the first
+ * min(n_blocks, *n_blocks_dev) ids, read on the device): per token t of block b,
+ *   rks[b][t] = bf16(max(max_d |k_rope[t][d]| / 127, 1e-8))
+ *   rk8[b][t][d] = clamp(rint(k_rope[t][d] / that scale before rounding), +-127)
+ * (the rki4 token-scale rule).  No reference counterpart: the reference
+ * scores MLA pages with the exact RoPE keys (selection/mla_score_torch.py:41);
+ * this summary halves the scorer's RoPE bytes.
+ *   cache (num_blocks, 16, 576) bf16; rk8 (num_blocks, 16, 64) int8, contiguous;
+ *   rks (num_blocks, 16) bf16, contiguous
+ */
+int32_t locks_mla_build_rope(const uint16_t* cache, int64_t c_stride_block, int64_t c_stride_tok,
+                             int32_t num_blocks, const int32_t* blocks, int32_t n_blocks,
+                             const int32_t* n_blocks_dev, int8_t* rk8, uint16_t* rks, void* stream);
 
 /*
  * Split-K sparse decode over the selected latent pages.  Replaces the

@@ -16,12 +16,16 @@
 // locks_build_rki4) -- the reference keeps fp32 factors Lf, Rf instead
 // (mla_select.py:69-108), larger than the page itself; the RoPE keys are
 // read exact (bf16) straight from the cache.  Per (page): 2738 B of summary
-// + 2048 B of RoPE keys.
+// + 2048 B of RoPE keys.  With the int8 RoPE summary (rk8: per token 64
+// int8 keys, rks: one bf16 scale, absmax / 127 -- 1056 B per page) the
+// scorer reads 3794 B per page, and q_rope is int8-quantized per head like
+// q_c, so the RoPE term is one i8 matrix-core dot per page.
 //
 //   tok[h][t] = cs_t sum_c c8[t][c] qt[h][c] + mud[h] + q_rope[h] . k_rope[t]
 //   qt[h][c]  = (sum_d V4[c][d] q8[h][d]) qs[h] vs[c]
 //   mud[h]    = (sum_d mu8[d] q8[h][d]) qs[h] mus
 //   score[p]  = scale * max_{h < H, t} tok[h][t]
+//   (int8 RoPE summary: q_rope[h] . k_rope[t] -> (qr8[h] . rk8[t]) qrs[h] rks[t])
 #include "locks_common.h"
 #include "locks_hip.h"
 
@@ -48,9 +52,18 @@ constexpr int MS_C8 = MS_MU + 1024;          // 2 x 128 coefficients
 constexpr int MS_CS = MS_C8 + 256;           // 2 x 32 token scales
 constexpr int MS_VS = MS_CS + 64;            // 2 x 16 column scales
 constexpr int MS_MUS = MS_VS + 32;           // 2 dwords: centroid scales (bf16 in the low half)
-constexpr int MS_RP = MS_MUS + 16;           // 2 x 16 x 144 B RoPE keys
-constexpr int MS_MD = MS_RP + 32 * MS_RROWB; // 2 x 16 fp32 centroid terms
-constexpr int MS_BYTES = MS_MD + 128;
+constexpr int MS_RP = MS_MUS + 16;           // 2 x 16 RoPE key rows
+// RoPE rows: exact bf16 keys (128 B, padded to 144) or int8 keys (64 B,
+// padded to 80: 16 rows at 80-B stride read 16 B each on distinct banks)
+// plus the two pages' bf16 token scales
+template <bool RQ>
+struct MsGeom {
+    static constexpr int RROWB = RQ ? 80 : MS_RROWB;
+    static constexpr int RS = MS_RP + 32 * RROWB;        // RQ: 2 x 16 bf16 key scales
+    static constexpr int MD = RS + (RQ ? 64 : 0);        // 2 x 16 fp32 centroid terms
+    static constexpr int BYTES = MD + 128;
+};
+constexpr int ML_RK_BLOCK = ML_PG * ML_DR;   // int8 RoPE keys per block (1024 B)
 
 __device__ __forceinline__ v4i perm_even_odd(const uint4 n) {
     // 16 int8 in d order -> even d of the window first, then odd d (the
@@ -69,11 +82,15 @@ __device__ __forceinline__ uint4 ld_nt16(const void* p) {
 // ---------------------------------------------------------------------------
 // latent page scorer: grid (chunks, requests), 4 waves; unit = 2 pages
 // ---------------------------------------------------------------------------
+// RQ: RoPE term from the int8 RoPE summary (rk8, rks) with int8 q_rope;
+// else from the exact bf16 keys of the cache with bf16 q_rope.
+template <bool RQ>
 __global__ __launch_bounds__(ML_BLK) void mla_score_kernel(
     const uint16_t* __restrict__ q, long q_sr, long q_sh,
     const uint8_t* __restrict__ v4, const uint16_t* __restrict__ vs,
     const int8_t* __restrict__ c8, const uint16_t* __restrict__ cs,
     const int8_t* __restrict__ mu8, const uint16_t* __restrict__ mus,
+    const int8_t* __restrict__ rk8, const uint16_t* __restrict__ rks,
     const uint16_t* __restrict__ cache, long c_sb, long c_st,
     int NB, const int* __restrict__ bt, long bt_sr, int bt_cols,
     const int* __restrict__ nsh, float* __restrict__ score, long sc_sr, int MP,
@@ -87,10 +104,12 @@ __global__ __launch_bounds__(ML_BLK) void mla_score_kernel(
     if (c0 >= c1) return;
 
     __shared__ __attribute__((aligned(16))) int8_t q8s[ML_H + 1][ML_D];   // row 16 = zeros
-    __shared__ __attribute__((aligned(16))) uint16_t qrs[ML_H][ML_DR];
+    using GM = MsGeom<RQ>;
+    __shared__ __attribute__((aligned(16))) uint16_t qrs[ML_H][ML_DR];   // bf16 q_rope (RQ: int8 in the first half)
     __shared__ float qss[ML_H];
+    __shared__ float qrss[ML_H];                                        // RQ: q_rope scale per head
     __shared__ int bt_l[ML_MAX_CHUNK];
-    __shared__ __attribute__((aligned(16))) uint8_t stage_l[ML_WAVES][MS_BYTES];
+    __shared__ __attribute__((aligned(16))) uint8_t stage_l[ML_WAVES][GM::BYTES];
 
     // ---- prologue: q rows of this wave's heads and the block ids in one
     // round trip; the first unit's summary loads are issued before q is
@@ -104,9 +123,15 @@ __global__ __launch_bounds__(ML_BLK) void mla_score_kernel(
         qw[i] = qrw[i] = make_uint4(0u, 0u, 0u, 0u);
         if (h < H) {
             qw[i] = *reinterpret_cast<const uint4*>(qh + 8 * lane);
-            if (lane < ML_DR / 8) qrw[i] = *reinterpret_cast<const uint4*>(qh + ML_D + 8 * lane);
+            if (!RQ && lane < ML_DR / 8) qrw[i] = *reinterpret_cast<const uint4*>(qh + ML_D + 8 * lane);
         }
     }
+    // RQ: the wave's QH q_rope rows side by side, lane l < 8 QH holding dims
+    // 8 (l & 7) .. of head wave + QH (l >> 3)
+    const int hr = wave + ML_WAVES * (lane >> 3);
+    const bool hr_ok = RQ && lane < 8 * QH && hr < H;
+    uint4 qrw8 = make_uint4(0u, 0u, 0u, 0u);
+    if (hr_ok) qrw8 = *reinterpret_cast<const uint4*>(q + (long)r * q_sr + (long)hr * q_sh + ML_D + 8 * (lane & 7));
     for (int i = tid; i < c1 - c0; i += ML_BLK) {
         const int b = bt[(long)r * bt_sr + min(c0 + i, bt_cols - 1)];
         bt_l[i] = min(max(b, 0), NB - 1);
@@ -115,7 +140,7 @@ __global__ __launch_bounds__(ML_BLK) void mla_score_kernel(
     __syncthreads();
     const int r16 = lane & 15, kg = lane >> 4;
     const int n_units = cdiv(c1 - c0, 2);
-    uint4 fv0, fv1, fv2, fv3, fmu, fc8, fcs, fvs, fr0, fr1, fr2, fr3;
+    uint4 fv0, fv1, fv2, fv3, fmu, fc8, fcs, fvs, fr0, fr1, fr2, fr3, frs;
     uint32_t fmus = 0u;
     // natural-order (coalesced) loads of unit u into registers
     auto load_unit = [&](int u) {
@@ -133,11 +158,20 @@ __global__ __launch_bounds__(ML_BLK) void mla_score_kernel(
         fcs = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(cs) + blk_of((lane >> 1) & 1) * (ML_PG * 2) + (lane & 1) * 16);
         fvs = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(vs) + blk_of(lane & 1) * (ML_RNK * 2));
         fmus = (uint32_t)mus[blk_of(lane & 1)];
-        // RoPE chunk i = (page i >> 7, token (i >> 3) & 15, 16-byte part i & 7)
-        auto rload = [&](int i) {
-            return ld_nt16(cache + blk_of(i >> 7) * c_sb + (long)((i >> 3) & 15) * c_st + ML_D + 8 * (i & 7));
-        };
-        fr0 = rload(lane); fr1 = rload(lane + 64); fr2 = rload(lane + 128); fr3 = rload(lane + 192);
+        if constexpr (RQ) {
+            // int8 key chunk i = (page i >> 6, 16-byte part i & 63 of the
+            // page's 1024 B); key scales: 16-byte part lane & 1 of page
+            // (lane >> 1) & 1
+            auto rload = [&](int i) { return ld_nt16(rk8 + blk_of(i >> 6) * ML_RK_BLOCK + (i & 63) * 16); };
+            fr0 = rload(lane); fr1 = rload(lane + 64);
+            frs = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(rks) + blk_of((lane >> 1) & 1) * (ML_PG * 2) + (lane & 1) * 16);
+        } else {
+            // RoPE chunk i = (page i >> 7, token (i >> 3) & 15, 16-byte part i & 7)
+            auto rload = [&](int i) {
+                return ld_nt16(cache + blk_of(i >> 7) * c_sb + (long)((i >> 3) & 15) * c_st + ML_D + 8 * (i & 7));
+            };
+            fr0 = rload(lane); fr1 = rload(lane + 64); fr2 = rload(lane + 128); fr3 = rload(lane + 192);
+        }
     };
     auto store_unit = [&](uint8_t* st) {
         // V chunk i: page i >> 7, column (i >> 4) & 7, 16-byte part i & 15
@@ -153,32 +187,49 @@ __global__ __launch_bounds__(ML_BLK) void mla_score_kernel(
             *reinterpret_cast<uint4*>(st + MS_VS + lane * 16) = fvs;
             *reinterpret_cast<uint32_t*>(st + MS_MUS + lane * 4) = fmus;
         }
-        // RoPE chunk i: (page, token) row i >> 3, 16-byte part i & 7
-        auto rofs = [&](int i) { return MS_RP + (i >> 3) * MS_RROWB + (i & 7) * 16; };
-        *reinterpret_cast<uint4*>(st + rofs(lane)) = fr0;
-        *reinterpret_cast<uint4*>(st + rofs(lane + 64)) = fr1;
-        *reinterpret_cast<uint4*>(st + rofs(lane + 128)) = fr2;
-        *reinterpret_cast<uint4*>(st + rofs(lane + 192)) = fr3;
+        if constexpr (RQ) {
+            // int8 key chunk i: (page, token) row i >> 2, 16-byte part i & 3
+            auto rofs = [&](int i) { return MS_RP + (i >> 2) * GM::RROWB + (i & 3) * 16; };
+            *reinterpret_cast<uint4*>(st + rofs(lane)) = fr0;
+            *reinterpret_cast<uint4*>(st + rofs(lane + 64)) = fr1;
+            if (lane < 4) *reinterpret_cast<uint4*>(st + GM::RS + lane * 16) = frs;
+        } else {
+            // RoPE chunk i: (page, token) row i >> 3, 16-byte part i & 7
+            auto rofs = [&](int i) { return MS_RP + (i >> 3) * MS_RROWB + (i & 7) * 16; };
+            *reinterpret_cast<uint4*>(st + rofs(lane)) = fr0;
+            *reinterpret_cast<uint4*>(st + rofs(lane + 64)) = fr1;
+            *reinterpret_cast<uint4*>(st + rofs(lane + 128)) = fr2;
+            *reinterpret_cast<uint4*>(st + rofs(lane + 192)) = fr3;
+        }
     };
 
     load_unit(min(wave, n_units - 1));          // every lane loads (exact wait counts)
-#pragma unroll
-    for (int i = 0; i < QH; ++i) {
-        const int h = wave + ML_WAVES * i;
+    // int8 round trip of one head's row, 8 values per lane: qs = max(absmax,
+    // 1e-8) / 127 over the wave, v = rint(a / qs) with the correctly rounded
+    // quotient: a * (1 / qs) is within 2 ulp of it and decides the rounding
+    // unless it lies within 2^-15 of a half-integer; those (rare) lanes redo
+    // the division.  Returns qs; packs the 8 values (zeros when !valid).
+    // g8: the row is 8 lanes wide (absmax over each 8-lane group) instead
+    // of the whole wave
+    auto quant8 = [&](const uint4 w, bool valid, uint32_t (&pk)[2], bool g8) -> float {
         float a[8];
         {
-            const uint32_t ws[4] = {qw[i].x, qw[i].y, qw[i].z, qw[i].w};
+            const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
             for (int e = 0; e < 4; ++e) { a[2 * e] = bf16lo(ws[e]); a[2 * e + 1] = bf16hi(ws[e]); }
         }
         float am = 0.f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) am = fmaxf(am, fabsf(a[e]));
-        am = wave_max(am);
+        if (g8) {
+            // quad swaps, then the half-row mirror (lane j <-> 7 - j of 8)
+            am = fmaxf(am, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(am), 0xB1, 0xF, 0xF, false)));
+            am = fmaxf(am, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(am), 0x4E, 0xF, 0xF, false)));
+            am = fmaxf(am, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(am), 0x141, 0xF, 0xF, false)));
+        } else {
+            am = wave_max(am);
+        }
         const float qs = fmaxf(am, 1e-8f) / 127.f;
-        // rint(a / qs) with the correctly rounded quotient: a * (1 / qs) is
-        // within 2 ulp of it and decides the rounding unless it lies within
-        // 2^-15 of a half-integer; those (rare) lanes redo the division
         const float inv = 1.f / qs;
         int iv[8];
         bool near = false;
@@ -195,15 +246,34 @@ __global__ __launch_bounds__(ML_BLK) void mla_score_kernel(
                 for (int e = 0; e < 8; ++e) iv[e] = (int)rintf(__fdiv_rn(a[e], qs));
             }
         }
-        uint32_t pk[2] = {0u, 0u};
+        pk[0] = pk[1] = 0u;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const int v = (h < H) ? iv[e] : 0;
+            const int v = valid ? iv[e] : 0;
             pk[e >> 2] |= ((uint32_t)(uint8_t)v) << (8 * (e & 3));
         }
+        return qs;
+    };
+#pragma unroll
+    for (int i = 0; i < QH; ++i) {
+        const int h = wave + ML_WAVES * i;
+        uint32_t pk[2];
+        const float qs = quant8(qw[i], h < H, pk, false);
         *reinterpret_cast<uint2*>(&q8s[h][8 * lane]) = make_uint2(pk[0], pk[1]);
-        if (lane < ML_DR / 8) *reinterpret_cast<uint4*>(&qrs[h][8 * lane]) = qrw[i];
+        if constexpr (!RQ) {
+            if (lane < ML_DR / 8) *reinterpret_cast<uint4*>(&qrs[h][8 * lane]) = qrw[i];
+        }
         if (lane == 0) qss[h] = (h < H) ? qs : 0.f;
+    }
+    if constexpr (RQ) {
+        // q_rope: the same round trip over each head's 64 dims, the wave's
+        // QH heads at once
+        uint32_t pr[2];
+        const float qsr = quant8(qrw8, hr_ok, pr, true);
+        if (lane < 8 * QH) {
+            *reinterpret_cast<uint2*>(reinterpret_cast<int8_t*>(&qrs[hr][0]) + 8 * (lane & 7)) = make_uint2(pr[0], pr[1]);
+            if ((lane & 7) == 0) qrss[hr] = hr_ok ? qsr : 0.f;
+        }
     }
     __syncthreads();
     const uint32_t MH = 0xF0F0F0F0u;
@@ -218,10 +288,21 @@ __global__ __launch_bounds__(ML_BLK) void mla_score_kernel(
             Bq[k4][1] = perm_even_odd(*reinterpret_cast<const uint4*>(&q8s[hrow][128 * k4 + 32 * kg + 16]));
         }
     }
+    // RoPE B operand: exact form, bf16 q_rope of head r16 (k-step s, slot
+    // kg: dims 32 s + 8 kg ..); int8 form, lane group kg holds dims
+    // 16 kg .. 16 kg + 15 of head r16 (the same dims as the A rows' bytes)
     v8bf Br[2];
+    v4i Br8 = {0, 0, 0, 0};
+    float qrsj = 0.f;
+    if constexpr (RQ) {
+        const uint4 w = *reinterpret_cast<const uint4*>(reinterpret_cast<const int8_t*>(&qrs[r16][0]) + 16 * kg);
+        Br8 = v4i{(int)w.x, (int)w.y, (int)w.z, (int)w.w};
+        qrsj = qrss[r16];
+    } else {
 #pragma unroll
-    for (int s = 0; s < 2; ++s)
-        Br[s] = __builtin_bit_cast(v8bf, *reinterpret_cast<const uint4*>(&qrs[r16][32 * s + 8 * kg]));
+        for (int s = 0; s < 2; ++s)
+            Br[s] = __builtin_bit_cast(v8bf, *reinterpret_cast<const uint4*>(&qrs[r16][32 * s + 8 * kg]));
+    }
     const float qsj = qss[r16];
     const bool col_ok = r16 < H;
 
@@ -267,7 +348,7 @@ __global__ __launch_bounds__(ML_BLK) void mla_score_kernel(
             }
         }
         // centroid term of (page v, head r16) lives in lanes kg = 0, v = 0/1
-        float* md = reinterpret_cast<float*>(st + MS_MD);
+        float* md = reinterpret_cast<float*>(st + GM::MD);
         if (kg == 0) {
 #pragma unroll
             for (int v = 0; v < 2; ++v) {
@@ -288,11 +369,23 @@ __global__ __launch_bounds__(ML_BLK) void mla_score_kernel(
                 tk = __builtin_amdgcn_mfma_f32_16x16x4f32(a, qt[2 * hh + pg], tk, 0, 0, 0);
             }
             v4f rp = {0.f, 0.f, 0.f, 0.f};
+            if constexpr (RQ) {
+                // rows = the page's 16 tokens, 16 int8 dims per lane group
+                const uint4 w = *reinterpret_cast<const uint4*>(st + MS_RP + (pg * 16 + r16) * GM::RROWB + 16 * kg);
+                const v4i ri = __builtin_amdgcn_mfma_i32_16x16x64_i8(v4i{(int)w.x, (int)w.y, (int)w.z, (int)w.w},
+                                                                     Br8, v4i{0, 0, 0, 0}, 0, 0, 0);
+                const uint2 rsw = *reinterpret_cast<const uint2*>(st + GM::RS + pg * 32 + kg * 8);
+                rp[0] = (float)ri[0] * qrsj * bf16lo(rsw.x);
+                rp[1] = (float)ri[1] * qrsj * bf16hi(rsw.x);
+                rp[2] = (float)ri[2] * qrsj * bf16lo(rsw.y);
+                rp[3] = (float)ri[3] * qrsj * bf16hi(rsw.y);
+            } else {
 #pragma unroll
-            for (int s = 0; s < 2; ++s) {
-                const v8bf a = __builtin_bit_cast(v8bf, *reinterpret_cast<const uint4*>(
-                    st + MS_RP + (pg * 16 + r16) * MS_RROWB + (32 * s + 8 * kg) * 2));
-                rp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, Br[s], rp, 0, 0, 0);
+                for (int s = 0; s < 2; ++s) {
+                    const v8bf a = __builtin_bit_cast(v8bf, *reinterpret_cast<const uint4*>(
+                        st + MS_RP + (pg * 16 + r16) * MS_RROWB + (32 * s + 8 * kg) * 2));
+                    rp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, Br[s], rp, 0, 0, 0);
+                }
             }
             const uint2 csw = *reinterpret_cast<const uint2*>(st + MS_CS + pg * 32 + kg * 8);
             const float mud = md[pg * 16 + r16];
@@ -306,6 +399,48 @@ __global__ __launch_bounds__(ML_BLK) void mla_score_kernel(
         }
         wave_lds_sync();                                 // stage reused by the next unit
     }
+}
+
+// ---------------------------------------------------------------------------
+// int8 RoPE summary of listed blocks: one wave per block, lane = (token
+// lane >> 2, 16 dims 16 (lane & 3) ..); per token scale = max(absmax / 127,
+// 1e-8) (the rki4 token-scale rule), key = clamp(rint(k / scale), +-127),
+// scale stored as bf16
+// ---------------------------------------------------------------------------
+constexpr int MR_WAVES = 4;
+__global__ __launch_bounds__(MR_WAVES * kWave) void mla_rope_quant_kernel(
+    const uint16_t* __restrict__ cache, long c_sb, long c_st, int NB,
+    const int* __restrict__ blocks, int n, const int* __restrict__ n_dev, int8_t* __restrict__ rk8,
+    uint16_t* __restrict__ rks)
+{
+    const int i = blockIdx.x * MR_WAVES + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (n_dev) n = min(n, *n_dev);                                 // device-side count
+    if (i >= n) return;
+    const int b = blocks[i];
+    if (b < 0 || b >= NB) return;                                  // skipped id
+    const int t = lane >> 2, part = lane & 3;
+    const uint16_t* src = cache + (long)b * c_sb + (long)t * c_st + ML_D + 16 * part;
+    const uint4 w0 = *reinterpret_cast<const uint4*>(src);
+    const uint4 w1 = *reinterpret_cast<const uint4*>(src + 8);
+    const uint32_t ws[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+    float x[16];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) { x[2 * e] = bf16lo(ws[e]); x[2 * e + 1] = bf16hi(ws[e]); }
+    float am = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) am = fmaxf(am, fabsf(x[e]));
+    am = fmaxf(am, __shfl_xor(am, 1));
+    am = fmaxf(am, __shfl_xor(am, 2));
+    const float sc = fmaxf(__fdiv_rn(am, 127.f), 1e-8f);
+    uint32_t pk[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        const int v = (int)fminf(fmaxf(rintf(__fdiv_rn(x[e], sc)), -127.f), 127.f);
+        pk[e >> 2] |= ((uint32_t)(uint8_t)v) << (8 * (e & 3));
+    }
+    *reinterpret_cast<uint4*>(rk8 + (long)b * ML_RK_BLOCK + t * ML_DR + 16 * part) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+    if (part == 0) rks[(long)b * ML_PG + t] = f32_to_bf16(sc);
 }
 
 // ---------------------------------------------------------------------------
@@ -651,7 +786,8 @@ using namespace locks;
 extern "C" int32_t locks_mla_score(
     const uint16_t* q, int64_t q_stride_req, int64_t q_stride_head,
     const uint8_t* v4, const uint16_t* vs, const int8_t* c8, const uint16_t* cs,
-    const int8_t* mu8, const uint16_t* mus, const uint16_t* cache, int64_t c_stride_block,
+    const int8_t* mu8, const uint16_t* mus, const int8_t* rk8, const uint16_t* rks,
+    const uint16_t* cache, int64_t c_stride_block,
     int64_t c_stride_tok, int32_t num_blocks, const int32_t* block_table, int64_t bt_stride,
     int32_t bt_cols, const int32_t* n_sel_hi, float* score, int64_t score_stride,
     int32_t max_pages, int32_t chunk, int32_t n_req, int32_t n_heads, int32_t kv_lora_rank,
@@ -667,16 +803,39 @@ extern "C" int32_t locks_mla_score(
                   "locks_mla_score: chunk %d must be even in [2, %d]", chunk, ML_MAX_CHUNK);
     LOCKS_REQUIRE(q_stride_head % 8 == 0 && q_stride_req % 8 == 0 && c_stride_tok % 8 == 0 &&
                   c_stride_block % 8 == 0, "locks_mla_score: strides must be multiples of 8 elements");
-    LOCKS_REQUIRE(q && v4 && vs && c8 && cs && mu8 && mus && cache && block_table && n_sel_hi && score,
+    LOCKS_REQUIRE((rk8 == nullptr) == (rks == nullptr),
+                  "locks_mla_score: rk8 and rks must both be given (int8 RoPE summary) or both NULL");
+    LOCKS_REQUIRE(q && v4 && vs && c8 && cs && mu8 && mus && (rk8 || cache) && block_table && n_sel_hi && score,
                   "locks_mla_score: null pointer argument");
     if (n_req == 0) return 0;
     const int Z = cdiv(max_pages, chunk);
-    hipLaunchKernelGGL(mla_score_kernel, dim3(Z, n_req), dim3(ML_BLK), 0, (hipStream_t)stream, q,
-                       (long)q_stride_req, (long)q_stride_head, v4, vs, c8, cs, mu8, mus, cache,
-                       (long)c_stride_block, (long)c_stride_tok, num_blocks, block_table,
-                       (long)bt_stride, bt_cols, n_sel_hi, score, (long)score_stride, max_pages,
-                       n_heads, scale, chunk);
+#define LAUNCH_RQ(RQ)                                                                               \
+    hipLaunchKernelGGL(mla_score_kernel<RQ>, dim3(Z, n_req), dim3(ML_BLK), 0, (hipStream_t)stream, q, \
+                       (long)q_stride_req, (long)q_stride_head, v4, vs, c8, cs, mu8, mus, rk8, rks,  \
+                       cache, (long)c_stride_block, (long)c_stride_tok, num_blocks, block_table,     \
+                       (long)bt_stride, bt_cols, n_sel_hi, score, (long)score_stride, max_pages,     \
+                       n_heads, scale, chunk)
+    if (rk8) LAUNCH_RQ(true);
+    else LAUNCH_RQ(false);
+#undef LAUNCH_RQ
     return check_launch("mla_score_kernel");
+}
+
+extern "C" int32_t locks_mla_build_rope(const uint16_t* cache, int64_t c_stride_block,
+                                        int64_t c_stride_tok, int32_t num_blocks,
+                                        const int32_t* blocks, int32_t n_blocks,
+                                        const int32_t* n_blocks_dev, int8_t* rk8, uint16_t* rks,
+                                        void* stream)
+{
+    LOCKS_REQUIRE(num_blocks >= 1 && n_blocks >= 0, "locks_mla_build_rope: bad geometry");
+    LOCKS_REQUIRE(c_stride_tok % 8 == 0 && c_stride_block % 8 == 0,
+                  "locks_mla_build_rope: strides must be multiples of 8 elements");
+    LOCKS_REQUIRE(cache && blocks && rk8 && rks, "locks_mla_build_rope: null pointer argument");
+    if (n_blocks == 0) return 0;
+    hipLaunchKernelGGL(mla_rope_quant_kernel, dim3(cdiv(n_blocks, MR_WAVES)), dim3(MR_WAVES * kWave), 0,
+                       (hipStream_t)stream, cache, (long)c_stride_block, (long)c_stride_tok, num_blocks,
+                       blocks, n_blocks, n_blocks_dev, rk8, rks);
+    return check_launch("mla_rope_quant_kernel");
 }
 
 extern "C" int32_t locks_mla_score_auto_chunk(int32_t n_req, int32_t max_pages) {

@@ -10,7 +10,7 @@ import ctypes
 import os
 
 _LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "liblocks_hip.so")
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 _c = ctypes
 _i32, _i64, _f32, _f64, _p = _c.c_int32, _c.c_int64, _c.c_float, _c.c_double, _c.c_void_p
@@ -43,10 +43,11 @@ SIGNATURES = {
                                        _i32, _i32, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p]),
     "locks_calib_read": (_i32, [_p, _i64, _p, _p]),
     "locks_pack_rki4": (_i32, [_p, _p, _p, _p, _p, _i32, _i32, _i32, _p, _p, _p, _p, _p, _p, _p, _p]),
-    "locks_mla_score": (_i32, [_p, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _p,
+    "locks_mla_score": (_i32, [_p, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _p,
                                _i64, _i32, _p, _p, _i64, _i32, _i32, _i32, _i32, _i32, _i32,
                                _i32, _f32, _p]),
     "locks_mla_score_auto_chunk": (_i32, [_i32, _i32]),
+    "locks_mla_build_rope": (_i32, [_p, _i64, _i64, _i32, _p, _i32, _p, _p, _p, _p]),
     "locks_mla_decode_splitk": (_i32, [_p, _i64, _i64, _p, _i64, _i64, _i32, _p, _i64, _i32, _p,
                                        _i64, _i32, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32,
                                        _i32, _i32, _i32, _f32, _p]),

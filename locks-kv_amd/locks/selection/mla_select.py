@@ -32,9 +32,10 @@ def _split_cache(kv_cache):
 
 @torch.no_grad()
 def mla_build_blocks(st, layer: int, kv_cache, blocks) -> int:
-    """(Re)build the latent summaries of the listed physical blocks of one
-    layer (the reference's per-sequence factor build, mla_select.py:69-108,
-    replaced by the block-keyed rki4 latent record)."""
+    """(Re)build the latent summaries (and, for an int8-RoPE state, the int8
+    RoPE summary) of the listed physical blocks of one layer (the reference's
+    per-sequence factor build, mla_select.py:69-108, replaced by the
+    block-keyed rki4 latent record)."""
     cache, sb, stt = _split_cache(kv_cache)
     b = blocks.to(device=cache.device, dtype=torch.int32).contiguous()
     n = int(b.numel())
@@ -47,6 +48,11 @@ def mla_build_blocks(st, layer: int, kv_cache, blocks) -> int:
         st.page, _lib.ptr(v4), _lib.ptr(vs), _lib.ptr(c8), _lib.ptr(cs), _lib.ptr(mu8),
         _lib.ptr(mus), _lib.rows_arg(st), _lib.ptr(tag), _lib.stream_ptr(cache.device)),
         "build_rki4 (latent)")
+    rk8, rks = st.rope_state(layer)
+    if rk8 is not None:
+        _lib.check(lib.locks_mla_build_rope(
+            _lib.ptr(cache), sb, stt, int(min(st.NB, cache.shape[0])), _lib.ptr(b), n, None,
+            _lib.ptr(rk8), _lib.ptr(rks), _lib.stream_ptr(cache.device)), "mla_build_rope")
     return n
 
 
@@ -67,10 +73,12 @@ def mla_score_only(st, layer: int, q, kv_cache, block_table, n_req: int, scale: 
     _check_i32("block_table", block_table)
     cache, sb, stt = _split_cache(kv_cache)
     v4, vs, c8, cs, mu8, mus, _tag = st.layer_state(layer)
+    rk8, rks = st.rope_state(layer)
     lib = _lib.load()
     _lib.check(lib.locks_mla_score(
         _lib.ptr(q), q.stride(0), q.stride(1), _lib.ptr(v4), _lib.ptr(vs), _lib.ptr(c8),
-        _lib.ptr(cs), _lib.ptr(mu8), _lib.ptr(mus), _lib.ptr(cache), sb, stt,
+        _lib.ptr(cs), _lib.ptr(mu8), _lib.ptr(mus), _lib.ptr(rk8), _lib.ptr(rks),
+        _lib.ptr(cache), sb, stt,
         int(min(st.NB, cache.shape[0])), _lib.ptr(block_table), block_table.stride(0),
         int(block_table.shape[1]), _lib.ptr(st.n_sel_hi), _lib.ptr(st.score_h),
         st.score_h.stride(0), int(st.max_pages), int(st.score_chunk), int(n_req), int(q.shape[1]),

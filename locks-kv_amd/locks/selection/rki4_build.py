@@ -160,6 +160,18 @@ def _refresh(st, mode: str, K_layers, block_table, seq_lens, n_req: int, rows=No
         int(st.d), int(st.page), int(st.NB), _lib.ptr(v4), _lib.ptr(vs), _lib.ptr(c8),
         _lib.ptr(cs), _lib.ptr(mu8), _lib.ptr(mus), _lib.rows_arg(st), _lib.ptr(tag), stream),
         "build_rki4_layers")
+    if getattr(st, "pp_rk8", None) is not None:
+        # MLA state with the int8 RoPE summary: the latent views start at the
+        # cache rows, whose RoPE keys follow the latent ([kv_c | k_pe] rows,
+        # backend/mla_attn.py:100-101); same device block list and count
+        if K0.shape[-1] != st.D or K0.stride(1) < st.D + st.Dr:
+            raise TypeError("MLA K_layers must be the (NB, page, 1, kv_lora_rank) latent views "
+                            "of (NB, page, kv_lora_rank + rope_dim) cache rows")
+        for layer, K in enumerate(K_layers):
+            _lib.check(lib.locks_mla_build_rope(
+                _lib.ptr(K), K.stride(0), K.stride(1), nb, _lib.ptr(st.refresh_blocks), bound,
+                _lib.ptr(st.refresh_count), _lib.ptr(st.pp_rk8[layer]), _lib.ptr(st.pp_rks[layer]),
+                stream), "mla_build_rope")
     return bound
 
 

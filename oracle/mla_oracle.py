@@ -26,9 +26,16 @@ Two things are restated here (paths relative to the reference package
      mla_score_rki4       tok[h][t] = (q8.mu8)qs mus + cs_t sum_c c8[t][c]
                           (sum_d V4[c][d] q8[h][d]) qs vs_c + q_rope[h].k_rope[t]
                           page score = scale * max_{h, t} tok[h][t]
-   The reference ships no latent rki4 format (this layout is new: the
-   reference scores with fp32 factors, mla_select.py:69-108); the max-union
-   score, the budget rule and the attention are the reference's.
+     mla_build_rope       int8 RoPE summary: per token scale max(absmax/127,
+                          1e-8) (the rki4 token-scale rule, rki4_build.py's
+                          C8 quantisation), keys rint(k / scale) clipped to
+                          +-127, scale stored as bf16
+     mla_score_rki4(rope=) RoPE term (qr8[h].rk8[t]) qrs[h] rks[t] with
+                          q_rope int8-quantized per head like q_c
+   The reference ships no latent rki4 format and no RoPE summary (these
+   layouts are new: the reference scores with fp32 factors and the exact
+   keys, mla_select.py:69-108, mla_score_torch.py:41); the max-union score,
+   the budget rule and the attention are the reference's.
 
 Ties: the reference's ``topb_middle`` uses ``torch.topk``, whose order among
 equal scores is unspecified; ``topb_middle`` here breaks ties by the lowest
@@ -134,18 +141,43 @@ def mla_build_summaries(cache_bf16: np.ndarray, blocks, n_blocks: int, Lkv: int 
     return O.build_state_slabs(lat, np.asarray(blocks), n_blocks)
 
 
-def mla_score_rki4(q_bf16, slabs, cache_bf16, bt, nsh, scale, MP, Lkv=512):
-    """Page score from the latent rki4 summary + exact RoPE keys.
+def mla_build_rope(cache_bf16: np.ndarray, blocks, n_blocks: int, Lkv: int = 512):
+    """int8 RoPE summary of the listed physical blocks (ids outside
+    [0, n_blocks) skipped; unlisted blocks stay zero).  cache_bf16
+    (NB, page, Lkv + Dr) bf16 bits.  Returns dict rk8 (NB, page, Dr) int8,
+    rks (NB, page) bf16 bits."""
+    f32 = np.float32
+    NB, page, HS = cache_bf16.shape
+    Dr = HS - Lkv
+    rk8 = np.zeros((n_blocks, page, Dr), np.int8)
+    rks = np.zeros((n_blocks, page), np.uint16)
+    blk = np.array([b for b in np.asarray(blocks).tolist() if 0 <= b < n_blocks], np.int64)
+    if blk.size:
+        k = O.bf16_to_f32(cache_bf16[blk, :, Lkv:])                      # (n, page, Dr)
+        sc = np.maximum((np.abs(k).max(axis=-1) / f32(127.0)).astype(f32), f32(1e-8))
+        rk8[blk] = np.clip(np.rint(k / sc[..., None]), -127, 127).astype(np.int8)
+        rks[blk] = O.f32_to_bf16(sc)
+    return dict(rk8=rk8, rks=rks)
+
+
+def mla_score_rki4(q_bf16, slabs, cache_bf16, bt, nsh, scale, MP, Lkv=512, rope=None):
+    """Page score from the latent rki4 summary + RoPE keys.
 
     q (R, H, Lkv + Dr) bf16 bits: q_c = q[..., :Lkv] is int8-quantized per
-    head (absmax / 127, as the GQA scorer), q_rope = q[..., Lkv:] is used as
-    bf16.  Returns (R, MP) fp32 for p < nsh[r] (0 elsewhere): scale *
-    max_{h, t} (q_c8[h] . khat[t] + q_rope[h] . k_rope[t]), khat = mu + C V^T."""
+    head (absmax / 127, as the GQA scorer).  rope None: q_rope = q[..., Lkv:]
+    as bf16 against the exact keys of the cache; rope = mla_build_rope(...):
+    q_rope int8-quantized per head the same way, against rk8 * rks.  Returns
+    (R, MP) fp32 for p < nsh[r] (0 elsewhere): scale * max_{h, t}
+    (q_c8[h] . khat[t] + q_rope[h] . k_rope[t]), khat = mu + C V^T."""
     R, H, HS = q_bf16.shape
     NB = slabs["v4"].shape[0]
     q8, qs = O.quantize_q(q_bf16[:, :, :Lkv])
     qc = (q8.astype(np.float64) * qs[..., None].astype(np.float64))     # (R,H,Lkv)
-    qr = O.bf16_to_f32(q_bf16[:, :, Lkv:]).astype(np.float64)          # (R,H,Dr)
+    if rope is None:
+        qr = O.bf16_to_f32(q_bf16[:, :, Lkv:]).astype(np.float64)      # (R,H,Dr)
+    else:
+        qr8, qrs = O.quantize_q(q_bf16[:, :, Lkv:])
+        qr = qr8.astype(np.float64) * qrs[..., None].astype(np.float64)
     out = np.zeros((R, MP), np.float32)
     for r in range(R):
         P = int(nsh[r])
@@ -157,7 +189,10 @@ def mla_score_rki4(q_bf16, slabs, cache_bf16, bt, nsh, scale, MP, Lkv=512):
         Cref = slabs["c8"][blk, 0].astype(np.float64) * O.bf16_to_f32(slabs["cs"][blk, 0])[..., None]
         muref = slabs["mu8"][blk, 0].astype(np.float64) * O.bf16_to_f32(slabs["mus"][blk, 0])[..., None]
         khat = muref[:, None, :] + np.einsum("ptc,pcd->ptd", Cref, Vref)  # (P,page,Lkv)
-        kr = O.bf16_to_f32(cache_bf16[blk, :, Lkv:]).astype(np.float64)  # (P,page,Dr)
+        if rope is None:
+            kr = O.bf16_to_f32(cache_bf16[blk, :, Lkv:]).astype(np.float64)  # (P,page,Dr)
+        else:
+            kr = rope["rk8"][blk].astype(np.float64) * O.bf16_to_f32(rope["rks"][blk])[..., None]
         s = np.einsum("hd,ptd->hpt", qc[r], khat) + np.einsum("hd,ptd->hpt", qr[r], kr)
         out[r, :P] = (s.max(axis=2).max(axis=0) * scale).astype(np.float32)
     return out

@@ -36,22 +36,39 @@ def _dev(c):
                 sl=torch.from_numpy(c["sl"]).cuda())
 
 
-def _state(c, budget, L=1, window=10, sink=1):
+def _state(c, budget, L=1, window=10, sink=1, rope="exact"):
     from locks.selection import MlaState
     return MlaState("cuda", num_layers=L, num_blocks=c["NB"], n_heads=c["H"], max_reqs=c["R"],
-                    max_pages=c["MP"], budget_pages=budget, sink_pages=sink, window_pages=window)
+                    max_pages=c["MP"], budget_pages=budget, sink_pages=sink, window_pages=window,
+                    rope=rope)
 
 
-def _upload_slabs(st, slabs, layer=0):
+def _copy(t, a):
     import torch
+    if a.dtype == np.uint16:
+        t.copy_(torch.from_numpy(a.view(np.int16).copy()).view(torch.bfloat16).reshape(t.shape))
+    else:
+        t.copy_(torch.from_numpy(a.copy()).reshape(t.shape))
+
+
+def _upload_slabs(st, slabs, layer=0, rope=None):
     for k, name in (("v4", "pp_v4"), ("vs", "pp_vs"), ("c8", "pp_c8"), ("cs", "pp_cs"),
                     ("mu8", "pp_mu8"), ("mus", "pp_mus")):
-        a = slabs[k]
-        t = getattr(st, name)[layer]
-        if a.dtype == np.uint16:
-            t.copy_(torch.from_numpy(a.view(np.int16).copy()).view(torch.bfloat16).reshape(t.shape))
-        else:
-            t.copy_(torch.from_numpy(a.copy()).reshape(t.shape))
+        _copy(getattr(st, name)[layer], slabs[k])
+    if st.rope == "int8":
+        assert rope is not None, "an int8-RoPE state needs the oracle's RoPE summary"
+        _copy(st.pp_rk8[layer], rope["rk8"])
+        _copy(st.pp_rks[layer], rope["rks"])
+
+
+def _oracle_summaries(c, st, layer=0):
+    """Oracle latent slabs (+ int8 RoPE summary for an int8-RoPE state) of the
+    case's full blocks, uploaded into st; returns (slabs, rope or None)."""
+    blocks = _blocks_of(c)
+    slabs = M.mla_build_summaries(c["cache"], blocks, c["NB"])
+    rope = M.mla_build_rope(c["cache"], blocks, c["NB"]) if st.rope == "int8" else None
+    _upload_slabs(st, slabs, layer, rope)
+    return slabs, rope
 
 
 def _blocks_of(c):
@@ -61,22 +78,25 @@ def _blocks_of(c):
     return np.array(sorted(set(out)), np.int32)
 
 
+@pytest.mark.parametrize("rope", ["int8", "exact"])
 @pytest.mark.parametrize("seq_lens,H", [([16 * 40 + 5], 16), ([16 * 300, 16 * 77 + 9], 16), ([16 * 50 + 1], 5)])
-def test_mla_score_matches_oracle(seq_lens, H):
+def test_mla_score_matches_oracle(seq_lens, H, rope):
     import torch
     from locks.selection import mla_derive, mla_score_only
-    say("score", seq_lens, H)
+    say("score", seq_lens, H, rope)
     c = _case(11, seq_lens, H)
     d = _dev(c)
-    st = _state(c, budget=32)
-    slabs = M.mla_build_summaries(c["cache"], _blocks_of(c), c["NB"])
-    _upload_slabs(st, slabs)
+    st = _state(c, budget=32, rope=rope)
+    slabs, rs = _oracle_summaries(c, st)
     mla_derive(st, d["sl"], c["R"])
     st.score_h.fill_(123.0)
-    mla_score_only(st, 0, d["q"], d["cache"], d["bt"], c["R"], 0.07)
+    # the int8-RoPE scorer must not read the cache: hand it a cache whose
+    # RoPE keys are garbage (the latent part is unused by the scorer too)
+    cache_arg = d["cache"].clone().fill_(float("nan")) if rope == "int8" else d["cache"]
+    mla_score_only(st, 0, d["q"], cache_arg, d["bt"], c["R"], 0.07)
     torch.cuda.synchronize()
     npg, nsh, b = M.mla_derive(c["sl"], PAGE, 10, 1, 32)
-    ref = M.mla_score_rki4(c["q"], slabs, c["cache"], c["bt"], nsh, 0.07, c["MP"])
+    ref = M.mla_score_rki4(c["q"], slabs, c["cache"], c["bt"], nsh, 0.07, c["MP"], rope=rs)
     got = st.score_h[:, 0, 0, :].cpu().numpy()
     for r in range(c["R"]):
         P = int(nsh[r])
@@ -87,37 +107,38 @@ def test_mla_score_matches_oracle(seq_lens, H):
 
 
 def test_mla_score_q_quantisation_ties():
-    """Latent q rows whose q / qs quotients are exact half-integers (qs =
-    2^-4) must round to even like the reference's rint; rounding half away
-    from zero would move the page scores ~50x past the tolerance (checked on
-    the oracle)."""
+    """q rows (latent and RoPE parts) whose q / qs quotients are exact
+    half-integers (qs = 2^-4) must round to even like the reference's rint;
+    rounding half away from zero would move the page scores ~50x past the
+    tolerance (checked on the oracle).  Both quantisations are exercised:
+    q_c, and q_rope of the int8-RoPE scorer."""
     import torch
     from locks.selection import mla_derive, mla_score_only
     say("score q ties")
     c = _case(13, [16 * 40 + 5], 16)
     rng = np.random.default_rng(14)
-    k = rng.integers(-120, 120, size=(1, 16, LKV))
+    k = rng.integers(-120, 120, size=(1, 16, HS))
     q = O.bf16_to_f32(c["q"]).copy()
-    q_tie, q_away = q.copy(), q.copy()
-    q_tie[:, :, :LKV] = (k + 0.5) / 16.0
-    q_away[:, :, :LKV] = np.where(k >= 0, k + 1, k) / 16.0
-    q_tie[:, :, 0] = q_away[:, :, 0] = 127.0 / 16.0        # row max -> qs = 2^-4
+    q_tie = (k + 0.5) / 16.0
+    q_tie[:, :, 0] = q_tie[:, :, LKV] = 127.0 / 16.0         # row maxima -> qs = 2^-4
     c["q"] = O.f32_to_bf16(q_tie.astype(np.float32))
-    assert np.array_equal(O.bf16_to_f32(c["q"])[:, :, :LKV], q_tie[:, :, :LKV].astype(np.float32))
+    assert np.array_equal(O.bf16_to_f32(c["q"]), q_tie.astype(np.float32))
     d = _dev(c)
-    st = _state(c, budget=32)
-    slabs = M.mla_build_summaries(c["cache"], _blocks_of(c), c["NB"])
-    _upload_slabs(st, slabs)
+    st = _state(c, budget=32, rope="int8")
+    slabs, rs = _oracle_summaries(c, st)
     mla_derive(st, d["sl"], c["R"])
     mla_score_only(st, 0, d["q"], d["cache"], d["bt"], c["R"], 0.07)
     torch.cuda.synchronize()
     npg, nsh, b = M.mla_derive(c["sl"], PAGE, 10, 1, 32)
     P = int(nsh[0])
-    ref = M.mla_score_rki4(c["q"], slabs, c["cache"], c["bt"], nsh, 0.07, c["MP"])[0, :P]
-    away = M.mla_score_rki4(O.f32_to_bf16(q_away.astype(np.float32)), slabs, c["cache"], c["bt"],
-                            nsh, 0.07, c["MP"])[0, :P]
+    ref = M.mla_score_rki4(c["q"], slabs, c["cache"], c["bt"], nsh, 0.07, c["MP"], rope=rs)[0, :P]
     tol = 2e-4 * max(1.0, np.abs(ref).max())
-    assert np.abs(away - ref).max() > 10 * tol
+    for part in (slice(1, LKV), slice(LKV + 1, HS)):          # half away from zero, one part at a time
+        q_away = q_tie.copy()
+        q_away[:, :, part] = np.where(k[:, :, part] >= 0, k[:, :, part] + 1, k[:, :, part]) / 16.0
+        away = M.mla_score_rki4(O.f32_to_bf16(q_away.astype(np.float32)), slabs, c["cache"], c["bt"],
+                                nsh, 0.07, c["MP"], rope=rs)[0, :P]
+        assert np.abs(away - ref).max() > 10 * tol, part
     got = st.score_h[0, 0, 0, :P].cpu().numpy()
     assert np.abs(got - ref).max() <= tol
 
@@ -130,7 +151,7 @@ def test_mla_build_matches_oracle_through_the_score():
     say("build")
     c = _case(12, [16 * 64 + 3])
     d = _dev(c)
-    st = _state(c, budget=32)
+    st = _state(c, budget=32, rope="int8")
     blocks = _blocks_of(c)
     mla_build_blocks(st, 0, d["cache"], torch.from_numpy(blocks).cuda())
     torch.cuda.synchronize()
@@ -138,6 +159,9 @@ def test_mla_build_matches_oracle_through_the_score():
                c8=st.pp_c8[0].cpu().numpy(), cs=st.pp_cs[0].view(torch.int16).cpu().numpy().view(np.uint16),
                mu8=st.pp_mu8[0].cpu().numpy(), mus=st.pp_mus[0].view(torch.int16).cpu().numpy().view(np.uint16))
     ref = M.mla_build_summaries(c["cache"], blocks, c["NB"])
+    rope = M.mla_build_rope(c["cache"], blocks, c["NB"])                   # int8 RoPE summary: bit-exact
+    assert np.array_equal(st.pp_rk8[0].cpu().numpy(), rope["rk8"])
+    assert np.array_equal(st.pp_rks[0].view(torch.int16).cpu().numpy().view(np.uint16), rope["rks"])
     assert np.array_equal(gpu["mu8"][blocks], ref["mu8"][blocks])          # mean path is exact
     assert np.array_equal(gpu["mus"][blocks], ref["mus"][blocks])
     npg, nsh, b = M.mla_derive(c["sl"], PAGE, 10, 1, 32)
@@ -157,8 +181,7 @@ def test_mla_select_matches_topb_middle(seq_lens, budget):
     c = _case(13, seq_lens)
     d = _dev(c)
     st = _state(c, budget=budget)
-    slabs = M.mla_build_summaries(c["cache"], _blocks_of(c), c["NB"])
-    _upload_slabs(st, slabs)
+    _oracle_summaries(c, st)
     mla_select_pages(st, 0, d["q"], d["cache"], d["bt"], d["sl"], c["R"], 0.07)
     torch.cuda.synchronize()
     tab, cnt = st.page_table[:, 0].cpu().numpy(), st.page_cnt[:, 0].cpu().numpy()
@@ -175,18 +198,20 @@ def test_mla_select_matches_topb_middle(seq_lens, budget):
         assert cnt[r] == min(P, budget)
 
 
-@pytest.mark.parametrize("seq_lens,budget,H", [([16 * 60 + 5], 24, 16), ([16 * 30, 16 * 7 + 2], 16, 16),
-                                               ([16 * 2048], 128, 16), ([16 * 90 + 3, 16 * 33], 20, 5),
-                                               ([16 * 64], 32, 1)])
-def test_mla_decode_matches_oracle(seq_lens, budget, H):
+@pytest.mark.parametrize("seq_lens,budget,H,rope", [([16 * 60 + 5], 24, 16, "exact"),
+                                                    ([16 * 30, 16 * 7 + 2], 16, 16, "exact"),
+                                                    ([16 * 2048], 128, 16, "exact"),
+                                                    ([16 * 2048], 128, 16, "int8"),
+                                                    ([16 * 90 + 3, 16 * 33], 20, 5, "int8"),
+                                                    ([16 * 64], 32, 1, "exact")])
+def test_mla_decode_matches_oracle(seq_lens, budget, H, rope):
     import torch
     from locks.backend.mla_attn import mla_forward_mqa
-    say("decode", seq_lens, budget, H)
+    say("decode", seq_lens, budget, H, rope)
     c = _case(14, seq_lens, H)
     d = _dev(c)
-    st = _state(c, budget=budget)
-    slabs = M.mla_build_summaries(c["cache"], _blocks_of(c), c["NB"])
-    _upload_slabs(st, slabs)
+    st = _state(c, budget=budget, rope=rope)
+    _oracle_summaries(c, st)
     out = torch.empty(c["R"], c["H"], LKV, dtype=torch.bfloat16, device="cuda")
     o, lse = mla_forward_mqa(d["q"], d["cache"], d["bt"], d["sl"], st, 0.07, out=out, layer=0)
     torch.cuda.synchronize()

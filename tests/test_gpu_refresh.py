@@ -48,6 +48,15 @@ def _assert_same(a, b):
         np.testing.assert_array_equal(a[n], b[n], err_msg=n)
 
 
+def _assert_same_rope(a, b):
+    """int8 RoPE summaries of two MLA states, byte for byte."""
+    import torch
+    torch.cuda.synchronize()
+    for n in ("pp_rk8", "pp_rks"):
+        np.testing.assert_array_equal(getattr(a, n).contiguous().view(torch.uint8).cpu().numpy(),
+                                      getattr(b, n).contiguous().view(torch.uint8).cpu().numpy(), err_msg=n)
+
+
 def _per_layer(st, ks, blocks):
     import torch
     from locks.selection import rki4_build_blocks
@@ -259,7 +268,7 @@ def test_gate_keeps_every_finalized_page_fresh():
 def test_mla_latent_refresh_equals_per_layer_build():
     """The batched producers serve the MLA latent summaries too (head_dim 512,
     one latent head): bulk and delta over the latent views of the cache give
-    the bytes of the per-layer latent build."""
+    the bytes of the per-layer latent build, int8 RoPE summary included."""
     import torch
     from locks.selection import MlaState, mla_build_blocks, rki4_build_bulk, rki4_build_delta
     L, NB, MP = 2, 40, 16
@@ -272,7 +281,7 @@ def test_mla_latent_refresh_equals_per_layer_build():
 
     def state():
         return MlaState("cuda", num_layers=L, num_blocks=NB, n_heads=16, max_reqs=2,
-                        max_pages=MP, budget_pages=8, sink_pages=1, window_pages=2)
+                        max_pages=MP, budget_pages=8, sink_pages=1, window_pages=2, rope="int8")
 
     print("[case] mla latent bulk/delta", flush=True)
     a = state()
@@ -282,12 +291,16 @@ def test_mla_latent_refresh_equals_per_layer_build():
     for layer in range(L):
         mla_build_blocks(b, layer, caches[layer], torch.tensor(fin, dtype=torch.int32))
     _assert_same(_slab_bytes(a), _slab_bytes(b))
+    _assert_same_rope(a, b)
+    assert a.pp_rk8.abs().sum() > 0                       # the int8 RoPE summary was built
     assert rki4_build_delta(a, lat, bt, sl, 2, 11) == 0
     caches[1][fin[2], PAGE - 1, 5] += 1.0                  # latent tag channel
+    caches[1][fin[2], PAGE - 1, 512 + 7] += 3.0            # and a RoPE key of the same token
     assert rki4_build_delta(a, lat, bt, sl, 2, 11) == L
     for layer in range(L):
         mla_build_blocks(b, layer, caches[layer], torch.tensor([fin[2]], dtype=torch.int32))
     _assert_same(_slab_bytes(a), _slab_bytes(b))
+    _assert_same_rope(a, b)
 
 
 def test_bulk_replays_in_a_graph():

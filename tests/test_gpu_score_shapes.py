@@ -176,9 +176,11 @@ def test_score_six_slabs_equal_records(d, page, n_kv, G, seq, zsplit):
     assert torch.equal(pm, rec_pm), "page_max differs between six slabs and records"
 
 
-def test_mla_score_8k_pages():
+@pytest.mark.parametrize("rope", ["int8", "exact"])
+def test_mla_score_8k_pages(rope):
     """MLA latent scorer over the config-5 row (128K tokens, window 10:
-    8182 scored pages) at its automatic chunking."""
+    8182 scored pages) at its automatic chunking, with the int8 RoPE summary
+    and with the exact keys."""
     import torch
     from oracle import mla_oracle as M
     from locks.selection import MlaState, mla_derive, mla_score_only
@@ -192,8 +194,12 @@ def test_mla_score_8k_pages():
     slabs = rs(rng, NB, 1, d=512)
     q = O.f32_to_bf16(rng.standard_normal((1, 16, 576)).astype(np.float32))
     st = MlaState("cuda", num_layers=1, num_blocks=NB, n_heads=16, max_reqs=1, max_pages=MP,
-                  budget_pages=128, sink_pages=1, window_pages=10)
-    say(f"mla chunk={st.score_chunk}")
+                  budget_pages=128, sink_pages=1, window_pages=10, rope=rope)
+    say(f"mla chunk={st.score_chunk} rope={rope}")
+    rsum = M.mla_build_rope(cache, np.arange(NB), NB) if rope == "int8" else None
+    if rsum is not None:
+        st.pp_rk8[0].copy_(torch.from_numpy(rsum["rk8"]))
+        st.pp_rks[0].copy_(torch.from_numpy(rsum["rks"].view(np.int16)).view(torch.bfloat16))
     for k, name in (("v4", "pp_v4"), ("vs", "pp_vs"), ("c8", "pp_c8"), ("cs", "pp_cs"),
                     ("mu8", "pp_mu8"), ("mus", "pp_mus")):
         a = slabs[k]
@@ -217,7 +223,7 @@ def test_mla_score_8k_pages():
     for lo in range(0, P, 1024):
         hi = min(lo + 1024, P)
         ref[lo:hi] = M.mla_score_rki4(q, slabs, cache, np.ascontiguousarray(bt[:, lo:hi]),
-                                      np.array([hi - lo]), scale, hi - lo)[0]
+                                      np.array([hi - lo]), scale, hi - lo, rope=rsum)[0]
     err = np.abs(got[:P] - ref).max()
     say(f"mla 8182 pages: max |d| {err:.2e}")
     assert err <= 2e-4 * max(1.0, np.abs(ref).max())

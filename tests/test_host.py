@@ -202,15 +202,21 @@ def test_mla_entries_reject_bad_geometry_without_device():
     from locks import _lib
     lib = _lib.load()
     # locks_mla_score: kv_lora_rank 256 is outside this build
-    args = [1, 16 * 576, 576] + [1] * 7 + [16 * 576, 576, 8, 1, 64, 64, 1, 1, 64, 64, 64, 1, 16,
+    args = [1, 16 * 576, 576] + [1] * 9 + [16 * 576, 576, 8, 1, 64, 64, 1, 1, 64, 64, 64, 1, 16,
                                              256, 64, 16, 0.1, None]
     assert lib.locks_mla_score(*args) == -1 and b"geometry" in lib.locks_last_error()
-    args[22] = 17                                       # 17 heads
-    args[23] = 512
+    args[24] = 17                                       # 17 heads
+    args[25] = 512
     assert lib.locks_mla_score(*args) == -1 and b"n_heads=17" in lib.locks_last_error()
-    args[22] = 16
-    args[20] = 3                                        # odd chunk
+    args[24] = 16
+    args[22] = 3                                        # odd chunk
     assert lib.locks_mla_score(*args) == -1 and b"chunk 3" in lib.locks_last_error()
+    args[22] = 64
+    args[10] = None                                     # rk8 without rks
+    assert lib.locks_mla_score(*args) == -1 and b"rk8 and rks" in lib.locks_last_error()
+    # the int8 RoPE builder: strides must allow 16-byte loads
+    assert lib.locks_mla_build_rope(1, 16 * 576 + 4, 576, 8, 1, 1, None, 1, 1, None) == -1
+    assert b"multiples of 8" in lib.locks_last_error()
     # decode: split above the partial buffers' bound
     dargs = [1, 16 * 576, 576, 1, 16 * 576, 576, 8, 1, 64, 64, 1, 64, 64, 1, 1, 1, 1, 1,
              1, 16, 512, 64, 16, 513, 4, 0.1, None]

@@ -151,13 +151,102 @@ def test_latent_score_constant_page_closed_form():
     assert abs(got[0, 0] - want) <= 1e-4 * max(1.0, abs(want))
 
 
-def test_latent_summary_tracks_reference_selection():
+# ---- int8 RoPE summary ---------------------------------------------------
+def test_rope_summary_scale_rule_and_round_trip():
+    """Per token: the stored scale is bf16(max(absmax/127, 1e-8)), the
+    largest key maps to +-127, every key dequantizes within half a step of
+    the f32 scale plus the bf16 rounding of the scale (<= 2^-9 relative, x127),
+    listed out-of-range ids are skipped and unlisted blocks stay zero."""
+    rng = np.random.default_rng(21)
+    cache = M.synth_latent(rng, 6, 16)
+    cache[2, 5, 512:] = 0                                              # all-zero token
+    rope = M.mla_build_rope(cache, np.array([0, 2, 3, 9, -1]), 6)
+    k = O.bf16_to_f32(cache[:, :, 512:]).astype(np.float64)
+    am = np.abs(k).max(axis=-1)
+    sc_f32 = np.maximum(am / 127.0, 1e-8)
+    sc = O.bf16_to_f32(rope["rks"]).astype(np.float64)
+    for b in (0, 2, 3):
+        assert np.allclose(sc[b], sc_f32[b], rtol=2.0 ** -8, atol=0)
+        deq = rope["rk8"][b].astype(np.float64) * sc[b][:, None]
+        bound = 0.5 * sc_f32[b] + 127 * np.abs(sc[b] - sc_f32[b]) + 1e-12
+        assert np.all(np.abs(deq - k[b]) <= bound[:, None])
+        nz = am[b] > 0
+        assert np.all(np.abs(rope["rk8"][b]).max(axis=-1)[nz] == 127)
+    assert np.all(rope["rk8"][2, 5] == 0)
+    for b in (1, 4, 5):
+        assert not rope["rk8"][b].any() and not rope["rks"][b].any()
+
+
+def _representable_case(rng, H=4):
+    """Keys = integers in [-127, 127] (one +-127 per token) x 2^-3 and q_rope
+    = integers (one +-127 per head) x 2^-4: both int8 round trips are exact."""
+    cache = M.synth_latent(rng, 3, 16)
+    ki = rng.integers(-127, 128, size=(3, 16, 64))
+    ki[:, :, 0] = 127 * np.where(rng.random((3, 16)) < 0.5, -1, 1)
+    cache[:, :, 512:] = O.f32_to_bf16((ki * 2.0 ** -3).astype(np.float32))
+    q = O.f32_to_bf16(rng.standard_normal((1, H, 576)).astype(np.float32))
+    qi = rng.integers(-127, 128, size=(1, H, 64))
+    qi[:, :, 3] = 127
+    q[:, :, 512:] = O.f32_to_bf16((qi * 2.0 ** -4).astype(np.float32))
+    return cache, q, ki
+
+
+def test_int8_rope_score_equals_exact_on_representable_keys():
+    rng = np.random.default_rng(22)
+    cache, q, ki = _representable_case(rng)
+    rope = M.mla_build_rope(cache, np.arange(3), 3)
+    assert np.array_equal(rope["rk8"].astype(np.int64), ki)
+    assert np.all(O.bf16_to_f32(rope["rks"]) == np.float32(2.0 ** -3))
+    slabs = M.mla_build_summaries(cache, np.arange(3), 3)
+    bt = np.array([[2, 0, 1]], np.int32)
+    nsh = np.array([3])
+    exact = M.mla_score_rki4(q, slabs, cache, bt, nsh, 0.3, 3)
+    r8 = M.mla_score_rki4(q, slabs, cache, bt, nsh, 0.3, 3, rope=rope)
+    assert np.array_equal(exact, r8)
+
+
+def test_int8_rope_score_vs_explicit_loop():
+    """The int8 RoPE term recomputed by loops from the summary bytes: integer
+    dot of the int8 keys with the int8 q_rope, times both scales."""
+    _, cache, bt, q, sl = _latent_case(5)
+    npg = (sl + 15) // 16
+    nsh = np.array([npg - 1])
+    blocks = bt[0, :npg - 1]
+    slabs = M.mla_build_summaries(cache, blocks, cache.shape[0])
+    rope = M.mla_build_rope(cache, blocks, cache.shape[0])
+    got = M.mla_score_rki4(q, slabs, cache, bt, nsh, 0.1, npg, rope=rope)
+    base = M.mla_score_rki4(q, slabs, cache, bt, nsh, 0.1, npg)
+    q8, qs = O.quantize_q(q[0, :, :512])
+    qc = q8.astype(np.float64) * qs[:, None]
+    qf = O.bf16_to_f32(q[0, :, 512:]).astype(np.float64)
+    for p in range(int(nsh[0])):
+        b = bt[0, p]
+        V = O.unpack_i4(slabs["v4"][b, 0]).astype(np.float64) * O.bf16_to_f32(slabs["vs"][b, 0])[:, None]
+        best = -np.inf
+        for t in range(16):
+            k = (slabs["mu8"][b, 0] * O.bf16_to_f32(slabs["mus"][b, 0:1])[0]).astype(np.float64)
+            for c in range(8):
+                k = k + float(slabs["c8"][b, 0, t, c]) * float(O.bf16_to_f32(slabs["cs"][b, 0, t:t + 1])[0]) * V[c]
+            ks = float(O.bf16_to_f32(rope["rks"][b, t:t + 1])[0])
+            for h in range(q.shape[1]):
+                am = max(abs(float(x)) for x in qf[h])
+                qsr = np.float32(max(am, 1e-8)) / np.float32(127.0)
+                dot = sum(int(np.rint(np.float32(qf[h, d]) / qsr)) * int(rope["rk8"][b, t, d]) for d in range(64))
+                best = max(best, (qc[h] @ k + dot * float(qsr) * ks) * 0.1)
+        assert abs(got[0, p] - best) <= 1e-5 * max(1.0, abs(best))
+    # the summary moves the scores by about the keys' quantisation step only
+    assert np.abs(got - base).max() <= 0.02 * np.abs(base).max()
+
+
+@pytest.mark.parametrize("rope", [False, True])
+def test_latent_summary_tracks_reference_selection(rope):
     """Quality link to the reference: on the BASELINE-shaped distribution
     with planted query-matching tokens, the int4 latent summary keeps every
     planted page (as the reference's fp32 factors do) and its recall of the
     exact top pages (max logit over the full-precision page) is within 0.1
     of the reference estimator's.  Informative bound, not bit parity: the two
-    estimators differ (rank-8 about the mean, quantized, vs uncentred fp32)."""
+    estimators differ (rank-8 about the mean, quantized, vs uncentred fp32).
+    With ``rope`` the RoPE term comes from the int8 RoPE summary."""
     rng = np.random.default_rng(7)
     Lkv, Dr, H = 512, 64, 16
     NB, sl, budget = 200, 16 * 190 + 7, 40
@@ -181,7 +270,8 @@ def test_latent_summary_tracks_reference_selection():
     keep_ref = M.mla_select_pages_ref(O.bf16_to_f32(qb[0, :, :Lkv]), O.bf16_to_f32(qb[0, :, Lkv:]),
                                       cf, bt[0], sl, 0.07, 8, budget, 1, 10)
     slabs = M.mla_build_summaries(cache, bt[0, :int(nsh[0])], NB)
-    sc = M.mla_score_rki4(qb, slabs, cache, bt, nsh, 0.07, P)
+    rs = M.mla_build_rope(cache, bt[0, :int(nsh[0])], NB) if rope else None
+    sc = M.mla_score_rki4(qb, slabs, cache, bt, nsh, 0.07, P, rope=rs)
     tab, cnt = O.topb_select(sc[:, None, :], npg, nsh, b, 1, P)
     ours = set(tab[0, 0, :cnt[0, 0]].tolist())
     ref = set(np.nonzero(keep_ref)[0].tolist())
