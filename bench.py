@@ -114,7 +114,7 @@ def make_model(wl, budget_pages, seed=0, summaries="build", zsplit=None):
                 NB=NB, build_s=t_build, scale=1.0 / math.sqrt(D))
 
 
-def sparse_step(m, out):
+def sparse_step(m, out, vsources=None):
     from locks.backend import _runtime
     from locks.selection import derive_page_params
     st = m["st"]
@@ -123,8 +123,32 @@ def sparse_step(m, out):
         kv = m["kv"][layer]
         _runtime._rki4_select_adapter(m["q"][layer], kv, m["bt"], m["sl"], st, m["R"],
                                       m["scale"], None)
-        _runtime.decode_dispatch(m["q"][layer], kv, m["bt"], m["sl"], st, out[layer], None,
-                                 m["scale"], None)
+        _runtime.decode_dispatch(m["q"][layer], kv, m["bt"], m["sl"], st, out[layer],
+                                 vsources[layer] if vsources else None, m["scale"], None)
+
+
+def make_tier(m, mode):
+    """DRAM-tier V source for every layer (mem-v): ``pool`` = every page's V
+    in the pinned host pool; ``hot`` = every complete page in a hot slot of
+    its own (slot = block id), partial pages from the pool."""
+    import torch
+    from locks.tier import TierBuffers
+    L, NB, n_kv = m["L"], m["NB"], m["n_kv"]
+    t = TierBuffers("cuda", num_layers=L, num_blocks=NB, n_kv=n_kv, head_dim=D, page=PAGE,
+                    hot_slots=NB if mode == "hot" else 1, stage_blocks=1)
+    sls = m["sl"].tolist()
+    partial = [int(m["bt"][r, s // PAGE]) for r, s in enumerate(sls) if s % PAGE]
+    for layer in range(L):
+        kv = m["kv"][layer]
+        if mode == "hot":
+            t.hot[layer].copy_(kv[:, 1].permute(2, 0, 1, 3))
+            t.page2slot[layer].copy_(torch.arange(NB, dtype=torch.int32, device="cuda").expand(n_kv, NB))
+            if partial:
+                t.offload(layer, kv, partial)
+        else:
+            t.offload(layer, kv, list(range(NB)))
+    torch.cuda.synchronize()
+    return t
 
 
 def dense_split(m, split=0):
@@ -666,6 +690,9 @@ def main():
     ap.add_argument("--mla-rope", default="exact", choices=["exact", "int8"],
                     help="MLA scorer RoPE term: int8 RoPE summary or the exact cache keys")
     ap.add_argument("--no-dense", action="store_true")
+    ap.add_argument("--tier", default="", choices=["", "pool", "hot"],
+                    help="also time the step with V through the DRAM tier (pinned host pool, "
+                         "or every complete page in a hot slot)")
     ap.add_argument("--no-1m", action="store_true",
                     help="default workload only: skip the GLM-4-9B 1M north-star point")
     ap.add_argument("--dense-split", type=int, default=0,
@@ -780,6 +807,26 @@ def measure_gqa(a, wl, workload, summaries=None, quickstart=False):
         st.budget_abs = keep_b
         del gq
         sparse_step(m, out)                  # restore the headline budget's page tables
+        torch.cuda.synchronize()
+    if a.tier:
+        # the same step with V through the DRAM tier: bit-identical output
+        t0 = time.perf_counter()
+        tier = make_tier(m, a.tier)
+        log(f"{workload}: tier ({a.tier}) ready in {time.perf_counter() - t0:.1f}s")
+        vs = [tier.vsource(layer) for layer in range(m["L"])]
+        out_t = [torch.empty_like(o) for o in out]
+        sparse_step(m, out_t, vs)
+        torch.cuda.synchronize()
+        assert all(torch.equal(x, y) for x, y in zip(out, out_t)), "tiered step differs from resident"
+        gt = capture(lambda: sparse_step(m, out_t, vs))
+        ms_t = time_graph(gt, a.steps, a.warmup)
+        v_bytes = by["decode"] // 2                           # V half of the decode bytes
+        res["tier"] = dict(source=a.tier, ms_per_step=round(ms_t, 4),
+                           decode_v_bytes_per_step=v_bytes,
+                           v_GBps_if_all_extra_time=round(v_bytes / max((ms_t - ms) * 1e-3, 1e-9) / 1e9, 1)
+                           if a.tier == "pool" else None)
+        log(f"{workload}: tier ({a.tier}) step {ms_t:.3f} ms vs resident {ms:.3f} ms")
+        del gt, tier, vs, out_t
         torch.cuda.synchronize()
     score_us = scorer_roofline(m)
     score_gbps = by["score_per_launch"] / (score_us * 1e-6) / 1e9

@@ -41,7 +41,7 @@
 
 #include <stdint.h>
 
-#define LOCKS_ABI_VERSION 8
+#define LOCKS_ABI_VERSION 9
 
 #ifdef __cplusplus
 extern "C" {
@@ -175,6 +175,59 @@ int32_t locks_decode_splitk(const uint16_t* q, int64_t q_stride_req, int64_t q_s
                             float* l_part, float* acc_part, int32_t n_req, int32_t n_kv,
                             int32_t G, int32_t head_dim, int32_t page, int32_t split,
                             int32_t pps_min, int32_t max_cnt, float sm_scale, void* stream);
+
+/*
+ * DRAM-tier V source of the split decode (the mem tier's data plane).
+ * Replaces decode_split(..., v_src = 1, tier_pack) (attention/decode_cuda.py:
+ * 960-1031, tier select :178-222, pack :1043-1070).  Per (selected page pt,
+ * kv head kh) with physical block blk, one source is chosen:
+ *   hot      complete page ((pt + 1) * page <= seq_len) and
+ *            page2slot[kh * num_blocks + blk] = slot in [0, hot_slots):
+ *            hot_v + (kh * hot_slots + slot) * page * head_dim, token stride head_dim;
+ *   staged   else vbo[blk] = b in [0, stage_blocks): stage_v + b * stage_stride_block +
+ *            kh * stage_stride_head, token stride stage_stride_tok;
+ *   pinned   else pool_v + ((layer * num_blocks + blk) * n_kv + kh) * page * head_dim,
+ *            token stride head_dim (pinned host memory through its device
+ *            address, locks_host_device_pointer).
+ * With k_tier (mem-kv) K follows the same select from hot_k / stage_k / pool_k
+ * (same layouts); otherwise K is read from the paged cache.  On tier bytes
+ * equal to the cache's, the partials equal locks_decode_splitk's bit for bit.
+ * All pointers are device-visible and stay valid (graph-safe); the tier's
+ * control plane (residency, staging, offload) is the caller's.
+ */
+typedef struct locks_tier_src {
+    const uint16_t* hot_v;        /* (n_kv, hot_slots, page, head_dim) bf16, this layer */
+    const uint16_t* stage_v;      /* staging pool of this layer, element strides below */
+    const uint16_t* pool_v;       /* (layers, num_blocks, n_kv, page, head_dim) bf16, device address */
+    const uint16_t* hot_k;        /* k_tier only, as hot_v */
+    const uint16_t* stage_k;      /* k_tier only, as stage_v (same strides) */
+    const uint16_t* pool_k;       /* k_tier only, as pool_v */
+    const int32_t* page2slot;     /* (n_kv, num_blocks) hot slot of (kv head, block), -1 = none */
+    const int32_t* vbo;           /* (num_blocks,) staging block of a block, -1 = none */
+    int64_t stage_stride_block, stage_stride_tok, stage_stride_head;
+    int32_t num_blocks;           /* must equal the call's num_blocks */
+    int32_t hot_slots;            /* slots per (layer, kv head); page2slot values >= it are ignored */
+    int32_t stage_blocks;         /* staging blocks; vbo values >= it are ignored */
+    int32_t layer;                /* layer index into the pinned pools (< their layer count) */
+    int32_t k_tier;
+} locks_tier_src;
+
+int32_t locks_decode_splitk_tier(const uint16_t* q, int64_t q_stride_req, int64_t q_stride_head,
+                                 const uint16_t* k_cache, int64_t k_stride_block,
+                                 int64_t k_stride_tok, int64_t k_stride_head,
+                                 const uint16_t* v_cache, int64_t v_stride_block,
+                                 int64_t v_stride_tok, int64_t v_stride_head, int32_t num_blocks,
+                                 const int32_t* block_table, int64_t bt_stride, int32_t bt_cols,
+                                 const int32_t* page_table, int64_t pt_stride_req,
+                                 int64_t pt_stride_head, int32_t pt_cols, const int32_t* page_cnt,
+                                 int64_t cnt_stride, const int32_t* seq_lens, float* m_part,
+                                 float* l_part, float* acc_part, int32_t n_req, int32_t n_kv,
+                                 int32_t G, int32_t head_dim, int32_t page, int32_t split,
+                                 int32_t pps_min, int32_t max_cnt, float sm_scale,
+                                 const locks_tier_src* tier, void* stream);
+
+/* Device address of pinned (hipHostMalloc'd) host memory, for pool_v / pool_k. */
+int32_t locks_host_device_pointer(void* host, void** dev);
 
 /*
  * LSE merge of the split-K partials into the attention output.

@@ -257,7 +257,21 @@ __device__ __forceinline__ void wait_vm_steps(int ahead) {
 // DENSE: every page of the row in logical order (page count from seq_len,
 // no page table) -- the dense full-KV comparator.  KVPOL: cache policy bits
 // of the K/V DMA.  pg_sh: log2(page / 16).
-template <bool FUSED, bool DENSE = false, int NST = 2, int KVPOL = 0, int D = 128>
+// DRAM-tier V source (reference attention/decode_cuda.py:178-222, the mem
+// tier's per-(page, kv head) pointer select): a complete page whose (kv
+// head, block) holds a hot slot reads the hot buffer (n_kv, S, page, d);
+// else a staged block (vbo >= 0) reads the staging pool at its strides; else
+// the pinned host pool (L, NB, n_kv, page, d), device-visible.  K follows
+// the same select when k_tier (mem-kv), else stays in the paged cache.
+struct TierSrc {
+    const uint16_t* hotv; const uint16_t* stgv; const uint16_t* poolv;
+    const uint16_t* hotk; const uint16_t* stgk; const uint16_t* poolk;
+    const int* p2s; const int* vbo;
+    long svb, svt, svh, S, NV;
+    int lidx, k_tier;
+};
+
+template <bool FUSED, bool DENSE = false, int NST = 2, int KVPOL = 0, int D = 128, bool TIER = false>
 __global__ __launch_bounds__(DC_BLK) void decode_split_kernel(
     const uint16_t* __restrict__ q, long q_sr, long q_sh,
     const uint16_t* __restrict__ kc, long k_sb, long k_st, long k_sh,
@@ -267,9 +281,11 @@ __global__ __launch_bounds__(DC_BLK) void decode_split_kernel(
     const int* __restrict__ pcnt, long cnt_sr, const int* __restrict__ seq_lens,
     float* __restrict__ m_part, float* __restrict__ l_part, float* __restrict__ acc_part,
     int G, int split, int pps_min, float sm_scale, int pg_sh,
-    int* __restrict__ counters, void* __restrict__ out, long o_sr, long o_sh, int out_f32)
+    int* __restrict__ counters, void* __restrict__ out, long o_sr, long o_sh, int out_f32,
+    const TierSrc tier)
 {
     using GM = DcGeom<D>;
+    static_assert(!(TIER && (FUSED || DENSE)), "the tier source serves the split kernel");
     constexpr int KS = GM::KS, DPL = GM::DPL, NI = GM::NI, KB = GM::KBYTES, SB = GM::STEP_BYTES;
     const int sp = blockIdx.x, kh = blockIdx.y, r = blockIdx.z;
     const int n_kv = gridDim.y;
@@ -339,7 +355,7 @@ __global__ __launch_bounds__(DC_BLK) void decode_split_kernel(
     // Page and block ids of up to 64 steps of this wave are fetched up front
     // (lane i holds step i), so no dependent id load sits behind a stage's
     // DMA in the in-order vmcnt queue.
-    int ptv = 0, blkv = 0;
+    int ptv = 0, blkv = 0, slotv = -1, vbov = -1;
     auto fetch_ids = [&](int jb, bool spec) {
         const int jj = jb + DC_WAVES * lane;
         ptv = 0;
@@ -349,6 +365,10 @@ __global__ __launch_bounds__(DC_BLK) void decode_split_kernel(
             else ptv = spec ? pt_spec : prow[jj >> pg_sh];
             const int ptc = min(max(ptv, 0), bt_cols - 1);
             blkv = min(max(bt[(long)r * bt_sr + ptc], 0), NB - 1);
+            if constexpr (TIER) {                 // the tier's keys of (kv head, block)
+                slotv = tier.p2s[(long)kh * NB + blkv];
+                vbov = tier.vbo[blkv];
+            }
         }
     };
     // DMA step s of the current id batch (16 tokens from token 16 * sub of
@@ -360,22 +380,43 @@ __global__ __launch_bounds__(DC_BLK) void decode_split_kernel(
         const int pt = __builtin_amdgcn_readlane(ptv, s);
         const int blk = __builtin_amdgcn_readlane(blkv, s);
         const long t0 = (long)sub * 16;
-        const uint16_t* kp = kc + (long)blk * k_sb + (long)kh * k_sh + (t0 + c16) * k_st + 8 * kg;
+        const uint16_t* kpage = kc + (long)blk * k_sb + (long)kh * k_sh;
+        const uint16_t* vpage = vc + (long)blk * v_sb + (long)kh * v_sh;
+        long kst = k_st, vst = v_st;
+        if constexpr (TIER) {
+            // one wave-uniform source per (page, kv head)
+            const int slot = __builtin_amdgcn_readlane(slotv, s);
+            const int vbs = __builtin_amdgcn_readlane(vbov, s);
+            const bool complete = (long)(pt + 1) * PG <= (long)seq_len;
+            const bool hot = complete && slot >= 0 && slot < tier.S;   // out-of-range keys: the pool
+            const bool stg = !hot && vbs >= 0 && vbs < tier.NV;
+            const long pe = (long)PG * D;
+            const long hot_off = ((long)kh * tier.S + (hot ? slot : 0)) * pe;
+            const long stg_off = (long)(stg ? vbs : 0) * tier.svb + (long)kh * tier.svh;
+            const long pin_off = (((long)tier.lidx * NB + blk) * n_kv + kh) * pe;
+            vpage = hot ? tier.hotv + hot_off : stg ? tier.stgv + stg_off : tier.poolv + pin_off;
+            vst = stg ? tier.svt : (long)D;
+            if (tier.k_tier) {
+                kpage = hot ? tier.hotk + hot_off : stg ? tier.stgk + stg_off : tier.poolk + pin_off;
+                kst = vst;
+            }
+        }
+        const uint16_t* kp = kpage + (t0 + c16) * kst + 8 * kg;
 #pragma unroll
         for (int i = 0; i < KS; ++i)
             __builtin_amdgcn_global_load_lds(kp + 32 * i, (lds_ptr)(st + i * 1024), 16, 0, KVPOL);
-        const uint16_t* vb = vc + (long)blk * v_sb + (long)kh * v_sh + t0 * v_st;
+        const uint16_t* vb = vpage + t0 * vst;
         if constexpr (D == 64) {
 #pragma unroll
             for (int i = 0; i < 2; ++i)
-                __builtin_amdgcn_global_load_lds(vb + (long)(8 * i + (lane >> 3)) * v_st + 8 * (lane & 7),
+                __builtin_amdgcn_global_load_lds(vb + (long)(8 * i + (lane >> 3)) * vst + 8 * (lane & 7),
                                                  (lds_ptr)(st + KB + i * 1024), 16, 0, KVPOL);
         } else {
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
                 for (int hh = 0; hh < DPL / 8; ++hh)
-                    __builtin_amdgcn_global_load_lds(vb + (long)(4 * kg + i) * v_st + DPL * c16 + 8 * hh,
+                    __builtin_amdgcn_global_load_lds(vb + (long)(4 * kg + i) * vst + DPL * c16 + 8 * hh,
                                                      (lds_ptr)(st + KB + (i * (DPL / 8) + hh) * 1024), 16, 0, KVPOL);
         }
         return pt;
@@ -752,7 +793,7 @@ static bool dc_geometry(int head_dim, int page, int* pg_sh) {
         else { LAUNCH_D(256); }                              \
     } while (0)
 
-extern "C" int32_t locks_decode_splitk(
+static int32_t decode_splitk_impl(
     const uint16_t* q, int64_t q_stride_req, int64_t q_stride_head,
     const uint16_t* k_cache, int64_t k_stride_block, int64_t k_stride_tok, int64_t k_stride_head,
     const uint16_t* v_cache, int64_t v_stride_block, int64_t v_stride_tok, int64_t v_stride_head,
@@ -761,7 +802,8 @@ extern "C" int32_t locks_decode_splitk(
     const int32_t* page_cnt, int64_t cnt_stride, const int32_t* seq_lens,
     float* m_part, float* l_part, float* acc_part,
     int32_t n_req, int32_t n_kv, int32_t G, int32_t head_dim, int32_t page,
-    int32_t split, int32_t pps_min, int32_t max_cnt, float sm_scale, void* stream)
+    int32_t split, int32_t pps_min, int32_t max_cnt, float sm_scale, void* stream,
+    const locks_tier_src* ts)
 {
     int pg_sh = 0;
     LOCKS_REQUIRE(dc_geometry(head_dim, page, &pg_sh),
@@ -776,9 +818,28 @@ extern "C" int32_t locks_decode_splitk(
                   "locks_decode_splitk: q/K/V strides must be multiples of 8 elements (16-byte loads)");
     LOCKS_REQUIRE(q && k_cache && v_cache && block_table && page_table && page_cnt && seq_lens &&
                   m_part && l_part && acc_part, "locks_decode_splitk: null pointer argument");
+    TierSrc tier{};
+    if (ts) {
+        LOCKS_REQUIRE(ts->hot_v && ts->stage_v && ts->pool_v && ts->page2slot && ts->vbo,
+                      "locks_decode_splitk_tier: null tier pointer");
+        LOCKS_REQUIRE(!ts->k_tier || (ts->hot_k && ts->stage_k && ts->pool_k),
+                      "locks_decode_splitk_tier: k_tier needs the K hot / staging / pool pointers");
+        LOCKS_REQUIRE(ts->num_blocks == num_blocks,
+                      "locks_decode_splitk_tier: tier num_blocks %d != cache num_blocks %d", ts->num_blocks, num_blocks);
+        LOCKS_REQUIRE(ts->hot_slots >= 0 && ts->stage_blocks >= 0 && ts->layer >= 0,
+                      "locks_decode_splitk_tier: hot_slots %d / stage_blocks %d / layer %d < 0",
+                      ts->hot_slots, ts->stage_blocks, ts->layer);
+        LOCKS_REQUIRE(ts->stage_stride_block % 8 == 0 && ts->stage_stride_tok % 8 == 0 &&
+                      ts->stage_stride_head % 8 == 0,
+                      "locks_decode_splitk_tier: staging strides must be multiples of 8 elements");
+        tier = TierSrc{ts->hot_v, ts->stage_v, ts->pool_v, ts->hot_k, ts->stage_k, ts->pool_k,
+                       ts->page2slot, ts->vbo, (long)ts->stage_stride_block, (long)ts->stage_stride_tok,
+                       (long)ts->stage_stride_head, (long)ts->hot_slots, (long)ts->stage_blocks, ts->layer,
+                       ts->k_tier ? 1 : 0};
+    }
     if (n_req == 0) return 0;
 #define LAUNCH_D(DV)                                                                                   \
-    hipLaunchKernelGGL((decode_split_kernel<false, false, 2, 0, DV>),                                  \
+    if (ts) hipLaunchKernelGGL((decode_split_kernel<false, false, 2, 0, DV, true>),                   \
                        dim3(launched_splits(split, pps_min, max_cnt), n_kv, n_req), dim3(DC_BLK), 0,    \
                        (hipStream_t)stream, q, (long)q_stride_req, (long)q_stride_head, k_cache,       \
                        (long)k_stride_block, (long)k_stride_tok, (long)k_stride_head, v_cache,         \
@@ -786,10 +847,68 @@ extern "C" int32_t locks_decode_splitk(
                        block_table, (long)bt_stride, bt_cols, page_table, (long)pt_stride_req,         \
                        (long)pt_stride_head, pt_cols, page_cnt, (long)cnt_stride, seq_lens,            \
                        m_part, l_part, acc_part, G, split, pps_min, sm_scale, pg_sh,                   \
-                       nullptr, nullptr, 0L, 0L, 0)
+                       nullptr, nullptr, 0L, 0L, 0, tier);                                              \
+    else hipLaunchKernelGGL((decode_split_kernel<false, false, 2, 0, DV>),                             \
+                       dim3(launched_splits(split, pps_min, max_cnt), n_kv, n_req), dim3(DC_BLK), 0,    \
+                       (hipStream_t)stream, q, (long)q_stride_req, (long)q_stride_head, k_cache,       \
+                       (long)k_stride_block, (long)k_stride_tok, (long)k_stride_head, v_cache,         \
+                       (long)v_stride_block, (long)v_stride_tok, (long)v_stride_head, num_blocks,      \
+                       block_table, (long)bt_stride, bt_cols, page_table, (long)pt_stride_req,         \
+                       (long)pt_stride_head, pt_cols, page_cnt, (long)cnt_stride, seq_lens,            \
+                       m_part, l_part, acc_part, G, split, pps_min, sm_scale, pg_sh,                   \
+                       nullptr, nullptr, 0L, 0L, 0, TierSrc{})
     DC_BY_D(head_dim, LAUNCH_D);
 #undef LAUNCH_D
     return check_launch("decode_split_kernel");
+}
+
+extern "C" int32_t locks_decode_splitk(
+    const uint16_t* q, int64_t q_stride_req, int64_t q_stride_head,
+    const uint16_t* k_cache, int64_t k_stride_block, int64_t k_stride_tok, int64_t k_stride_head,
+    const uint16_t* v_cache, int64_t v_stride_block, int64_t v_stride_tok, int64_t v_stride_head,
+    int32_t num_blocks, const int32_t* block_table, int64_t bt_stride, int32_t bt_cols,
+    const int32_t* page_table, int64_t pt_stride_req, int64_t pt_stride_head, int32_t pt_cols,
+    const int32_t* page_cnt, int64_t cnt_stride, const int32_t* seq_lens,
+    float* m_part, float* l_part, float* acc_part,
+    int32_t n_req, int32_t n_kv, int32_t G, int32_t head_dim, int32_t page,
+    int32_t split, int32_t pps_min, int32_t max_cnt, float sm_scale, void* stream)
+{
+    return decode_splitk_impl(q, q_stride_req, q_stride_head, k_cache, k_stride_block, k_stride_tok,
+                              k_stride_head, v_cache, v_stride_block, v_stride_tok, v_stride_head,
+                              num_blocks, block_table, bt_stride, bt_cols, page_table, pt_stride_req,
+                              pt_stride_head, pt_cols, page_cnt, cnt_stride, seq_lens, m_part, l_part,
+                              acc_part, n_req, n_kv, G, head_dim, page, split, pps_min, max_cnt,
+                              sm_scale, stream, nullptr);
+}
+
+extern "C" int32_t locks_decode_splitk_tier(
+    const uint16_t* q, int64_t q_stride_req, int64_t q_stride_head,
+    const uint16_t* k_cache, int64_t k_stride_block, int64_t k_stride_tok, int64_t k_stride_head,
+    const uint16_t* v_cache, int64_t v_stride_block, int64_t v_stride_tok, int64_t v_stride_head,
+    int32_t num_blocks, const int32_t* block_table, int64_t bt_stride, int32_t bt_cols,
+    const int32_t* page_table, int64_t pt_stride_req, int64_t pt_stride_head, int32_t pt_cols,
+    const int32_t* page_cnt, int64_t cnt_stride, const int32_t* seq_lens,
+    float* m_part, float* l_part, float* acc_part,
+    int32_t n_req, int32_t n_kv, int32_t G, int32_t head_dim, int32_t page,
+    int32_t split, int32_t pps_min, int32_t max_cnt, float sm_scale,
+    const locks_tier_src* tier, void* stream)
+{
+    LOCKS_REQUIRE(tier, "locks_decode_splitk_tier: null tier");
+    return decode_splitk_impl(q, q_stride_req, q_stride_head, k_cache, k_stride_block, k_stride_tok,
+                              k_stride_head, v_cache, v_stride_block, v_stride_tok, v_stride_head,
+                              num_blocks, block_table, bt_stride, bt_cols, page_table, pt_stride_req,
+                              pt_stride_head, pt_cols, page_cnt, cnt_stride, seq_lens, m_part, l_part,
+                              acc_part, n_req, n_kv, G, head_dim, page, split, pps_min, max_cnt,
+                              sm_scale, stream, tier);
+}
+
+extern "C" int32_t locks_host_device_pointer(void* host, void** dev)
+{
+    LOCKS_REQUIRE(host && dev, "locks_host_device_pointer: null pointer argument");
+    const hipError_t e = hipHostGetDevicePointer(dev, host, 0);
+    LOCKS_REQUIRE(e == hipSuccess && *dev, "locks_host_device_pointer: %p is not pinned host memory (%s)",
+                  host, hipGetErrorString(e));
+    return 0;
 }
 
 extern "C" int32_t locks_decode_fused(
@@ -831,7 +950,7 @@ extern "C" int32_t locks_decode_fused(
                        block_table, (long)bt_stride, bt_cols, page_table, (long)pt_stride_req,         \
                        (long)pt_stride_head, pt_cols, page_cnt, (long)cnt_stride, seq_lens,            \
                        m_part, l_part, acc_part, G, split, pps_min, sm_scale, pg_sh,                   \
-                       counters, out, (long)out_stride_req, (long)out_stride_head, out_is_f32)
+                       counters, out, (long)out_stride_req, (long)out_stride_head, out_is_f32, TierSrc{})
     DC_BY_D(head_dim, LAUNCH_D);
 #undef LAUNCH_D
     return check_launch("decode_split_kernel<fused>");
@@ -897,7 +1016,7 @@ extern "C" int32_t locks_decode_dense(
                        (long)v_stride_block, (long)v_stride_tok, (long)v_stride_head, num_blocks,   \
                        block_table, (long)bt_stride, bt_cols, nullptr, 0L, 0L, 1, nullptr, 0L,      \
                        seq_lens, m_part, l_part, acc_part, G, split, 1, sm_scale, pg_sh,            \
-                       nullptr, nullptr, 0L, 0L, 0)
+                       nullptr, nullptr, 0L, 0L, 0, TierSrc{})
     DC_BY_D(head_dim, LAUNCH_D);
 #undef LAUNCH_D
     int rc = check_launch("decode_split_kernel<dense>");

@@ -10,10 +10,22 @@ import ctypes
 import os
 
 _LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "liblocks_hip.so")
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 _c = ctypes
 _i32, _i64, _f32, _f64, _p = _c.c_int32, _c.c_int64, _c.c_float, _c.c_double, _c.c_void_p
+
+
+
+class TierSrc(_c.Structure):
+    """locks_tier_src: the DRAM-tier V (and mem-kv K) source of the split decode."""
+    _fields_ = [("hot_v", _p), ("stage_v", _p), ("pool_v", _p),
+                ("hot_k", _p), ("stage_k", _p), ("pool_k", _p),
+                ("page2slot", _p), ("vbo", _p),
+                ("stage_stride_block", _i64), ("stage_stride_tok", _i64), ("stage_stride_head", _i64),
+                ("num_blocks", _i32), ("hot_slots", _i32), ("stage_blocks", _i32), ("layer", _i32),
+                ("k_tier", _i32)]
+
 
 # name -> (restype, argtypes); mirrors include/locks_hip.h one to one
 SIGNATURES = {
@@ -31,6 +43,11 @@ SIGNATURES = {
                                    _i32, _p, _i64, _i32, _p, _i64, _i64, _i32, _p, _i64, _p,
                                    _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
                                    _f32, _p]),
+    "locks_decode_splitk_tier": (_i32, [_p, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64,
+                                        _i32, _p, _i64, _i32, _p, _i64, _i64, _i32, _p, _i64, _p,
+                                        _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
+                                        _f32, _p, _p]),
+    "locks_host_device_pointer": (_i32, [_p, _p]),
     "locks_decode_fused": (_i32, [_p, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64,
                                   _i32, _p, _i64, _i32, _p, _i64, _i64, _i32, _p, _i64, _p,
                                   _p, _p, _p, _p, _p, _i64, _i64, _i32,

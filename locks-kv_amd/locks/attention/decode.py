@@ -9,6 +9,8 @@ V-source seam (only the resident source exists in this build).
 """
 from __future__ import annotations
 
+import ctypes
+
 import math
 
 import torch
@@ -108,6 +110,27 @@ def decode_splitk(q, k, v, block_table, seq_lens, page_table, page_cnt, m_part, 
         _lib.ptr(m_part), _lib.ptr(l_part), _lib.ptr(acc_part), int(n_req), int(n_kv), int(G),
         int(d), int(page), int(split), int(pps_min), int(max_cnt), float(scale),
         _lib.stream_ptr(q.device)), "decode_splitk")
+
+
+def decode_splitk_tier(q, k, v, block_table, seq_lens, page_table, page_cnt, m_part, l_part,
+                       acc_part, tier_src, *, n_req: int, G: int, split: int, pps_min: int,
+                       scale: float, max_cnt: int = 0) -> None:
+    """The split kernel with V (and, for mem-kv, K) from the DRAM tier
+    (``locks.tier.TierVSource.tier_src()``; attention/decode_cuda.py:178-222).
+    k, v: (NB, page, n_kv, d) views of the paged cache; v is never read and
+    may be any view of k's shape when the cache holds no V half."""
+    NB, page, n_kv, d = k.shape
+    lib = _lib.load()
+    _lib.check(lib.locks_decode_splitk_tier(
+        _lib.ptr(q), q.stride(0), q.stride(1),
+        _lib.ptr(k), k.stride(0), k.stride(1), k.stride(2),
+        _lib.ptr(v), v.stride(0), v.stride(1), v.stride(2), int(NB),
+        _lib.ptr(block_table), block_table.stride(0), int(block_table.shape[1]),
+        _lib.ptr(page_table), page_table.stride(0), page_table.stride(1),
+        int(page_table.shape[2]), _lib.ptr(page_cnt), page_cnt.stride(0), _lib.ptr(seq_lens),
+        _lib.ptr(m_part), _lib.ptr(l_part), _lib.ptr(acc_part), int(n_req), int(n_kv), int(G),
+        int(d), int(page), int(split), int(pps_min), int(max_cnt), float(scale),
+        ctypes.addressof(tier_src), _lib.stream_ptr(q.device)), "decode_splitk_tier")
 
 
 def _check_out(out) -> None:
@@ -210,11 +233,23 @@ def sparse_paged_decode_batched(q, kv_cache, block_table, seq_lens, st, out,
     k, _ = _split_kv(kv_cache)
     if vsource is None:
         vsource = ResidentVSource(kv_cache)
-    if vsource.SRC_ID != 0:
-        raise NotImplementedError("only the resident V source exists in this build")
-    v = vsource.args()[0]
     pps = _pps_min(n_req, st.n_kv)
     mc = page_cnt_bound(st)
+    if vsource.SRC_ID == 1:
+        # DRAM tier (decode_cuda.py:1301-1314): split kernel with the tier's
+        # source select, then the same merge
+        _, v_res = _split_kv(kv_cache)
+        decode_splitk_tier(q, k, v_res if v_res is not None else k, block_table, seq_lens,
+                           st.page_table, st.page_cnt, st.m_part, st.l_part, st.acc_part,
+                           vsource.tier_src(), n_req=n_req, G=st.G, split=st.split,
+                           pps_min=pps, scale=scale, max_cnt=mc)
+        decode_merge(st.m_part, st.l_part, st.acc_part, st.page_cnt, out, n_req=n_req,
+                     n_kv=st.n_kv, G=st.G, split=st.split, pps_min=pps,
+                     pt_cols=st.page_table.shape[2], max_cnt=mc)
+        return
+    if vsource.SRC_ID != 0:
+        raise NotImplementedError(f"V source {vsource.SRC_ID} is not built (0 = resident, 1 = DRAM tier)")
+    v = vsource.args()[0]
     if FUSED_MERGE:
         decode_fused(q, k, v, block_table, seq_lens, st.page_table, st.page_cnt, st.m_part,
                      st.l_part, st.acc_part, st.dec_counters, out, n_req=n_req, G=st.G,

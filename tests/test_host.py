@@ -82,6 +82,23 @@ def test_rejects_bad_geometry_without_device():
     rc = lib.locks_decode_splitk(*([1, 8, 8] + [1, 8, 8, 8] * 2 + [1, 1, 8, 1, 1, 8, 8, 1, 1,
                                    8, 1, 1, 1, 1, 1, 2, 17, 128, 16, 4, 1, 0, 0.1, None]))
     assert rc == -1 and b"G=17" in lib.locks_last_error()
+    # the DRAM-tier split: the tier struct is checked before any launch
+    import ctypes
+    targs = [1, 8, 8] + [1, 8, 8, 8] * 2 + [4, 1, 8, 1, 1, 8, 8, 1, 1, 8, 1, 1, 1, 1,
+                                             1, 2, 4, 128, 16, 4, 1, 0, 0.1]
+    assert lib.locks_decode_splitk_tier(*(targs + [None, None])) == -1
+    assert b"null tier" in lib.locks_last_error()
+    ts = _lib.TierSrc(hot_v=1, stage_v=1, pool_v=1, page2slot=1, vbo=1, stage_stride_block=8,
+                      stage_stride_tok=8, stage_stride_head=8, num_blocks=3, hot_slots=2)
+    assert lib.locks_decode_splitk_tier(*(targs + [ctypes.addressof(ts), None])) == -1
+    assert b"num_blocks 3 != cache num_blocks 4" in lib.locks_last_error()
+    ts.num_blocks, ts.k_tier = 4, 1
+    assert lib.locks_decode_splitk_tier(*(targs + [ctypes.addressof(ts), None])) == -1
+    assert b"k_tier needs" in lib.locks_last_error()
+    ts.k_tier, ts.stage_stride_tok = 0, 12
+    assert lib.locks_decode_splitk_tier(*(targs + [ctypes.addressof(ts), None])) == -1
+    assert b"staging strides" in lib.locks_last_error()
+    assert lib.locks_host_device_pointer(None, None) == -1
     # two chunks (max_pages 4096) need the candidate workspace: rejected pre-launch
     rc = lib.locks_select_nrm_topb(*([1, 1, 1] + [1] * 7 + [0, 1, 2, 4, 1, 4096, 0, 0, None]))
     assert rc == -1 and b"workspace" in lib.locks_last_error()
