@@ -392,7 +392,7 @@ def cpu_baseline(a, runs=10, warmup=2):
 # --------------------------------------------------------------------------- #
 # MLA (config 5)
 # --------------------------------------------------------------------------- #
-def make_mla_model(wl, seed=0, rope="exact"):
+def make_mla_model(wl, seed=0, rope="exact", split=None):
     import torch
     from locks.selection import MlaState, mla_build_blocks
     dev = torch.device("cuda")
@@ -410,7 +410,7 @@ def make_mla_model(wl, seed=0, rope="exact"):
         off += n
     st = MlaState(dev, num_layers=L, num_blocks=NB, n_heads=H, max_reqs=R, max_pages=MP,
                   budget_pages=wl["budget_pages"], sink_pages=1, window_pages=wl["window_pages"],
-                  rope=rope)
+                  rope=rope, split=split)
     fin = torch.cat([bt[r, : sls[r] // PAGE] for r in range(R)])
     caches, t_build = [], 0.0
     for layer in range(L):
@@ -544,7 +544,7 @@ def mla_cpu_baseline(m, sample_pages=1024):
 def run_mla(a, wl):
     import torch
     t0 = time.perf_counter()
-    m = make_mla_model(wl, rope=a.mla_rope)
+    m = make_mla_model(wl, rope=a.mla_rope, split=a.mla_split or None)
     log(f"MLA model ready in {time.perf_counter() - t0:.1f}s (latent summary build {m['build_s']:.1f}s)")
     R, H, L = m["R"], m["H"], m["L"]
     out = [torch.empty(R, H, MLA_LKV, dtype=torch.bfloat16, device="cuda") for _ in range(L)]
@@ -689,6 +689,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--mla-rope", default="exact", choices=["exact", "int8"],
                     help="MLA scorer RoPE term: int8 RoPE summary or the exact cache keys")
+    ap.add_argument("--mla-split", type=int, default=0,
+                    help="MLA sparse decode split count (0: the state's default, ~4 pages per split)")
     ap.add_argument("--no-dense", action="store_true")
     ap.add_argument("--tier", default="", choices=["", "pool", "hot"],
                     help="also time the step with V through the DRAM tier (pinned host pool, "
