@@ -98,24 +98,26 @@ def _tiered(case, d, tab, cnt, k_tier, seed):
 
 
 CASES = [
-    (2, 4, [16 * 40 + 5, 16 * 9], 16, False),
-    (4, 5, [1000, 7, 0, 4099], 32, False),
-    (2, 16, [16 * 300 + 3], 64, True),
-    (8, 4, [16384], 128, False),
-    (8, 4, [16 * 500 + 1, 16 * 200], 128, True),
+    (2, 4, [16 * 40 + 5, 16 * 9], 16, False, 128, 16),
+    (4, 5, [1000, 7, 0, 4099], 32, False, 128, 16),
+    (2, 16, [16 * 300 + 3], 64, True, 128, 16),
+    (8, 4, [16384], 128, False, 128, 16),
+    (8, 4, [16 * 500 + 1, 16 * 200], 128, True, 128, 16),
+    (4, 4, [32 * 90 + 7, 32 * 20], 32, True, 64, 32),
+    (2, 8, [16 * 200 + 9], 32, False, 256, 16),
 ]
 
 
-@pytest.mark.parametrize("n_kv,G,seq_lens,split,k_tier", CASES)
-def test_tier_decode_equals_resident(n_kv, G, seq_lens, split, k_tier):
+@pytest.mark.parametrize("n_kv,G,seq_lens,split,k_tier,hd,page", CASES)
+def test_tier_decode_equals_resident(n_kv, G, seq_lens, split, k_tier, hd, page):
     import torch
     from locks.attention import decode_merge, decode_splitk, decode_splitk_tier
     from locks.attention.decode import _pps_min, _split_kv
-    say("tier", n_kv, G, seq_lens, split, "mem-kv" if k_tier else "mem-v")
-    MP = max(1, max((s + 15) // 16 for s in seq_lens))
-    case = make_case(31, n_kv, G, seq_lens, MP=MP, build=False)
+    say("tier", n_kv, G, seq_lens, split, "mem-kv" if k_tier else "mem-v", f"d={hd} page={page}")
+    MP = max(1, max((s + page - 1) // page for s in seq_lens))
+    case = make_case(31, n_kv, G, seq_lens, MP=MP, build=False, page=page, d=hd)
     rng = np.random.default_rng(32)
-    npg, nsh, b = O.derive_page_params(seq_lens, 16, 1, 1, 126, 0.1)
+    npg, nsh, b = O.derive_page_params(seq_lens, page, 1, 1, 126, 0.1)
     sc = rng.random((case.R, n_kv, MP)).astype(np.float32)
     tab, cnt = O.topb_select(sc, npg, nsh, b, 1, MP)
     st = _state(case, split)
