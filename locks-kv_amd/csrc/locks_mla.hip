@@ -500,14 +500,13 @@ __global__ __launch_bounds__(ML_BLK) void mla_decode_split_kernel(
 {
     static_assert(NST >= 2 && NST <= 4, "page stages");
     const int sp = blockIdx.x, r = blockIdx.y;
-    const int cnt = DENSE ? min(cdiv(seq_lens[r], ML_PG), bt_cols) : min(pcnt[r], pt_cols);
-    const int pps = max(cdiv(cnt, split), pps_min);
-    const int j0 = sp * pps;
-    if (j0 >= cnt) return;                               // inactive split: no store
-    const int j1 = min(j0 + pps, cnt);
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r16 = lane & 15, kg = lane >> 4;
-    const int seq_len = seq_lens[r];
+    // The page count, this thread's first page id assuming pps == pps_min
+    // (the usual sparse case) and the q rows are loaded together, so the
+    // page ids do not wait for the count.
+    const int js = sp * pps_min + tid;
+    const int pt_spec = DENSE ? 0 : ptab[(long)r * pt_sr + min(js, pt_cols - 1)];
 
     __shared__ __attribute__((aligned(16))) uint8_t stg[NST][MD_PAGE_B];
     __shared__ __attribute__((aligned(16))) float spart[ML_WAVES][kWave * 4];
@@ -526,6 +525,12 @@ __global__ __launch_bounds__(ML_BLK) void mla_decode_split_kernel(
             qb[i] = __builtin_bit_cast(v8bf, w);
         }
     }
+    const int cnt = DENSE ? min(cdiv(seq_lens[r], ML_PG), bt_cols) : min(pcnt[r], pt_cols);
+    const int pps = max(cdiv(cnt, split), pps_min);
+    const int j0 = sp * pps;
+    if (j0 >= cnt) return;                               // inactive split: no store
+    const int j1 = min(j0 + pps, cnt);
+    const int seq_len = seq_lens[r];
     float m = -INFINITY, lsum = 0.f;
     v4f o[8];
 #pragma unroll
@@ -552,8 +557,9 @@ __global__ __launch_bounds__(ML_BLK) void mla_decode_split_kernel(
     for (int jb = j0; jb < j1; jb += MD_IDS) {
         const int nb = min(MD_IDS, j1 - jb);
         __syncthreads();                                      // previous batch fully consumed
+        const bool spec = pps == pps_min && jb == j0;         // jb + tid == js
         for (int i = tid; i < nb; i += ML_BLK) {
-            const int pt = DENSE ? jb + i : ptab[(long)r * pt_sr + jb + i];
+            const int pt = DENSE ? jb + i : (spec && i == tid) ? pt_spec : ptab[(long)r * pt_sr + jb + i];
             const int ptc = min(max(pt, 0), bt_cols - 1);
             ids_pt[i] = pt;
             ids_blk[i] = min(max(bt[(long)r * bt_sr + ptc], 0), NB - 1);
