@@ -41,7 +41,7 @@
 
 #include <stdint.h>
 
-#define LOCKS_ABI_VERSION 9
+#define LOCKS_ABI_VERSION 10
 
 #ifdef __cplusplus
 extern "C" {
@@ -208,8 +208,12 @@ typedef struct locks_tier_src {
     int32_t num_blocks;           /* must equal the call's num_blocks */
     int32_t hot_slots;            /* slots per (layer, kv head); page2slot values >= it are ignored */
     int32_t stage_blocks;         /* staging blocks; vbo values >= it are ignored */
-    int32_t layer;                /* layer index into the pinned pools (< their layer count) */
+    int32_t layer;                /* layer index into the pinned pools, in [0, num_layers) */
     int32_t k_tier;
+    /* geometry the tier's buffers were laid out for; each must equal the
+     * call's (the kernel derives every hot / pool offset from the call's) */
+    int32_t n_kv, page, head_dim;
+    int32_t num_layers;           /* layers in the pinned pools */
 } locks_tier_src;
 
 int32_t locks_decode_splitk_tier(const uint16_t* q, int64_t q_stride_req, int64_t q_stride_head,

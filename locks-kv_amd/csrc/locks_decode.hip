@@ -826,9 +826,15 @@ static int32_t decode_splitk_impl(
                       "locks_decode_splitk_tier: k_tier needs the K hot / staging / pool pointers");
         LOCKS_REQUIRE(ts->num_blocks == num_blocks,
                       "locks_decode_splitk_tier: tier num_blocks %d != cache num_blocks %d", ts->num_blocks, num_blocks);
-        LOCKS_REQUIRE(ts->hot_slots >= 0 && ts->stage_blocks >= 0 && ts->layer >= 0,
-                      "locks_decode_splitk_tier: hot_slots %d / stage_blocks %d / layer %d < 0",
-                      ts->hot_slots, ts->stage_blocks, ts->layer);
+        LOCKS_REQUIRE(ts->hot_slots >= 0 && ts->stage_blocks >= 0,
+                      "locks_decode_splitk_tier: hot_slots %d / stage_blocks %d < 0",
+                      ts->hot_slots, ts->stage_blocks);
+        LOCKS_REQUIRE(ts->n_kv == n_kv && ts->page == page && ts->head_dim == head_dim,
+                      "locks_decode_splitk_tier: tier laid out for n_kv %d / page %d / head_dim %d, "
+                      "call has %d / %d / %d", ts->n_kv, ts->page, ts->head_dim, n_kv, page, head_dim);
+        LOCKS_REQUIRE(ts->layer >= 0 && ts->layer < ts->num_layers,
+                      "locks_decode_splitk_tier: layer %d outside the pool's [0, %d)",
+                      ts->layer, ts->num_layers);
         LOCKS_REQUIRE(ts->stage_stride_block % 8 == 0 && ts->stage_stride_tok % 8 == 0 &&
                       ts->stage_stride_head % 8 == 0,
                       "locks_decode_splitk_tier: staging strides must be multiples of 8 elements");
@@ -1070,7 +1076,12 @@ extern "C" int32_t locks_decode_fused_noalloc(
     const long rows = (long)n_req * n_kv;
     const long cnt_bytes = rows * LOCKS_DECODE_COUNTER_STRIDE * 4;
     const long ml = rows * split * G;                    // m or l floats
-    const long need = cnt_bytes + ml * 4 * 2 + ml * (long)head_dim * 4;
+    // every region starts 256-byte aligned: the fused kernel stores and
+    // merges the partials with 16-byte vector accesses, and an odd
+    // n_req x n_kv x split x G would otherwise leave acc_part 8-byte aligned
+    auto up256 = [](long b) { return (b + 255) & ~255L; };
+    const long off_m = up256(cnt_bytes), off_l = off_m + up256(ml * 4), off_acc = off_l + up256(ml * 4);
+    const long need = off_acc + ml * (long)head_dim * 4;
     LOCKS_REQUIRE(need <= LOCKS_NOALLOC_SCRATCH_BYTES,
                   "locks_decode_fused_noalloc: n_req=%d x n_kv=%d x split=%d x G=%d needs %ld B of "
                   "scratch, more than its %ld B (use locks_decode_fused with caller buffers)",
@@ -1079,9 +1090,9 @@ extern "C" int32_t locks_decode_fused_noalloc(
     if (int rc = scratch_on_current_device(&base)) return rc;
     if (n_req == 0) return 0;
     int* counters = reinterpret_cast<int*>(base);
-    float* m_part = reinterpret_cast<float*>(base + cnt_bytes);
-    float* l_part = m_part + ml;
-    float* acc_part = l_part + ml;
+    float* m_part = reinterpret_cast<float*>(base + off_m);
+    float* l_part = reinterpret_cast<float*>(base + off_l);
+    float* acc_part = reinterpret_cast<float*>(base + off_acc);
     // the counters must start at zero: a previous call leaves them zero, but
     // this array is shared by every call on the GPU, so clear them here (a
     // fill kernel, which a HIP graph may capture)

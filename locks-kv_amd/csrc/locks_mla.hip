@@ -404,8 +404,8 @@ __global__ __launch_bounds__(ML_BLK) void mla_score_kernel(
 // ---------------------------------------------------------------------------
 // int8 RoPE summary of listed blocks: one wave per block, lane = (token
 // lane >> 2, 16 dims 16 (lane & 3) ..); per token scale = max(absmax / 127,
-// 1e-8) (the rki4 token-scale rule), key = clamp(rint(k / scale), +-127),
-// scale stored as bf16
+// 1e-8) (the rki4 token-scale rule) rounded to bf16, key = clamp(rint(k /
+// bf16 scale), +-127); the bf16 scale is stored
 // ---------------------------------------------------------------------------
 constexpr int MR_WAVES = 4;
 __global__ __launch_bounds__(MR_WAVES * kWave) void mla_rope_quant_kernel(
@@ -432,7 +432,10 @@ __global__ __launch_bounds__(MR_WAVES * kWave) void mla_rope_quant_kernel(
     for (int e = 0; e < 16; ++e) am = fmaxf(am, fabsf(x[e]));
     am = fmaxf(am, __shfl_xor(am, 1));
     am = fmaxf(am, __shfl_xor(am, 2));
-    const float sc = fmaxf(__fdiv_rn(am, 127.f), 1e-8f);
+    // the stored bf16 scale is the one the keys are quantized with, so the
+    // scorer's dequantization k8 * scale uses exactly the quantization step
+    const uint16_t sb = f32_to_bf16(fmaxf(__fdiv_rn(am, 127.f), 1e-8f));
+    const float sc = __uint_as_float((uint32_t)sb << 16);
     uint32_t pk[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
@@ -440,7 +443,7 @@ __global__ __launch_bounds__(MR_WAVES * kWave) void mla_rope_quant_kernel(
         pk[e >> 2] |= ((uint32_t)(uint8_t)v) << (8 * (e & 3));
     }
     *reinterpret_cast<uint4*>(rk8 + (long)b * ML_RK_BLOCK + t * ML_DR + 16 * part) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-    if (part == 0) rks[(long)b * ML_PG + t] = f32_to_bf16(sc);
+    if (part == 0) rks[(long)b * ML_PG + t] = sb;
 }
 
 // ---------------------------------------------------------------------------

@@ -10,7 +10,7 @@ import ctypes
 import os
 
 _LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "liblocks_hip.so")
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 _c = ctypes
 _i32, _i64, _f32, _f64, _p = _c.c_int32, _c.c_int64, _c.c_float, _c.c_double, _c.c_void_p
@@ -24,7 +24,8 @@ class TierSrc(_c.Structure):
                 ("page2slot", _p), ("vbo", _p),
                 ("stage_stride_block", _i64), ("stage_stride_tok", _i64), ("stage_stride_head", _i64),
                 ("num_blocks", _i32), ("hot_slots", _i32), ("stage_blocks", _i32), ("layer", _i32),
-                ("k_tier", _i32)]
+                ("k_tier", _i32), ("n_kv", _i32), ("page", _i32), ("head_dim", _i32),
+                ("num_layers", _i32)]
 
 
 # name -> (restype, argtypes); mirrors include/locks_hip.h one to one

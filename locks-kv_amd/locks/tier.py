@@ -150,4 +150,5 @@ class TierVSource:
         ts.stage_stride_block, ts.stage_stride_tok, ts.stage_stride_head = vp.stride(0), vp.stride(1), vp.stride(2)
         ts.num_blocks, ts.hot_slots, ts.stage_blocks = t.NB, t.S, t.NV
         ts.layer, ts.k_tier = l, 1 if t.offload_k else 0
+        ts.n_kv, ts.page, ts.head_dim, ts.num_layers = t.n_kv, t.page, t.d, t.L
         return ts

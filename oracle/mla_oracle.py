@@ -155,8 +155,9 @@ def mla_build_rope(cache_bf16: np.ndarray, blocks, n_blocks: int, Lkv: int = 512
     if blk.size:
         k = O.bf16_to_f32(cache_bf16[blk, :, Lkv:])                      # (n, page, Dr)
         sc = np.maximum((np.abs(k).max(axis=-1) / f32(127.0)).astype(f32), f32(1e-8))
-        rk8[blk] = np.clip(np.rint(k / sc[..., None]), -127, 127).astype(np.int8)
         rks[blk] = O.f32_to_bf16(sc)
+        sc = O.bf16_to_f32(rks[blk])             # quantize with the stored scale
+        rk8[blk] = np.clip(np.rint(k / sc[..., None]), -127, 127).astype(np.int8)
     return dict(rk8=rk8, rks=rks)
 
 

@@ -80,15 +80,16 @@ def test_build_matches_oracle_build():
     rg, rr = recon(got), recon(ref)
     eg = np.linalg.norm(rg - dc) / np.linalg.norm(dc)
     er = np.linalg.norm(rr - dc) / np.linalg.norm(dc)
-    print(f"[case] reconstruction error gpu {eg:.4f} oracle {er:.4f}", flush=True)
-    assert abs(eg - er) < 0.01 and eg < 0.5
+    print(f"[case] reconstruction error gpu {eg:.6f} oracle {er:.6f}", flush=True)
+    assert abs(eg - er) <= 1e-3 * er
     npg, nsh, _ = O.derive_page_params(case.seq_lens, 16, 1, 1, 126, 0.1)
     sg = O.score_rki4_twin(case.q, got, case.bt, nsh, 2, 4, case.scale, case.MP)
     so = O.score_rki4_twin(case.q, ref, case.bt, nsh, 2, 4, case.scale, case.MP)
     P = int(nsh[0])
     diff = np.abs(sg[..., :P] - so[..., :P])
     print(f"[case] score |gpu-build - oracle-build| max {diff.max():.3e} mean {diff.mean():.3e}", flush=True)
-    assert diff.mean() < 0.02 and diff.max() < 0.5
+    # about 2x the MI355X measurement (max 1.25e-2, mean 2.2e-5)
+    assert diff.max() <= 0.025 and diff.mean() <= 5e-5
 
 
 def test_refresh_is_tag_gated():

@@ -201,15 +201,25 @@ def test_build_geometry(hd, page):
     _, _, dc, _ = O.summary_pre(case.k[b])
     eg = np.linalg.norm(recon(got) - dc) / np.linalg.norm(dc)
     er = np.linalg.norm(recon(ref) - dc) / np.linalg.norm(dc)
-    say(f"reconstruction error gpu {eg:.4f} oracle {er:.4f}")
-    assert abs(eg - er) < 0.01 and eg < 0.9
+    say(f"reconstruction error gpu {eg:.6f} oracle {er:.6f}")
+    assert abs(eg - er) <= 1e-3 * er
     npg, nsh, _ = O.derive_page_params(case.seq_lens, page, 1, 1, 40, 0.1)
     sg = O.score_rki4_twin(case.q, got, case.bt, nsh, n_kv, G, case.scale, case.MP)
     so = O.score_rki4_twin(case.q, ref, case.bt, nsh, n_kv, G, case.scale, case.MP)
     P = int(nsh[0])
     diff = np.abs(sg[..., :P] - so[..., :P])
     say(f"score |gpu-build - oracle-build| max {diff.max():.3e} mean {diff.mean():.3e}")
-    assert diff.mean() < 0.02 and diff.max() < 0.5
+    bmax, bmean = BUILD_SCORE_BARS[(hd, page)]
+    assert diff.max() <= bmax and diff.mean() <= bmean
+
+
+# (max, mean) of |score(GPU build) - score(LAPACK build)| per geometry: about
+# 2x what MI355X measured (max / mean: 64x16 5.9e-3 / 7.1e-6, 256x16 4.2e-2 /
+# 4.0e-5, 128x32 8.2e-3 / 2.7e-5, 64x32 7.8e-3 / 2.2e-5, 256x32 3.3e-3 /
+# 1.8e-5, 128x64 1.7e-3 / 8.1e-6, 64x64 1.0e-1 / 1.0e-4, 256x64 3.4e-3 / 2.4e-5)
+BUILD_SCORE_BARS = {(64, 16): (0.012, 1.5e-5), (256, 16): (0.085, 8e-5), (128, 32): (0.017, 6e-5),
+                    (64, 32): (0.016, 5e-5), (256, 32): (0.007, 4e-5), (128, 64): (0.0035, 2e-5),
+                    (64, 64): (0.2, 2.1e-4), (256, 64): (0.007, 5e-5)}
 
 
 @pytest.mark.parametrize("hd,page", [(64, 16), (256, 32), (128, 32), (128, 64)])

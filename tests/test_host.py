@@ -95,7 +95,20 @@ def test_rejects_bad_geometry_without_device():
     ts.num_blocks, ts.k_tier = 4, 1
     assert lib.locks_decode_splitk_tier(*(targs + [ctypes.addressof(ts), None])) == -1
     assert b"k_tier needs" in lib.locks_last_error()
-    ts.k_tier, ts.stage_stride_tok = 0, 12
+    ts.k_tier = 0
+    # a tier laid out for another geometry, or a layer past the pool's layers
+    for fields, msg in ((dict(n_kv=1, page=16, head_dim=128, num_layers=1), b"n_kv 1 / page 16"),
+                        (dict(n_kv=2, page=32, head_dim=128, num_layers=1), b"page 32"),
+                        (dict(n_kv=2, page=16, head_dim=64, num_layers=1), b"head_dim 64"),
+                        (dict(n_kv=2, page=16, head_dim=128, num_layers=0), b"layer 0 outside")):
+        for k, v in fields.items():
+            setattr(ts, k, v)
+        assert lib.locks_decode_splitk_tier(*(targs + [ctypes.addressof(ts), None])) == -1
+        assert msg in lib.locks_last_error(), lib.locks_last_error()
+    ts.num_layers, ts.layer = 2, 2
+    assert lib.locks_decode_splitk_tier(*(targs + [ctypes.addressof(ts), None])) == -1
+    assert b"layer 2 outside the pool's [0, 2)" in lib.locks_last_error()
+    ts.layer, ts.stage_stride_tok = 1, 12
     assert lib.locks_decode_splitk_tier(*(targs + [ctypes.addressof(ts), None])) == -1
     assert b"staging strides" in lib.locks_last_error()
     assert lib.locks_host_device_pointer(None, None) == -1

@@ -112,3 +112,18 @@ def test_noalloc_rejects_oversized_call():
     with pytest.raises(RuntimeError, match="scratch"):
         D.decode_fused_noalloc(q, k, v, bt, sl, tab, cnt, out, n_req=R, G=4, split=128,
                                pps_min=4, scale=case.scale)
+
+
+def test_noalloc_odd_partial_counts():
+    """n_req x n_kv x split x G odd (3, then 9): each scratch region still
+    starts 256-byte aligned, so the 16-byte partial stores and merge loads
+    stay aligned; bit-identical to the caller-buffer entry point."""
+    import torch
+    say("odd: n_kv=1 G=1 seq_lens=[3000] split=3")
+    case, d = _inputs(36, 1, 1, [3000], 60)
+    ref, out = _pair(case, d, 3, 4, torch.bfloat16)
+    assert _same(ref, out) and torch.isfinite(out.float()).all()
+    say("odd: n_kv=1 G=3 seq_lens=[1500] split=3")
+    case2, d2 = _inputs(37, 1, 3, [1500], 40)
+    ref2, out2 = _pair(case2, d2, 3, 2, torch.float32)
+    assert _same(ref2, out2) and torch.isfinite(out2).all()
