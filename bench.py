@@ -132,10 +132,10 @@ def make_tier(m, mode):
     in the pinned host pool; ``hot`` = every complete page in a hot slot of
     its own (slot = block id), partial pages from the pool."""
     import torch
-    from locks.tier import TierBuffers
+    from locks.tier import Tier
     L, NB, n_kv = m["L"], m["NB"], m["n_kv"]
-    t = TierBuffers("cuda", num_layers=L, num_blocks=NB, n_kv=n_kv, head_dim=D, page=PAGE,
-                    hot_slots=NB if mode == "hot" else 1, stage_blocks=1)
+    t = Tier("cuda", num_layers=L, num_blocks=NB, n_kv=n_kv, head_dim=D, page=PAGE,
+             hot_slots=NB if mode == "hot" else 1, v_blocks=2, max_tokens=PAGE)
     sls = m["sl"].tolist()
     partial = [int(m["bt"][r, s // PAGE]) for r, s in enumerate(sls) if s % PAGE]
     for layer in range(L):
@@ -542,6 +542,12 @@ def mla_cpu_baseline(m, sample_pages=1024):
 
 
 def run_mla(a, wl):
+    print(json.dumps(measure_mla(a, wl, a.workload)), flush=True)
+
+
+def measure_mla(a, wl, workload, cpu=True):
+    """The MLA workload: captured sparse step, dense
+    latent comparator, scorer roofline; returns the JSON line."""
     import torch
     t0 = time.perf_counter()
     m = make_mla_model(wl, rope=a.mla_rope, split=a.mla_split or None)
@@ -573,14 +579,17 @@ def run_mla(a, wl):
         res = dict(dense_ms_per_step=round(ms_dense, 4),
                    dense_achieved_GBps=round(by["dense"] / (ms_dense * 1e-3) / 1e9, 1),
                    speedup_vs_dense=round(ms_dense / ms, 3))
-    cpu = None if a.no_cpu else mla_cpu_baseline(m)
+    cpu = None if (a.no_cpu or not cpu) else mla_cpu_baseline(m)
     sparse_bytes = by["score"] + by["select"] + by["decode"]
+    if "dense_ms_per_step" in res:
+        ideal = by["dense"] / (HBM_PEAK_GBPS * 1e9) * 1e3
+        res.update(dense_ideal_ms_per_step=round(ideal, 4), speedup_vs_ideal_dense=round(ideal / ms, 3))
     line = {
         "metric": "decode ms/step + achieved HBM GB/s, bs=1 @128K/1M ctx, b=2048",
         "value": round(ms, 4), "unit": "ms/step", "n_gpus": 1, "steps": a.steps,
         "warmup": a.warmup, "ms_per_step": round(ms, 4), "higher_is_better": False,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
-        "config": {"workload": a.workload, "layers": L, "heads": H, "kv_lora_rank": MLA_LKV,
+        "config": {"workload": workload, "layers": L, "heads": H, "kv_lora_rank": MLA_LKV,
                    "rope_dim": MLA_DR, "seq_lens": wl["seq_lens"], "page": PAGE,
                    "budget_pages": wl["budget_pages"], "window_pages": wl["window_pages"],
                    "attended_pages": int(m["st"].page_cnt[0, 0].item()),
@@ -595,12 +604,15 @@ def run_mla(a, wl):
                      "avg_launch_us": round(score_us, 3),
                      "bytes_per_launch": by["score_per_launch"],
                      # the committed PMC traffic is the default (exact-key) scorer's
-                     "traffic": scorer_traffic(a.workload) if a.mla_rope == "exact" else None,
+                     "traffic": scorer_traffic(workload) if a.mla_rope == "exact" else None,
                      "stream_read_same_bytes_us": round(stream_us, 3),
                      "frac_of_stream_read": round(stream_us / score_us, 4)},
         "cpu_baseline": cpu,
     }
-    print(json.dumps(line), flush=True)
+    del g, m, out, lse
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return line
 
 
 def run_refresh(a, m):
@@ -695,6 +707,8 @@ def main():
     ap.add_argument("--tier", default="", choices=["", "pool", "hot"],
                     help="also time the step with V through the DRAM tier (pinned host pool, "
                          "or every complete page in a hot slot)")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the ragged GLM batch and MLA points of the default run")
     ap.add_argument("--no-1m", action="store_true",
                     help="default workload only: skip the GLM-4-9B 1M north-star point")
     ap.add_argument("--dense-split", type=int, default=0,
@@ -755,6 +769,17 @@ def main():
                 "dense_ms_per_step", "dense_achieved_GBps", "dense_ideal_ms_per_step",
                 "speedup_vs_dense", "speedup_vs_ideal_dense", "roofline", "config")
         line["glm9b_1m"] = {k: g1m[k] for k in keep if k in g1m}
+    if a.workload == "llama8b-128k" and not a.no_extra:
+        # BASELINE configs[3] (ragged GLM batch) and configs[4] (MLA) in the
+        # same line, each with its dense leg and scorer roofline
+        keep = ("ms_per_step", "tokens_per_s", "achieved_GBps", "step_algorithmic_bytes",
+                "dense_ms_per_step", "dense_achieved_GBps", "dense_ideal_ms_per_step",
+                "speedup_vs_dense", "speedup_vs_ideal_dense", "roofline", "config")
+        gb, _ = measure_gqa(a, WORKLOADS["glm9b-batch"], "glm9b-batch", summaries="copy",
+                            quickstart=False)
+        line["glm9b_batch"] = {k: gb[k] for k in keep if k in gb}
+        ml = measure_mla(a, WORKLOADS["dsv2lite-mla-128k"], "dsv2lite-mla-128k", cpu=False)
+        line["dsv2lite_mla_128k"] = {k: ml[k] for k in keep if k in ml}
     line["cpu_baseline"] = None if a.no_cpu else cpu_baseline(a)
     print(json.dumps(line), flush=True)
 

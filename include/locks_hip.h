@@ -234,6 +234,95 @@ int32_t locks_decode_splitk_tier(const uint16_t* q, int64_t q_stride_req, int64_
 int32_t locks_host_device_pointer(void* host, void** dev);
 
 /*
+ * DRAM tier control plane (the reference's staging lifecycle and exact-LRU
+ * residency, src/locks/tier/staging.py, tier/residency.py).  Every buffer is
+ * caller-owned device memory (pool_v / pool_k: the pinned pools' device
+ * addresses); launches go on `stream`, no host sync, graph-safe.
+ * Layouts: page2slot / pool_valid (layers, n_kv, num_blocks), slot2page / lru
+ * (layers, n_kv, hot_slots), clock (layers, n_kv); the per-layer entries take
+ * one layer's slice.  Staging pools (layers, stage_blocks, page, n_kv,
+ * head_dim) with the element strides given; vbo / v_flushed (num_blocks,).
+ */
+
+/* Replaces Residency.invalidate_written (residency.py:271-307, :389-419):
+ * every page written this step ((seq_len - q_len) / page .. (seq_len - 1) /
+ * page of each request with seq_len > 0) loses its hot slot and its pool
+ * validity in every layer and kv head. */
+int32_t locks_tier_invalidate(const int32_t* block_table, int64_t bt_stride, int32_t bt_cols,
+                              const int32_t* seq_lens, const int32_t* query_start_loc,
+                              int32_t n_req, int32_t* page2slot, int32_t* slot2page,
+                              int8_t* pool_valid, int32_t num_layers, int32_t n_kv,
+                              int32_t num_blocks, int32_t hot_slots, int32_t page, void* stream);
+
+/* Replaces Staging.begin_step's bookkeeping (staging.py:373-442: vflush_clear
+ * :125-138, flush_collect :141-191, valloc :194-221, vslot :224-244): one
+ * workgroup, requests in order.  Writes flush_list (max_flush, 2) = (block,
+ * staging block) pairs to copy and *flush_cnt, frees collected staging blocks
+ * onto free_stack, allocates one for every written page lacking one (stack
+ * underflow sets *overflow), and fills v_slot_mapping (max_tokens,) int64
+ * (staging block * page + offset, -1 = none).  Follow with
+ * locks_tier_flush_copy before this step's locks_tier_scatter. */
+int32_t locks_tier_stage_begin(const int32_t* block_table, int64_t bt_stride, int32_t bt_cols,
+                               const int32_t* seq_lens, const int32_t* query_start_loc,
+                               int32_t n_req, int32_t* vbo, int32_t* v_flushed,
+                               int32_t* free_stack, int32_t* free_top, int32_t* flush_list,
+                               int32_t* flush_cnt, int32_t max_flush, int64_t* v_slot_mapping,
+                               int32_t max_tokens, int32_t* overflow, int32_t num_blocks,
+                               int32_t stage_blocks, int32_t page, void* stream);
+
+/* Replaces _flush_copy_kernel (staging.py:247-277): every flush-list page of
+ * every layer and kv head from the staging pool(s) to the pinned pool(s)
+ * (layers, num_blocks, n_kv, page, head_dim), setting pool_valid. */
+int32_t locks_tier_flush_copy(const int32_t* flush_list, const int32_t* flush_cnt,
+                              int32_t max_flush, const uint16_t* stage_v, const uint16_t* stage_k,
+                              int64_t stage_stride_layer, int64_t stage_stride_block,
+                              int64_t stage_stride_tok, int64_t stage_stride_head,
+                              uint16_t* pool_v, uint16_t* pool_k, int8_t* pool_valid,
+                              int32_t num_layers, int32_t n_kv, int32_t num_blocks, int32_t page,
+                              int32_t head_dim, int32_t k_tier, void* stream);
+
+/* Replaces Staging.scatter_kv (staging.py:57-82, :444-460): token t's V (and,
+ * k_tier, K) (n_kv, head_dim) into one layer's staging pool(s) at
+ * v_slot_mapping[t] (skipped when negative). */
+int32_t locks_tier_scatter(const uint16_t* value, int64_t v_stride_tok, int64_t v_stride_head,
+                           const uint16_t* key, int64_t k_stride_tok, int64_t k_stride_head,
+                           int32_t n_tokens, const int64_t* v_slot_mapping, uint16_t* stage_v,
+                           uint16_t* stage_k, int64_t stage_stride_block, int64_t stage_stride_tok,
+                           int64_t stage_stride_head, int32_t n_kv, int32_t head_dim, int32_t page,
+                           int32_t stage_blocks, int32_t k_tier, void* stream);
+
+/* Replaces Residency.gather_plan (residency.py:437-459: the clock advance,
+ * _miss_diff_kernel :51-88, _select_victims_kernel :91-145) for one layer:
+ * the selected complete pages of each (request, kv head) that have a hot
+ * slot are touched; the others are misses (miss_pages (n_req, n_kv, pt_cols),
+ * miss_cnt (n_req, n_kv)); each block's first miss takes the least recently
+ * used slot not touched in this call (ties: lowest slot), evicting its page
+ * (victims: the slot, -1 for later occurrences or when no slot is left,
+ * which sets *overflow).  fetch_list (n_kv, fetch_cap, 2) = (block, slot) of
+ * every install, fetch_cnt (n_kv,).  clock: this layer's (n_kv,) slice. */
+int32_t locks_tier_plan(const int32_t* page_table, int64_t pt_stride_req, int64_t pt_stride_head,
+                        int32_t pt_cols, const int32_t* page_cnt, int64_t cnt_stride,
+                        const int32_t* block_table, int64_t bt_stride, int32_t bt_cols,
+                        const int32_t* seq_lens, int32_t n_req, int32_t* page2slot,
+                        int32_t* slot2page, int32_t* lru, int32_t* clock, int32_t* miss_pages,
+                        int32_t* miss_cnt, int32_t* victims, int32_t* fetch_list,
+                        int32_t* fetch_cnt, int32_t fetch_cap, int32_t* overflow, int32_t n_kv,
+                        int32_t num_blocks, int32_t hot_slots, int32_t page, void* stream);
+
+/* Replaces Residency.gather_fetch (residency.py:216-268, :461-488) for one
+ * layer: each fetch-list page's V (and K) into its hot slot, from the pinned
+ * pool when pool_valid, else from the staging pool (vbo) with write-through
+ * to the pinned pool (sets pool_valid), else from the pinned pool. */
+int32_t locks_tier_fetch(const int32_t* fetch_list, const int32_t* fetch_cnt, int32_t fetch_cap,
+                         uint16_t* hot_v, uint16_t* hot_k, uint16_t* pool_v, uint16_t* pool_k,
+                         const uint16_t* stage_v, const uint16_t* stage_k,
+                         int64_t stage_stride_block, int64_t stage_stride_tok,
+                         int64_t stage_stride_head, const int32_t* vbo, int8_t* pool_valid,
+                         int32_t layer, int32_t num_layers, int32_t n_kv, int32_t num_blocks,
+                         int32_t hot_slots, int32_t stage_blocks, int32_t page, int32_t head_dim,
+                         int32_t k_tier, void* stream);
+
+/*
  * LSE merge of the split-K partials into the attention output.
  * Replaces merge_splits_kernel (attention/merge.py:105-152).  One workgroup
  * per (request, kv head, query head), so a row's partials are read by G

@@ -18,7 +18,7 @@ CSRC = os.path.join(HERE, "csrc")
 OUT_DIR = os.path.join(HERE, "locks", "_lib")
 LIB = os.path.join(OUT_DIR, "liblocks_hip.so")
 SOURCES = ["locks_capi.cpp", "locks_score.hip", "locks_select.hip", "locks_decode.hip", "locks_build.hip",
-           "locks_mla.hip",
+           "locks_mla.hip", "locks_tier.hip",
            "locks_calib.hip"]
 ARCH = "gfx950"
 EXAMPLES = [("examples/capi_decode.cpp", "capi_decode")]

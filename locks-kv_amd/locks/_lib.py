@@ -49,6 +49,18 @@ SIGNATURES = {
                                         _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
                                         _f32, _p, _p]),
     "locks_host_device_pointer": (_i32, [_p, _p]),
+    "locks_tier_invalidate": (_i32, [_p, _i64, _i32, _p, _p, _i32, _p, _p, _p, _i32, _i32, _i32,
+                                     _i32, _i32, _p]),
+    "locks_tier_stage_begin": (_i32, [_p, _i64, _i32, _p, _p, _i32, _p, _p, _p, _p, _p, _p, _i32,
+                                      _p, _i32, _p, _i32, _i32, _i32, _p]),
+    "locks_tier_flush_copy": (_i32, [_p, _p, _i32, _p, _p, _i64, _i64, _i64, _i64, _p, _p, _p,
+                                     _i32, _i32, _i32, _i32, _i32, _i32, _p]),
+    "locks_tier_scatter": (_i32, [_p, _i64, _i64, _p, _i64, _i64, _i32, _p, _p, _p, _i64, _i64,
+                                  _i64, _i32, _i32, _i32, _i32, _i32, _p]),
+    "locks_tier_plan": (_i32, [_p, _i64, _i64, _i32, _p, _i64, _p, _i64, _i32, _p, _i32, _p, _p,
+                               _p, _p, _p, _p, _p, _p, _p, _i32, _p, _i32, _i32, _i32, _i32, _p]),
+    "locks_tier_fetch": (_i32, [_p, _p, _i32, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _p,
+                                _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p]),
     "locks_decode_fused": (_i32, [_p, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64,
                                   _i32, _p, _i64, _i32, _p, _i64, _i64, _i32, _p, _i64, _p,
                                   _p, _p, _p, _p, _p, _i64, _i64, _i32,

@@ -39,7 +39,8 @@ class ResidentVSource:
         _, v = _split_kv(kv_cache)
         if v is None:
             raise ValueError("ResidentVSource requires a resident V half; this cache is "
-                             "K-only (mem variant, not built for MI355X)")
+                             "K-only: decode it with the DRAM tier's source "
+                             "(locks.tier.TierVSource, mem variants)")
         self._v = v
 
     def args(self):
@@ -120,6 +121,12 @@ def decode_splitk_tier(q, k, v, block_table, seq_lens, page_table, page_cnt, m_p
     k, v: (NB, page, n_kv, d) views of the paged cache; v is never read and
     may be any view of k's shape when the cache holds no V half."""
     NB, page, n_kv, d = k.shape
+    ts = tier_src
+    if (ts.n_kv, ts.page, ts.head_dim, ts.num_blocks) != (n_kv, page, d, NB) \
+            or not 0 <= ts.layer < ts.num_layers:
+        raise ValueError(f"tier laid out for n_kv {ts.n_kv} / page {ts.page} / head_dim {ts.head_dim} / "
+                         f"{ts.num_blocks} blocks, layer {ts.layer} of {ts.num_layers}; the cache is "
+                         f"n_kv {n_kv} / page {page} / head_dim {d} / {NB} blocks")
     lib = _lib.load()
     _lib.check(lib.locks_decode_splitk_tier(
         _lib.ptr(q), q.stride(0), q.stride(1),

@@ -14,7 +14,13 @@ integration spreads this over:
 * the pure single-token decode forward of the attention impl
   (backend/attn.py:338-378): select the pages of every kv head, then the
   split-K sparse decode with the LSE merge.  Other steps (prefill, mixed
-  batches) are the engine's dense attention, as in the reference.
+  batches) are the engine's dense attention, as in the reference;
+* for the DRAM-tier variants (``mem-v`` / ``mem-kv``) the tier of
+  ``locks.tier`` (tier/tier.py:38-302, its decode source :704-784): the
+  prologue runs its per-step lifecycle (tier.py:239-301), ``write_kv``
+  copies each layer's new V (K) into the staging pool (tier.py:386-392),
+  and ``forward`` runs the layer's residency step between selection and the
+  decode, which then reads V (K) through ``TierVSource``.
 
 A vLLM-ROCm attention backend calls ``prologue`` from its metadata builder
 and ``forward`` from its impl; any other engine can drive it directly.
@@ -25,15 +31,18 @@ import torch
 
 from ..attention.decode import _split_kv, ensure_stage_b_buffers
 from ..selection import Rki4State, derive_page_params
+from ..tier import Tier
 from . import _runtime
 from .refresh import RefreshGate
 
 
 class LocksEngine:
     def __init__(self, cfg, kv_caches, *, num_heads_q: int, num_heads_kv: int, head_dim: int,
-                 block_size: int, max_num_seqs: int, max_model_len: int, split: int = 128):
-        if cfg.is_mem:
-            raise ValueError("locks: the DRAM-tier variants are not part of this build")
+                 block_size: int, max_num_seqs: int, max_model_len: int, split: int = 128,
+                 max_num_batched_tokens: int = 8192):
+        if cfg.mem_summary_cache:
+            raise ValueError("locks: mem_summary_cache (summary records in the engine page, K only "
+                             "in the tier) is not built; use mem-kv with the K half resident")
         if num_heads_q % num_heads_kv:
             raise ValueError("num_heads_q must be a multiple of num_heads_kv")
         if not kv_caches:
@@ -54,6 +63,12 @@ class LocksEngine:
         self.st._layer_of = {kv.data_ptr(): i for i, kv in enumerate(self.kv_caches)}
         self.k_layers = [_split_kv(kv)[0] for kv in self.kv_caches]
         self.gate = RefreshGate(page)
+        self.tier = None
+        if cfg.is_mem:
+            self.tier = Tier.from_config(
+                cfg, num_layers=len(self.kv_caches), num_blocks=int(K0.shape[0]),
+                n_kv=int(num_heads_kv), page=page, d=int(head_dim), max_reqs=int(max_num_seqs),
+                max_pages=self.st.max_pages, max_tokens=int(max_num_batched_tokens), device=dev)
 
     @torch.no_grad()
     def prologue(self, block_table, seq_lens, query_start_loc, n_req: int,
@@ -64,6 +79,11 @@ class LocksEngine:
         steps are in the cache.  Returns the state the layers read."""
         if n_req > self.st.max_reqs:
             raise ValueError(f"n_req {n_req} > max_num_seqs {self.st.max_reqs}")
+        if self.tier is not None:
+            qsl = query_start_loc
+            n_tok = (int(query_start_loc_cpu[n_req]) if query_start_loc_cpu is not None
+                     else int(qsl[n_req].item()))
+            self.tier.begin_step(block_table, seq_lens, qsl[: n_req + 1], n_req, n_tok)
         need_derive = self.gate.refresh(self.st, self.k_layers, block_table, seq_lens,
                                         query_start_loc, n_req, seq_lens_cpu,
                                         query_start_loc_cpu)
@@ -78,5 +98,18 @@ class LocksEngine:
         (n_req, H, d) written in place."""
         _state, _derive, select_pages, _graph_safe = _runtime.resolve_selection()
         select_pages(q, kv_cache, block_table, seq_lens, self.st, n_req, scale, self.cfg)
-        _runtime.decode_dispatch(q, kv_cache, block_table, seq_lens, self.st, out, None, scale,
+        vsource = None
+        if self.tier is not None:
+            layer = _runtime._layer_index(self.st, kv_cache)
+            self.tier.step(layer, self.st.page_table, self.st.page_cnt, block_table, seq_lens, n_req)
+            vsource = self.tier.vsource(layer)
+        _runtime.decode_dispatch(q, kv_cache, block_table, seq_lens, self.st, out, vsource, scale,
                                  self.cfg)
+
+    @torch.no_grad()
+    def write_kv(self, layer: int, key, value) -> None:
+        """After the engine wrote this step's K / V (n_tokens, n_kv, d) of one
+        layer into its cache: the DRAM tier's copy of them (tier.py:386-392).
+        A no-op for the resident variant."""
+        if self.tier is not None:
+            self.tier.write_kv(layer, value, key)

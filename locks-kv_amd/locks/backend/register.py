@@ -32,10 +32,6 @@ def register(overrides: dict | None = None) -> None:
               flush=True)
         return
     cfg = LocksConfig.load(overrides)
-    if cfg.is_mem:
-        raise NotImplementedError(
-            f"locks: variant {cfg.variant!r} (DRAM tier) is not part of the MI355X build; "
-            "use variant='fast'")
     _runtime.set_config(cfg)
     try:
         from vllm.platforms import rocm  # noqa: F401

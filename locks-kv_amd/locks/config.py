@@ -2,9 +2,10 @@
 
 Field names, defaults, validation and the ``load()`` precedence mirror the
 reference (src/locks/config.py:26-214) so an existing ``LOCKS_CONFIG`` file
-works unchanged.  This build serves the ``fast`` variant (K+V resident);
-the DRAM-tier ``mem-v`` / ``mem-kv`` variants validate but are refused when
-state is created (they are outside the MI355X hot path built here).
+works unchanged.  Every variant is served: ``fast`` (K+V resident) and the
+DRAM-tier ``mem-v`` / ``mem-kv`` (V, or K and V, decoded from the tier of
+``locks.tier``); ``mem_summary_cache`` (summary records in the engine page)
+is refused when state is created.
 """
 from __future__ import annotations
 

@@ -39,14 +39,14 @@ def _state(case, split):
 
 
 def _tiered(case, d, tab, cnt, k_tier, seed):
-    """TierBuffers with one true source per used (kv head, block); returns
+    """A Tier with one true source per used (kv head, block); returns
     (tier, {(kh, blk): source}) and poisons the cache halves the tier replaces."""
     import torch
-    from locks.tier import TierBuffers
+    from locks.tier import Tier
     rng = np.random.default_rng(seed)
-    t = TierBuffers("cuda", num_layers=LAYERS, num_blocks=case.NB, n_kv=case.n_kv,
-                    head_dim=case.d, page=case.page, hot_slots=HOT_SLOTS,
-                    stage_blocks=STAGE_BLOCKS, offload_k=k_tier)
+    t = Tier("cuda", num_layers=LAYERS, num_blocks=case.NB, n_kv=case.n_kv,
+             head_dim=case.d, page=case.page, hot_slots=HOT_SLOTS, v_blocks=STAGE_BLOCKS,
+             max_tokens=case.page, offload_k=k_tier)
     t.offload(LAYER, d["kv"], np.arange(case.NB))
     # (row, page) of every selected page, its block and completeness
     used = {}
@@ -58,7 +58,7 @@ def _tiered(case, d, tab, cnt, k_tier, seed):
     blocks = sorted({b for (_, b) in used})
     staged = [b for b in blocks if rng.random() < 0.3][:STAGE_BLOCKS]
     for i, b in enumerate(staged):
-        t.stage(LAYER, d["kv"], b, i)
+        t.stage([d["kv"]] * LAYERS, b, i)
     nan = float("nan")
     src = {}
     next_slot = [0] * case.n_kv
@@ -105,6 +105,8 @@ CASES = [
     (8, 4, [16 * 500 + 1, 16 * 200], 128, True, 128, 16),
     (4, 4, [32 * 90 + 7, 32 * 20], 32, True, 64, 32),
     (2, 8, [16 * 200 + 9], 32, False, 256, 16),
+    (2, 4, [64 * 40 + 5, 64 * 9], 16, False, 128, 64),
+    (2, 4, [64 * 40 + 5, 64 * 9], 16, True, 128, 64),
 ]
 
 
@@ -180,9 +182,9 @@ def test_tier_through_the_reference_call_and_graph():
     ref = torch.empty(case.R, H, case.d, dtype=torch.bfloat16, device="cuda")
     decode_dispatch(d["q"], d["kv"], d["bt"], d["sl"], st, ref, None, case.scale, None)
     torch.cuda.synchronize()
-    from locks.tier import TierBuffers
-    t = TierBuffers("cuda", num_layers=1, num_blocks=case.NB, n_kv=n_kv, head_dim=case.d,
-                    hot_slots=HOT_SLOTS, stage_blocks=STAGE_BLOCKS)
+    from locks.tier import Tier
+    t = Tier("cuda", num_layers=1, num_blocks=case.NB, n_kv=n_kv, head_dim=case.d,
+             hot_slots=HOT_SLOTS, v_blocks=STAGE_BLOCKS, max_tokens=16)
     t.offload(0, d["kv"], np.arange(case.NB))
     blk0 = [int(case.bt[0, p]) for p in tab[0, 0, :cnt[0, 0]].tolist()]
     for i, blk in enumerate(blk0[:HOT_SLOTS]):
@@ -206,7 +208,7 @@ def test_tier_through_the_reference_call_and_graph():
         if rep == 1:                                  # evict two hot pages, stage another block
             t.evict(0, 0, blk0[0])
             t.evict(0, 0, blk0[1])
-            t.stage(0, kv_src, blk0[-1], 0)
+            t.stage([kv_src], blk0[-1], 0)
         if rep == 2:
             t.unstage(blk0[-1])
         torch.cuda.synchronize()

@@ -157,16 +157,15 @@ def test_config_surface(monkeypatch, tmp_path):
         LocksConfig.load()
 
 
-def test_register_inert_and_mem_refused(monkeypatch, capsys):
+def test_register_inert_then_registers_any_variant(monkeypatch, capsys):
     import locks
     from locks.backend import _runtime, register as regmod
     monkeypatch.delenv("LOCKS_CONFIG", raising=False)
     monkeypatch.setattr(regmod, "_APPLIED", False)
     locks.register()
     assert "INERT" in capsys.readouterr().out
-    with pytest.raises(NotImplementedError):
-        locks.register({"variant": "mem-v"})
-    locks.register({"budget_pages": 126})
+    locks.register({"variant": "mem-v", "budget_pages": 126})   # the DRAM tier is served
+    assert _runtime.get_config().variant == "mem-v"
     assert _runtime.get_config().budget_pages == 126
 
 
@@ -297,9 +296,9 @@ def test_engine_and_producers_validate_on_the_host():
     from locks.backend.engine import LocksEngine
     from locks.config import LocksConfig
     from locks.selection import rki4_build_tail
-    with pytest.raises(ValueError):
-        LocksEngine(LocksConfig(variant="mem-v"), [torch.zeros(1)], num_heads_q=8,
-                    num_heads_kv=2, head_dim=128, block_size=16, max_num_seqs=1,
+    with pytest.raises(ValueError):                      # summary records in the engine page
+        LocksEngine(LocksConfig(variant="mem-kv", mem_summary_cache=True), [torch.zeros(1)],
+                    num_heads_q=8, num_heads_kv=2, head_dim=128, block_size=16, max_num_seqs=1,
                     max_model_len=64)
     with pytest.raises(ValueError):
         LocksEngine(LocksConfig(), [torch.zeros(1)], num_heads_q=6, num_heads_kv=4,
