@@ -114,7 +114,9 @@ def make_model(wl, budget_pages, seed=0, summaries="build", zsplit=None):
                 NB=NB, build_s=t_build, scale=1.0 / math.sqrt(D))
 
 
-def sparse_step(m, out, vsources=None):
+def sparse_step(m, out, vsources=None, tier=None):
+    """One decode step; with ``tier`` (a locks.tier.Tier) each layer runs the
+    tier's residency step (plan + fetch) between selection and the decode."""
     from locks.backend import _runtime
     from locks.selection import derive_page_params
     st = m["st"]
@@ -123,6 +125,8 @@ def sparse_step(m, out, vsources=None):
         kv = m["kv"][layer]
         _runtime._rki4_select_adapter(m["q"][layer], kv, m["bt"], m["sl"], st, m["R"],
                                       m["scale"], None)
+        if tier is not None:
+            tier.step(layer, st.page_table, st.page_cnt, m["bt"], m["sl"], m["R"])
         _runtime.decode_dispatch(m["q"][layer], kv, m["bt"], m["sl"], st, out[layer],
                                  vsources[layer] if vsources else None, m["scale"], None)
 
@@ -130,12 +134,16 @@ def sparse_step(m, out, vsources=None):
 def make_tier(m, mode):
     """DRAM-tier V source for every layer (mem-v): ``pool`` = every page's V
     in the pinned host pool; ``hot`` = every complete page in a hot slot of
-    its own (slot = block id), partial pages from the pool."""
+    its own (slot = block id), partial pages from the pool; ``lru`` = every
+    page's V in the pinned pool and an empty exact-LRU hot buffer of the
+    reference's default size (6 x the 10 % budget's pages + sink + window per
+    (layer, kv head)), filled by the tier's own residency step."""
     import torch
     from locks.tier import Tier
     L, NB, n_kv = m["L"], m["NB"], m["n_kv"]
+    hot = {"hot": NB, "pool": 1}.get(mode) or Tier.recommend_hot_slots(0.1, m["MP"], n_seqs=m["R"])
     t = Tier("cuda", num_layers=L, num_blocks=NB, n_kv=n_kv, head_dim=D, page=PAGE,
-             hot_slots=NB if mode == "hot" else 1, v_blocks=2, max_tokens=PAGE)
+             hot_slots=hot, max_reqs=m["R"], max_pages=m["MP"], max_tokens=PAGE)
     sls = m["sl"].tolist()
     partial = [int(m["bt"][r, s // PAGE]) for r, s in enumerate(sls) if s % PAGE]
     for layer in range(L):
@@ -704,9 +712,9 @@ def main():
     ap.add_argument("--mla-split", type=int, default=0,
                     help="MLA sparse decode split count (0: the state's default, ~4 pages per split)")
     ap.add_argument("--no-dense", action="store_true")
-    ap.add_argument("--tier", default="", choices=["", "pool", "hot"],
+    ap.add_argument("--tier", default="", choices=["", "pool", "hot", "lru"],
                     help="also time the step with V through the DRAM tier (pinned host pool, "
-                         "or every complete page in a hot slot)")
+                         "every complete page in a hot slot, or the tier's own LRU residency)")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the ragged GLM batch and MLA points of the default run")
     ap.add_argument("--no-1m", action="store_true",
@@ -841,17 +849,39 @@ def measure_gqa(a, wl, workload, summaries=None, quickstart=False):
         tier = make_tier(m, a.tier)
         log(f"{workload}: tier ({a.tier}) ready in {time.perf_counter() - t0:.1f}s")
         vs = [tier.vsource(layer) for layer in range(m["L"])]
+        lru = tier if a.tier == "lru" else None
         out_t = [torch.empty_like(o) for o in out]
-        sparse_step(m, out_t, vs)
+        sparse_step(m, out_t, vs, lru)
         torch.cuda.synchronize()
         assert all(torch.equal(x, y) for x, y in zip(out, out_t)), "tiered step differs from resident"
-        gt = capture(lambda: sparse_step(m, out_t, vs))
+        gt = capture(lambda: sparse_step(m, out_t, vs, lru))
         ms_t = time_graph(gt, a.steps, a.warmup)
         v_bytes = by["decode"] // 2                           # V half of the decode bytes
         res["tier"] = dict(source=a.tier, ms_per_step=round(ms_t, 4),
                            decode_v_bytes_per_step=v_bytes,
                            v_GBps_if_all_extra_time=round(v_bytes / max((ms_t - ms) * 1e-3, 1e-9) / 1e9, 1)
                            if a.tier == "pool" else None)
+        if lru is not None:
+            # steady state above: the selection repeats, every page hits.  Cold:
+            # empty hot buffers before each replay, every selected page misses
+            # and is fetched from the pinned pool over the host link
+            s_ = torch.cuda.current_stream()
+            tot = 0.0
+            for _ in range(5):
+                tier.page2slot.fill_(-1)
+                tier.slot2page.fill_(-1)
+                tier.lru.zero_()
+                tier.clock.zero_()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(s_)
+                gt.replay()
+                e1.record(s_)
+                torch.cuda.synchronize()
+                tot += e0.elapsed_time(e1)
+                assert all(torch.equal(x, y) for x, y in zip(out, out_t)), "cold tiered step differs"
+            res["tier"].update(hot_slots=tier.S, cold_ms_per_step=round(tot / 5, 4),
+                               selected_pages_per_step=int(attended * m["n_kv"] * m["L"] * m["R"]))
+            log(f"{workload}: tier (lru) cold step {tot / 5:.3f} ms")
         log(f"{workload}: tier ({a.tier}) step {ms_t:.3f} ms vs resident {ms:.3f} ms")
         del gt, tier, vs, out_t
         torch.cuda.synchronize()

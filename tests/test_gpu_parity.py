@@ -504,3 +504,86 @@ def test_end_to_end_runtime_path(budget_pages):
     nd = _near_tie_ok(gtab, gcnt, tab, cnt, comb, npg, nsh, b, 1)
     say("near-tie differences:", nd)
     _decode_check(case, st, d, out, gtab, gcnt)
+
+
+def _aliased_case(seed, n_kv, G, seq_len, NB=4096):
+    """A long row (page ids up to seq_len / 16, a block table that wide) over
+    a small physical pool: logical pages map to random blocks of NB, several
+    pages per block.  The decode reads only what the block table names, so
+    the index arithmetic runs at full length without a full-size cache."""
+    import types
+    rng = np.random.default_rng(seed)
+    MP = (seq_len + 15) // 16
+    k, v, _ = O.synth_kv(rng, NB, 16, n_kv, 128)
+    q = O.f32_to_bf16(rng.standard_normal((1, n_kv * G, 128), dtype=np.float32))
+    bt = rng.integers(0, NB, (1, MP), dtype=np.int32)
+    return types.SimpleNamespace(n_kv=n_kv, G=G, seq_lens=[seq_len], MP=MP, NB=NB, k=k, v=v, q=q,
+                                 bt=bt, page=16, d=128, R=1, scale=1.0 / np.sqrt(128))
+
+
+@pytest.mark.parametrize("split,max_cnt", [(128, 128), (128, 0), (64, 10)])
+def test_decode_matches_oracle_at_1m(split, max_cnt):
+    """BASELINE configs[2]'s row: 1M tokens (65 536 pages, page ids to 65 535
+    through a 65 536-wide block table), 2 kv heads x G 16, b = 126 + sink +
+    window spread over the row; bf16 and fp32 outputs at the north-star bar."""
+    import torch
+    from locks.attention import decode_merge, decode_splitk
+    from locks.attention.decode import _pps_min, _split_kv
+    say("decode 1M", split, max_cnt)
+    case = _aliased_case(41, 2, 16, 1 << 20)
+    rng = np.random.default_rng(42)
+    npg, nsh, b = O.derive_page_params(case.seq_lens, 16, 1, 1, 126, 0.1)
+    sc = rng.random((1, 2, case.MP)).astype(np.float32)
+    tab, cnt = O.topb_select(sc, npg, nsh, b, 1, case.MP)
+    assert int(cnt[0, 0]) == 128 and int(tab[0, 0, 127]) == case.MP - 1
+    st = _state(case, split=split)
+    d = to_dev(case)
+    st.page_table.copy_(torch.from_numpy(tab))
+    st.page_cnt.copy_(torch.from_numpy(cnt))
+    k, v = _split_kv(d["kv"])
+    for dt in (torch.bfloat16, torch.float32):
+        out = torch.full((1, 32, 128), float("nan"), dtype=dt, device="cuda")
+        pps = _pps_min(1)
+        decode_splitk(d["q"], k, v, d["bt"], d["sl"], st.page_table, st.page_cnt, st.m_part,
+                      st.l_part, st.acc_part, n_req=1, G=16, split=st.split, pps_min=pps,
+                      scale=case.scale, max_cnt=max_cnt)
+        decode_merge(st.m_part, st.l_part, st.acc_part, st.page_cnt, out, n_req=1, n_kv=2,
+                     G=16, split=st.split, pps_min=pps, pt_cols=st.page_table.shape[2],
+                     max_cnt=max_cnt)
+        torch.cuda.synchronize()
+        _decode_check(case, st, d, out, tab, cnt)
+
+
+@pytest.mark.parametrize("seq_len,split", [(131072, 128), (131072 + 7, 256)])
+def test_dense_comparator_matches_sdpa_at_128k(seq_len, split):
+    """The dense comparator over a whole 128K row (8 192 pages; a partial last
+    page in the second case) against float64 SDPA over the same tokens."""
+    import torch
+    from locks.attention import decode_dense
+    from locks.attention.decode import _split_kv
+    say("dense comparator 128K", seq_len, split)
+    n_kv, G = 8, 4
+    case = _aliased_case(43, n_kv, G, seq_len)
+    d = to_dev(case)
+    k, v = _split_kv(d["kv"])
+    mp = torch.empty(1, n_kv, split, G, device="cuda")
+    lp = torch.empty_like(mp)
+    ap = torch.empty(1, n_kv, split, G, 128, device="cuda")
+    out = torch.full((1, n_kv * G, 128), float("nan"), dtype=torch.bfloat16, device="cuda")
+    decode_dense(d["q"], k, v, d["bt"], d["sl"], mp, lp, ap, out, n_req=1, G=G, split=split,
+                 scale=case.scale)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()[0]
+    npg = (seq_len + 15) // 16
+    K = O.bf16_to_f32(case.k[case.bt[0, :npg]]).reshape(-1, n_kv, 128)[:seq_len]
+    V = O.bf16_to_f32(case.v[case.bt[0, :npg]]).reshape(-1, n_kv, 128)[:seq_len]
+    Q = O.bf16_to_f32(case.q[0]).reshape(n_kv, G, 128)
+    qt = torch.from_numpy(Q).double()
+    kt = torch.from_numpy(K).double().permute(1, 0, 2)[:, None]
+    vt = torch.from_numpy(V).double().permute(1, 0, 2)[:, None]
+    ref = torch.nn.functional.scaled_dot_product_attention(
+        qt[:, :, None], kt.expand(-1, G, -1, -1), vt.expand(-1, G, -1, -1), scale=float(case.scale))
+    rb = O.bf16_round(ref[:, :, 0].reshape(n_kv * G, 128).numpy().astype(np.float32))
+    e = np.abs(got - rb)
+    say(f"dense 128K: max-abs {e.max():.3e} mean-rel {e.sum() / np.abs(rb).sum():.3e}")
+    assert e.max() <= 2e-2 and e.sum() / np.abs(rb).sum() <= 1e-3
