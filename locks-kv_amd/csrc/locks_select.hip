@@ -1174,7 +1174,15 @@ extern "C" int32_t locks_select_nrm_topb(
     int* spill_page = (int*)(ws + cap * Z1 * SEL_CH * 8 + cap * (long)max_pages * 4);
     int* cand_cnt = (int*)(ws + cap * Z1 * SEL_CH * 8 + cap * (long)max_pages * 8);
     int* ghist = cand_cnt + cap * Z1;
-    if (max_pages <= ROW_MAXP && max_pages % 4 == 0 && max_pages > SEL_CH) {
+    // A whole row's score_h (G x pages x 4 B) goes through one CU in the row
+    // kernel; above 64K (head, page) entries the page-parallel chunk route
+    // wins (GLM G = 16, measured per step: 8192 pages 1.485 -> 1.400 ms;
+    // 4096 pages 1.202 row vs 1.355 chunk)
+#ifndef SEL_ROW_MAX_GP
+#define SEL_ROW_MAX_GP 65536L
+#endif
+    if (max_pages <= ROW_MAXP && max_pages % 4 == 0 && max_pages > SEL_CH &&
+        (long)G * max_pages <= SEL_ROW_MAX_GP) {
 #define ROW_LAUNCH(EV)                                                                     \
         hipLaunchKernelGGL((sel_row_kernel<EV>), dim3(n_kv, n_req), dim3(ROW_BLK), 0, st, score_h, \
                            page_max, score_chunks, n_pages, n_sel_hi, b_fix, score, page_table, \
