@@ -762,7 +762,15 @@ def main():
     if a.ladder:
         run_ladder(a, wl)
         return
+    # the default run also times the Llama step through the DRAM tier's own
+    # LRU residency (the `tier` object of the line); the other workloads run
+    # resident
+    default_tier = a.workload == "llama8b-128k" and not a.no_extra and not a.tier
+    if default_tier:
+        a.tier = "lru"
     res = measure_gqa(a, wl, a.workload, quickstart=(a.workload == "llama8b-128k"))
+    if default_tier:
+        a.tier = ""
     if res is None:
         return
     line, ms = res
