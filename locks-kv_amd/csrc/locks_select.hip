@@ -790,7 +790,7 @@ constexpr int F2_CAP = F2_BLK * 16;                    // register-resident cand
 // BAND = true (large budgets): add the chunk's key histogram (top 12 bits)
 // into the row's global histogram instead; sel_band_kernel then emits the
 // candidates at or above the row's boundary bin.
-template <bool BAND>
+template <bool BAND, int E = C2_E>
 __global__ __launch_bounds__(C2_BLK) void sel_chunk2_kernel(
     const float* __restrict__ score_h, const float* __restrict__ pmax, int Zs,
     const int* __restrict__ npg, const int* __restrict__ nsh, const int* __restrict__ bfix,
@@ -803,8 +803,11 @@ __global__ __launch_bounds__(C2_BLK) void sel_chunk2_kernel(
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const long rk = (long)r * n_kv + kh;
     const int n_sel_hi = min(nsh[r], MP);
-    const int c0 = z * SEL_CH;
-    const int p0 = c0 + C2_E * tid;                     // this thread's C2_E pages
+    static_assert(E == 1 || E == 2, "one or two pages per thread");
+    static_assert(!BAND || E == C2_E, "the band route keeps 2048-page chunks");
+    constexpr int CH = E * C2_BLK;                      // pages per chunk
+    const int c0 = z * CH;
+    const int p0 = c0 + E * tid;                        // this thread's E pages
 
     __shared__ float hm[16];
     __shared__ int hist[4096];
@@ -816,11 +819,15 @@ __global__ __launch_bounds__(C2_BLK) void sel_chunk2_kernel(
     const float* shb = score_h + rk * (long)G * MP;
     float2 xv[16];
 #pragma unroll
-    for (int g = 0; g < 16; ++g)                         // clamped, unconditional (see the row kernel)
-        xv[g] = *reinterpret_cast<const float2*>(shb + (long)min(g, G - 1) * MP + min(p0, MP - 2));
+    for (int g = 0; g < 16; ++g) {                       // clamped, unconditional (see the row kernel)
+        if constexpr (E == 2)
+            xv[g] = *reinterpret_cast<const float2*>(shb + (long)min(g, G - 1) * MP + min(p0, MP - 2));
+        else
+            xv[g] = make_float2(shb[(long)min(g, G - 1) * MP + min(p0, MP - 1)], 0.f);
+    }
     int* trow = page_table + rk * (long)MP;
 #pragma unroll
-    for (int e = 0; e < C2_E; ++e)
+    for (int e = 0; e < E; ++e)
         if (p0 + e < MP) trow[p0 + e] = -1;
     if (combine == 0) {
         for (int g = wave; g < G; g += C2_BLK / kWave) {
@@ -829,15 +836,15 @@ __global__ __launch_bounds__(C2_BLK) void sel_chunk2_kernel(
         }
         lds_barrier();
     }
-    float acc[C2_E];
+    float acc[E];
 #pragma unroll
-    for (int e = 0; e < C2_E; ++e) acc[e] = (combine == 0) ? 0.f : -INFINITY;
+    for (int e = 0; e < E; ++e) acc[e] = (combine == 0) ? 0.f : -INFINITY;
 #pragma unroll
     for (int g = 0; g < 16; ++g) {
         if (g < G) {
             const float x4[2] = {xv[g].x, xv[g].y};
 #pragma unroll
-            for (int e = 0; e < C2_E; ++e) {
+            for (int e = 0; e < E; ++e) {
                 if (combine == 0) acc[e] += __expf(x4[e] - hm[g]);
                 else acc[e] = (g == 0) ? x4[e] : fmaxf(acc[e], x4[e]);
             }
@@ -845,21 +852,25 @@ __global__ __launch_bounds__(C2_BLK) void sel_chunk2_kernel(
     }
     const int pend = max(n_sel_hi, 0);
     float* srow = score + rk * (long)MP;
-    if (p0 + C2_E <= pend) {
-        *reinterpret_cast<float2*>(srow + p0) = make_float2(acc[0], acc[1]);
-    } else {
+    if constexpr (E == 2) {
+        if (p0 + E <= pend) {
+            *reinterpret_cast<float2*>(srow + p0) = make_float2(acc[0], acc[E - 1]);
+        } else {
 #pragma unroll
-        for (int e = 0; e < C2_E; ++e)
-            if (p0 + e < pend) srow[p0 + e] = acc[e];
+            for (int e = 0; e < E; ++e)
+                if (p0 + e < pend) srow[p0 + e] = acc[e];
+        }
+    } else {
+        if (p0 < pend) srow[p0] = acc[0];
     }
     const int n_sel = n_sel_hi - n_sink;
     int b = bfix[r];
     b = max(1, min(b, max(n_sel, 1)));
-    uint32_t key[C2_E];
-    bool val[C2_E];
+    uint32_t key[E];
+    bool val[E];
     int nv = 0;
 #pragma unroll
-    for (int e = 0; e < C2_E; ++e) {
+    for (int e = 0; e < E; ++e) {
         const int p = p0 + e;
         val[e] = (n_sel > 1) && p >= n_sink && p < n_sel_hi;
         key[e] = f2u(acc[e]);
@@ -869,7 +880,7 @@ __global__ __launch_bounds__(C2_BLK) void sel_chunk2_kernel(
         for (int i = tid; i < 4096; i += C2_BLK) hist[i] = 0;
         lds_barrier();
 #pragma unroll
-        for (int e = 0; e < C2_E; ++e) hist_add(hist, (int)(key[e] >> 20), val[e]);
+        for (int e = 0; e < E; ++e) hist_add(hist, (int)(key[e] >> 20), val[e]);
         lds_barrier();
         int* gh = ghist + rk * 4096;
         for (int i = tid; i < 4096; i += C2_BLK)
@@ -884,8 +895,8 @@ __global__ __launch_bounds__(C2_BLK) void sel_chunk2_kernel(
     if (n_loc > 0) {
         const int k_loc = min(b, n_loc);
         RadixSel rs{0u, 0u, 0, true};                    // k_loc == n_loc: keep every valid key (>= 0)
-        if (k_loc < n_loc) rs = reg_kth_largest<C2_BLK, C2_E>(key, val, k_loc, hist, wtot, s3);
-        ncand = reg_emit<C2_BLK, C2_E>(key, val, rs, wsum, [&](int pos, int e) {
+        if (k_loc < n_loc) rs = reg_kth_largest<C2_BLK, E>(key, val, k_loc, hist, wtot, s3);
+        ncand = reg_emit<C2_BLK, E>(key, val, rs, wsum, [&](int pos, int e) {
             ck[pos] = key[e];
             cp[pos] = p0 + e;
         });
@@ -1130,9 +1141,14 @@ static long sel_row_bytes(long Z1, long max_pages) {
     return Z1 * SEL_CH * 8 + max_pages * 8 + Z1 * 4 + 4096 * 4;
 }
 
+// Chunk lists are laid out for the largest chunk count any route uses: the
+// 1024-page chunks of the small-budget page-parallel route (each list keeps
+// its SEL_CH-entry slot).
+constexpr int SEL_CH_MIN = SEL_CH / 2;
+
 extern "C" int64_t locks_select_workspace_bytes(int32_t n_req, int32_t n_kv, int32_t max_pages) {
     if (n_req < 0 || n_kv < 1 || max_pages < 1) return -1;
-    const long Z1 = cdiv(max_pages, SEL_CH);
+    const long Z1 = cdiv(max_pages, SEL_CH_MIN);
     const long rows = (long)n_req * n_kv;
     const long bytes = rows * sel_row_bytes(Z1, max_pages);
     return (bytes + 255) / 256 * 256;
@@ -1166,14 +1182,15 @@ extern "C" int32_t locks_select_nrm_topb(
     // call's n_req: the band route's row histograms must stay zero between
     // calls (the finisher clears them), so they may never move onto bytes a
     // call with another batch size used for candidates.
-    const long cap = workspace ? (long)(workspace_bytes / sel_row_bytes(Z1, max_pages)) : 0;
+    const long ZW = cdiv(max_pages, SEL_CH_MIN);           // chunk slots per row in the layout
+    const long cap = workspace ? (long)(workspace_bytes / sel_row_bytes(ZW, max_pages)) : 0;
     uint8_t* ws = (uint8_t*)workspace;
     uint32_t* cand_key = (uint32_t*)ws;
-    int* cand_page = (int*)(ws + cap * Z1 * SEL_CH * 4);
-    uint32_t* spill_key = (uint32_t*)(ws + cap * Z1 * SEL_CH * 8);
-    int* spill_page = (int*)(ws + cap * Z1 * SEL_CH * 8 + cap * (long)max_pages * 4);
-    int* cand_cnt = (int*)(ws + cap * Z1 * SEL_CH * 8 + cap * (long)max_pages * 8);
-    int* ghist = cand_cnt + cap * Z1;
+    int* cand_page = (int*)(ws + cap * ZW * SEL_CH * 4);
+    uint32_t* spill_key = (uint32_t*)(ws + cap * ZW * SEL_CH * 8);
+    int* spill_page = (int*)(ws + cap * ZW * SEL_CH * 8 + cap * (long)max_pages * 4);
+    int* cand_cnt = (int*)(ws + cap * ZW * SEL_CH * 8 + cap * (long)max_pages * 8);
+    int* ghist = cand_cnt + cap * ZW;
     // A whole row's score_h (G x pages x 4 B) goes through one CU in the row
     // kernel; above 64K (head, page) entries the page-parallel chunk route
     // wins (GLM G = 16, measured per step: 8192 pages 1.485 -> 1.400 ms;
@@ -1197,6 +1214,25 @@ extern "C" int32_t locks_select_nrm_topb(
         // the histogram (band) route is faster (measured at 256K..1M with
         // b = 1638..6553: 25-36 us against 40-160 us).
         const bool band = (long)b_max * Z1 > F2_BLK * 4;
+        // With a small budget and a wide GQA group, 1024-page chunks (one page
+        // per thread) halve the score_h each workgroup pulls through its CU
+        // (G x 4 KB), while the finisher's lists still fit its slotted
+        // layout (GLM G = 16, measured per step: 128K 1.379 -> 1.285 ms, 256K 1.530 ->
+        // 1.440, 512K 1.791 -> 1.708, ragged batch 2.047 -> 1.977)
+        const int Zs = cdiv(max_pages, SEL_CH_MIN);
+        const bool small_chunks = !band && G > 4 && (long)Zs * cdiv(min(b_max, SEL_CH), 4) <= F2_BLK;
+        if (small_chunks) {
+            hipLaunchKernelGGL((sel_chunk2_kernel<false, 1>), dim3(Zs, n_kv, n_req), dim3(C2_BLK), 0, st,
+                               score_h, page_max, score_chunks, n_pages, n_sel_hi, b_fix, score,
+                               page_table, cand_key, cand_page, cand_cnt, nullptr, n_sink, max_pages,
+                               G, combine);
+            int rc = check_launch("sel_chunk2_kernel<small>");
+            if (rc) return rc;
+            hipLaunchKernelGGL(sel_finish2_kernel, dim3(1, n_kv, n_req), dim3(F2_BLK), 0, st,
+                               n_pages, n_sel_hi, b_fix, page_table, page_cnt, cand_key, cand_page,
+                               cand_cnt, spill_key, spill_page, nullptr, n_sink, max_pages, Zs);
+            return check_launch("sel_finish2_kernel");
+        }
         if (band) {
             hipLaunchKernelGGL(sel_chunk2_kernel<true>, dim3(Z1, n_kv, n_req), dim3(C2_BLK), 0, st,
                                score_h, page_max, score_chunks, n_pages, n_sel_hi, b_fix, score,
