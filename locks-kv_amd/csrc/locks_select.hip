@@ -1198,7 +1198,10 @@ extern "C" int32_t locks_select_nrm_topb(
 #ifndef SEL_ROW_MAX_GP
 #define SEL_ROW_MAX_GP 65536L
 #endif
-    if (max_pages <= ROW_MAXP && max_pages % 4 == 0 && max_pages > SEL_CH &&
+    // The row kernel also serves rows of one chunk or less: against the
+    // single-chunk kernel it measured GLM 16K 1.225 -> 1.083 ms and 32K
+    // 1.327 -> 1.104 ms per step
+    if (max_pages <= ROW_MAXP && max_pages % 4 == 0 &&
         (long)G * max_pages <= SEL_ROW_MAX_GP) {
 #define ROW_LAUNCH(EV)                                                                     \
         hipLaunchKernelGGL((sel_row_kernel<EV>), dim3(n_kv, n_req), dim3(ROW_BLK), 0, st, score_h, \
