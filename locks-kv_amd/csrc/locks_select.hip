@@ -31,6 +31,8 @@
 // slower than the second launch.)
 // Radix keys are the order-preserving fp32 -> u32 map; the keep test is a
 // key compare, so it is exact for every finite score.
+#include <type_traits>
+
 #include "locks_common.h"
 #include "locks_hip.h"
 
@@ -1058,28 +1060,38 @@ __global__ __launch_bounds__(F2_BLK) void sel_finish2_kernel(
     // consecutive threads, 4 slots each, so thread order is page order and the
     // counts load in the same round trip as the candidates (no offset scan).
     // Only on the local-top-b route (no histogram): band lists can be longer.
-    const int tpc = cdiv(min(b, SEL_CH), 4);          // threads per chunk list
-    if (!ghist && (long)Z1 * tpc <= F2_BLK) {
-        const int z = tid / tpc, sl = (tid - z * tpc) * 4;
+    // (4 slots per thread; 8 when the lists need more than the workgroup's
+    // threads at 4, e.g. 64 chunks of 1024 pages at 1M)
+    auto slotted = [&](auto slots) {
+        constexpr int SL = decltype(slots)::value;
+        const int tpc = cdiv(min(b, SEL_CH), SL);          // threads per chunk list
+        const int z = tid / tpc, sl = (tid - z * tpc) * SL;
         const bool zin = z < Z1;
         const long src = (rk * Z1 + (zin ? z : 0)) * (long)SEL_CH + sl;
         const int czl = cand_cnt[rk * Z1 + (zin ? z : 0)];
-        uint32_t key[4];
-        int page[4];
-        bool val[4];
+        uint32_t key[SL];
+        int page[SL];
+        bool val[SL];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {                     // slots past the count are masked
+        for (int e = 0; e < SL; ++e) {                     // slots past the count are masked
             key[e] = cand_key[src + e];
             page[e] = cand_page[src + e];
         }
         const int cz = zin ? czl : 0;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
+        for (int e = 0; e < SL; ++e) {
             val[e] = zin && sl + e < cz;
             if (!val[e]) key[e] = 0u;
         }
-        finish2_select<4>(rk, b, n_sink, n_pages, n_sel_hi, trow, page_cnt, key, page, val, hist,
-                          wtot, s3, wsum);
+        finish2_select<SL>(rk, b, n_sink, n_pages, n_sel_hi, trow, page_cnt, key, page, val, hist,
+                           wtot, s3, wsum);
+    };
+    if (!ghist && (long)Z1 * cdiv(min(b, SEL_CH), 4) <= F2_BLK) {
+        slotted(std::integral_constant<int, 4>{});
+        return;
+    }
+    if (!ghist && (long)Z1 * cdiv(min(b, SEL_CH), 8) <= F2_BLK) {
+        slotted(std::integral_constant<int, 8>{});
         return;
     }
     {
@@ -1220,10 +1232,11 @@ extern "C" int32_t locks_select_nrm_topb(
         // With a small budget and a wide GQA group, 1024-page chunks (one page
         // per thread) halve the score_h each workgroup pulls through its CU
         // (G x 4 KB), while the finisher's lists still fit its slotted
-        // layout (GLM G = 16, measured per step: 128K 1.379 -> 1.285 ms, 256K 1.530 ->
-        // 1.440, 512K 1.791 -> 1.708, ragged batch 2.047 -> 1.977)
+        // layout, at 8 slots per thread when 4 do not fit (GLM G = 16, measured
+        // per step: 128K 1.379 -> 1.285 ms, 256K 1.530 -> 1.440, 512K 1.791 ->
+        // 1.708, ragged batch 2.047 -> 1.977; 1M, 64 chunks: 2.297 -> 2.25-2.27)
         const int Zs = cdiv(max_pages, SEL_CH_MIN);
-        const bool small_chunks = !band && G > 4 && (long)Zs * cdiv(min(b_max, SEL_CH), 4) <= F2_BLK;
+        const bool small_chunks = !band && G > 4 && (long)Zs * cdiv(min(b_max, SEL_CH), 8) <= F2_BLK;
         if (small_chunks) {
             hipLaunchKernelGGL((sel_chunk2_kernel<false, 1>), dim3(Zs, n_kv, n_req), dim3(C2_BLK), 0, st,
                                score_h, page_max, score_chunks, n_pages, n_sel_hi, b_fix, score,
