@@ -400,7 +400,7 @@ def cpu_baseline(a, runs=10, warmup=2):
 # --------------------------------------------------------------------------- #
 # MLA (config 5)
 # --------------------------------------------------------------------------- #
-def make_mla_model(wl, seed=0, rope="exact", split=None):
+def make_mla_model(wl, seed=0, rope="exact", split=None, zsplit=None):
     import torch
     from locks.selection import MlaState, mla_build_blocks
     dev = torch.device("cuda")
@@ -433,6 +433,8 @@ def make_mla_model(wl, seed=0, rope="exact", split=None):
         torch.cuda.synchronize()
         t_build += time.perf_counter() - t0
     st._layer_of = {c.data_ptr(): i for i, c in enumerate(caches)}
+    if zsplit:                                   # scorer chunks per request (sweeps)
+        st.score_chunk = max(2, 2 * ((MP + 2 * zsplit - 1) // (2 * zsplit)))
     q = [torch.randn(R, H, MLA_LKV + MLA_DR, generator=g, device=dev).to(torch.bfloat16)
          for _ in range(L)]
     sl = torch.tensor(sls, dtype=torch.int32, device=dev)
@@ -558,7 +560,7 @@ def measure_mla(a, wl, workload, cpu=True):
     latent comparator, scorer roofline; returns the JSON line."""
     import torch
     t0 = time.perf_counter()
-    m = make_mla_model(wl, rope=a.mla_rope, split=a.mla_split or None)
+    m = make_mla_model(wl, rope=a.mla_rope, split=a.mla_split or None, zsplit=a.zsplit or None)
     log(f"MLA model ready in {time.perf_counter() - t0:.1f}s (latent summary build {m['build_s']:.1f}s)")
     R, H, L = m["R"], m["H"], m["L"]
     out = [torch.empty(R, H, MLA_LKV, dtype=torch.bfloat16, device="cuda") for _ in range(L)]
