@@ -674,13 +674,15 @@ __global__ __launch_bounds__(MH_BLK) void decode_merge_heads_kernel(
     // indices clamped into the buffers (entries past the active count are
     // masked below, never combined), so the merge costs one round trip.
     const int cnt_raw = pcnt ? pcnt[(long)r * cnt_sr + kh] : seq_lens[r];
+    // (clamped to the launched splits, not the buffer's: rows past them were
+    // never written this call, and reading them only doubled the traffic)
     float4 pre[MH_PF];
 #pragma unroll
     for (int k = 0; k < MH_PF; ++k) {
-        const int sidx = min(strm + k * MH_STREAMS, split - 1);
+        const int sidx = min(strm + k * MH_STREAMS, nsplit - 1);
         pre[k] = *reinterpret_cast<const float4*>(acc_part + ((rk * split + sidx) * G + g) * D + col * 4);
     }
-    const long ml0 = (rk * split + min(tid, split - 1)) * G + g;
+    const long ml0 = (rk * split + min(tid, nsplit - 1)) * G + g;
     const float m0 = m_part[ml0], l0 = l_part[ml0];
     const int cnt = pcnt ? min(cnt_raw, pt_cols) : min(cdiv(cnt_raw, pg), bt_cols);
     const int pps = max(cdiv(cnt, nsplit), pps_min);
