@@ -22,8 +22,10 @@
 //   * mu . q8 uses the same MFMA with B = one mu row per column (page);
 //   * the per-token reconstruction sum_c c8[t][c] qt[g][c] is a 16x8 by
 //     8xG product per page: v_mfma_f32_16x16x4_f32 with pages packed side by
-//     side when G < 16 (block-diagonal B), so the VALU only does the cs/mu
-//     epilogue and the 16-token LSE (4 tokens per lane + 2 cross-row steps).
+//     side when 4 < G < 16 (block-diagonal B); for G <= 4,
+//     v_mfma_f32_4x4x1_16b_f32 with one 4x4 block per (page, 4-token quad),
+//     so no block-diagonal zeros are multiplied.  The VALU only does the
+//     cs/mu epilogue and the 16-token LSE.
 // Summary bytes are read exactly once, DMA'd straight from the six slabs
 // (through the block table) into per-wave LDS stages, one unit ahead.  Per-WG page maxima are published to `pmax` so the
 // selector can form the per-head max without re-reading score_h.
@@ -159,6 +161,10 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
     const int jcol = lane & 15;
     const int psub_l = jcol / GW;            // page slot of this lane's column
     const int g_l = jcol % GW;               // head of this lane's column
+    // G <= 4: the token stage runs on v_mfma_f32_4x4x1_16b_f32, 16 blocks of
+    // (page, 4-token quad) x 4 heads, instead of block-diagonal 16x16x4
+    // products three quarters zero
+    constexpr bool TK4 = (GW == 4);
     const uint32_t MH = 0xF0F0F0F0u;
     const int n_tiles = cdiv(c1 - c0, SC_TILE);
     const int n_units = n_tiles;             // (8-page tile) units of the chunk
@@ -301,7 +307,7 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
     {
         const float qsj = qsp[r16 % GW] * 0.0625f;
 #pragma unroll
-        for (int ps = 0; ps < PPM; ++ps) qsjm[ps] = (psub_l == ps) ? qsj : 0.f;
+        for (int ps = 0; ps < PPM; ++ps) qsjm[ps] = (TK4 || psub_l == ps) ? qsj : 0.f;
     }
 
     float wrun = -INFINITY;                          // running per-head max of this lane's column
@@ -327,14 +333,21 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
         // qt[pp][v] = qt[head j % GW][page 2pp + (v & 1)][column 2kg + (v >> 1)],
         // which is exactly the B operand the token stage needs (its k-slot
         // kg, step hh reads column 2kg + hh), so qt never goes through LDS.
-        const int i_pg = r16 & 1, i_c = 2 * (r16 >> 2) + ((r16 >> 1) & 1);
+        // TK4: MFMA pp covers pages 4 (pp >> 1) .. + 3 x columns 4 (pp & 1) ..
+        // + 3 (row 4a + b <-> page 4 (pp >> 1) + a, column 4 (pp & 1) + b), so
+        // lane group kg ends with all 8 columns of page 4 gi + kg, the B
+        // operand of its 4x4 blocks.
+        const int i_pg = TK4 ? (r16 >> 2) : (r16 & 1);
+        const int i_c = TK4 ? (r16 & 3) : 2 * (r16 >> 2) + ((r16 >> 1) & 1);
+        auto pr_page = [&](int pp, int i) { return TK4 ? 4 * (pp >> 1) + i : 2 * pp + i; };
+        auto pr_col = [&](int pp, int i) { return TK4 ? 4 * (pp & 1) + i : i; };
         // lane group kg reads D / 8 packed bytes (d in [kg D / 4, (kg + 1) D / 4))
         uint32_t vv[4][D / 32];
         float2 vsf[4][2];
 #pragma unroll
         for (int pp = 0; pp < 4; ++pp) {
             // (page 2pp + i_pg, column i_c); lane group kg: bytes kg D / 8 ..
-            const uint8_t* rp = st + (2 * pp + i_pg) * RB + i_c * (D / 2) + kg * (D / 8);
+            const uint8_t* rp = st + pr_page(pp, i_pg) * RB + pr_col(pp, i_c) * (D / 2) + kg * (D / 8);
             if constexpr (D == 64) {
                 const uint2 x = *reinterpret_cast<const uint2*>(rp);
                 vv[pp][0] = x.x; vv[pp][1] = x.y;
@@ -345,10 +358,16 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
                     vv[pp][4 * k] = x.x; vv[pp][4 * k + 1] = x.y; vv[pp][4 * k + 2] = x.z; vv[pp][4 * k + 3] = x.w;
                 }
             }
+            if constexpr (TK4) {                    // column scales 4 (pp & 1) .. + 3 of page 4 (pp >> 1) + kg
+                const uint2 w = *reinterpret_cast<const uint2*>(st + pr_page(pp, kg) * RB + O_VS + 8 * (pp & 1));
+                vsf[pp][0] = make_float2(bf16lo(w.x), bf16hi(w.x));
+                vsf[pp][1] = make_float2(bf16lo(w.y), bf16hi(w.y));
+            } else {
 #pragma unroll
-            for (int pg = 0; pg < 2; ++pg) {        // column scales (2kg, 2kg+1) of page 2pp+pg
-                const uint32_t w = *reinterpret_cast<const uint32_t*>(st + (2 * pp + pg) * RB + O_VS + kg * 4);
-                vsf[pp][pg] = make_float2(bf16lo(w), bf16hi(w));
+                for (int pg = 0; pg < 2; ++pg) {    // column scales (2kg, 2kg+1) of page 2pp+pg
+                    const uint32_t w = *reinterpret_cast<const uint32_t*>(st + (2 * pp + pg) * RB + O_VS + kg * 4);
+                    vsf[pp][pg] = make_float2(bf16lo(w), bf16hi(w));
+                }
             }
         }
         v4i mu[NWIN];
@@ -379,8 +398,13 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
             // the column scale, a power of two, so qt is exact to the same bits
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const float2 w = vsf[pp][v & 1];
-                qt[pp][v] = (float)acc[v] * ((v >> 1) ? w.y : w.x) * qsjm[(2 * pp + (v & 1)) % PPM];
+                if constexpr (TK4) {
+                    const float2 w = vsf[pp][v >> 1];
+                    qt[pp][v] = (float)acc[v] * ((v & 1) ? w.y : w.x) * qsjm[0];
+                } else {
+                    const float2 w = vsf[pp][v & 1];
+                    qt[pp][v] = (float)acc[v] * ((v >> 1) ? w.y : w.x) * qsjm[(2 * pp + (v & 1)) % PPM];
+                }
             }
         }
         {
@@ -402,111 +426,186 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
         // ---- token reconstruction + PG-token LSE per (page, head) --------
         // k-slot kg, step hh <-> basis column 2kg + hh (both operands);
         // tokens in blocks of 16 (tb < PG / 16)
-        auto tok_group = [&](int gi, int tb) -> v4f {   // cs * (C8 qt) of group gi, 4 tokens
+        if constexpr (TK4) {
+        // 4x4 block b = 4 kg + qd: page 4 gi + kg, tokens 4 qd .. 4 qd + 3 (A
+        // lane 4 b + i: token 4 qd + i = r16), columns = heads (lane & 3).
+        // One k step per basis column c; B = qt of the lane's own page, column
+        // c (projection pair 2 gi + (c >> 2), element c & 3).  The token
+        // scale rides on the coefficient operand (int8 x bf16 is exact in
+        // fp32).  Lane (kg, qd, g) receives tokens 4 qd .. + 3 of (page, head g).
+        auto tok4 = [&](int gi, int tb) -> v4f {
+            const uint8_t* rp = st + (4 * gi + kg) * RB;
+            const uint2 cw = *reinterpret_cast<const uint2*>(rp + O_C8 + (16 * tb + r16) * 8);
+            const float cf = __uint_as_float((uint32_t)*reinterpret_cast<const uint16_t*>(rp + O_CS + (16 * tb + r16) * 2) << 16);
             v4f acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int ps = 0; ps < PPM; ++ps) {
-                const int page = gi * PPM + ps;
-                const uint8_t* rp = st + page * RB;
-                const uint32_t cw = *reinterpret_cast<const uint16_t*>(rp + O_C8 + (16 * tb + r16) * 8 + 2 * kg);
-                // the token scale rides on the coefficient operand: int8 x
-                // bf16 is exact in fp32
-                const float cf = __uint_as_float((uint32_t)*reinterpret_cast<const uint16_t*>(rp + O_CS + (16 * tb + r16) * 2) << 16);
-                const float a0 = (float)(int8_t)cw * cf, a1 = (float)(int8_t)(cw >> 8) * cf;
-                // qt is already zero where this lane's column is not page slot ps
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, qt[page >> 1][page & 1], acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, qt[page >> 1][2 + (page & 1)], acc, 0, 0, 0);
+            for (int c = 0; c < 8; ++c) {
+                const uint32_t w = (c < 4) ? cw.x : cw.y;
+                const float a = (float)(int8_t)(w >> (8 * (c & 3))) * cf;
+                acc = __builtin_amdgcn_mfma_f32_4x4x1f32(a, qt[2 * gi + (c >> 2)][c & 3], acc, 0, 0, 0);
             }
             return acc;
         };
-        // 16-token LSE taken relative to the centroid term: tok - mud =
-        // cs * acc.  The exp2 sum is exact whenever it lies in [2^-60, 2^60]
-        // (no overflow; flushed terms < 2^-62 of the sum).  All groups are
-        // formed first (independent matrix-core chains interleave), then one
-        // wave-wide test picks this fast form or the exact-max recomputation.
-        // Per-lane partial sums (4 tokens) of every group, then one
-        // transposing reduction per 4 groups: two row-pair swaps and one
-        // half swap leave group 4s + kg's 16-token total in row kg (same
-        // pairing and order as a per-group butterfly, so the same bits).
-        // Each lane then finishes only its own row's group.
-        constexpr int NSET = (NGRP + 3) / 4;
-        float ev[NGRP];
+        const int qd = r16 >> 2;
+        float ev[2] = {0.f, 0.f};
 #pragma unroll
-        for (int gi = 0; gi < NGRP; ++gi) {
-            ev[gi] = 0.f;
-#pragma unroll
-            for (int tb = 0; tb < NTB; ++tb) {
-                const v4f x = tok_group(gi, tb);
-                ev[gi] += __builtin_amdgcn_exp2f(x[0]) + __builtin_amdgcn_exp2f(x[1]) +
-                          __builtin_amdgcn_exp2f(x[2]) + __builtin_amdgcn_exp2f(x[3]);
-            }
+        for (int tb = 0; tb < NTB; ++tb) {
+            const v4f x0 = tok4(0, tb), x1 = tok4(1, tb);
+            ev[0] += __builtin_amdgcn_exp2f(x0[0]) + __builtin_amdgcn_exp2f(x0[1]) +
+                     __builtin_amdgcn_exp2f(x0[2]) + __builtin_amdgcn_exp2f(x0[3]);
+            ev[1] += __builtin_amdgcn_exp2f(x1[0]) + __builtin_amdgcn_exp2f(x1[1]) +
+                     __builtin_amdgcn_exp2f(x1[2]) + __builtin_amdgcn_exp2f(x1[3]);
         }
-        float tot[NSET];
+        // sum over the 4 quads of a (page, head): lanes 4 apart in the row
 #pragma unroll
-        for (int sx = 0; sx < NSET; ++sx) {
-            auto pair16 = [](float u, float v) {
-                const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(u), __float_as_uint(v), false, false);
-                return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-            };
-            if constexpr (NGRP >= 4) {
-                const float A = pair16(ev[4 * sx], ev[4 * sx + 1]);      // rows: g0 01, g1 01, g0 23, g1 23
-                const float B = pair16(ev[4 * sx + 2], ev[4 * sx + 3]);  // rows: g2 01, g3 01, g2 23, g3 23
-                const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(A), __float_as_uint(B), false, false);
-                tot[sx] = __uint_as_float(r[0]) + __uint_as_float(r[1]); // row k: group 4 sx + k
-            } else {
-                tot[sx] = xor32_sum(pair16(ev[0], ev[1]));               // row k: group k & 1
-            }
+        for (int gi = 0; gi < 2; ++gi) {
+            ev[gi] += row_ror<4>(ev[gi]);
+            ev[gi] += row_ror<8>(ev[gi]);
         }
-        auto grp_of = [&](int sx) { return (NGRP >= 4) ? 4 * sx + kg : (kg & 1); };
-        bool ok = true;
-#pragma unroll
-        for (int sx = 0; sx < NSET; ++sx) ok = ok && (tot[sx] >= 0x1p-60f) && (tot[sx] <= 0x1p60f);
-        float Sv[NSET];
+        // quads 0-1 finish group 0, quads 2-3 group 1 (one log per lane)
+        const int gsel = qd >> 1;
+        const float tot = gsel ? ev[1] : ev[0];
+        const int page = 4 * gsel + kg;
+        const bool ok = (tot >= 0x1p-60f) && (tot <= 0x1p60f);
+        float Sv;
         if (__builtin_expect(__ballot(!ok) == 0ull, 1)) {
-#pragma unroll
-            for (int sx = 0; sx < NSET; ++sx)
-                Sv[sx] = (*mud_at(grp_of(sx) * PPM + psub_l, g_l) + __builtin_amdgcn_logf(tot[sx])) *
-                         0.6931471805599453f;
+            Sv = (*mud_at(page, g_l) + __builtin_amdgcn_logf(tot)) * 0.6931471805599453f;
         } else {
-            // exact-max form (rare): every lane computes every group
-            float Sa[NGRP];
+            // exact-max form (rare)
+            float Sa[2];
 #pragma unroll
-            for (int gi = 0; gi < NGRP; ++gi) {
+            for (int gi = 0; gi < 2; ++gi) {
                 v4f x[NTB];
                 float m = -INFINITY;
 #pragma unroll
                 for (int tb = 0; tb < NTB; ++tb) {
-                    x[tb] = tok_group(gi, tb);
+                    x[tb] = tok4(gi, tb);
                     m = fmaxf(m, fmaxf(fmaxf(x[tb][0], x[tb][1]), fmaxf(x[tb][2], x[tb][3])));
                 }
-                m = xor32_max(xor16_max(m));
+                m = fmaxf(m, row_ror<4>(m));
+                m = fmaxf(m, row_ror<8>(m));
                 float f = 0.f;
 #pragma unroll
                 for (int tb = 0; tb < NTB; ++tb)
                     f += __builtin_amdgcn_exp2f(x[tb][0] - m) + __builtin_amdgcn_exp2f(x[tb][1] - m) +
                          __builtin_amdgcn_exp2f(x[tb][2] - m) + __builtin_amdgcn_exp2f(x[tb][3] - m);
-                f = xor32_sum(xor16_sum(f));
-                Sa[gi] = ((*mud_at(gi * PPM + psub_l, g_l) + m) + __builtin_amdgcn_logf(f)) * 0.6931471805599453f;
+                f += row_ror<4>(f);
+                f += row_ror<8>(f);
+                Sa[gi] = ((*mud_at(4 * gi + kg, g_l) + m) + __builtin_amdgcn_logf(f)) * 0.6931471805599453f;
             }
-#pragma unroll
+            Sv = gsel ? Sa[1] : Sa[0];
+        }
+        if ((qd & 1) == 0 && page < nvalid && g_l < G) {
+            wrun = fmaxf(wrun, Sv);
+            score_h[(((long)r * n_kv + h) * G + g_l) * (long)MP + p0 + page] = Sv;
+        }
+        } else {
+            auto tok_group = [&](int gi, int tb) -> v4f {   // cs * (C8 qt) of group gi, 4 tokens
+                v4f acc = {0.f, 0.f, 0.f, 0.f};
+    #pragma unroll
+                for (int ps = 0; ps < PPM; ++ps) {
+                    const int page = gi * PPM + ps;
+                    const uint8_t* rp = st + page * RB;
+                    const uint32_t cw = *reinterpret_cast<const uint16_t*>(rp + O_C8 + (16 * tb + r16) * 8 + 2 * kg);
+                    // the token scale rides on the coefficient operand: int8 x
+                    // bf16 is exact in fp32
+                    const float cf = __uint_as_float((uint32_t)*reinterpret_cast<const uint16_t*>(rp + O_CS + (16 * tb + r16) * 2) << 16);
+                    const float a0 = (float)(int8_t)cw * cf, a1 = (float)(int8_t)(cw >> 8) * cf;
+                    // qt is already zero where this lane's column is not page slot ps
+                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, qt[page >> 1][page & 1], acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, qt[page >> 1][2 + (page & 1)], acc, 0, 0, 0);
+                }
+                return acc;
+            };
+            // 16-token LSE taken relative to the centroid term: tok - mud =
+            // cs * acc.  The exp2 sum is exact whenever it lies in [2^-60, 2^60]
+            // (no overflow; flushed terms < 2^-62 of the sum).  All groups are
+            // formed first (independent matrix-core chains interleave), then one
+            // wave-wide test picks this fast form or the exact-max recomputation.
+            // Per-lane partial sums (4 tokens) of every group, then one
+            // transposing reduction per 4 groups: two row-pair swaps and one
+            // half swap leave group 4s + kg's 16-token total in row kg (same
+            // pairing and order as a per-group butterfly, so the same bits).
+            // Each lane then finishes only its own row's group.
+            constexpr int NSET = (NGRP + 3) / 4;
+            float ev[NGRP];
+    #pragma unroll
+            for (int gi = 0; gi < NGRP; ++gi) {
+                ev[gi] = 0.f;
+    #pragma unroll
+                for (int tb = 0; tb < NTB; ++tb) {
+                    const v4f x = tok_group(gi, tb);
+                    ev[gi] += __builtin_amdgcn_exp2f(x[0]) + __builtin_amdgcn_exp2f(x[1]) +
+                              __builtin_amdgcn_exp2f(x[2]) + __builtin_amdgcn_exp2f(x[3]);
+                }
+            }
+            float tot[NSET];
+    #pragma unroll
             for (int sx = 0; sx < NSET; ++sx) {
-                float v = Sa[0];
-#pragma unroll
-                for (int gi = 1; gi < NGRP; ++gi) v = (grp_of(sx) == gi) ? Sa[gi] : v;
-                Sv[sx] = v;
+                auto pair16 = [](float u, float v) {
+                    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(u), __float_as_uint(v), false, false);
+                    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+                };
+                if constexpr (NGRP >= 4) {
+                    const float A = pair16(ev[4 * sx], ev[4 * sx + 1]);      // rows: g0 01, g1 01, g0 23, g1 23
+                    const float B = pair16(ev[4 * sx + 2], ev[4 * sx + 3]);  // rows: g2 01, g3 01, g2 23, g3 23
+                    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(A), __float_as_uint(B), false, false);
+                    tot[sx] = __uint_as_float(r[0]) + __uint_as_float(r[1]); // row k: group 4 sx + k
+                } else {
+                    tot[sx] = xor32_sum(pair16(ev[0], ev[1]));               // row k: group k & 1
+                }
             }
-        }
-        float tmax = -INFINITY;
-        const bool row_owner = (NGRP >= 4) || (kg < 2);      // rows 2, 3 repeat rows 0, 1
-#pragma unroll
-        for (int sx = 0; sx < NSET; ++sx) {
-            const int page = grp_of(sx) * PPM + psub_l;
-            if (row_owner && (page < nvalid) && (g_l < G)) {
-                tmax = fmaxf(tmax, Sv[sx]);
-                score_h[(((long)r * n_kv + h) * G + g_l) * (long)MP + p0 + page] = Sv[sx];
+            auto grp_of = [&](int sx) { return (NGRP >= 4) ? 4 * sx + kg : (kg & 1); };
+            bool ok = true;
+    #pragma unroll
+            for (int sx = 0; sx < NSET; ++sx) ok = ok && (tot[sx] >= 0x1p-60f) && (tot[sx] <= 0x1p60f);
+            float Sv[NSET];
+            if (__builtin_expect(__ballot(!ok) == 0ull, 1)) {
+    #pragma unroll
+                for (int sx = 0; sx < NSET; ++sx)
+                    Sv[sx] = (*mud_at(grp_of(sx) * PPM + psub_l, g_l) + __builtin_amdgcn_logf(tot[sx])) *
+                             0.6931471805599453f;
+            } else {
+                // exact-max form (rare): every lane computes every group
+                float Sa[NGRP];
+    #pragma unroll
+                for (int gi = 0; gi < NGRP; ++gi) {
+                    v4f x[NTB];
+                    float m = -INFINITY;
+    #pragma unroll
+                    for (int tb = 0; tb < NTB; ++tb) {
+                        x[tb] = tok_group(gi, tb);
+                        m = fmaxf(m, fmaxf(fmaxf(x[tb][0], x[tb][1]), fmaxf(x[tb][2], x[tb][3])));
+                    }
+                    m = xor32_max(xor16_max(m));
+                    float f = 0.f;
+    #pragma unroll
+                    for (int tb = 0; tb < NTB; ++tb)
+                        f += __builtin_amdgcn_exp2f(x[tb][0] - m) + __builtin_amdgcn_exp2f(x[tb][1] - m) +
+                             __builtin_amdgcn_exp2f(x[tb][2] - m) + __builtin_amdgcn_exp2f(x[tb][3] - m);
+                    f = xor32_sum(xor16_sum(f));
+                    Sa[gi] = ((*mud_at(gi * PPM + psub_l, g_l) + m) + __builtin_amdgcn_logf(f)) * 0.6931471805599453f;
+                }
+    #pragma unroll
+                for (int sx = 0; sx < NSET; ++sx) {
+                    float v = Sa[0];
+    #pragma unroll
+                    for (int gi = 1; gi < NGRP; ++gi) v = (grp_of(sx) == gi) ? Sa[gi] : v;
+                    Sv[sx] = v;
+                }
             }
+            float tmax = -INFINITY;
+            const bool row_owner = (NGRP >= 4) || (kg < 2);      // rows 2, 3 repeat rows 0, 1
+    #pragma unroll
+            for (int sx = 0; sx < NSET; ++sx) {
+                const int page = grp_of(sx) * PPM + psub_l;
+                if (row_owner && (page < nvalid) && (g_l < G)) {
+                    tmax = fmaxf(tmax, Sv[sx]);
+                    score_h[(((long)r * n_kv + h) * G + g_l) * (long)MP + p0 + page] = Sv[sx];
+                }
+            }
+            wrun = fmaxf(wrun, tmax);
         }
-        wrun = fmaxf(wrun, tmax);
         // the DMA source registers stay allocated until here: a VGPR that a
         // pending DMA reads its address from is not reused (a later write to
         // it would have to wait for the DMA)
@@ -528,7 +627,7 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
 #pragma unroll
     for (int o = GW; o < 16; o <<= 1)        // max over the lanes of one head column
         wrun = fmaxf(wrun, o == 4 ? row_ror<4>(wrun) : o == 8 ? row_ror<8>(wrun) : row_ror<2>(wrun));
-    if ((NGRP >= 4 || kg < 2) && (lane & 15) < GW && (lane & 15) < G) atomicMax(&wmax[lane & 15], f2u(wrun));
+    if ((TK4 || NGRP >= 4 || kg < 2) && (lane & 15) < GW && (lane & 15) < G) atomicMax(&wmax[lane & 15], f2u(wrun));
     __syncthreads();
     if (tid < 16) pm_out[tid] = u2f(wmax[tid]);
 }
