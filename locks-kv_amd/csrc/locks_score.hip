@@ -90,7 +90,7 @@ __device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d) {
            ((uint32_t)(uint8_t)c << 16) | ((uint32_t)(uint8_t)d << 24);
 }
 
-template <int GW, int D = 128, int PG = 16, bool PK = true>
+template <int GW, int D = 128, int PG = 16, bool PK = true, bool PIPE = true>
 __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
     const uint16_t* __restrict__ q, long q_sr, long q_sh, SlabRows S, int NB, const int* __restrict__ bt, long bt_sr, int bt_cols,
     const int* __restrict__ nsh, float* __restrict__ score_h, int MP,
@@ -125,6 +125,9 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
     __shared__ __attribute__((aligned(16))) uint8_t sa_l[SC_WAVES][GM::ST_BYTES];
     __shared__ __attribute__((aligned(16))) uint8_t sb_l[SC_WAVES][GM::ST_BYTES];
     __shared__ uint32_t wmax[16];
+    // PIPE: centroid terms mud[page][head] of a wave's last two units (rows
+    // 8-15: idle lanes); otherwise they go to the unit's consumed stage rows
+    __shared__ __attribute__((aligned(16))) float mud_l[PIPE ? SC_WAVES : 1][2][PIPE ? 16 * 16 : 4];
     // dynamic LDS: slab rows (block x n_kv + kv head) of the chunk
     extern __shared__ __attribute__((aligned(16))) int dyn_l[];
     int* bt_l = dyn_l;
@@ -311,18 +314,40 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
     }
 
     float wrun = -INFINITY;                          // running per-head max of this lane's column
-    auto score_unit = [&](int u, uint8_t* st, uint8_t* st_next) {
-        // per-page centroid terms mud[page][head] go into the first 64 B of
-        // the page's stage row (packed V, consumed by then)
-        auto mud_at = [&](int page, int g) -> float* { return reinterpret_cast<float*>(st + page * RB) + g; };
+    // Software pipeline over a wave's units.  front(u) waits for unit u's
+    // rows, reads every operand of the unit from its stage into registers
+    // (packed V, column scales, centroid, and the token stage's coefficients
+    // and token scales), issues the next unit's DMA, and runs the projection
+    // and centroid MFMAs; back(u) runs the token stage, the LSE and the
+    // stores from those registers and the unit's centroid terms.  A wave
+    // runs front(u + 4) before back(u): the two chains are independent and
+    // share one basic block, so the scheduler interleaves the projection of
+    // one unit with the token MFMAs and exponentials of the one before.  No
+    // stage holds live data after its front, so two stages per wave still
+    // suffice; the centroid terms mud[page][head] go to a per-wave buffer of
+    // two slots (rows 8-15 of a slot take the idle lanes' stores).
+    // Without PIPE (grids of three workgroups per CU, which the pipeline's
+    // registers and buffer do not fit) each unit runs front then back, and
+    // mud goes into the first 64 B of each page's stage row (packed V,
+    // consumed by then).
+    constexpr int MUD_RS = PIPE ? 16 : RB / 4;                 // mud row stride (floats)
+    struct Carry {
+        float qt[4][4];
+        uint2 c8w[TK4 ? 2 : 1][NTB];              // TK4: 8 coefficients of (page 4 gi + kg, token)
+        uint32_t tw[TK4 ? 2 : SC_TILE][NTB];      // TK4: token scale bits; else cw | cs << 16
+        int p0, nvalid;
+        UnitSrc nf;                               // next unit's DMA sources
+        bool more;
+    };
+    auto front = [&](int u, uint8_t* st, uint8_t* st_next, float* mud) -> Carry {
         __builtin_amdgcn_s_waitcnt(0x0070);          // this unit's rows have landed in the stage
         wave_lds_sync();
         const float musf = ((lane & 15) < 8) ? bf16lo(fmus) : 0.f;   // before the next unit's load
-        const bool more = u + SC_WAVES < n_units;
-        UnitSrc nf;
-        if (more) nf = unit_src(u + SC_WAVES);
-        const int p0 = c0 + u * SC_TILE;
-        const int nvalid = min(SC_TILE, c1 - p0);
+        Carry c;
+        c.more = u + SC_WAVES < n_units;
+        if (c.more) c.nf = unit_src(u + SC_WAVES);
+        c.p0 = c0 + u * SC_TILE;
+        c.nvalid = min(SC_TILE, c1 - c.p0);
 
         wave_lds_sync();
 
@@ -346,7 +371,6 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
         float2 vsf[4][2];
 #pragma unroll
         for (int pp = 0; pp < 4; ++pp) {
-            // (page 2pp + i_pg, column i_c); lane group kg: bytes kg D / 8 ..
             const uint8_t* rp = st + pr_page(pp, i_pg) * RB + pr_col(pp, i_c) * (D / 2) + kg * (D / 8);
             if constexpr (D == 64) {
                 const uint2 x = *reinterpret_cast<const uint2*>(rp);
@@ -379,11 +403,31 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
             for (int w = 0; w < NWIN; ++w)
                 mu[w] = *reinterpret_cast<const v4i*>(st + pg * RB + O_MU + kg * (D / 4) + 16 * w);
         }
+        // token-stage operands: coefficients and token scales of the lane's
+        // token row (16 tb + r16)
+#pragma unroll
+        for (int tb = 0; tb < NTB; ++tb) {
+            if constexpr (TK4) {
+#pragma unroll
+                for (int gi = 0; gi < 2; ++gi) {
+                    const uint8_t* rp = st + (4 * gi + kg) * RB;
+                    c.c8w[gi][tb] = *reinterpret_cast<const uint2*>(rp + O_C8 + (16 * tb + r16) * 8);
+                    c.tw[gi][tb] = *reinterpret_cast<const uint16_t*>(rp + O_CS + (16 * tb + r16) * 2);
+                }
+            } else {
+#pragma unroll
+                for (int page = 0; page < SC_TILE; ++page) {
+                    const uint8_t* rp = st + page * RB;
+                    const uint32_t cw = *reinterpret_cast<const uint16_t*>(rp + O_C8 + (16 * tb + r16) * 8 + 2 * kg);
+                    const uint32_t cs = *reinterpret_cast<const uint16_t*>(rp + O_CS + (16 * tb + r16) * 2);
+                    c.tw[page][tb] = cw | (cs << 16);
+                }
+            }
+        }
         // the next unit's rows stream in under this unit's projection and
-        // token stages (issued after the V / centroid reads, which the
-        // compiler would otherwise hold behind the DMA)
-        if (more) issue(nf, st_next);
-        float qt[4][4];
+        // the previous unit's token stage (issued after every read of this
+        // stage, which the compiler would otherwise hold behind the DMA)
+        if (c.more) issue(c.nf, st_next);
 #pragma unroll
         for (int pp = 0; pp < 4; ++pp) {
             // signed nibbles moved to the high half of each byte: 16 * V as int8
@@ -400,10 +444,10 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
             for (int v = 0; v < 4; ++v) {
                 if constexpr (TK4) {
                     const float2 w = vsf[pp][v >> 1];
-                    qt[pp][v] = (float)acc[v] * ((v & 1) ? w.y : w.x) * qsjm[0];
+                    c.qt[pp][v] = (float)acc[v] * ((v & 1) ? w.y : w.x) * qsjm[0];
                 } else {
                     const float2 w = vsf[pp][v & 1];
-                    qt[pp][v] = (float)acc[v] * ((v >> 1) ? w.y : w.x) * qsjm[(2 * pp + (v & 1)) % PPM];
+                    c.qt[pp][v] = (float)acc[v] * ((v >> 1) ? w.y : w.x) * qsjm[(2 * pp + (v & 1)) % PPM];
                 }
             }
         }
@@ -412,20 +456,21 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
 #pragma unroll
             for (int w = 0; w < NWIN; ++w)
                 accm = __builtin_amdgcn_mfma_i32_16x16x64_i8(Amu[w], mu[w], accm, 0, 0, 0);
-            if ((lane & 15) < 8) {
-                float4 md;
-                md.x = (float)accm[0] * qsl.x * musf;
-                md.y = (float)accm[1] * qsl.y * musf;
-                md.z = (float)accm[2] * qsl.z * musf;
-                md.w = (float)accm[3] * qsl.w * musf;
-                *reinterpret_cast<float4*>(mud_at(lane & 15, 4 * kg)) = md;
-            }
+            float4 md;                               // PIPE: lanes & 15 >= 8 store zeros into rows 8-15
+            md.x = (float)accm[0] * qsl.x * musf;
+            md.y = (float)accm[1] * qsl.y * musf;
+            md.z = (float)accm[2] * qsl.z * musf;
+            md.w = (float)accm[3] * qsl.w * musf;
+            if (PIPE || (lane & 15) < 8)
+                *reinterpret_cast<float4*>(mud + (lane & 15) * MUD_RS + 4 * kg) = md;
         }
-        wave_lds_sync();
+        return c;
+    };
 
+    auto back = [&](const Carry& c, const float* mud) {
+        auto mud_at = [&](int page, int g) -> float { return mud[page * MUD_RS + g]; };
+        const int p0 = c.p0, nvalid = c.nvalid;
         // ---- token reconstruction + PG-token LSE per (page, head) --------
-        // k-slot kg, step hh <-> basis column 2kg + hh (both operands);
-        // tokens in blocks of 16 (tb < PG / 16)
         if constexpr (TK4) {
         // 4x4 block b = 4 kg + qd: page 4 gi + kg, tokens 4 qd .. 4 qd + 3 (A
         // lane 4 b + i: token 4 qd + i = r16), columns = heads (lane & 3).
@@ -434,15 +479,14 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
         // scale rides on the coefficient operand (int8 x bf16 is exact in
         // fp32).  Lane (kg, qd, g) receives tokens 4 qd .. + 3 of (page, head g).
         auto tok4 = [&](int gi, int tb) -> v4f {
-            const uint8_t* rp = st + (4 * gi + kg) * RB;
-            const uint2 cw = *reinterpret_cast<const uint2*>(rp + O_C8 + (16 * tb + r16) * 8);
-            const float cf = __uint_as_float((uint32_t)*reinterpret_cast<const uint16_t*>(rp + O_CS + (16 * tb + r16) * 2) << 16);
+            const uint2 cw = c.c8w[gi][tb];
+            const float cf = __uint_as_float(c.tw[gi][tb] << 16);
             v4f acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int c = 0; c < 8; ++c) {
-                const uint32_t w = (c < 4) ? cw.x : cw.y;
-                const float a = (float)(int8_t)(w >> (8 * (c & 3))) * cf;
-                acc = __builtin_amdgcn_mfma_f32_4x4x1f32(a, qt[2 * gi + (c >> 2)][c & 3], acc, 0, 0, 0);
+            for (int k = 0; k < 8; ++k) {
+                const uint32_t w = (k < 4) ? cw.x : cw.y;
+                const float a = (float)(int8_t)(w >> (8 * (k & 3))) * cf;
+                acc = __builtin_amdgcn_mfma_f32_4x4x1f32(a, c.qt[2 * gi + (k >> 2)][k & 3], acc, 0, 0, 0);
             }
             return acc;
         };
@@ -469,7 +513,7 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
         const bool ok = (tot >= 0x1p-60f) && (tot <= 0x1p60f);
         float Sv;
         if (__builtin_expect(__ballot(!ok) == 0ull, 1)) {
-            Sv = (*mud_at(page, g_l) + __builtin_amdgcn_logf(tot)) * 0.6931471805599453f;
+            Sv = (mud_at(page, g_l) + __builtin_amdgcn_logf(tot)) * 0.6931471805599453f;
         } else {
             // exact-max form (rare)
             float Sa[2];
@@ -491,7 +535,7 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
                          __builtin_amdgcn_exp2f(x[tb][2] - m) + __builtin_amdgcn_exp2f(x[tb][3] - m);
                 f += row_ror<4>(f);
                 f += row_ror<8>(f);
-                Sa[gi] = ((*mud_at(4 * gi + kg, g_l) + m) + __builtin_amdgcn_logf(f)) * 0.6931471805599453f;
+                Sa[gi] = ((mud_at(4 * gi + kg, g_l) + m) + __builtin_amdgcn_logf(f)) * 0.6931471805599453f;
             }
             Sv = gsel ? Sa[1] : Sa[0];
         }
@@ -500,127 +544,157 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
             score_h[(((long)r * n_kv + h) * G + g_l) * (long)MP + p0 + page] = Sv;
         }
         } else {
-            auto tok_group = [&](int gi, int tb) -> v4f {   // cs * (C8 qt) of group gi, 4 tokens
-                v4f acc = {0.f, 0.f, 0.f, 0.f};
-    #pragma unroll
-                for (int ps = 0; ps < PPM; ++ps) {
-                    const int page = gi * PPM + ps;
-                    const uint8_t* rp = st + page * RB;
-                    const uint32_t cw = *reinterpret_cast<const uint16_t*>(rp + O_C8 + (16 * tb + r16) * 8 + 2 * kg);
-                    // the token scale rides on the coefficient operand: int8 x
-                    // bf16 is exact in fp32
-                    const float cf = __uint_as_float((uint32_t)*reinterpret_cast<const uint16_t*>(rp + O_CS + (16 * tb + r16) * 2) << 16);
-                    const float a0 = (float)(int8_t)cw * cf, a1 = (float)(int8_t)(cw >> 8) * cf;
-                    // qt is already zero where this lane's column is not page slot ps
-                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, qt[page >> 1][page & 1], acc, 0, 0, 0);
-                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, qt[page >> 1][2 + (page & 1)], acc, 0, 0, 0);
-                }
-                return acc;
+        // k-slot kg, step hh <-> basis column 2kg + hh (both operands);
+        // tokens in blocks of 16 (tb < PG / 16)
+        auto tok_group = [&](int gi, int tb) -> v4f {   // cs * (C8 qt) of group gi, 4 tokens
+            v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ps = 0; ps < PPM; ++ps) {
+                const int page = gi * PPM + ps;
+                const uint32_t w = c.tw[page][tb];
+                // the token scale rides on the coefficient operand: int8 x
+                // bf16 is exact in fp32
+                const float cf = __uint_as_float(w & 0xFFFF0000u);
+                const float a0 = (float)(int8_t)w * cf, a1 = (float)(int8_t)(w >> 8) * cf;
+                // qt is already zero where this lane's column is not page slot ps
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, c.qt[page >> 1][page & 1], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, c.qt[page >> 1][2 + (page & 1)], acc, 0, 0, 0);
+            }
+            return acc;
+        };
+        // 16-token LSE taken relative to the centroid term: tok - mud =
+        // cs * acc.  The exp2 sum is exact whenever it lies in [2^-60, 2^60]
+        // (no overflow; flushed terms < 2^-62 of the sum).  All groups are
+        // formed first (independent matrix-core chains interleave), then one
+        // wave-wide test picks this fast form or the exact-max recomputation.
+        // Per-lane partial sums (4 tokens) of every group, then one
+        // transposing reduction per 4 groups: two row-pair swaps and one
+        // half swap leave group 4s + kg's 16-token total in row kg (same
+        // pairing and order as a per-group butterfly, so the same bits).
+        // Each lane then finishes only its own row's group.
+        constexpr int NSET = (NGRP + 3) / 4;
+        float ev[NGRP];
+#pragma unroll
+        for (int gi = 0; gi < NGRP; ++gi) {
+            ev[gi] = 0.f;
+#pragma unroll
+            for (int tb = 0; tb < NTB; ++tb) {
+                const v4f x = tok_group(gi, tb);
+                ev[gi] += __builtin_amdgcn_exp2f(x[0]) + __builtin_amdgcn_exp2f(x[1]) +
+                          __builtin_amdgcn_exp2f(x[2]) + __builtin_amdgcn_exp2f(x[3]);
+            }
+        }
+        float tot[NSET];
+#pragma unroll
+        for (int sx = 0; sx < NSET; ++sx) {
+            auto pair16 = [](float u, float v) {
+                const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(u), __float_as_uint(v), false, false);
+                return __uint_as_float(r[0]) + __uint_as_float(r[1]);
             };
-            // 16-token LSE taken relative to the centroid term: tok - mud =
-            // cs * acc.  The exp2 sum is exact whenever it lies in [2^-60, 2^60]
-            // (no overflow; flushed terms < 2^-62 of the sum).  All groups are
-            // formed first (independent matrix-core chains interleave), then one
-            // wave-wide test picks this fast form or the exact-max recomputation.
-            // Per-lane partial sums (4 tokens) of every group, then one
-            // transposing reduction per 4 groups: two row-pair swaps and one
-            // half swap leave group 4s + kg's 16-token total in row kg (same
-            // pairing and order as a per-group butterfly, so the same bits).
-            // Each lane then finishes only its own row's group.
-            constexpr int NSET = (NGRP + 3) / 4;
-            float ev[NGRP];
-    #pragma unroll
-            for (int gi = 0; gi < NGRP; ++gi) {
-                ev[gi] = 0.f;
-    #pragma unroll
-                for (int tb = 0; tb < NTB; ++tb) {
-                    const v4f x = tok_group(gi, tb);
-                    ev[gi] += __builtin_amdgcn_exp2f(x[0]) + __builtin_amdgcn_exp2f(x[1]) +
-                              __builtin_amdgcn_exp2f(x[2]) + __builtin_amdgcn_exp2f(x[3]);
-                }
-            }
-            float tot[NSET];
-    #pragma unroll
-            for (int sx = 0; sx < NSET; ++sx) {
-                auto pair16 = [](float u, float v) {
-                    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(u), __float_as_uint(v), false, false);
-                    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-                };
-                if constexpr (NGRP >= 4) {
-                    const float A = pair16(ev[4 * sx], ev[4 * sx + 1]);      // rows: g0 01, g1 01, g0 23, g1 23
-                    const float B = pair16(ev[4 * sx + 2], ev[4 * sx + 3]);  // rows: g2 01, g3 01, g2 23, g3 23
-                    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(A), __float_as_uint(B), false, false);
-                    tot[sx] = __uint_as_float(r[0]) + __uint_as_float(r[1]); // row k: group 4 sx + k
-                } else {
-                    tot[sx] = xor32_sum(pair16(ev[0], ev[1]));               // row k: group k & 1
-                }
-            }
-            auto grp_of = [&](int sx) { return (NGRP >= 4) ? 4 * sx + kg : (kg & 1); };
-            bool ok = true;
-    #pragma unroll
-            for (int sx = 0; sx < NSET; ++sx) ok = ok && (tot[sx] >= 0x1p-60f) && (tot[sx] <= 0x1p60f);
-            float Sv[NSET];
-            if (__builtin_expect(__ballot(!ok) == 0ull, 1)) {
-    #pragma unroll
-                for (int sx = 0; sx < NSET; ++sx)
-                    Sv[sx] = (*mud_at(grp_of(sx) * PPM + psub_l, g_l) + __builtin_amdgcn_logf(tot[sx])) *
-                             0.6931471805599453f;
+            if constexpr (NGRP >= 4) {
+                const float A = pair16(ev[4 * sx], ev[4 * sx + 1]);      // rows: g0 01, g1 01, g0 23, g1 23
+                const float B = pair16(ev[4 * sx + 2], ev[4 * sx + 3]);  // rows: g2 01, g3 01, g2 23, g3 23
+                const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(A), __float_as_uint(B), false, false);
+                tot[sx] = __uint_as_float(r[0]) + __uint_as_float(r[1]); // row k: group 4 sx + k
             } else {
-                // exact-max form (rare): every lane computes every group
-                float Sa[NGRP];
-    #pragma unroll
-                for (int gi = 0; gi < NGRP; ++gi) {
-                    v4f x[NTB];
-                    float m = -INFINITY;
-    #pragma unroll
-                    for (int tb = 0; tb < NTB; ++tb) {
-                        x[tb] = tok_group(gi, tb);
-                        m = fmaxf(m, fmaxf(fmaxf(x[tb][0], x[tb][1]), fmaxf(x[tb][2], x[tb][3])));
-                    }
-                    m = xor32_max(xor16_max(m));
-                    float f = 0.f;
-    #pragma unroll
-                    for (int tb = 0; tb < NTB; ++tb)
-                        f += __builtin_amdgcn_exp2f(x[tb][0] - m) + __builtin_amdgcn_exp2f(x[tb][1] - m) +
-                             __builtin_amdgcn_exp2f(x[tb][2] - m) + __builtin_amdgcn_exp2f(x[tb][3] - m);
-                    f = xor32_sum(xor16_sum(f));
-                    Sa[gi] = ((*mud_at(gi * PPM + psub_l, g_l) + m) + __builtin_amdgcn_logf(f)) * 0.6931471805599453f;
-                }
-    #pragma unroll
-                for (int sx = 0; sx < NSET; ++sx) {
-                    float v = Sa[0];
-    #pragma unroll
-                    for (int gi = 1; gi < NGRP; ++gi) v = (grp_of(sx) == gi) ? Sa[gi] : v;
-                    Sv[sx] = v;
-                }
+                tot[sx] = xor32_sum(pair16(ev[0], ev[1]));               // row k: group k & 1
             }
-            float tmax = -INFINITY;
-            const bool row_owner = (NGRP >= 4) || (kg < 2);      // rows 2, 3 repeat rows 0, 1
-    #pragma unroll
+        }
+        auto grp_of = [&](int sx) { return (NGRP >= 4) ? 4 * sx + kg : (kg & 1); };
+        bool ok = true;
+#pragma unroll
+        for (int sx = 0; sx < NSET; ++sx) ok = ok && (tot[sx] >= 0x1p-60f) && (tot[sx] <= 0x1p60f);
+        float Sv[NSET];
+        if (__builtin_expect(__ballot(!ok) == 0ull, 1)) {
+#pragma unroll
+            for (int sx = 0; sx < NSET; ++sx)
+                Sv[sx] = (mud_at(grp_of(sx) * PPM + psub_l, g_l) + __builtin_amdgcn_logf(tot[sx])) *
+                         0.6931471805599453f;
+        } else {
+            // exact-max form (rare): every lane computes every group
+            float Sa[NGRP];
+#pragma unroll
+            for (int gi = 0; gi < NGRP; ++gi) {
+                v4f x[NTB];
+                float m = -INFINITY;
+#pragma unroll
+                for (int tb = 0; tb < NTB; ++tb) {
+                    x[tb] = tok_group(gi, tb);
+                    m = fmaxf(m, fmaxf(fmaxf(x[tb][0], x[tb][1]), fmaxf(x[tb][2], x[tb][3])));
+                }
+                m = xor32_max(xor16_max(m));
+                float f = 0.f;
+#pragma unroll
+                for (int tb = 0; tb < NTB; ++tb)
+                    f += __builtin_amdgcn_exp2f(x[tb][0] - m) + __builtin_amdgcn_exp2f(x[tb][1] - m) +
+                         __builtin_amdgcn_exp2f(x[tb][2] - m) + __builtin_amdgcn_exp2f(x[tb][3] - m);
+                f = xor32_sum(xor16_sum(f));
+                Sa[gi] = ((mud_at(gi * PPM + psub_l, g_l) + m) + __builtin_amdgcn_logf(f)) * 0.6931471805599453f;
+            }
+#pragma unroll
             for (int sx = 0; sx < NSET; ++sx) {
-                const int page = grp_of(sx) * PPM + psub_l;
-                if (row_owner && (page < nvalid) && (g_l < G)) {
-                    tmax = fmaxf(tmax, Sv[sx]);
-                    score_h[(((long)r * n_kv + h) * G + g_l) * (long)MP + p0 + page] = Sv[sx];
-                }
+                float v = Sa[0];
+#pragma unroll
+                for (int gi = 1; gi < NGRP; ++gi) v = (grp_of(sx) == gi) ? Sa[gi] : v;
+                Sv[sx] = v;
             }
-            wrun = fmaxf(wrun, tmax);
         }
-        // the DMA source registers stay allocated until here: a VGPR that a
-        // pending DMA reads its address from is not reused (a later write to
-        // it would have to wait for the DMA)
-        if (more) {
+        float tmax = -INFINITY;
+        const bool row_owner = (NGRP >= 4) || (kg < 2);      // rows 2, 3 repeat rows 0, 1
 #pragma unroll
-            for (int i = 0; i < (PK ? NDI : 1); ++i) asm volatile("" :: "v"(nf.off[i]));
-#pragma unroll
-            for (int i = 0; i < (PK ? 1 : NDI); ++i) asm volatile("" :: "v"(nf.addr[i]));
-            asm volatile("" :: "v"(nf.mus));
+        for (int sx = 0; sx < NSET; ++sx) {
+            const int page = grp_of(sx) * PPM + psub_l;
+            if (row_owner && (page < nvalid) && (g_l < G)) {
+                tmax = fmaxf(tmax, Sv[sx]);
+                score_h[(((long)r * n_kv + h) * G + g_l) * (long)MP + p0 + page] = Sv[sx];
+            }
         }
-        wave_lds_sync();                               // stages reused by the unit after next
+        wrun = fmaxf(wrun, tmax);
+        }
     };
-    for (int u = wave; u < n_units; u += 2 * SC_WAVES) {
-        score_unit(u, sa_l[wave], sb_l[wave]);
-        if (u + SC_WAVES < n_units) score_unit(u + SC_WAVES, sb_l[wave], sa_l[wave]);
+    // a pending DMA's source registers stay allocated until the unit after
+    // it has been waited for (a write to one would have to wait for the DMA)
+    auto pin = [&](const Carry& c) {
+        if (c.more) {
+#pragma unroll
+            for (int i = 0; i < (PK ? NDI : 1); ++i) asm volatile("" :: "v"(c.nf.off[i]));
+#pragma unroll
+            for (int i = 0; i < (PK ? 1 : NDI); ++i) asm volatile("" :: "v"(c.nf.addr[i]));
+            asm volatile("" :: "v"(c.nf.mus));
+        }
+    };
+    if constexpr (!PIPE) {
+        for (int u = wave; u < n_units; u += 2 * SC_WAVES) {
+            float* ma = reinterpret_cast<float*>(sa_l[wave]);
+            float* mb = reinterpret_cast<float*>(sb_l[wave]);
+            Carry c = front(u, sa_l[wave], sb_l[wave], ma);
+            wave_lds_sync();
+            back(c, ma);
+            pin(c);
+            wave_lds_sync();                           // stages reused by the unit after next
+            if (u + SC_WAVES < n_units) {
+                c = front(u + SC_WAVES, sb_l[wave], sa_l[wave], mb);
+                wave_lds_sync();
+                back(c, mb);
+                pin(c);
+                wave_lds_sync();
+            }
+        }
+    } else if (wave < n_units) {
+        int u = wave;
+        Carry ca = front(u, sa_l[wave], sb_l[wave], mud_l[wave][0]);
+        for (;;) {
+            u += SC_WAVES;
+            if (u >= n_units) { wave_lds_sync(); back(ca, mud_l[wave][0]); break; }
+            Carry cb = front(u, sb_l[wave], sa_l[wave], mud_l[wave][1]);
+            back(ca, mud_l[wave][0]);
+            pin(ca);
+            u += SC_WAVES;
+            if (u >= n_units) { wave_lds_sync(); back(cb, mud_l[wave][1]); break; }
+            ca = front(u, sa_l[wave], sb_l[wave], mud_l[wave][0]);
+            back(cb, mud_l[wave][1]);
+            pin(cb);
+        }
     }
     // per-head maxima of the workgroup -> LDS (ordered-uint atomic max), one
     // atomic per head column per row
@@ -707,11 +781,20 @@ extern "C" int32_t locks_score_rki4(
                         S.scs == RSB && S.smu == RSB && S.smus == RSB &&
                         S.mu == S.v4 + 4L * head_dim && S.c8 == S.mu + head_dim &&
                         S.cs == S.c8 + 8L * page && S.vs == S.cs + 2L * page && S.mus == S.vs + 16;
-#define LAUNCH(GWV, DV, PGV, PKV)                                                               \
-    hipLaunchKernelGGL((rki4_score_kernel<GWV, DV, PGV, PKV>), grid, dim3(SC_BLOCK), dyn, st, q, \
+#define LAUNCH_P(GWV, DV, PGV, PKV, PIPEV)                                                     \
+    hipLaunchKernelGGL((rki4_score_kernel<GWV, DV, PGV, PKV, PIPEV>), grid, dim3(SC_BLOCK), dyn, st, q, \
                        (long)q_stride_req, (long)q_stride_head, S,                             \
                        num_blocks, block_table, (long)bt_stride, bt_cols, n_sel_hi,            \
                        score_h, max_pages, page_max, n_kv, G, sm_scale, chunk)
+    // one request: ~512 workgroups, two per CU, each wave pipelining its
+    // units; several requests: the ~1024-workgroup grid of the auto chunk
+    // fits three per CU only without the pipeline's registers and buffer
+    // (ragged GLM batch step 2.05 -> 1.95 ms)
+#define LAUNCH(GWV, DV, PGV, PKV)                                    \
+    do {                                                             \
+        if (n_req == 1) LAUNCH_P(GWV, DV, PGV, PKV, true);           \
+        else LAUNCH_P(GWV, DV, PGV, PKV, false);                     \
+    } while (0)
 #define LAUNCH_GP(DV, PGV, PKV)                    \
     do {                                           \
         if (G <= 4) LAUNCH(4, DV, PGV, PKV);       \
@@ -739,5 +822,6 @@ extern "C" int32_t locks_score_rki4(
 #undef LAUNCH_G
 #undef LAUNCH_GP
 #undef LAUNCH
+#undef LAUNCH_P
     return check_launch("rki4_score_kernel");
 }
