@@ -107,6 +107,15 @@ def test_score_forced_chunks_g16(zsplit, chunk):
     _run(22, 2, 16, [4000], zsplit=zsplit, expect_chunk=chunk)
 
 
+@pytest.mark.parametrize("n_kv,G", [(8, 4), (4, 8), (2, 16)])
+def test_score_uneven_unit_counts(n_kv, G):
+    """One request (the software-pipelined unit loop): chunk 72 = 9 units,
+    so wave 0 scores 3 units and the others 2, and the last chunk's 19 pages
+    are 3 units with one wave idle; for each token-stage form (G = 4: 4x4
+    blocks, 8 and 16: 16x16 blocks)."""
+    _run(27 + G, n_kv, G, [1100 * 16], zsplit=16, expect_chunk=72)
+
+
 def test_score_llama_128k_full_row():
     """BASELINE configs[1] row: 8 kv heads x 8191 scored pages at the auto
     chunking (128 pages per workgroup) and at the engine's zsplit 64."""
