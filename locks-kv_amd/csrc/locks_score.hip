@@ -12,23 +12,27 @@
 //   score_h[g][p] = LSE_t tok[g][t]
 //
 // MI355X mapping.  One workgroup = 4 waves owns a contiguous chunk of pages
-// of one (request, kv head); a wave handles 8 pages per tile:
+// of one (request, kv head); a wave scores 8-page units:
 //   * the int4 x int8 projection of the whole GQA group runs on the matrix
-//     core: v_mfma_i32_16x16x64_i8 with A = q8 (16 head rows, zero padded)
-//     and B = 2 pages x 8 basis columns.  Each int4 nibble is moved to the
-//     high half of its byte (one shift and one AND per 8 values), so the
-//     operand is 16 V as int8, no sign extension; the 1/16 rides on the
-//     column scale;
-//   * mu . q8 uses the same MFMA with B = one mu row per column (page);
+//     core: v_mfma_i32_16x16x64_i8 with A = 16 packed-V rows (2 pages x 8
+//     basis columns; 4 pages x 4 columns when G <= 4) and B = int8 q (column
+//     = head).  Each int4 nibble is moved to the high half of its byte (a
+//     shift and two ANDs per 8 values), so the operand is 16 V as int8, no
+//     sign extension; the 1/16 rides on the column scale;
+//   * mu . q8 uses the same MFMA with A = the int8 q rows and B = one mu row
+//     per column (page);
 //   * the per-token reconstruction sum_c c8[t][c] qt[g][c] is a 16x8 by
 //     8xG product per page: v_mfma_f32_16x16x4_f32 with pages packed side by
 //     side when 4 < G < 16 (block-diagonal B); for G <= 4,
 //     v_mfma_f32_4x4x1_16b_f32 with one 4x4 block per (page, 4-token quad),
 //     so no block-diagonal zeros are multiplied.  The VALU only does the
 //     cs/mu epilogue and the 16-token LSE.
-// Summary bytes are read exactly once, DMA'd straight from the six slabs
-// (through the block table) into per-wave LDS stages, one unit ahead.  Per-WG page maxima are published to `pmax` so the
-// selector can form the per-head max without re-reading score_h.
+// Summary bytes are read exactly once: each unit's 8 records (or the six
+// separate slabs' rows) are DMA'd through the block table into a per-wave
+// LDS stage, one unit ahead, and with one request the units of a wave are
+// software-pipelined (the next unit's projection interleaves with this
+// unit's token stage).  Per-workgroup page maxima are published to `pmax`
+// so the selector can form the per-head max without re-reading score_h.
 #include "locks_common.h"
 #include "locks_hip.h"
 
