@@ -309,7 +309,8 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
     __syncthreads();                         // q rows consumed: the second stages are free
     // column head's q scale x 1/16 (the nibble shift), zeroed where the
     // token stage's block-diagonal B has no entry for this lane's column:
-    // qt of page p feeds page slot p % PPM only
+    // qt of page p feeds page slot p % PPM only (TK4: no zeros, every lane
+    // group's qt belongs to its own block's page)
     float qsjm[PPM];
     {
         const float qsj = qsp[r16 % GW] * 0.0625f;
