@@ -41,28 +41,42 @@ constexpr int ML_WAVES = 4;
 constexpr int ML_BLK = ML_WAVES * kWave;
 constexpr int ML_VROW = ML_RNK * ML_D / 2;   // 2048 B packed V per page
 constexpr int ML_MAX_CHUNK = 1024;
-// per-wave LDS stage of one unit (2 pages).  V rows (256 B) and RoPE token
-// rows (128 B) are padded by 16 B so that the MFMA-order reads of 16 rows at
-// once hit distinct banks.
-constexpr int MS_VROWB = 272;                // padded (page, column) V row
-constexpr int MS_RROWB = 144;                // padded (page, token) RoPE row
-constexpr int MS_V = 0;                      // 2 x 8 x 272 packed V
-constexpr int MS_MU = 16 * MS_VROWB;         // 2 x 512 centroid
-constexpr int MS_C8 = MS_MU + 1024;          // 2 x 128 coefficients
-constexpr int MS_CS = MS_C8 + 256;           // 2 x 32 token scales
-constexpr int MS_VS = MS_CS + 64;            // 2 x 16 column scales
-constexpr int MS_MUS = MS_VS + 32;           // 2 dwords: centroid scales (bf16 in the low half)
-constexpr int MS_RP = MS_MUS + 16;           // 2 x 16 RoPE key rows
-// RoPE rows: exact bf16 keys (128 B, padded to 144) or int8 keys (64 B,
-// padded to 80: 16 rows at 80-B stride read 16 B each on distinct banks)
-// plus the two pages' bf16 token scales
+// Per-wave LDS stage of one unit (2 pages), filled by LDS DMA
+// (global_load_lds_dwordx4: lane L of an instruction writes the 16 bytes at
+// 16 L of the instruction's 1-KB window, from its own source address).
+// Rows are stored unpadded with their 64-byte blocks permuted by an XOR of
+// the row index, so the MFMA-order reads (16 rows at once, the same part of
+// each) spread over four bank groups; the DMA fetches, for each LDS slot,
+// the part that belongs there.  (Permuting the 16-byte parts themselves
+// would spread the reads over all banks but break each lane quad's 64
+// contiguous source bytes into four requests: measured 15.6 vs 14.2 us.)
+constexpr int ML_CPOL_NT = 2;
+typedef __attribute__((address_space(3))) void* ml_lds_ptr;                // buffer-load cache policy: non-temporal
+constexpr int MS_V = 0;                      // 16 (page, column) rows x 256 B packed V
+constexpr int MS_MU = 4096;                  // 2 x 512 centroid
+constexpr int MS_RP = 5120;                  // 32 (page, token) RoPE rows
+// RoPE rows: exact bf16 keys (128 B) or int8 keys (64 B); then the small
+// rows (c8 | cs | vs | RQ: the int8 keys' bf16 scales) and the centroid terms
 template <bool RQ>
 struct MsGeom {
-    static constexpr int RROWB = RQ ? 80 : MS_RROWB;
-    static constexpr int RS = MS_RP + 32 * RROWB;        // RQ: 2 x 16 bf16 key scales
-    static constexpr int MD = RS + (RQ ? 64 : 0);        // 2 x 16 fp32 centroid terms
+    static constexpr int RROWB = RQ ? 64 : 128;
+    static constexpr int NRI = RQ ? 2 : 4;               // DMA instructions of the RoPE rows
+    static constexpr int SM = MS_RP + 32 * RROWB;        // small rows
+    static constexpr int S_C8 = SM, S_CS = SM + 256, S_VS = SM + 320, S_RS = SM + 352;
+    static constexpr int NSM = RQ ? 26 : 22;             // 16-byte chunks of the small rows
+    static constexpr int MD = SM + 16 * NSM;             // 2 x 16 fp32 centroid terms
     static constexpr int BYTES = MD + 128;
 };
+// LDS slot (16-byte part index) of part p of a stage row R, and its
+// inverse: packed V (256-B rows, four blocks), exact RoPE (128-B rows, two
+// blocks; two rows per 256-B bank span), int8 RoPE (64-B rows, one block)
+__device__ __forceinline__ int ms_vslot(int R, int p) { return (((p >> 2) ^ (R & 3)) << 2) | (p & 3); }
+__device__ __forceinline__ int ms_rslot(int R, int p) { return (((p >> 2) ^ ((R >> 1) & 1)) << 2) | (p & 3); }
+__device__ __forceinline__ int ms_vpos(int R, int p) { return MS_V + R * 256 + (ms_vslot(R, p) << 4); }
+template <bool RQ>
+__device__ __forceinline__ int ms_rpos(int R, int p) {
+    return RQ ? MS_RP + R * 64 + (p << 4) : MS_RP + R * 128 + (ms_rslot(R, p) << 4);
+}
 constexpr int ML_RK_BLOCK = ML_PG * ML_DR;   // int8 RoPE keys per block (1024 B)
 
 __device__ __forceinline__ v4i perm_even_odd(const uint4 n) {
@@ -96,6 +110,7 @@ __global__ __launch_bounds__(ML_BLK) void mla_score_kernel(
     const int* __restrict__ nsh, float* __restrict__ score, long sc_sr, int MP,
     int H, float scale, int chunk)
 {
+    using GM = MsGeom<RQ>;
     const int z = blockIdx.x, r = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int P = min(nsh[r], MP);
@@ -103,107 +118,123 @@ __global__ __launch_bounds__(ML_BLK) void mla_score_kernel(
     const int c1 = min(c0 + chunk, P);
     if (c0 >= c1) return;
 
-    __shared__ __attribute__((aligned(16))) int8_t q8s[ML_H + 1][ML_D];   // row 16 = zeros
-    using GM = MsGeom<RQ>;
-    __shared__ __attribute__((aligned(16))) uint16_t qrs[ML_H][ML_DR];   // bf16 q_rope (RQ: int8 in the first half)
+    // two stages per wave as separate LDS objects (a unit's reads never share
+    // an object with the next unit's DMA); the int8 q rows and the q_rope rows
+    // live in the second stages until the q operands are built
+    __shared__ __attribute__((aligned(16))) uint8_t sa_l[ML_WAVES][GM::BYTES];
+    __shared__ __attribute__((aligned(16))) uint8_t sb_l[ML_WAVES][GM::BYTES];
     __shared__ float qss[ML_H];
     __shared__ float qrss[ML_H];                                        // RQ: q_rope scale per head
-    __shared__ int bt_l[ML_MAX_CHUNK];
-    __shared__ __attribute__((aligned(16))) uint8_t stage_l[ML_WAVES][GM::BYTES];
+    extern __shared__ __attribute__((aligned(16))) int bt_l[];          // block ids of the chunk
+    static_assert((ML_H + 1) * ML_D + ML_H * ML_DR * 2 <= ML_WAVES * GM::BYTES, "q rows fit the second stages");
+    int8_t (*q8s)[ML_D] = reinterpret_cast<int8_t (*)[ML_D]>(&sb_l[0][0]);                   // row 16 = zeros
+    uint16_t (*qrs)[ML_DR] = reinterpret_cast<uint16_t (*)[ML_DR]>(&sb_l[0][0] + (ML_H + 1) * ML_D);  // RQ: int8 in the first half
 
     // ---- prologue: q rows of this wave's heads and the block ids in one
-    // round trip; the first unit's summary loads are issued before q is
-    // quantized (absmax / 127 per head), so the quantization overlaps them
+    // round trip; the first unit's DMA is issued before q is quantized
+    // (absmax / 127 per head), so the quantization overlaps it
+    // Unconditional loads (heads past H re-read head H - 1 and are zeroed
+    // or never stored): a guarded load is waited for at its branch join,
+    // which would serialise the heads' round trips.
     constexpr int QH = ML_H / ML_WAVES;
     uint4 qw[QH], qrw[QH];
 #pragma unroll
     for (int i = 0; i < QH; ++i) {
-        const int h = wave + ML_WAVES * i;
+        const int h = min(wave + ML_WAVES * i, H - 1);
         const uint16_t* qh = q + (long)r * q_sr + (long)h * q_sh;
-        qw[i] = qrw[i] = make_uint4(0u, 0u, 0u, 0u);
-        if (h < H) {
-            qw[i] = *reinterpret_cast<const uint4*>(qh + 8 * lane);
-            if (!RQ && lane < ML_DR / 8) qrw[i] = *reinterpret_cast<const uint4*>(qh + ML_D + 8 * lane);
-        }
+        qw[i] = *reinterpret_cast<const uint4*>(qh + 8 * lane);
+        qrw[i] = make_uint4(0u, 0u, 0u, 0u);
+        if constexpr (!RQ) qrw[i] = *reinterpret_cast<const uint4*>(qh + ML_D + 8 * (lane & 7));
     }
     // RQ: the wave's QH q_rope rows side by side, lane l < 8 QH holding dims
     // 8 (l & 7) .. of head wave + QH (l >> 3)
     const int hr = wave + ML_WAVES * (lane >> 3);
     const bool hr_ok = RQ && lane < 8 * QH && hr < H;
     uint4 qrw8 = make_uint4(0u, 0u, 0u, 0u);
-    if (hr_ok) qrw8 = *reinterpret_cast<const uint4*>(q + (long)r * q_sr + (long)hr * q_sh + ML_D + 8 * (lane & 7));
+    if constexpr (RQ)
+        qrw8 = *reinterpret_cast<const uint4*>(q + (long)r * q_sr + (long)min(hr, H - 1) * q_sh + ML_D + 8 * (lane & 7));
     for (int i = tid; i < c1 - c0; i += ML_BLK) {
         const int b = bt[(long)r * bt_sr + min(c0 + i, bt_cols - 1)];
         bt_l[i] = min(max(b, 0), NB - 1);
     }
-    for (int i = tid; i < ML_D / 4; i += ML_BLK) reinterpret_cast<int*>(&q8s[ML_H][0])[i] = 0;
     __syncthreads();
     const int r16 = lane & 15, kg = lane >> 4;
     const int n_units = cdiv(c1 - c0, 2);
-    uint4 fv0, fv1, fv2, fv3, fmu, fc8, fcs, fvs, fr0, fr1, fr2, fr3, frs;
-    uint32_t fmus = 0u;
-    // natural-order (coalesced) loads of unit u into registers
-    auto load_unit = [&](int u) {
-        const int p0 = 2 * u;
-        const int last = c1 - c0 - 1;
-        auto blk_of = [&](int pg) -> long { return (long)bt_l[min(p0 + pg, last)]; };
-        // 16-byte chunk i = lane + 64 m of the 2 V rows
-        // Rows read once by this workgroup (packed V, centroid, coefficients,
-        // RoPE keys) load non-temporally; the small scale rows, whose cache
-        // lines neighbouring blocks share, with the default policy.
-        auto vload = [&](int i) { return ld_nt16(v4 + blk_of(i >> 7) * ML_VROW + (i & 127) * 16); };
-        fv0 = vload(lane); fv1 = vload(lane + 64); fv2 = vload(lane + 128); fv3 = vload(lane + 192);
-        fmu = ld_nt16(mu8 + blk_of(lane >> 5) * ML_D + (lane & 31) * 16);
-        fc8 = ld_nt16(c8 + blk_of((lane >> 3) & 1) * (ML_PG * ML_RNK) + (lane & 7) * 16);
-        fcs = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(cs) + blk_of((lane >> 1) & 1) * (ML_PG * 2) + (lane & 1) * 16);
-        fvs = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(vs) + blk_of(lane & 1) * (ML_RNK * 2));
-        fmus = (uint32_t)mus[blk_of(lane & 1)];
-        if constexpr (RQ) {
-            // int8 key chunk i = (page i >> 6, 16-byte part i & 63 of the
-            // page's 1024 B); key scales: 16-byte part lane & 1 of page
-            // (lane >> 1) & 1
-            auto rload = [&](int i) { return ld_nt16(rk8 + blk_of(i >> 6) * ML_RK_BLOCK + (i & 63) * 16); };
-            fr0 = rload(lane); fr1 = rload(lane + 64);
-            frs = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(rks) + blk_of((lane >> 1) & 1) * (ML_PG * 2) + (lane & 1) * 16);
-        } else {
-            // RoPE chunk i = (page i >> 7, token (i >> 3) & 15, 16-byte part i & 7)
-            auto rload = [&](int i) {
-                return ld_nt16(cache + blk_of(i >> 7) * c_sb + (long)((i >> 3) & 15) * c_st + ML_D + 8 * (i & 7));
-            };
-            fr0 = rload(lane); fr1 = rload(lane + 64); fr2 = rload(lane + 128); fr3 = rload(lane + 192);
-        }
-    };
-    auto store_unit = [&](uint8_t* st) {
-        // V chunk i: page i >> 7, column (i >> 4) & 7, 16-byte part i & 15
-        auto vofs = [&](int i) { return MS_V + ((i >> 7) * 8 + ((i >> 4) & 7)) * MS_VROWB + (i & 15) * 16; };
-        *reinterpret_cast<uint4*>(st + vofs(lane)) = fv0;
-        *reinterpret_cast<uint4*>(st + vofs(lane + 64)) = fv1;
-        *reinterpret_cast<uint4*>(st + vofs(lane + 128)) = fv2;
-        *reinterpret_cast<uint4*>(st + vofs(lane + 192)) = fv3;
-        *reinterpret_cast<uint4*>(st + MS_MU + lane * 16) = fmu;
-        if (lane < 16) *reinterpret_cast<uint4*>(st + MS_C8 + lane * 16) = fc8;
-        if (lane < 4) *reinterpret_cast<uint4*>(st + MS_CS + lane * 16) = fcs;
-        if (lane < 2) {
-            *reinterpret_cast<uint4*>(st + MS_VS + lane * 16) = fvs;
-            *reinterpret_cast<uint32_t*>(st + MS_MUS + lane * 4) = fmus;
-        }
-        if constexpr (RQ) {
-            // int8 key chunk i: (page, token) row i >> 2, 16-byte part i & 3
-            auto rofs = [&](int i) { return MS_RP + (i >> 2) * GM::RROWB + (i & 3) * 16; };
-            *reinterpret_cast<uint4*>(st + rofs(lane)) = fr0;
-            *reinterpret_cast<uint4*>(st + rofs(lane + 64)) = fr1;
-            if (lane < 4) *reinterpret_cast<uint4*>(st + GM::RS + lane * 16) = frs;
-        } else {
-            // RoPE chunk i: (page, token) row i >> 3, 16-byte part i & 7
-            auto rofs = [&](int i) { return MS_RP + (i >> 3) * MS_RROWB + (i & 7) * 16; };
-            *reinterpret_cast<uint4*>(st + rofs(lane)) = fr0;
-            *reinterpret_cast<uint4*>(st + rofs(lane + 64)) = fr1;
-            *reinterpret_cast<uint4*>(st + rofs(lane + 128)) = fr2;
-            *reinterpret_cast<uint4*>(st + rofs(lane + 192)) = fr3;
-        }
-    };
 
-    load_unit(min(wave, n_units - 1));          // every lane loads (exact wait counts)
+    // ---- the unit DMA: per lane and instruction a source address; the LDS
+    // slot of lane L is fixed (16 L into the instruction's 1-KB window)
+    // small rows: lane -> (field base, page, byte offset) once for all units
+    const uint8_t* sm_base;
+    int sm_stride, sm_page, sm_off;
+    if (lane < 16) { sm_base = reinterpret_cast<const uint8_t*>(c8); sm_stride = ML_PG * ML_RNK; sm_page = lane >> 3; sm_off = (lane & 7) * 16; }
+    else if (lane < 20) { sm_base = reinterpret_cast<const uint8_t*>(cs); sm_stride = ML_PG * 2; sm_page = (lane - 16) >> 1; sm_off = ((lane - 16) & 1) * 16; }
+    else if (lane < 22 || !RQ) { sm_base = reinterpret_cast<const uint8_t*>(vs); sm_stride = ML_RNK * 2; sm_page = (lane - 20) & 1; sm_off = 0; }
+    else { sm_base = reinterpret_cast<const uint8_t*>(rks); sm_stride = ML_PG * 2; sm_page = ((lane - 22) >> 1) & 1; sm_off = ((lane - 22) & 1) * 16; }
+    struct UnitSrc {
+        const uint8_t* a[4 + 1 + GM::NRI + 1];      // V x 4, centroid, RoPE rows, small rows
+    };
+    constexpr int NI = 4 + 1 + GM::NRI + 1;
+    auto unit_src = [&](int u, uint32_t& mus_off) -> UnitSrc {
+        const int p0 = 2 * u, last = c1 - c0 - 1;
+        const long b0 = bt_l[min(p0, last)], b1 = bt_l[min(p0 + 1, last)];   // tail pair repeats the last page
+        UnitSrc f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {               // V rows 4 i .. 4 i + 3 (page i >> 1)
+            const int R = 4 * i + (lane >> 4), pq = ms_vslot(R, lane & 15);   // the permutation is an involution
+            f.a[i] = v4 + ((i >> 1) ? b1 : b0) * ML_VROW + (R & 7) * 256 + pq * 16;
+        }
+        f.a[4] = reinterpret_cast<const uint8_t*>(mu8) + ((lane >> 5) ? b1 : b0) * ML_D + (lane & 31) * 16;
+#pragma unroll
+        for (int j = 0; j < GM::NRI; ++j) {
+            if constexpr (RQ) {                     // int8 key rows 16 j .. (page j), 4 parts of 16 B
+                const int R = 16 * j + (lane >> 2), pq = lane & 3;
+                f.a[5 + j] = reinterpret_cast<const uint8_t*>(rk8) + (j ? b1 : b0) * ML_RK_BLOCK + (R & 15) * ML_DR + pq * 16;
+            } else {                                // exact key rows 8 j .. (page j >> 1), 8 parts of 16 B
+                const int R = 8 * j + (lane >> 3), pq = ms_rslot(R, lane & 7);
+                f.a[5 + j] = reinterpret_cast<const uint8_t*>(cache + ((j >> 1) ? b1 : b0) * c_sb + (long)(R & 15) * c_st + ML_D + 8 * pq);
+            }
+        }
+        f.a[NI - 1] = sm_base + (sm_page ? b1 : b0) * sm_stride + sm_off;
+        mus_off = (uint32_t)((lane & 1) ? b1 : b0);
+        return f;
+    };
+    uint32_t fmus = 0u;                               // centroid scale of page lane & 1
+    auto issue = [&](const UnitSrc& f, uint32_t mus_blk, uint8_t* st) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint8_t* src = f.a[i];
+            __builtin_amdgcn_global_load_lds(src, (ml_lds_ptr)(st + MS_V + 1024 * i), 16, 0, ML_CPOL_NT);
+        }
+        {
+            const uint8_t* src = f.a[4];
+            __builtin_amdgcn_global_load_lds(src, (ml_lds_ptr)(st + MS_MU), 16, 0, ML_CPOL_NT);
+        }
+#pragma unroll
+        for (int j = 0; j < GM::NRI; ++j) {
+            const uint8_t* src = f.a[5 + j];
+            __builtin_amdgcn_global_load_lds(src, (ml_lds_ptr)(st + MS_RP + 1024 * j), 16, 0, ML_CPOL_NT);
+        }
+        // the scale rows share cache lines with neighbouring blocks: default policy
+        if (lane < GM::NSM) {
+            const uint8_t* src = f.a[NI - 1];
+            __builtin_amdgcn_global_load_lds(src, (ml_lds_ptr)(st + GM::SM), 16, 0, 0);
+        }
+        fmus = (uint32_t)mus[mus_blk];
+    };
+    auto pin = [&](const UnitSrc& f) {              // DMA sources stay allocated until the unit ends
+#pragma unroll
+        for (int i = 0; i < NI; ++i) asm volatile("" :: "v"(f.a[i]));
+    };
+    // q rows resident before the first unit's DMA queues behind them (the
+    // compiler could not tell they are, and would wait for the DMA too)
+    __builtin_amdgcn_s_waitcnt(0x0070);
+    if (wave < n_units) {
+        uint32_t mb;
+        const UnitSrc f0 = unit_src(wave, mb);
+        pin(f0);
+        issue(f0, mb, sa_l[wave]);
+    }
+
     // int8 round trip of one head's row, 8 values per lane: qs = max(absmax,
     // 1e-8) / 127 over the wave, v = rint(a / qs) with the correctly rounded
     // quotient: a * (1 / qs) is within 2 ulp of it and decides the rounding
@@ -254,6 +285,7 @@ __global__ __launch_bounds__(ML_BLK) void mla_score_kernel(
         }
         return qs;
     };
+    for (int i = tid; i < ML_D / 4; i += ML_BLK) reinterpret_cast<int*>(&q8s[ML_H][0])[i] = 0;
 #pragma unroll
     for (int i = 0; i < QH; ++i) {
         const int h = wave + ML_WAVES * i;
@@ -261,7 +293,7 @@ __global__ __launch_bounds__(ML_BLK) void mla_score_kernel(
         const float qs = quant8(qw[i], h < H, pk, false);
         *reinterpret_cast<uint2*>(&q8s[h][8 * lane]) = make_uint2(pk[0], pk[1]);
         if constexpr (!RQ) {
-            if (lane < ML_DR / 8) *reinterpret_cast<uint4*>(&qrs[h][8 * lane]) = qrw[i];
+            if (lane < ML_DR / 8) *reinterpret_cast<uint4*>(&qrs[h][8 * lane]) = (h < H) ? qrw[i] : make_uint4(0u, 0u, 0u, 0u);
         }
         if (lane == 0) qss[h] = (h < H) ? qs : 0.f;
     }
@@ -275,7 +307,11 @@ __global__ __launch_bounds__(ML_BLK) void mla_score_kernel(
             if ((lane & 7) == 0) qrss[hr] = hr_ok ? qsr : 0.f;
         }
     }
-    __syncthreads();
+    // barrier on the q rows while the first unit's DMA is in flight: the
+    // compiler's LDS fences would also wait for the DMA (it writes LDS), so
+    // the LDS completion wait and the barrier are explicit, the asm a
+    // compiler memory barrier
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     const uint32_t MH = 0xF0F0F0F0u;
     // q operands shared by every unit: projection B (column j = head j),
     // RoPE B (column = head), per-head scale of this lane's column
@@ -305,56 +341,79 @@ __global__ __launch_bounds__(ML_BLK) void mla_score_kernel(
     }
     const float qsj = qss[r16];
     const bool col_ok = r16 < H;
+    // q rows consumed: the second stages are free (explicit for the same reason)
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
-    uint8_t* st = stage_l[wave];
-    for (int u = wave; u < n_units; u += ML_WAVES) {
-        store_unit(st);
-        if (u + ML_WAVES < n_units) load_unit(u + ML_WAVES);   // next unit in flight
+    // a unit's page scores are stored after the next unit's wait (vmcnt(0)
+    // would otherwise also wait for the stores just issued)
+    float pend_m[2] = {0.f, 0.f};
+    long pend_at = -1;
+    int pend_n = 0;
+    auto flush = [&]() {
+        if (lane == 0 && pend_at >= 0) {
+            score[pend_at] = pend_m[0];
+            if (pend_n > 1) score[pend_at + 1] = pend_m[1];
+        }
+    };
+    auto score_unit = [&](int u, uint8_t* st, uint8_t* st_next) {
+        __builtin_amdgcn_s_waitcnt(0x0070);          // this unit's rows have landed in the stage
         wave_lds_sync();
+        flush();
+        // centroid scales of the pair, before the next unit's load replaces them
+        const uint32_t mus0 = (uint32_t)__builtin_amdgcn_readlane((int)fmus, 0);
+        const uint32_t mus1 = (uint32_t)__builtin_amdgcn_readlane((int)fmus, 1);
+        const bool more = u + ML_WAVES < n_units;
+        UnitSrc nf;
+        uint32_t nmb = 0u;
+        if (more) nf = unit_src(u + ML_WAVES, nmb);
         const int p0 = c0 + 2 * u;
         const int nvalid = min(2, c1 - p0);
 
         // ---- projection (A = the 16 V rows of the pair, row 4a + b <->
         // page b & 1, column 2a + (b >> 1); B = int8 q) and the centroid
-        // term (A rows 0/1 = the two mu rows, same B) ----------------------
+        // term (A rows 0/1 = the two mu rows, same B); every read of this
+        // stage's V and centroid is issued before the next unit's DMA
         const int i_pg = r16 & 1, i_c = 2 * (r16 >> 2) + ((r16 >> 1) & 1);
+        const int Rv = i_pg * 8 + i_c;
+        uint4 wv[4], wm[4][2];
+#pragma unroll
+        for (int k4 = 0; k4 < 4; ++k4) {
+            wv[k4] = *reinterpret_cast<const uint4*>(st + ms_vpos(Rv, k4 * 4 + kg));
+            wm[k4][0] = wm[k4][1] = make_uint4(0u, 0u, 0u, 0u);
+            if (r16 < 2) {
+                wm[k4][0] = *reinterpret_cast<const uint4*>(st + MS_MU + r16 * ML_D + 128 * k4 + 32 * kg);
+                wm[k4][1] = *reinterpret_cast<const uint4*>(st + MS_MU + r16 * ML_D + 128 * k4 + 32 * kg + 16);
+            }
+        }
+        const uint32_t vsw0 = *reinterpret_cast<const uint32_t*>(st + GM::S_VS + 0 * 16 + kg * 4);
+        const uint32_t vsw1 = *reinterpret_cast<const uint32_t*>(st + GM::S_VS + 1 * 16 + kg * 4);
+        if (more) issue(nf, nmb, st_next);
         v4i acc = {0, 0, 0, 0}, accm = {0, 0, 0, 0};
 #pragma unroll
         for (int k4 = 0; k4 < 4; ++k4) {
-            const uint4 w = *reinterpret_cast<const uint4*>(st + MS_V + (i_pg * 8 + i_c) * MS_VROWB + k4 * 64 + kg * 16);
+            const uint4 w = wv[k4];
             const v4i a0 = {(int)((w.x << 4) & MH), (int)((w.y << 4) & MH), (int)(w.x & MH), (int)(w.y & MH)};
             const v4i a1 = {(int)((w.z << 4) & MH), (int)((w.w << 4) & MH), (int)(w.z & MH), (int)(w.w & MH)};
             acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, Bq[k4][0], acc, 0, 0, 0);
             acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, Bq[k4][1], acc, 0, 0, 0);
-            v4i m0 = {0, 0, 0, 0}, m1 = {0, 0, 0, 0};
-            if (r16 < 2) {
-                m0 = perm_even_odd(*reinterpret_cast<const uint4*>(st + MS_MU + r16 * ML_D + 128 * k4 + 32 * kg));
-                m1 = perm_even_odd(*reinterpret_cast<const uint4*>(st + MS_MU + r16 * ML_D + 128 * k4 + 32 * kg + 16));
-            }
-            accm = __builtin_amdgcn_mfma_i32_16x16x64_i8(m0, Bq[k4][0], accm, 0, 0, 0);
-            accm = __builtin_amdgcn_mfma_i32_16x16x64_i8(m1, Bq[k4][1], accm, 0, 0, 0);
+            accm = __builtin_amdgcn_mfma_i32_16x16x64_i8(perm_even_odd(wm[k4][0]), Bq[k4][0], accm, 0, 0, 0);
+            accm = __builtin_amdgcn_mfma_i32_16x16x64_i8(perm_even_odd(wm[k4][1]), Bq[k4][1], accm, 0, 0, 0);
         }
         // qt[v] = qt[head r16][page v & 1][column 2kg + (v >> 1)]; the 1/16 of
         // the high-nibble operand rides on the power-of-two column scale
         float qt[4];
-        {
-            const uint32_t w0 = *reinterpret_cast<const uint32_t*>(st + MS_VS + 0 * 16 + kg * 4);
-            const uint32_t w1 = *reinterpret_cast<const uint32_t*>(st + MS_VS + 1 * 16 + kg * 4);
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const uint32_t w = (v & 1) ? w1 : w0;
-                const float vsc = ((v >> 1) ? bf16hi(w) : bf16lo(w)) * 0.0625f;
-                qt[v] = (float)acc[v] * qsj * vsc;
-            }
+        for (int v = 0; v < 4; ++v) {
+            const uint32_t w = (v & 1) ? vsw1 : vsw0;
+            const float vsc = ((v >> 1) ? bf16hi(w) : bf16lo(w)) * 0.0625f;
+            qt[v] = (float)acc[v] * qsj * vsc;
         }
         // centroid term of (page v, head r16) lives in lanes kg = 0, v = 0/1
         float* md = reinterpret_cast<float*>(st + GM::MD);
         if (kg == 0) {
 #pragma unroll
-            for (int v = 0; v < 2; ++v) {
-                const float musf = bf16lo(*reinterpret_cast<const uint32_t*>(st + MS_MUS + v * 4));
-                md[v * 16 + r16] = (float)accm[v] * qsj * musf;
-            }
+            for (int v = 0; v < 2; ++v)
+                md[v * 16 + r16] = (float)accm[v] * qsj * bf16lo(v ? mus1 : mus0);
         }
         wave_lds_sync();
 
@@ -362,19 +421,20 @@ __global__ __launch_bounds__(ML_BLK) void mla_score_kernel(
 #pragma unroll
         for (int pg = 0; pg < 2; ++pg) {
             v4f tk = {0.f, 0.f, 0.f, 0.f};
-            const uint32_t cw = *reinterpret_cast<const uint16_t*>(st + MS_C8 + pg * 128 + r16 * 8 + 2 * kg);
+            const uint32_t cw = *reinterpret_cast<const uint16_t*>(st + GM::S_C8 + pg * 128 + r16 * 8 + 2 * kg);
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh) {
                 const float a = (float)(int8_t)(cw >> (8 * hh));
                 tk = __builtin_amdgcn_mfma_f32_16x16x4f32(a, qt[2 * hh + pg], tk, 0, 0, 0);
             }
             v4f rp = {0.f, 0.f, 0.f, 0.f};
+            const int Rr = pg * 16 + r16;               // RoPE row of this lane's token
             if constexpr (RQ) {
                 // rows = the page's 16 tokens, 16 int8 dims per lane group
-                const uint4 w = *reinterpret_cast<const uint4*>(st + MS_RP + (pg * 16 + r16) * GM::RROWB + 16 * kg);
+                const uint4 w = *reinterpret_cast<const uint4*>(st + ms_rpos<RQ>(Rr, kg));
                 const v4i ri = __builtin_amdgcn_mfma_i32_16x16x64_i8(v4i{(int)w.x, (int)w.y, (int)w.z, (int)w.w},
                                                                      Br8, v4i{0, 0, 0, 0}, 0, 0, 0);
-                const uint2 rsw = *reinterpret_cast<const uint2*>(st + GM::RS + pg * 32 + kg * 8);
+                const uint2 rsw = *reinterpret_cast<const uint2*>(st + GM::S_RS + pg * 32 + kg * 8);
                 rp[0] = (float)ri[0] * qrsj * bf16lo(rsw.x);
                 rp[1] = (float)ri[1] * qrsj * bf16hi(rsw.x);
                 rp[2] = (float)ri[2] * qrsj * bf16lo(rsw.y);
@@ -382,12 +442,11 @@ __global__ __launch_bounds__(ML_BLK) void mla_score_kernel(
             } else {
 #pragma unroll
                 for (int s = 0; s < 2; ++s) {
-                    const v8bf a = __builtin_bit_cast(v8bf, *reinterpret_cast<const uint4*>(
-                        st + MS_RP + (pg * 16 + r16) * MS_RROWB + (32 * s + 8 * kg) * 2));
+                    const v8bf a = __builtin_bit_cast(v8bf, *reinterpret_cast<const uint4*>(st + ms_rpos<RQ>(Rr, 4 * s + kg)));
                     rp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, Br[s], rp, 0, 0, 0);
                 }
             }
-            const uint2 csw = *reinterpret_cast<const uint2*>(st + MS_CS + pg * 32 + kg * 8);
+            const uint2 csw = *reinterpret_cast<const uint2*>(st + GM::S_CS + pg * 32 + kg * 8);
             const float mud = md[pg * 16 + r16];
             const float t0 = fmaf(tk[0], bf16lo(csw.x), rp[0]);
             const float t1 = fmaf(tk[1], bf16hi(csw.x), rp[1]);
@@ -395,10 +454,18 @@ __global__ __launch_bounds__(ML_BLK) void mla_score_kernel(
             const float t3 = fmaf(tk[3], bf16hi(csw.y), rp[3]);
             float m = col_ok ? fmaxf(fmaxf(t0, t1), fmaxf(t2, t3)) + mud : -INFINITY;
             m = wave_max(m);
-            if (lane == 0 && pg < nvalid) score[(long)r * sc_sr + p0 + pg] = m * scale;
+            pend_m[pg] = m * scale;
         }
-        wave_lds_sync();                                 // stage reused by the next unit
+        pend_at = (long)r * sc_sr + p0;
+        pend_n = nvalid;
+        if (more) pin(nf);
+        wave_lds_sync();                                 // stage reused by the unit after next
+    };
+    for (int u = wave; u < n_units; u += 2 * ML_WAVES) {
+        score_unit(u, sa_l[wave], sb_l[wave]);
+        if (u + ML_WAVES < n_units) score_unit(u + ML_WAVES, sb_l[wave], sa_l[wave]);
     }
+    flush();
 }
 
 // ---------------------------------------------------------------------------
@@ -819,7 +886,7 @@ extern "C" int32_t locks_mla_score(
     if (n_req == 0) return 0;
     const int Z = cdiv(max_pages, chunk);
 #define LAUNCH_RQ(RQ)                                                                               \
-    hipLaunchKernelGGL(mla_score_kernel<RQ>, dim3(Z, n_req), dim3(ML_BLK), 0, (hipStream_t)stream, q, \
+    hipLaunchKernelGGL(mla_score_kernel<RQ>, dim3(Z, n_req), dim3(ML_BLK), (size_t)chunk * sizeof(int), (hipStream_t)stream, q, \
                        (long)q_stride_req, (long)q_stride_head, v4, vs, c8, cs, mu8, mus, rk8, rks,  \
                        cache, (long)c_stride_block, (long)c_stride_tok, num_blocks, block_table,     \
                        (long)bt_stride, bt_cols, n_sel_hi, score, (long)score_stride, max_pages,     \
