@@ -283,7 +283,11 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
             *reinterpret_cast<uint2*>(qrow + 8) = make_uint2(pack4_i8(iq[8], iq[9], iq[10], iq[11]), pack4_i8(iq[12], iq[13], iq[14], iq[15]));
         if (c % LPH == 0) qsp[hq] = qs * s2;
     }
-    __syncthreads();
+    // barriers on the q rows while the first unit's DMA is in flight: the
+    // compiler's LDS fences count a pending LDS DMA as an LDS write and would
+    // wait for it, so the LDS completion wait and the barrier are explicit
+    // (the asm a compiler memory barrier)
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
     // int8 q rows of this kv head's GQA group as matrix-core operands (the
     // same for every unit of the workgroup):
@@ -306,7 +310,7 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
         }
     }
     const float4 qsl = *reinterpret_cast<const float4*>(&qsp[4 * kg]);   // rows 4kg.. (mud)
-    __syncthreads();                         // q rows consumed: the second stages are free
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");   // q rows consumed: the second stages are free
     // column head's q scale x 1/16 (the nibble shift), zeroed where the
     // token stage's block-diagonal B has no entry for this lane's column:
     // qt of page p feeds page slot p % PPM only (TK4: no zeros, every lane
