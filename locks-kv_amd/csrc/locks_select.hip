@@ -493,7 +493,7 @@ constexpr int ROW_NW = ROW_BLK / kWave;
 // 20.5 us; G = 16: 44.8 vs 25.7 us).
 constexpr int ROW_MAXP = 8 * ROW_BLK;
 
-template <int E>
+template <int E, int HB = (E <= 8) ? 8 : 4>
 __global__ __launch_bounds__(ROW_BLK) void sel_row_kernel(
     const float* __restrict__ score_h, const float* __restrict__ pmax, int Zs,
     const int* __restrict__ npg, const int* __restrict__ nsh, const int* __restrict__ bfix,
@@ -522,7 +522,8 @@ __global__ __launch_bounds__(ROW_BLK) void sel_row_kernel(
     // ---- score_h of the first HB heads in flight before the head maxima.
     // Loads are bounded by the row (MP), not by n_sel_hi, so they do not wait
     // for the per-request parameters; pages >= n_sel_hi are ignored below.
-    constexpr int HB = (E <= 8) ? 8 : 4;                  // heads per load batch
+    // HB heads per load batch: the host passes 4 for groups of at most 4
+    // (the clamped loads of heads past G re-read the last head)
     const float* shb = score_h + rk * (long)G * MP;
     float4 xv[HB][E / 4];
     auto load_batch = [&](int g0) {
@@ -1215,12 +1216,21 @@ extern "C" int32_t locks_select_nrm_topb(
     // 1.327 -> 1.104 ms per step
     if (max_pages <= ROW_MAXP && max_pages % 4 == 0 &&
         (long)G * max_pages <= SEL_ROW_MAX_GP) {
-#define ROW_LAUNCH(EV)                                                                     \
-        hipLaunchKernelGGL((sel_row_kernel<EV>), dim3(n_kv, n_req), dim3(ROW_BLK), 0, st, score_h, \
+#define ROW_LAUNCH(EV, HBV)                                                                \
+        hipLaunchKernelGGL((sel_row_kernel<EV, HBV>), dim3(n_kv, n_req), dim3(ROW_BLK), 0, st, score_h, \
                            page_max, score_chunks, n_pages, n_sel_hi, b_fix, score, page_table, \
                            page_cnt, n_sink, max_pages, G, combine)
-        if (max_pages <= 4 * ROW_BLK) ROW_LAUNCH(4);
-        else ROW_LAUNCH(8);
+        // heads per load batch: no clamped duplicate loads for one head (MLA)
+        // or groups of at most 4 (Llama G = 4: 16 -> 8 loads per thread)
+        if (max_pages <= 4 * ROW_BLK) {
+            if (G == 1) ROW_LAUNCH(4, 1);
+            else if (G <= 4) ROW_LAUNCH(4, 4);
+            else ROW_LAUNCH(4, 8);
+        } else {
+            if (G == 1) ROW_LAUNCH(8, 1);
+            else if (G <= 4) ROW_LAUNCH(8, 4);
+            else ROW_LAUNCH(8, 8);
+        }
 #undef ROW_LAUNCH
         return check_launch("sel_row_kernel");
     }
