@@ -793,7 +793,9 @@ constexpr int F2_CAP = F2_BLK * 16;                    // register-resident cand
 // BAND = true (large budgets): add the chunk's key histogram (top 12 bits)
 // into the row's global histogram instead; sel_band_kernel then emits the
 // candidates at or above the row's boundary bin.
-template <bool BAND, int E = C2_E>
+// GL: heads loaded per thread (>= G; the host picks 1, 4, 8 or 16), so
+// small groups issue no clamped duplicate loads.
+template <bool BAND, int E = C2_E, int GL = 16>
 __global__ __launch_bounds__(C2_BLK) void sel_chunk2_kernel(
     const float* __restrict__ score_h, const float* __restrict__ pmax, int Zs,
     const int* __restrict__ npg, const int* __restrict__ nsh, const int* __restrict__ bfix,
@@ -820,9 +822,9 @@ __global__ __launch_bounds__(C2_BLK) void sel_chunk2_kernel(
 
     // score_h of every head in flight first (row-bounded, no parameter wait)
     const float* shb = score_h + rk * (long)G * MP;
-    float2 xv[16];
+    float2 xv[GL];
 #pragma unroll
-    for (int g = 0; g < 16; ++g) {                       // clamped, unconditional (see the row kernel)
+    for (int g = 0; g < GL; ++g) {                       // clamped, unconditional (see the row kernel)
         if constexpr (E == 2)
             xv[g] = *reinterpret_cast<const float2*>(shb + (long)min(g, G - 1) * MP + min(p0, MP - 2));
         else
@@ -843,7 +845,7 @@ __global__ __launch_bounds__(C2_BLK) void sel_chunk2_kernel(
 #pragma unroll
     for (int e = 0; e < E; ++e) acc[e] = (combine == 0) ? 0.f : -INFINITY;
 #pragma unroll
-    for (int g = 0; g < 16; ++g) {
+    for (int g = 0; g < GL; ++g) {
         if (g < G) {
             const float x4[2] = {xv[g].x, xv[g].y};
 #pragma unroll
@@ -1247,11 +1249,23 @@ extern "C" int32_t locks_select_nrm_topb(
         // 1.708, ragged batch 2.047 -> 1.977; 1M, 64 chunks: 2.297 -> 2.25-2.27)
         const int Zs = cdiv(max_pages, SEL_CH_MIN);
         const bool small_chunks = !band && G > 4 && (long)Zs * cdiv(min(b_max, SEL_CH), 8) <= F2_BLK;
+        // heads loaded per thread: the group rounded up to 1, 4, 8 or 16
+        const int gl = G == 1 ? 1 : G <= 4 ? 4 : G <= 8 ? 8 : 16;
+#define C2_LAUNCH(BANDV, EV, ZV, HISTV)                                                              \
+        do {                                                                                          \
+            auto go = [&](auto glc) {                                                                 \
+                hipLaunchKernelGGL((sel_chunk2_kernel<BANDV, EV, decltype(glc)::value>), dim3(ZV, n_kv, n_req), \
+                                   dim3(C2_BLK), 0, st, score_h, page_max, score_chunks, n_pages,     \
+                                   n_sel_hi, b_fix, score, page_table, cand_key, cand_page, cand_cnt, \
+                                   HISTV, n_sink, max_pages, G, combine);                            \
+            };                                                                                        \
+            if (gl == 1) go(std::integral_constant<int, 1>{});                                        \
+            else if (gl == 4) go(std::integral_constant<int, 4>{});                                   \
+            else if (gl == 8) go(std::integral_constant<int, 8>{});                                   \
+            else go(std::integral_constant<int, 16>{});                                               \
+        } while (0)
         if (small_chunks) {
-            hipLaunchKernelGGL((sel_chunk2_kernel<false, 1>), dim3(Zs, n_kv, n_req), dim3(C2_BLK), 0, st,
-                               score_h, page_max, score_chunks, n_pages, n_sel_hi, b_fix, score,
-                               page_table, cand_key, cand_page, cand_cnt, nullptr, n_sink, max_pages,
-                               G, combine);
+            C2_LAUNCH(false, 1, Zs, nullptr);
             int rc = check_launch("sel_chunk2_kernel<small>");
             if (rc) return rc;
             hipLaunchKernelGGL(sel_finish2_kernel, dim3(1, n_kv, n_req), dim3(F2_BLK), 0, st,
@@ -1260,10 +1274,7 @@ extern "C" int32_t locks_select_nrm_topb(
             return check_launch("sel_finish2_kernel");
         }
         if (band) {
-            hipLaunchKernelGGL(sel_chunk2_kernel<true>, dim3(Z1, n_kv, n_req), dim3(C2_BLK), 0, st,
-                               score_h, page_max, score_chunks, n_pages, n_sel_hi, b_fix, score,
-                               page_table, cand_key, cand_page, cand_cnt, ghist, n_sink, max_pages,
-                               G, combine);
+            C2_LAUNCH(true, C2_E, Z1, ghist);
             int rc = check_launch("sel_chunk2_kernel<band>");
             if (rc) return rc;
             hipLaunchKernelGGL(sel_band_kernel, dim3(Z1, n_kv, n_req), dim3(C2_BLK), 0, st,
@@ -1272,10 +1283,7 @@ extern "C" int32_t locks_select_nrm_topb(
             rc = check_launch("sel_band_kernel");
             if (rc) return rc;
         } else {
-            hipLaunchKernelGGL(sel_chunk2_kernel<false>, dim3(Z1, n_kv, n_req), dim3(C2_BLK), 0, st,
-                               score_h, page_max, score_chunks, n_pages, n_sel_hi, b_fix, score,
-                               page_table, cand_key, cand_page, cand_cnt, nullptr, n_sink, max_pages,
-                               G, combine);
+            C2_LAUNCH(false, C2_E, Z1, nullptr);
             int rc = check_launch("sel_chunk2_kernel");
             if (rc) return rc;
         }
@@ -1284,6 +1292,7 @@ extern "C" int32_t locks_select_nrm_topb(
                            cand_cnt, spill_key, spill_page, band ? ghist : nullptr, n_sink,
                            max_pages, Z1);
         return check_launch("sel_finish2_kernel");
+#undef C2_LAUNCH
     }
     hipLaunchKernelGGL(sel_chunk_kernel, dim3(Z1, n_kv, n_req), dim3(SEL_BLK), 0, st,
                        score_h, page_max, score_chunks, n_pages, n_sel_hi, b_fix, score,
