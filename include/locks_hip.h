@@ -92,7 +92,8 @@ int32_t locks_score_num_chunks(int32_t max_pages, int32_t chunk);
  *   block_table (n_req, bt_cols) i32, row stride bt_stride; page p -> block
  *   n_sel_hi   (n_req,) i32: pages [0, n_sel_hi) are scored
  *   score_h    (n_req, n_kv, G, max_pages) f32 -- written for p < n_sel_hi only
- *   page_max   (n_req, n_kv, chunks, 16) f32 -- per-chunk per-head maxima
+ *   page_max   (n_req, n_kv, 16, chunks) f32 -- per-head per-chunk maxima
+ *              (head-major: one head's chunk maxima are contiguous)
  *   chunk      pages per workgroup (locks_score_auto_chunk); one workgroup
  *              scores its chunk for one kv head (grid: chunks x n_kv x n_req)
  * Block ids are clamped to [0, num_blocks) and page ids to [0, bt_cols).

@@ -114,10 +114,10 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
     const int P = min(nsh[r], MP);          // never score past the score_h row
     const int c0 = z * chunk;
     const int c1 = min(c0 + chunk, P);
-    float* pm_out = pmax + (((long)r * n_kv + h) * Z + z) * 16;
+    float* pm_out = pmax + ((long)r * n_kv + h) * 16 * Z + z;     // head-major: pm_out[g * Z]
 
     if (c0 >= P) {                          // no page of this chunk is scored
-        if (tid < 16) pm_out[tid] = -INFINITY;
+        if (tid < 16) pm_out[(long)tid * Z] = -INFINITY;
         return;
     }
 
@@ -712,7 +712,7 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
         wrun = fmaxf(wrun, o == 4 ? row_ror<4>(wrun) : o == 8 ? row_ror<8>(wrun) : row_ror<2>(wrun));
     if ((TK4 || NGRP >= 4 || kg < 2) && (lane & 15) < GW && (lane & 15) < G) atomicMax(&wmax[lane & 15], f2u(wrun));
     __syncthreads();
-    if (tid < 16) pm_out[tid] = u2f(wmax[tid]);
+    if (tid < 16) pm_out[(long)tid * Z] = u2f(wmax[tid]);
 }
 
 }  // namespace locks

@@ -192,19 +192,19 @@ __device__ int emit_topk(const uint32_t* keys, int n, int k, uint32_t tau, PageO
     return total;
 }
 
-// Max over the n per-chunk entries p[16 * z] held by this wave's lanes, 8
-// independent loads in flight per lane (a serial load chain costs one
-// memory latency per step).
+// Max over one head's n per-chunk maxima p[0 .. n) (the scorer's page_max
+// is head-major, so a wave's loads are contiguous), 4 independent loads in
+// flight per lane (a serial load chain costs one memory latency per step).
 __device__ __forceinline__ float chunk_max(const float* __restrict__ p, int n) {
     const int lane = threadIdx.x & 63;
     float m = -INFINITY;
-    for (int z0 = lane; z0 < n; z0 += 8 * kWave) {
-        float t[8];
+    for (int z0 = lane; z0 < n; z0 += 4 * kWave) {
+        float t[4];
 #pragma unroll
-        for (int j = 0; j < 8; ++j)                    // clamped: a repeat leaves the max
-            t[j] = p[(long)min(z0 + j * kWave, n - 1) * 16];
+        for (int j = 0; j < 4; ++j)                    // clamped: a repeat leaves the max
+            t[j] = p[min(z0 + j * kWave, n - 1)];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) m = fmaxf(m, t[j]);
+        for (int j = 0; j < 4; ++j) m = fmaxf(m, t[j]);
     }
     return m;
 }
@@ -542,7 +542,7 @@ __global__ __launch_bounds__(ROW_BLK) void sel_row_kernel(
     if (combine == 0) {
         if (wave < G) {
             float m = -INFINITY;
-            m = chunk_max(pmax + rk * Zs * 16 + wave, Zs);
+            m = chunk_max(pmax + (rk * 16 + wave) * Zs, Zs);
             m = wave_max(m);
             if (lane == 0) hm[wave] = m;
         }
@@ -671,7 +671,7 @@ __global__ __launch_bounds__(SEL_BLK) void sel_chunk_kernel(
     if (combine == 0) {
         for (int g = wave; g < G; g += SEL_BLK / kWave) {
             float m = -INFINITY;
-            m = chunk_max(pmax + rk * Zs * 16 + g, Zs);
+            m = chunk_max(pmax + (rk * 16 + g) * Zs, Zs);
             m = wave_max(m);
             if (lane == 0) hm[g] = m;
         }
@@ -836,7 +836,7 @@ __global__ __launch_bounds__(C2_BLK) void sel_chunk2_kernel(
         if (p0 + e < MP) trow[p0 + e] = -1;
     if (combine == 0) {
         for (int g = wave; g < G; g += C2_BLK / kWave) {
-            const float m = wave_max(chunk_max(pmax + rk * Zs * 16 + g, Zs));
+            const float m = wave_max(chunk_max(pmax + (rk * 16 + g) * Zs, Zs));
             if (lane == 0) hm[g] = m;
         }
         lds_barrier();

@@ -14,8 +14,8 @@ Tensor names, shapes and dtypes follow the reference's six-slab layout
 Per-step outputs: score (R, n_kv, MP) f32, page_table (R, n_kv, MP) i32,
 page_cnt (R, n_kv) i32, score_h (R, n_kv, G, MP) f32, n_pages / n_sel_hi /
 b_fix (R,) i32.  Added for the MI355X kernels (all persistent, allocated here
-so no call allocates): page_max (R, n_kv, chunks, 16) f32 -- the scorer's
-per-chunk maxima -- and sel_ws, the selector's candidate workspace.
+so no call allocates): page_max (R, n_kv, 16, chunks) f32 -- the scorer's
+per-chunk maxima, head-major -- and sel_ws, the selector's candidate workspace.
 
 Footprint per (page, kv head): 5d + 10*page + 18 bytes of summary (818 B at
 d=128, page 16) + 16 B tag (rki4_state.py:18-22, record_bytes :124-141).
@@ -153,7 +153,7 @@ class Rki4State:
         self.score_chunk = chunk
         self.score_chunks = int(lib.locks_score_num_chunks(MP, chunk))
         self.zsplit = self.score_chunks
-        self.page_max = torch.full((R, n_kv, self.score_chunks, 16), float("-inf"),
+        self.page_max = torch.full((R, n_kv, 16, self.score_chunks), float("-inf"),
                                    device=dev, dtype=f32)
         ws = int(lib.locks_select_workspace_bytes(R, n_kv, MP))
         self.sel_ws = torch.zeros(max(ws, 256), device=dev, dtype=torch.uint8)

@@ -153,7 +153,7 @@ def test_score_geometry(hd, page, n_kv, G, seq_lens):
     ref64 = O.score_rki4_intpath(case.q, case.slabs, case.bt, nsh, n_kv, G, case.scale,
                                  case.MP, dtype=np.float64)
     got = st.score_h.cpu().numpy()
-    pm = st.page_max.cpu().numpy()
+    pm = st.page_max.cpu().numpy().transpose(0, 1, 3, 2)   # (R, n_kv, chunks, 16)
     for r in range(case.R):
         P = int(nsh[r])
         err = np.abs(got[r, ..., :P] - ref[r, ..., :P]).max() if P else 0.0

@@ -87,7 +87,7 @@ def test_score_matches_oracle(n_kv, G, ctx):
     say(f"max|gpu-twin|={err:.3e} max|gpu-exact|={err64:.3e}")
     assert err <= 2e-5 and err64 <= 2e-5
     # per-chunk maxima published for the selector
-    pm = st.page_max.cpu().numpy()
+    pm = st.page_max.cpu().numpy().transpose(0, 1, 3, 2)   # (R, n_kv, chunks, 16)
     for z in range(st.score_chunks):
         lo, hi = z * st.score_chunk, min((z + 1) * st.score_chunk, P)
         for kh in range(n_kv):
@@ -163,7 +163,7 @@ def _random_select_inputs(seed, n_kv, G, seq_lens, MP, st, ties=None):
             if hi > lo:
                 pm[r, :, z, :G] = sh[r, :, :, lo:hi].max(axis=-1)
     st.score_h.copy_(torch.from_numpy(sh))
-    st.page_max.copy_(torch.from_numpy(pm))
+    st.page_max.copy_(torch.from_numpy(np.ascontiguousarray(pm.transpose(0, 1, 3, 2))))
     return sh, npg, nsh, b
 
 

@@ -65,7 +65,7 @@ def _run(seed, n_kv, G, seq_lens, zsplit=None, expect_chunk=None, check64=True):
     rki4_score_only(st, 0, dq, dbt, dsl, R, scale)
     torch.cuda.synchronize()
     got = st.score_h.cpu().numpy()
-    pm = st.page_max.cpu().numpy()
+    pm = st.page_max.cpu().numpy().transpose(0, 1, 3, 2)   # (R, n_kv, chunks, 16)
     nsh = st.n_sel_hi.cpu().numpy()
     ref = score_oracle_chunked(q, slabs, bt, nsh, n_kv, G, scale, MP)
     ref64 = score_oracle_chunked(q, slabs, bt, nsh, n_kv, G, scale, MP,
