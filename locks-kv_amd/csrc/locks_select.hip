@@ -551,20 +551,39 @@ __global__ __launch_bounds__(ROW_BLK) void sel_row_kernel(
     float acc[E];
 #pragma unroll
     for (int e = 0; e < E; ++e) acc[e] = (combine == 0) ? 0.f : -INFINITY;
+    // The combine mode is tested once, outside the loops, and heads past G
+    // are masked by selects, not branches: a uniform branch per element
+    // split every exp into its own basic block (no overlap between them).
+    // Heads are summed in ascending order either way.
     for (int g0 = 0; g0 < G; g0 += HB) {
         if (g0 > 0) load_batch(g0);
+        if (combine == 0) {
 #pragma unroll
-        for (int j = 0; j < HB; ++j) {
-            const int g = g0 + j;
-            if (g >= G) break;
-            const float h = (combine == 0) ? hm[g] : 0.f;
+            for (int j = 0; j < HB; ++j) {
+                const bool on = g0 + j < G;
+                const float h = hm[min(g0 + j, G - 1)];
 #pragma unroll
-            for (int v = 0; v < E / 4; ++v) {
-                const float x4[4] = {xv[j][v].x, xv[j][v].y, xv[j][v].z, xv[j][v].w};
+                for (int v = 0; v < E / 4; ++v) {
+                    const float x4[4] = {xv[j][v].x, xv[j][v].y, xv[j][v].z, xv[j][v].w};
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    if (combine == 0) acc[4 * v + i] += __expf(x4[i] - h);
-                    else acc[4 * v + i] = (g == 0) ? x4[i] : fmaxf(acc[4 * v + i], x4[i]);
+                    for (int i = 0; i < 4; ++i) {
+                        const float t = __expf(x4[i] - h);
+                        acc[4 * v + i] = on ? acc[4 * v + i] + t : acc[4 * v + i];
+                    }
+                }
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < HB; ++j) {
+                const int g = g0 + j;
+#pragma unroll
+                for (int v = 0; v < E / 4; ++v) {
+                    const float x4[4] = {xv[j][v].x, xv[j][v].y, xv[j][v].z, xv[j][v].w};
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float mx = (g == 0) ? x4[i] : fmaxf(acc[4 * v + i], x4[i]);
+                        acc[4 * v + i] = (g < G) ? mx : acc[4 * v + i];
+                    }
                 }
             }
         }
@@ -844,14 +863,27 @@ __global__ __launch_bounds__(C2_BLK) void sel_chunk2_kernel(
     float acc[E];
 #pragma unroll
     for (int e = 0; e < E; ++e) acc[e] = (combine == 0) ? 0.f : -INFINITY;
+    // combine mode tested once, heads past G masked by selects (see the row
+    // kernel)
+    if (combine == 0) {
 #pragma unroll
-    for (int g = 0; g < GL; ++g) {
-        if (g < G) {
+        for (int g = 0; g < GL; ++g) {
+            const float x4[2] = {xv[g].x, xv[g].y};
+            const float h = hm[min(g, G - 1)];
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                const float t = __expf(x4[e] - h);
+                acc[e] = (g < G) ? acc[e] + t : acc[e];
+            }
+        }
+    } else {
+#pragma unroll
+        for (int g = 0; g < GL; ++g) {
             const float x4[2] = {xv[g].x, xv[g].y};
 #pragma unroll
             for (int e = 0; e < E; ++e) {
-                if (combine == 0) acc[e] += __expf(x4[e] - hm[g]);
-                else acc[e] = (g == 0) ? x4[e] : fmaxf(acc[e], x4[e]);
+                const float mx = (g == 0) ? x4[e] : fmaxf(acc[e], x4[e]);
+                acc[e] = (g < G) ? mx : acc[e];
             }
         }
     }
