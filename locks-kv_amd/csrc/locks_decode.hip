@@ -721,13 +721,20 @@ __global__ __launch_bounds__(MH_BLK) void decode_merge_heads_kernel(
 #pragma unroll
     for (int w = 0; w < MH_BLK / kWave; ++w) lt += red[w];
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    // weights of the prefetched partials: every LDS read issued before the
+    // first use (a guarded read per partial was one LDS round trip each);
+    // partials past the active count are left out by selects
+    float wk[MH_PF];
 #pragma unroll
-    for (int k = 0; k < MH_PF; ++k) {
-        const int sidx = strm + k * MH_STREAMS;
-        if (sidx < n_act) {
-            const float w = w_s[sidx];
-            acc.x += w * pre[k].x; acc.y += w * pre[k].y; acc.z += w * pre[k].z; acc.w += w * pre[k].w;
-        }
+    for (int k = 0; k < MH_PF; ++k) wk[k] = w_s[min(strm + k * MH_STREAMS, MAX_SPLIT - 1)];
+#pragma unroll
+    for (int k = 0; k < MH_PF; ++k) {          // selects, not branches (stale rows may hold NaN)
+        const bool on = strm + k * MH_STREAMS < n_act;
+        const float w = wk[k];
+        acc.x = on ? acc.x + w * pre[k].x : acc.x;
+        acc.y = on ? acc.y + w * pre[k].y : acc.y;
+        acc.z = on ? acc.z + w * pre[k].z : acc.z;
+        acc.w = on ? acc.w + w * pre[k].w : acc.w;
     }
 #pragma unroll 4
     for (int s = strm + MH_PF * MH_STREAMS; s < n_act; s += MH_STREAMS) {

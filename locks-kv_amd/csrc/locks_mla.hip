@@ -806,13 +806,19 @@ __global__ __launch_bounds__(MG_BLK) void mla_merge_kernel(
     for (int w = 0; w < MG_BLK / kWave; ++w) L += red[w];
     // acc over this slice: column c (4 dims), split group g
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    // every weight read issued before the first use (a guarded read per
+    // partial was one LDS round trip each); inactive partials left out by
+    // selects (their rows may be stale)
+    float wk[PF];
+#pragma unroll
+    for (int k = 0; k < PF; ++k) wk[k] = w_s[min(g + k * MG_GRP, MD_MAX_SPLIT - 1)];
 #pragma unroll
     for (int k = 0; k < PF; ++k) {
-        const int s = g + k * MG_GRP;
-        if (s < n_act) {
-            const float w = w_s[s];
-            acc.x += w * pre[k].x; acc.y += w * pre[k].y; acc.z += w * pre[k].z; acc.w += w * pre[k].w;
-        }
+        const bool on = g + k * MG_GRP < n_act;
+        acc.x = on ? acc.x + wk[k] * pre[k].x : acc.x;
+        acc.y = on ? acc.y + wk[k] * pre[k].y : acc.y;
+        acc.z = on ? acc.z + wk[k] * pre[k].z : acc.z;
+        acc.w = on ? acc.w + wk[k] * pre[k].w : acc.w;
     }
     int s = g + PF * MG_GRP;
     for (; s + (PF - 1) * MG_GRP < n_act; s += PF * MG_GRP) {
