@@ -47,7 +47,8 @@ constexpr int FIN_MAXZ = 1024;     // chunks per row the finisher can index
 // ---------------------------------------------------------------------------
 // block primitives
 // ---------------------------------------------------------------------------
-template <int BLK>
+// TAIL: the closing barrier that lets the caller reuse wsum right away
+template <int BLK, bool TAIL = true>
 __device__ __forceinline__ int block_excl_scan(int v, int* wsum, int& total) {
     constexpr int NW = BLK / kWave;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -63,7 +64,7 @@ __device__ __forceinline__ int block_excl_scan(int v, int* wsum, int& total) {
     lds_barrier();
     const int res = wsum[w] + incl - v;
     total = wsum[NW];
-    lds_barrier();
+    if constexpr (TAIL) lds_barrier();
     return res;
 }
 
@@ -363,23 +364,30 @@ __device__ RadixSel reg_kth_largest_abs(const uint32_t (&key)[E], const bool (&v
 // Llama 128K, chunk select -0.7 us at 1M).  A boundary in the clamped bin 0
 // (the k-th key more than 16 binades below the maximum) falls back to the
 // absolute radix.
+//
+// mk_bound != 0: an upper bound of every valid key known to the caller (the
+// bins are placed relative to it instead of the exact maximum, one block
+// reduction and barrier fewer); the caller has then also zeroed hist and
+// s3[3] before a barrier that every thread passed since.
 template <int BLK, int E, bool COMPACT = true>
 __device__ RadixSel reg_kth_largest(const uint32_t (&key)[E], const bool (&val)[E], int k,
-                                    int* hist, int* wtot, int* s3) {
+                                    int* hist, int* wtot, int* s3, uint32_t mk_bound = 0u) {
     constexpr int NW = BLK / kWave;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    // row maximum over the valid keys (0 when none: every valid key >= 0)
-    uint32_t mx = 0u;
+    uint32_t mk = mk_bound;
+    if (mk_bound == 0u) {
+        // row maximum over the valid keys (0 when none: every valid key >= 0)
+        uint32_t mx = 0u;
 #pragma unroll
-    for (int e = 0; e < E; ++e) mx = val[e] ? max(mx, key[e]) : mx;
-    for (int i = tid; i < 4096; i += BLK) hist[i] = 0;
-    if (tid == 0) s3[3] = 0;                                  // candidate counter (compaction below)
-    mx = wave_max_u32(mx);
-    if (lane == 0) wtot[wave] = (int)mx;
-    lds_barrier();
-    uint32_t mk = 0u;
+        for (int e = 0; e < E; ++e) mx = val[e] ? max(mx, key[e]) : mx;
+        for (int i = tid; i < 4096; i += BLK) hist[i] = 0;
+        if (tid == 0) s3[3] = 0;                              // candidate counter (compaction below)
+        mx = wave_max_u32(mx);
+        if (lane == 0) wtot[wave] = (int)mx;
+        lds_barrier();
 #pragma unroll
-    for (int w = 0; w < NW; ++w) mk = max(mk, (uint32_t)wtot[w]);
+        for (int w = 0; w < NW; ++w) mk = max(mk, (uint32_t)wtot[w]);
+    }
     // pass 0: bins relative to mk
 #pragma unroll
     for (int e = 0; e < E; ++e) {
@@ -450,7 +458,7 @@ __device__ RadixSel reg_kth_largest(const uint32_t (&key)[E], const bool (&val)[
 
 // Emission in item order: out(pos, e) is called for every kept item of
 // this thread with its rank among all kept items.  Returns the kept count.
-template <int BLK, int E, class Out>
+template <int BLK, int E, bool TAIL = true, class Out>
 __device__ int reg_emit(const uint32_t (&key)[E], const bool (&val)[E], const RadixSel& rs,
                         int* wsum, Out out) {
     int gt = 0, eq = 0;
@@ -461,7 +469,7 @@ __device__ int reg_emit(const uint32_t (&key)[E], const bool (&val)[E], const Ra
         else { gt += key[e] > rs.tau; eq += key[e] == rs.tau; }
     }
     int tot;
-    const int ex = block_excl_scan<BLK>(gt | (eq << 16), wsum, tot);
+    const int ex = block_excl_scan<BLK, TAIL>(gt | (eq << 16), wsum, tot);
     const int quota = rs.whole_bin ? 0 : rs.k;
     int pos = (ex & 0xFFFF) + min(ex >> 16, quota);
     int er = ex >> 16;
@@ -518,6 +526,12 @@ __global__ __launch_bounds__(ROW_BLK) void sel_row_kernel(
     __shared__ int wtot[ROW_NW];
     __shared__ int s3[4];
     __shared__ int wsum[ROW_NW + 1];
+    // nrm: the radix histogram is zeroed here, ahead of the head-max barrier
+    // (the selection then needs no barrier of its own before its first pass)
+    if (combine == 0) {
+        for (int i = tid; i < 4096; i += ROW_BLK) hist[i] = 0;
+        if (tid == 0) s3[3] = 0;
+    }
 
     // ---- score_h of the first HB heads in flight before the head maxima.
     // Loads are bounded by the row (MP), not by n_sel_hi, so they do not wait
@@ -619,8 +633,12 @@ __global__ __launch_bounds__(ROW_BLK) void sel_row_kernel(
         val[e] = (p >= n_sink) && (p < n_sel_hi);
         key[e] = f2u(acc[e]);
     }
-    const RadixSel rs = reg_kth_largest<ROW_BLK, E>(key, val, b, hist, wtot, s3);
-    reg_emit<ROW_BLK, E>(key, val, rs, wsum, [&](int pos, int e) { trow[n_sink + pos] = p0 + e; });
+    // nrm keys are sums of G terms exp(s - max_p s) <= 1: 2G bounds them
+    // (with a binade to spare), so the bins need no block maximum
+    const uint32_t mk_bound = (combine == 0) ? f2u(2.f * (float)G) : 0u;
+    const RadixSel rs = reg_kth_largest<ROW_BLK, E>(key, val, b, hist, wtot, s3, mk_bound);
+    // wsum is not used again: no closing barrier after the emission scan
+    reg_emit<ROW_BLK, E, false>(key, val, rs, wsum, [&](int pos, int e) { trow[n_sink + pos] = p0 + e; });
     const int cnt = n_sink + b + (n_pages - n_sel_hi);
     if (p0 >= cnt && p0 + E <= MP) {                      // padding only
 #pragma unroll
