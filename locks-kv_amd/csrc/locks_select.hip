@@ -872,6 +872,12 @@ __global__ __launch_bounds__(C2_BLK) void sel_chunk2_kernel(
     for (int e = 0; e < E; ++e)
         if (p0 + e < MP) trow[p0 + e] = -1;
     if (combine == 0) {
+        // the radix histogram is zeroed ahead of this barrier (the local
+        // selection then needs no barrier of its own before its first pass)
+        if constexpr (!BAND) {
+            for (int i = tid; i < 4096; i += C2_BLK) hist[i] = 0;
+            if (tid == 0) s3[3] = 0;
+        }
         for (int g = wave; g < G; g += C2_BLK / kWave) {
             const float m = wave_max(chunk_max(pmax + (rk * 16 + g) * Zs, Zs));
             if (lane == 0) hm[g] = m;
@@ -923,13 +929,11 @@ __global__ __launch_bounds__(C2_BLK) void sel_chunk2_kernel(
     b = max(1, min(b, max(n_sel, 1)));
     uint32_t key[E];
     bool val[E];
-    int nv = 0;
 #pragma unroll
     for (int e = 0; e < E; ++e) {
         const int p = p0 + e;
         val[e] = (n_sel > 1) && p >= n_sink && p < n_sel_hi;
         key[e] = f2u(acc[e]);
-        nv += val[e];
     }
     if constexpr (BAND) {
         for (int i = tid; i < 4096; i += C2_BLK) hist[i] = 0;
@@ -942,16 +946,20 @@ __global__ __launch_bounds__(C2_BLK) void sel_chunk2_kernel(
             if (hist[i]) __hip_atomic_fetch_add(gh + i, hist[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return;
     }
-    int n_loc;
-    block_excl_scan<C2_BLK>(nv, wsum, n_loc);
+    // valid pages of the chunk: [max(c0, n_sink), min(c0 + CH, n_sel_hi))
+    const int n_loc = (n_sel > 1) ? max(0, min(c0 + CH, n_sel_hi) - max(c0, n_sink)) : 0;
     uint32_t* ck = cand_key + (rk * Z1 + z) * (long)SEL_CH;
     int* cp = cand_page + (rk * Z1 + z) * (long)SEL_CH;
     int ncand = 0;
     if (n_loc > 0) {
         const int k_loc = min(b, n_loc);
         RadixSel rs{0u, 0u, 0, true};                    // k_loc == n_loc: keep every valid key (>= 0)
-        if (k_loc < n_loc) rs = reg_kth_largest<C2_BLK, E>(key, val, k_loc, hist, wtot, s3);
-        ncand = reg_emit<C2_BLK, E>(key, val, rs, wsum, [&](int pos, int e) {
+        // nrm keys are sums of G terms <= 1: 2G bounds them (see the row
+        // kernel); the histogram was zeroed before the head-max barrier
+        if (k_loc < n_loc)
+            rs = reg_kth_largest<C2_BLK, E>(key, val, k_loc, hist, wtot, s3,
+                                            combine == 0 ? f2u(2.f * (float)G) : 0u);
+        ncand = reg_emit<C2_BLK, E, false>(key, val, rs, wsum, [&](int pos, int e) {
             ck[pos] = key[e];
             cp[pos] = p0 + e;
         });
