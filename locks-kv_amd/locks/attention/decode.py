@@ -60,13 +60,21 @@ PPS_MIN_OVERRIDE = None        # set by bench sweeps; None = the table below
 def _pps_min(n_req: int, n_kv: int = 8) -> int:
     """Minimum pages per split workgroup (4 waves, 1-2 pages each at bs=1):
     amortises the q load, the 4-wave LDS merge and the partial store.
-    Measured on MI355X at 128 attended pages: 4 for >= 4 kv heads (Llama,
-    256 workgroups), 8 for 2 kv heads (GLM)."""
+    Measured on MI355X at 128 attended pages per row (step ms, pps_min
+    16 / 8 / 4): bs=1, 4 for >= 4 kv heads (Llama, 256 workgroups), 8 for 2
+    (GLM); with several requests the best keeps ~256 split workgroups, i.e.
+    rows / 2 pages per split for rows = n_req x n_kv -- GLM ragged batch of
+    4 (8 rows) 1.907 / 1.853 / 1.846, GLM 8 x 64K (16 rows) 1.765 / 1.733 /
+    1.801, Llama 4 requests (32 rows) 2.108 / 2.168 / 2.268; from 16
+    requests 32 (Llama 16 x 32K: 2.88-2.90 ms against 2.89-2.99 at 16)."""
     if PPS_MIN_OVERRIDE:
         return int(PPS_MIN_OVERRIDE)
     if n_req == 1:
         return 4 if n_kv >= 4 else 8
-    return 16 if n_req < 16 else 32
+    if n_req >= 16:
+        return 32
+    half = max(1, -(-int(n_req) * int(n_kv) // 2))
+    return min(16, max(4, 1 << (half - 1).bit_length()))
 
 
 def _adaptive_split(max_reqs: int, max_pages: int, budget: float, hard_cap: int) -> int:
