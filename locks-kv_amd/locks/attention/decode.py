@@ -60,17 +60,16 @@ PPS_MIN_OVERRIDE = None        # set by bench sweeps; None = the table below
 def _pps_min(n_req: int, n_kv: int = 8) -> int:
     """Minimum pages per split workgroup (4 waves, 1-2 pages each at bs=1):
     amortises the q load, the 4-wave LDS merge and the partial store.
-    Measured on MI355X at 128 attended pages per row (step ms, pps_min
-    16 / 8 / 4): bs=1, 4 for >= 4 kv heads (Llama, 256 workgroups), 8 for 2
-    (GLM); with several requests the best keeps ~256 split workgroups, i.e.
-    rows / 2 pages per split for rows = n_req x n_kv -- GLM ragged batch of
-    4 (8 rows) 1.907 / 1.853 / 1.846, GLM 8 x 64K (16 rows) 1.765 / 1.733 /
-    1.801, Llama 4 requests (32 rows) 2.108 / 2.168 / 2.268; from 16
-    requests 32 (Llama 16 x 32K: 2.88-2.90 ms against 2.89-2.99 at 16)."""
+    Measured on MI355X at 128 attended pages per row: the best keeps ~256
+    split workgroups, i.e. rows / 2 pages per split (at least 4) for rows =
+    n_req x n_kv.  Steps at pps_min 16 / 8 / 4: GLM ragged batch of 4 (8
+    rows) 1.907 / 1.853 / 1.846 ms, GLM 8 x 64K (16 rows) 1.765 / 1.733 /
+    1.801, Llama 4 requests (32 rows) 2.108 / 2.168 / 2.268; bs = 1: Llama
+    (8 rows) 4, GLM 1M (2 rows) at 8 / 4 / 2: 2.089-2.093 / 2.048-2.073 /
+    2.071-2.084.  From 16 requests 32 (Llama 16 x 32K: 2.88-2.90 ms against
+    2.89-2.99 at 16)."""
     if PPS_MIN_OVERRIDE:
         return int(PPS_MIN_OVERRIDE)
-    if n_req == 1:
-        return 4 if n_kv >= 4 else 8
     if n_req >= 16:
         return 32
     half = max(1, -(-int(n_req) * int(n_kv) // 2))
