@@ -12,6 +12,7 @@ import numpy as np
 import pytest
 
 from oracle import locks_oracle as O
+from oracle import mla_oracle as M
 from tests.golden import make_golden as MG
 
 PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "locks_golden.npz")
@@ -84,6 +85,34 @@ def test_ties_case(gold):
         sel = gold["ties_comb_max"][0, kh, sink:nsh]
         tau = np.sort(sel)[::-1][b - 1]
         assert (sel == tau).sum() > (np.sort(sel)[::-1][:b] == tau).sum()
+
+
+def test_mla_case(gold):
+    m = MG.MLA
+    slabs = {k: gold["mla_slab_" + k] for k in MG.SLAB_KEYS}
+    got = MG.mla_outputs(gold["mla_q"], gold["mla_cache"], gold["mla_bt"], slabs,
+                         gold["mla_seq_lens"].tolist(), m["budget_pages"], m["sink"], m["window"],
+                         m["scale"])
+    for k in ("npg", "nsh", "b", "tab", "cnt"):
+        assert np.array_equal(got[k], gold["mla_" + k]), k
+    for k in ("score", "out", "lse"):
+        _close(got[k], gold["mla_" + k])
+    # a real selection: fewer pages kept than the row has
+    assert int(gold["mla_cnt"][0]) == m["budget_pages"] < int(gold["mla_npg"][0])
+
+
+def test_mla_slabs_are_the_builders(gold):
+    bt, sl = gold["mla_bt"], gold["mla_seq_lens"]
+    fin = sorted({int(bt[r, j]) for r in range(len(sl)) for j in range(int(sl[r]) // 16)})
+    slabs = M.mla_build_summaries(gold["mla_cache"], np.array(fin, np.int32), gold["mla_cache"].shape[0])
+    for k in ("mu8", "mus"):
+        assert np.array_equal(slabs[k][fin], gold["mla_slab_" + k][fin]), k
+    for k in ("c8", "v4"):
+        a, b = slabs[k][fin], gold["mla_slab_" + k][fin]
+        if k == "v4":
+            a, b = O.unpack_i4(a), O.unpack_i4(b)
+        d = np.abs(a.astype(np.int32) - b.astype(np.int32))
+        assert d.max() <= 1 and (d > 0).mean() < 0.01, k
 
 
 def test_derive_table(gold):

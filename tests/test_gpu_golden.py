@@ -150,6 +150,52 @@ def test_golden_select(gold, prefix, combine):
     _check_select(st, prefix, gold, combine, G)
 
 
+def test_golden_mla(gold):
+    """MLA path: derive + latent score + topb_middle, then the split decode
+    and merge over the selection."""
+    import torch
+    from locks.attention import mla_decode
+    from locks.selection import MlaState, mla_select_pages
+    u16 = lambda a: torch.from_numpy(a.view(np.int16).copy()).view(torch.bfloat16).cuda()
+    q, cache, bt, sl = gold["mla_q"], gold["mla_cache"], gold["mla_bt"], gold["mla_seq_lens"]
+    R, H, _ = q.shape
+    say("mla", R, H, sl.tolist())
+    st = MlaState("cuda", num_layers=1, num_blocks=cache.shape[0], n_heads=H, max_reqs=R,
+                  max_pages=bt.shape[1], budget_pages=14, sink_pages=1, window_pages=10, rope="exact")
+    for k, name in (("v4", "pp_v4"), ("vs", "pp_vs"), ("c8", "pp_c8"), ("cs", "pp_cs"),
+                    ("mu8", "pp_mu8"), ("mus", "pp_mus")):
+        a = gold["mla_slab_" + k]
+        t = getattr(st, name)[0]
+        if a.dtype == np.uint16:
+            t.copy_(torch.from_numpy(a.view(np.int16).copy()).view(torch.bfloat16).reshape(t.shape))
+        else:
+            t.copy_(torch.from_numpy(a.copy()).reshape(t.shape))
+    dq, dc = u16(q), u16(cache)
+    dbt, dsl = torch.from_numpy(bt).cuda(), torch.from_numpy(sl).cuda()
+    mla_select_pages(st, 0, dq, dc, dbt, dsl, R, 0.07)
+    torch.cuda.synchronize()
+    ref = gold["mla_score"]
+    got = st.score_h[:, 0, 0, :].cpu().numpy()
+    for r in range(R):
+        P = int(gold["mla_nsh"][r])
+        err = np.abs(got[r, :P] - ref[r, :P]).max()
+        say(f"score: {P} pages, max|gpu - golden| = {err:.3e}")
+        assert err <= 2e-4 * max(1.0, np.abs(ref[r, :P]).max())
+    assert np.array_equal(st.page_table[:, 0].cpu().numpy(), gold["mla_tab"])
+    assert np.array_equal(st.page_cnt[:, 0].cpu().numpy(), gold["mla_cnt"])
+    out = torch.empty(R, H, 512, dtype=torch.bfloat16, device="cuda")
+    lse = torch.empty(R, H, dtype=torch.float32, device="cuda")
+    mla_decode(st, dq, dc, dbt, dsl, R, 0.07, out, lse=lse)
+    torch.cuda.synchronize()
+    ro = O.bf16_round(gold["mla_out"].astype(np.float32)).astype(np.float64)
+    go = out.float().cpu().numpy().astype(np.float64)
+    err = np.abs(go - ro)
+    mr = err.sum() / np.abs(ro).sum()
+    lerr = np.abs(lse.cpu().numpy() - gold["mla_lse"]).max()
+    say(f"decode: max-abs {err.max():.3e} mean-rel {mr:.3e}; lse max-abs {lerr:.3e}")
+    assert err.max() <= 2e-2 and mr <= 1e-3 and lerr <= 2e-3
+
+
 def test_golden_decode(gold):
     import torch
     from locks.attention import decode_merge, decode_splitk
