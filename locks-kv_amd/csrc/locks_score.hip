@@ -43,6 +43,7 @@ constexpr int SC_TILE = 8;    // pages per wave tile
 constexpr int SC_WAVES = 4;
 constexpr int SC_BLOCK = SC_WAVES * kWave;
 constexpr int SC_MAX_CHUNK = 1024;          // pages per workgroup, upper bound
+constexpr int SC_STAGE_F = 4096;            // STG: floats of score_h staged per workgroup (16 KB)
 constexpr int SC_CPOL_NT = 2;                // buffer-load cache policy: non-temporal
 
 // Per-geometry layout (head_dim D in {64, 128, 256}, page PG in {16, 32, 64}).
@@ -94,7 +95,7 @@ __device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d) {
            ((uint32_t)(uint8_t)c << 16) | ((uint32_t)(uint8_t)d << 24);
 }
 
-template <int GW, int D = 128, int PG = 16, bool PK = true, bool PIPE = true>
+template <int GW, int D = 128, int PG = 16, bool PK = true, bool PIPE = true, bool STG = false>
 __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
     const uint16_t* __restrict__ q, long q_sr, long q_sh, SlabRows S, int NB, const int* __restrict__ bt, long bt_sr, int bt_cols,
     const int* __restrict__ nsh, float* __restrict__ score_h, int MP,
@@ -129,6 +130,14 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
     __shared__ __attribute__((aligned(16))) uint8_t sa_l[SC_WAVES][GM::ST_BYTES];
     __shared__ __attribute__((aligned(16))) uint8_t sb_l[SC_WAVES][GM::ST_BYTES];
     __shared__ uint32_t wmax[16];
+    // STG: the workgroup's scores [head][page of the chunk], written out
+    // coalesced after the last unit.  Stored straight to score_h, each unit's
+    // scattered stores (8 pages x G per wave) sat in the vector-memory counter
+    // ahead of the next unit's record DMA, and the wait for that DMA waited
+    // for them too (GLM 1M scorer 28.5 -> 26 us with the stores left out).  A
+    // static object of its own: the compiler sees it is not a DMA target and
+    // does not wait for the DMA before writing it.
+    __shared__ __attribute__((aligned(16))) float sc_l[STG ? SC_STAGE_F : 1];
     // PIPE: centroid terms mud[page][head] of a wave's last two units (rows
     // 8-15: idle lanes); otherwise they go to the unit's consumed stage rows
     __shared__ __attribute__((aligned(16))) float mud_l[PIPE ? SC_WAVES : 1][2][PIPE ? 16 * 16 : 4];
@@ -550,7 +559,8 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
         }
         if ((qd & 1) == 0 && page < nvalid && g_l < G) {
             wrun = fmaxf(wrun, Sv);
-            score_h[(((long)r * n_kv + h) * G + g_l) * (long)MP + p0 + page] = Sv;
+            if constexpr (STG) sc_l[g_l * (c1 - c0) + (p0 - c0) + page] = Sv;
+            else score_h[(((long)r * n_kv + h) * G + g_l) * (long)MP + p0 + page] = Sv;
         }
         } else {
         // k-slot kg, step hh <-> basis column 2kg + hh (both operands);
@@ -655,7 +665,8 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
             const int page = grp_of(sx) * PPM + psub_l;
             if (row_owner && (page < nvalid) && (g_l < G)) {
                 tmax = fmaxf(tmax, Sv[sx]);
-                score_h[(((long)r * n_kv + h) * G + g_l) * (long)MP + p0 + page] = Sv[sx];
+                if constexpr (STG) sc_l[g_l * (c1 - c0) + (p0 - c0) + page] = Sv[sx];
+                else score_h[(((long)r * n_kv + h) * G + g_l) * (long)MP + p0 + page] = Sv[sx];
             }
         }
         wrun = fmaxf(wrun, tmax);
@@ -712,6 +723,12 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
         wrun = fmaxf(wrun, o == 4 ? row_ror<4>(wrun) : o == 8 ? row_ror<8>(wrun) : row_ror<2>(wrun));
     if ((TK4 || NGRP >= 4 || kg < 2) && (lane & 15) < GW && (lane & 15) < G) atomicMax(&wmax[lane & 15], f2u(wrun));
     __syncthreads();
+    if constexpr (STG) {
+        const int n = c1 - c0;
+        float* srow = score_h + ((long)r * n_kv + h) * G * (long)MP + c0;
+        for (int g = 0; g < G; ++g)
+            for (int p = tid; p < n; p += SC_BLOCK) srow[(long)g * MP + p] = sc_l[g * n + p];
+    }
     if (tid < 16) pm_out[(long)tid * Z] = u2f(wmax[tid]);
 }
 
@@ -781,6 +798,11 @@ extern "C" int32_t locks_score_rki4(
     const int Z = cdiv(max_pages, chunk);
     dim3 grid(Z, n_kv, n_req);
     const size_t dyn = (size_t)chunk * sizeof(int);
+    // one request and a wide group: the scores are staged in LDS when the
+    // chunk's fit (GLM 1M, G = 16: step 2.051 -> 2.017 ms; at Llama's G = 4
+    // a unit stores 32 scores, and the closing copy cost more than it saved:
+    // 1.035 -> 1.052 ms)
+    const bool stg = G > 8 && (long)chunk * G <= SC_STAGE_F;
     hipStream_t st = (hipStream_t)stream;
     // packed rows: all six fields of a row together, in the kernel's order,
     // rows of one common stride (any stride >= the fields: the reference's
@@ -790,8 +812,8 @@ extern "C" int32_t locks_score_rki4(
                         S.scs == RSB && S.smu == RSB && S.smus == RSB &&
                         S.mu == S.v4 + 4L * head_dim && S.c8 == S.mu + head_dim &&
                         S.cs == S.c8 + 8L * page && S.vs == S.cs + 2L * page && S.mus == S.vs + 16;
-#define LAUNCH_P(GWV, DV, PGV, PKV, PIPEV)                                                     \
-    hipLaunchKernelGGL((rki4_score_kernel<GWV, DV, PGV, PKV, PIPEV>), grid, dim3(SC_BLOCK), dyn, st, q, \
+#define LAUNCH_P(GWV, DV, PGV, PKV, PIPEV, STGV)                                               \
+    hipLaunchKernelGGL((rki4_score_kernel<GWV, DV, PGV, PKV, PIPEV, STGV>), grid, dim3(SC_BLOCK), dyn, st, q, \
                        (long)q_stride_req, (long)q_stride_head, S,                             \
                        num_blocks, block_table, (long)bt_stride, bt_cols, n_sel_hi,            \
                        score_h, max_pages, page_max, n_kv, G, sm_scale, chunk)
@@ -801,8 +823,9 @@ extern "C" int32_t locks_score_rki4(
     // (ragged GLM batch step 2.05 -> 1.95 ms)
 #define LAUNCH(GWV, DV, PGV, PKV)                                    \
     do {                                                             \
-        if (n_req == 1) LAUNCH_P(GWV, DV, PGV, PKV, true);           \
-        else LAUNCH_P(GWV, DV, PGV, PKV, false);                     \
+        if (n_req == 1 && stg) LAUNCH_P(GWV, DV, PGV, PKV, true, true); \
+        else if (n_req == 1) LAUNCH_P(GWV, DV, PGV, PKV, true, false); \
+        else LAUNCH_P(GWV, DV, PGV, PKV, false, false);              \
     } while (0)
 #define LAUNCH_GP(DV, PGV, PKV)                    \
     do {                                           \
