@@ -853,7 +853,7 @@ extern "C" int32_t locks_score_rki4(
     // (ragged GLM batch step 2.05 -> 1.95 ms)
 #define LAUNCH(GWV, DV, PGV, PKV)                                    \
     do {                                                             \
-        if (n_req == 1 && stg) LAUNCH_P(GWV, DV, PGV, PKV, true, true); \
+        if (n_req == 1 && stg) LAUNCH_P(GWV, DV, PGV, PKV, true, (GWV == 16)); \
         else if (n_req == 1) LAUNCH_P(GWV, DV, PGV, PKV, true, false); \
         else LAUNCH_P(GWV, DV, PGV, PKV, false, false);              \
     } while (0)
