@@ -137,7 +137,9 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
     // for them too (GLM 1M scorer 28.5 -> 26 us with the stores left out).  A
     // static object of its own: the compiler sees it is not a DMA target and
     // does not wait for the DMA before writing it.
-    __shared__ __attribute__((aligned(16))) float sc_l[STG ? SC_STAGE_F : 1];
+    // (rows padded by one float: at a 256-page chunk the heads of one store
+    // would otherwise all hit one bank)
+    __shared__ __attribute__((aligned(16))) float sc_l[STG ? SC_STAGE_F + 16 : 1];
     // PIPE: centroid terms mud[page][head] of a wave's last two units (rows
     // 8-15: idle lanes); otherwise they go to the unit's consumed stage rows
     __shared__ __attribute__((aligned(16))) float mud_l[PIPE ? SC_WAVES : 1][2][PIPE ? 16 * 16 : 4];
@@ -587,7 +589,7 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
         const bool keep = (qd & 1) == 0 && page < nvalid && g_l < G;
         if (keep) {
             wrun = fmaxf(wrun, Sv);
-            if constexpr (STG) sc_l[g_l * (c1 - c0) + (p0 - c0) + page] = Sv;
+            if constexpr (STG) sc_l[g_l * (c1 - c0 + 1) + (p0 - c0) + page] = Sv;
         }
         put_score(0, (((long)r * n_kv + h) * G + g_l) * (long)MP + p0 + page, Sv, keep);
         } else {
@@ -694,7 +696,7 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
             const bool keep = row_owner && (page < nvalid) && (g_l < G);
             if (keep) {
                 tmax = fmaxf(tmax, Sv[sx]);
-                if constexpr (STG) sc_l[g_l * (c1 - c0) + (p0 - c0) + page] = Sv[sx];
+                if constexpr (STG) sc_l[g_l * (c1 - c0 + 1) + (p0 - c0) + page] = Sv[sx];
             }
             put_score(STG ? 0 : sx, (((long)r * n_kv + h) * G + g_l) * (long)MP + p0 + page, Sv[sx], keep);
         }
@@ -757,7 +759,7 @@ __global__ __launch_bounds__(SC_BLOCK) void rki4_score_kernel(
         const int n = c1 - c0;
         float* srow = score_h + ((long)r * n_kv + h) * G * (long)MP + c0;
         for (int g = 0; g < G; ++g)
-            for (int p = tid; p < n; p += SC_BLOCK) srow[(long)g * MP + p] = sc_l[g * n + p];
+            for (int p = tid; p < n; p += SC_BLOCK) srow[(long)g * MP + p] = sc_l[g * (n + 1) + p];
     }
     if (tid < 16) pm_out[(long)tid * Z] = u2f(wmax[tid]);
 }
