@@ -781,13 +781,12 @@ extern "C" int32_t locks_score_auto_chunk(int32_t n_req, int32_t n_kv, int32_t m
     const long units = tiles * (n_kv > 0 ? n_kv : 1) * (n_req > 0 ? n_req : 1);
     const long target = n_req > 1 ? 1024 : 512;
     long ct = (units + target - 1) / target;             // tiles per workgroup (one kv head)
-    // Small grids: at least units / 256 tiles per workgroup (up to 8, two
-    // units per wave), so a short row's waves overlap one unit's gather
-    // with the other's scoring instead of each paying a whole prologue for
-    // one unit (GLM G = 16 step: 128K 1.408 -> 1.372 ms, 64K 1.194 ->
-    // 1.183 ms; at 16K, 256 units, the floor is 1: 32 workgroups measured
-    // 1.284 against 1.215 ms)
-    const long floor_ct = units / 256 < 8 ? units / 256 : 8;
+    // Small grids: at least units / 256 tiles per workgroup, up to 4 (one
+    // unit per wave): GLM G = 16 step at 32K 0.996 (2 tiles) vs 1.005 ms (1),
+    // 64K 1.032 (4) vs 1.056 (2), 128K 1.219 (4) vs 1.242 (8) vs 1.410 (2);
+    // at 16K, 256 units, the floor is 1 (32 workgroups measured 1.284
+    // against 1.215 ms)
+    const long floor_ct = units / 256 < 4 ? units / 256 : 4;
     if (ct < floor_ct) ct = floor_ct;
     if (ct < 1) ct = 1;
     if (ct > SC_MAX_CHUNK / SC_TILE) ct = SC_MAX_CHUNK / SC_TILE;
